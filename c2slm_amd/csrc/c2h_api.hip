@@ -1,0 +1,954 @@
+// Host side of the C ABI in include/c2h.h: context, weight upload and
+// repack, HIP-graph capture of the decode step, and the entry points.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/c2h.h"
+#include "c2h_device.h"
+#include "c2h_kernels.h"
+
+using namespace c2h;
+
+namespace {
+
+constexpr int kStateRing = 256;
+
+struct Tensor {
+  uint8_t* q = nullptr;
+  uint16_t* d = nullptr;
+  int type = -1;
+  int64_t rows = 0, cols = 0;
+  bool present() const { return q != nullptr; }
+  WeightRef ref() const { return WeightRef{q, d}; }
+};
+
+struct Layer {
+  float *attn_norm = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr, *ffn_norm = nullptr;
+  Tensor wq, wk, wv, wo, wg, wu, wd;
+};
+
+}  // namespace
+
+struct c2h_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool has_model = false;
+  c2h_model_desc desc{};
+  std::string err;
+  std::vector<void*> allocs;
+
+  std::vector<Layer> layers;
+  Tensor embd, output;
+  float* output_norm = nullptr;
+
+  float *X = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *h = nullptr;
+  float* normx[2] = {nullptr, nullptr};
+  int nx_cur = 0, nx_prev = 0;
+  float* kv = nullptr;
+  int32_t* token_ids = nullptr;
+  float *rope_cos = nullptr, *rope_sin = nullptr;
+  float* part_v = nullptr;
+  int* part_i = nullptr;
+  int n_part = 0;
+  float* logits = nullptr;
+  C2hState* state_dev = nullptr;
+  C2hState* state_ring = nullptr;  // pinned
+  int32_t* tok_host = nullptr;     // pinned
+  unsigned ring_next = 0;
+
+  hipGraphExec_t g_step = nullptr, g_fwd = nullptr;
+  bool graphs_ready = false;
+  bool use_graphs = true;
+  size_t attn_lds = 0;
+
+  // kernel-only scratch (c2h_gemv / c2h_quantize_q8k host forms)
+  std::vector<void*> scratch;
+};
+
+namespace {
+
+int fail(c2h_ctx* c, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  if (c) c->err = buf;
+  return code;
+}
+
+#define HIPCHK(c, call)                                                                                 \
+  do {                                                                                                  \
+    hipError_t e_ = (call);                                                                             \
+    if (e_ != hipSuccess) return fail((c), C2H_ERR_HIP, "%s failed: %s", #call, hipGetErrorString(e_)); \
+  } while (0)
+
+template <class T>
+int dalloc(c2h_ctx* c, T** p, size_t bytes) {
+  void* ptr = nullptr;
+  HIPCHK(c, hipMalloc(&ptr, bytes < 256 ? 256 : bytes));
+  c->allocs.push_back(ptr);
+  *p = reinterpret_cast<T*>(ptr);
+  return C2H_OK;
+}
+
+int nb_k(int64_t cols) { return (int)(cols / 256); }
+int nb8_of(int64_t cols) { return (int)(cols / 32); }
+int nq_of(int64_t cols) { return (nb8_of(cols) + 3) / 4; }
+
+size_t native_row_bytes(int type, int64_t cols) {
+  switch (type) {
+    case C2H_Q4_K: return (size_t)nb_k(cols) * BS_Q4K;
+    case C2H_Q6_K: return (size_t)nb_k(cols) * BS_Q6K;
+    case C2H_Q8_0: return (size_t)nb8_of(cols) * BS_Q8_0;
+    case C2H_F32: return (size_t)cols * 4;
+  }
+  return 0;
+}
+
+// Sizes of the q and d parts of the device layout.
+void packed_parts(int type, int64_t rows, int64_t cols, size_t* qb, size_t* db) {
+  *qb = *db = 0;
+  switch (type) {
+    case C2H_Q4_K: *qb = (size_t)rows * nb_k(cols) * BS_Q4K; break;
+    case C2H_Q6_K:
+      *qb = (size_t)rows * nb_k(cols) * BS_Q6K_PACKED;
+      *db = (size_t)rows * nb_k(cols) * 2;
+      break;
+    case C2H_Q8_0:
+      *qb = (size_t)rows * nq_of(cols) * 128;
+      *db = (size_t)rows * nb8_of(cols) * 2;
+      break;
+  }
+}
+
+void pack_host(int type, int64_t rows, int64_t cols, const uint8_t* src, uint8_t* qdst, uint8_t* ddst) {
+  if (type == C2H_Q4_K) {
+    memcpy(qdst, src, (size_t)rows * nb_k(cols) * BS_Q4K);
+  } else if (type == C2H_Q6_K) {
+    size_t n = (size_t)rows * nb_k(cols);
+    for (size_t i = 0; i < n; ++i) {
+      memcpy(qdst + i * BS_Q6K_PACKED, src + i * BS_Q6K, BS_Q6K_PACKED);
+      memcpy(ddst + i * 2, src + i * BS_Q6K + 208, 2);
+    }
+  } else if (type == C2H_Q8_0) {
+    int nb8 = nb8_of(cols), nq = nq_of(cols);
+    memset(qdst, 0, (size_t)rows * nq * 128);
+    for (int64_t r = 0; r < rows; ++r) {
+      const uint8_t* row = src + (size_t)r * nb8 * BS_Q8_0;
+      uint8_t* qr = qdst + (size_t)r * nq * 128;
+      for (int b = 0; b < nb8; ++b) {
+        const uint8_t* blk = row + (size_t)b * BS_Q8_0;
+        memcpy(ddst + ((size_t)r * nb8 + b) * 2, blk, 2);
+        int bq = b >> 2, bb = b & 3;
+        for (int j = 0; j < 8; ++j)
+          for (int i = 0; i < 4; ++i) qr[(bq * 8 + j) * 16 + bb * 4 + i] = blk[2 + j + 8 * i];
+      }
+    }
+  }
+}
+
+int check_type_shape(c2h_ctx* c, int type, int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return fail(c, C2H_ERR_INVALID, "rows/cols must be positive");
+  if (type == C2H_Q4_K || type == C2H_Q6_K) {
+    if (cols < 256) return fail(c, C2H_ERR_UNSUPPORTED, "K-quant rows need at least 256 columns");
+    if (nb_k(cols) > LDS_Q8K_BLOCKS) return fail(c, C2H_ERR_UNSUPPORTED, "more than 16384 columns");
+    return C2H_OK;
+  }
+  if (type == C2H_Q8_0) {
+    if (cols < 32) return fail(c, C2H_ERR_UNSUPPORTED, "Q8_0 rows need at least 32 columns");
+    return C2H_OK;
+  }
+  return fail(c, C2H_ERR_UNSUPPORTED, "ggml type %d is not run by this build", type);
+}
+
+int upload_quant(c2h_ctx* c, Tensor* t, int type, int64_t rows, int64_t cols, const void* host, size_t bytes) {
+  int rc = check_type_shape(c, type, rows, cols);
+  if (rc) return rc;
+  size_t need = (size_t)rows * native_row_bytes(type, cols);
+  if (bytes < need) return fail(c, C2H_ERR_INVALID, "tensor payload %zu bytes < %zu needed", bytes, need);
+  size_t qb, db;
+  packed_parts(type, rows, cols, &qb, &db);
+  std::vector<uint8_t> qh(qb), dh(db);
+  pack_host(type, rows, cols, reinterpret_cast<const uint8_t*>(host), qh.data(), dh.data());
+  uint8_t* q;
+  if ((rc = dalloc(c, &q, qb))) return rc;
+  HIPCHK(c, hipMemcpy(q, qh.data(), qb, hipMemcpyHostToDevice));
+  uint16_t* d = nullptr;
+  if (db) {
+    if ((rc = dalloc(c, &d, db))) return rc;
+    HIPCHK(c, hipMemcpy(d, dh.data(), db, hipMemcpyHostToDevice));
+  }
+  t->q = q;
+  t->d = d;
+  t->type = type;
+  t->rows = rows;
+  t->cols = cols;
+  c->graphs_ready = false;
+  return C2H_OK;
+}
+
+int upload_f32(c2h_ctx* c, float** dst, int64_t n_expected, int type, int64_t rows, int64_t cols, const void* host,
+               size_t bytes) {
+  if (type != C2H_F32) return fail(c, C2H_ERR_UNSUPPORTED, "norm/bias tensors must be F32");
+  if (rows * cols != n_expected || bytes < (size_t)n_expected * 4)
+    return fail(c, C2H_ERR_INVALID, "F32 tensor has %lld elements, expected %lld", (long long)(rows * cols),
+                (long long)n_expected);
+  int rc;
+  if (!*dst && (rc = dalloc(c, dst, (size_t)n_expected * 4))) return rc;
+  HIPCHK(c, hipMemcpy(*dst, host, (size_t)n_expected * 4, hipMemcpyHostToDevice));
+  c->graphs_ready = false;
+  return C2H_OK;
+}
+
+// ------------------------------------------------------------- launches
+
+size_t gemv_lds_bytes(int n_x_lds) { return sizeof(Q8KLds) + (size_t)2 * n_x_lds * sizeof(float); }
+
+void add_job(GemvParams& P, int* task, const Tensor& w, const Tensor* w2, int mode, float* y, const float* bias,
+             int32_t* isums) {
+  GemvJob& J = P.jobs[P.n_jobs++];
+  J.w = w.ref();
+  J.type = w.type;
+  if (w2) {
+    J.w2 = w2->ref();
+    J.type2 = w2->type;
+  } else {
+    J.w2 = WeightRef{nullptr, nullptr};
+    J.type2 = w.type;
+  }
+  J.rows = (int)w.rows;
+  J.nb = nb_k(w.cols);
+  J.rpt = 64 / J.nb;
+  J.n_tasks = (J.rows + J.rpt - 1) / J.rpt;
+  J.task_begin = *task;
+  *task += J.n_tasks;
+  J.mode = mode;
+  J.y = y;
+  J.bias = bias;
+  J.isums = isums;
+}
+
+void launch_gemv(c2h_ctx* c, GemvParams& P, int total_tasks) {
+  int grid = (total_tasks + 3) / 4;
+  size_t lds = gemv_lds_bytes(P.n_x_lds);
+  hipLaunchKernelGGL(k_gemv, dim3(grid), dim3(256), lds, c->stream, P);
+}
+
+int round4(int n) { return (n + 3) & ~3; }
+
+GemvParams base_params(c2h_ctx* c) {
+  GemvParams P;
+  memset(&P, 0, sizeof(P));
+  P.eps = c->desc.rms_eps;
+  P.n_vocab = c->desc.n_vocab;
+  P.max_ctx = c->desc.max_ctx;
+  P.token_ids = c->token_ids;
+  P.state = c->state_dev;
+  P.emb = c->embd.ref();
+  P.part_v = c->part_v;
+  P.part_i = c->part_i;
+  P.n_part = c->n_part;
+  return P;
+}
+
+const Tensor& out_weight(c2h_ctx* c) { return c->output.present() ? c->output : c->embd; }
+
+void enqueue_vocab(c2h_ctx* c, int apply_penalty, float* logits_out, int x_sel, const float* x) {
+  VocabParams V;
+  memset(&V, 0, sizeof(V));
+  V.w = out_weight(c).ref();
+  V.n_vocab = c->desc.n_vocab;
+  V.n_embd = c->desc.n_embd;
+  V.x_sel = x_sel;
+  V.x = x;
+  V.x_buf[0] = c->normx[0];
+  V.x_buf[1] = c->normx[1];
+  V.token_ids = c->token_ids;
+  V.apply_penalty = apply_penalty;
+  V.logits_out = logits_out;
+  V.part_v = c->part_v;
+  V.part_i = c->part_i;
+  V.state = c->state_dev;
+  size_t lds = (size_t)nq_of(c->desc.n_embd) * 4 * 32 * sizeof(float);
+  hipLaunchKernelGGL(k_vocab, dim3(c->n_part), dim3(256), lds, c->stream, V);
+}
+
+// The 24-layer body of engine.Forward plus the final RMSNorm; layer 0 embeds
+// either state->token (forward) or the argmax of the vocab partials (step).
+void enqueue_layers(c2h_ctx* c, bool from_argmax) {
+  const c2h_model_desc& D = c->desc;
+  const int E = D.n_embd;
+  for (int l = 0; l < D.n_layers; ++l) {
+    Layer& L = c->layers[l];
+    {  // attn_in
+      GemvParams P = base_params(c);
+      P.prologue = (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM;
+      P.n_x = E;
+      P.n_x_lds = round4(E);
+      P.x = c->X;
+      P.x_out = c->X;
+      P.norm_w = L.attn_norm;
+      P.nb_in = nb_k(E);
+      int task = 0;
+      add_job(P, &task, L.wq, nullptr, L.bq ? MODE_BIAS : MODE_STORE, c->q, L.bq, nullptr);
+      add_job(P, &task, L.wk, nullptr, L.bk ? MODE_BIAS : MODE_STORE, c->k, L.bk, nullptr);
+      add_job(P, &task, L.wv, nullptr, L.bv ? MODE_BIAS : MODE_STORE, c->v, L.bv, nullptr);
+      launch_gemv(c, P, task);
+    }
+    {  // attention
+      AttnParams A;
+      memset(&A, 0, sizeof(A));
+      A.q = c->q;
+      A.k = c->k;
+      A.v = c->v;
+      A.out = c->attn;
+      A.kv = c->kv;
+      A.rope_cos = c->rope_cos;
+      A.rope_sin = c->rope_sin;
+      A.rope_len = D.max_ctx;
+      A.layer = l;
+      A.n_layers = D.n_layers;
+      A.n_heads = D.n_heads;
+      A.n_kv_heads = D.n_kv_heads;
+      A.max_ctx = D.max_ctx;
+      A.scale = (float)(1.0 / std::sqrt((double)D.head_dim));
+      A.state = c->state_dev;
+      hipLaunchKernelGGL(k_attention, dim3(D.n_heads), dim3(256), c->attn_lds, c->stream, A);
+    }
+    {  // attn_out: X += Wo * Q8_K(attn)
+      GemvParams P = base_params(c);
+      P.prologue = PRO_QUANT;
+      P.x = c->attn;
+      P.nb_in = nb_k(E);
+      int task = 0;
+      add_job(P, &task, L.wo, nullptr, MODE_RESID, c->X, nullptr, nullptr);
+      launch_gemv(c, P, task);
+    }
+    {  // ffn_in: h = SwiGLU(Wg * n, Wu * n), n = Q8_K(RMSNorm(X))
+      GemvParams P = base_params(c);
+      P.prologue = PRO_NORM;
+      P.n_x = E;
+      P.n_x_lds = round4(E);
+      P.x = c->X;
+      P.norm_w = L.ffn_norm;
+      P.nb_in = nb_k(E);
+      int task = 0;
+      add_job(P, &task, L.wg, &L.wu, MODE_SWIGLU, c->h, nullptr, nullptr);
+      launch_gemv(c, P, task);
+    }
+    {  // ffn_out: X += Wd * Q8_K(h)
+      GemvParams P = base_params(c);
+      P.prologue = PRO_QUANT;
+      P.x = c->h;
+      P.nb_in = nb_k(D.n_ff);
+      int task = 0;
+      add_job(P, &task, L.wd, nullptr, MODE_RESID, c->X, nullptr, nullptr);
+      launch_gemv(c, P, task);
+    }
+  }
+  NormParams N;
+  memset(&N, 0, sizeof(N));
+  N.x = c->X;
+  N.w = c->output_norm;
+  N.eps = D.rms_eps;
+  N.n = E;
+  N.out_sel = 1;
+  N.out_buf[0] = c->normx[0];
+  N.out_buf[1] = c->normx[1];
+  N.state = c->state_dev;
+  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), (size_t)2 * round4(E) * sizeof(float), c->stream, N);
+}
+
+void enqueue_step(c2h_ctx* c) {
+  enqueue_vocab(c, 1, nullptr, 1, nullptr);
+  enqueue_layers(c, true);
+}
+
+int validate_model(c2h_ctx* c) {
+  if (!c->has_model) return fail(c, C2H_ERR_STATE, "context has no model");
+  if (!c->embd.present() || c->embd.type != C2H_Q8_0)
+    return fail(c, C2H_ERR_STATE, "token_embd (Q8_0) not uploaded");
+  if (c->output.present() && c->output.type != C2H_Q8_0)
+    return fail(c, C2H_ERR_UNSUPPORTED, "output.weight must be Q8_0");
+  if (!c->output_norm) return fail(c, C2H_ERR_STATE, "output_norm not uploaded");
+  for (int l = 0; l < c->desc.n_layers; ++l) {
+    Layer& L = c->layers[l];
+    if (!L.attn_norm || !L.ffn_norm) return fail(c, C2H_ERR_STATE, "layer %d norms missing", l);
+    const Tensor* ts[] = {&L.wq, &L.wk, &L.wv, &L.wo, &L.wg, &L.wu, &L.wd};
+    for (const Tensor* t : ts) {
+      if (!t->present()) return fail(c, C2H_ERR_STATE, "layer %d projection missing", l);
+      if (t->type != C2H_Q4_K && t->type != C2H_Q6_K)
+        return fail(c, C2H_ERR_UNSUPPORTED, "layer %d: projections must be Q4_K or Q6_K", l);
+    }
+    if (L.wg.cols != L.wu.cols || L.wg.rows != L.wu.rows)
+      return fail(c, C2H_ERR_INVALID, "layer %d gate/up shapes differ", l);
+  }
+  return C2H_OK;
+}
+
+int build_graphs(c2h_ctx* c) {
+  if (c->graphs_ready) return C2H_OK;
+  int rc = validate_model(c);
+  if (rc) return rc;
+  if (c->g_step) (void)hipGraphExecDestroy(c->g_step);
+  if (c->g_fwd) (void)hipGraphExecDestroy(c->g_fwd);
+  c->g_step = c->g_fwd = nullptr;
+  if (c->use_graphs) {
+    for (int which = 0; which < 2; ++which) {
+      hipGraph_t g;
+      HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+      if (which == 0)
+        enqueue_step(c);
+      else
+        enqueue_layers(c, false);
+      HIPCHK(c, hipStreamEndCapture(c->stream, &g));
+      hipGraphExec_t ge;
+      HIPCHK(c, hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+      (void)hipGraphDestroy(g);
+      (which == 0 ? c->g_step : c->g_fwd) = ge;
+    }
+  }
+  c->graphs_ready = true;
+  return C2H_OK;
+}
+
+// Writes the per-launch state through a ring of pinned slots; the stream
+// orders the copy before the graph.  Slots are reused only after a sync.
+int push_state(c2h_ctx* c, const C2hState& s) {
+  unsigned slot = c->ring_next++ % kStateRing;
+  if (slot == 0 && c->ring_next > 1) HIPCHK(c, hipStreamSynchronize(c->stream));
+  c->state_ring[slot] = s;
+  HIPCHK(c, hipMemcpyAsync(c->state_dev, &c->state_ring[slot], sizeof(C2hState), hipMemcpyHostToDevice, c->stream));
+  return C2H_OK;
+}
+
+int run_graph(c2h_ctx* c, bool step) {
+  if (c->use_graphs) {
+    HIPCHK(c, hipGraphLaunch(step ? c->g_step : c->g_fwd, c->stream));
+  } else {
+    if (step)
+      enqueue_step(c);
+    else
+      enqueue_layers(c, false);
+    HIPCHK(c, hipGetLastError());
+  }
+  return C2H_OK;
+}
+
+thread_local std::string g_create_err;
+
+}  // namespace
+
+// ====================================================================== ABI
+
+extern "C" {
+
+int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
+  if (!out) return C2H_ERR_INVALID;
+  *out = nullptr;
+  c2h_ctx* c = new c2h_ctx();
+  c->device = device;
+  g_create_err.clear();
+  auto bail = [&](int rc) {
+    g_create_err = c->err.empty() ? "HIP runtime call failed during create" : c->err;
+    c2h_destroy(c);
+    return rc;
+  };
+  if (hipSetDevice(device) != hipSuccess) {
+    g_create_err = "hipSetDevice failed";
+    delete c;
+    return C2H_ERR_HIP;
+  }
+  if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+    g_create_err = "hipStreamCreate failed";
+    delete c;
+    return C2H_ERR_HIP;
+  }
+  const char* ng = getenv("C2H_NO_GRAPH");
+  c->use_graphs = !(ng && ng[0] == '1');
+  void* pinned = nullptr;
+  if (hipHostMalloc(&pinned, sizeof(C2hState) * kStateRing + 64, hipHostMallocDefault) != hipSuccess) return bail(C2H_ERR_HIP);
+  c->state_ring = reinterpret_cast<C2hState*>(pinned);
+  c->tok_host = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(pinned) + sizeof(C2hState) * kStateRing);
+  int rc;
+  if ((rc = dalloc(c, &c->state_dev, sizeof(C2hState)))) return bail(rc);
+  if (!desc) {
+    C2hState s0;
+    memset(&s0, 0, sizeof(s0));
+    s0.penalty = 1.15f;
+    s0.im_end = -1;
+    s0.eos = -1;
+    if (push_state(c, s0) || hipStreamSynchronize(c->stream) != hipSuccess) return bail(C2H_ERR_HIP);
+    *out = c;
+    return C2H_OK;
+  }
+  const c2h_model_desc& D = *desc;
+  if (D.n_layers <= 0 || D.n_embd <= 0 || D.n_heads <= 0 || D.n_kv_heads <= 0 || D.n_ff <= 0 || D.n_vocab <= 0 ||
+      D.max_ctx <= 0)
+    return bail(fail(c, C2H_ERR_INVALID, "model dimensions must be positive"));
+  if (D.head_dim != 64 || D.n_embd != D.n_heads * D.head_dim || D.n_heads % D.n_kv_heads)
+    return bail(fail(c, C2H_ERR_UNSUPPORTED, "this build runs head_dim 64 with n_embd = n_heads*64"));
+  if (D.n_embd % 256 != 128 && D.n_embd % 256 != 0 && D.n_embd < 256)
+    return bail(fail(c, C2H_ERR_UNSUPPORTED, "n_embd too small"));
+  if (D.n_embd % 32 || D.n_embd > 4096 || D.n_ff % 4 || D.n_ff > 16384)
+    return bail(fail(c, C2H_ERR_UNSUPPORTED, "n_embd must be a multiple of 32 up to 4096, n_ff up to 16384"));
+  if ((size_t)D.max_ctx * 4 > 128 * 1024)
+    return bail(fail(c, C2H_ERR_UNSUPPORTED, "max_ctx above 32768 is not supported by the exact attention kernel"));
+  c->desc = D;
+  c->has_model = true;
+  c->layers.resize(D.n_layers);
+  const int E = D.n_embd, KV = D.n_kv_heads * D.head_dim, F = D.n_ff;
+  if ((rc = dalloc(c, &c->X, E * 4)) || (rc = dalloc(c, &c->q, E * 4)) || (rc = dalloc(c, &c->k, KV * 4)) ||
+      (rc = dalloc(c, &c->v, KV * 4)) || (rc = dalloc(c, &c->attn, E * 4)) || (rc = dalloc(c, &c->h, F * 4)) ||
+      (rc = dalloc(c, &c->normx[0], E * 4)) || (rc = dalloc(c, &c->normx[1], E * 4)))
+    return bail(rc);
+  size_t kv_bytes = (size_t)2 * D.n_layers * D.n_kv_heads * D.max_ctx * D.head_dim * 4;
+  if ((rc = dalloc(c, &c->kv, kv_bytes))) return bail(rc);
+  if (hipMemset(c->kv, 0, kv_bytes) != hipSuccess) return bail(fail(c, C2H_ERR_HIP, "hipMemset kv"));
+  if ((rc = dalloc(c, &c->token_ids, (size_t)D.max_ctx * 4))) return bail(rc);
+  if (hipMemset(c->token_ids, 0, (size_t)D.max_ctx * 4) != hipSuccess) return bail(fail(c, C2H_ERR_HIP, "memset"));
+  if (hipMemset(c->normx[0], 0, E * 4) != hipSuccess || hipMemset(c->normx[1], 0, E * 4) != hipSuccess)
+    return bail(fail(c, C2H_ERR_HIP, "memset"));
+  // RoPE table, tensor.NewRoPETable (tensor/ops.go:237-257) in float64
+  {
+    int half = D.head_dim / 2;
+    std::vector<float> cs((size_t)D.max_ctx * half), sn((size_t)D.max_ctx * half);
+    for (int p = 0; p < D.max_ctx; ++p)
+      for (int i = 0; i < half; ++i) {
+        double freq = 1.0 / std::pow((double)D.rope_theta, (double)(2 * i) / (double)D.head_dim);
+        double val = (double)p * freq;
+        cs[(size_t)p * half + i] = (float)std::cos(val);
+        sn[(size_t)p * half + i] = (float)std::sin(val);
+      }
+    if ((rc = dalloc(c, &c->rope_cos, cs.size() * 4)) || (rc = dalloc(c, &c->rope_sin, sn.size() * 4))) return bail(rc);
+    if (hipMemcpy(c->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(c->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+      return bail(fail(c, C2H_ERR_HIP, "rope upload"));
+  }
+  int tiles = (D.n_vocab + 31) / 32;
+  c->n_part = (tiles + VOCAB_TILES - 1) / VOCAB_TILES;
+  if ((rc = dalloc(c, &c->part_v, (size_t)c->n_part * 4)) || (rc = dalloc(c, &c->part_i, (size_t)c->n_part * 4)) ||
+      (rc = dalloc(c, &c->logits, (size_t)D.n_vocab * 4)))
+    return bail(rc);
+  c->attn_lds = (size_t)D.max_ctx * 4;
+  if (hipFuncSetAttribute((const void*)k_attention, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->attn_lds) !=
+      hipSuccess)
+    return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
+  C2hState s0;
+  memset(&s0, 0, sizeof(s0));
+  s0.penalty = 1.15f;
+  s0.nx_out = 1;
+  if (push_state(c, s0) || hipStreamSynchronize(c->stream) != hipSuccess) return bail(C2H_ERR_HIP);
+  *out = c;
+  return C2H_OK;
+}
+
+void c2h_destroy(c2h_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  if (c->g_step) (void)hipGraphExecDestroy(c->g_step);
+  if (c->g_fwd) (void)hipGraphExecDestroy(c->g_fwd);
+  for (void* p : c->allocs) (void)hipFree(p);
+  for (void* p : c->scratch) (void)hipFree(p);
+  if (c->state_ring) (void)hipHostFree(c->state_ring);
+  if (c->stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+const char* c2h_last_error(const c2h_ctx* c) {
+  if (!c) return g_create_err.c_str();
+  return c->err.c_str();
+}
+
+int c2h_upload_tensor(c2h_ctx* c, int32_t layer, int32_t role, int32_t type, int64_t rows, int64_t cols,
+                      const void* host, size_t bytes) {
+  if (!c || !host) return C2H_ERR_INVALID;
+  if (!c->has_model) return fail(c, C2H_ERR_STATE, "kernel-only context");
+  HIPCHK(c, hipSetDevice(c->device));
+  const c2h_model_desc& D = c->desc;
+  const int64_t E = D.n_embd, KV = (int64_t)D.n_kv_heads * D.head_dim, F = D.n_ff, V = D.n_vocab;
+  auto want = [&](int64_t r, int64_t cl) -> int {
+    if (rows != r || cols != cl)
+      return fail(c, C2H_ERR_INVALID, "role %d: shape %lldx%lld, expected %lldx%lld", role, (long long)rows,
+                  (long long)cols, (long long)r, (long long)cl);
+    return C2H_OK;
+  };
+  int rc;
+  if (role == C2H_ROLE_TOKEN_EMBD) {
+    if ((rc = want(V, E))) return rc;
+    if (type != C2H_Q8_0) return fail(c, C2H_ERR_UNSUPPORTED, "token_embd must be Q8_0");
+    return upload_quant(c, &c->embd, type, rows, cols, host, bytes);
+  }
+  if (role == C2H_ROLE_OUTPUT) {
+    if ((rc = want(V, E))) return rc;
+    if (type != C2H_Q8_0) return fail(c, C2H_ERR_UNSUPPORTED, "output.weight must be Q8_0");
+    return upload_quant(c, &c->output, type, rows, cols, host, bytes);
+  }
+  if (role == C2H_ROLE_OUTPUT_NORM) return upload_f32(c, &c->output_norm, E, type, rows, cols, host, bytes);
+  if (layer < 0 || layer >= D.n_layers) return fail(c, C2H_ERR_INVALID, "layer %d out of range", layer);
+  Layer& L = c->layers[layer];
+  switch (role) {
+    case C2H_ROLE_ATTN_NORM: return upload_f32(c, &L.attn_norm, E, type, rows, cols, host, bytes);
+    case C2H_ROLE_FFN_NORM: return upload_f32(c, &L.ffn_norm, E, type, rows, cols, host, bytes);
+    case C2H_ROLE_ATTN_Q_BIAS: return upload_f32(c, &L.bq, E, type, rows, cols, host, bytes);
+    case C2H_ROLE_ATTN_K_BIAS: return upload_f32(c, &L.bk, KV, type, rows, cols, host, bytes);
+    case C2H_ROLE_ATTN_V_BIAS: return upload_f32(c, &L.bv, KV, type, rows, cols, host, bytes);
+    case C2H_ROLE_ATTN_Q: if ((rc = want(E, E))) return rc; return upload_quant(c, &L.wq, type, rows, cols, host, bytes);
+    case C2H_ROLE_ATTN_K: if ((rc = want(KV, E))) return rc; return upload_quant(c, &L.wk, type, rows, cols, host, bytes);
+    case C2H_ROLE_ATTN_V: if ((rc = want(KV, E))) return rc; return upload_quant(c, &L.wv, type, rows, cols, host, bytes);
+    case C2H_ROLE_ATTN_OUT: if ((rc = want(E, E))) return rc; return upload_quant(c, &L.wo, type, rows, cols, host, bytes);
+    case C2H_ROLE_FFN_GATE: if ((rc = want(F, E))) return rc; return upload_quant(c, &L.wg, type, rows, cols, host, bytes);
+    case C2H_ROLE_FFN_UP: if ((rc = want(F, E))) return rc; return upload_quant(c, &L.wu, type, rows, cols, host, bytes);
+    case C2H_ROLE_FFN_DOWN: if ((rc = want(E, F))) return rc; return upload_quant(c, &L.wd, type, rows, cols, host, bytes);
+  }
+  return fail(c, C2H_ERR_INVALID, "unknown role %d", role);
+}
+
+int c2h_set_token_ids(c2h_ctx* c, int32_t pos0, const int32_t* ids, int32_t n) {
+  if (!c || (!ids && n > 0)) return C2H_ERR_INVALID;
+  if (!c->has_model) return fail(c, C2H_ERR_STATE, "kernel-only context");
+  if (pos0 < 0 || n < 0 || pos0 + n > c->desc.max_ctx) return fail(c, C2H_ERR_RANGE, "token ids out of range");
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (n) HIPCHK(c, hipMemcpy(c->token_ids + pos0, ids, (size_t)n * 4, hipMemcpyHostToDevice));
+  return C2H_OK;
+}
+
+int c2h_forward(c2h_ctx* c, int32_t token, int32_t pos, float* normx_out) {
+  if (!c) return C2H_ERR_INVALID;
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = build_graphs(c);
+  if (rc) return rc;
+  if (pos < 0 || pos >= c->desc.max_ctx) return fail(c, C2H_ERR_RANGE, "pos %d outside [0, %d)", pos, c->desc.max_ctx);
+  C2hState s;
+  memset(&s, 0, sizeof(s));
+  s.pos = pos;
+  s.token = token;
+  s.penalty = 1.15f;
+  s.nx_in = c->nx_cur;
+  s.nx_out = c->nx_cur ^ 1;
+  if ((rc = push_state(c, s))) return rc;
+  if ((rc = run_graph(c, false))) return rc;
+  c->nx_prev = c->nx_cur;
+  c->nx_cur ^= 1;
+  if (normx_out) {
+    HIPCHK(c, hipMemcpyAsync(normx_out, c->normx[c->nx_cur], (size_t)c->desc.n_embd * 4, hipMemcpyDeviceToHost,
+                             c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+  }
+  return C2H_OK;
+}
+
+int c2h_logits(c2h_ctx* c, float* logits_out) {
+  if (!c || !logits_out) return C2H_ERR_INVALID;
+  if (!c->has_model) return fail(c, C2H_ERR_STATE, "kernel-only context");
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = validate_model(c);
+  if (rc) return rc;
+  C2hState s;
+  memset(&s, 0, sizeof(s));
+  s.penalty = 1.15f;
+  s.nx_in = c->nx_cur;
+  s.nx_out = c->nx_cur ^ 1;
+  if ((rc = push_state(c, s))) return rc;
+  enqueue_vocab(c, 0, c->logits, 1, nullptr);
+  HIPCHK(c, hipGetLastError());
+  HIPCHK(c, hipMemcpyAsync(logits_out, c->logits, (size_t)c->desc.n_vocab * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return C2H_OK;
+}
+
+int c2h_step(c2h_ctx* c, int32_t pos, float penalty, int32_t im_end, int32_t eos, int32_t* next_token) {
+  if (!c) return C2H_ERR_INVALID;
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = build_graphs(c);
+  if (rc) return rc;
+  if (pos < 0 || pos >= c->desc.max_ctx) return fail(c, C2H_ERR_RANGE, "pos %d outside [0, %d)", pos, c->desc.max_ctx);
+  C2hState s;
+  memset(&s, 0, sizeof(s));
+  s.pos = pos;
+  s.token = 0;
+  s.im_end = im_end;
+  s.eos = eos;
+  s.penalty = penalty;
+  s.nx_in = c->nx_cur;
+  s.nx_out = c->nx_cur ^ 1;
+  if ((rc = push_state(c, s))) return rc;
+  if ((rc = run_graph(c, true))) return rc;
+  c->nx_prev = c->nx_cur;
+  c->nx_cur ^= 1;
+  HIPCHK(c, hipMemcpyAsync(c->tok_host, &c->state_dev->token, 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (next_token) *next_token = *c->tok_host;
+  return C2H_OK;
+}
+
+int c2h_restore_normx(c2h_ctx* c) {
+  if (!c) return C2H_ERR_INVALID;
+  c->nx_cur = c->nx_prev;
+  return C2H_OK;
+}
+
+int c2h_get_normx(c2h_ctx* c, float* out) {
+  if (!c || !out) return C2H_ERR_INVALID;
+  if (!c->has_model) return fail(c, C2H_ERR_STATE, "kernel-only context");
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipMemcpyAsync(out, c->normx[c->nx_cur], (size_t)c->desc.n_embd * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return C2H_OK;
+}
+
+int c2h_get_kv(c2h_ctx* c, int32_t which, int32_t layer, int32_t kv_head, int32_t n, float* out) {
+  if (!c || !out) return C2H_ERR_INVALID;
+  if (!c->has_model) return fail(c, C2H_ERR_STATE, "kernel-only context");
+  const c2h_model_desc& D = c->desc;
+  if (which < 0 || which > 1 || layer < 0 || layer >= D.n_layers || kv_head < 0 || kv_head >= D.n_kv_heads || n < 0 ||
+      n > D.max_ctx)
+    return fail(c, C2H_ERR_INVALID, "kv index out of range");
+  HIPCHK(c, hipSetDevice(c->device));
+  size_t off = ((((size_t)which * D.n_layers + layer) * D.n_kv_heads + kv_head) * D.max_ctx) * D.head_dim;
+  HIPCHK(c, hipMemcpyAsync(out, c->kv + off, (size_t)n * D.head_dim * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return C2H_OK;
+}
+
+size_t c2h_packed_size(int32_t type, int64_t rows, int64_t cols) {
+  size_t qb, db;
+  packed_parts(type, rows, cols, &qb, &db);
+  return qb + db;
+}
+
+int c2h_pack_weights(int32_t type, int64_t rows, int64_t cols, const void* native, size_t native_bytes, void* packed,
+                     size_t packed_bytes) {
+  if (!native || !packed) return C2H_ERR_INVALID;
+  if (check_type_shape(nullptr, type, rows, cols)) return C2H_ERR_UNSUPPORTED;
+  if (native_bytes < (size_t)rows * native_row_bytes(type, cols)) return C2H_ERR_INVALID;
+  size_t qb, db;
+  packed_parts(type, rows, cols, &qb, &db);
+  if (packed_bytes < qb + db) return C2H_ERR_INVALID;
+  uint8_t* p = reinterpret_cast<uint8_t*>(packed);
+  pack_host(type, rows, cols, reinterpret_cast<const uint8_t*>(native), p, p + qb);
+  return C2H_OK;
+}
+
+int c2h_quantize_q8k_dev(c2h_ctx* c, const float* x, int32_t cols, void* q8k_out) {
+  if (!c || !x || !q8k_out || cols < 0) return C2H_ERR_INVALID;
+  HIPCHK(c, hipSetDevice(c->device));
+  int nb = cols / 256;
+  if (nb == 0) return C2H_OK;
+  hipLaunchKernelGGL(k_quantize_q8k, dim3((nb + 3) / 4), dim3(256), 0, c->stream, x, nb,
+                     reinterpret_cast<uint8_t*>(q8k_out));
+  HIPCHK(c, hipGetLastError());
+  return C2H_OK;
+}
+
+int c2h_gemv_dev(c2h_ctx* c, int32_t type, const void* w_packed, const void* xq, int32_t rows, int32_t cols, float* y,
+                 int32_t* isums_out) {
+  if (!c || !w_packed || !xq || !y) return C2H_ERR_INVALID;
+  int rc = check_type_shape(c, type, rows, cols);
+  if (rc) return rc;
+  HIPCHK(c, hipSetDevice(c->device));
+  size_t qb, db;
+  packed_parts(type, rows, cols, &qb, &db);
+  Tensor t;
+  t.q = reinterpret_cast<uint8_t*>(const_cast<void*>(w_packed));
+  t.d = db ? reinterpret_cast<uint16_t*>(t.q + qb) : nullptr;
+  t.type = type;
+  t.rows = rows;
+  t.cols = cols;
+  if (type == C2H_Q8_0) {
+    // the vocab kernel without penalty, logits to y
+    int tiles = (rows + 31) / 32;
+    int n_part = (tiles + VOCAB_TILES - 1) / VOCAB_TILES;
+    // scratch for the argmax candidates
+    float* pv = nullptr;
+    int* pi = nullptr;
+    HIPCHK(c, hipMalloc(&pv, (size_t)n_part * 4 + 256));
+    c->scratch.push_back(pv);
+    HIPCHK(c, hipMalloc(&pi, (size_t)n_part * 4 + 256));
+    c->scratch.push_back(pi);
+    VocabParams V;
+    memset(&V, 0, sizeof(V));
+    V.w = t.ref();
+    V.n_vocab = rows;
+    V.n_embd = cols;
+    V.x = reinterpret_cast<const float*>(xq);
+    V.token_ids = nullptr;
+    V.apply_penalty = 0;
+    V.logits_out = y;
+    V.part_v = pv;
+    V.part_i = pi;
+    V.state = c->state_dev;
+    size_t lds = (size_t)nq_of(cols) * 4 * 32 * sizeof(float);
+    hipLaunchKernelGGL(k_vocab, dim3(n_part), dim3(256), lds, c->stream, V);
+    HIPCHK(c, hipGetLastError());
+    return C2H_OK;
+  }
+  GemvParams P;
+  memset(&P, 0, sizeof(P));
+  P.prologue = PRO_Q8K;
+  P.q8k_in = reinterpret_cast<const uint8_t*>(xq);
+  P.nb_in = nb_k(cols);
+  P.state = c->state_dev;
+  int task = 0;
+  add_job(P, &task, t, nullptr, MODE_STORE, y, nullptr, isums_out);
+  launch_gemv(c, P, task);
+  HIPCHK(c, hipGetLastError());
+  return C2H_OK;
+}
+
+int c2h_sync(c2h_ctx* c) {
+  if (!c) return C2H_ERR_INVALID;
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  // kernel-only scratch from c2h_gemv_dev is released once the stream drained
+  for (void* p : c->scratch) (void)hipFree(p);
+  c->scratch.clear();
+  return C2H_OK;
+}
+
+int c2h_quantize_q8k(c2h_ctx* c, const float* x, int32_t cols, void* q8k_out) {
+  if (!c || !x || !q8k_out || cols < 0) return C2H_ERR_INVALID;
+  HIPCHK(c, hipSetDevice(c->device));
+  int nb = cols / 256;
+  if (nb == 0) return C2H_OK;
+  float* dx = nullptr;
+  uint8_t* dy = nullptr;
+  HIPCHK(c, hipMalloc(&dx, (size_t)nb * 256 * 4));
+  if (hipMalloc(&dy, (size_t)nb * BS_Q8K) != hipSuccess) {
+    (void)hipFree(dx);
+    return fail(c, C2H_ERR_HIP, "hipMalloc");
+  }
+  int rc = C2H_OK;
+  if (hipMemcpy(dx, x, (size_t)nb * 256 * 4, hipMemcpyHostToDevice) != hipSuccess) rc = C2H_ERR_HIP;
+  if (!rc) rc = c2h_quantize_q8k_dev(c, dx, cols, dy);
+  if (!rc && hipStreamSynchronize(c->stream) != hipSuccess) rc = C2H_ERR_HIP;
+  if (!rc && hipMemcpy(q8k_out, dy, (size_t)nb * BS_Q8K, hipMemcpyDeviceToHost) != hipSuccess) rc = C2H_ERR_HIP;
+  (void)hipFree(dx);
+  (void)hipFree(dy);
+  if (rc == C2H_ERR_HIP) return fail(c, rc, "quantize copy failed");
+  return rc;
+}
+
+int c2h_gemv(c2h_ctx* c, int32_t type, const void* w, const void* xq, int32_t rows, int32_t cols, float* y,
+             int32_t* isums_out) {
+  if (!c || !w || !xq || !y) return C2H_ERR_INVALID;
+  int rc = check_type_shape(c, type, rows, cols);
+  if (rc) return rc;
+  HIPCHK(c, hipSetDevice(c->device));
+  size_t nbytes = (size_t)rows * native_row_bytes(type, cols);
+  size_t pbytes = c2h_packed_size(type, rows, cols);
+  std::vector<uint8_t> packed(pbytes);
+  size_t qb, db;
+  packed_parts(type, rows, cols, &qb, &db);
+  pack_host(type, rows, cols, reinterpret_cast<const uint8_t*>(w), packed.data(), packed.data() + qb);
+  (void)nbytes;
+  size_t xbytes = (type == C2H_Q8_0) ? (size_t)cols * 4 : (size_t)nb_k(cols) * BS_Q8K;
+  size_t isz = 0;
+  if (isums_out && type == C2H_Q4_K) isz = (size_t)rows * nb_k(cols) * 8 * 4;
+  if (isums_out && type == C2H_Q6_K) isz = (size_t)rows * nb_k(cols) * 4;
+  uint8_t *dw = nullptr, *dx = nullptr;
+  float* dy = nullptr;
+  int32_t* di = nullptr;
+  auto cleanup = [&]() {
+    if (dw) (void)hipFree(dw);
+    if (dx) (void)hipFree(dx);
+    if (dy) (void)hipFree(dy);
+    if (di) (void)hipFree(di);
+  };
+  if (hipMalloc(&dw, pbytes) != hipSuccess || hipMalloc(&dx, xbytes) != hipSuccess ||
+      hipMalloc(&dy, (size_t)rows * 4) != hipSuccess || (isz && hipMalloc(&di, isz) != hipSuccess)) {
+    cleanup();
+    return fail(c, C2H_ERR_HIP, "hipMalloc failed");
+  }
+  rc = C2H_OK;
+  if (hipMemcpy(dw, packed.data(), pbytes, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(dx, xq, xbytes, hipMemcpyHostToDevice) != hipSuccess)
+    rc = fail(c, C2H_ERR_HIP, "copy in failed");
+  if (!rc) rc = c2h_gemv_dev(c, type, dw, dx, rows, cols, dy, di);
+  if (!rc && c2h_sync(c)) rc = C2H_ERR_HIP;
+  if (!rc && hipMemcpy(y, dy, (size_t)rows * 4, hipMemcpyDeviceToHost) != hipSuccess)
+    rc = fail(c, C2H_ERR_HIP, "copy out failed");
+  if (!rc && isz && hipMemcpy(isums_out, di, isz, hipMemcpyDeviceToHost) != hipSuccess)
+    rc = fail(c, C2H_ERR_HIP, "copy out failed");
+  cleanup();
+  return rc;
+}
+
+int c2h_time_vocab(c2h_ctx* c, int32_t iters, int32_t pos, float* ms) {
+  if (!c || !ms || iters <= 0) return C2H_ERR_INVALID;
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = validate_model(c);
+  if (rc) return rc;
+  if (pos < 0 || pos >= c->desc.max_ctx) return fail(c, C2H_ERR_RANGE, "pos out of range");
+  C2hState s;
+  memset(&s, 0, sizeof(s));
+  s.pos = pos;
+  s.penalty = 1.15f;
+  s.im_end = -1;
+  s.eos = -1;
+  s.nx_in = c->nx_cur;
+  s.nx_out = c->nx_cur ^ 1;
+  if ((rc = push_state(c, s))) return rc;
+  enqueue_vocab(c, 1, nullptr, 1, nullptr);  // warm-up
+  hipEvent_t e0, e1;
+  HIPCHK(c, hipEventCreate(&e0));
+  HIPCHK(c, hipEventCreate(&e1));
+  HIPCHK(c, hipEventRecord(e0, c->stream));
+  for (int i = 0; i < iters; ++i) enqueue_vocab(c, 1, nullptr, 1, nullptr);
+  HIPCHK(c, hipEventRecord(e1, c->stream));
+  HIPCHK(c, hipEventSynchronize(e1));
+  float t = 0;
+  HIPCHK(c, hipEventElapsedTime(&t, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *ms = t / iters;
+  return C2H_OK;
+}
+
+int c2h_time_steps(c2h_ctx* c, int32_t pos, int32_t iters, float penalty, int32_t im_end, int32_t eos, float* ms) {
+  if (!c || !ms || iters <= 0) return C2H_ERR_INVALID;
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = build_graphs(c);
+  if (rc) return rc;
+  if (pos < 0 || pos + iters > c->desc.max_ctx) return fail(c, C2H_ERR_RANGE, "positions out of range");
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  c->ring_next = 0;  // all earlier state copies have completed
+  hipEvent_t e0, e1;
+  HIPCHK(c, hipEventCreate(&e0));
+  HIPCHK(c, hipEventCreate(&e1));
+  HIPCHK(c, hipEventRecord(e0, c->stream));
+  for (int i = 0; i < iters; ++i) {
+    C2hState s;
+    memset(&s, 0, sizeof(s));
+    s.pos = pos + i;
+    s.im_end = im_end;
+    s.eos = eos;
+    s.penalty = penalty;
+    s.nx_in = c->nx_cur;
+    s.nx_out = c->nx_cur ^ 1;
+    if ((rc = push_state(c, s))) return rc;
+    if ((rc = run_graph(c, true))) return rc;
+    c->nx_prev = c->nx_cur;
+    c->nx_cur ^= 1;
+  }
+  HIPCHK(c, hipEventRecord(e1, c->stream));
+  HIPCHK(c, hipEventSynchronize(e1));
+  float t = 0;
+  HIPCHK(c, hipEventElapsedTime(&t, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *ms = t / iters;
+  return C2H_OK;
+}
+
+}  // extern "C"

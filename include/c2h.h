@@ -1,0 +1,182 @@
+/*
+ * c2h.h — C ABI of the MI355X (gfx950) decode path for c2slm.
+ *
+ * Plain C: pointers, sizes and status codes; no exceptions cross it.  Every
+ * entry point selects the context's device first (cgo calls may land on any
+ * OS thread).  A context owns one HIP stream and all device buffers; it is
+ * not safe for concurrent use, like the reference's Engine
+ * (engine/pool.go:22-42 keeps unsynchronised task state).
+ *
+ * Status: 0 = OK, < 0 = error; c2h_last_error() describes the last failure.
+ */
+#ifndef C2H_H
+#define C2H_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define C2H_OK 0
+#define C2H_ERR_INVALID (-1)     /* bad argument or shape */
+#define C2H_ERR_HIP (-2)         /* a HIP runtime call failed */
+#define C2H_ERR_UNSUPPORTED (-3) /* format or shape this build does not run */
+#define C2H_ERR_STATE (-4)       /* model incomplete / wrong call order */
+#define C2H_ERR_RANGE (-5)       /* position beyond the KV cache */
+
+/* ggml tensor types (gguf/reader.go:21-37) */
+#define C2H_F32 0
+#define C2H_Q8_0 8
+#define C2H_Q4_K 12
+#define C2H_Q6_K 14
+
+/* Tensor roles: what engine/model.go:114-207 binds.  Per-layer roles take
+ * the layer index; global roles ignore it. */
+enum c2h_role {
+  C2H_ROLE_TOKEN_EMBD = 0,  /* token_embd.weight (also the tied output) */
+  C2H_ROLE_OUTPUT = 1,      /* output.weight, when present */
+  C2H_ROLE_OUTPUT_NORM = 2, /* output_norm.weight */
+  C2H_ROLE_ATTN_NORM = 10,
+  C2H_ROLE_ATTN_Q = 11,
+  C2H_ROLE_ATTN_Q_BIAS = 12,
+  C2H_ROLE_ATTN_K = 13,
+  C2H_ROLE_ATTN_K_BIAS = 14,
+  C2H_ROLE_ATTN_V = 15,
+  C2H_ROLE_ATTN_V_BIAS = 16,
+  C2H_ROLE_ATTN_OUT = 17,
+  C2H_ROLE_FFN_NORM = 18,
+  C2H_ROLE_FFN_GATE = 19,
+  C2H_ROLE_FFN_UP = 20,
+  C2H_ROLE_FFN_DOWN = 21
+};
+
+/* Model dimensions, as engine.LoadModel resolves them (engine/model.go:64-145). */
+typedef struct c2h_model_desc {
+  int32_t n_layers;   /* qwen2.block_count (24) */
+  int32_t n_embd;     /* qwen2.embedding_length (896) */
+  int32_t n_heads;    /* qwen2.attention.head_count (14) */
+  int32_t n_kv_heads; /* qwen2.attention.head_count_kv (2) */
+  int32_t head_dim;   /* n_embd / n_heads (64) */
+  int32_t n_ff;       /* qwen2.feed_forward_length (4864) */
+  int32_t n_vocab;    /* token_embd dims[1] (151936) */
+  int32_t max_ctx;    /* KV positions; engine.MaxContextLen = 16384 (engine/kvcache.go:11) */
+  float rms_eps;      /* 1e-6 */
+  float rope_theta;   /* 1e6 */
+  int32_t reserved[6];
+} c2h_model_desc;
+
+typedef struct c2h_ctx c2h_ctx;
+
+/* ---- context ------------------------------------------------------------ */
+
+/* Replaces engine.LoadModel's model setup plus engine.NewKVCache and
+ * engine.NewArena (engine/model.go:58-210, engine/kvcache.go:49-81,
+ * engine/forward.go:28-43): allocates weights, fp32 KV cache
+ * [2][L][KVH][max_ctx][HD], activations, and the RoPE table built on the host
+ * in float64 exactly as tensor.NewRoPETable (tensor/ops.go:237-257).
+ * desc == NULL creates a kernel-only context (stream + scratch) for the
+ * c2h_*_dev and c2h_quantize_q8k / c2h_gemv entry points. */
+int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out);
+
+/* Frees everything (Engine.Close, c2slm.go:44-55).  NULL is a no-op. */
+void c2h_destroy(c2h_ctx* ctx);
+
+/* Text of the last error on this context (static text for ctx == NULL). */
+const char* c2h_last_error(const c2h_ctx* ctx);
+
+/* Uploads one tensor once, replacing the reference's []byte views into the
+ * mmap (gguf/reader.go:497-508) that the hot path reads per token.  `host`
+ * is borrowed for the call only.  Quantized rows use the reference's row
+ * stride (cols/QK)*blockSize (tensor/ops.go:26,78,121,183), so a 896-wide
+ * K-quant row covers 3 super-blocks exactly as the reference reads it;
+ * `bytes` must cover rows*stride.  Types: Q4_K/Q6_K projections, Q8_0
+ * embedding/output, F32 norms and biases. */
+int c2h_upload_tensor(c2h_ctx* ctx, int32_t layer, int32_t role, int32_t ggml_type, int64_t rows, int64_t cols,
+                      const void* host, size_t bytes);
+
+/* Mirrors KVCache.StoreTokenID (engine/kvcache.go:120-125) for ids the
+ * device did not write itself; c2h_forward and c2h_step record their own. */
+int c2h_set_token_ids(c2h_ctx* ctx, int32_t pos0, const int32_t* ids, int32_t n);
+
+/* ---- decode path -------------------------------------------------------- */
+
+/* engine.Forward(m, cache, a, token, pos) (engine/forward.go:54-138): one
+ * decoder step for `token` at `pos`, storing K/V at pos and
+ * TokenIDs[pos] = token; writes the final normX to normx_out (n_embd floats,
+ * nullable).  pos outside [0, max_ctx) returns C2H_ERR_RANGE (the reference
+ * skips RoPE and the KV store silently there, engine/kvcache.go:144-146). */
+int c2h_forward(c2h_ctx* ctx, int32_t token, int32_t pos, float* normx_out);
+
+/* engine.ComputeLogits(m, a, normX, out, nil) (engine/forward.go:171-191) on
+ * the current normX: n_vocab fp32 logits to logits_out. */
+int c2h_logits(c2h_ctx* ctx, float* logits_out);
+
+/* One iteration of the generate loop body (c2slm.go:153-222): logits of the
+ * current normX, repetition penalty over TokenIDs[max(0,pos-64), pos)
+ * skipping im_end/eos, greedy argmax (lowest id on ties), then
+ * engine.Forward(best, pos) and TokenIDs[pos] = best.  Only the chosen id
+ * crosses to the host.  The new normX becomes current; c2h_restore_normx
+ * undoes that for a caller that rejects the token (stop strings,
+ * c2slm.go:205-216). */
+int c2h_step(c2h_ctx* ctx, int32_t pos, float penalty, int32_t im_end, int32_t eos, int32_t* next_token);
+
+/* Makes the normX that was current before the last c2h_step current again. */
+int c2h_restore_normx(c2h_ctx* ctx);
+
+/* Copies the current normX (n_embd floats) to the host. */
+int c2h_get_normx(c2h_ctx* ctx, float* normx_out);
+
+/* Copies K or V (which = 0/1) of one layer/KV head for positions [0, n) to
+ * the host ([n][head_dim] floats): KVCache.GetKey/GetValue
+ * (engine/kvcache.go:159-169). */
+int c2h_get_kv(c2h_ctx* ctx, int32_t which, int32_t layer, int32_t kv_head, int32_t n, float* out);
+
+/* ---- kernel entry points (tensor/ops.go operators) ----------------------- */
+
+/* tensor.QuantizeRowQ8_K (tensor/ops.go:170-172): floor(cols/256) blocks of
+ * 292 bytes (f32 d | int8 qs[256] | int16 bsums[16]) from host x. */
+int c2h_quantize_q8k(c2h_ctx* ctx, const float* x, int32_t cols, void* q8k_out);
+
+/* tensor.GEMVQ4_K_Q8_K / GEMVQ6_K_Q8_K / GEMVQ8_0 (tensor/ops.go:77-203)
+ * on host buffers.  w is the reference's native layout (row stride as
+ * above); xq is the Q8_K row for Q4_K/Q6_K and the f32 vector for Q8_0.
+ * isums_out (nullable, K-quants only) receives the integer sums: Q4_K 8 per
+ * (row, super-block), the 32-element sums in q8 order; Q6_K 1 per
+ * (row, super-block), the scaled super-block sum. */
+int c2h_gemv(c2h_ctx* ctx, int32_t ggml_type, const void* w, const void* xq, int32_t rows, int32_t cols, float* y,
+             int32_t* isums_out);
+
+/* Device-layout size and host-side repack of one weight tensor
+ * (native reference layout -> the layout the kernels read).  Byte count
+ * per row is unchanged except for alignment padding of Q8_0 rows whose
+ * block count is not a multiple of 4. */
+size_t c2h_packed_size(int32_t ggml_type, int64_t rows, int64_t cols);
+int c2h_pack_weights(int32_t ggml_type, int64_t rows, int64_t cols, const void* native, size_t native_bytes,
+                     void* packed, size_t packed_bytes);
+
+/* Device-pointer forms for device-resident pipelines and measurement; they
+ * run on the context stream and return without synchronising
+ * (c2h_sync waits).  w_packed is in the c2h_pack_weights layout. */
+int c2h_quantize_q8k_dev(c2h_ctx* ctx, const float* x, int32_t cols, void* q8k_out);
+int c2h_gemv_dev(c2h_ctx* ctx, int32_t ggml_type, const void* w_packed, const void* xq, int32_t rows, int32_t cols,
+                 float* y, int32_t* isums_out);
+int c2h_sync(c2h_ctx* ctx);
+
+/* ---- measurement --------------------------------------------------------- */
+
+/* Average device time (ms) of `iters` back-to-back launches of the fused
+ * vocab projection + penalty + argmax kernel on the context stream, bracketed
+ * by HIP events on that stream; uses the current normX and pos. */
+int c2h_time_vocab(c2h_ctx* ctx, int32_t iters, int32_t pos, float* ms_per_launch);
+
+/* Average device time (ms) of `iters` decode steps (graph replays) at
+ * positions pos, pos+1, ...; tokens are fed back on the device. */
+int c2h_time_steps(c2h_ctx* ctx, int32_t pos, int32_t iters, float penalty, int32_t im_end, int32_t eos,
+                   float* ms_per_step);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* C2H_H */

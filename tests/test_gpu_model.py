@@ -1,0 +1,118 @@
+"""Model-level parity on the GPU: engine.Forward, ComputeLogits and the
+greedy generate loop through libc2h.so against the oracle on the same
+synthetic GGUF weights.  Everything is compared bit for bit; the greedy
+stream must be identical."""
+import numpy as np
+import pytest
+
+from c2slm_amd import _lib as H
+from c2slm_amd import gguf as G
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+PENALTY = 1.15  # c2slm.go:165,167
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def open_pair(path, max_ctx, threads=16):
+    gf = G.GGUFFile(path)
+    desc = H.desc_from_gguf(gf, max_ctx=max_ctx)
+    ctx = H.Ctx(desc)
+    H.load_gguf_into(ctx, gf)
+    orc = O.OracleEngine(gf, max_ctx=max_ctx, n_threads=threads)
+    _, im_end, eos = G.special_token_ids(gf)
+    return gf, ctx, orc, im_end, eos
+
+
+@pytest.fixture(scope="module")
+def tiny(tiny_model_path):
+    gf, ctx, orc, im_end, eos = open_pair(tiny_model_path, 512)
+    yield gf, ctx, orc, im_end, eos
+    ctx.close()
+    orc.close()
+
+
+def test_forward_bitexact_with_kv(tiny):
+    gf, ctx, orc, _, _ = tiny
+    rng = np.random.default_rng(1)
+    toks = rng.integers(0, 4096, 12)
+    toks[3] = -5      # invalid ids embed row 0 (engine/model.go:222-224)
+    toks[7] = 99999
+    for p, t in enumerate(toks):
+        got = ctx.forward(int(t), p)
+        want = orc.forward(int(t), p)
+        assert np.array_equal(bits(got), bits(want)), p
+    kv = orc.kv()
+    n = len(toks)
+    for which in (0, 1):
+        for layer in range(2):
+            for h in range(2):
+                assert np.array_equal(bits(ctx.kv(which, layer, h, n)), bits(kv[which, layer, h, :n]))
+
+
+def test_logits_bitexact(tiny):
+    gf, ctx, orc, _, _ = tiny
+    ctx.forward(17, 0)
+    nx = orc.forward(17, 0)
+    assert np.array_equal(bits(ctx.normx()), bits(nx))
+    assert np.array_equal(bits(ctx.logits()), bits(orc.compute_logits(nx)))
+
+
+def gpu_generate(ctx, prompt, max_new, im_end, eos, penalty=PENALTY):
+    """The c2slm.go:92-117 ingest and :144-226 loop over the C ABI."""
+    ctx.set_token_ids(0, prompt)
+    for p, t in enumerate(prompt):
+        ctx.forward(int(t), p, want_normx=False)
+    out = []
+    pos = len(prompt)
+    for _ in range(max_new):
+        best = ctx.step(pos, penalty, im_end, eos)
+        out.append(best)
+        pos += 1
+        if best in (im_end, eos):
+            break
+    return np.array(out, np.int32)
+
+
+def oracle_generate(orc, prompt, max_new, im_end, eos, penalty=PENALTY):
+    orc.ingest_from(0, prompt)
+    return orc.generate(max_new, im_end, eos, penalty)
+
+
+def test_greedy_stream_tiny(tiny):
+    gf, ctx, orc, im_end, eos = tiny
+    rng = np.random.default_rng(32)
+    prompt = rng.integers(0, 4096, 32).astype(np.int32)
+    got = gpu_generate(ctx, prompt, 64, im_end, eos)
+    orc2 = O.OracleEngine(gf, max_ctx=512, n_threads=16)
+    want = oracle_generate(orc2, prompt, 64, im_end, eos)
+    assert np.array_equal(got, want)
+    want_nx = np.ctypeslib.as_array(O.lib().orc_state_normx(orc2.state), shape=(896,)).copy()
+    assert np.array_equal(bits(ctx.normx()), bits(want_nx))
+    orc2.close()
+
+
+def test_session_differential_ingestion(tiny):
+    # c2slm_test.go:60-105: prefix then suffix == one shot, bit for bit
+    gf, ctx, orc, _, _ = tiny
+    toks = np.arange(100, 120, dtype=np.int32)
+    for p, t in enumerate(toks):
+        ctx.forward(int(t), p, want_normx=False)
+    ref = ctx.logits()
+    for p, t in enumerate(toks[:10]):
+        ctx.forward(int(t), p, want_normx=False)
+    for p, t in enumerate(toks[10:], start=10):
+        ctx.forward(int(t), p, want_normx=False)
+    assert np.array_equal(bits(ctx.logits()), bits(ref))
+
+
+def test_position_bounds_rejected(tiny):
+    gf, ctx, orc, _, _ = tiny
+    with pytest.raises(H.C2hError):
+        ctx.forward(1, 512)
+    with pytest.raises(H.C2hError):
+        ctx.forward(1, -1)

@@ -1,0 +1,621 @@
+"""Pins of the CPU oracle (oracle/c2slm_oracle.c).
+
+Every function of the oracle is checked against something it does not
+restate: the reference's golden values and fixtures, the reference's own C
+dequantisation oracles (oracle/_ref, built from the reference checkout),
+closed forms, float64 textbook results, brute-force integer sums, and
+hand-derived known answers chosen so that a wrong summation order, a dropped
+term, a sign or an index error changes the answer.
+"""
+import math
+import struct
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests import refdequant as R
+
+L = O.lib()
+F32P, U8P, I32P = O.F32P, O.U8P, O.I32P
+
+
+def f32bits(x):
+    return struct.unpack("<I", struct.pack("<f", x))[0]
+
+
+def fbits(x):
+    return np.float32(x).view(np.uint32)
+
+
+# ------------------------------------------------------------------ fp16
+
+
+def test_fp16_reference_cases():
+    # tensor/ops_test.go:10-28
+    for h, want in [(0x0000, 0.0), (0x3C00, 1.0), (0xBC00, -1.0), (0x4000, 2.0), (0x3555, 0.33325195)]:
+        assert abs(L.orc_fp16_tensor(h) - want) <= 1e-4
+        assert abs(L.orc_fp16_simd(h) - want) <= 1e-4
+
+
+def test_fp16_exhaustive_against_ieee():
+    hs = np.arange(65536, dtype=np.uint32)
+    ieee = hs.astype(np.uint16).view(np.float16).astype(np.float32).view(np.uint32)
+    simd = np.array([L.orc_fp16_simd_bits(int(h)) for h in hs], np.uint32)
+    tens = np.array([L.orc_fp16_tensor_bits(int(h)) for h in hs], np.uint32)
+    exp = (hs >> 10) & 31
+    finite = exp != 31
+    # finite values are exact IEEE conversions; the simd LUT maps -0 to +0
+    assert np.array_equal(tens[finite], ieee[finite])
+    want_simd = ieee.copy()
+    want_simd[0x8000] = 0
+    assert np.array_equal(simd[finite], want_simd[finite])
+    # Inf/NaN keep their payload (c2_tensor_dot_q8_0_gen.go:56-59)
+    nonf = ~finite
+    payload = ((hs >> 15) << 31) | 0x7F800000 | ((hs & 0x3FF) << 13)
+    assert np.array_equal(simd[nonf], payload[nonf])
+    assert np.array_equal(tens[nonf], payload[nonf])
+
+
+# ------------------------------------------------------------------ Q8_K
+
+
+def ref_fixture_x(cols):
+    # internal/simd/c2_tensor_dot_q4_k_q8_k_test.go:170-172
+    return np.array([((i % 17) - 8) * 0.125 for i in range(cols)], np.float32)
+
+
+def test_q8k_known_answer_reference_fixture():
+    x = ref_fixture_x(512)
+    y = O.quantize_row_q8k(x)
+    for b in range(2):
+        blk = y[b * 292:(b + 1) * 292]
+        # amax = 1.0 -> d = 1/127 rounded to f32
+        assert blk[0:4].view("<u4")[0] == fbits(np.float32(1.0) / np.float32(127.0))
+        q = blk[4:260].view(np.int8)
+        for e in range(256):
+            k = ((b * 256 + e) % 17) - 8
+            v = Fraction(127 * k, 8)  # x*127 exactly
+            r = math.floor(abs(v) + Fraction(1, 2))  # round half away from zero
+            assert q[e] == (r if v >= 0 else -r), (b, e)
+        bs = blk[260:292].view("<i2")
+        assert np.array_equal(bs, q.reshape(16, 16).astype(np.int32).sum(1))
+
+
+def test_q8k_invariants_random():
+    rng = np.random.default_rng(7)
+    x = rng.normal(size=4864).astype(np.float32) * np.float32(37.0)
+    y = O.quantize_row_q8k(x)
+    for b in range(19):
+        blk = y[b * 292:(b + 1) * 292]
+        xb = x[b * 256:(b + 1) * 256].astype(np.float64)
+        d = float(blk[0:4].view("<f4")[0])
+        q = blk[4:260].view(np.int8).astype(np.float64)
+        amax = np.abs(xb).max()
+        assert d == float(np.float32(np.float32(amax) / np.float32(127)))
+        assert np.abs(q).max() <= 127
+        assert abs(q[np.argmax(np.abs(xb))]) == 127
+        assert np.all(np.abs(xb - q * d) <= d * 0.5 * (1 + 1e-5))
+        assert np.array_equal(blk[260:292].view("<i2"), q.reshape(16, 16).sum(1).astype(np.int16))
+
+
+def test_q8k_floor_semantics_and_zero_block():
+    x = np.zeros(896, np.float32)
+    x[768:] = 5.0  # beyond floor(896/256)*256: never read
+    y = O.quantize_row_q8k(x, y_len=4 * 292)
+    assert len(y) == 4 * 292 and not y.any()
+    # a zero block clears the destination from its qs to the end of the slice
+    buf = np.full(3 * 292, 0xAB, np.uint8)
+    x2 = np.zeros(512, np.float32)
+    x2[300] = 1.0
+    L.orc_quantize_row_q8k(O.ptr(x2, F32P), O.ptr(buf, U8P), 512, len(buf))
+    assert not buf[4:292].any()
+    assert buf[292:292 + 4].view("<f4")[0] == np.float32(1) / np.float32(127)
+    assert not buf[2 * 292:].any()  # cleared by block 0, never rewritten
+
+
+def test_q8k_nan_follows_go_amd64_conversion():
+    # int(NaN) on amd64 is 0x8000000000000000 -> clamped to -127; NaN never wins amax
+    x = np.zeros(256, np.float32)
+    x[3] = 2.0
+    x[10] = np.nan
+    y = O.quantize_row_q8k(x)
+    q = y[4:260].view(np.int8)
+    assert q[3] == 127 and q[10] == -127
+
+
+# ------------------------------------------------------------------ Q4_K
+
+
+def q4k_fixture_block():
+    # tensor/oracle_q4_k_test.go:140-149
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = [0x00, 0x3C]
+    blk[2:4] = [0x00, 0x38]
+    blk[4:16] = [(i * 37 + 193) & 0xFF for i in range(12)]
+    blk[16:144] = [(i * 13 + 7) & 0xFF for i in range(128)]
+    return blk
+
+
+def hostile_blocks(size, scale_slots):
+    out = []
+    for val in (0x00, 0xFF, 0xAA, 0x55):
+        b = np.full(size, val, np.uint8)
+        for off, bts in scale_slots:
+            b[off:off + 2] = bts
+        out.append(b)
+    return out
+
+
+@pytest.mark.skipif(not R.ref_available("q4_k"), reason="oracle/_ref not built (needs the reference checkout)")
+def test_q4k_unit_vectors_vs_reference_c_oracle():
+    blocks = [q4k_fixture_block()] + hostile_blocks(144, [(0, [0x00, 0x3C]), (2, [0x00, 0x38])])
+    for blk in blocks:
+        want, _ = R.run_ref_dequant("q4_k", blk.tobytes())
+        for i in range(256):
+            got = L.orc_dot_q4k_q8k(O.ptr(blk, U8P), O.ptr(R.q8k_onehot(i), U8P), 256)
+            w = float(want[i])
+            assert got == w and (f32bits(got) == f32bits(w) or got == 0.0), (i, got, w)
+
+
+@pytest.mark.skipif(not R.ref_available("q4_k"), reason="oracle/_ref not built (needs the reference checkout)")
+def test_q4k_integer_sums_vs_reference_layout():
+    rng = np.random.default_rng(11)
+    for trial in range(8):
+        blk = rng.integers(0, 256, 144, dtype=np.uint8)
+        # d = 1, dmin = 0, every scale 1, every min 0: the C oracle returns the raw nibbles
+        unit = blk.copy()
+        unit[0:4] = [0x00, 0x3C, 0x00, 0x00]
+        unit[4:16] = [1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1]
+        nib, _ = R.run_ref_dequant("q4_k", unit.tobytes())
+        nib = nib.astype(np.int64)
+        assert np.all((nib >= 0) & (nib <= 15))
+        q8 = np.zeros(292, np.uint8)
+        q8[0:4] = np.frombuffer(np.float32(0.5).tobytes(), np.uint8)
+        qv = rng.integers(-127, 128, 256).astype(np.int8)
+        q8[4:260] = qv.view(np.uint8)
+        q8[260:292] = qv.astype(np.int16).reshape(16, 16).sum(1).astype("<i2").view(np.uint8)
+        s = np.zeros(8, np.int32)
+        L.orc_q4k_block_isums(O.ptr(blk, U8P), O.ptr(q8, U8P), O.ptr(s, I32P))
+        want = (nib * qv.astype(np.int64)).reshape(8, 32).sum(1)
+        assert np.array_equal(s, want), trial
+
+
+def test_q4k_gemv_vs_float64_dequant():
+    rng = np.random.default_rng(5)
+    from c2slm_amd import gguf as G
+    for rows, cols in [(64, 896), (16, 4864)]:
+        nb = cols // 256
+        w = G.synth_q4_k(rng, rows * nb)
+        x = rng.normal(size=cols).astype(np.float32)
+        q8k = O.quantize_row_q8k(x)
+        y = O.gemv(w, G.Q4_K, rows, cols, q8k=q8k)
+        wd = R.dequant_q4k_f64(w).reshape(rows, nb * 256)
+        xd = R.q8k_dequant_f64(q8k, nb)
+        want = wd @ xd
+        scale = np.abs(wd).sum(1) * np.abs(xd).max()
+        assert np.all(np.abs(y - want) <= 1e-5 * scale), (rows, cols)
+
+
+def test_q4k_gemv2_reference_fixture_rows_match_dot():
+    # internal/simd/c2_tensor_gemv2_q4_k_q8_k_test.go:165-206: both rows through the row function
+    cols = 512
+    w0 = np.zeros(2 * 144, np.uint8)
+    w1 = np.zeros(2 * 144, np.uint8)
+    for b in range(2):
+        b0 = w0[b * 144:(b + 1) * 144]
+        b0[0:4] = [0x00, 0x3C, 0x00, 0x38]
+        b0[4:16] = [(b * 37 + i * 19 + 17) & 0xFF for i in range(12)]
+        b0[16:] = [(b * 13 + i * 7 + 3) & 0xFF for i in range(128)]
+        b1 = w1[b * 144:(b + 1) * 144]
+        b1[0:4] = [0x00, 0x3A, 0x00, 0x34]
+        b1[4:16] = [(b * 41 + i * 23 + 19) & 0xFF for i in range(12)]
+        b1[16:] = [(b * 17 + i * 11 + 5) & 0xFF for i in range(128)]
+    q8k = O.quantize_row_q8k(ref_fixture_x(cols))
+    xd = R.q8k_dequant_f64(q8k, 2)
+    for w in (w0, w1):
+        got = L.orc_dot_q4k_q8k(O.ptr(w, U8P), O.ptr(q8k, U8P), cols)
+        want = R.dequant_q4k_f64(w).reshape(-1) @ xd
+        assert abs(got - want) <= 1e-5 * abs(want) + 1e-3
+
+
+# ------------------------------------------------------------------ Q6_K
+
+
+def q6k_golden_weights():
+    # internal/simd/c2_tensor_gemv2_q6_k_q8_k_test.go:17-43
+    w0 = np.zeros(2 * 210, np.uint8)
+    w1 = np.zeros(2 * 210, np.uint8)
+    for b in range(2):
+        b0 = w0[b * 210:(b + 1) * 210]
+        b0[208:210] = [0x00, 0x3C]
+        b0[0:128] = [(b * 37 + i * 19 + 17) & 0xFF for i in range(128)]
+        b0[128:192] = [(b * 13 + i * 7 + 3) & 0xFF for i in range(64)]
+        b0[192:208] = [(i * 3 - 8) & 0xFF for i in range(16)]
+        b1 = w1[b * 210:(b + 1) * 210]
+        b1[208:210] = [0x00, 0x38]
+        b1[0:128] = [(b * 41 + i * 23 + 19) & 0xFF for i in range(128)]
+        b1[128:192] = [(b * 17 + i * 11 + 5) & 0xFF for i in range(64)]
+        b1[192:208] = [(i * 2 - 7) & 0xFF for i in range(16)]
+    return w0, w1
+
+
+def test_q6k_golden_values():
+    # want0/want1 at c2_tensor_gemv2_q6_k_q8_k_test.go:55-56, tolerance 1e-2 (:64-69)
+    w0, w1 = q6k_golden_weights()
+    q8k = O.quantize_row_q8k(ref_fixture_x(512))
+    got0 = L.orc_dot_q6k_q8k(O.ptr(w0, U8P), O.ptr(q8k, U8P), 512)
+    got1 = L.orc_dot_q6k_q8k(O.ptr(w1, U8P), O.ptr(q8k, U8P), 512)
+    assert abs(got0 - (-8705.69238281)) <= 1e-2
+    assert abs(got1 - 3759.21655273) <= 1e-2
+    # Sharper: the golden row 0 is exactly the FMA-contracted accumulation
+    # acc = fma(f32(isum), d*q8d, acc) of the same integer sums, while the Go
+    # source (two roundings, as restated) lands 1 ulp away; row 1 agrees
+    # either way.  This pins every integer super-block sum and scale product.
+    import ctypes
+    libm = ctypes.CDLL("libm.so.6")
+    libm.fmaf.restype = ctypes.c_float
+    libm.fmaf.argtypes = [ctypes.c_float] * 3
+    for w, want, plain in ((w0, -8705.69238281, got0), (w1, 3759.21655273, got1)):
+        acc_fma = 0.0
+        acc = np.float32(0.0)
+        for b in range(2):
+            blk = w[b * 210:(b + 1) * 210]
+            qb = q8k[b * 292:(b + 1) * 292]
+            isum = L.orc_q6k_block_isum(O.ptr(np.ascontiguousarray(blk), U8P), O.ptr(np.ascontiguousarray(qb), U8P))
+            d = np.float32(L.orc_fp16_simd(int(blk[208]) | (int(blk[209]) << 8)))
+            sc = d * qb[0:4].view("<f4")[0]
+            acc_fma = libm.fmaf(float(np.float32(isum)), float(sc), acc_fma)
+            acc = acc + np.float32(isum) * sc
+        assert np.float32(acc_fma) == np.float32(want)
+        assert acc == np.float32(plain)
+    assert got1 == np.float32(3759.21655273)
+    assert abs(got0 - np.float32(-8705.69238281)) == np.spacing(np.float32(8705.69))
+
+
+def q6k_fixture_block():
+    # tensor/oracle_q6_k_test.go:141-152
+    blk = np.zeros(210, np.uint8)
+    blk[0:128] = [(i * 19 + 5) & 0xFF for i in range(128)]
+    blk[128:192] = [(i * 29 + 17) & 0xFF for i in range(64)]
+    blk[192:208] = [(i * 7 - 31) & 0xFF for i in range(16)]
+    blk[208:210] = [0x00, 0x3C]
+    return blk
+
+
+@pytest.mark.skipif(not R.ref_available("q6_k"), reason="oracle/_ref not built (needs the reference checkout)")
+def test_q6k_unit_vectors_vs_reference_c_oracle():
+    blocks = [q6k_fixture_block()] + hostile_blocks(210, [(208, [0x00, 0x3C])])
+    for blk in blocks:
+        want, _ = R.run_ref_dequant("q6_k", blk.tobytes())
+        for i in range(256):
+            got = L.orc_dot_q6k_q8k(O.ptr(blk, U8P), O.ptr(R.q8k_onehot(i), U8P), 256)
+            w = float(want[i])
+            assert got == w, (i, got, w)
+
+
+@pytest.mark.skipif(not R.ref_available("q6_k"), reason="oracle/_ref not built (needs the reference checkout)")
+def test_q6k_integer_sum_vs_reference_layout():
+    rng = np.random.default_rng(13)
+    for trial in range(8):
+        blk = rng.integers(0, 256, 210, dtype=np.uint8)
+        blk[192:208] = rng.integers(-63, 64, 16).astype(np.int8).view(np.uint8)
+        unit = blk.copy()
+        unit[208:210] = [0x00, 0x3C]  # d = 1: the C oracle returns sc*(q6-32) exactly
+        scaled, _ = R.run_ref_dequant("q6_k", unit.tobytes())
+        scaled = scaled.astype(np.int64)
+        q8 = np.zeros(292, np.uint8)
+        q8[0:4] = np.frombuffer(np.float32(0.25).tobytes(), np.uint8)
+        qv = rng.integers(-127, 128, 256).astype(np.int8)
+        q8[4:260] = qv.view(np.uint8)
+        q8[260:292] = qv.astype(np.int16).reshape(16, 16).sum(1).astype("<i2").view(np.uint8)
+        got = L.orc_q6k_block_isum(O.ptr(blk, U8P), O.ptr(q8, U8P))
+        assert got == int((scaled * qv.astype(np.int64)).sum()), trial
+
+
+def test_q6k_gemv_vs_float64_dequant():
+    rng = np.random.default_rng(6)
+    from c2slm_amd import gguf as G
+    for rows, cols in [(32, 4864), (128, 896)]:
+        nb = cols // 256
+        w = G.synth_q6_k(rng, rows * nb)
+        x = rng.normal(size=cols).astype(np.float32)
+        q8k = O.quantize_row_q8k(x)
+        y = O.gemv(w, G.Q6_K, rows, cols, q8k=q8k)
+        wd = R.dequant_q6k_f64(w).reshape(rows, nb * 256)
+        xd = R.q8k_dequant_f64(q8k, nb)
+        want = wd @ xd
+        scale = np.abs(wd).sum(1) * np.abs(xd).max()
+        assert np.all(np.abs(y - want) <= 1e-5 * scale)
+
+
+# ------------------------------------------------------------------ Q8_0
+
+
+def q8_0_row(vals, d_bits=0x3C00):
+    vals = np.asarray(vals, np.int64).reshape(-1, 32)
+    out = np.zeros((len(vals), 34), np.uint8)
+    out[:, 0] = d_bits & 0xFF
+    out[:, 1] = d_bits >> 8
+    out[:, 2:] = vals.astype(np.int8).view(np.uint8)
+    return out.reshape(-1)
+
+
+def test_q8_0_unit_vectors():
+    # tensor/oracle_c_test.go:151-168
+    blk = q8_0_row([(i * 2 - 31) for i in range(32)])
+    for i in range(32):
+        x = np.zeros(32, np.float32)
+        x[i] = 1.0
+        assert L.orc_dot_q8_0(O.ptr(blk, U8P), O.ptr(x, F32P), 32) == float(np.int8(i * 2 - 31))
+
+
+def test_q8_0_summation_order_known_answers():
+    big = float(2 ** 24)
+    one = q8_0_row(np.ones(32))
+    # inside a lane: (w0x0 + w8x8) + (w16x16 + w24x24) = (2^24+1) + 2 -> 2^24+2
+    x = np.zeros(32, np.float32)
+    x[[0, 8, 16, 24]] = [big, 1, 1, 1]
+    assert L.orc_dot_q8_0(O.ptr(one, U8P), O.ptr(x, F32P), 32) == big + 2
+    # across lanes: ((((((a0+a1)+a2)+a3)+a4)+a5)+a6)+a7 -> 2^24 (each +1 ties to even)
+    x = np.zeros(32, np.float32)
+    x[0] = big
+    x[1:8] = 1
+    assert L.orc_dot_q8_0(O.ptr(one, U8P), O.ptr(x, F32P), 32) == big
+    # across blocks: acc[0] += per-block sum, sequentially -> 2^24
+    three = q8_0_row(np.ones(96))
+    x = np.zeros(96, np.float32)
+    x[0] = big
+    x[32] = 1
+    x[64] = 1
+    assert L.orc_dot_q8_0(O.ptr(three, U8P), O.ptr(x, F32P), 96) == big
+
+
+def test_q8_0_reference_fixture_vs_float64():
+    # internal/simd/c2_tensor_dot_q8_0_test.go:63-76
+    w = np.zeros(28 * 34, np.uint8)
+    x = np.zeros(896, np.float32)
+    for b in range(28):
+        w[b * 34:b * 34 + 2] = [0x00, 0x3C]
+        for i in range(32):
+            w[b * 34 + 2 + i] = np.uint8(np.int8((b * 7 + i * 13) % 127))
+            x[b * 32 + i] = np.float32(((i % 5) - 2) * 0.1)
+    got = L.orc_dot_q8_0(O.ptr(w, U8P), O.ptr(x, F32P), 896)
+    want = R.dequant_q8_0_f64(w).reshape(-1) @ x.astype(np.float64)
+    assert abs(got - want) <= 1e-5 * max(1.0, abs(want))
+
+
+# ----------------------------------------------------------- small ops
+
+
+def rmsnorm(x, w, eps=1e-6):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    L.orc_rmsnorm(O.ptr(out, F32P), O.ptr(x, F32P), O.ptr(w, F32P), len(x), eps)
+    return out
+
+
+def test_rmsnorm_reference_case():
+    out = rmsnorm([1, 2, 3, 4], [1, 1, 1, 1])  # tensor/ops_test.go:30-43
+    assert abs(out[0] - 1.0 / math.sqrt(7.5)) <= 1e-5
+
+
+def test_rmsnorm_sequential_sum_known_answer():
+    # squares 2^24,1,1,1: sequential f32 sum stays 2^24 (pairwise would be 2^24+2),
+    # mean 2^22, inv exactly 2^-11
+    out = rmsnorm([4096, 1, 1, 1], [1, 1, 1, 1])
+    assert out[1] == np.float32(2.0 ** -11)
+    assert out[0] == np.float32(4096 * 2.0 ** -11)
+
+
+def test_rmsnorm_vs_float64():
+    rng = np.random.default_rng(3)
+    x = (rng.normal(size=896) * 1e3).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 896).astype(np.float32)
+    out = rmsnorm(x, w)
+    xd = x.astype(np.float64)
+    want = xd / np.sqrt((xd * xd).mean() + 1e-6) * w
+    assert np.allclose(out, want, rtol=1e-5, atol=1e-6)
+
+
+def rope_table(maxlen, hd, theta=1e6):
+    c = np.empty(maxlen * hd // 2, np.float32)
+    s = np.empty_like(c)
+    L.orc_rope_table(O.ptr(c, F32P), O.ptr(s, F32P), maxlen, hd, theta)
+    return c, s
+
+
+def rope_apply(vec, nh, pos, c, s, maxlen, hd):
+    v = np.ascontiguousarray(vec, np.float32).copy()
+    L.orc_rope_apply(O.ptr(v, F32P), len(v), nh, pos, O.ptr(c, F32P), O.ptr(s, F32P), maxlen, hd)
+    return v
+
+
+def test_rope_table_angles():
+    c, s = rope_table(2048, 64)
+    p = np.arange(2048)[:, None].astype(np.float64)
+    i = np.arange(32)[None, :]
+    ang = p * (1e6 ** (-(2.0 * i) / 64.0))
+    assert np.allclose(c.reshape(2048, 32), np.cos(ang), atol=2e-7)
+    assert np.allclose(s.reshape(2048, 32), np.sin(ang), atol=2e-7)
+
+
+def test_rope_apply_reference_cases():
+    # tensor/ops_test.go:45-61 and tensor/rope_test.go:24-66
+    c, s = rope_table(16, 64)
+    v = rope_apply(np.ones(64), 1, 0, c, s, 16, 64)
+    assert np.all(v == 1.0)
+    c8, s8 = rope_table(16, 8)
+    orig = np.arange(1, 9, dtype=np.float32)
+    for pos in (16, 1016, -1):
+        assert np.array_equal(rope_apply(orig, 1, pos, c8, s8, 16, 8), orig)
+    assert np.array_equal(rope_apply(orig, 2, 1, c8, s8, 16, 8), orig)
+    c4, s4 = rope_table(4, 8)
+    v = rope_apply([1, 0, 0, 0, 0, 0, 0, 0], 1, 1, c4, s4, 4, 8)
+    assert 0 < v[0] < 1 and abs(v[4]) > 1e-9
+    # NeoX rotate-half direction: (x0, x_half) -> (x0 cos - x_half sin, x0 sin + x_half cos)
+    assert v[0] == c4[4] and v[4] == s4[4] and v[4] > 0
+
+
+def test_rope_preserves_pair_norms():
+    rng = np.random.default_rng(2)
+    c, s = rope_table(512, 64)
+    vec = rng.normal(size=14 * 64).astype(np.float32)
+    out = rope_apply(vec, 14, 333, c, s, 512, 64)
+    a = vec.reshape(14, 2, 32).astype(np.float64)
+    b = out.reshape(14, 2, 32).astype(np.float64)
+    assert np.allclose(np.hypot(a[:, 0], a[:, 1]), np.hypot(b[:, 0], b[:, 1]), rtol=1e-6)
+
+
+def softmax(x):
+    x = np.ascontiguousarray(x, np.float32).copy()
+    L.orc_softmax(O.ptr(x, F32P), len(x))
+    return x
+
+
+def test_softmax_reference_and_float64():
+    y = softmax([1, 2, 3])  # tensor/ops_test.go:63-79
+    assert abs(float(y.sum()) - 1.0) <= 1e-6 and y[0] < y[1] < y[2]
+    rng = np.random.default_rng(4)
+    x = (rng.normal(size=1000) * 5).astype(np.float32)
+    xd = x.astype(np.float64)
+    want = np.exp(xd - xd.max())
+    want /= want.sum()
+    assert np.allclose(softmax(x), want, rtol=1e-5, atol=1e-9)
+    z = softmax(np.array([np.nan, 1, 2], np.float32))
+    assert np.all(np.isnan(z))
+
+
+def lcg_fixture(hd, pos, seed):
+    # internal/simd/c2_tensor_attn_test.go:28-67
+    state = np.uint32(seed)
+    vals = []
+
+    def nxt():
+        nonlocal state
+        state = np.uint32((int(state) * 1664525 + 1013904223) & 0xFFFFFFFF)
+        return np.float32(((int(state) >> 8) & 0xFFFFFF) / float(0x1000000))
+
+    q = np.array([nxt() * 2 - 1 for _ in range(hd)], np.float32)
+    nk = (pos + 1) * hd
+    k = np.array([nxt() * 2 - 1 for _ in range(nk)], np.float32)
+    v = np.array([np.float32(0.25) + np.float32(0.5) * nxt() for _ in range(nk)], np.float32)
+    sc = np.array([np.float32(0.25) + np.float32(0.5) * nxt() for _ in range(pos + 1)], np.float32)
+    return q, k, v, sc
+
+
+def attn_qk(q, k, pos, hd, scale):
+    out = np.empty(pos + 1, np.float32)
+    L.orc_attn_qk(O.ptr(q, F32P), O.ptr(k, F32P), pos, hd, scale, O.ptr(out, F32P), hd)
+    return out
+
+
+def attn_av(sc, v, pos, hd):
+    out = np.empty(hd, np.float32)
+    L.orc_attn_av(O.ptr(sc, F32P), O.ptr(v, F32P), pos, hd, O.ptr(out, F32P), hd)
+    return out
+
+
+def max_rel(got, want):
+    ref = np.maximum(np.abs(want), 1.0)
+    return float(np.max(np.abs(got - want) / ref))
+
+
+@pytest.mark.parametrize("hd,pos,seed", [(64, 0, 7), (64, 1, 7), (64, 63, 11), (64, 255, 13), (64, 256, 17),
+                                         (64, 2048, 19), (128, 128, 29)])
+def test_attention_kernels_vs_textbook(hd, pos, seed):
+    # cases from internal/simd/c2_tensor_attn_test.go:136-150, tolerance 1e-5 (:134)
+    q, k, v, sc = lcg_fixture(hd, pos, seed)
+    got = attn_qk(q, k, pos, hd, 0.125)
+    want = (k.reshape(pos + 1, hd).astype(np.float64) @ q.astype(np.float64)) * 0.125
+    assert max_rel(got, want) <= 1e-5
+    got = attn_av(sc, v, pos, hd)
+    want = sc.astype(np.float64) @ v.reshape(pos + 1, hd).astype(np.float64)
+    assert max_rel(got, want) <= 1e-5
+
+
+def test_attention_fma_known_answers():
+    a = np.float32(1 + 2.0 ** -23)
+    c = np.float32(-(1 + 2.0 ** -22))
+    # QK: lane 0 of acc0 sees q0*k0 then q16*k16: fma keeps 2^-46
+    q = np.zeros(64, np.float32)
+    k = np.zeros(64, np.float32)
+    q[0], k[0] = c, 1
+    q[16], k[16] = a, a
+    assert attn_qk(q, k, 0, 64, 1.0)[0] == np.float32(2.0 ** -46)
+    # AV: one fma chain per dim over positions
+    sc = np.array([1, a], np.float32)
+    v = np.zeros(128, np.float32)
+    v[0] = c
+    v[64] = a
+    assert attn_av(sc, v, 1, 64)[0] == np.float32(2.0 ** -46)
+
+
+def swiglu(g, u):
+    g = np.ascontiguousarray(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    out = np.empty_like(g)
+    L.orc_swiglu(O.ptr(out, F32P), O.ptr(g, F32P), O.ptr(u, F32P), len(g))
+    return out
+
+
+def test_swiglu_reference_precision():
+    # internal/simd/c2_tensor_swiglu_test.go:8-37
+    n = 6144
+    g = np.array([(i - 3072) / 256.0 for i in range(n)], np.float32)
+    u = np.array([(i % 100) / 100.0 for i in range(n)], np.float32)
+    gd = g.astype(np.float64)
+    want = (gd / (1 + np.exp(-gd))).astype(np.float32) * u
+    assert np.max(np.abs(swiglu(g, u) - want)) <= 1e-4
+
+
+def test_swiglu_tail_and_extremes():
+    g = np.array([-200, -90, -30, 0, 30, 90, 200, 1.5, 2.5, -2.5, 0.1], np.float32)
+    u = np.full(len(g), 2.0, np.float32)
+    out = swiglu(g, u)
+    gd = g.astype(np.float64)
+    want = gd / (1 + np.exp(-gd)) * 2.0
+    assert np.allclose(out, want, rtol=2e-4, atol=1e-30)
+    assert out[0] == 0.0 and out[6] == np.float32(400.0)
+    # the last n%8 lanes use the float64 formula
+    tail = (np.float32(gd[8:] / (1 + np.exp(-gd[8:])))) * np.float32(2.0)
+    assert np.array_equal(out[8:], tail.astype(np.float32))
+
+
+# ------------------------------------------------------- penalty/argmax
+
+
+def pen_argmax(logits, ids, pos, im_end=-7, eos=-8, penalty=1.15):
+    lg = np.ascontiguousarray(logits, np.float32).copy()
+    t = np.ascontiguousarray(ids, np.int32)
+    r = L.orc_penalty_argmax(O.ptr(lg, F32P), len(lg), O.ptr(t, I32P), pos, im_end, eos, penalty)
+    return r, lg
+
+
+def test_penalty_semantics():
+    p = np.float32(1.15)
+    lg = np.array([0.5, 2.0, -1.0, 3.0, 1.0], np.float32)
+    r, out = pen_argmax(lg, [1, 1, 2, 9, -3, 4], 6, im_end=4)
+    assert out[1] == np.float32(np.float32(2.0) / p) / p  # duplicates compound, in order
+    assert out[2] == np.float32(-1.0) * p  # non-positive logits are multiplied
+    assert out[4] == 1.0  # im_end exempt; ids outside [0, V) skipped
+    assert r == 3
+    # only the last 64 positions count
+    ids = [3] + [0] * 64
+    r, out = pen_argmax(lg, ids, 65)
+    assert out[3] == 3.0
+    r, out = pen_argmax(lg, ids, 64)
+    assert out[3] == np.float32(3.0) / p
+
+
+def test_argmax_ties_and_nan():
+    r, _ = pen_argmax(np.array([1, 5, 5, 2], np.float32), [], 0)
+    assert r == 1
+    r, _ = pen_argmax(np.array([np.nan, 5, 9], np.float32), [], 0)
+    assert r == 0
+    r, _ = pen_argmax(np.array([1, np.nan, 0.5, 3], np.float32), [], 0)
+    assert r == 3
+    r, _ = pen_argmax(np.array([-0.0, 0.0, -1], np.float32), [], 0)
+    assert r == 0
