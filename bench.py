@@ -1,0 +1,154 @@
+"""Decode throughput of the gfx950 path on the Qwen2.5-0.5B-shaped synthetic
+model (24 layers, hidden 896, 14/2 heads, FFN 4864, vocab 151936; Q4_K
+projections, Q6_K attn_v/ffn_down, Q8_0 tied embedding), random-init
+weights written as GGUF v3 from a fixed seed.
+
+Workload per run: a 32-token prompt of uniform random ids is ingested
+(engine.Forward per token, untimed), W greedy steps warm up, then K greedy
+steps are timed.  A step is the reference's generate-loop body
+(c2slm.go:153-222): vocab projection + repetition penalty 1.15 + argmax,
+then Forward(best, pos); only the chosen id crosses to the host each step.
+
+Prints one JSON line (see the contract in the repository's design notes):
+value = K / wall time of the K steps on one GPU, plus the roofline of the
+dominant kernel (the fused vocab projection) and the CPU baseline (the
+oracle on this host's cores, same workload).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+PROMPT_LEN = 32
+SEED = 20261201
+PENALTY = 1.15  # c2slm.go:165,167 (the reference's constant)
+# Algorithmic bytes of one vocab launch at 151936x896 Q8_0: weights 144,643,072
+# + normX 3,584 + 64 window ids 256 + the chosen id 4.
+VOCAB_BYTES = 144_643_072 + 3_584 + 256 + 4
+
+
+def synth_model(path: str):
+    from c2slm_amd import gguf as G
+    if not os.path.exists(path):
+        G.write_synthetic_model(path, G.QWEN05B, seed=SEED)
+    return path
+
+
+def cpu_baseline(gf, prompt, steps, im_end, eos):
+    """The oracle (C restatement of the reference's CPU path) on this host:
+    same prompt ingest, `steps` greedy steps timed."""
+    from oracle import oracle as O
+    threads = min(os.cpu_count() or 1, 16)
+    orc = O.OracleEngine(gf, max_ctx=512, n_threads=threads)
+    orc.ingest_from(0, prompt)
+    t0 = time.perf_counter()
+    toks = orc.generate(steps, -1, -1, PENALTY)  # run exactly `steps` steps
+    dt = time.perf_counter() - t0
+    orc.close()
+    return {"value": round(len(toks) / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"oracle/c2slm_oracle.c (OpenMP, {threads} threads): {PROMPT_LEN}-token prompt ingest "
+                      f"untimed, then {len(toks)} greedy steps timed ({dt:.1f} s)"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--model", default=None, help="GGUF path (default: synthesise the seeded model)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--max-ctx", type=int, default=16384)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    from c2slm_amd import _lib as H
+    from c2slm_amd import gguf as G
+
+    tmpdir = None
+    path = args.model
+    if path is None:
+        tmpdir = tempfile.mkdtemp(prefix="c2slm_bench_")
+        path = os.path.join(tmpdir, "qwen05b_synth.gguf")
+    synth_model(path)
+    gf = G.GGUFFile(path)
+    desc = H.desc_from_gguf(gf, max_ctx=args.max_ctx)
+    ctx = H.Ctx(desc)
+    H.load_gguf_into(ctx, gf)
+    _, im_end, eos = G.special_token_ids(gf)
+    rng = np.random.default_rng(SEED)
+    prompt = rng.integers(0, desc.n_vocab, PROMPT_LEN).astype(np.int32)
+
+    ctx.set_token_ids(0, prompt)
+    for p, t in enumerate(prompt):
+        ctx.forward(int(t), p, want_normx=False)
+    pos = PROMPT_LEN
+    for _ in range(args.warmup):
+        ctx.step(pos, PENALTY, im_end, eos)
+        pos += 1
+    ctx.normx()  # drain
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ctx.step(pos, PENALTY, im_end, eos)
+        pos += 1
+    dt = time.perf_counter() - t0
+    ms_per_step = dt * 1000.0 / args.steps
+    value = args.steps / dt
+
+    vocab_ms = ctx.time_vocab(50, pos)
+    achieved = VOCAB_BYTES / (vocab_ms * 1e-3) / 1e9
+    pipelined_ms = ctx.time_steps(pos, 64, PENALTY, im_end, eos)
+
+    base = None
+    if not args.no_cpu_baseline:
+        base = cpu_baseline(gf, prompt, args.steps, im_end, eos)
+
+    line = {
+        "metric": "decode tok/s @ Qwen2.5-0.5B-shape Q4_K_M, 1 GPU; achieved HBM GB/s",
+        "value": round(value, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 dot / fp32",
+        "data": "synthetic (random-init GGUF v3, seed 20261201; random prompt ids)",
+        "config": {"workload": f"full decode, Qwen2.5-0.5B shape (24L, 896, 14/2 heads, FFN 4864, vocab 151936), "
+                               f"Q4_K/Q6_K/Q8_0, {PROMPT_LEN}-token prompt then greedy steps at positions "
+                               f"{PROMPT_LEN + args.warmup}..{PROMPT_LEN + args.warmup + args.steps - 1}, "
+                               f"repetition penalty {PENALTY}",
+                   "batch": 1, "prompt_len": PROMPT_LEN, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_vocab (151936x896 Q8_0 + penalty + argmax)",
+                     "ms_per_launch": round(vocab_ms, 5)},
+        "cpu_baseline": base,
+        "extra": {"pipelined_ms_per_step": round(pipelined_ms, 4),
+                  "pipelined_tok_s": round(1000.0 / pipelined_ms, 1)},
+    }
+    print(json.dumps(line))
+    ctx.close()
+    if tmpdir:
+        try:
+            os.remove(path)
+            os.rmdir(tmpdir)
+        except OSError:
+            pass
+
+
+if __name__ == "__main__":
+    main()

@@ -11,7 +11,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libc2h.so")
+# C2H_LIB selects another build of the same ABI (for example an instrumented one)
+LIB_PATH = os.environ.get("C2H_LIB") or os.path.join(HERE, "libc2h.so")
 
 C2H_OK = 0
 F32, Q8_0, Q4_K, Q6_K = 0, 8, 12, 14

@@ -67,6 +67,9 @@ struct c2h_ctx {
   bool graphs_ready = false;
   bool use_graphs = true;
   size_t attn_lds = 0;
+  int attn_a_lds = 0;
+  int attn_b_lds = 0;
+  int attn_vchunk = 0;
 
   // kernel-only scratch (c2h_gemv / c2h_quantize_q8k host forms)
   std::vector<void*> scratch;
@@ -122,10 +125,7 @@ void packed_parts(int type, int64_t rows, int64_t cols, size_t* qb, size_t* db) 
       *qb = (size_t)rows * nb_k(cols) * BS_Q6K_PACKED;
       *db = (size_t)rows * nb_k(cols) * 2;
       break;
-    case C2H_Q8_0:
-      *qb = (size_t)rows * nq_of(cols) * 128;
-      *db = (size_t)rows * nb8_of(cols) * 2;
-      break;
+    case C2H_Q8_0: *qb = (size_t)rows * q8_0_row_stride(nb8_of(cols)); break;
   }
 }
 
@@ -139,14 +139,18 @@ void pack_host(int type, int64_t rows, int64_t cols, const uint8_t* src, uint8_t
       memcpy(ddst + i * 2, src + i * BS_Q6K + 208, 2);
     }
   } else if (type == C2H_Q8_0) {
-    int nb8 = nb8_of(cols), nq = nq_of(cols);
-    memset(qdst, 0, (size_t)rows * nq * 128);
+    // per row: fp16 scales padded to dpad halves, then the lane-interleaved quants
+    (void)ddst;
+    const int nb8 = nb8_of(cols);
+    const size_t stride = q8_0_row_stride(nb8), dbytes = (size_t)q8_0_dpad(nb8) * 2;
+    memset(qdst, 0, (size_t)rows * stride);
     for (int64_t r = 0; r < rows; ++r) {
       const uint8_t* row = src + (size_t)r * nb8 * BS_Q8_0;
-      uint8_t* qr = qdst + (size_t)r * nq * 128;
+      uint8_t* dr = qdst + (size_t)r * stride;
+      uint8_t* qr = dr + dbytes;
       for (int b = 0; b < nb8; ++b) {
         const uint8_t* blk = row + (size_t)b * BS_Q8_0;
-        memcpy(ddst + ((size_t)r * nb8 + b) * 2, blk, 2);
+        memcpy(dr + (size_t)b * 2, blk, 2);
         int bq = b >> 2, bb = b & 3;
         for (int j = 0; j < 8; ++j)
           for (int i = 0; i < 4; ++i) qr[(bq * 8 + j) * 16 + bb * 4 + i] = blk[2 + j + 8 * i];
@@ -210,7 +214,9 @@ int upload_f32(c2h_ctx* c, float** dst, int64_t n_expected, int type, int64_t ro
 
 // ------------------------------------------------------------- launches
 
-size_t gemv_lds_bytes(int n_x_lds) { return sizeof(Q8KLds) + (size_t)2 * n_x_lds * sizeof(float); }
+// Q8_K row, 512 term/partial slots, 256 Q6_K scale slots, 256 + 192
+// quantiser slots, x and x*x buffers.
+size_t gemv_lds_bytes(int n_x_lds) { return sizeof(Q8KLds) + (size_t)(1216 + 2 * n_x_lds) * sizeof(float); }
 
 void add_job(GemvParams& P, int* task, const Tensor& w, const Tensor* w2, int mode, float* y, const float* bias,
              int32_t* isums) {
@@ -226,23 +232,34 @@ void add_job(GemvParams& P, int* task, const Tensor& w, const Tensor* w2, int mo
   }
   J.rows = (int)w.rows;
   J.nb = nb_k(w.cols);
-  J.rpt = 64 / J.nb;
-  J.n_tasks = (J.rows + J.rpt - 1) / J.rpt;
-  J.task_begin = *task;
-  *task += J.n_tasks;
+  J.rpw = 256 / (4 * J.nb);
+  J.n_wg = (J.rows + J.rpw - 1) / J.rpw;
+  J.wg_begin = *task;
+  *task += J.n_wg;
   J.mode = mode;
   J.y = y;
   J.bias = bias;
   J.isums = isums;
 }
 
-void launch_gemv(c2h_ctx* c, GemvParams& P, int total_tasks) {
-  int grid = (total_tasks + 3) / 4;
+void launch_gemv(c2h_ctx* c, GemvParams& P, int total_wg) {
   size_t lds = gemv_lds_bytes(P.n_x_lds);
-  hipLaunchKernelGGL(k_gemv, dim3(grid), dim3(256), lds, c->stream, P);
+  hipLaunchKernelGGL(k_gemv, dim3(total_wg), dim3(256), lds, c->stream, P);
 }
 
-int round4(int n) { return (n + 3) & ~3; }
+typedef void (*AttnKernel)(AttnFusedParams);
+AttnKernel attn_kernel(int nb) {
+  switch (nb) {
+    case 1: return k_attn_fused<1>;
+    case 2: return k_attn_fused<2>;
+    case 3: return k_attn_fused<3>;
+    default: return k_attn_fused<4>;
+  }
+}
+
+// LDS floats for a chained-sum buffer of n values: rounded up to 32 plus 32
+// floats of read-ahead slack (the chain loads 32 values ahead).
+int lds16(int n) { return ((n + 31) & ~31) + 32; }
 
 GemvParams base_params(c2h_ctx* c) {
   GemvParams P;
@@ -288,27 +305,32 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
   const int E = D.n_embd;
   for (int l = 0; l < D.n_layers; ++l) {
     Layer& L = c->layers[l];
-    {  // attn_in
-      GemvParams P = base_params(c);
-      P.prologue = (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM;
-      P.n_x = E;
-      P.n_x_lds = round4(E);
-      P.x = c->X;
-      P.x_out = c->X;
-      P.norm_w = L.attn_norm;
-      P.nb_in = nb_k(E);
-      int task = 0;
-      add_job(P, &task, L.wq, nullptr, L.bq ? MODE_BIAS : MODE_STORE, c->q, L.bq, nullptr);
-      add_job(P, &task, L.wk, nullptr, L.bk ? MODE_BIAS : MODE_STORE, c->k, L.bk, nullptr);
-      add_job(P, &task, L.wv, nullptr, L.bv ? MODE_BIAS : MODE_STORE, c->v, L.bv, nullptr);
-      launch_gemv(c, P, task);
-    }
-    {  // attention
-      AttnParams A;
+    {  // attention block: [embed] RMSNorm, q|k|v rows per head, RoPE, KV store, attention
+      AttnFusedParams A;
       memset(&A, 0, sizeof(A));
-      A.q = c->q;
-      A.k = c->k;
-      A.v = c->v;
+      A.prologue = (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM;
+      A.n_embd = E;
+      A.nb = nb_k(E);
+      A.n_x_lds = lds16(E);
+      A.eps = D.rms_eps;
+      A.x = c->X;
+      A.x_out = c->X;
+      A.norm_w = L.attn_norm;
+      A.emb = c->embd.ref();
+      A.n_vocab = D.n_vocab;
+      A.part_v = c->part_v;
+      A.part_i = c->part_i;
+      A.n_part = c->n_part;
+      A.token_ids = c->token_ids;
+      A.wq = L.wq.ref();
+      A.wk = L.wk.ref();
+      A.wv = L.wv.ref();
+      A.tq = L.wq.type;
+      A.tk = L.wk.type;
+      A.tv = L.wv.type;
+      A.bq = L.bq;
+      A.bk = L.bk;
+      A.bv = L.bv;
       A.out = c->attn;
       A.kv = c->kv;
       A.rope_cos = c->rope_cos;
@@ -319,9 +341,12 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
       A.n_heads = D.n_heads;
       A.n_kv_heads = D.n_kv_heads;
       A.max_ctx = D.max_ctx;
+      A.a_lds = c->attn_a_lds;
+      A.b_lds = c->attn_b_lds;
+      A.vchunk = c->attn_vchunk;
       A.scale = (float)(1.0 / std::sqrt((double)D.head_dim));
       A.state = c->state_dev;
-      hipLaunchKernelGGL(k_attention, dim3(D.n_heads), dim3(256), c->attn_lds, c->stream, A);
+      hipLaunchKernelGGL(attn_kernel(A.nb), dim3(D.n_heads), dim3(256), c->attn_lds, c->stream, A);
     }
     {  // attn_out: X += Wo * Q8_K(attn)
       GemvParams P = base_params(c);
@@ -336,7 +361,7 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
       GemvParams P = base_params(c);
       P.prologue = PRO_NORM;
       P.n_x = E;
-      P.n_x_lds = round4(E);
+      P.n_x_lds = lds16(E);
       P.x = c->X;
       P.norm_w = L.ffn_norm;
       P.nb_in = nb_k(E);
@@ -364,7 +389,8 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
   N.out_buf[0] = c->normx[0];
   N.out_buf[1] = c->normx[1];
   N.state = c->state_dev;
-  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), (size_t)2 * round4(E) * sizeof(float), c->stream, N);
+  N.n_lds = lds16(E);
+  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), (size_t)2 * N.n_lds * sizeof(float), c->stream, N);
 }
 
 void enqueue_step(c2h_ctx* c) {
@@ -496,10 +522,10 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
     return bail(fail(c, C2H_ERR_INVALID, "model dimensions must be positive"));
   if (D.head_dim != 64 || D.n_embd != D.n_heads * D.head_dim || D.n_heads % D.n_kv_heads)
     return bail(fail(c, C2H_ERR_UNSUPPORTED, "this build runs head_dim 64 with n_embd = n_heads*64"));
-  if (D.n_embd % 256 != 128 && D.n_embd % 256 != 0 && D.n_embd < 256)
-    return bail(fail(c, C2H_ERR_UNSUPPORTED, "n_embd too small"));
-  if (D.n_embd % 32 || D.n_embd > 4096 || D.n_ff % 4 || D.n_ff > 16384)
-    return bail(fail(c, C2H_ERR_UNSUPPORTED, "n_embd must be a multiple of 32 up to 4096, n_ff up to 16384"));
+  if (D.n_embd < 256 || D.n_ff < 256)
+    return bail(fail(c, C2H_ERR_UNSUPPORTED, "K-quant projections need n_embd and n_ff of at least 256"));
+  if (D.n_embd % 32 || D.n_embd > 1024 || D.n_ff % 4 || D.n_ff > 16384)
+    return bail(fail(c, C2H_ERR_UNSUPPORTED, "n_embd must be a multiple of 32 up to 1024, n_ff up to 16384"));
   if ((size_t)D.max_ctx * 4 > 128 * 1024)
     return bail(fail(c, C2H_ERR_UNSUPPORTED, "max_ctx above 32768 is not supported by the exact attention kernel"));
   c->desc = D;
@@ -538,9 +564,27 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   if ((rc = dalloc(c, &c->part_v, (size_t)c->n_part * 4)) || (rc = dalloc(c, &c->part_i, (size_t)c->n_part * 4)) ||
       (rc = dalloc(c, &c->logits, (size_t)D.n_vocab * 4)))
     return bail(rc);
-  c->attn_lds = (size_t)D.max_ctx * 4;
-  if (hipFuncSetAttribute((const void*)k_attention, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->attn_lds) !=
-      hipSuccess)
+  // attention-block LDS within the 160 KB of a gfx950 workgroup (4 KB kept
+  // for static shared data):
+  //   region A = Q8_K row | red | scl | dq | x | x*x, reused for staged V;
+  //   region B = GEMV terms, then all scores of the context.
+  {
+    int a_gemv = (int)(sizeof(Q8KLds) / 4) + 256 + 192 + 3 * 64 * FUSED_MAX_NB + 2 * lds16(E);
+    int b = lds16(D.max_ctx);
+    if (b < 3 * 256 * FUSED_MAX_NB) b = 3 * 256 * FUSED_MAX_NB;
+    long room = (160L * 1024 - 4096) / 4 - b;  // floats left for region A
+    if (room < a_gemv) return bail(fail(c, C2H_ERR_UNSUPPORTED, "max_ctx too large for the exact attention kernel"));
+    int vchunk = (int)(room / 64);
+    vchunk = vchunk > 256 ? 256 : (vchunk & ~15);
+    if (vchunk < 16) return bail(fail(c, C2H_ERR_UNSUPPORTED, "max_ctx too large for the exact attention kernel"));
+    int a = a_gemv > vchunk * 64 ? a_gemv : vchunk * 64;
+    c->attn_a_lds = (a + 3) & ~3;
+    c->attn_b_lds = b;
+    c->attn_vchunk = vchunk;
+  }
+  c->attn_lds = ((size_t)c->attn_a_lds + (size_t)c->attn_b_lds) * 4;
+  if (hipFuncSetAttribute((const void*)attn_kernel(E / 256), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)c->attn_lds) != hipSuccess)
     return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
   C2hState s0;
   memset(&s0, 0, sizeof(s0));
@@ -745,8 +789,7 @@ int c2h_quantize_q8k_dev(c2h_ctx* c, const float* x, int32_t cols, void* q8k_out
   HIPCHK(c, hipSetDevice(c->device));
   int nb = cols / 256;
   if (nb == 0) return C2H_OK;
-  hipLaunchKernelGGL(k_quantize_q8k, dim3((nb + 3) / 4), dim3(256), 0, c->stream, x, nb,
-                     reinterpret_cast<uint8_t*>(q8k_out));
+  hipLaunchKernelGGL(k_quantize_q8k, dim3(nb), dim3(256), 0, c->stream, x, nb, reinterpret_cast<uint8_t*>(q8k_out));
   HIPCHK(c, hipGetLastError());
   return C2H_OK;
 }

@@ -104,6 +104,49 @@ __device__ __forceinline__ float swiglu_tail(float g32, float up) {
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// ---- wave64 reductions through DPP (VALU lane moves, no LDS round trip)
+
+enum : int {
+  DPP_QUAD_1032 = 0xB1,   // quad_perm [1,0,3,2]
+  DPP_QUAD_2301 = 0x4E,   // quad_perm [2,3,0,1]
+  DPP_HALF_MIRROR = 0x141,
+  DPP_MIRROR = 0x140,
+  DPP_BCAST15 = 0x142,
+  DPP_BCAST31 = 0x143,
+};
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, CTRL, ROW_MASK, 0xf, false);
+}
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(dpp_i<CTRL, ROW_MASK>(__float_as_int(v)));
+}
+
+__device__ __forceinline__ float fmax_gt(float a, float b) { return (b > a) ? b : a; }
+
+// Max over the 64 lanes of values that are never NaN ('>' semantics, so a
+// -0 never replaces +0); the result is returned in every lane.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmax_gt(v, dpp_f<DPP_QUAD_1032>(v));
+  v = fmax_gt(v, dpp_f<DPP_QUAD_2301>(v));
+  v = fmax_gt(v, dpp_f<DPP_HALF_MIRROR>(v));
+  v = fmax_gt(v, dpp_f<DPP_MIRROR>(v));
+  v = fmax_gt(v, dpp_f<DPP_BCAST15, 0xa>(v));
+  v = fmax_gt(v, dpp_f<DPP_BCAST31, 0xc>(v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Integer sum over each row of 16 lanes; every lane of the row gets it.
+__device__ __forceinline__ int row16_sum_dpp(int v) {
+  v += dpp_i<DPP_QUAD_1032>(v);
+  v += dpp_i<DPP_QUAD_2301>(v);
+  v += dpp_i<DPP_HALF_MIRROR>(v);
+  v += dpp_i<DPP_MIRROR>(v);
+  return v;
+}
+
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 // 16-byte streaming load (weights are read once per step).

@@ -30,13 +30,18 @@ struct Q8KLds {
 // A weight tensor in its device layout:
 //   Q4_K: the reference's rows back to back, row stride (cols/256)*144;
 //   Q6_K: per super-block 208 bytes ql|qh|scales in q, the fp16 d in d;
-//   Q8_0: per row ceil(nb/4) groups of 8 lanes x 16 bytes (lane j holds
-//         bytes j, j+8, j+16, j+24 of four consecutive blocks) in q, the
-//         per-block fp16 d in d.
+//   Q8_0: per row the fp16 block scales (padded to a multiple of 32 halves,
+//         64 bytes for 28 blocks) followed by ceil(nb/4) groups of 8 lanes x
+//         16 bytes (lane j holds bytes j, j+8, j+16, j+24 of four
+//         consecutive blocks); d is unused.
 struct WeightRef {
   const uint8_t* q;
   const uint16_t* d;
 };
+
+__host__ __device__ inline int q8_0_dpad(int nb8) { return ((nb8 + 31) / 32) * 32; }
+__host__ __device__ inline int q8_0_nq(int nb8) { return (nb8 + 3) / 4; }
+__host__ __device__ inline size_t q8_0_row_stride(int nb8) { return (size_t)q8_0_dpad(nb8) * 2 + (size_t)q8_0_nq(nb8) * 128; }
 
 enum Prologue : int {
   PRO_Q8K = 0,                // copy an external Q8_K row
@@ -53,16 +58,19 @@ enum GemvMode : int {
   MODE_SWIGLU = 3,  // y = SwiGLU(acc(w), acc(w2))
 };
 
+// One matrix of a fused GEMV launch.  A workgroup owns `rpw` consecutive
+// rows; each of its threads owns one quarter of one super-block of one row
+// (Q4_K: one 32-element pair; Q6_K: 16 of the 32 lanes of one half).
 struct GemvJob {
   WeightRef w;
   WeightRef w2;
   int type;
   int type2;
   int rows;
-  int nb;          // super-blocks per row (floor(cols/256))
-  int rpt;         // rows per wave task = floor(64/nb)
-  int task_begin;  // first wave task of this job
-  int n_tasks;
+  int nb;        // super-blocks per row (floor(cols/256))
+  int rpw;       // rows per workgroup = floor(256 / (4*nb))
+  int wg_begin;  // first workgroup of this job
+  int n_wg;
   int mode;
   float* y;
   const float* bias;
@@ -75,7 +83,7 @@ struct GemvParams {
   int prologue;
   int nb_in;
   int n_x;      // length of x for the norm prologues
-  int n_x_lds;  // LDS floats reserved for x (multiple of 4)
+  int n_x_lds;  // LDS floats reserved for x (multiple of 16, plus 16 of padding)
   float eps;
   const float* x;
   const float* norm_w;
@@ -98,17 +106,36 @@ struct NormParams {
   const float* w;
   float eps;
   int n;
+  int n_lds;  // LDS floats per buffer (multiple of 16, plus 16 of padding)
   int out_sel;  // 1: write out_buf[state->nx_out]
   float* out;
   float* out_buf[2];
   C2hState* state;
 };
 
-struct AttnParams {
-  const float* q;
-  const float* k;
-  const float* v;
-  float* out;
+// The attention block of one layer in one launch, one workgroup per query
+// head: [embed] + RMSNorm + Q8_K, the head's 64 q rows and its KV head's
+// 64 k and 64 v rows (+ bias), RoPE, KV store, attention.
+constexpr int FUSED_MAX_NB = 4;  // n_embd/256 this kernel handles (items per thread = 3*nb)
+struct AttnFusedParams {
+  int prologue;  // PRO_NORM, PRO_EMBED_NORM or PRO_ARGMAX_EMBED_NORM
+  int n_embd;
+  int nb;        // floor(n_embd/256)
+  int n_x_lds;
+  float eps;
+  const float* x;
+  float* x_out;
+  const float* norm_w;
+  WeightRef emb;
+  int n_vocab;
+  const float* part_v;
+  const int* part_i;
+  int n_part;
+  int32_t* token_ids;
+  WeightRef wq, wk, wv;
+  int tq, tk, tv;
+  const float *bq, *bk, *bv;
+  float* out;  // attention output [n_heads*64]
   float* kv;
   const float* rope_cos;
   const float* rope_sin;
@@ -118,11 +145,14 @@ struct AttnParams {
   int n_heads;
   int n_kv_heads;
   int max_ctx;
+  int a_lds;    // floats of region A (Q8_K row, x, x*x, scales; reused for V)
+  int b_lds;    // floats of region B (GEMV terms, then scores)
+  int vchunk;   // positions of V staged in LDS per pass
   float scale;
   C2hState* state;
 };
 
-constexpr int VOCAB_TILES = 4;  // 32-row tiles per vocab workgroup
+constexpr int VOCAB_TILES = 1;  // 32-row tiles per vocab workgroup
 
 struct VocabParams {
   WeightRef w;
@@ -142,7 +172,8 @@ struct VocabParams {
 __global__ void k_quantize_q8k(const float* __restrict__ x, int nb, uint8_t* __restrict__ y);
 __global__ void k_gemv(GemvParams P);
 __global__ void k_rmsnorm(NormParams P);
-__global__ void k_attention(AttnParams P);
+template <int NB>
+__global__ void k_attn_fused(AttnFusedParams P);
 __global__ void k_vocab(VocabParams P);
 __global__ void k_argmax_final(const float* pv, const int* pi, int n, C2hState* state);
 

@@ -38,18 +38,19 @@ def test_pack_weights_layouts():
     blocks = w6.reshape(38, 210)
     assert np.array_equal(p6[:38 * 208].reshape(38, 208), blocks[:, :208])
     assert np.array_equal(p6[38 * 208:].reshape(38, 2), blocks[:, 208:])
-    # Q8_0: lane j of a 4-block group holds bytes j, j+8, j+16, j+24 of each block
+    # Q8_0: per row 64 bytes of fp16 scales (28 used), then groups of 4 blocks
+    # where lane j holds bytes j, j+8, j+16, j+24 of each block
     w8 = G.synth_q8_0(rng, 3 * 28)
-    p8 = H.pack_weights(H.Q8_0, 3, 896, w8)
-    assert len(p8) == 3 * 7 * 128 + 3 * 28 * 2
+    p8 = H.pack_weights(H.Q8_0, 3, 896, w8).reshape(3, 960)
     qs = w8.reshape(3, 28, 34)[:, :, 2:]
-    q = p8[:3 * 7 * 128].reshape(3, 7, 8, 4, 4)  # row, group, lane, block-in-group, byte
+    assert np.array_equal(p8[:, :56].reshape(3, 28, 2), w8.reshape(3, 28, 34)[:, :, :2])
+    assert not p8[:, 56:64].any()
+    q = p8[:, 64:].reshape(3, 7, 8, 4, 4)  # row, group, lane, block-in-group, byte
     for r in range(3):
         for b in range(28):
             for j in range(8):
                 for i in range(4):
                     assert q[r, b // 4, j, b % 4, i] == qs[r, b, j + 8 * i]
-    assert np.array_equal(p8[3 * 7 * 128:].reshape(3, 28, 2), w8.reshape(3, 28, 34)[:, :, :2])
 
 
 def test_pack_rejects_bad_shapes():
