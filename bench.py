@@ -60,6 +60,30 @@ def cpu_baseline(gf, prompt, steps, im_end, eos):
                       f"untimed, then {len(toks)} greedy steps timed ({dt:.1f} s)"}
 
 
+def vocab_traffic():
+    """HBM bytes per vocab launch as measured by the rocprofv3 --pmc passes
+    (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration) recorded
+    in profiles/k_vocab_traffic.txt; None when that record is absent."""
+    path = os.path.join(ROOT, "profiles", "k_vocab_traffic.txt")
+    try:
+        with open(path, encoding="utf-8") as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch"):
+                    return int(line.split("=", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
+def copy_calibration(ctx, mib: int, reps: int = 5):
+    """A plain device-to-device copy of `mib` MiB (k_copy16), `reps` times:
+    under rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE per dispatch against
+    the known size gives the counters' scale factor."""
+    ms = ctx.copy_bench(mib << 20, reps)
+    print(f"copy calibration: {reps} x {mib} MiB device copies, {ms:.4f} ms each "
+          f"({2 * (mib << 20) / (ms * 1e-3) / 1e9:.1f} GB/s read+write)", file=sys.stderr)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -68,6 +92,10 @@ def main():
     ap.add_argument("--model", default=None, help="GGUF path (default: synthesise the seeded model)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--max-ctx", type=int, default=16384)
+    ap.add_argument("--vocab-iters", type=int, default=50, help="launches in each vocab timing")
+    ap.add_argument("--pipelined-iters", type=int, default=64, help="steps in the pipelined (no host sync) timing")
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="also run plain device copies of this size (counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported", file=sys.stderr)
@@ -106,9 +134,15 @@ def main():
     ms_per_step = dt * 1000.0 / args.steps
     value = args.steps / dt
 
-    vocab_ms = ctx.time_vocab(50, pos)
+    pipelined_ms = ctx.time_steps(pos, args.pipelined_iters, PENALTY, im_end, eos)
+    # In-step timing: a forward pass between launches streams the layer
+    # weights, so the vocab rows come from HBM as they do inside a step.
+    vocab_ms = ctx.time_vocab(args.vocab_iters, pos, in_step=True)
+    vocab_b2b_ms = ctx.time_vocab(args.vocab_iters, pos, in_step=False)
     achieved = VOCAB_BYTES / (vocab_ms * 1e-3) / 1e9
-    pipelined_ms = ctx.time_steps(pos, 64, PENALTY, im_end, eos)
+    traffic = vocab_traffic()
+    if args.copy_calib_mib:
+        copy_calibration(ctx, args.copy_calib_mib)
 
     base = None
     if not args.no_cpu_baseline:
@@ -133,11 +167,12 @@ def main():
                                f"repetition penalty {PENALTY}",
                    "batch": 1, "prompt_len": PROMPT_LEN, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "k_vocab (151936x896 Q8_0 + penalty + argmax)",
                      "ms_per_launch": round(vocab_ms, 5)},
         "cpu_baseline": base,
-        "extra": {"pipelined_ms_per_step": round(pipelined_ms, 4),
+        "extra": {"vocab_ms_back_to_back": round(vocab_b2b_ms, 5),
+                  "pipelined_ms_per_step": round(pipelined_ms, 4),
                   "pipelined_tok_s": round(1000.0 / pipelined_ms, 1)},
     }
     print(json.dumps(line))

@@ -73,7 +73,8 @@ def lib():
             "c2h_quantize_q8k_dev": (C.c_int, [VP, VP, I32, VP]),
             "c2h_gemv_dev": (C.c_int, [VP, I32, VP, VP, I32, I32, VP, VP]),
             "c2h_sync": (C.c_int, [VP]),
-            "c2h_time_vocab": (C.c_int, [VP, I32, I32, C.POINTER(C.c_float)]),
+            "c2h_time_vocab": (C.c_int, [VP, I32, I32, I32, C.POINTER(C.c_float)]),
+            "c2h_copy_bench": (C.c_int, [VP, C.c_int64, I32, C.POINTER(C.c_float)]),
             "c2h_time_steps": (C.c_int, [VP, I32, I32, C.c_float, I32, I32, C.POINTER(C.c_float)]),
         }
         for name, (res, args) in sig.items():
@@ -158,9 +159,14 @@ class Ctx:
         self._chk(lib().c2h_get_kv(self.h, which, layer, kv_head, n, _p(out)))
         return out
 
-    def time_vocab(self, iters: int, pos: int) -> float:
+    def time_vocab(self, iters: int, pos: int, in_step: bool = True) -> float:
         ms = C.c_float()
-        self._chk(lib().c2h_time_vocab(self.h, iters, pos, C.byref(ms)))
+        self._chk(lib().c2h_time_vocab(self.h, iters, pos, int(in_step), C.byref(ms)))
+        return ms.value
+
+    def copy_bench(self, nbytes: int, reps: int) -> float:
+        ms = C.c_float()
+        self._chk(lib().c2h_copy_bench(self.h, nbytes, reps, C.byref(ms)))
         return ms.value
 
     def time_steps(self, pos: int, iters: int, penalty: float, im_end: int, eos: int) -> float:

@@ -50,6 +50,7 @@ struct c2h_ctx {
 
   float *X = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *h = nullptr;
   float* normx[2] = {nullptr, nullptr};
+  float* zero_bias = nullptr;  // n_embd zeros read in place of an absent q/k/v bias
   int nx_cur = 0, nx_prev = 0;
   float* kv = nullptr;
   int32_t* token_ids = nullptr;
@@ -67,9 +68,6 @@ struct c2h_ctx {
   bool graphs_ready = false;
   bool use_graphs = true;
   size_t attn_lds = 0;
-  int attn_a_lds = 0;
-  int attn_b_lds = 0;
-  int attn_vchunk = 0;
 
   // kernel-only scratch (c2h_gemv / c2h_quantize_q8k host forms)
   std::vector<void*> scratch;
@@ -214,9 +212,8 @@ int upload_f32(c2h_ctx* c, float** dst, int64_t n_expected, int type, int64_t ro
 
 // ------------------------------------------------------------- launches
 
-// Q8_K row, 512 term/partial slots, 256 Q6_K scale slots, 256 + 192
-// quantiser slots, x and x*x buffers.
-size_t gemv_lds_bytes(int n_x_lds) { return sizeof(Q8KLds) + (size_t)(1216 + 2 * n_x_lds) * sizeof(float); }
+// k_gemv_q8k: the external Q8_K row plus 256 term and 256 scale slots.
+size_t gemv_q8k_lds_bytes() { return sizeof(Q8KLds) + (size_t)512 * sizeof(float); }
 
 void add_job(GemvParams& P, int* task, const Tensor& w, const Tensor* w2, int mode, float* y, const float* bias,
              int32_t* isums) {
@@ -242,37 +239,60 @@ void add_job(GemvParams& P, int* task, const Tensor& w, const Tensor* w2, int mo
   J.isums = isums;
 }
 
-void launch_gemv(c2h_ctx* c, GemvParams& P, int total_wg) {
-  size_t lds = gemv_lds_bytes(P.n_x_lds);
-  hipLaunchKernelGGL(k_gemv, dim3(total_wg), dim3(256), lds, c->stream, P);
+typedef void (*GemvKernel)(GemvParams);
+
+// Row-kernel instance for (super-blocks per row, prologue, mode); nullptr
+// when this build has none for that width.
+GemvKernel gemv_row_kernel(int nb, int pro, int mode) {
+  if (pro == PRO_QUANT && mode == MODE_RESID) {
+    switch (nb) {
+      case 3: return k_gemv_row<3, PRO_QUANT, MODE_RESID>;
+      case 4: return k_gemv_row<4, PRO_QUANT, MODE_RESID>;
+      case 12: return k_gemv_row<12, PRO_QUANT, MODE_RESID>;
+      case 19: return k_gemv_row<19, PRO_QUANT, MODE_RESID>;
+      default: return nullptr;
+    }
+  }
+  if (pro == PRO_NORM && mode == MODE_SWIGLU) {
+    switch (nb) {
+      case 3: return k_gemv_row<3, PRO_NORM, MODE_SWIGLU>;
+      case 4: return k_gemv_row<4, PRO_NORM, MODE_SWIGLU>;
+      default: return nullptr;
+    }
+  }
+  return nullptr;
+}
+
+// One job per row-kernel launch; PRO_NORM needs the x*x chain buffer.
+void launch_gemv_row(c2h_ctx* c, GemvParams& P) {
+  const GemvJob& J = P.jobs[0];
+  GemvKernel k = gemv_row_kernel(J.nb, P.prologue, J.mode);
+  size_t lds = (P.prologue == PRO_NORM) ? (size_t)P.n_x_lds * sizeof(float) : 0;
+  hipLaunchKernelGGL(k, dim3(J.n_wg), dim3(256), lds, c->stream, P);
 }
 
 typedef void (*AttnKernel)(AttnFusedParams);
-AttnKernel attn_kernel(int nb) {
-  switch (nb) {
-    case 1: return k_attn_fused<1>;
-    case 2: return k_attn_fused<2>;
-    case 3: return k_attn_fused<3>;
-    default: return k_attn_fused<4>;
-  }
-}
 
-// LDS floats for a chained-sum buffer of n values: rounded up to 32 plus 32
-// floats of read-ahead slack (the chain loads 32 values ahead).
-int lds16(int n) { return ((n + 31) & ~31) + 32; }
+// Attention-block instance for (super-blocks per row of n_embd, prologue);
+// nullptr when this build has none for that width.
+AttnKernel attn_kernel(int nb, int pro) {
+  if (nb == 3) {
+    if (pro == PRO_EMBED_NORM) return k_attn<3, PRO_EMBED_NORM>;
+    if (pro == PRO_ARGMAX_EMBED_NORM) return k_attn<3, PRO_ARGMAX_EMBED_NORM>;
+    return k_attn<3, PRO_NORM>;
+  }
+  if (nb == 4) {
+    if (pro == PRO_EMBED_NORM) return k_attn<4, PRO_EMBED_NORM>;
+    if (pro == PRO_ARGMAX_EMBED_NORM) return k_attn<4, PRO_ARGMAX_EMBED_NORM>;
+    return k_attn<4, PRO_NORM>;
+  }
+  return nullptr;
+}
 
 GemvParams base_params(c2h_ctx* c) {
   GemvParams P;
   memset(&P, 0, sizeof(P));
   P.eps = c->desc.rms_eps;
-  P.n_vocab = c->desc.n_vocab;
-  P.max_ctx = c->desc.max_ctx;
-  P.token_ids = c->token_ids;
-  P.state = c->state_dev;
-  P.emb = c->embd.ref();
-  P.part_v = c->part_v;
-  P.part_i = c->part_i;
-  P.n_part = c->n_part;
   return P;
 }
 
@@ -308,10 +328,9 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
     {  // attention block: [embed] RMSNorm, q|k|v rows per head, RoPE, KV store, attention
       AttnFusedParams A;
       memset(&A, 0, sizeof(A));
-      A.prologue = (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM;
+      const int pro = (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM;
       A.n_embd = E;
-      A.nb = nb_k(E);
-      A.n_x_lds = lds16(E);
+      A.n_x_lds = chain_lds_floats(E);
       A.eps = D.rms_eps;
       A.x = c->X;
       A.x_out = c->X;
@@ -328,9 +347,10 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
       A.tq = L.wq.type;
       A.tk = L.wk.type;
       A.tv = L.wv.type;
-      A.bq = L.bq;
-      A.bk = L.bk;
-      A.bv = L.bv;
+      A.bq = L.bq ? L.bq : c->zero_bias;
+      A.bk = L.bk ? L.bk : c->zero_bias;
+      A.bv = L.bv ? L.bv : c->zero_bias;
+      A.bias_mask = (L.bq ? 1 : 0) | (L.bk ? 2 : 0) | (L.bv ? 4 : 0);
       A.out = c->attn;
       A.kv = c->kv;
       A.rope_cos = c->rope_cos;
@@ -341,12 +361,9 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
       A.n_heads = D.n_heads;
       A.n_kv_heads = D.n_kv_heads;
       A.max_ctx = D.max_ctx;
-      A.a_lds = c->attn_a_lds;
-      A.b_lds = c->attn_b_lds;
-      A.vchunk = c->attn_vchunk;
       A.scale = (float)(1.0 / std::sqrt((double)D.head_dim));
       A.state = c->state_dev;
-      hipLaunchKernelGGL(attn_kernel(A.nb), dim3(D.n_heads), dim3(256), c->attn_lds, c->stream, A);
+      hipLaunchKernelGGL(attn_kernel(nb_k(E), pro), dim3(D.n_heads), dim3(256), c->attn_lds, c->stream, A);
     }
     {  // attn_out: X += Wo * Q8_K(attn)
       GemvParams P = base_params(c);
@@ -355,19 +372,19 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
       P.nb_in = nb_k(E);
       int task = 0;
       add_job(P, &task, L.wo, nullptr, MODE_RESID, c->X, nullptr, nullptr);
-      launch_gemv(c, P, task);
+      launch_gemv_row(c, P);
     }
     {  // ffn_in: h = SwiGLU(Wg * n, Wu * n), n = Q8_K(RMSNorm(X))
       GemvParams P = base_params(c);
       P.prologue = PRO_NORM;
       P.n_x = E;
-      P.n_x_lds = lds16(E);
+      P.n_x_lds = chain_lds_floats(E);
       P.x = c->X;
       P.norm_w = L.ffn_norm;
       P.nb_in = nb_k(E);
       int task = 0;
       add_job(P, &task, L.wg, &L.wu, MODE_SWIGLU, c->h, nullptr, nullptr);
-      launch_gemv(c, P, task);
+      launch_gemv_row(c, P);
     }
     {  // ffn_out: X += Wd * Q8_K(h)
       GemvParams P = base_params(c);
@@ -376,7 +393,7 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
       P.nb_in = nb_k(D.n_ff);
       int task = 0;
       add_job(P, &task, L.wd, nullptr, MODE_RESID, c->X, nullptr, nullptr);
-      launch_gemv(c, P, task);
+      launch_gemv_row(c, P);
     }
   }
   NormParams N;
@@ -389,8 +406,8 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
   N.out_buf[0] = c->normx[0];
   N.out_buf[1] = c->normx[1];
   N.state = c->state_dev;
-  N.n_lds = lds16(E);
-  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), (size_t)2 * N.n_lds * sizeof(float), c->stream, N);
+  N.n_lds = chain_lds_floats(E);
+  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), (size_t)N.n_lds * sizeof(float), c->stream, N);
 }
 
 void enqueue_step(c2h_ctx* c) {
@@ -526,16 +543,22 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
     return bail(fail(c, C2H_ERR_UNSUPPORTED, "K-quant projections need n_embd and n_ff of at least 256"));
   if (D.n_embd % 32 || D.n_embd > 1024 || D.n_ff % 4 || D.n_ff > 16384)
     return bail(fail(c, C2H_ERR_UNSUPPORTED, "n_embd must be a multiple of 32 up to 1024, n_ff up to 16384"));
-  if ((size_t)D.max_ctx * 4 > 128 * 1024)
-    return bail(fail(c, C2H_ERR_UNSUPPORTED, "max_ctx above 32768 is not supported by the exact attention kernel"));
+  if (!attn_kernel(nb_k(D.n_embd), PRO_NORM) || !gemv_row_kernel(nb_k(D.n_embd), PRO_QUANT, MODE_RESID) ||
+      !gemv_row_kernel(nb_k(D.n_embd), PRO_NORM, MODE_SWIGLU) ||
+      !gemv_row_kernel(nb_k(D.n_ff), PRO_QUANT, MODE_RESID))
+    return bail(fail(c, C2H_ERR_UNSUPPORTED,
+                     "no kernel instance for n_embd %d / n_ff %d (built: n_embd/256 in {3,4}, n_ff/256 in {3,4,12,19})",
+                     D.n_embd, D.n_ff));
   c->desc = D;
   c->has_model = true;
   c->layers.resize(D.n_layers);
   const int E = D.n_embd, KV = D.n_kv_heads * D.head_dim, F = D.n_ff;
   if ((rc = dalloc(c, &c->X, E * 4)) || (rc = dalloc(c, &c->q, E * 4)) || (rc = dalloc(c, &c->k, KV * 4)) ||
       (rc = dalloc(c, &c->v, KV * 4)) || (rc = dalloc(c, &c->attn, E * 4)) || (rc = dalloc(c, &c->h, F * 4)) ||
-      (rc = dalloc(c, &c->normx[0], E * 4)) || (rc = dalloc(c, &c->normx[1], E * 4)))
+      (rc = dalloc(c, &c->normx[0], E * 4)) || (rc = dalloc(c, &c->normx[1], E * 4)) ||
+      (rc = dalloc(c, &c->zero_bias, E * 4)))
     return bail(rc);
+  if (hipMemset(c->zero_bias, 0, E * 4) != hipSuccess) return bail(fail(c, C2H_ERR_HIP, "memset"));
   size_t kv_bytes = (size_t)2 * D.n_layers * D.n_kv_heads * D.max_ctx * D.head_dim * 4;
   if ((rc = dalloc(c, &c->kv, kv_bytes))) return bail(rc);
   if (hipMemset(c->kv, 0, kv_bytes) != hipSuccess) return bail(fail(c, C2H_ERR_HIP, "hipMemset kv"));
@@ -564,28 +587,16 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   if ((rc = dalloc(c, &c->part_v, (size_t)c->n_part * 4)) || (rc = dalloc(c, &c->part_i, (size_t)c->n_part * 4)) ||
       (rc = dalloc(c, &c->logits, (size_t)D.n_vocab * 4)))
     return bail(rc);
-  // attention-block LDS within the 160 KB of a gfx950 workgroup (4 KB kept
-  // for static shared data):
-  //   region A = Q8_K row | red | scl | dq | x | x*x, reused for staged V;
-  //   region B = GEMV terms, then all scores of the context.
-  {
-    int a_gemv = (int)(sizeof(Q8KLds) / 4) + 256 + 192 + 3 * 64 * FUSED_MAX_NB + 2 * lds16(E);
-    int b = lds16(D.max_ctx);
-    if (b < 3 * 256 * FUSED_MAX_NB) b = 3 * 256 * FUSED_MAX_NB;
-    long room = (160L * 1024 - 4096) / 4 - b;  // floats left for region A
-    if (room < a_gemv) return bail(fail(c, C2H_ERR_UNSUPPORTED, "max_ctx too large for the exact attention kernel"));
-    int vchunk = (int)(room / 64);
-    vchunk = vchunk > 256 ? 256 : (vchunk & ~15);
-    if (vchunk < 16) return bail(fail(c, C2H_ERR_UNSUPPORTED, "max_ctx too large for the exact attention kernel"));
-    int a = a_gemv > vchunk * 64 ? a_gemv : vchunk * 64;
-    c->attn_a_lds = (a + 3) & ~3;
-    c->attn_b_lds = b;
-    c->attn_vchunk = vchunk;
-  }
-  c->attn_lds = ((size_t)c->attn_a_lds + (size_t)c->attn_b_lds) * 4;
-  if (hipFuncSetAttribute((const void*)attn_kernel(E / 256), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)c->attn_lds) != hipSuccess)
-    return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
+  // attention-block LDS within the 160 KB of a gfx950 workgroup (8 KB kept
+  // for the kernel's static shared data): staged V | GEMV terms | Q6_K
+  // scales | x*x | all scores of the context
+  c->attn_lds = (size_t)attn_lds_floats(nb_k(E), chain_lds_floats(E), D.max_ctx) * 4;
+  if (c->attn_lds > 152u * 1024)
+    return bail(fail(c, C2H_ERR_UNSUPPORTED, "max_ctx %d too large for the exact attention kernel", D.max_ctx));
+  for (int pro : {PRO_NORM, PRO_EMBED_NORM, PRO_ARGMAX_EMBED_NORM})
+    if (hipFuncSetAttribute((const void*)attn_kernel(nb_k(E), pro), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)c->attn_lds) != hipSuccess)
+      return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
   C2hState s0;
   memset(&s0, 0, sizeof(s0));
   s0.penalty = 1.15f;
@@ -841,10 +852,9 @@ int c2h_gemv_dev(c2h_ctx* c, int32_t type, const void* w_packed, const void* xq,
   P.prologue = PRO_Q8K;
   P.q8k_in = reinterpret_cast<const uint8_t*>(xq);
   P.nb_in = nb_k(cols);
-  P.state = c->state_dev;
   int task = 0;
   add_job(P, &task, t, nullptr, MODE_STORE, y, nullptr, isums_out);
-  launch_gemv(c, P, task);
+  hipLaunchKernelGGL(k_gemv_q8k, dim3(task), dim3(256), gemv_q8k_lds_bytes(), c->stream, P);
   HIPCHK(c, hipGetLastError());
   return C2H_OK;
 }
@@ -927,12 +937,45 @@ int c2h_gemv(c2h_ctx* c, int32_t type, const void* w, const void* xq, int32_t ro
   return rc;
 }
 
-int c2h_time_vocab(c2h_ctx* c, int32_t iters, int32_t pos, float* ms) {
-  if (!c || !ms || iters <= 0) return C2H_ERR_INVALID;
+int c2h_copy_bench(c2h_ctx* c, int64_t bytes, int32_t reps, float* ms) {
+  if (!c || !ms || bytes <= 0 || (bytes & 15) || reps <= 0) return C2H_ERR_INVALID;
   HIPCHK(c, hipSetDevice(c->device));
-  int rc = validate_model(c);
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  void *src = nullptr, *dst = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = C2H_OK;
+  float t = 0;
+  if (hipMalloc(&src, (size_t)bytes) != hipSuccess || hipMalloc(&dst, (size_t)bytes) != hipSuccess ||
+      hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+    rc = fail(c, C2H_ERR_HIP, "copy bench: allocation failed");
+  } else {
+    const size_t n16 = (size_t)bytes / 16;
+    (void)hipMemsetAsync(src, 1, (size_t)bytes, c->stream);
+    (void)hipEventRecord(e0, c->stream);
+    for (int i = 0; i < reps; ++i)
+      hipLaunchKernelGGL(k_copy16, dim3(8192), dim3(256), 0, c->stream, (const uint4*)src, (uint4*)dst, n16);
+    (void)hipEventRecord(e1, c->stream);
+    hipError_t e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipEventElapsedTime(&t, e0, e1);
+    if (e != hipSuccess) rc = fail(c, C2H_ERR_HIP, "copy bench: %s", hipGetErrorString(e));
+  }
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (src) (void)hipFree(src);
+  if (dst) (void)hipFree(dst);
+  if (rc) return rc;
+  *ms = t / reps;
+  return C2H_OK;
+}
+
+int c2h_time_vocab(c2h_ctx* c, int32_t iters, int32_t pos, int32_t in_step, float* ms) {
+  if (!c || !ms || iters <= 0 || iters > 4096) return C2H_ERR_INVALID;
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = build_graphs(c);
   if (rc) return rc;
   if (pos < 0 || pos >= c->desc.max_ctx) return fail(c, C2H_ERR_RANGE, "pos out of range");
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  c->ring_next = 0;
   C2hState s;
   memset(&s, 0, sizeof(s));
   s.pos = pos;
@@ -943,18 +986,30 @@ int c2h_time_vocab(c2h_ctx* c, int32_t iters, int32_t pos, float* ms) {
   s.nx_out = c->nx_cur ^ 1;
   if ((rc = push_state(c, s))) return rc;
   enqueue_vocab(c, 1, nullptr, 1, nullptr);  // warm-up
-  hipEvent_t e0, e1;
-  HIPCHK(c, hipEventCreate(&e0));
-  HIPCHK(c, hipEventCreate(&e1));
-  HIPCHK(c, hipEventRecord(e0, c->stream));
-  for (int i = 0; i < iters; ++i) enqueue_vocab(c, 1, nullptr, 1, nullptr);
-  HIPCHK(c, hipEventRecord(e1, c->stream));
-  HIPCHK(c, hipEventSynchronize(e1));
-  float t = 0;
-  HIPCHK(c, hipEventElapsedTime(&t, e0, e1));
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
-  *ms = t / iters;
+  std::vector<hipEvent_t> ev(2 * (size_t)iters, nullptr);
+  for (auto& e : ev) HIPCHK(c, hipEventCreate(&e));
+  rc = C2H_OK;
+  for (int i = 0; i < iters && rc == C2H_OK; ++i) {
+    if (in_step) rc = run_graph(c, false);
+    if (rc == C2H_OK) {
+      (void)hipEventRecord(ev[2 * i], c->stream);
+      enqueue_vocab(c, 1, nullptr, 1, nullptr);
+      (void)hipEventRecord(ev[2 * i + 1], c->stream);
+    }
+  }
+  double total = 0;
+  if (rc == C2H_OK) {
+    hipError_t e = hipEventSynchronize(ev.back());
+    for (int i = 0; i < iters && e == hipSuccess; ++i) {
+      float t = 0;
+      e = hipEventElapsedTime(&t, ev[2 * i], ev[2 * i + 1]);
+      total += t;
+    }
+    if (e != hipSuccess) rc = fail(c, C2H_ERR_HIP, "vocab timing: %s", hipGetErrorString(e));
+  }
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  if (rc) return rc;
+  *ms = (float)(total / iters);
   return C2H_OK;
 }
 

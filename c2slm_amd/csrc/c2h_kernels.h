@@ -20,12 +20,14 @@ struct C2hState {
 
 // Q8_K row as the GEMVs keep it in LDS: quants packed four per dword, the
 // f32 scale and the sixteen 16-element sums widened to int32.
-constexpr int LDS_Q8K_BLOCKS = 64;
-struct Q8KLds {
-  uint32_t q[LDS_Q8K_BLOCKS][64];
-  float d[LDS_Q8K_BLOCKS];
-  int32_t bs[LDS_Q8K_BLOCKS][16];
+template <int NB>
+struct Q8KRow {
+  uint32_t q[NB][64];
+  float d[NB];
+  int32_t bs[NB][16];
 };
+constexpr int LDS_Q8K_BLOCKS = 64;  // 16384 columns (the reference's Q8_K scratch, engine/pool.go:59)
+typedef Q8KRow<LDS_Q8K_BLOCKS> Q8KLds;
 
 // A weight tensor in its device layout:
 //   Q4_K: the reference's rows back to back, row stride (cols/256)*144;
@@ -58,8 +60,8 @@ enum GemvMode : int {
   MODE_SWIGLU = 3,  // y = SwiGLU(acc(w), acc(w2))
 };
 
-// One matrix of a fused GEMV launch.  A workgroup owns `rpw` consecutive
-// rows; each of its threads owns one quarter of one super-block of one row
+// One matrix of a GEMV launch.  A workgroup owns `rpw` consecutive rows;
+// each of its threads owns one quarter of one super-block of one row
 // (Q4_K: one 32-element pair; Q6_K: 16 of the 32 lanes of one half).
 struct GemvJob {
   WeightRef w;
@@ -82,31 +84,26 @@ constexpr int MAX_JOBS = 4;
 struct GemvParams {
   int prologue;
   int nb_in;
-  int n_x;      // length of x for the norm prologues
-  int n_x_lds;  // LDS floats reserved for x (multiple of 16, plus 16 of padding)
+  int n_x;      // length of x for the norm prologue
+  int n_x_lds;  // LDS floats of the x*x buffer (see chain_lds_floats)
   float eps;
   const float* x;
   const float* norm_w;
   const uint8_t* q8k_in;
-  float* x_out;
-  WeightRef emb;
-  int n_vocab;
-  int max_ctx;
-  int32_t* token_ids;
-  const float* part_v;
-  const int* part_i;
-  int n_part;
-  C2hState* state;
   int n_jobs;
   GemvJob jobs[MAX_JOBS];
 };
+
+// LDS floats for a chained-sum buffer of n values: the chain reads two
+// 32-value chunks ahead of the one it adds.
+__host__ __device__ inline int chain_lds_floats(int n) { return ((n + 31) & ~31) + 64; }
 
 struct NormParams {
   const float* x;
   const float* w;
   float eps;
   int n;
-  int n_lds;  // LDS floats per buffer (multiple of 16, plus 16 of padding)
+  int n_lds;    // chain_lds_floats(n)
   int out_sel;  // 1: write out_buf[state->nx_out]
   float* out;
   float* out_buf[2];
@@ -116,11 +113,10 @@ struct NormParams {
 // The attention block of one layer in one launch, one workgroup per query
 // head: [embed] + RMSNorm + Q8_K, the head's 64 q rows and its KV head's
 // 64 k and 64 v rows (+ bias), RoPE, KV store, attention.
-constexpr int FUSED_MAX_NB = 4;  // n_embd/256 this kernel handles (items per thread = 3*nb)
+constexpr int ATT_CH = 128;   // V positions staged in LDS per pass (chunk 0 prefetched)
+constexpr int ATT_KPF = 256;  // positions whose K row is prefetched (one per thread)
 struct AttnFusedParams {
-  int prologue;  // PRO_NORM, PRO_EMBED_NORM or PRO_ARGMAX_EMBED_NORM
   int n_embd;
-  int nb;        // floor(n_embd/256)
   int n_x_lds;
   float eps;
   const float* x;
@@ -134,7 +130,8 @@ struct AttnFusedParams {
   int32_t* token_ids;
   WeightRef wq, wk, wv;
   int tq, tk, tv;
-  const float *bq, *bk, *bv;
+  const float *bq, *bk, *bv;  // never null: a zero buffer stands in for an absent bias
+  int bias_mask;              // bit 0/1/2: q/k/v bias present (tensor/ops.go:221-225 adds only those)
   float* out;  // attention output [n_heads*64]
   float* kv;
   const float* rope_cos;
@@ -145,12 +142,15 @@ struct AttnFusedParams {
   int n_heads;
   int n_kv_heads;
   int max_ctx;
-  int a_lds;    // floats of region A (Q8_K row, x, x*x, scales; reused for V)
-  int b_lds;    // floats of region B (GEMV terms, then scores)
-  int vchunk;   // positions of V staged in LDS per pass
   float scale;
   C2hState* state;
 };
+
+// Dynamic LDS of the attention kernel, in floats: staged V | GEMV terms |
+// Q6_K block scales | x*x chain buffer | scores.
+__host__ __device__ inline int attn_lds_floats(int nb, int n_x_lds, int max_ctx) {
+  return ATT_CH * 64 + 3 * 64 * 4 * nb + 3 * 64 * nb + n_x_lds + chain_lds_floats(max_ctx);
+}
 
 constexpr int VOCAB_TILES = 1;  // 32-row tiles per vocab workgroup
 
@@ -170,11 +170,14 @@ struct VocabParams {
 };
 
 __global__ void k_quantize_q8k(const float* __restrict__ x, int nb, uint8_t* __restrict__ y);
-__global__ void k_gemv(GemvParams P);
+__global__ void k_gemv_q8k(GemvParams P);
+template <int NB, int PRO, int MODE>
+__global__ void k_gemv_row(GemvParams P);
 __global__ void k_rmsnorm(NormParams P);
-template <int NB>
-__global__ void k_attn_fused(AttnFusedParams P);
+template <int NB, int PRO>
+__global__ void k_attn(AttnFusedParams P);
 __global__ void k_vocab(VocabParams P);
 __global__ void k_argmax_final(const float* pv, const int* pi, int n, C2hState* state);
+__global__ void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16);
 
 }  // namespace c2h

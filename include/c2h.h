@@ -166,10 +166,21 @@ int c2h_sync(c2h_ctx* ctx);
 
 /* ---- measurement --------------------------------------------------------- */
 
-/* Average device time (ms) of `iters` back-to-back launches of the fused
- * vocab projection + penalty + argmax kernel on the context stream, bracketed
- * by HIP events on that stream; uses the current normX and pos. */
-int c2h_time_vocab(c2h_ctx* ctx, int32_t iters, int32_t pos, float* ms_per_launch);
+/* Average device time (ms) of `iters` launches of the fused vocab projection
+ * + penalty + argmax kernel, each bracketed by its own pair of HIP events on
+ * the context stream; uses the current normX and pos.  With in_step != 0 a
+ * forward pass (token 0 at pos, all layers) runs between launches, so the
+ * 144 MB matrix is read from HBM as inside a decode step rather than from
+ * the 256 MB last-level cache; that forward pass overwrites the KV entry at
+ * pos and the non-current normX buffer.  With in_step == 0 the launches run
+ * back to back. */
+int c2h_time_vocab(c2h_ctx* ctx, int32_t iters, int32_t pos, int32_t in_step, float* ms_per_launch);
+
+/* Measurement aid with no counterpart in the reference: `reps` plain
+ * device-to-device copies of `bytes` (a multiple of 16) between two scratch
+ * buffers it allocates and frees; the average ms per copy.  Its known
+ * traffic calibrates the memory counters of a profiler run. */
+int c2h_copy_bench(c2h_ctx* ctx, int64_t bytes, int32_t reps, float* ms_per_copy);
 
 /* Average device time (ms) of `iters` decode steps (graph replays) at
  * positions pos, pos+1, ...; tokens are fed back on the device. */
