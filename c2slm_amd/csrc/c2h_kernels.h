@@ -20,9 +20,11 @@ struct C2hState {
 
 // Q8_K row as the GEMVs keep it in LDS: quants packed four per dword, the
 // f32 scale and the sixteen 16-element sums widened to int32.
+// Block rows are padded to 68 dwords so that neighbouring blocks start in
+// different LDS banks.
 template <int NB>
 struct Q8KRow {
-  uint32_t q[NB][64];
+  uint32_t q[NB][68];
   float d[NB];
   int32_t bs[NB][16];
 };

@@ -67,70 +67,64 @@ __device__ __forceinline__ float amax_key(float v) {
 
 // ------------------------------------------------------------- Q8_K (A1)
 
-// Q8_K quantisation of NB blocks held one element per thread: v[k] is
-// element threadIdx.x of block k.  internal/simd/c2_quantize_q8_k_gen.go:22-90:
-// amax of branch-|x|, d = amax/127, q = int(x*(127/amax) ± 0.5) clamped to
-// ±127, zero block when amax == 0, bsums over 16 quants.  The per-block
-// wave reductions of all blocks run interleaved (DPP steps, no LDS).
-// red: LDS float[4*NB]; scl: LDS float[2*NB].
+// One quant of internal/simd/c2_quantize_q8_k_gen.go:58-74: q = int(x*isc
+// ± 0.5) clamped to ±127, 0 in a zero block (m == 0).  Branch-free: |x*isc|
+// is at most 127(1+2^-23) whenever isc is finite, so only NaN and ±Inf
+// (isc = Inf for a tiny amax) reach Go's out-of-range conversion, whose
+// INT64_MIN result clamps to -127.
+__device__ __forceinline__ int quant1(float x, float isc, float m) {
+  const float tq = x * isc;
+  const float r = (tq >= 0.0f) ? (tq + 0.5f) : (tq - 0.5f);
+  const bool in_range = (r >= -9223372036854775808.0f) && (r < 9223372036854775808.0f);
+  const int q = in_range ? (int)fminf(fmaxf(r, -127.0f), 127.0f) : -127;
+  return (m != 0.0f) ? q : 0;
+}
+
+// amax_key as int bits: non-negative non-NaN floats order like their bits.
+__device__ __forceinline__ int amax_bits(float v) { return __float_as_int(amax_key(v)); }
+
+// Q8_K quantisation of block b by one wave; lane l holds elements 4l..4l+3
+// (internal/simd/c2_quantize_q8_k_gen.go:22-90: amax of branch-|x|,
+// d = amax/127, q = int(x*(127/amax) ± 0.5) clamped to ±127, zero block when
+// amax == 0, bsums over 16 quants).  The whole block stays in one wave:
+// the amax is a DPP reduction, the four quants of a lane pack into the
+// dword q[b][l], a 16-quant bsum is a quad reduction.  No barrier.
+template <class Row>
+__device__ __forceinline__ void quantize_wave(const float4& v, int b, Row& s) {
+  const int lane = threadIdx.x & 63;
+  int a = max(max(amax_bits(v.x), amax_bits(v.y)), max(amax_bits(v.z), amax_bits(v.w)));
+  a = max(a, dpp_i<DPP_QUAD_1032>(a));
+  a = max(a, dpp_i<DPP_QUAD_2301>(a));
+  a = max(a, dpp_i<DPP_HALF_MIRROR>(a));
+  a = max(a, dpp_i<DPP_MIRROR>(a));
+  a = max(a, dpp_i<DPP_BCAST15, 0xa>(a));
+  a = max(a, dpp_i<DPP_BCAST31, 0xc>(a));
+  const float m = __int_as_float(__builtin_amdgcn_readlane(a, 63));
+  float d = 0.0f, isc = 0.0f;
+  if (m != 0.0f) {
+    d = m / 127.0f;
+    isc = 127.0f / m;
+  }
+  const int q0 = quant1(v.x, isc, m), q1 = quant1(v.y, isc, m);
+  const int q2 = quant1(v.z, isc, m), q3 = quant1(v.w, isc, m);
+  s.q[b][lane] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+                 ((uint32_t)(q3 & 0xff) << 24);
+  int bsum = (q0 + q1) + (q2 + q3);
+  bsum += dpp_i<DPP_QUAD_1032>(bsum);
+  bsum += dpp_i<DPP_QUAD_2301>(bsum);
+  if ((lane & 3) == 0) s.bs[b][lane >> 2] = bsum;
+  if (lane == 0) s.d[b] = d;
+}
+
+// Quantise NB blocks of a row held as float4 per lane: wave w owns blocks
+// w, w+4, ... (v[i] = elements 4l..4l+3 of block w+4i).  Ends with a barrier.
 template <int NB, class Row>
-__device__ __forceinline__ void quantize_regs(const float (&v)[NB], Row& s, float* red, float* scl) {
-  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-  float a[NB];
+__device__ __forceinline__ void quantize_row_waves(const float4 (&v)[(NB + 3) / 4], Row& s) {
+  const int wave = threadIdx.x >> 6;
 #pragma unroll
-  for (int k = 0; k < NB; ++k) a[k] = amax_key(v[k]);
-#pragma unroll
-  for (int k = 0; k < NB; ++k) a[k] = fmaxf(a[k], dpp_f<DPP_QUAD_1032>(a[k]));
-#pragma unroll
-  for (int k = 0; k < NB; ++k) a[k] = fmaxf(a[k], dpp_f<DPP_QUAD_2301>(a[k]));
-#pragma unroll
-  for (int k = 0; k < NB; ++k) a[k] = fmaxf(a[k], dpp_f<DPP_HALF_MIRROR>(a[k]));
-#pragma unroll
-  for (int k = 0; k < NB; ++k) a[k] = fmaxf(a[k], dpp_f<DPP_MIRROR>(a[k]));
-#pragma unroll
-  for (int k = 0; k < NB; ++k) a[k] = fmaxf(a[k], dpp_f<DPP_BCAST15, 0xa>(a[k]));
-#pragma unroll
-  for (int k = 0; k < NB; ++k) a[k] = fmaxf(a[k], dpp_f<DPP_BCAST31, 0xc>(a[k]));
-  if (lane == 63) {
-#pragma unroll
-    for (int k = 0; k < NB; ++k) red[wave * NB + k] = a[k];
-  }
-  __syncthreads();
-  if (t < NB) {
-    const float m = fmaxf(fmaxf(red[t], red[NB + t]), fmaxf(red[2 * NB + t], red[3 * NB + t]));
-    float d = 0.0f, isc = 0.0f;
-    if (m != 0.0f) {
-      d = m / 127.0f;
-      isc = 127.0f / m;
-    }
-    scl[t] = isc;
-    scl[NB + t] = m;
-    s.d[t] = d;
-  }
-  __syncthreads();
-  int q[NB];
-#pragma unroll
-  for (int k = 0; k < NB; ++k) {
-    int qq = 0;
-    if (scl[NB + k] != 0.0f) {
-      const float tq = v[k] * scl[k];
-      const float r = (tq >= 0.0f) ? (tq + 0.5f) : (tq - 0.5f);
-      qq = go_f32_to_int_clamped127(r);
-    }
-    reinterpret_cast<int8_t*>(s.q[k])[t] = (int8_t)qq;
-    q[k] = qq;
-  }
-#pragma unroll
-  for (int k = 0; k < NB; ++k) q[k] += dpp_i<DPP_QUAD_1032>(q[k]);
-#pragma unroll
-  for (int k = 0; k < NB; ++k) q[k] += dpp_i<DPP_QUAD_2301>(q[k]);
-#pragma unroll
-  for (int k = 0; k < NB; ++k) q[k] += dpp_i<DPP_HALF_MIRROR>(q[k]);
-#pragma unroll
-  for (int k = 0; k < NB; ++k) q[k] += dpp_i<DPP_MIRROR>(q[k]);
-  if ((t & 15) == 0) {
-#pragma unroll
-    for (int k = 0; k < NB; ++k) s.bs[k][t >> 4] = q[k];
+  for (int i = 0; i < (NB + 3) / 4; ++i) {
+    const int b = wave + 4 * i;
+    if (b < NB) quantize_wave(v[i], b, s);
   }
   __syncthreads();
 }
@@ -191,9 +185,13 @@ __device__ __forceinline__ float seq_sum_lds(const float* a, int n) {
   const int nc = n >> 5;
   int i = 0;
   for (; i + 2 <= nc; i += 2) {
+    // the scheduler would otherwise sink each chunk's reads below the adds
+    // of the previous chunk and expose the LDS latency on every chunk
     load_chunk(B, a4, i + 1);
+    __builtin_amdgcn_sched_barrier(0);
     add_chunk(s, A);
     load_chunk(A, a4, i + 2);
+    __builtin_amdgcn_sched_barrier(0);
     add_chunk(s, B);
   }
   const int r = n & 31;
@@ -219,17 +217,13 @@ __device__ __forceinline__ float seq_sum_lds(const float* a, int n) {
   return s;
 }
 
-// 1/rms of the n values x[tid + 256k] (k < NX), tensor/ops.go:207-218:
-// sequential f32 sum of x*x, inv = f32(1/sqrt(f64(sum/n + eps))).
-// sq: LDS scratch of chain_lds_floats(n) floats.
-template <int NX>
-__device__ __forceinline__ float rms_inv(const float (&xr)[NX], int n, float eps, float* sq, float* inv_slot) {
+// 1/rms of n values (n <= 1024, a multiple of 4) held as elements 4t..4t+3
+// by thread t < n/4, tensor/ops.go:207-218: sequential f32 sum of x*x,
+// inv = f32(1/sqrt(f64(sum/n + eps))).  sq: LDS scratch of
+// chain_lds_floats(n) floats.
+__device__ __forceinline__ float rms_inv4(const float4& x, int n, float eps, float* sq, float* inv_slot) {
   const int tid = threadIdx.x;
-#pragma unroll
-  for (int k = 0; k < NX; ++k) {
-    const int i = tid + 256 * k;
-    if (i < n) sq[i] = xr[k] * xr[k];
-  }
+  if (4 * tid < n) reinterpret_cast<float4*>(sq)[tid] = make_float4(x.x * x.x, x.y * x.y, x.z * x.z, x.w * x.w);
   __syncthreads();
   if (tid == 0) {
     const float s = seq_sum_lds(sq, n);
@@ -244,12 +238,14 @@ __device__ __forceinline__ float rms_inv(const float (&xr)[NX], int n, float eps
 // loads, then computes.
 __device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
 
-// x[min(tid + 256k, n-1)]: unconditional loads (the clamped duplicates of
-// the tail are never used).
-template <int NX>
-__device__ __forceinline__ void load_strided(const float* __restrict__ x, int n, float (&r)[NX]) {
-#pragma unroll
-  for (int k = 0; k < NX; ++k) r[k] = x[min((int)threadIdx.x + 256 * k, n - 1)];
+// Elements 4t..4t+3 of x (n a multiple of 4): an unconditional load, clamped
+// to the last four for threads past the end (their values are never used).
+__device__ __forceinline__ float4 load4(const float* __restrict__ x, int n) {
+  return *reinterpret_cast<const float4*>(x + min(4 * (int)threadIdx.x, n - 4));
+}
+
+__device__ __forceinline__ float4 norm4(const float4& x, float inv, const float4& w) {
+  return make_float4((x.x * inv) * w.x, (x.y * inv) * w.y, (x.z * inv) * w.z, (x.w * inv) * w.w);
 }
 
 // ------------------------------------------------------------- GEMV items
@@ -403,6 +399,43 @@ __device__ __forceinline__ float fold_row(int type, const float* terms, const fl
   return acc;
 }
 
+// Value of one item for the layer kernels' fold: Q4_K the pair term; Q6_K
+// the block's f32(isum)*(d*q8d), isum summed (exactly) over the block's
+// four quarter-items, which sit in the adjacent lanes of one quad and are
+// always active together.
+template <class Row>
+__device__ __forceinline__ float item_value(const ItemW& it, int type, const Row& s, int b, int u) {
+  if (type == T_Q4_K) {
+    int32_t lo, hi;
+    return q4k_item(it, s, b, u, &lo, &hi);
+  }
+  int32_t part = q6k_item(it, s, b, u);
+  part += dpp_i<DPP_QUAD_1032>(part);
+  part += dpp_i<DPP_QUAD_2301>(part);
+  return (float)part * (fp16_simd(it.d) * s.d[b]);
+}
+
+// Item value into the row's term slots [4b + u] (Q6_K: once per block, at u == 0).
+__device__ __forceinline__ void store_item(float* row_terms, int type, int b, int u, float v) {
+  if (type == T_Q4_K || u == 0) row_terms[4 * b + u] = v;
+}
+
+// Fold of one row in the reference's order: Q4_K acc += term over (block,
+// pair), c2_tensor_dot_q4_k_q8_k_gen.go:85; Q6_K acc += f32(isum)*(d*q8d)
+// over blocks, c2_tensor_gemv2_q6_k_q8_k_gen.go:208-209.
+template <int NB>
+__device__ __forceinline__ float fold_terms(int type, const float* row_terms) {
+  float acc = 0.0f;
+  if (type == T_Q4_K) {
+#pragma unroll
+    for (int i = 0; i < 4 * NB; ++i) acc = acc + row_terms[i];
+  } else {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc = acc + row_terms[4 * b];
+  }
+  return acc;
+}
+
 // ------------------------------------------------------------- prologues
 
 // Argmax over the vocab kernel's per-workgroup candidates.
@@ -440,27 +473,25 @@ __device__ __forceinline__ float q8_0_scale(uint32_t h16) {
 }
 
 // Token embedding (engine/model.go:221-247 -> tensor/ops.go:412-424) of
-// elements tid + 256k from the packed Q8_0 table, decoded like
+// elements 4t..4t+3 from the packed Q8_0 table, decoded like
 // tensor.FP16ToF32 (-0 kept).  Loads are unconditional (clamped index).
-template <int NX>
-__device__ __forceinline__ void embed_regs(const WeightRef& emb, int n_vocab, int E, int tok, float (&xr)[NX]) {
+__device__ __forceinline__ float4 embed4(const WeightRef& emb, int n_vocab, int E, int tok) {
   if (tok >= n_vocab || tok < 0) tok = 0;
   const int nb8 = E / QK8_0;
   const uint8_t* row = emb.q + (size_t)tok * q8_0_row_stride(nb8);
   const uint16_t* drow = reinterpret_cast<const uint16_t*>(row);
   const uint8_t* qsrow = row + (size_t)q8_0_dpad(nb8) * 2;
-  int8_t qv[NX];
-  uint16_t dv[NX];
+  const int e0 = min(4 * (int)threadIdx.x, E - 4);
+  const int b = e0 >> 5;  // the four elements share block b
+  int8_t qv[4];
 #pragma unroll
-  for (int k = 0; k < NX; ++k) {
-    const int e = min((int)threadIdx.x + 256 * k, E - 1);
-    const int b = e >> 5, kk = e & 31;
-    const int j = kk & 7, i = kk >> 3;  // element kk of block b is byte i of lane j's dword
-    qv[k] = (int8_t)qsrow[((b >> 2) * 8 + j) * 16 + (b & 3) * 4 + i];
-    dv[k] = drow[b];
+  for (int i = 0; i < 4; ++i) {
+    const int kk = (e0 + i) & 31;
+    // element kk of block b is byte kk>>3 of lane (kk&7)'s dword
+    qv[i] = (int8_t)qsrow[((b >> 2) * 8 + (kk & 7)) * 16 + (b & 3) * 4 + (kk >> 3)];
   }
-#pragma unroll
-  for (int k = 0; k < NX; ++k) xr[k] = fp16_tensor(dv[k]) * (float)qv[k];
+  const float d = fp16_tensor(drow[b]);
+  return make_float4(d * (float)qv[0], d * (float)qv[1], d * (float)qv[2], d * (float)qv[3]);
 }
 
 // ------------------------------------------------------ GEMV (row kernel)
@@ -471,69 +502,67 @@ __device__ __forceinline__ void embed_regs(const WeightRef& emb, int n_vocab, in
 //   PRO_NORM   Q8_K(RMSNorm(x) * norm_w).
 // MODE_RESID: y[r] += acc (o and down projections); MODE_SWIGLU: y[r] =
 // SwiGLU(acc(w), acc(w2)) (gate|up, the pair shares the input).
-// Thread t owns item (row t/(4NB), block, quarter); the fold runs per row
-// in the reference's order.
+// Items are laid out block-major: thread t owns block t/(4*RPW), row
+// (t%(4*RPW))/4, quarter t%4, so the lanes of a 16-lane LDS access group
+// read the same block of the Q8_K row (broadcast, no bank conflicts).  The
+// fold runs per row in the reference's order.
 template <int NB, int PRO, int MODE>
 __global__ void __launch_bounds__(256) k_gemv_row(GemvParams P) {
   constexpr int IPR = 4 * NB;
   constexpr int RPW = 256 / IPR;
+  constexpr int BPW = (NB + 3) / 4;  // Q8_K blocks quantised per wave
   constexpr bool PAIRED = (MODE == MODE_SWIGLU);
-  constexpr int NX = (PRO == PRO_NORM) ? NB + 1 : NB;
+  static_assert(PRO != PRO_NORM || NB <= 4, "the norm prologue holds one float4 per thread");
   extern __shared__ __align__(16) unsigned char smem[];
   float* sq = reinterpret_cast<float*>(smem);  // [n_x_lds] (PRO_NORM only)
   __shared__ Q8KRow<NB> s;
-  __shared__ float red[4 * NB];
-  __shared__ float scl[2 * NB];
-  __shared__ float terms[PAIRED ? 2 : 1][256];
-  __shared__ float dq[PAIRED ? 2 : 1][RPW * NB];
+  __shared__ __align__(16) float terms[PAIRED ? 2 : 1][RPW * IPR];
   __shared__ float inv_slot;
 
   const GemvJob& J = P.jobs[0];
   const int tid = threadIdx.x;
-  const int r_local = tid / IPR;
-  const int rem = tid - r_local * IPR;
-  const int b = rem >> 2, u = rem & 3;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int b = tid / (4 * RPW);
+  const int r_local = (tid - b * 4 * RPW) >> 2;
+  const int u = tid & 3;
   const int row0 = (int)blockIdx.x * RPW;
   const int row = row0 + r_local;
-  const bool active = (r_local < RPW) && (row < J.rows);
-  const int row_c = min(row0 + min(r_local, RPW - 1), J.rows - 1);
+  const bool active = (b < NB) && (row < J.rows);
+  const int row_c = min(row, J.rows - 1);
+  const int b_c = min(b, NB - 1);
 
   // ---- loads, in the order they are consumed
-  float xa[NX];
-  float nw[NX];
+  float4 xa[BPW];
+  float4 nw = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   if (PRO == PRO_NORM) {
-    load_strided<NX>(P.x, P.n_x, xa);
-    load_strided<NX>(P.norm_w, P.n_x, nw);
+    xa[0] = load4(P.x, P.n_x);
+    nw = load4(P.norm_w, P.n_x);
   } else {
 #pragma unroll
-    for (int k = 0; k < NB; ++k) xa[k] = P.x[k * QK_K + tid];
+    for (int i = 0; i < BPW; ++i)
+      xa[i] = reinterpret_cast<const float4*>(P.x + min(wave + 4 * i, NB - 1) * QK_K)[lane];
   }
-  const ItemW w1 = load_item(J.w, J.type, NB, row_c, b, u);
+  const ItemW w1 = load_item(J.w, J.type, NB, row_c, b_c, u);
   ItemW w2;
-  if (PAIRED) w2 = load_item(J.w2, J.type2, NB, row_c, b, u);
+  if (PAIRED) w2 = load_item(J.w2, J.type2, NB, row_c, b_c, u);
   float yres = 0.0f;
   if (MODE == MODE_RESID) yres = J.y[min(row0 + min(tid, RPW - 1), J.rows - 1)];
   issue_fence();
 
   // ---- prologue: the Q8_K input row in LDS
   if (PRO == PRO_NORM) {
-    const float inv = rms_inv<NX>(xa, P.n_x, P.eps, sq, &inv_slot);
-    float xn[NB];
-#pragma unroll
-    for (int k = 0; k < NB; ++k) xn[k] = (xa[k] * inv) * nw[k];
-    quantize_regs<NB>(xn, s, red, scl);
+    const float inv = rms_inv4(xa[0], P.n_x, P.eps, sq, &inv_slot);
+    const float4 xn[1] = {norm4(xa[0], inv, nw)};  // wave w holds block w
+    if (wave < NB) quantize_wave(xn[0], wave, s);
+    __syncthreads();
   } else {
-    float xq[NB];
-#pragma unroll
-    for (int k = 0; k < NB; ++k) xq[k] = xa[k];
-    quantize_regs<NB>(xq, s, red, scl);
+    quantize_row_waves<NB>(xa, s);
   }
 
   // ---- items
   if (active) {
-    run_item(w1, J.type, s, b, u, &terms[0][tid], &dq[0][r_local * NB + b], nullptr, 0);
-    if (PAIRED) run_item(w2, J.type2, s, b, u, &terms[PAIRED ? 1 : 0][tid], &dq[PAIRED ? 1 : 0][r_local * NB + b],
-                         nullptr, 0);
+    store_item(&terms[0][r_local * IPR], J.type, b, u, item_value(w1, J.type, s, b, u));
+    if (PAIRED) store_item(&terms[PAIRED ? 1 : 0][r_local * IPR], J.type2, b, u, item_value(w2, J.type2, s, b, u));
   }
   __syncthreads();
 
@@ -541,10 +570,9 @@ __global__ void __launch_bounds__(256) k_gemv_row(GemvParams P) {
   if (tid < RPW) {
     const int r = row0 + tid;
     if (r < J.rows) {
-      const float acc = fold_row(J.type, &terms[0][tid * IPR], &dq[0][tid * NB], NB, nullptr, 0);
+      const float acc = fold_terms<NB>(J.type, &terms[0][tid * IPR]);
       if (PAIRED) {
-        const float up = fold_row(J.type2, &terms[PAIRED ? 1 : 0][tid * IPR], &dq[PAIRED ? 1 : 0][tid * NB], NB,
-                                  nullptr, 0);
+        const float up = fold_terms<NB>(J.type2, &terms[PAIRED ? 1 : 0][tid * IPR]);
         const int n8 = J.rows - (J.rows % 8);
         J.y[r] = (r < n8) ? swiglu_poly(acc, up) : swiglu_tail(acc, up);
       } else {
@@ -618,23 +646,17 @@ __global__ void __launch_bounds__(256) k_gemv_q8k(GemvParams P) {
 // ------------------------------------------------------------- final norm
 
 // normX = RMSNorm(X) * output_norm (engine/forward.go:135); x and w are
-// loaded up front, rows of up to 1280 values.
-constexpr int NORM_NX = 5;
+// loaded up front, rows of up to 1024 values (a multiple of 4).
 __global__ void __launch_bounds__(256) k_rmsnorm(NormParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
   float* sq = reinterpret_cast<float*>(smem);
   __shared__ float inv_slot;
-  float xr[NORM_NX], wr[NORM_NX];
-  load_strided<NORM_NX>(P.x, P.n, xr);
-  load_strided<NORM_NX>(P.w, P.n, wr);
+  const float4 x = load4(P.x, P.n);
+  const float4 w = load4(P.w, P.n);
   issue_fence();
-  const float inv = rms_inv<NORM_NX>(xr, P.n, P.eps, sq, &inv_slot);
+  const float inv = rms_inv4(x, P.n, P.eps, sq, &inv_slot);
   float* out = P.out_sel ? P.out_buf[P.state->nx_out] : P.out;
-#pragma unroll
-  for (int k = 0; k < NORM_NX; ++k) {
-    const int i = threadIdx.x + 256 * k;
-    if (i < P.n) out[i] = (xr[k] * inv) * wr[k];
-  }
+  if (4 * (int)threadIdx.x < P.n) reinterpret_cast<float4*>(out)[threadIdx.x] = norm4(x, inv, w);
 }
 
 // ------------------------------------------------------- attention block
@@ -683,20 +705,17 @@ __device__ __forceinline__ float attn_score(const float* q_s, const float4 (&kk4
 // place.
 template <int NB, int PRO>
 __global__ void __launch_bounds__(256) k_attn(AttnFusedParams P) {
-  constexpr int NX = NB + 1;
+  static_assert(NB <= 4, "the norm prologue holds one float4 per thread");
   constexpr int HD = 64;
   constexpr int IPR = 4 * NB;
   constexpr int IPM = HD * IPR;  // items per matrix (= 256*NB)
   constexpr int VPT = ATT_CH * HD / 4 / 256;  // staged float4 of V per thread
   extern __shared__ __align__(16) unsigned char smem[];
   float* vbuf = reinterpret_cast<float*>(smem);  // [ATT_CH][64]
-  float* terms = vbuf + ATT_CH * HD;             // [3][IPM]
-  float* dq = terms + 3 * IPM;                   // [3][64][NB]
-  float* sq = dq + 3 * HD * NB;                  // [n_x_lds]
+  float* terms = vbuf + ATT_CH * HD;             // [3][64][IPR]
+  float* sq = terms + 3 * IPM + 3 * HD * NB;     // [n_x_lds]
   float* sc = sq + P.n_x_lds;                    // [chain_lds_floats(max_ctx)]
   __shared__ Q8KRow<NB> s;
-  __shared__ float red[4 * NB];
-  __shared__ float scl[2 * NB];
   __shared__ __align__(16) float qkv_s[3][HD];
   __shared__ float red_m[4];
   __shared__ float inv_slot;
@@ -715,28 +734,28 @@ __global__ void __launch_bounds__(256) k_attn(AttnFusedParams P) {
   const int plast = max(min(pos, P.max_ctx) - 1, 0);  // last stored position (clamp target)
 
   // ---- loads, in the order they are consumed
-  float xr[NX], nw[NX];
+  // x: elements 4t..4t+3; items: thread t owns row t/4, quarter t%4 of
+  // every block j of the three matrices (block-major: a 16-lane LDS access
+  // group reads one block of the Q8_K row)
+  float4 xr;
   int tok = 0;
   if (PRO == PRO_NORM) {
-    load_strided<NX>(P.x, E, xr);
+    xr = load4(P.x, E);
   } else {
     tok = (PRO == PRO_ARGMAX_EMBED_NORM) ? reduce_argmax_partials(P.part_v, P.part_i, P.n_part, ared)
                                          : P.state->token;
-    embed_regs<NX>(P.emb, P.n_vocab, E, tok, xr);
+    xr = embed4(P.emb, P.n_vocab, E, tok);
   }
-  load_strided<NX>(P.norm_w, E, nw);
+  const float4 nw = load4(P.norm_w, E);
   const WeightRef* W[3] = {&P.wq, &P.wk, &P.wv};
   const int T3[3] = {P.tq, P.tk, P.tv};
   const int rbase[3] = {h * HD, g * HD, g * HD};
+  const int ir = tid >> 2, iu = tid & 3;
   ItemW w[3][NB];
 #pragma unroll
   for (int m = 0; m < 3; ++m) {
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      const int i = tid + 256 * j;
-      const int r = i / IPR, rem = i - r * IPR;
-      w[m][j] = load_item(*W[m], T3[m], NB, rbase[m] + r, rem >> 2, rem & 3);
-    }
+    for (int j = 0; j < NB; ++j) w[m][j] = load_item(*W[m], T3[m], NB, rbase[m] + ir, j, iu);
   }
   // bias of row tid%64 of matrix tid/64 (threads < 192 use it).  The host
   // passes a valid buffer for absent biases and says in bias_mask which
@@ -754,34 +773,25 @@ __global__ void __launch_bounds__(256) k_attn(AttnFusedParams P) {
 
   // ---- prologue: layer 0 publishes the embedded token
   if (PRO != PRO_NORM && blockIdx.x == 0) {
-#pragma unroll
-    for (int k = 0; k < NX; ++k) {
-      const int i = tid + 256 * k;
-      if (i < E) P.x_out[i] = xr[k];
-    }
+    if (4 * tid < E) reinterpret_cast<float4*>(P.x_out)[tid] = xr;
     if (tid == 0) {
       P.state->token = tok;
       if (pos >= 0 && pos < P.max_ctx) P.token_ids[pos] = tok;
     }
   }
   {
-    const float inv = rms_inv<NX>(xr, E, P.eps, sq, &inv_slot);
-    float xn[NB];
-#pragma unroll
-    for (int k = 0; k < NB; ++k) xn[k] = (xr[k] * inv) * nw[k];
-    quantize_regs<NB>(xn, s, red, scl);
+    const float inv = rms_inv4(xr, E, P.eps, sq, &inv_slot);
+    const int wave = tid >> 6;
+    if (wave < NB) quantize_wave(norm4(xr, inv, nw), wave, s);  // wave w holds block w
+    __syncthreads();
   }
 
   // ---- items -> terms [m][r][4nb]
 #pragma unroll
   for (int m = 0; m < 3; ++m) {
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      const int i = tid + 256 * j;
-      const int r = i / IPR, rem = i - r * IPR;
-      const int b = rem >> 2, u = rem & 3;
-      run_item(w[m][j], T3[m], s, b, u, terms + m * IPM + i, dq + (m * HD + r) * NB + b, nullptr, 0);
-    }
+    for (int j = 0; j < NB; ++j)
+      store_item(terms + m * IPM + ir * IPR, T3[m], j, iu, item_value(w[m][j], T3[m], s, j, iu));
   }
   __syncthreads();
 
@@ -805,7 +815,7 @@ __global__ void __launch_bounds__(256) k_attn(AttnFusedParams P) {
   if (tid < 3 * HD) {
     const int m = tid / HD, r = tid - m * HD;
     const int tm = (m == 0) ? P.tq : (m == 1 ? P.tk : P.tv);  // no dynamic index into a local array
-    float acc = fold_row(tm, terms + m * IPM + r * IPR, dq + (m * HD + r) * NB, NB, nullptr, 0);
+    float acc = fold_terms<NB>(tm, terms + m * IPM + r * IPR);
     if (has_bias) acc = acc + bval;
     qkv_s[m][r] = acc;
   }
