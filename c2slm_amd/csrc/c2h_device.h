@@ -40,6 +40,26 @@ __device__ __forceinline__ float fp16_simd(uint32_t h) {
   return bits_f32(sign | ((e + 112u) << 23) | (m << 13));
 }
 
+// c ? a : b as mask arithmetic: the compiler turns some ternaries on
+// per-lane conditions into divergent branches, which this cannot become.
+__device__ __forceinline__ uint32_t blend_u32(bool c, uint32_t a, uint32_t b) {
+  const uint32_t m = 0u - (uint32_t)c;
+  return (a & m) | (b & ~m);
+}
+
+// fp16_simd without branches (identical bits): blends the subnormal, normal
+// and Inf/NaN encodings, so a per-lane value never splits the wave.
+__device__ __forceinline__ float fp16_simd_nb(uint32_t h) {
+  const uint32_t sign = (h >> 15) << 31;
+  const uint32_t e = (h >> 10) & 31u;
+  const uint32_t m = h & 0x3ffu;
+  // subnormal (or zero): m * 2^-24 is exact; both zeros give +0
+  const uint32_t sub = __float_as_uint((float)m * 0x1p-24f) | blend_u32(m != 0u, sign, 0u);
+  const uint32_t normal = sign | ((e + 112u) << 23) | (m << 13);
+  const uint32_t special = sign | 0x7f800000u | (m << 13);
+  return bits_f32(blend_u32(e == 0u, sub, blend_u32(e == 31u, special, normal)));
+}
+
 // tensor.FP16ToF32 (tensor/fp16.go:16-50): as above but -0 keeps its sign.
 __device__ __forceinline__ float fp16_tensor(uint32_t h) {
   if ((h & 0x7fffu) == 0) return bits_f32((h >> 15) << 31);

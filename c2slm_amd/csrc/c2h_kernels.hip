@@ -295,23 +295,23 @@ template <class Row>
 __device__ __forceinline__ float q4k_item(const ItemW& it, const Row& s, int b, int u, int32_t* lo_out,
                                           int32_t* hi_out) {
   const float q8d = s.d[b];
-  const float dW = fp16_simd(it.a.x & 0xffffu) * q8d;
-  const float mW = fp16_simd(it.a.x >> 16) * q8d;
-  // scale/min pairs 2u, 2u+1 (gen.go:47-61); scale bytes sit at 4..15
-  auto sb = [&](int i) { return byte_of(it.a, 4 + i); };
-  uint32_t sc0, sc1, m0, m1;
-  if (u < 2) {
-    sc0 = sb(2 * u) & 63;
-    m0 = sb(2 * u + 4) & 63;
-    sc1 = sb(2 * u + 1) & 63;
-    m1 = sb(2 * u + 5) & 63;
-  } else {
-    const int k0 = 2 * u - 4, k1 = 2 * u - 3;
-    sc0 = (sb(k0 + 8) & 15) | ((sb(k0) >> 6) << 4);
-    m0 = (sb(k0 + 8) >> 4) | ((sb(k0 + 4) >> 6) << 4);
-    sc1 = (sb(k1 + 8) & 15) | ((sb(k1) >> 6) << 4);
-    m1 = (sb(k1 + 8) >> 4) | ((sb(k1 + 4) >> 6) << 4);
-  }
+  const float dW = fp16_simd_nb(it.a.x & 0xffffu) * q8d;
+  const float mW = fp16_simd_nb(it.a.x >> 16) * q8d;
+  // scale/min pairs 2u, 2u+1 (gen.go:47-61), branch-free in u: the scale
+  // bytes sit at 4..15 (words S0 = bytes 0-3, S1 = 4-7, S2 = 8-11 of the
+  // 12), and both the low (u < 2) and the high (u >= 2) forms use byte
+  // offsets 2(u&1) and 2(u&1)+1 of their words.
+  const uint32_t S0 = it.a.y, S1 = it.a.z, S2 = it.a.w;
+  const uint32_t o0 = 16u * (uint32_t)(u & 1), o1 = o0 + 8u;
+  const bool hi_pair = u >= 2;
+  const uint32_t sc0 = blend_u32(hi_pair, __builtin_amdgcn_ubfe(S2, o0, 4) | (__builtin_amdgcn_ubfe(S0, o0 + 6, 2) << 4),
+                                 __builtin_amdgcn_ubfe(S0, o0, 6));
+  const uint32_t m0 = blend_u32(hi_pair, __builtin_amdgcn_ubfe(S2, o0 + 4, 4) | (__builtin_amdgcn_ubfe(S1, o0 + 6, 2) << 4),
+                                __builtin_amdgcn_ubfe(S1, o0, 6));
+  const uint32_t sc1 = blend_u32(hi_pair, __builtin_amdgcn_ubfe(S2, o1, 4) | (__builtin_amdgcn_ubfe(S0, o1 + 6, 2) << 4),
+                                 __builtin_amdgcn_ubfe(S0, o1, 6));
+  const uint32_t m1 = blend_u32(hi_pair, __builtin_amdgcn_ubfe(S2, o1 + 4, 4) | (__builtin_amdgcn_ubfe(S1, o1 + 6, 2) << 4),
+                                __builtin_amdgcn_ubfe(S1, o1, 6));
   const uint32_t* q8 = s.q[b] + 16 * u;
   int lo = 0, hi = 0;
 #pragma unroll
@@ -412,7 +412,7 @@ __device__ __forceinline__ float item_value(const ItemW& it, int type, const Row
   int32_t part = q6k_item(it, s, b, u);
   part += dpp_i<DPP_QUAD_1032>(part);
   part += dpp_i<DPP_QUAD_2301>(part);
-  return (float)part * (fp16_simd(it.d) * s.d[b]);
+  return (float)part * (fp16_simd_nb(it.d) * s.d[b]);
 }
 
 // Item value into the row's term slots [4b + u] (Q6_K: once per block, at u == 0).
