@@ -217,6 +217,83 @@ __device__ __forceinline__ float seq_sum_lds(const float* a, int n) {
   return s;
 }
 
+// Wave-wide inclusive prefix sum (DPP, Hillis-Steele within rows of 16,
+// then across rows).  It only steers the speculation in seq_sum_wave; its
+// roundings never reach a result.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_or0(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, false));
+}
+__device__ __forceinline__ float wave_incl_scan(float x) {
+  x = x + dpp_or0<0x111>(x);  // row_shr:1
+  x = x + dpp_or0<0x112>(x);  // row_shr:2
+  x = x + dpp_or0<0x114>(x);  // row_shr:4
+  x = x + dpp_or0<0x118>(x);  // row_shr:8
+  x = x + dpp_or0<DPP_BCAST15, 0xa>(x);
+  x = x + dpp_or0<DPP_BCAST31, 0xc>(x);
+  return x;
+}
+__device__ __forceinline__ float wave_shift_up(float x) { return dpp_or0<0x138>(x); }  // wave_shr:1, lane 0 gets 0
+
+// The reference's sequential f32 sum (((0 + a[0]) + a[1]) + ...) + a[n-1]
+// (tensor/ops.go:209-211 RMSNorm, :331-333 Softmax) of n <= 1024 values
+// a[i] >= +0 in LDS, computed by one whole wave and returned in every lane,
+// bit-identical to the one-lane chain but ~6x shorter:
+//   lane l owns chunk [16l, 16l+16); from a start S_l it runs the chunk's
+//   16 dependent adds to R_l.  Lane 0's start is 0 (exact).  If R_l ==
+//   S_{l+1} for every l, each start is by induction the exact sequential
+//   partial sum and R_63 is the exact total.  The starts begin as a
+//   parallel-prefix guess; each round keeps the verified prefix, sets the
+//   first unverified start to its predecessor's (now exact) R, and shifts
+//   the later ones by the accumulated differences, which is exact while
+//   the sums stay in one binade.  Each round extends the exact prefix by at
+//   least one chunk; after SPEC_ROUNDS lane 0 finishes sequentially from
+//   the last exact start.  a must be readable up to round_up(n, 16).
+constexpr int SPEC_C = 16;
+constexpr int SPEC_ROUNDS = 10;
+__device__ __forceinline__ float seq_sum_wave(const float* a, int n) {
+  const int lane = threadIdx.x & 63;
+  const int base = lane * SPEC_C;
+  float v[SPEC_C];
+  {
+    const float4* a4 = reinterpret_cast<const float4*>(a + min(base, (n - 1) & ~(SPEC_C - 1)));
+#pragma unroll
+    for (int k = 0; k < SPEC_C / 4; ++k) {
+      const float4 t = a4[k];
+      v[4 * k + 0] = t.x;
+      v[4 * k + 1] = t.y;
+      v[4 * k + 2] = t.z;
+      v[4 * k + 3] = t.w;
+    }
+#pragma unroll
+    for (int k = 0; k < SPEC_C; ++k) v[k] = (base + k < n) ? v[k] : 0.0f;  // +0 adds are exact no-ops
+  }
+  float cs = 0.0f;
+#pragma unroll
+  for (int k = 0; k < SPEC_C; ++k) cs = cs + v[k];
+  float S = (lane == 0) ? 0.0f : wave_shift_up(wave_incl_scan(cs));
+  int m = -1;  // lanes <= m have verified starts
+  for (int round = 0; round < SPEC_ROUNDS; ++round) {
+    float R = S;
+#pragma unroll
+    for (int k = 0; k < SPEC_C; ++k) R = R + v[k];
+    const float s_next = __shfl_down(S, 1);
+    const unsigned long long bad = __ballot(lane < 63 && !(R == s_next));
+    if (bad == 0ull) return __shfl(R, 63);
+    m = __ffsll(bad) - 1;  // first lane whose successor's start is wrong; starts 0..m are exact
+    const float e = (lane < 63) ? (R - s_next) : 0.0f;
+    const float shift = (lane == 0) ? 0.0f : wave_shift_up(wave_incl_scan(e));
+    const float r_prev = __shfl_up(R, 1);
+    S = (lane <= m) ? S : ((lane == m + 1) ? r_prev : S + shift);
+  }
+  // starts 0..m+1 are exact: finish sequentially from chunk m+1
+  float s = __shfl(S, m + 1);
+  if (lane == 0) {
+    for (int i = (m + 1) * SPEC_C; i < n; ++i) s = s + a[i];
+  }
+  return __shfl(s, 0);
+}
+
 // 1/rms of n values (n <= 1024, a multiple of 4) held as elements 4t..4t+3
 // by thread t < n/4, tensor/ops.go:207-218: sequential f32 sum of x*x,
 // inv = f32(1/sqrt(f64(sum/n + eps))).  sq: LDS scratch of
@@ -225,9 +302,9 @@ __device__ __forceinline__ float rms_inv4(const float4& x, int n, float eps, flo
   const int tid = threadIdx.x;
   if (4 * tid < n) reinterpret_cast<float4*>(sq)[tid] = make_float4(x.x * x.x, x.y * x.y, x.z * x.z, x.w * x.w);
   __syncthreads();
-  if (tid == 0) {
-    const float s = seq_sum_lds(sq, n);
-    *inv_slot = (float)(1.0 / sqrt((double)(s / (float)n + eps)));
+  if (tid < 64) {
+    const float s = seq_sum_wave(sq, n);
+    if (tid == 0) *inv_slot = (float)(1.0 / sqrt((double)(s / (float)n + eps)));
   }
   __syncthreads();
   return *inv_slot;
@@ -872,7 +949,14 @@ __global__ void __launch_bounds__(256) k_attn(AttnFusedParams P) {
   if (sc[0] != sc[0]) mx = sc[0];
   for (int p = tid; p < T; p += blockDim.x) sc[p] = (float)exp((double)(sc[p] - mx));
   __syncthreads();
-  if (tid == 0) inv_slot = 1.0f / seq_sum_lds(sc, T);
+  if (T <= 64 * SPEC_C) {
+    if (tid < 64) {
+      const float ssum = seq_sum_wave(sc, T);
+      if (tid == 0) inv_slot = 1.0f / ssum;
+    }
+  } else if (tid == 0) {
+    inv_slot = 1.0f / seq_sum_lds(sc, T);
+  }
 #pragma unroll
   for (int i = 0; i < VPT; ++i) reinterpret_cast<f32x4_t*>(vbuf)[tid + 256 * i] = vreg[i];
   __syncthreads();
