@@ -50,7 +50,6 @@ struct c2h_ctx {
 
   float *X = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *h = nullptr;
   float* normx[2] = {nullptr, nullptr};
-  float* zero_bias = nullptr;  // n_embd zeros read in place of an absent q/k/v bias
   int nx_cur = 0, nx_prev = 0;
   float* kv = nullptr;
   int32_t* token_ids = nullptr;
@@ -260,39 +259,40 @@ GemvKernel gemv_row_kernel(int nb, int pro, int mode) {
       default: return nullptr;
     }
   }
+  if (mode == MODE_BIAS && nb == 3) {
+    if (pro == PRO_NORM) return k_gemv_row<3, PRO_NORM, MODE_BIAS>;
+    if (pro == PRO_EMBED_NORM) return k_gemv_row<3, PRO_EMBED_NORM, MODE_BIAS>;
+    if (pro == PRO_ARGMAX_EMBED_NORM) return k_gemv_row<3, PRO_ARGMAX_EMBED_NORM, MODE_BIAS>;
+  }
+  if (mode == MODE_BIAS && nb == 4) {
+    if (pro == PRO_NORM) return k_gemv_row<4, PRO_NORM, MODE_BIAS>;
+    if (pro == PRO_EMBED_NORM) return k_gemv_row<4, PRO_EMBED_NORM, MODE_BIAS>;
+    if (pro == PRO_ARGMAX_EMBED_NORM) return k_gemv_row<4, PRO_ARGMAX_EMBED_NORM, MODE_BIAS>;
+  }
   return nullptr;
 }
 
-// One job per row-kernel launch; PRO_NORM needs the x*x chain buffer.
-void launch_gemv_row(c2h_ctx* c, GemvParams& P) {
+// A row-kernel launch over all its jobs (same width and mode); the norm
+// prologues need the x*x chain buffer.
+void launch_gemv_row(c2h_ctx* c, GemvParams& P, int total_wg) {
   const GemvJob& J = P.jobs[0];
   GemvKernel k = gemv_row_kernel(J.nb, P.prologue, J.mode);
-  size_t lds = (P.prologue == PRO_NORM) ? (size_t)P.n_x_lds * sizeof(float) : 0;
-  hipLaunchKernelGGL(k, dim3(J.n_wg), dim3(256), lds, c->stream, P);
-}
-
-typedef void (*AttnKernel)(AttnFusedParams);
-
-// Attention-block instance for (super-blocks per row of n_embd, prologue);
-// nullptr when this build has none for that width.
-AttnKernel attn_kernel(int nb, int pro) {
-  if (nb == 3) {
-    if (pro == PRO_EMBED_NORM) return k_attn<3, PRO_EMBED_NORM>;
-    if (pro == PRO_ARGMAX_EMBED_NORM) return k_attn<3, PRO_ARGMAX_EMBED_NORM>;
-    return k_attn<3, PRO_NORM>;
-  }
-  if (nb == 4) {
-    if (pro == PRO_EMBED_NORM) return k_attn<4, PRO_EMBED_NORM>;
-    if (pro == PRO_ARGMAX_EMBED_NORM) return k_attn<4, PRO_ARGMAX_EMBED_NORM>;
-    return k_attn<4, PRO_NORM>;
-  }
-  return nullptr;
+  size_t lds = (P.prologue != PRO_QUANT) ? (size_t)P.n_x_lds * sizeof(float) : 0;
+  hipLaunchKernelGGL(k, dim3(total_wg), dim3(256), lds, c->stream, P);
 }
 
 GemvParams base_params(c2h_ctx* c) {
   GemvParams P;
   memset(&P, 0, sizeof(P));
   P.eps = c->desc.rms_eps;
+  P.emb = c->embd.ref();
+  P.n_vocab = c->desc.n_vocab;
+  P.part_v = c->part_v;
+  P.part_i = c->part_i;
+  P.n_part = c->n_part;
+  P.token_ids = c->token_ids;
+  P.max_ctx = c->desc.max_ctx;
+  P.state = c->state_dev;
   return P;
 }
 
@@ -325,32 +325,27 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
   const int E = D.n_embd;
   for (int l = 0; l < D.n_layers; ++l) {
     Layer& L = c->layers[l];
-    {  // attention block: [embed] RMSNorm, q|k|v rows per head, RoPE, KV store, attention
-      AttnFusedParams A;
+    {  // q|k|v = W * Q8_K(RMSNorm(X)) + bias; layer 0 embeds the token first
+      GemvParams P = base_params(c);
+      P.prologue = (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM;
+      P.n_x = E;
+      P.n_x_lds = chain_lds_floats(E);
+      P.x = c->X;
+      P.x_out = c->X;
+      P.norm_w = L.attn_norm;
+      P.nb_in = nb_k(E);
+      int task = 0;
+      add_job(P, &task, L.wq, nullptr, MODE_BIAS, c->q, L.bq, nullptr);
+      add_job(P, &task, L.wk, nullptr, MODE_BIAS, c->k, L.bk, nullptr);
+      add_job(P, &task, L.wv, nullptr, MODE_BIAS, c->v, L.bv, nullptr);
+      launch_gemv_row(c, P, task);
+    }
+    {  // attention: RoPE, KV store, scores, softmax, AV; one workgroup per query head
+      AttnCoreParams A;
       memset(&A, 0, sizeof(A));
-      const int pro = (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM;
-      A.n_embd = E;
-      A.n_x_lds = chain_lds_floats(E);
-      A.eps = D.rms_eps;
-      A.x = c->X;
-      A.x_out = c->X;
-      A.norm_w = L.attn_norm;
-      A.emb = c->embd.ref();
-      A.n_vocab = D.n_vocab;
-      A.part_v = c->part_v;
-      A.part_i = c->part_i;
-      A.n_part = c->n_part;
-      A.token_ids = c->token_ids;
-      A.wq = L.wq.ref();
-      A.wk = L.wk.ref();
-      A.wv = L.wv.ref();
-      A.tq = L.wq.type;
-      A.tk = L.wk.type;
-      A.tv = L.wv.type;
-      A.bq = L.bq ? L.bq : c->zero_bias;
-      A.bk = L.bk ? L.bk : c->zero_bias;
-      A.bv = L.bv ? L.bv : c->zero_bias;
-      A.bias_mask = (L.bq ? 1 : 0) | (L.bk ? 2 : 0) | (L.bv ? 4 : 0);
+      A.q = c->q;
+      A.k = c->k;
+      A.v = c->v;
       A.out = c->attn;
       A.kv = c->kv;
       A.rope_cos = c->rope_cos;
@@ -363,7 +358,7 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
       A.max_ctx = D.max_ctx;
       A.scale = (float)(1.0 / std::sqrt((double)D.head_dim));
       A.state = c->state_dev;
-      hipLaunchKernelGGL(attn_kernel(nb_k(E), pro), dim3(D.n_heads), dim3(256), c->attn_lds, c->stream, A);
+      hipLaunchKernelGGL(k_attn_core, dim3(D.n_heads), dim3(256), c->attn_lds, c->stream, A);
     }
     {  // attn_out: X += Wo * Q8_K(attn)
       GemvParams P = base_params(c);
@@ -372,7 +367,7 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
       P.nb_in = nb_k(E);
       int task = 0;
       add_job(P, &task, L.wo, nullptr, MODE_RESID, c->X, nullptr, nullptr);
-      launch_gemv_row(c, P);
+      launch_gemv_row(c, P, task);
     }
     {  // ffn_in: h = SwiGLU(Wg * n, Wu * n), n = Q8_K(RMSNorm(X))
       GemvParams P = base_params(c);
@@ -384,7 +379,7 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
       P.nb_in = nb_k(E);
       int task = 0;
       add_job(P, &task, L.wg, &L.wu, MODE_SWIGLU, c->h, nullptr, nullptr);
-      launch_gemv_row(c, P);
+      launch_gemv_row(c, P, task);
     }
     {  // ffn_out: X += Wd * Q8_K(h)
       GemvParams P = base_params(c);
@@ -393,7 +388,7 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
       P.nb_in = nb_k(D.n_ff);
       int task = 0;
       add_job(P, &task, L.wd, nullptr, MODE_RESID, c->X, nullptr, nullptr);
-      launch_gemv_row(c, P);
+      launch_gemv_row(c, P, task);
     }
   }
   NormParams N;
@@ -543,7 +538,7 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
     return bail(fail(c, C2H_ERR_UNSUPPORTED, "K-quant projections need n_embd and n_ff of at least 256"));
   if (D.n_embd % 32 || D.n_embd > 1024 || D.n_ff % 4 || D.n_ff > 16384)
     return bail(fail(c, C2H_ERR_UNSUPPORTED, "n_embd must be a multiple of 32 up to 1024, n_ff up to 16384"));
-  if (!attn_kernel(nb_k(D.n_embd), PRO_NORM) || !gemv_row_kernel(nb_k(D.n_embd), PRO_QUANT, MODE_RESID) ||
+  if (!gemv_row_kernel(nb_k(D.n_embd), PRO_NORM, MODE_BIAS) || !gemv_row_kernel(nb_k(D.n_embd), PRO_QUANT, MODE_RESID) ||
       !gemv_row_kernel(nb_k(D.n_embd), PRO_NORM, MODE_SWIGLU) ||
       !gemv_row_kernel(nb_k(D.n_ff), PRO_QUANT, MODE_RESID))
     return bail(fail(c, C2H_ERR_UNSUPPORTED,
@@ -555,10 +550,8 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   const int E = D.n_embd, KV = D.n_kv_heads * D.head_dim, F = D.n_ff;
   if ((rc = dalloc(c, &c->X, E * 4)) || (rc = dalloc(c, &c->q, E * 4)) || (rc = dalloc(c, &c->k, KV * 4)) ||
       (rc = dalloc(c, &c->v, KV * 4)) || (rc = dalloc(c, &c->attn, E * 4)) || (rc = dalloc(c, &c->h, F * 4)) ||
-      (rc = dalloc(c, &c->normx[0], E * 4)) || (rc = dalloc(c, &c->normx[1], E * 4)) ||
-      (rc = dalloc(c, &c->zero_bias, E * 4)))
+      (rc = dalloc(c, &c->normx[0], E * 4)) || (rc = dalloc(c, &c->normx[1], E * 4)))
     return bail(rc);
-  if (hipMemset(c->zero_bias, 0, E * 4) != hipSuccess) return bail(fail(c, C2H_ERR_HIP, "memset"));
   size_t kv_bytes = (size_t)2 * D.n_layers * D.n_kv_heads * D.max_ctx * D.head_dim * 4;
   if ((rc = dalloc(c, &c->kv, kv_bytes))) return bail(rc);
   if (hipMemset(c->kv, 0, kv_bytes) != hipSuccess) return bail(fail(c, C2H_ERR_HIP, "hipMemset kv"));
@@ -587,16 +580,14 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   if ((rc = dalloc(c, &c->part_v, (size_t)c->n_part * 4)) || (rc = dalloc(c, &c->part_i, (size_t)c->n_part * 4)) ||
       (rc = dalloc(c, &c->logits, (size_t)D.n_vocab * 4)))
     return bail(rc);
-  // attention-block LDS within the 160 KB of a gfx950 workgroup (8 KB kept
-  // for the kernel's static shared data): staged V | GEMV terms | Q6_K
-  // scales | x*x | all scores of the context
-  c->attn_lds = (size_t)attn_lds_floats(nb_k(E), chain_lds_floats(E), D.max_ctx) * 4;
+  // attention LDS within the 160 KB of a gfx950 workgroup (8 KB kept for
+  // the kernel's static shared data): staged V | all scores of the context
+  c->attn_lds = (size_t)attn_lds_floats(D.max_ctx) * 4;
   if (c->attn_lds > 152u * 1024)
     return bail(fail(c, C2H_ERR_UNSUPPORTED, "max_ctx %d too large for the exact attention kernel", D.max_ctx));
-  for (int pro : {PRO_NORM, PRO_EMBED_NORM, PRO_ARGMAX_EMBED_NORM})
-    if (hipFuncSetAttribute((const void*)attn_kernel(nb_k(E), pro), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)c->attn_lds) != hipSuccess)
-      return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
+  if (hipFuncSetAttribute((const void*)k_attn_core, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->attn_lds) !=
+      hipSuccess)
+    return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
   C2hState s0;
   memset(&s0, 0, sizeof(s0));
   s0.penalty = 1.15f;

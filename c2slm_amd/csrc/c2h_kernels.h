@@ -86,12 +86,23 @@ constexpr int MAX_JOBS = 4;
 struct GemvParams {
   int prologue;
   int nb_in;
-  int n_x;      // length of x for the norm prologue
+  int n_x;      // length of x for the norm prologues
   int n_x_lds;  // LDS floats of the x*x buffer (see chain_lds_floats)
   float eps;
   const float* x;
   const float* norm_w;
   const uint8_t* q8k_in;
+  // layer-0 prologues: embed state->token or the argmax of the vocab
+  // candidates, publish it (x_out, state->token, token_ids[pos])
+  WeightRef emb;
+  int n_vocab;
+  const float* part_v;
+  const int* part_i;
+  int n_part;
+  float* x_out;
+  int32_t* token_ids;
+  int max_ctx;
+  C2hState* state;
   int n_jobs;
   GemvJob jobs[MAX_JOBS];
 };
@@ -112,29 +123,15 @@ struct NormParams {
   C2hState* state;
 };
 
-// The attention block of one layer in one launch, one workgroup per query
-// head: [embed] + RMSNorm + Q8_K, the head's 64 q rows and its KV head's
-// 64 k and 64 v rows (+ bias), RoPE, KV store, attention.
+// Attention of one layer, one workgroup per query head, over the q|k|v the
+// QKV GEMV wrote: RoPE, KV store, scores, softmax, AV.
 constexpr int ATT_CH = 128;   // V positions staged in LDS per pass (chunk 0 prefetched)
 constexpr int ATT_KPF = 256;  // positions whose K row is prefetched (one per thread)
-struct AttnFusedParams {
-  int n_embd;
-  int n_x_lds;
-  float eps;
-  const float* x;
-  float* x_out;
-  const float* norm_w;
-  WeightRef emb;
-  int n_vocab;
-  const float* part_v;
-  const int* part_i;
-  int n_part;
-  int32_t* token_ids;
-  WeightRef wq, wk, wv;
-  int tq, tk, tv;
-  const float *bq, *bk, *bv;  // never null: a zero buffer stands in for an absent bias
-  int bias_mask;              // bit 0/1/2: q/k/v bias present (tensor/ops.go:221-225 adds only those)
-  float* out;  // attention output [n_heads*64]
+struct AttnCoreParams {
+  const float* q;  // [n_heads*64], bias added, before RoPE
+  const float* k;  // [n_kv_heads*64]
+  const float* v;
+  float* out;      // attention output [n_heads*64]
   float* kv;
   const float* rope_cos;
   const float* rope_sin;
@@ -148,11 +145,8 @@ struct AttnFusedParams {
   C2hState* state;
 };
 
-// Dynamic LDS of the attention kernel, in floats: staged V | GEMV terms |
-// Q6_K block scales | x*x chain buffer | scores.
-__host__ __device__ inline int attn_lds_floats(int nb, int n_x_lds, int max_ctx) {
-  return ATT_CH * 64 + 3 * 64 * 4 * nb + 3 * 64 * nb + n_x_lds + chain_lds_floats(max_ctx);
-}
+// Dynamic LDS of the attention kernel, in floats: staged V | scores.
+__host__ __device__ inline int attn_lds_floats(int max_ctx) { return ATT_CH * 64 + chain_lds_floats(max_ctx); }
 
 constexpr int VOCAB_TILES = 1;  // 32-row tiles per vocab workgroup
 
@@ -176,8 +170,7 @@ __global__ void k_gemv_q8k(GemvParams P);
 template <int NB, int PRO, int MODE>
 __global__ void k_gemv_row(GemvParams P);
 __global__ void k_rmsnorm(NormParams P);
-template <int NB, int PRO>
-__global__ void k_attn(AttnFusedParams P);
+__global__ void k_attn_core(AttnCoreParams P);
 __global__ void k_vocab(VocabParams P);
 __global__ void k_argmax_final(const float* pv, const int* pi, int n, C2hState* state);
 __global__ void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16);

@@ -589,45 +589,68 @@ __global__ void __launch_bounds__(256) k_gemv_row(GemvParams P) {
   constexpr int RPW = 256 / IPR;
   constexpr int BPW = (NB + 3) / 4;  // Q8_K blocks quantised per wave
   constexpr bool PAIRED = (MODE == MODE_SWIGLU);
-  static_assert(PRO != PRO_NORM || NB <= 4, "the norm prologue holds one float4 per thread");
+  constexpr bool NORM = (PRO == PRO_NORM || PRO == PRO_EMBED_NORM || PRO == PRO_ARGMAX_EMBED_NORM);
+  static_assert(!NORM || NB <= 4, "the norm prologue holds one float4 per thread");
   extern __shared__ __align__(16) unsigned char smem[];
-  float* sq = reinterpret_cast<float*>(smem);  // [n_x_lds] (PRO_NORM only)
+  float* sq = reinterpret_cast<float*>(smem);  // [n_x_lds] (norm prologues only)
   __shared__ Q8KRow<NB> s;
   __shared__ __align__(16) float terms[PAIRED ? 2 : 1][RPW * IPR];
   __shared__ float inv_slot;
+  __shared__ ArgCand ared[4];
 
-  const GemvJob& J = P.jobs[0];
+  // the job of this workgroup (uniform)
+  int ji = 0;
+#pragma unroll
+  for (int j = 1; j < MAX_JOBS; ++j)
+    if (j < P.n_jobs && (int)blockIdx.x >= P.jobs[j].wg_begin) ji = j;
+  const GemvJob& J = P.jobs[ji];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int b = tid / (4 * RPW);
   const int r_local = (tid - b * 4 * RPW) >> 2;
   const int u = tid & 3;
-  const int row0 = (int)blockIdx.x * RPW;
+  const int row0 = ((int)blockIdx.x - J.wg_begin) * RPW;
   const int row = row0 + r_local;
   const bool active = (b < NB) && (row < J.rows);
   const int row_c = min(row, J.rows - 1);
   const int b_c = min(b, NB - 1);
+  const int out_row = min(row0 + min(tid, RPW - 1), J.rows - 1);  // epilogue row of thread tid < RPW
 
   // ---- loads, in the order they are consumed
   float4 xa[BPW];
   float4 nw = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  int tok = 0;
   if (PRO == PRO_NORM) {
     xa[0] = load4(P.x, P.n_x);
-    nw = load4(P.norm_w, P.n_x);
+  } else if (NORM) {  // layer 0: the token's embedding row
+    tok = (PRO == PRO_ARGMAX_EMBED_NORM) ? reduce_argmax_partials(P.part_v, P.part_i, P.n_part, ared)
+                                         : P.state->token;
+    xa[0] = embed4(P.emb, P.n_vocab, P.n_x, tok);
   } else {
 #pragma unroll
     for (int i = 0; i < BPW; ++i)
       xa[i] = reinterpret_cast<const float4*>(P.x + min(wave + 4 * i, NB - 1) * QK_K)[lane];
   }
+  if (NORM) nw = load4(P.norm_w, P.n_x);
   const ItemW w1 = load_item(J.w, J.type, NB, row_c, b_c, u);
   ItemW w2;
   if (PAIRED) w2 = load_item(J.w2, J.type2, NB, row_c, b_c, u);
   float yres = 0.0f;
-  if (MODE == MODE_RESID) yres = J.y[min(row0 + min(tid, RPW - 1), J.rows - 1)];
+  if (MODE == MODE_RESID) yres = J.y[out_row];
+  // an absent bias reads x instead (a valid address) and is not added
+  if (MODE == MODE_BIAS) yres = (J.bias ? J.bias : P.x)[J.bias ? out_row : 0];
   issue_fence();
 
   // ---- prologue: the Q8_K input row in LDS
-  if (PRO == PRO_NORM) {
+  if (NORM) {
+    if (PRO != PRO_NORM && blockIdx.x == 0) {  // layer 0 publishes the embedded token
+      if (4 * tid < P.n_x) reinterpret_cast<float4*>(P.x_out)[tid] = xa[0];
+      if (tid == 0) {
+        const int pos = P.state->pos;
+        P.state->token = tok;
+        if (pos >= 0 && pos < P.max_ctx) P.token_ids[pos] = tok;
+      }
+    }
     const float inv = rms_inv4(xa[0], P.n_x, P.eps, sq, &inv_slot);
     const float4 xn[1] = {norm4(xa[0], inv, nw)};  // wave w holds block w
     if (wave < NB) quantize_wave(xn[0], wave, s);
@@ -652,6 +675,8 @@ __global__ void __launch_bounds__(256) k_gemv_row(GemvParams P) {
         const float up = fold_terms<NB>(J.type2, &terms[PAIRED ? 1 : 0][tid * IPR]);
         const int n8 = J.rows - (J.rows % 8);
         J.y[r] = (r < n8) ? swiglu_poly(acc, up) : swiglu_tail(acc, up);
+      } else if (MODE == MODE_BIAS) {
+        J.y[r] = J.bias ? acc + yres : acc;
       } else {
         J.y[r] = yres + acc;
       }
@@ -666,6 +691,12 @@ C2H_GEMV_ROW(12, PRO_QUANT, MODE_RESID)
 C2H_GEMV_ROW(19, PRO_QUANT, MODE_RESID)
 C2H_GEMV_ROW(3, PRO_NORM, MODE_SWIGLU)
 C2H_GEMV_ROW(4, PRO_NORM, MODE_SWIGLU)
+C2H_GEMV_ROW(3, PRO_NORM, MODE_BIAS)
+C2H_GEMV_ROW(4, PRO_NORM, MODE_BIAS)
+C2H_GEMV_ROW(3, PRO_EMBED_NORM, MODE_BIAS)
+C2H_GEMV_ROW(4, PRO_EMBED_NORM, MODE_BIAS)
+C2H_GEMV_ROW(3, PRO_ARGMAX_EMBED_NORM, MODE_BIAS)
+C2H_GEMV_ROW(4, PRO_ARGMAX_EMBED_NORM, MODE_BIAS)
 #undef C2H_GEMV_ROW
 
 // ------------------------------------------- GEMV on an external Q8_K row
@@ -767,42 +798,30 @@ __device__ __forceinline__ float attn_score(const float* q_s, const float4 (&kk4
   return sco * scale;
 }
 
-// One query head h per workgroup (engine/forward.go:66-106 for that head):
-//   [embed] RMSNorm -> Q8_K, q rows [64h, 64h+64), k and v rows of KV head
-//   g = h/qpkv (+ bias, tensor/ops.go:221-225), RoPE (tensor/ops.go:262-286)
-//   on q_h and k_g, KV store (engine/kvcache.go:143-157) by the group's
-//   first head, then attention (engine/forward.go:143-155 with
-//   internal/simd/c2_tensor_attn_gen.go and tensor.Softmax): scores in the
-//   two-accumulator FMA order, softmax with f64 exp and a sequential f32 sum,
-//   one FMA chain over positions per output dim with V staged through LDS.
-// Heads of one group recompute their shared k/v rows (64+64 rows of NB
-// super-blocks), which costs less than a launch and a global round trip.
-// K rows of positions < ATT_KPF and V rows of positions < ATT_CH are
-// prefetched into registers at entry; longer contexts load the rest in
-// place.
-template <int NB, int PRO>
-__global__ void __launch_bounds__(256) k_attn(AttnFusedParams P) {
-  static_assert(NB <= 4, "the norm prologue holds one float4 per thread");
+// Attention of one query head h per workgroup (engine/forward.go:94-106 and
+// :143-168 for that head) over the q|k|v rows the QKV GEMV wrote:
+//   RoPE (tensor/ops.go:262-286) on q_h and k_g (g = h/qpkv), KV store
+//   (engine/kvcache.go:143-157) by the group's first head, then scores in
+//   the two-accumulator FMA order (internal/simd/c2_tensor_attn_gen.go:9-66),
+//   softmax with f64 exp and a sequential f32 sum (tensor/ops.go:317-339),
+//   and one FMA chain over positions per output dim
+//   (c2_tensor_attn_gen.go:85-117) with V staged through LDS.
+// Every load (q/k/v, RoPE row, the K row of position tid, the V rows of the
+// first ATT_CH positions) is issued at entry.
+__global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   constexpr int HD = 64;
-  constexpr int IPR = 4 * NB;
-  constexpr int IPM = HD * IPR;  // items per matrix (= 256*NB)
   constexpr int VPT = ATT_CH * HD / 4 / 256;  // staged float4 of V per thread
   extern __shared__ __align__(16) unsigned char smem[];
   float* vbuf = reinterpret_cast<float*>(smem);  // [ATT_CH][64]
-  float* terms = vbuf + ATT_CH * HD;             // [3][64][IPR]
-  float* sq = terms + 3 * IPM + 3 * HD * NB;     // [n_x_lds]
-  float* sc = sq + P.n_x_lds;                    // [chain_lds_floats(max_ctx)]
-  __shared__ Q8KRow<NB> s;
+  float* sc = vbuf + ATT_CH * HD;                // [chain_lds_floats(max_ctx)]
   __shared__ __align__(16) float qkv_s[3][HD];
   __shared__ float red_m[4];
   __shared__ float inv_slot;
-  __shared__ ArgCand ared[4];
 
   const int tid = threadIdx.x;
   const int h = blockIdx.x;
   const int qpkv = P.n_heads / P.n_kv_heads;
   const int g = h / qpkv;
-  const int E = P.n_embd;
   const int pos = P.state->pos;
   const int T = pos + 1;
   const size_t head_stride = (size_t)P.max_ctx * HD;
@@ -811,70 +830,13 @@ __global__ void __launch_bounds__(256) k_attn(AttnFusedParams P) {
   const int plast = max(min(pos, P.max_ctx) - 1, 0);  // last stored position (clamp target)
 
   // ---- loads, in the order they are consumed
-  // x: elements 4t..4t+3; items: thread t owns row t/4, quarter t%4 of
-  // every block j of the three matrices (block-major: a 16-lane LDS access
-  // group reads one block of the Q8_K row)
-  float4 xr;
-  int tok = 0;
-  if (PRO == PRO_NORM) {
-    xr = load4(P.x, E);
-  } else {
-    tok = (PRO == PRO_ARGMAX_EMBED_NORM) ? reduce_argmax_partials(P.part_v, P.part_i, P.n_part, ared)
-                                         : P.state->token;
-    xr = embed4(P.emb, P.n_vocab, E, tok);
-  }
-  const float4 nw = load4(P.norm_w, E);
-  const WeightRef* W[3] = {&P.wq, &P.wk, &P.wv};
-  const int T3[3] = {P.tq, P.tk, P.tv};
-  const int rbase[3] = {h * HD, g * HD, g * HD};
-  const int ir = tid >> 2, iu = tid & 3;
-  ItemW w[3][NB];
-#pragma unroll
-  for (int m = 0; m < 3; ++m) {
-#pragma unroll
-    for (int j = 0; j < NB; ++j) w[m][j] = load_item(*W[m], T3[m], NB, rbase[m] + ir, j, iu);
-  }
-  // bias of row tid%64 of matrix tid/64 (threads < 192 use it).  The host
-  // passes a valid buffer for absent biases and says in bias_mask which
-  // exist: one unconditional load, since a load under a divergent branch
-  // would force a wait for every load issued before it.
+  // thread t < 192 holds element t%64 of q_h (t < 64), k_g, v_g
   const int bm = min(tid >> 6, 2);
-  const float* bptr = (bm == 0) ? P.bq : (bm == 1 ? P.bk : P.bv);
-  const float bval = bptr[((bm == 0) ? h * HD : g * HD) + (tid & 63)];
-  const bool has_bias = (P.bias_mask >> bm) & 1;
+  const float* src = (bm == 0) ? P.q + h * HD : ((bm == 1) ? P.k : P.v) + g * HD;
+  const float own = src[tid & 63];
   const int rp = min(max(pos, 0), P.rope_len - 1);
   const float rcos = P.rope_cos[(size_t)rp * (HD / 2) + (tid & 31)];
   const float rsin = P.rope_sin[(size_t)rp * (HD / 2) + (tid & 31)];
-
-  issue_fence();
-
-  // ---- prologue: layer 0 publishes the embedded token
-  if (PRO != PRO_NORM && blockIdx.x == 0) {
-    if (4 * tid < E) reinterpret_cast<float4*>(P.x_out)[tid] = xr;
-    if (tid == 0) {
-      P.state->token = tok;
-      if (pos >= 0 && pos < P.max_ctx) P.token_ids[pos] = tok;
-    }
-  }
-  {
-    const float inv = rms_inv4(xr, E, P.eps, sq, &inv_slot);
-    const int wave = tid >> 6;
-    if (wave < NB) quantize_wave(norm4(xr, inv, nw), wave, s);  // wave w holds block w
-    __syncthreads();
-  }
-
-  // ---- items -> terms [m][r][4nb]
-#pragma unroll
-  for (int m = 0; m < 3; ++m) {
-#pragma unroll
-    for (int j = 0; j < NB; ++j)
-      store_item(terms + m * IPM + ir * IPR, T3[m], j, iu, item_value(w[m][j], T3[m], s, j, iu));
-  }
-  __syncthreads();
-
-  // K row of position tid and the V rows of chunk 0, issued once the weight
-  // registers are free (holding them from entry would spill); they arrive
-  // while the fold, RoPE and KV store run
   float4 kreg[16];
   {
     const float4* kr = reinterpret_cast<const float4*>(kcache + (size_t)min(tid, plast) * HD);
@@ -887,15 +849,9 @@ __global__ void __launch_bounds__(256) k_attn(AttnFusedParams P) {
     const int f = tid + 256 * i;  // float4 index within the chunk
     vreg[i] = reinterpret_cast<const f32x4_t*>(vcache + (size_t)min(f >> 4, plast) * HD)[f & 15];
   }
+  issue_fence();
 
-  // ---- fold + bias: thread t < 192 owns row t%64 of matrix t/64
-  if (tid < 3 * HD) {
-    const int m = tid / HD, r = tid - m * HD;
-    const int tm = (m == 0) ? P.tq : (m == 1 ? P.tk : P.tv);  // no dynamic index into a local array
-    float acc = fold_terms<NB>(tm, terms + m * IPM + r * IPR);
-    if (has_bias) acc = acc + bval;
-    qkv_s[m][r] = acc;
-  }
+  if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;
   __syncthreads();
 
   float* q_s = qkv_s[0];
@@ -1003,14 +959,6 @@ __global__ void __launch_bounds__(256) k_attn(AttnFusedParams P) {
   }
 }
 
-#define C2H_ATTN(NB_, PRO_) template __global__ void k_attn<NB_, PRO_>(AttnFusedParams);
-C2H_ATTN(3, PRO_NORM)
-C2H_ATTN(3, PRO_EMBED_NORM)
-C2H_ATTN(3, PRO_ARGMAX_EMBED_NORM)
-C2H_ATTN(4, PRO_NORM)
-C2H_ATTN(4, PRO_EMBED_NORM)
-C2H_ATTN(4, PRO_ARGMAX_EMBED_NORM)
-#undef C2H_ATTN
 
 // ------------------------------------------------------------------ vocab
 
