@@ -11,9 +11,25 @@
  * GOAMD64=v1 Go build; fmaf() appears only where the reference calls
  * archsimd MulAdd).
  *
- * Each function names the reference file:line it restates.  What pins each
- * function (golden vectors, closed forms, brute force, the reference's own C
- * dequant oracles) is listed in oracle/README.md.
+ * Each function names the reference file:line it restates.  What pins it
+ * (tests/test_oracle.py):
+ *   fp16 decode        exhaustive 65,536 values vs IEEE; tensor/ops_test.go cases
+ *   Q8_K quantiser     known-answer fixture (c2_tensor_dot_q4_k_q8_k_test.go:92-94),
+ *                      invariants, floor/zero-block, Go NaN conversion
+ *   Q4_K/Q6_K sums     the reference's own C dequant oracles (oracle/_ref),
+ *                      brute force over unpacked nibbles
+ *   Q6_K dot           golden values c2_tensor_gemv2_q6_k_q8_k_test.go:55-56
+ *   Q4_K/Q8_0 fold     float64 dequant, order known answers, unit vectors
+ *   RMSNorm/RoPE/      reference cases, float64, invariants
+ *   Softmax
+ *   attention          textbook float64 attention, FMA-order known answers
+ *   SwiGLU             c2_tensor_swiglu_test.go:34 precision, extremes
+ *   penalty/argmax     brute force, ties, NaN at id 0
+ * Parity unpinned (needs the Go toolchain, absent here): the last ulp of Go's
+ * float64 math.Exp / Pow / Cos / Sin (glibc is used; after the f32 rounding
+ * they differ only in rare double-rounding cases), archsimd ConvertToInt32 in
+ * SwiGLU (truncation assumed; the reference pins it to 1e-4), and the
+ * reference's own end-to-end stream.
  */
 #include <math.h>
 #include <stdint.h>
