@@ -61,6 +61,7 @@ def lib():
             "c2h_upload_tensor": (C.c_int, [VP, I32, I32, I32, I64, I64, VP, C.c_size_t]),
             "c2h_set_token_ids": (C.c_int, [VP, I32, VP, I32]),
             "c2h_forward": (C.c_int, [VP, I32, I32, VP]),
+            "c2h_prefill": (C.c_int, [VP, VP, I32, I32, VP]),
             "c2h_logits": (C.c_int, [VP, VP]),
             "c2h_step": (C.c_int, [VP, I32, C.c_float, I32, I32, C.POINTER(I32)]),
             "c2h_restore_normx": (C.c_int, [VP]),
@@ -134,6 +135,13 @@ class Ctx:
     def forward(self, token: int, pos: int, want_normx: bool = True):
         out = np.empty(self.desc.n_embd, np.float32) if want_normx else None
         self._chk(lib().c2h_forward(self.h, token, pos, _p(out) if want_normx else None))
+        return out
+
+    def prefill(self, tokens, pos0: int, want_normx: bool = True):
+        """Engine.IngestFrom's Forward loop for all tokens at once (batched)."""
+        toks = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32))
+        out = np.empty(self.desc.n_embd, np.float32) if want_normx else None
+        self._chk(lib().c2h_prefill(self.h, _p(toks), len(toks), pos0, _p(out) if want_normx else None))
         return out
 
     def logits(self) -> np.ndarray:

@@ -2,8 +2,10 @@
 // repack, HIP-graph capture of the decode step, and the entry points.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
+#include <initializer_list>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -67,6 +69,18 @@ struct c2h_ctx {
   bool graphs_ready = false;
   bool use_graphs = true;
   size_t attn_lds = 0;
+
+  // batched prefill buffers (allocated by the first c2h_prefill)
+  struct {
+    bool ready = false;
+    float *X = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
+    float *g = nullptr, *u = nullptr, *h = nullptr;
+    int8_t* q8 = nullptr;
+    float* q8d = nullptr;
+    int32_t* q8bs = nullptr;
+    int32_t* tok = nullptr;
+    int nbs = 0;
+  } pf;
 
   // kernel-only scratch (c2h_gemv / c2h_quantize_q8k host forms)
   std::vector<void*> scratch;
@@ -347,6 +361,7 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
       A.k = c->k;
       A.v = c->v;
       A.out = c->attn;
+      A.store_kv = 1;
       A.kv = c->kv;
       A.rope_cos = c->rope_cos;
       A.rope_sin = c->rope_sin;
@@ -691,6 +706,224 @@ int c2h_forward(c2h_ctx* c, int32_t token, int32_t pos, float* normx_out) {
                              c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
   }
+  return C2H_OK;
+}
+
+namespace {
+
+int pf_alloc(c2h_ctx* c) {
+  if (c->pf.ready) return C2H_OK;
+  const c2h_model_desc& D = c->desc;
+  const size_t E = D.n_embd, KV = (size_t)D.n_kv_heads * D.head_dim, F = D.n_ff, M = PF_MAX;
+  auto& p = c->pf;
+  p.nbs = std::max(nb_k(D.n_embd), nb_k(D.n_ff));
+  int rc;
+  if ((rc = dalloc(c, &p.X, M * E * 4)) || (rc = dalloc(c, &p.q, M * E * 4)) || (rc = dalloc(c, &p.k, M * KV * 4)) ||
+      (rc = dalloc(c, &p.v, M * KV * 4)) || (rc = dalloc(c, &p.attn, M * E * 4)) ||
+      (rc = dalloc(c, &p.g, M * F * 4)) || (rc = dalloc(c, &p.u, M * F * 4)) || (rc = dalloc(c, &p.h, M * F * 4)) ||
+      (rc = dalloc(c, &p.q8, M * p.nbs * QK_K)) || (rc = dalloc(c, &p.q8d, M * p.nbs * 4)) ||
+      (rc = dalloc(c, &p.q8bs, M * p.nbs * 16 * 4)) || (rc = dalloc(c, &p.tok, M * 4)))
+    return rc;
+  p.ready = true;
+  return C2H_OK;
+}
+
+typedef void (*PFGemmKernel)(PFGemmParams);
+PFGemmKernel pf_gemm_kernel(int type, int mode) {
+  if (type == C2H_Q4_K) return mode == MODE_RESID ? k_pf_gemm<T_Q4_K, MODE_RESID> : k_pf_gemm<T_Q4_K, MODE_BIAS>;
+  return mode == MODE_RESID ? k_pf_gemm<T_Q6_K, MODE_RESID> : k_pf_gemm<T_Q6_K, MODE_BIAS>;
+}
+
+// y[t][r] (=|+=) W * q8[t] for the given matrices: one launch per weight
+// type, the matrices of one type as jobs of that launch.
+void pf_gemm(c2h_ctx* c, int m, int m_pad, int nb, int mode, std::initializer_list<const Tensor*> ws,
+             std::initializer_list<float*> ys, std::initializer_list<const float*> biases,
+             std::initializer_list<int> ldys) {
+  std::vector<const Tensor*> W(ws);
+  std::vector<float*> Y(ys);
+  std::vector<const float*> B(biases);
+  std::vector<int> L(ldys);
+  for (int type : {(int)C2H_Q4_K, (int)C2H_Q6_K}) {
+    PFGemmParams P;
+    memset(&P, 0, sizeof(P));
+    P.in = PFQ8{c->pf.q8, c->pf.q8d, c->pf.q8bs, c->pf.nbs};
+    P.nb = nb;
+    P.m = m;
+    int tiles = 0;
+    for (size_t i = 0; i < W.size(); ++i) {
+      if (W[i]->type != type) continue;
+      PFJob& J = P.jobs[P.n_jobs++];
+      J.w = W[i]->ref();
+      J.type = type;
+      J.rows = (int)W[i]->rows;
+      J.tile_begin = tiles;
+      tiles += (J.rows + PF_TILE - 1) / PF_TILE;
+      J.mode = mode;
+      J.y = Y[i];
+      J.ldy = L[i];
+      J.bias = B[i];
+    }
+    if (P.n_jobs == 0) continue;
+    hipLaunchKernelGGL(pf_gemm_kernel(type, mode), dim3(tiles, m_pad / PF_TILE), dim3(256), 0, c->stream, P);
+  }
+}
+
+typedef void (*PFNormKernel)(PFNormParams);
+typedef void (*PFQuantKernel)(PFQuantParams);
+PFNormKernel pf_norm_kernel(int nb) { return nb == 3 ? k_pf_norm_quant<3> : k_pf_norm_quant<4>; }
+PFQuantKernel pf_quant_kernel(int nb) {
+  switch (nb) {
+    case 3: return k_pf_quant<3>;
+    case 4: return k_pf_quant<4>;
+    case 12: return k_pf_quant<12>;
+    default: return k_pf_quant<19>;
+  }
+}
+
+// One pass of up to PF_MAX tokens at positions pos0.. (engine.Forward per
+// token, batched layer by layer).
+int pf_pass(c2h_ctx* c, const int32_t* tokens, int m, int pos0) {
+  const c2h_model_desc& D = c->desc;
+  const int E = D.n_embd, KV = D.n_kv_heads * D.head_dim, F = D.n_ff;
+  const int m_pad = (m + PF_TILE - 1) / PF_TILE * PF_TILE;
+  auto& p = c->pf;
+  int rc;
+  HIPCHK(c, hipMemcpyAsync(p.tok, tokens, (size_t)m * 4, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, hipMemcpyAsync(c->token_ids + pos0, p.tok, (size_t)m * 4, hipMemcpyDeviceToDevice, c->stream));
+  C2hState s;
+  memset(&s, 0, sizeof(s));
+  s.pos = pos0;
+  s.penalty = 1.15f;
+  s.nx_in = c->nx_cur;
+  s.nx_out = c->nx_cur ^ 1;
+  if ((rc = push_state(c, s))) return rc;
+  const PFQ8 q8{p.q8, p.q8d, p.q8bs, p.nbs};
+  const size_t norm_lds = (size_t)chain_lds_floats(E) * 4;
+  for (int l = 0; l < D.n_layers; ++l) {
+    Layer& L = c->layers[l];
+    {  // [embed] RMSNorm -> Q8_K
+      PFNormParams N;
+      memset(&N, 0, sizeof(N));
+      N.embed = (l == 0);
+      N.n_x = E;
+      N.eps = D.rms_eps;
+      N.X = p.X;
+      N.norm_w = L.attn_norm;
+      N.tokens = p.tok;
+      N.emb = c->embd.ref();
+      N.n_vocab = D.n_vocab;
+      N.m = m;
+      N.nb = nb_k(E);
+      N.out = q8;
+      hipLaunchKernelGGL(pf_norm_kernel(nb_k(E)), dim3(m_pad), dim3(256), norm_lds, c->stream, N);
+    }
+    pf_gemm(c, m, m_pad, nb_k(E), MODE_BIAS, {&L.wq, &L.wk, &L.wv}, {p.q, p.k, p.v}, {L.bq, L.bk, L.bv},
+            {E, KV, KV});
+    {
+      PFRopeParams R;
+      memset(&R, 0, sizeof(R));
+      R.k = p.k;
+      R.v = p.v;
+      R.ld = KV;
+      R.kv = c->kv;
+      R.rope_cos = c->rope_cos;
+      R.rope_sin = c->rope_sin;
+      R.rope_len = D.max_ctx;
+      R.pos0 = pos0;
+      R.m = m;
+      R.layer = l;
+      R.n_layers = D.n_layers;
+      R.n_kv_heads = D.n_kv_heads;
+      R.max_ctx = D.max_ctx;
+      hipLaunchKernelGGL(k_pf_rope_store, dim3(m, D.n_kv_heads), dim3(64), 0, c->stream, R);
+    }
+    {
+      AttnCoreParams A;
+      memset(&A, 0, sizeof(A));
+      A.q = p.q;
+      A.k = p.k;
+      A.v = p.v;
+      A.out = p.attn;
+      A.q_ld = E;
+      A.kv_ld = KV;
+      A.out_ld = E;
+      A.store_kv = 0;
+      A.kv = c->kv;
+      A.rope_cos = c->rope_cos;
+      A.rope_sin = c->rope_sin;
+      A.rope_len = D.max_ctx;
+      A.layer = l;
+      A.n_layers = D.n_layers;
+      A.n_heads = D.n_heads;
+      A.n_kv_heads = D.n_kv_heads;
+      A.max_ctx = D.max_ctx;
+      A.scale = (float)(1.0 / std::sqrt((double)D.head_dim));
+      A.state = c->state_dev;
+      const size_t lds = (size_t)attn_lds_floats(pos0 + m) * 4;
+      hipLaunchKernelGGL(k_attn_core, dim3(D.n_heads, m), dim3(256), lds, c->stream, A);
+    }
+    {
+      PFQuantParams Q{p.attn, E, m, q8};
+      hipLaunchKernelGGL(pf_quant_kernel(nb_k(E)), dim3(m_pad), dim3(256), 0, c->stream, Q);
+    }
+    pf_gemm(c, m, m_pad, nb_k(E), MODE_RESID, {&L.wo}, {p.X}, {nullptr}, {E});
+    {
+      PFNormParams N;
+      memset(&N, 0, sizeof(N));
+      N.n_x = E;
+      N.eps = D.rms_eps;
+      N.X = p.X;
+      N.norm_w = L.ffn_norm;
+      N.m = m;
+      N.nb = nb_k(E);
+      N.out = q8;
+      hipLaunchKernelGGL(pf_norm_kernel(nb_k(E)), dim3(m_pad), dim3(256), norm_lds, c->stream, N);
+    }
+    pf_gemm(c, m, m_pad, nb_k(E), MODE_BIAS, {&L.wg, &L.wu}, {p.g, p.u}, {nullptr, nullptr}, {F, F});
+    hipLaunchKernelGGL(k_pf_swiglu, dim3((F + 255) / 256, m), dim3(256), 0, c->stream, p.g, p.u, p.h, F, m);
+    {
+      PFQuantParams Q{p.h, F, m, q8};
+      hipLaunchKernelGGL(pf_quant_kernel(nb_k(F)), dim3(m_pad), dim3(256), 0, c->stream, Q);
+    }
+    pf_gemm(c, m, m_pad, nb_k(F), MODE_RESID, {&L.wd}, {p.X}, {nullptr}, {E});
+  }
+  // normX of the last token (engine/forward.go:135)
+  NormParams N;
+  memset(&N, 0, sizeof(N));
+  N.x = p.X + (size_t)(m - 1) * E;
+  N.w = c->output_norm;
+  N.eps = D.rms_eps;
+  N.n = E;
+  N.out = c->normx[c->nx_cur ^ 1];
+  N.n_lds = chain_lds_floats(E);
+  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), (size_t)N.n_lds * sizeof(float), c->stream, N);
+  HIPCHK(c, hipGetLastError());
+  c->nx_prev = c->nx_cur;
+  c->nx_cur ^= 1;
+  return C2H_OK;
+}
+
+}  // namespace
+
+int c2h_prefill(c2h_ctx* c, const int32_t* tokens, int32_t n, int32_t pos0, float* normx_out) {
+  if (!c || (!tokens && n > 0) || n < 0) return C2H_ERR_INVALID;
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = validate_model(c);
+  if (rc) return rc;
+  if (pos0 < 0 || (int64_t)pos0 + n > c->desc.max_ctx)
+    return fail(c, C2H_ERR_RANGE, "positions [%d, %d) outside [0, %d)", pos0, pos0 + n, c->desc.max_ctx);
+  if (n == 0) return C2H_OK;
+  if ((rc = pf_alloc(c))) return rc;
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  c->ring_next = 0;
+  for (int done = 0; done < n;) {
+    const int m = std::min(n - done, PF_MAX);
+    if ((rc = pf_pass(c, tokens + done, m, pos0 + done))) return rc;
+    HIPCHK(c, hipStreamSynchronize(c->stream));  // tokens are copied from the caller's buffer
+    done += m;
+  }
+  if (normx_out)
+    HIPCHK(c, hipMemcpy(normx_out, c->normx[c->nx_cur], (size_t)c->desc.n_embd * 4, hipMemcpyDeviceToHost));
   return C2H_OK;
 }
 

@@ -127,11 +127,15 @@ struct NormParams {
 // QKV GEMV wrote: RoPE, KV store, scores, softmax, AV.
 constexpr int ATT_CH = 128;   // V positions staged in LDS per pass (chunk 0 prefetched)
 constexpr int ATT_KPF = 256;  // positions whose K row is prefetched (one per thread)
+// grid (n_heads, tokens): query token i of a batch sits at position
+// state->pos + i; decode launches one token.
 struct AttnCoreParams {
-  const float* q;  // [n_heads*64], bias added, before RoPE
-  const float* k;  // [n_kv_heads*64]
+  const float* q;  // [tokens][q_ld]: n_heads*64, bias added, before RoPE
+  const float* k;  // [tokens][kv_ld]: n_kv_heads*64
   const float* v;
-  float* out;      // attention output [n_heads*64]
+  float* out;      // attention output [tokens][out_ld]
+  int q_ld, kv_ld, out_ld;
+  int store_kv;    // 1: the first head of each group stores K/V at pos
   float* kv;
   const float* rope_cos;
   const float* rope_sin;
@@ -147,6 +151,76 @@ struct AttnCoreParams {
 
 // Dynamic LDS of the attention kernel, in floats: staged V | scores.
 __host__ __device__ inline int attn_lds_floats(int max_ctx) { return ATT_CH * 64 + chain_lds_floats(max_ctx); }
+
+// ---- batched prefill (a prompt of up to PF_MAX tokens per pass)
+
+constexpr int PF_TILE = 64;   // rows and tokens of one prefill GEMM workgroup
+constexpr int PF_MAX = 512;   // tokens per prefill pass (buffers are sized for it)
+
+// Q8_K rows of a token batch in global memory: token t, block b at
+// q[(t*nbs + b)*256], d[t*nbs + b], bs[(t*nbs + b)*16] (bsums as int32).
+struct PFQ8 {
+  int8_t* q;
+  float* d;
+  int32_t* bs;
+  int nbs;  // block stride per token
+};
+
+// Per token: [embed tokens[t] into X[t]] RMSNorm(X[t]) * w -> Q8_K.
+struct PFNormParams {
+  int embed;
+  int n_x;
+  float eps;
+  float* X;  // [m_pad][n_x]
+  const float* norm_w;
+  const int32_t* tokens;
+  WeightRef emb;
+  int n_vocab;
+  int m;
+  int nb;  // floor(n_x/256) blocks quantised
+  PFQ8 out;
+};
+
+// Per token: Q8_K of x[t][0 .. nb*256).
+struct PFQuantParams {
+  const float* x;
+  int ld;
+  int m;
+  PFQ8 out;
+};
+
+struct PFJob {
+  WeightRef w, w2;
+  int type, type2;
+  int rows;
+  int tile_begin;  // first row tile (blockIdx.x) of this job
+  int mode;
+  float* y;  // [m_pad][ldy]
+  int ldy;
+  const float* bias;
+};
+
+struct PFGemmParams {
+  PFQ8 in;
+  int nb;  // super-blocks per row
+  int m;   // valid tokens
+  int n_jobs;
+  PFJob jobs[3];
+};
+
+// Per token and KV head: RoPE(k), then K/V stored at pos0 + t.
+struct PFRopeParams {
+  const float* k;
+  const float* v;
+  int ld;
+  float* kv;
+  const float* rope_cos;
+  const float* rope_sin;
+  int rope_len;
+  int pos0;
+  int m;
+  int layer, n_layers, n_kv_heads, max_ctx;
+};
 
 constexpr int VOCAB_TILES = 1;  // 32-row tiles per vocab workgroup
 
@@ -171,6 +245,14 @@ template <int NB, int PRO, int MODE>
 __global__ void k_gemv_row(GemvParams P);
 __global__ void k_rmsnorm(NormParams P);
 __global__ void k_attn_core(AttnCoreParams P);
+template <int NB>
+__global__ void k_pf_norm_quant(PFNormParams P);
+template <int NB>
+__global__ void k_pf_quant(PFQuantParams P);
+template <int TYPE, int MODE>
+__global__ void k_pf_gemm(PFGemmParams P);
+__global__ void k_pf_rope_store(PFRopeParams P);
+__global__ void k_pf_swiglu(const float* gate, const float* up, float* h, int n, int m);
 __global__ void k_vocab(VocabParams P);
 __global__ void k_argmax_final(const float* pv, const int* pi, int n, C2hState* state);
 __global__ void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16);

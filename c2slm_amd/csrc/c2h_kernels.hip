@@ -820,9 +820,10 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
 
   const int tid = threadIdx.x;
   const int h = blockIdx.x;
+  const int ti = blockIdx.y;  // query token of the batch (0 in decode)
   const int qpkv = P.n_heads / P.n_kv_heads;
   const int g = h / qpkv;
-  const int pos = P.state->pos;
+  const int pos = P.state->pos + ti;
   const int T = pos + 1;
   const size_t head_stride = (size_t)P.max_ctx * HD;
   float* kcache = P.kv + ((size_t)P.layer * P.n_kv_heads + g) * head_stride;
@@ -832,7 +833,8 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   // ---- loads, in the order they are consumed
   // thread t < 192 holds element t%64 of q_h (t < 64), k_g, v_g
   const int bm = min(tid >> 6, 2);
-  const float* src = (bm == 0) ? P.q + h * HD : ((bm == 1) ? P.k : P.v) + g * HD;
+  const float* src = (bm == 0) ? P.q + (size_t)ti * P.q_ld + h * HD
+                               : ((bm == 1) ? P.k : P.v) + (size_t)ti * P.kv_ld + g * HD;
   const float own = src[tid & 63];
   const int rp = min(max(pos, 0), P.rope_len - 1);
   const float rcos = P.rope_cos[(size_t)rp * (HD / 2) + (tid & 31)];
@@ -868,7 +870,8 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   }
   __syncthreads();
 
-  if ((h % qpkv) == 0 && tid < HD && pos < P.max_ctx) {
+  // (a batch of query tokens has its K/V stored by a kernel before this one)
+  if (P.store_kv && (h % qpkv) == 0 && tid < HD && pos < P.max_ctx) {
     kcache[(size_t)pos * HD + tid] = k_s[tid];
     vcache[(size_t)pos * HD + tid] = v_s[tid];
   }
@@ -955,10 +958,337 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   }
   if (tid < HD) {
     acc = __builtin_fmaf(sc[pos], v_s[d], acc);
-    P.out[h * HD + d] = acc;
+    P.out[(size_t)ti * P.out_ld + h * HD + d] = acc;
   }
 }
 
+
+// ------------------------------------------------------- prefill (A17)
+//
+// A prompt of m tokens through one layer at a time, each token's arithmetic
+// identical to engine.Forward's (so KV and normX equal sequential ingest bit
+// for bit; c2slm.go:107-115 runs Forward per token):
+//   k_pf_norm_quant   [embed] RMSNorm -> Q8_K per token
+//   k_pf_gemm         int8 MFMA GEMM (tokens x rows) whose per-sub-block int32
+//                     sums feed the reference's per-row float fold in order
+//   k_pf_rope_store   RoPE(k), K/V stored at their positions
+//   k_attn_core       causal attention per (head, token)
+//   k_pf_quant        Q8_K of the attention / SwiGLU rows
+//   k_pf_swiglu       h = SwiGLU(gate, up)
+
+// One token's Q8_K row (LDS form) into the batch buffer.
+template <int NB>
+__device__ __forceinline__ void store_q8_row(const Q8KRow<NB>& s, const PFQ8& o, int t) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < NB * 64; i += 256) {
+    const int b = i >> 6, w = i & 63;
+    reinterpret_cast<uint32_t*>(o.q + ((size_t)t * o.nbs + b) * QK_K)[w] = s.q[b][w];
+  }
+  for (int i = tid; i < NB * 16; i += 256) o.bs[((size_t)t * o.nbs + (i >> 4)) * 16 + (i & 15)] = s.bs[i >> 4][i & 15];
+  if (tid < NB) o.d[(size_t)t * o.nbs + tid] = s.d[tid];
+}
+
+// Token blockIdx.x (rows past m repeat token m-1; their results are dropped).
+template <int NB>
+__global__ void __launch_bounds__(256) k_pf_norm_quant(PFNormParams P) {
+  static_assert(NB <= 4, "one float4 per thread");
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* sq = reinterpret_cast<float*>(smem);  // [chain_lds_floats(n_x)]
+  __shared__ Q8KRow<NB> s;
+  __shared__ float inv_slot;
+  const int tid = threadIdx.x;
+  const int t = blockIdx.x;
+  const int tc = min(t, P.m - 1);
+  const float4 x = P.embed ? embed4(P.emb, P.n_vocab, P.n_x, P.tokens[tc]) : load4(P.X + (size_t)tc * P.n_x, P.n_x);
+  const float4 w = load4(P.norm_w, P.n_x);
+  issue_fence();
+  if (P.embed && 4 * tid < P.n_x) reinterpret_cast<float4*>(P.X + (size_t)t * P.n_x)[tid] = x;
+  const float inv = rms_inv4(x, P.n_x, P.eps, sq, &inv_slot);
+  const int wave = tid >> 6;
+  if (wave < NB) quantize_wave(norm4(x, inv, w), wave, s);
+  __syncthreads();
+  store_q8_row<NB>(s, P.out, t);
+}
+
+template <int NB>
+__global__ void __launch_bounds__(256) k_pf_quant(PFQuantParams P) {
+  constexpr int BPW = (NB + 3) / 4;
+  __shared__ Q8KRow<NB> s;
+  const int t = blockIdx.x;
+  const int tc = min(t, P.m - 1);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float4 xa[BPW];
+#pragma unroll
+  for (int i = 0; i < BPW; ++i)
+    xa[i] = reinterpret_cast<const float4*>(P.x + (size_t)tc * P.ld + min(wave + 4 * i, NB - 1) * QK_K)[lane];
+  quantize_row_waves<NB>(xa, s);
+  store_q8_row<NB>(s, P.out, t);
+}
+
+// RoPE of token t's k (tensor/ops.go:262-286, same expressions as the
+// attention kernel) and the K/V store at pos0 + t (engine/kvcache.go:143-157).
+__global__ void __launch_bounds__(64) k_pf_rope_store(PFRopeParams P) {
+  const int t = blockIdx.x, g = blockIdx.y, d = threadIdx.x;
+  const int pos = P.pos0 + t;
+  if (t >= P.m || pos >= P.max_ctx) return;
+  const float* kr = P.k + (size_t)t * P.ld + g * 64;
+  const float* vr = P.v + (size_t)t * P.ld + g * 64;
+  float kv = kr[d];
+  if (pos < P.rope_len) {
+    const int i = d & 31;
+    const float c = P.rope_cos[(size_t)pos * 32 + i], sn = P.rope_sin[(size_t)pos * 32 + i];
+    const float x0 = kr[i], x1 = kr[i + 32];
+    kv = (d < 32) ? (x0 * c) - (x1 * sn) : (x0 * sn) + (x1 * c);
+  }
+  const size_t head_stride = (size_t)P.max_ctx * 64;
+  P.kv[((size_t)P.layer * P.n_kv_heads + g) * head_stride + (size_t)pos * 64 + d] = kv;
+  P.kv[(((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * head_stride + (size_t)pos * 64 + d] = vr[d];
+}
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// One super-block of one weight row as the MFMA A operand needs it: lane
+// (r = lane%16, k-group lk = lane/16) holds 8 consecutive quants of every
+// 32-element chunk: Q4_K qs[32p + 8lk .. +8) (low nibbles: chunk 2p, high:
+// 2p+1); Q6_K ql/qh bytes of quarter (n, k).  Plus the row's scale header.
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+struct PFA {
+  u32x2_t a[16];  // Q4_K: a[p] = qs bytes of pair p; Q6_K: a[c] = ql, a[8 + c] = qh of chunk c = 4n + k
+  u32x4_t hdr;    // Q4_K: d | dmin | scales[12]; Q6_K: scales[16]
+  uint32_t d6;    // Q6_K fp16 d
+};
+
+template <int TYPE>
+__device__ __forceinline__ PFA pf_load_a(const WeightRef& W, int nb, int row, int b, int lk) {
+  PFA A;
+  const size_t blk = (size_t)row * nb + b;
+  if (TYPE == T_Q4_K) {
+    const uint8_t* base = W.q + blk * BS_Q4K;
+    A.hdr = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(base));
+#pragma unroll
+    for (int p = 0; p < 4; ++p) A.a[p] = *reinterpret_cast<const u32x2_t*>(base + 16 + 32 * p + 8 * lk);
+#pragma unroll
+    for (int p = 4; p < 16; ++p) A.a[p] = A.a[0];
+    A.d6 = 0;
+  } else {
+    const uint8_t* base = W.q + blk * BS_Q6K_PACKED;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int n = c >> 2, k = c & 3;
+      A.a[c] = *reinterpret_cast<const u32x2_t*>(base + 64 * n + 32 * (k & 1) + 8 * lk);
+      A.a[8 + c] = *reinterpret_cast<const u32x2_t*>(base + 128 + 32 * n + 8 * lk);
+    }
+    A.hdr = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(base + 192));
+    A.d6 = W.d[blk];
+  }
+  return A;
+}
+
+__device__ __forceinline__ long as_long(u32x2_t v) { return (long)((uint64_t)v.x | ((uint64_t)v.y << 32)); }
+
+// Row parameters a row's lanes publish for the lanes that fold its outputs:
+// Q4_K d, dmin, sc[8], m[8] (c2_tensor_dot_q4_k_q8_k_gen.go:38-61);
+// Q6_K d, sc[16] (int8).
+constexpr int PF_RP = 20;
+template <int TYPE>
+__device__ __forceinline__ void pf_row_params(const PFA& A, int32_t* rp) {
+  if (TYPE == T_Q4_K) {
+    rp[0] = __float_as_int(fp16_simd_nb(A.hdr.x & 0xffffu));
+    rp[1] = __float_as_int(fp16_simd_nb(A.hdr.x >> 16));
+    const uint4 h = make_uint4(A.hdr.x, A.hdr.y, A.hdr.z, A.hdr.w);
+    auto s = [&](int i) { return (int)byte_of(h, 4 + i); };
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      rp[2 + j] = s(j) & 63;
+      rp[10 + j] = s(j + 4) & 63;
+      rp[2 + 4 + j] = (s(j + 8) & 15) | ((s(j) >> 6) << 4);
+      rp[10 + 4 + j] = (s(j + 8) >> 4) | ((s(j + 4) >> 6) << 4);
+    }
+  } else {
+    rp[0] = __float_as_int(fp16_simd_nb(A.d6));
+    const uint4 h = make_uint4(A.hdr.x, A.hdr.y, A.hdr.z, A.hdr.w);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) rp[1 + j] = (int)(int8_t)byte_of(h, j);
+  }
+}
+
+// tokens x rows GEMM of one prefill projection: workgroup tile = 64 rows x
+// 64 tokens; wave w owns rows [16w, 16w+16) against all 64 tokens (four
+// 16x16 MFMA tiles).  Per super-block the token tile's Q8_K block is staged
+// in LDS and the next block's weights are loaded while this one runs.
+//   Q4_K: per pair p two v_mfma_i32_16x16x32_i8 (low nibbles x q8[64p..+32),
+//   high nibbles x q8[64p+32..+32)) give s_lo, s_hi; the lane then adds the
+//   pair term of c2_tensor_dot_q4_k_q8_k_gen.go:85 for its 4 rows x 1 token.
+//   Q6_K: per 32-element quarter c two MFMAs (q8 masked to each 16-element
+//   half) give the sub-block sums; isum += (s - 32*bsum)*sc (exact int), and
+//   per super-block acc += f32(isum)*(d*q8d)
+//   (c2_tensor_gemv2_q6_k_q8_k_gen.go:168-209).
+template <int TYPE, int MODE>
+__global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
+  __shared__ __align__(16) uint32_t sq[PF_TILE][68];  // Q8_K quants of the token tile (4-dword pad per row)
+  __shared__ float sd[PF_TILE];
+  __shared__ int32_t sbs[PF_TILE][17];
+  __shared__ int32_t rp[4][16][PF_RP];
+
+  int ji = 0;
+#pragma unroll
+  for (int j = 1; j < 3; ++j)
+    if (j < P.n_jobs && (int)blockIdx.x >= P.jobs[j].tile_begin) ji = j;
+  const PFJob& J = P.jobs[ji];
+  const int row0 = ((int)blockIdx.x - J.tile_begin) * PF_TILE;
+  const int t0 = (int)blockIdx.y * PF_TILE;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lr = lane & 15, lk = lane >> 4;
+  const int arow = min(row0 + 16 * wave + lr, J.rows - 1);  // the A-operand row of this lane
+  const int nb = P.nb;
+
+  float acc[4][4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[tt][v] = 0.0f;
+
+  PFA cur = pf_load_a<TYPE>(J.w, nb, arow, 0, lk);
+  for (int b = 0; b < nb; ++b) {
+    // the token tile's block b: 16 dwords of quants, the scale and 4 bsums per thread
+    u32x4_t qv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int f = tid + 256 * i, t = f >> 4, w4 = f & 15;
+      qv[i] = reinterpret_cast<const u32x4_t*>(P.in.q + ((size_t)(t0 + t) * P.in.nbs + b) * QK_K)[w4];
+    }
+    const float dv = P.in.d[(size_t)(t0 + (tid & 63)) * P.in.nbs + b];
+    int32_t bsv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int f = tid + 256 * i;
+      bsv[i] = P.in.bs[((size_t)(t0 + (f >> 4)) * P.in.nbs + b) * 16 + (f & 15)];
+    }
+    const PFA nxt = pf_load_a<TYPE>(J.w, nb, arow, min(b + 1, nb - 1), lk);
+    __syncthreads();  // the previous block is consumed
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int f = tid + 256 * i, t = f >> 4, w4 = f & 15;
+      *reinterpret_cast<u32x4_t*>(&sq[t][4 * w4]) = qv[i];
+      sbs[t][f & 15] = bsv[i];
+    }
+    if (tid < PF_TILE) sd[tid] = dv;
+    if (lk == 0) pf_row_params<TYPE>(cur, rp[wave][lr]);
+    __syncthreads();
+
+    if (TYPE == T_Q4_K) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const u32x2_t qs = cur.a[p];
+        const long a_lo = as_long(qs & 0x0f0f0f0fu);
+        const long a_hi = as_long((qs >> 4) & 0x0f0f0f0fu);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          const int t = tt * 16 + lr;
+          const long b_lo = as_long(*reinterpret_cast<const u32x2_t*>(&sq[t][16 * p + 2 * lk]));
+          const long b_hi = as_long(*reinterpret_cast<const u32x2_t*>(&sq[t][16 * p + 8 + 2 * lk]));
+          const i32x4_t zero = {0, 0, 0, 0};
+          const i32x4_t slo = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, b_lo, zero, 0, 0, 0);
+          const i32x4_t shi = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, b_hi, zero, 0, 0, 0);
+          const float q8d = sd[t];
+          const float bA = (float)(sbs[t][4 * p] + sbs[t][4 * p + 1]);
+          const float bB = (float)(sbs[t][4 * p + 2] + sbs[t][4 * p + 3]);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int32_t* r = rp[wave][4 * lk + v];
+            const float dW = __int_as_float(r[0]) * q8d;
+            const float mW = __int_as_float(r[1]) * q8d;
+            const float sc0 = (float)r[2 + 2 * p], sc1 = (float)r[3 + 2 * p];
+            const float m0 = (float)r[10 + 2 * p], m1 = (float)r[11 + 2 * p];
+            const float term = (((float)slo[v] * (dW * sc0)) - (bA * (mW * m0))) +
+                               (((float)shi[v] * (dW * sc1)) - (bB * (mW * m1)));
+            acc[tt][v] = acc[tt][v] + term;
+          }
+        }
+      }
+    } else {
+      int32_t isum[4][4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) isum[tt][v] = 0;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const int k = c & 3;
+        const u32x2_t ql = cur.a[c], qh = cur.a[8 + c];
+        const u32x2_t lo = (k < 2) ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
+        const long a = as_long(lo | (((qh >> (2 * k)) & 0x03030303u) << 4));
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          const int t = tt * 16 + lr;
+          const long bq = as_long(*reinterpret_cast<const u32x2_t*>(&sq[t][8 * c + 2 * lk]));
+          const long b0 = (lk < 2) ? bq : 0l;  // sub-block 2c: elements 0..15 of the chunk
+          const long b1 = (lk < 2) ? 0l : bq;  // sub-block 2c+1: elements 16..31
+          const i32x4_t zero = {0, 0, 0, 0};
+          const i32x4_t s0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b0, zero, 0, 0, 0);
+          const i32x4_t s1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, zero, 0, 0, 0);
+          const int32_t bs0 = sbs[t][2 * c], bs1 = sbs[t][2 * c + 1];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int32_t* r = rp[wave][4 * lk + v];
+            isum[tt][v] += (s0[v] - 32 * bs0) * r[1 + 2 * c] + (s1[v] - 32 * bs1) * r[2 + 2 * c];
+          }
+        }
+      }
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const float q8d = sd[tt * 16 + lr];
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          acc[tt][v] = acc[tt][v] + (float)isum[tt][v] * (__int_as_float(rp[wave][4 * lk + v][0]) * q8d);
+      }
+    }
+    cur = nxt;
+  }
+
+  // ---- epilogue: lane holds rows 16w + 4lk + v, tokens 16tt + lr
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const int t = t0 + tt * 16 + lr;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int r = row0 + 16 * wave + 4 * lk + v;
+      if (t < P.m && r < J.rows) {
+        float* y = J.y + (size_t)t * J.ldy + r;
+        if (MODE == MODE_RESID)
+          *y = *y + acc[tt][v];
+        else
+          *y = J.bias ? acc[tt][v] + J.bias[r] : acc[tt][v];
+      }
+    }
+  }
+}
+
+// h = SwiGLU(gate, up) elementwise (c2_tensor_swiglu_gen.go; the tail of
+// n % 8 elements per row takes the scalar f64 path).
+__global__ void __launch_bounds__(256) k_pf_swiglu(const float* gate, const float* up, float* h, int n, int m) {
+  const int t = blockIdx.y;
+  const int n8 = n - (n % 8);
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+    if (t >= m) break;
+    const size_t o = (size_t)t * n + i;
+    h[o] = (i < n8) ? swiglu_poly(gate[o], up[o]) : swiglu_tail(gate[o], up[o]);
+  }
+}
+
+#define C2H_PF(NB_)                                                 \
+  template __global__ void k_pf_norm_quant<NB_>(PFNormParams);      \
+  template __global__ void k_pf_quant<NB_>(PFQuantParams);
+C2H_PF(3)
+C2H_PF(4)
+#undef C2H_PF
+template __global__ void k_pf_quant<12>(PFQuantParams);
+template __global__ void k_pf_quant<19>(PFQuantParams);
+template __global__ void k_pf_gemm<T_Q4_K, MODE_BIAS>(PFGemmParams);
+template __global__ void k_pf_gemm<T_Q4_K, MODE_RESID>(PFGemmParams);
+template __global__ void k_pf_gemm<T_Q6_K, MODE_BIAS>(PFGemmParams);
+template __global__ void k_pf_gemm<T_Q6_K, MODE_RESID>(PFGemmParams);
 
 // ------------------------------------------------------------------ vocab
 

@@ -109,6 +109,15 @@ int c2h_set_token_ids(c2h_ctx* ctx, int32_t pos0, const int32_t* ids, int32_t n)
  * skips RoPE and the KV store silently there, engine/kvcache.go:144-146). */
 int c2h_forward(c2h_ctx* ctx, int32_t token, int32_t pos, float* normx_out);
 
+/* Engine.IngestFrom's loop (c2slm.go:107-115: engine.Forward per token at
+ * pos0, pos0+1, ...; TokenIDs recorded) for n tokens at once: each layer runs
+ * over the whole batch (int8 MFMA GEMMs, causal attention), with every
+ * token's arithmetic identical to Forward's, so the KV cache and the final
+ * normX (written to normx_out, nullable) equal sequential ingest bit for
+ * bit.  Batches of up to 512 tokens per pass.  [pos0, pos0+n) must lie in
+ * [0, max_ctx) (C2H_ERR_RANGE otherwise). */
+int c2h_prefill(c2h_ctx* ctx, const int32_t* tokens, int32_t n, int32_t pos0, float* normx_out);
+
 /* engine.ComputeLogits(m, a, normX, out, nil) (engine/forward.go:171-191) on
  * the current normX: n_vocab fp32 logits to logits_out. */
 int c2h_logits(c2h_ctx* ctx, float* logits_out);

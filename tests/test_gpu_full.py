@@ -35,3 +35,35 @@ def test_full_model_greedy_64_steps(full_model_path):
     assert np.max(np.abs(lg - want_lg)) <= 1e-3 * np.max(np.abs(want_lg))
     ctx.close()
     orc.close()
+
+
+def test_full_model_prefill_512_then_128_steps(full_model_path):
+    # batched prefill of a 512-token prompt (int8 MFMA GEMMs), then 128 greedy
+    # steps: KV, normX and the stream equal the oracle's sequential ingest
+    gf = G.GGUFFile(full_model_path)
+    _, im_end, eos = G.special_token_ids(gf)
+    ctx = H.Ctx(H.desc_from_gguf(gf, max_ctx=1024))
+    H.load_gguf_into(ctx, gf)
+    orc = O.OracleEngine(gf, max_ctx=1024, n_threads=16)
+    rng = np.random.default_rng(4)
+    prompt = rng.integers(0, 151936, 512).astype(np.int32)
+    got_nx = ctx.prefill(prompt, 0)
+    want_nx = orc.ingest_from(0, prompt)
+    assert np.array_equal(bits(got_nx), bits(want_nx))
+    kv = orc.kv()
+    for which in (0, 1):
+        for layer in (0, 11, 23):
+            for h in (0, 1):
+                assert np.array_equal(bits(ctx.kv(which, layer, h, 512)), bits(kv[which, layer, h, :512]))
+    got = []
+    pos = 512
+    for _ in range(128):
+        t = ctx.step(pos, 1.15, im_end, eos)
+        got.append(t)
+        pos += 1
+        if t in (im_end, eos):
+            break
+    want = orc.generate(128, im_end, eos, 1.15)
+    assert np.array_equal(np.array(got, np.int32), want)
+    ctx.close()
+    orc.close()
