@@ -67,6 +67,10 @@ def lib():
             "c2h_restore_normx": (C.c_int, [VP]),
             "c2h_get_normx": (C.c_int, [VP, VP]),
             "c2h_get_kv": (C.c_int, [VP, I32, I32, I32, I32, VP]),
+            "c2h_set_kv": (C.c_int, [VP, I32, I32, I32, I32, I32, VP]),
+            "c2h_set_seq": (C.c_int, [VP, I32]),
+            "c2h_get_token_ids": (C.c_int, [VP, I32, I32, VP]),
+            "c2h_get_seq": (C.c_int, [VP, C.POINTER(I32)]),
             "c2h_quantize_q8k": (C.c_int, [VP, VP, I32, VP]),
             "c2h_gemv": (C.c_int, [VP, I32, VP, VP, I32, I32, VP, VP]),
             "c2h_packed_size": (C.c_size_t, [I32, I64, I64]),
@@ -166,6 +170,24 @@ class Ctx:
         out = np.empty((n, self.desc.head_dim), np.float32)
         self._chk(lib().c2h_get_kv(self.h, which, layer, kv_head, n, _p(out)))
         return out
+
+    def set_kv(self, which: int, layer: int, kv_head: int, pos0: int, data: np.ndarray):
+        a = np.ascontiguousarray(data, dtype=np.float32).reshape(-1, self.desc.head_dim)
+        self._chk(lib().c2h_set_kv(self.h, which, layer, kv_head, pos0, a.shape[0], _p(a)))
+
+    def token_ids(self, pos0: int, n: int) -> np.ndarray:
+        out = np.empty(n, np.int32)
+        self._chk(lib().c2h_get_token_ids(self.h, pos0, n, _p(out)))
+        return out
+
+    @property
+    def seq_len(self) -> int:
+        n = I32()
+        self._chk(lib().c2h_get_seq(self.h, C.byref(n)))
+        return n.value
+
+    def set_seq(self, n: int):
+        self._chk(lib().c2h_set_seq(self.h, n))
 
     def time_vocab(self, iters: int, pos: int, in_step: bool = True) -> float:
         ms = C.c_float()

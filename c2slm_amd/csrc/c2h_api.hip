@@ -21,6 +21,7 @@ using namespace c2h;
 namespace {
 
 constexpr int kStateRing = 256;
+constexpr int PF_ATT_SUB = 16;  // batch tokens per long-context attention launch
 
 struct Tensor {
   uint8_t* q = nullptr;
@@ -65,10 +66,17 @@ struct c2h_ctx {
   int32_t* tok_host = nullptr;     // pinned
   unsigned ring_next = 0;
 
-  hipGraphExec_t g_step = nullptr, g_fwd = nullptr;
+  // graphs [0] attend with k_attn_core, [1] with the long-context kernels
+  hipGraphExec_t g_step[2] = {nullptr, nullptr}, g_fwd[2] = {nullptr, nullptr};
   bool graphs_ready = false;
   bool use_graphs = true;
   size_t attn_lds = 0;
+  int att_split = 0;     // positions attended up to which k_attn_core runs
+  bool long_attn = false;
+  float* att_sc = nullptr;  // [PF_ATT_SUB][n_heads][sc_ld] scores / probabilities
+  float* att_bmax = nullptr;
+  int att_sc_ld = 0, att_n_blk = 0;
+  int32_t seq_len = 0;   // KVCache.SeqLen (engine/kvcache.go:25-47)
 
   // batched prefill buffers (allocated by the first c2h_prefill)
   struct {
@@ -332,9 +340,43 @@ void enqueue_vocab(c2h_ctx* c, int apply_penalty, float* logits_out, int x_sel, 
   hipLaunchKernelGGL(k_vocab, dim3(c->n_part), dim3(256), lds, c->stream, V);
 }
 
+AttnCoreParams attn_params(c2h_ctx* c, int layer) {
+  const c2h_model_desc& D = c->desc;
+  AttnCoreParams A;
+  memset(&A, 0, sizeof(A));
+  A.kv = c->kv;
+  A.rope_cos = c->rope_cos;
+  A.rope_sin = c->rope_sin;
+  A.rope_len = D.max_ctx;
+  A.layer = layer;
+  A.n_layers = D.n_layers;
+  A.n_heads = D.n_heads;
+  A.n_kv_heads = D.n_kv_heads;
+  A.max_ctx = D.max_ctx;
+  A.scale = (float)(1.0 / std::sqrt((double)D.head_dim));
+  A.state = c->state_dev;
+  A.sc = c->att_sc;
+  A.bmax = c->att_bmax;
+  A.sc_ld = c->att_sc_ld;
+  A.n_blk = c->att_n_blk;
+  return A;
+}
+
+// Long-context attention of `ntok` query tokens (rows tok0..): scores over
+// every block of the context, softmax, AV.  Blocks past a token's context
+// return at once, so the grid covers max_ctx and graphs replay at any pos.
+void enqueue_attn_long(c2h_ctx* c, const AttnCoreParams& A, int ntok) {
+  const c2h_model_desc& D = c->desc;
+  hipLaunchKernelGGL(k_attn_scores, dim3(c->att_n_blk, D.n_kv_heads, ntok), dim3(256), 0, c->stream, A);
+  hipLaunchKernelGGL(k_attn_softmax, dim3(D.n_heads, ntok), dim3(1024),
+                     (size_t)attn_softmax_lds_floats(D.max_ctx) * 4, c->stream, A);
+  hipLaunchKernelGGL(k_attn_av, dim3(D.n_heads, ntok), dim3(1024), (size_t)ATT_AV_LDS_FLOATS * 4, c->stream, A);
+}
+
 // The 24-layer body of engine.Forward plus the final RMSNorm; layer 0 embeds
 // either state->token (forward) or the argmax of the vocab partials (step).
-void enqueue_layers(c2h_ctx* c, bool from_argmax) {
+// long_attn selects the long-context attention kernels.
+void enqueue_layers(c2h_ctx* c, bool from_argmax, bool long_attn) {
   const c2h_model_desc& D = c->desc;
   const int E = D.n_embd;
   for (int l = 0; l < D.n_layers; ++l) {
@@ -354,26 +396,17 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
       add_job(P, &task, L.wv, nullptr, MODE_BIAS, c->v, L.bv, nullptr);
       launch_gemv_row(c, P, task);
     }
-    {  // attention: RoPE, KV store, scores, softmax, AV; one workgroup per query head
-      AttnCoreParams A;
-      memset(&A, 0, sizeof(A));
+    {  // attention: RoPE, KV store, scores, softmax, AV
+      AttnCoreParams A = attn_params(c, l);
       A.q = c->q;
       A.k = c->k;
       A.v = c->v;
       A.out = c->attn;
       A.store_kv = 1;
-      A.kv = c->kv;
-      A.rope_cos = c->rope_cos;
-      A.rope_sin = c->rope_sin;
-      A.rope_len = D.max_ctx;
-      A.layer = l;
-      A.n_layers = D.n_layers;
-      A.n_heads = D.n_heads;
-      A.n_kv_heads = D.n_kv_heads;
-      A.max_ctx = D.max_ctx;
-      A.scale = (float)(1.0 / std::sqrt((double)D.head_dim));
-      A.state = c->state_dev;
-      hipLaunchKernelGGL(k_attn_core, dim3(D.n_heads), dim3(256), c->attn_lds, c->stream, A);
+      if (long_attn)
+        enqueue_attn_long(c, A, 1);
+      else
+        hipLaunchKernelGGL(k_attn_core, dim3(D.n_heads), dim3(256), c->attn_lds, c->stream, A);
     }
     {  // attn_out: X += Wo * Q8_K(attn)
       GemvParams P = base_params(c);
@@ -420,9 +453,9 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax) {
   hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), (size_t)N.n_lds * sizeof(float), c->stream, N);
 }
 
-void enqueue_step(c2h_ctx* c) {
+void enqueue_step(c2h_ctx* c, bool long_attn) {
   enqueue_vocab(c, 1, nullptr, 1, nullptr);
-  enqueue_layers(c, true);
+  enqueue_layers(c, true, long_attn);
 }
 
 int validate_model(c2h_ctx* c) {
@@ -447,26 +480,34 @@ int validate_model(c2h_ctx* c) {
   return C2H_OK;
 }
 
+void destroy_graphs(c2h_ctx* c) {
+  for (int t = 0; t < 2; ++t) {
+    if (c->g_step[t]) (void)hipGraphExecDestroy(c->g_step[t]);
+    if (c->g_fwd[t]) (void)hipGraphExecDestroy(c->g_fwd[t]);
+    c->g_step[t] = c->g_fwd[t] = nullptr;
+  }
+}
+
 int build_graphs(c2h_ctx* c) {
   if (c->graphs_ready) return C2H_OK;
   int rc = validate_model(c);
   if (rc) return rc;
-  if (c->g_step) (void)hipGraphExecDestroy(c->g_step);
-  if (c->g_fwd) (void)hipGraphExecDestroy(c->g_fwd);
-  c->g_step = c->g_fwd = nullptr;
+  destroy_graphs(c);
   if (c->use_graphs) {
-    for (int which = 0; which < 2; ++which) {
-      hipGraph_t g;
-      HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-      if (which == 0)
-        enqueue_step(c);
-      else
-        enqueue_layers(c, false);
-      HIPCHK(c, hipStreamEndCapture(c->stream, &g));
-      hipGraphExec_t ge;
-      HIPCHK(c, hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
-      (void)hipGraphDestroy(g);
-      (which == 0 ? c->g_step : c->g_fwd) = ge;
+    for (int tier = 0; tier < (c->long_attn ? 2 : 1); ++tier) {
+      for (int which = 0; which < 2; ++which) {
+        hipGraph_t g;
+        HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+        if (which == 0)
+          enqueue_step(c, tier == 1);
+        else
+          enqueue_layers(c, false, tier == 1);
+        HIPCHK(c, hipStreamEndCapture(c->stream, &g));
+        hipGraphExec_t ge;
+        HIPCHK(c, hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+        (void)hipGraphDestroy(g);
+        (which == 0 ? c->g_step : c->g_fwd)[tier] = ge;
+      }
     }
   }
   c->graphs_ready = true;
@@ -483,14 +524,17 @@ int push_state(c2h_ctx* c, const C2hState& s) {
   return C2H_OK;
 }
 
-int run_graph(c2h_ctx* c, bool step) {
+// Decode at `pos` attends to pos+1 positions: the long-context kernels
+// take over past the split length.
+int run_graph(c2h_ctx* c, bool step, int pos) {
+  const bool long_attn = c->long_attn && pos + 1 > c->att_split;
   if (c->use_graphs) {
-    HIPCHK(c, hipGraphLaunch(step ? c->g_step : c->g_fwd, c->stream));
+    HIPCHK(c, hipGraphLaunch(step ? c->g_step[long_attn] : c->g_fwd[long_attn], c->stream));
   } else {
     if (step)
-      enqueue_step(c);
+      enqueue_step(c, long_attn);
     else
-      enqueue_layers(c, false);
+      enqueue_layers(c, false, long_attn);
     HIPCHK(c, hipGetLastError());
   }
   return C2H_OK;
@@ -595,14 +639,36 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   if ((rc = dalloc(c, &c->part_v, (size_t)c->n_part * 4)) || (rc = dalloc(c, &c->part_i, (size_t)c->n_part * 4)) ||
       (rc = dalloc(c, &c->logits, (size_t)D.n_vocab * 4)))
     return bail(rc);
-  // attention LDS within the 160 KB of a gfx950 workgroup (8 KB kept for
-  // the kernel's static shared data): staged V | all scores of the context
-  c->attn_lds = (size_t)attn_lds_floats(D.max_ctx) * 4;
-  if (c->attn_lds > 152u * 1024)
-    return bail(fail(c, C2H_ERR_UNSUPPORTED, "max_ctx %d too large for the exact attention kernel", D.max_ctx));
+  // Attention: k_attn_core while a token attends to at most att_split
+  // positions (staged V | all scores in LDS, within the 160 KB of a gfx950
+  // workgroup, 8 KB kept for static shared data), the long-context kernels
+  // beyond.  C2H_ATT_SPLIT overrides the split length (measurement aid).
+  c->att_split = ATT_SPLIT_T;
+  if (const char* sp = getenv("C2H_ATT_SPLIT")) c->att_split = std::max(1, atoi(sp));
+  while (c->att_split > 1 && (size_t)attn_lds_floats(c->att_split) * 4 > 152u * 1024) --c->att_split;
+  c->att_split = std::min(c->att_split, D.max_ctx);
+  c->long_attn = D.max_ctx > c->att_split;
+  c->attn_lds = (size_t)attn_lds_floats(c->att_split) * 4;
   if (hipFuncSetAttribute((const void*)k_attn_core, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->attn_lds) !=
       hipSuccess)
     return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
+  if (c->long_attn) {
+    if (D.max_ctx > ATT_LONG_MAX_CTX)
+      return bail(fail(c, C2H_ERR_UNSUPPORTED, "max_ctx %d above the %d positions of the exact attention kernels",
+                       D.max_ctx, ATT_LONG_MAX_CTX));
+    if (D.n_heads / D.n_kv_heads > ATT_MAX_QPKV)
+      return bail(fail(c, C2H_ERR_UNSUPPORTED, "more than %d query heads per KV head", ATT_MAX_QPKV));
+    c->att_sc_ld = (D.max_ctx + 3) & ~3;
+    c->att_n_blk = (D.max_ctx + ATT_SB - 1) / ATT_SB;
+    if ((rc = dalloc(c, &c->att_sc, (size_t)PF_ATT_SUB * D.n_heads * c->att_sc_ld * 4)) ||
+        (rc = dalloc(c, &c->att_bmax, (size_t)PF_ATT_SUB * D.n_heads * c->att_n_blk * 4)))
+      return bail(rc);
+    if (hipFuncSetAttribute((const void*)k_attn_softmax, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            attn_softmax_lds_floats(D.max_ctx) * 4) != hipSuccess ||
+        hipFuncSetAttribute((const void*)k_attn_av, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            ATT_AV_LDS_FLOATS * 4) != hipSuccess)
+      return bail(fail(c, C2H_ERR_HIP, "long attention LDS attribute"));
+  }
   C2hState s0;
   memset(&s0, 0, sizeof(s0));
   s0.penalty = 1.15f;
@@ -616,8 +682,7 @@ void c2h_destroy(c2h_ctx* c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
   if (c->stream) (void)hipStreamSynchronize(c->stream);
-  if (c->g_step) (void)hipGraphExecDestroy(c->g_step);
-  if (c->g_fwd) (void)hipGraphExecDestroy(c->g_fwd);
+  destroy_graphs(c);
   for (void* p : c->allocs) (void)hipFree(p);
   for (void* p : c->scratch) (void)hipFree(p);
   if (c->state_ring) (void)hipHostFree(c->state_ring);
@@ -698,9 +763,10 @@ int c2h_forward(c2h_ctx* c, int32_t token, int32_t pos, float* normx_out) {
   s.nx_in = c->nx_cur;
   s.nx_out = c->nx_cur ^ 1;
   if ((rc = push_state(c, s))) return rc;
-  if ((rc = run_graph(c, false))) return rc;
+  if ((rc = run_graph(c, false, pos))) return rc;
   c->nx_prev = c->nx_cur;
   c->nx_cur ^= 1;
+  c->seq_len = pos + 1;
   if (normx_out) {
     HIPCHK(c, hipMemcpyAsync(normx_out, c->normx[c->nx_cur], (size_t)c->desc.n_embd * 4, hipMemcpyDeviceToHost,
                              c->stream));
@@ -837,9 +903,8 @@ int pf_pass(c2h_ctx* c, const int32_t* tokens, int m, int pos0) {
       R.max_ctx = D.max_ctx;
       hipLaunchKernelGGL(k_pf_rope_store, dim3(m, D.n_kv_heads), dim3(64), 0, c->stream, R);
     }
-    {
-      AttnCoreParams A;
-      memset(&A, 0, sizeof(A));
+    {  // causal attention of every token (its K/V and the earlier ones are stored)
+      AttnCoreParams A = attn_params(c, l);
       A.q = p.q;
       A.k = p.k;
       A.v = p.v;
@@ -848,19 +913,15 @@ int pf_pass(c2h_ctx* c, const int32_t* tokens, int m, int pos0) {
       A.kv_ld = KV;
       A.out_ld = E;
       A.store_kv = 0;
-      A.kv = c->kv;
-      A.rope_cos = c->rope_cos;
-      A.rope_sin = c->rope_sin;
-      A.rope_len = D.max_ctx;
-      A.layer = l;
-      A.n_layers = D.n_layers;
-      A.n_heads = D.n_heads;
-      A.n_kv_heads = D.n_kv_heads;
-      A.max_ctx = D.max_ctx;
-      A.scale = (float)(1.0 / std::sqrt((double)D.head_dim));
-      A.state = c->state_dev;
-      const size_t lds = (size_t)attn_lds_floats(pos0 + m) * 4;
-      hipLaunchKernelGGL(k_attn_core, dim3(D.n_heads, m), dim3(256), lds, c->stream, A);
+      if (pos0 + m <= c->att_split) {
+        const size_t lds = (size_t)attn_lds_floats(pos0 + m) * 4;
+        hipLaunchKernelGGL(k_attn_core, dim3(D.n_heads, m), dim3(256), lds, c->stream, A);
+      } else {
+        for (int t0 = 0; t0 < m; t0 += PF_ATT_SUB) {
+          A.tok0 = t0;
+          enqueue_attn_long(c, A, std::min(PF_ATT_SUB, m - t0));
+        }
+      }
     }
     {
       PFQuantParams Q{p.attn, E, m, q8};
@@ -921,6 +982,7 @@ int c2h_prefill(c2h_ctx* c, const int32_t* tokens, int32_t n, int32_t pos0, floa
     if ((rc = pf_pass(c, tokens + done, m, pos0 + done))) return rc;
     HIPCHK(c, hipStreamSynchronize(c->stream));  // tokens are copied from the caller's buffer
     done += m;
+    c->seq_len = pos0 + done;
   }
   if (normx_out)
     HIPCHK(c, hipMemcpy(normx_out, c->normx[c->nx_cur], (size_t)c->desc.n_embd * 4, hipMemcpyDeviceToHost));
@@ -962,9 +1024,10 @@ int c2h_step(c2h_ctx* c, int32_t pos, float penalty, int32_t im_end, int32_t eos
   s.nx_in = c->nx_cur;
   s.nx_out = c->nx_cur ^ 1;
   if ((rc = push_state(c, s))) return rc;
-  if ((rc = run_graph(c, true))) return rc;
+  if ((rc = run_graph(c, true, pos))) return rc;
   c->nx_prev = c->nx_cur;
   c->nx_cur ^= 1;
+  c->seq_len = pos + 1;
   HIPCHK(c, hipMemcpyAsync(c->tok_host, &c->state_dev->token, 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
   if (next_token) *next_token = *c->tok_host;
@@ -997,6 +1060,46 @@ int c2h_get_kv(c2h_ctx* c, int32_t which, int32_t layer, int32_t kv_head, int32_
   size_t off = ((((size_t)which * D.n_layers + layer) * D.n_kv_heads + kv_head) * D.max_ctx) * D.head_dim;
   HIPCHK(c, hipMemcpyAsync(out, c->kv + off, (size_t)n * D.head_dim * 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
+  return C2H_OK;
+}
+
+int c2h_set_kv(c2h_ctx* c, int32_t which, int32_t layer, int32_t kv_head, int32_t pos0, int32_t n, const float* src) {
+  if (!c || (!src && n > 0)) return C2H_ERR_INVALID;
+  if (!c->has_model) return fail(c, C2H_ERR_STATE, "kernel-only context");
+  const c2h_model_desc& D = c->desc;
+  if (which < 0 || which > 1 || layer < 0 || layer >= D.n_layers || kv_head < 0 || kv_head >= D.n_kv_heads)
+    return fail(c, C2H_ERR_INVALID, "kv index out of range");
+  if (pos0 < 0 || n < 0 || (int64_t)pos0 + n > D.max_ctx)
+    return fail(c, C2H_ERR_RANGE, "positions [%d, %d) outside [0, %d)", pos0, pos0 + n, D.max_ctx);
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  size_t off = ((((size_t)which * D.n_layers + layer) * D.n_kv_heads + kv_head) * D.max_ctx + pos0) * D.head_dim;
+  if (n) HIPCHK(c, hipMemcpy(c->kv + off, src, (size_t)n * D.head_dim * 4, hipMemcpyHostToDevice));
+  return C2H_OK;
+}
+
+int c2h_get_token_ids(c2h_ctx* c, int32_t pos0, int32_t n, int32_t* out) {
+  if (!c || (!out && n > 0)) return C2H_ERR_INVALID;
+  if (!c->has_model) return fail(c, C2H_ERR_STATE, "kernel-only context");
+  if (pos0 < 0 || n < 0 || (int64_t)pos0 + n > c->desc.max_ctx) return fail(c, C2H_ERR_RANGE, "token ids out of range");
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (n) HIPCHK(c, hipMemcpy(out, c->token_ids + pos0, (size_t)n * 4, hipMemcpyDeviceToHost));
+  return C2H_OK;
+}
+
+int c2h_set_seq(c2h_ctx* c, int32_t seq_len) {
+  if (!c) return C2H_ERR_INVALID;
+  if (!c->has_model) return fail(c, C2H_ERR_STATE, "kernel-only context");
+  if (seq_len < 0 || seq_len > c->desc.max_ctx)
+    return fail(c, C2H_ERR_RANGE, "seq_len %d outside [0, %d]", seq_len, c->desc.max_ctx);
+  c->seq_len = seq_len;
+  return C2H_OK;
+}
+
+int c2h_get_seq(c2h_ctx* c, int32_t* seq_len) {
+  if (!c || !seq_len) return C2H_ERR_INVALID;
+  *seq_len = c->seq_len;
   return C2H_OK;
 }
 
@@ -1214,7 +1317,7 @@ int c2h_time_vocab(c2h_ctx* c, int32_t iters, int32_t pos, int32_t in_step, floa
   for (auto& e : ev) HIPCHK(c, hipEventCreate(&e));
   rc = C2H_OK;
   for (int i = 0; i < iters && rc == C2H_OK; ++i) {
-    if (in_step) rc = run_graph(c, false);
+    if (in_step) rc = run_graph(c, false, pos);
     if (rc == C2H_OK) {
       (void)hipEventRecord(ev[2 * i], c->stream);
       enqueue_vocab(c, 1, nullptr, 1, nullptr);
@@ -1259,10 +1362,11 @@ int c2h_time_steps(c2h_ctx* c, int32_t pos, int32_t iters, float penalty, int32_
     s.nx_in = c->nx_cur;
     s.nx_out = c->nx_cur ^ 1;
     if ((rc = push_state(c, s))) return rc;
-    if ((rc = run_graph(c, true))) return rc;
+    if ((rc = run_graph(c, true, pos + i))) return rc;
     c->nx_prev = c->nx_cur;
     c->nx_cur ^= 1;
   }
+  c->seq_len = pos + iters;
   HIPCHK(c, hipEventRecord(e1, c->stream));
   HIPCHK(c, hipEventSynchronize(e1));
   float t = 0;

@@ -107,8 +107,8 @@ struct GemvParams {
   GemvJob jobs[MAX_JOBS];
 };
 
-// LDS floats for a chained-sum buffer of n values: the chain reads two
-// 32-value chunks ahead of the one it adds.
+// LDS floats for a chained-sum buffer of n values (whole 16-value chunks
+// of the speculative sum are readable, with slack).
 __host__ __device__ inline int chain_lds_floats(int n) { return ((n + 31) & ~31) + 64; }
 
 struct NormParams {
@@ -123,19 +123,31 @@ struct NormParams {
   C2hState* state;
 };
 
-// Attention of one layer, one workgroup per query head, over the q|k|v the
-// QKV GEMV wrote: RoPE, KV store, scores, softmax, AV.
+// Attention of one layer over the q|k|v the QKV GEMV wrote: RoPE, KV store,
+// scores, softmax, AV.  Two exact forms with the same arithmetic:
+//   short contexts (T <= the context's split length): k_attn_core, one
+//     workgroup per query head does everything with the scores in LDS;
+//   long contexts: k_attn_scores (workgroups over position blocks, one K
+//     row read for all query heads of a group) -> k_attn_softmax (one
+//     workgroup per head, exps in LDS) -> k_attn_av (one workgroup per head:
+//     one wave runs the FMA chains, the others stage V through LDS).
 constexpr int ATT_CH = 128;   // V positions staged in LDS per pass (chunk 0 prefetched)
 constexpr int ATT_KPF = 256;  // positions whose K row is prefetched (one per thread)
-// grid (n_heads, tokens): query token i of a batch sits at position
-// state->pos + i; decode launches one token.
+constexpr int ATT_SPLIT_T = 1024;  // default split length (positions attended)
+constexpr int ATT_SB = 256;        // positions per k_attn_scores workgroup
+constexpr int ATT_AV_CH = 256;     // positions per k_attn_av LDS chunk
+constexpr int ATT_MAX_QPKV = 8;    // query heads per KV head the long form handles
+constexpr int ATT_LONG_MAX_CTX = 36864;  // exps of one head in LDS (k_attn_softmax)
+// grid (n_heads, tokens) for k_attn_core / k_attn_softmax / k_attn_av and
+// (blocks, n_kv_heads, tokens) for k_attn_scores: query token i of a launch
+// sits at position state->pos + tok0 + i; decode launches one token.
 struct AttnCoreParams {
   const float* q;  // [tokens][q_ld]: n_heads*64, bias added, before RoPE
   const float* k;  // [tokens][kv_ld]: n_kv_heads*64
   const float* v;
   float* out;      // attention output [tokens][out_ld]
   int q_ld, kv_ld, out_ld;
-  int store_kv;    // 1: the first head of each group stores K/V at pos
+  int store_kv;    // 1: K/V of pos come from k/v and are stored by this launch
   float* kv;
   const float* rope_cos;
   const float* rope_sin;
@@ -147,10 +159,21 @@ struct AttnCoreParams {
   int max_ctx;
   float scale;
   C2hState* state;
+  int tok0;  // first query token of this launch within the q/k/v/out rows
+  // long form: scores / probabilities sc[(i*n_heads + h)*sc_ld + p] of
+  // launch token i, block maxima bmax[(i*n_heads + h)*n_blk + b]
+  float* sc;
+  float* bmax;
+  int sc_ld;
+  int n_blk;
 };
 
 // Dynamic LDS of the attention kernel, in floats: staged V | scores.
 __host__ __device__ inline int attn_lds_floats(int max_ctx) { return ATT_CH * 64 + chain_lds_floats(max_ctx); }
+// Dynamic LDS of k_attn_softmax (exps of up to max_ctx positions) and of
+// k_attn_av (two chunks of V rows and probabilities), in floats.
+__host__ __device__ inline int attn_softmax_lds_floats(int max_ctx) { return (max_ctx + 3) & ~3; }
+constexpr int ATT_AV_LDS_FLOATS = 2 * ATT_AV_CH * (64 + 1);
 
 // ---- batched prefill (a prompt of up to PF_MAX tokens per pass)
 
@@ -245,6 +268,9 @@ template <int NB, int PRO, int MODE>
 __global__ void k_gemv_row(GemvParams P);
 __global__ void k_rmsnorm(NormParams P);
 __global__ void k_attn_core(AttnCoreParams P);
+__global__ void k_attn_scores(AttnCoreParams P);
+__global__ void k_attn_softmax(AttnCoreParams P);
+__global__ void k_attn_av(AttnCoreParams P);
 template <int NB>
 __global__ void k_pf_norm_quant(PFNormParams P);
 template <int NB>

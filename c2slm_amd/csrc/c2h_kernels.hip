@@ -158,65 +158,6 @@ __global__ void __launch_bounds__(256) k_quantize_q8k(const float* __restrict__ 
 
 // ------------------------------------------------------------ RMSNorm (A8)
 
-// Sequential f32 sum a[0] + a[1] + ... + a[n-1] (one dependent add per
-// element, the reference's order) of an LDS buffer readable to
-// chain_lds_floats(n).  Two 32-value chunks are double-buffered so the
-// chain runs at add latency with no register copies.
-__device__ __forceinline__ void add_chunk(float& s, const float4 (&c)[8]) {
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    s = s + c[k].x;
-    s = s + c[k].y;
-    s = s + c[k].z;
-    s = s + c[k].w;
-  }
-}
-
-__device__ __forceinline__ void load_chunk(float4 (&c)[8], const float4* a4, int chunk) {
-#pragma unroll
-  for (int k = 0; k < 8; ++k) c[k] = a4[8 * chunk + k];
-}
-
-__device__ __forceinline__ float seq_sum_lds(const float* a, int n) {
-  const float4* a4 = reinterpret_cast<const float4*>(a);
-  float s = 0.0f;
-  float4 A[8], B[8];
-  load_chunk(A, a4, 0);
-  const int nc = n >> 5;
-  int i = 0;
-  for (; i + 2 <= nc; i += 2) {
-    // the scheduler would otherwise sink each chunk's reads below the adds
-    // of the previous chunk and expose the LDS latency on every chunk
-    load_chunk(B, a4, i + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    add_chunk(s, A);
-    load_chunk(A, a4, i + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    add_chunk(s, B);
-  }
-  const int r = n & 31;
-  if (i < nc) {  // one full chunk (in A) left, the tail in B
-    load_chunk(B, a4, i + 1);
-    add_chunk(s, A);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (4 * k + 0 < r) s = s + B[k].x;
-      if (4 * k + 1 < r) s = s + B[k].y;
-      if (4 * k + 2 < r) s = s + B[k].z;
-      if (4 * k + 3 < r) s = s + B[k].w;
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (4 * k + 0 < r) s = s + A[k].x;
-      if (4 * k + 1 < r) s = s + A[k].y;
-      if (4 * k + 2 < r) s = s + A[k].z;
-      if (4 * k + 3 < r) s = s + A[k].w;
-    }
-  }
-  return s;
-}
-
 // Wave-wide inclusive prefix sum (DPP, Hillis-Steele within rows of 16,
 // then across rows).  It only steers the speculation in seq_sum_wave; its
 // roundings never reach a result.
@@ -291,6 +232,48 @@ __device__ __forceinline__ float seq_sum_wave(const float* a, int n) {
   if (lane == 0) {
     for (int i = (m + 1) * SPEC_C; i < n; ++i) s = s + a[i];
   }
+  return __shfl(s, 0);
+}
+
+// The same exact sequential sum for any n >= 1 (softmax over long contexts):
+// lane l owns [l*C, l*C + C), C = ceil(n/64) rounded up to a multiple of 4,
+// and re-reads its chunk from LDS each round.  a: 16-byte aligned LDS.
+__device__ __forceinline__ float chunk_chain(const float* a, int b0, int b1, float s) {
+  int i = b0;
+  for (; i + 16 <= b1; i += 16) {
+    const float4 c0 = *reinterpret_cast<const float4*>(a + i);
+    const float4 c1 = *reinterpret_cast<const float4*>(a + i + 4);
+    const float4 c2 = *reinterpret_cast<const float4*>(a + i + 8);
+    const float4 c3 = *reinterpret_cast<const float4*>(a + i + 12);
+    s = s + c0.x; s = s + c0.y; s = s + c0.z; s = s + c0.w;
+    s = s + c1.x; s = s + c1.y; s = s + c1.z; s = s + c1.w;
+    s = s + c2.x; s = s + c2.y; s = s + c2.z; s = s + c2.w;
+    s = s + c3.x; s = s + c3.y; s = s + c3.z; s = s + c3.w;
+  }
+  for (; i < b1; ++i) s = s + a[i];
+  return s;
+}
+
+__device__ __forceinline__ float seq_sum_wave_n(const float* a, int n) {
+  const int lane = threadIdx.x & 63;
+  const int C = (((n + 63) >> 6) + 3) & ~3;
+  const int b0 = min(lane * C, n), b1 = min(b0 + C, n);
+  const float cs = chunk_chain(a, b0, b1, 0.0f);
+  float S = (lane == 0) ? 0.0f : wave_shift_up(wave_incl_scan(cs));
+  int m = -1;
+  for (int round = 0; round < SPEC_ROUNDS; ++round) {
+    const float R = chunk_chain(a, b0, b1, S);
+    const float s_next = __shfl_down(S, 1);
+    const unsigned long long bad = __ballot(lane < 63 && !(R == s_next));
+    if (bad == 0ull) return __shfl(R, 63);
+    m = __ffsll(bad) - 1;
+    const float e = (lane < 63) ? (R - s_next) : 0.0f;
+    const float shift = (lane == 0) ? 0.0f : wave_shift_up(wave_incl_scan(e));
+    const float r_prev = __shfl_up(R, 1);
+    S = (lane <= m) ? S : ((lane == m + 1) ? r_prev : S + shift);
+  }
+  float s = __shfl(S, m + 1);
+  if (lane == 0) s = chunk_chain(a, min((m + 1) * C, n), n, s);
   return __shfl(s, 0);
 }
 
@@ -820,7 +803,7 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
 
   const int tid = threadIdx.x;
   const int h = blockIdx.x;
-  const int ti = blockIdx.y;  // query token of the batch (0 in decode)
+  const int ti = P.tok0 + blockIdx.y;  // query token of the batch (0 in decode)
   const int qpkv = P.n_heads / P.n_kv_heads;
   const int g = h / qpkv;
   const int pos = P.state->pos + ti;
@@ -913,8 +896,9 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
       const float ssum = seq_sum_wave(sc, T);
       if (tid == 0) inv_slot = 1.0f / ssum;
     }
-  } else if (tid == 0) {
-    inv_slot = 1.0f / seq_sum_lds(sc, T);
+  } else if (tid < 64) {
+    const float ssum = seq_sum_wave_n(sc, T);
+    if (tid == 0) inv_slot = 1.0f / ssum;
   }
 #pragma unroll
   for (int i = 0; i < VPT; ++i) reinterpret_cast<f32x4_t*>(vbuf)[tid + 256 * i] = vreg[i];
@@ -962,6 +946,213 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   }
 }
 
+
+// ------------------------------------------- attention, long contexts
+//
+// The arithmetic of k_attn_core, split so that a context of tens of
+// thousands of positions is scored by many workgroups:
+//   k_attn_scores   scores of ATT_SB positions for every query head of one
+//                   KV group (each K row read once), block maxima per head;
+//   k_attn_softmax  max over the block maxima (x[0] first: a NaN score[0]
+//                   makes the max NaN, tensor/ops.go:321-326), f64 exp, the
+//                   sequential f32 sum (exact speculative form), p = e/sum;
+//   k_attn_av       per output dim the FMA chain over p = 0..pos in order,
+//                   run by wave 0 while waves 1..15 stage V rows and
+//                   probabilities through two LDS chunks.
+
+// In decode (store_kv) the workgroup whose block holds pos stores RoPE(k)
+// and v at pos; a batch has stored its K/V before the launch.
+__global__ void __launch_bounds__(256) k_attn_scores(AttnCoreParams P) {
+  constexpr int HD = 64;
+  __shared__ __align__(16) float qs[ATT_MAX_QPKV][HD];
+  __shared__ __align__(16) float ks[HD];
+  __shared__ float bm[4][ATT_MAX_QPKV];
+  const int tid = threadIdx.x;
+  const int g = blockIdx.y;
+  const int ti = P.tok0 + blockIdx.z;
+  const int qpkv = P.n_heads / P.n_kv_heads;
+  const int pos = P.state->pos + ti;
+  const int T = pos + 1;
+  const int p0 = blockIdx.x * ATT_SB;
+  if (p0 >= T) return;  // uniform: blocks past the context do nothing
+  const size_t head_stride = (size_t)P.max_ctx * HD;
+  float* kcache = P.kv + ((size_t)P.layer * P.n_kv_heads + g) * head_stride;
+  float* vcache = P.kv + (((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * head_stride;
+  const int p = p0 + tid;
+  const int kmax = P.store_kv ? max(pos - 1, 0) : pos;  // last K row already in the cache
+
+  // ---- loads
+  const int nq4 = qpkv * (HD / 4);
+  const float4 qv = reinterpret_cast<const float4*>(P.q + (size_t)ti * P.q_ld + (size_t)g * qpkv * HD)[min(tid, nq4 - 1)];
+  const float kn = P.k[(size_t)ti * P.kv_ld + g * HD + (tid & 63)];
+  const float vn = P.v[(size_t)ti * P.kv_ld + g * HD + (tid & 63)];
+  const int rp = min(max(pos, 0), P.rope_len - 1);
+  const float rcos = P.rope_cos[(size_t)rp * (HD / 2) + (tid & 31)];
+  const float rsin = P.rope_sin[(size_t)rp * (HD / 2) + (tid & 31)];
+  float4 kreg[16];
+  {
+    const float4* kr = reinterpret_cast<const float4*>(kcache + (size_t)min(p, kmax) * HD);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) kreg[i] = kr[i];
+  }
+  issue_fence();
+
+  if (tid < nq4) reinterpret_cast<float4*>(&qs[0][0])[tid] = qv;
+  if (tid < HD) ks[tid] = kn;
+  __syncthreads();
+  // RoPE (tensor/ops.go:262-286) of the group's query heads and of k
+  if (pos >= 0 && pos < P.rope_len) {
+    for (int i = tid; i < (qpkv + 1) * 32; i += 256) {  // i & 31 == tid & 31
+      float* x = (i < qpkv * 32) ? qs[i >> 5] : ks;
+      const int j = i & 31;
+      const float x0 = x[j], x1 = x[j + 32];
+      x[j] = (x0 * rcos) - (x1 * rsin);
+      x[j + 32] = (x0 * rsin) + (x1 * rcos);
+    }
+  }
+  __syncthreads();
+  if (P.store_kv && tid < HD && pos >= p0 && pos < p0 + ATT_SB && pos < P.max_ctx) {
+    kcache[(size_t)pos * HD + tid] = ks[tid];
+    vcache[(size_t)pos * HD + tid] = vn;
+  }
+  if (P.store_kv && p == pos) {
+    const float4* ks4 = reinterpret_cast<const float4*>(ks);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) kreg[i] = ks4[i];
+  }
+
+  const bool valid = p < T;
+  float* srow = P.sc + ((size_t)blockIdx.z * P.n_heads + (size_t)g * qpkv) * P.sc_ld;
+  for (int hh = 0; hh < qpkv; ++hh) {
+    const float sco = attn_score(qs[hh], kreg, P.scale);
+    if (valid) srow[(size_t)hh * P.sc_ld + p] = sco;
+    float lm = (valid && sco > -__builtin_inff()) ? sco : -__builtin_inff();  // NaN never wins
+    lm = wave_max_dpp(lm);
+    if ((tid & 63) == 0) bm[tid >> 6][hh] = lm;
+  }
+  __syncthreads();
+  if (tid < qpkv) {
+    const float m = fmax_gt(fmax_gt(fmax_gt(bm[0][tid], bm[1][tid]), bm[2][tid]), bm[3][tid]);
+    P.bmax[((size_t)blockIdx.z * P.n_heads + (size_t)g * qpkv + tid) * P.n_blk + blockIdx.x] = m;
+  }
+}
+
+__global__ void __launch_bounds__(1024) k_attn_softmax(AttnCoreParams P) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* e = reinterpret_cast<float*>(smem);  // [attn_softmax_lds_floats(max_ctx)]
+  __shared__ float red[16];
+  __shared__ float inv_slot;
+  const int tid = threadIdx.x;
+  const int h = blockIdx.x;
+  const int i = blockIdx.y;
+  const int pos = P.state->pos + P.tok0 + i;
+  const int T = pos + 1;
+  float* s = P.sc + ((size_t)i * P.n_heads + h) * P.sc_ld;
+  const float* bmx = P.bmax + ((size_t)i * P.n_heads + h) * P.n_blk;
+  const int nb = (T + ATT_SB - 1) / ATT_SB;
+  float lm = -__builtin_inff();
+  for (int b = tid; b < nb; b += 1024) lm = fmax_gt(lm, bmx[b]);  // block maxima are never NaN
+  lm = wave_max_dpp(lm);
+  if ((tid & 63) == 0) red[tid >> 6] = lm;
+  __syncthreads();
+  float mx = red[0];
+#pragma unroll
+  for (int w = 1; w < 16; ++w) mx = fmax_gt(mx, red[w]);
+  const float s0 = s[0];
+  if (s0 != s0) mx = s0;
+  for (int p = tid; p < T; p += 1024) e[p] = (float)exp((double)(s[p] - mx));
+  __syncthreads();
+  if (tid < 64) {
+    const float ssum = seq_sum_wave_n(e, T);
+    if (tid == 0) inv_slot = 1.0f / ssum;
+  }
+  __syncthreads();
+  const float inv = inv_slot;
+  for (int p = tid; p < T; p += 1024) s[p] = e[p] * inv;
+}
+
+__global__ void __launch_bounds__(1024) k_attn_av(AttnCoreParams P) {
+  constexpr int HD = 64;
+  constexpr int NV4 = ATT_AV_CH * HD / 4;  // float4 of V per chunk
+  constexpr int NP4 = ATT_AV_CH / 4;       // float4 of probabilities per chunk
+  constexpr int NPROD = 1024 - 64;         // staging threads (waves 1..15)
+  constexpr int PER = (NV4 + NP4 + NPROD - 1) / NPROD;
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* vb = reinterpret_cast<float*>(smem);  // [2][ATT_AV_CH][64]
+  float* pb = vb + 2 * ATT_AV_CH * HD;         // [2][ATT_AV_CH]
+  const int tid = threadIdx.x;
+  const int h = blockIdx.x, i = blockIdx.y;
+  const int ti = P.tok0 + i;
+  const int g = h / (P.n_heads / P.n_kv_heads);
+  const int pos = P.state->pos + ti;
+  const int T = pos + 1;
+  const float* vcache = P.kv + (((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * (size_t)P.max_ctx * HD;
+  const float* s = P.sc + ((size_t)i * P.n_heads + h) * P.sc_ld;
+  const int nch = (T + ATT_AV_CH - 1) / ATT_AV_CH;
+  const int j = tid - 64;
+  const int plast4 = (T - 1) & ~3;
+  f32x4_t r[PER];
+  // chunk c into registers: V rows c*CH.. (clamped to pos) and their
+  // probabilities (a float4 that starts before T stays inside the row)
+  auto load_chunk = [&](int c) {
+    const int base = c * ATT_AV_CH;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int f = j + NPROD * k;
+      const int pp = min(base + (f >> 4), T - 1);
+      const float* va = vcache + (size_t)pp * HD + 4 * (f & 15);
+      const float* sa = s + min(base + 4 * (f - NV4), plast4);
+      r[k] = *reinterpret_cast<const f32x4_t*>((f < NV4) ? va : sa);
+    }
+  };
+  auto store_chunk = [&](int c) {
+    float* vbb = vb + (c & 1) * ATT_AV_CH * HD;
+    float* pbb = pb + (c & 1) * ATT_AV_CH;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int f = j + NPROD * k;
+      if (f < NV4)
+        reinterpret_cast<f32x4_t*>(vbb)[f] = r[k];
+      else if (f < NV4 + NP4)
+        reinterpret_cast<f32x4_t*>(pbb)[f - NV4] = r[k];
+    }
+  };
+  if (tid >= 64) {
+    load_chunk(0);
+    store_chunk(0);
+    if (nch > 1) load_chunk(1);
+  }
+  __syncthreads();
+  float acc = 0.0f;
+  const int d = tid & 63;
+  for (int c = 0; c < nch; ++c) {
+    if (tid < 64) {
+      const float* vbb = vb + (c & 1) * ATT_AV_CH * HD;
+      const float* pbb = pb + (c & 1) * ATT_AV_CH;
+      const int np = min(ATT_AV_CH, T - c * ATT_AV_CH);
+      int p = 0;
+      for (; p + 16 <= np; p += 16) {
+        float vv[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) vv[k] = vbb[(p + k) * HD + d];
+        const float4 s0 = *reinterpret_cast<const float4*>(pbb + p);
+        const float4 s1 = *reinterpret_cast<const float4*>(pbb + p + 4);
+        const float4 s2 = *reinterpret_cast<const float4*>(pbb + p + 8);
+        const float4 s3 = *reinterpret_cast<const float4*>(pbb + p + 12);
+        const float ss[16] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w,
+                              s2.x, s2.y, s2.z, s2.w, s3.x, s3.y, s3.z, s3.w};
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc = __builtin_fmaf(ss[k], vv[k], acc);
+      }
+      for (; p < np; ++p) acc = __builtin_fmaf(pbb[p], vbb[p * HD + d], acc);
+    } else {
+      if (c + 1 < nch) store_chunk(c + 1);
+      if (c + 2 < nch) load_chunk(c + 2);
+    }
+    __syncthreads();
+  }
+  if (tid < 64) P.out[(size_t)ti * P.out_ld + h * HD + d] = acc;
+}
 
 // ------------------------------------------------------- prefill (A17)
 //

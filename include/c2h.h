@@ -61,7 +61,8 @@ typedef struct c2h_model_desc {
   int32_t head_dim;   /* n_embd / n_heads (64) */
   int32_t n_ff;       /* qwen2.feed_forward_length (4864) */
   int32_t n_vocab;    /* token_embd dims[1] (151936) */
-  int32_t max_ctx;    /* KV positions; engine.MaxContextLen = 16384 (engine/kvcache.go:11) */
+  int32_t max_ctx;    /* KV positions; engine.MaxContextLen = 16384 (engine/kvcache.go:11);
+                         this build runs up to 36864 */
   float rms_eps;      /* 1e-6 */
   float rope_theta;   /* 1e6 */
   int32_t reserved[6];
@@ -99,6 +100,20 @@ int c2h_upload_tensor(c2h_ctx* ctx, int32_t layer, int32_t role, int32_t ggml_ty
 /* Mirrors KVCache.StoreTokenID (engine/kvcache.go:120-125) for ids the
  * device did not write itself; c2h_forward and c2h_step record their own. */
 int c2h_set_token_ids(c2h_ctx* ctx, int32_t pos0, const int32_t* ids, int32_t n);
+
+/* Reads KVCache.TokenIDs[pos0 .. pos0+n) (engine/kvcache.go:25-47), the
+ * token fingerprint c2slm_test.go:76-80 checks. */
+int c2h_get_token_ids(c2h_ctx* ctx, int32_t pos0, int32_t n, int32_t* out);
+
+/* KVCache.SeqLen (engine/kvcache.go:25-47): the count of materialised
+ * positions.  c2h_forward(pos) and c2h_step(pos) set it to pos+1 and
+ * c2h_prefill to pos0+n, as Engine.IngestFrom and generate do
+ * (c2slm.go:114,187,200,222).  c2h_set_seq is KVCache.Reset (seq_len 0,
+ * engine/kvcache.go:101-103) and Rewind (engine/kvcache.go:109-117): no
+ * memory moves; entries past the cursor stay until overwritten.
+ * seq_len outside [0, max_ctx] returns C2H_ERR_RANGE. */
+int c2h_set_seq(c2h_ctx* ctx, int32_t seq_len);
+int c2h_get_seq(c2h_ctx* ctx, int32_t* seq_len);
 
 /* ---- decode path -------------------------------------------------------- */
 
@@ -141,6 +156,13 @@ int c2h_get_normx(c2h_ctx* ctx, float* normx_out);
  * the host ([n][head_dim] floats): KVCache.GetKey/GetValue
  * (engine/kvcache.go:159-169). */
 int c2h_get_kv(c2h_ctx* ctx, int32_t which, int32_t layer, int32_t kv_head, int32_t n, float* out);
+
+/* The reverse copy, KVCache.StoreKV (engine/kvcache.go:143-157) for a run of
+ * positions of one layer/KV head: src holds [n][head_dim] floats written to
+ * positions [pos0, pos0+n) of K or V (which = 0/1); for callers that restore
+ * or pre-fill a cache.  The range must lie in [0, max_ctx). */
+int c2h_set_kv(c2h_ctx* ctx, int32_t which, int32_t layer, int32_t kv_head, int32_t pos0, int32_t n,
+               const float* src);
 
 /* ---- kernel entry points (tensor/ops.go operators) ----------------------- */
 

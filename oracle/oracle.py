@@ -245,6 +245,17 @@ class OracleEngine:
         return np.ctypeslib.as_array(lib().orc_state_token_ids(self.state), shape=(self.max_ctx,)).copy()
 
     def kv(self) -> np.ndarray:
+        return self.kv_view().copy()
+
+    def kv_view(self) -> np.ndarray:
+        """Writable view of the KV cache [2][L][KVH][max_ctx][HD] (for pre-filling)."""
         n = 2 * self.n_layers * self.n_kv_heads * self.max_ctx * self.head_dim
         a = np.ctypeslib.as_array(lib().orc_state_kv(self.state), shape=(n,))
-        return a.reshape(2, self.n_layers, self.n_kv_heads, self.max_ctx, self.head_dim).copy()
+        return a.reshape(2, self.n_layers, self.n_kv_heads, self.max_ctx, self.head_dim)
+
+    def set_token_ids(self, pos0: int, ids) -> None:
+        ids = np.asarray(ids, np.int32)
+        np.ctypeslib.as_array(lib().orc_state_token_ids(self.state), shape=(self.max_ctx,))[pos0:pos0 + len(ids)] = ids
+
+    def set_seq_len(self, n: int) -> None:
+        lib().orc_state_set_seq_len(self.state, n)
