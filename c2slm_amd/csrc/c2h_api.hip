@@ -370,7 +370,8 @@ void enqueue_attn_long(c2h_ctx* c, const AttnCoreParams& A, int ntok) {
   hipLaunchKernelGGL(k_attn_scores, dim3(c->att_n_blk, D.n_kv_heads, ntok), dim3(256), 0, c->stream, A);
   hipLaunchKernelGGL(k_attn_softmax, dim3(D.n_heads, ntok), dim3(1024),
                      (size_t)attn_softmax_lds_floats(D.max_ctx) * 4, c->stream, A);
-  hipLaunchKernelGGL(k_attn_av, dim3(D.n_heads, ntok), dim3(1024), (size_t)ATT_AV_LDS_FLOATS * 4, c->stream, A);
+  hipLaunchKernelGGL(k_attn_av, dim3(D.n_heads, ntok), dim3(ATT_AV_THREADS), (size_t)ATT_AV_LDS_FLOATS * 4, c->stream,
+                     A);
 }
 
 // The 24-layer body of engine.Forward plus the final RMSNorm; layer 0 embeds
@@ -544,6 +545,46 @@ thread_local std::string g_create_err;
 
 }  // namespace
 
+namespace {
+
+// Device offset of one layer/KV head slot of K (which 0) or V (which 1).
+size_t kv_slot_offset(const c2h_model_desc& D, int which, int layer, int kv_head) {
+  return (((size_t)which * D.n_layers + layer) * D.n_kv_heads + kv_head) * (size_t)kv_slot(D.max_ctx) * D.head_dim;
+}
+
+int check_kv_args(c2h_ctx* c, int which, int layer, int kv_head, int pos0, int n) {
+  if (!c->has_model) return fail(c, C2H_ERR_STATE, "kernel-only context");
+  const c2h_model_desc& D = c->desc;
+  if (which < 0 || which > 1 || layer < 0 || layer >= D.n_layers || kv_head < 0 || kv_head >= D.n_kv_heads)
+    return fail(c, C2H_ERR_INVALID, "kv index out of range");
+  if (pos0 < 0 || n < 0 || (int64_t)pos0 + n > D.max_ctx)
+    return fail(c, C2H_ERR_RANGE, "positions [%d, %d) outside [0, %d)", pos0, pos0 + n, D.max_ctx);
+  return C2H_OK;
+}
+
+// V rows [pos0, pos0+n) <-> the quad-major slot: the covering quads travel
+// whole and are (re)ordered on the host.
+int v_rows_copy(c2h_ctx* c, int layer, int kv_head, int pos0, int n, float* rows, bool to_device) {
+  const c2h_model_desc& D = c->desc;
+  const int q0 = pos0 >> 2, q1 = (pos0 + n + 3) >> 2;
+  std::vector<float> quads((size_t)(q1 - q0) * 256);
+  float* dev = c->kv + kv_slot_offset(D, 1, layer, kv_head) + (size_t)q0 * 256;
+  HIPCHK(c, hipMemcpy(quads.data(), dev, quads.size() * 4, hipMemcpyDeviceToHost));
+  for (int p = pos0; p < pos0 + n; ++p)
+    for (int d = 0; d < 64; ++d) {
+      float& q = quads[vq_index(p, d) - (size_t)q0 * 256];
+      float& r = rows[(size_t)(p - pos0) * 64 + d];
+      if (to_device)
+        q = r;
+      else
+        r = q;
+    }
+  if (to_device) HIPCHK(c, hipMemcpy(dev, quads.data(), quads.size() * 4, hipMemcpyHostToDevice));
+  return C2H_OK;
+}
+
+}  // namespace
+
 // ====================================================================== ABI
 
 extern "C" {
@@ -611,7 +652,7 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
       (rc = dalloc(c, &c->v, KV * 4)) || (rc = dalloc(c, &c->attn, E * 4)) || (rc = dalloc(c, &c->h, F * 4)) ||
       (rc = dalloc(c, &c->normx[0], E * 4)) || (rc = dalloc(c, &c->normx[1], E * 4)))
     return bail(rc);
-  size_t kv_bytes = (size_t)2 * D.n_layers * D.n_kv_heads * D.max_ctx * D.head_dim * 4;
+  size_t kv_bytes = (size_t)2 * D.n_layers * D.n_kv_heads * kv_slot(D.max_ctx) * D.head_dim * 4;
   if ((rc = dalloc(c, &c->kv, kv_bytes))) return bail(rc);
   if (hipMemset(c->kv, 0, kv_bytes) != hipSuccess) return bail(fail(c, C2H_ERR_HIP, "hipMemset kv"));
   if ((rc = dalloc(c, &c->token_ids, (size_t)D.max_ctx * 4))) return bail(rc);
@@ -1050,31 +1091,30 @@ int c2h_get_normx(c2h_ctx* c, float* out) {
 }
 
 int c2h_get_kv(c2h_ctx* c, int32_t which, int32_t layer, int32_t kv_head, int32_t n, float* out) {
-  if (!c || !out) return C2H_ERR_INVALID;
-  if (!c->has_model) return fail(c, C2H_ERR_STATE, "kernel-only context");
+  if (!c || (!out && n > 0)) return C2H_ERR_INVALID;
+  int rc = check_kv_args(c, which, layer, kv_head, 0, n);
+  if (rc) return rc;
   const c2h_model_desc& D = c->desc;
-  if (which < 0 || which > 1 || layer < 0 || layer >= D.n_layers || kv_head < 0 || kv_head >= D.n_kv_heads || n < 0 ||
-      n > D.max_ctx)
-    return fail(c, C2H_ERR_INVALID, "kv index out of range");
   HIPCHK(c, hipSetDevice(c->device));
-  size_t off = ((((size_t)which * D.n_layers + layer) * D.n_kv_heads + kv_head) * D.max_ctx) * D.head_dim;
-  HIPCHK(c, hipMemcpyAsync(out, c->kv + off, (size_t)n * D.head_dim * 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (n == 0) return C2H_OK;
+  if (which == 1) return v_rows_copy(c, layer, kv_head, 0, n, out, false);
+  HIPCHK(c, hipMemcpy(out, c->kv + kv_slot_offset(D, 0, layer, kv_head), (size_t)n * D.head_dim * 4,
+                      hipMemcpyDeviceToHost));
   return C2H_OK;
 }
 
 int c2h_set_kv(c2h_ctx* c, int32_t which, int32_t layer, int32_t kv_head, int32_t pos0, int32_t n, const float* src) {
   if (!c || (!src && n > 0)) return C2H_ERR_INVALID;
-  if (!c->has_model) return fail(c, C2H_ERR_STATE, "kernel-only context");
+  int rc = check_kv_args(c, which, layer, kv_head, pos0, n);
+  if (rc) return rc;
   const c2h_model_desc& D = c->desc;
-  if (which < 0 || which > 1 || layer < 0 || layer >= D.n_layers || kv_head < 0 || kv_head >= D.n_kv_heads)
-    return fail(c, C2H_ERR_INVALID, "kv index out of range");
-  if (pos0 < 0 || n < 0 || (int64_t)pos0 + n > D.max_ctx)
-    return fail(c, C2H_ERR_RANGE, "positions [%d, %d) outside [0, %d)", pos0, pos0 + n, D.max_ctx);
   HIPCHK(c, hipSetDevice(c->device));
   HIPCHK(c, hipStreamSynchronize(c->stream));
-  size_t off = ((((size_t)which * D.n_layers + layer) * D.n_kv_heads + kv_head) * D.max_ctx + pos0) * D.head_dim;
-  if (n) HIPCHK(c, hipMemcpy(c->kv + off, src, (size_t)n * D.head_dim * 4, hipMemcpyHostToDevice));
+  if (n == 0) return C2H_OK;
+  if (which == 1) return v_rows_copy(c, layer, kv_head, pos0, n, const_cast<float*>(src), true);
+  HIPCHK(c, hipMemcpy(c->kv + kv_slot_offset(D, 0, layer, kv_head) + (size_t)pos0 * D.head_dim, src,
+                      (size_t)n * D.head_dim * 4, hipMemcpyHostToDevice));
   return C2H_OK;
 }
 

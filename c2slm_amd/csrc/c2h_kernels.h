@@ -123,6 +123,14 @@ struct NormParams {
   C2hState* state;
 };
 
+// KV cache: [K|V][layer][kv head][kv_slot(max_ctx)][64] floats.  K rows are
+// position-major (row p at p*64); V is quad-major within a head slot:
+// element (p, d) at vq_index(p, d), so positions 4q..4q+3 of dim d are 16
+// contiguous bytes and quad q (all dims) is 1 KB.  The attention chains
+// read four positions per 16-byte access and V chunks copy to LDS as is.
+__host__ __device__ inline int kv_slot(int max_ctx) { return (max_ctx + 3) & ~3; }
+__host__ __device__ inline size_t vq_index(int p, int d) { return ((size_t)(p >> 2) * 64 + d) * 4 + (p & 3); }
+
 // Attention of one layer over the q|k|v the QKV GEMV wrote: RoPE, KV store,
 // scores, softmax, AV.  Two exact forms with the same arithmetic:
 //   short contexts (T <= the context's split length): k_attn_core, one
@@ -136,6 +144,7 @@ constexpr int ATT_KPF = 256;  // positions whose K row is prefetched (one per th
 constexpr int ATT_SPLIT_T = 1024;  // default split length (positions attended)
 constexpr int ATT_SB = 256;        // positions per k_attn_scores workgroup
 constexpr int ATT_AV_CH = 256;     // positions per k_attn_av LDS chunk
+constexpr int ATT_AV_THREADS = 512;  // k_attn_av: one chain wave, seven staging waves
 constexpr int ATT_MAX_QPKV = 8;    // query heads per KV head the long form handles
 constexpr int ATT_LONG_MAX_CTX = 36864;  // exps of one head in LDS (k_attn_softmax)
 // grid (n_heads, tokens) for k_attn_core / k_attn_softmax / k_attn_av and
@@ -168,10 +177,10 @@ struct AttnCoreParams {
   int n_blk;
 };
 
-// Dynamic LDS of the attention kernel, in floats: staged V | scores.
-__host__ __device__ inline int attn_lds_floats(int max_ctx) { return ATT_CH * 64 + chain_lds_floats(max_ctx); }
+// Dynamic LDS of k_attn_core, in floats: two staged V chunks | scores.
+__host__ __device__ inline int attn_lds_floats(int max_ctx) { return 2 * ATT_CH * 64 + chain_lds_floats(max_ctx); }
 // Dynamic LDS of k_attn_softmax (exps of up to max_ctx positions) and of
-// k_attn_av (two chunks of V rows and probabilities), in floats.
+// k_attn_av (two chunks of V quads and probabilities), in floats.
 __host__ __device__ inline int attn_softmax_lds_floats(int max_ctx) { return (max_ctx + 3) & ~3; }
 constexpr int ATT_AV_LDS_FLOATS = 2 * ATT_AV_CH * (64 + 1);
 

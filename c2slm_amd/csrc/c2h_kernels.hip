@@ -238,17 +238,38 @@ __device__ __forceinline__ float seq_sum_wave(const float* a, int n) {
 // The same exact sequential sum for any n >= 1 (softmax over long contexts):
 // lane l owns [l*C, l*C + C), C = ceil(n/64) rounded up to a multiple of 4,
 // and re-reads its chunk from LDS each round.  a: 16-byte aligned LDS.
+// Sequential adds of a[b0 .. b1) onto s; the LDS reads of the next 16
+// values are issued before the adds of the current 16, so the chain runs at
+// add latency.
+__device__ __forceinline__ void load16(float4 (&c)[4], const float* a) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) c[k] = reinterpret_cast<const float4*>(a)[k];
+}
+__device__ __forceinline__ float add16(float s, const float4 (&c)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    s = s + c[k].x;
+    s = s + c[k].y;
+    s = s + c[k].z;
+    s = s + c[k].w;
+  }
+  return s;
+}
 __device__ __forceinline__ float chunk_chain(const float* a, int b0, int b1, float s) {
   int i = b0;
-  for (; i + 16 <= b1; i += 16) {
-    const float4 c0 = *reinterpret_cast<const float4*>(a + i);
-    const float4 c1 = *reinterpret_cast<const float4*>(a + i + 4);
-    const float4 c2 = *reinterpret_cast<const float4*>(a + i + 8);
-    const float4 c3 = *reinterpret_cast<const float4*>(a + i + 12);
-    s = s + c0.x; s = s + c0.y; s = s + c0.z; s = s + c0.w;
-    s = s + c1.x; s = s + c1.y; s = s + c1.z; s = s + c1.w;
-    s = s + c2.x; s = s + c2.y; s = s + c2.z; s = s + c2.w;
-    s = s + c3.x; s = s + c3.y; s = s + c3.z; s = s + c3.w;
+  float4 A[4], B[4];
+  if (i + 16 <= b1) load16(A, a + i);
+  for (; i + 32 <= b1; i += 32) {  // A holds [i, i+16)
+    load16(B, a + i + 16);
+    __builtin_amdgcn_sched_barrier(0);
+    s = add16(s, A);
+    if (i + 48 <= b1) load16(A, a + i + 32);
+    __builtin_amdgcn_sched_barrier(0);
+    s = add16(s, B);
+  }
+  if (i + 16 <= b1) {
+    s = add16(s, A);
+    i += 16;
   }
   for (; i < b1; ++i) s = s + a[i];
   return s;
@@ -752,6 +773,83 @@ __global__ void __launch_bounds__(256) k_rmsnorm(NormParams P) {
 
 // ------------------------------------------------------- attention block
 
+// out[d] chain of AV (internal/simd/c2_tensor_attn_gen.go:85-117):
+// acc = fma(p[i], V[i][d], acc) for i = 0 .. n-1 in order.  V sits in LDS
+// quad-major: vq[(i/4)*64 + d] holds V[4(i/4) .. 4(i/4)+3][d], so one
+// 16-byte read gives a lane four positions; p (LDS) is read as broadcast
+// 16-byte reads.  Sixteen positions per batch; the reads of the next batch
+// are issued before the FMAs of the current one.
+
+__device__ __forceinline__ float fma4(float acc, const float4& p, const f32x4_t& v) {
+  acc = __builtin_fmaf(p.x, v.x, acc);
+  acc = __builtin_fmaf(p.y, v.y, acc);
+  acc = __builtin_fmaf(p.z, v.z, acc);
+  acc = __builtin_fmaf(p.w, v.w, acc);
+  return acc;
+}
+
+// the last n % 16 positions, by quads (p readable to round_up(n, 4))
+template <typename PLOAD>
+__device__ __forceinline__ float av_tail_q(PLOAD pl, const f32x4_t* vq, int i, int n, int d, float acc) {
+  for (; i < n; i += 4) {
+    const f32x4_t v = vq[(i >> 2) * 64 + d];
+    const float4 p = pl(i);
+    acc = __builtin_fmaf(p.x, v.x, acc);
+    if (i + 1 < n) acc = __builtin_fmaf(p.y, v.y, acc);
+    if (i + 2 < n) acc = __builtin_fmaf(p.z, v.z, acc);
+    if (i + 3 < n) acc = __builtin_fmaf(p.w, v.w, acc);
+  }
+  return acc;
+}
+
+// Batches of sixteen: while two remain, load the second, run the first,
+// load the next (clamped, always issued), run the second; every load in
+// the loop is consumed on every path, so none is sunk into a branch.
+template <typename BLOAD>
+__device__ __forceinline__ float av_batches(BLOAD load, int nb, float acc) {
+  f32x4_t va[4], vb[4];
+  float4 pa[4], pb[4];
+  load(0, va, pa);
+  int b = 0;
+  for (; b + 2 <= nb; b += 2) {  // va/pa hold batch b
+    load(b + 1, vb, pb);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc = fma4(acc, pa[k], va[k]);
+    load(min(b + 2, nb - 1), va, pa);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc = fma4(acc, pb[k], vb[k]);
+  }
+  if (b < nb) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc = fma4(acc, pa[k], va[k]);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ float av_chain_q(const float* p, const f32x4_t* vq, int n, int d, float acc) {
+  const int nb = n >> 4;
+  const float4* p4 = reinterpret_cast<const float4*>(p);
+  if (nb > 0)
+    acc = av_batches(
+        [&](int b, f32x4_t(&v)[4], float4(&pp)[4]) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            v[k] = vq[(4 * b + k) * 64 + d];
+            pp[k] = p4[4 * b + k];
+          }
+        },
+        nb, acc);
+  return av_tail_q([&](int i) { return p4[i >> 2]; }, vq, nb * 16, n, d, acc);
+}
+
+// Quad qi of a head slot's V (positions 4qi..4qi+3, all dims, 1 KB):
+// lane l's 16 bytes are dim l.
+__device__ __forceinline__ f32x4_t vquad_load(const float* vslot, int qi) {
+  return reinterpret_cast<const f32x4_t*>(vslot)[(size_t)qi * 64 + (threadIdx.x & 63)];
+}
+
 // Score of one position (internal/simd/c2_tensor_attn_gen.go:18-50): two
 // 8-lane FMA accumulators over d = 0,16,32,48 (lanes l and 8+l), then
 // ((l0+l1)+(l2+l3))+((l4+l5)+(l6+l7)) of acc0+acc1, times scale.
@@ -789,14 +887,23 @@ __device__ __forceinline__ float attn_score(const float* q_s, const float4 (&kk4
 //   softmax with f64 exp and a sequential f32 sum (tensor/ops.go:317-339),
 //   and one FMA chain over positions per output dim
 //   (c2_tensor_attn_gen.go:85-117) with V staged through LDS.
-// Every load (q/k/v, RoPE row, the K row of position tid, the V rows of the
-// first ATT_CH positions) is issued at entry.
+// Every load (q/k/v, RoPE row, the K rows of positions tid and tid+256, the
+// V rows of the first ATT_CH positions) is issued at entry.  Past the first
+// chunk, waves 1..3 stage V chunk by chunk (three chunks in flight in
+// registers, two in LDS) while wave 0 runs the chains.
+template <int PER>
+struct VStage {
+  f32x4_t r[PER];
+};
+
 __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   constexpr int HD = 64;
-  constexpr int VPT = ATT_CH * HD / 4 / 256;  // staged float4 of V per thread
+  constexpr int NQ = ATT_CH / 4;    // quads (four V rows) per chunk
+  constexpr int VPT = NQ / 4;       // quads of chunk 0 per wave
+  constexpr int PER = (NQ + 2) / 3;  // quads per staging wave (waves 1..3)
   extern __shared__ __align__(16) unsigned char smem[];
-  float* vbuf = reinterpret_cast<float*>(smem);  // [ATT_CH][64]
-  float* sc = vbuf + ATT_CH * HD;                // [chain_lds_floats(max_ctx)]
+  f32x4_t* vbuf = reinterpret_cast<f32x4_t*>(smem);               // [2][NQ][64] quad-major
+  float* sc = reinterpret_cast<float*>(vbuf + 2 * NQ * HD);       // [chain_lds_floats(split)]
   __shared__ __align__(16) float qkv_s[3][HD];
   __shared__ float red_m[4];
   __shared__ float inv_slot;
@@ -808,10 +915,12 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   const int g = h / qpkv;
   const int pos = P.state->pos + ti;
   const int T = pos + 1;
-  const size_t head_stride = (size_t)P.max_ctx * HD;
+  const size_t head_stride = (size_t)kv_slot(P.max_ctx) * HD;
   float* kcache = P.kv + ((size_t)P.layer * P.n_kv_heads + g) * head_stride;
   float* vcache = P.kv + (((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * head_stride;
   const int plast = max(min(pos, P.max_ctx) - 1, 0);  // last stored position (clamp target)
+  const int qlast = plast >> 2;                        // its V quad
+  const int nch = (pos + ATT_CH - 1) / ATT_CH;         // V chunks of positions [0, pos)
 
   // ---- loads, in the order they are consumed
   // thread t < 192 holds element t%64 of q_h (t < 64), k_g, v_g
@@ -822,18 +931,20 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   const int rp = min(max(pos, 0), P.rope_len - 1);
   const float rcos = P.rope_cos[(size_t)rp * (HD / 2) + (tid & 31)];
   const float rsin = P.rope_sin[(size_t)rp * (HD / 2) + (tid & 31)];
-  float4 kreg[16];
+  issue_fence();  // q/k/v and the RoPE row are needed first: issue them first
+  float4 kreg[16], kreg2[16];
   {
     const float4* kr = reinterpret_cast<const float4*>(kcache + (size_t)min(tid, plast) * HD);
+    const float4* kr2 = reinterpret_cast<const float4*>(kcache + (size_t)min(tid + ATT_KPF, plast) * HD);
 #pragma unroll
     for (int i = 0; i < 16; ++i) kreg[i] = kr[i];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) kreg2[i] = kr2[i];
   }
+  const int wave = tid >> 6;
   f32x4_t vreg[VPT];  // native vectors: a float4 array copied whole is kept in scratch
 #pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int f = tid + 256 * i;  // float4 index within the chunk
-    vreg[i] = reinterpret_cast<const f32x4_t*>(vcache + (size_t)min(f >> 4, plast) * HD)[f & 15];
-  }
+  for (int i = 0; i < VPT; ++i) vreg[i] = vquad_load(vcache, min(wave + 4 * i, qlast));
   issue_fence();
 
   if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;
@@ -856,25 +967,37 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   // (a batch of query tokens has its K/V stored by a kernel before this one)
   if (P.store_kv && (h % qpkv) == 0 && tid < HD && pos < P.max_ctx) {
     kcache[(size_t)pos * HD + tid] = k_s[tid];
-    vcache[(size_t)pos * HD + tid] = v_s[tid];
+    vcache[vq_index(pos, tid)] = v_s[tid];
   }
   if (T > P.max_ctx) return;  // rejected on the host; kept as a guard
 
   // ---- scores; position pos uses this launch's k (not yet visible in the cache)
+  // (both prefetched rows are consumed on every path: a load left pending
+  // on one path would make the compiler wait for all later loads before
+  // reusing its registers)
+  const float4* ks4 = reinterpret_cast<const float4*>(k_s);
   float lmax = -__builtin_inff();
-  if (tid < T) {
+  {
     if (tid == pos) {
-      const float4* ks4 = reinterpret_cast<const float4*>(k_s);
 #pragma unroll
       for (int i = 0; i < 16; ++i) kreg[i] = ks4[i];
     }
     const float sco = attn_score(q_s, kreg, P.scale);
-    sc[tid] = sco;
-    lmax = (sco > lmax) ? sco : lmax;
+    if (tid < T) sc[tid] = sco;
+    lmax = (tid < T && sco > lmax) ? sco : lmax;
   }
-  for (int p = tid + ATT_KPF; p < T; p += ATT_KPF) {
-    const float4* kr = (p == pos) ? reinterpret_cast<const float4*>(k_s)
-                                  : reinterpret_cast<const float4*>(kcache + (size_t)p * HD);
+  {
+    const int p2 = tid + ATT_KPF;
+    if (p2 == pos) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) kreg2[i] = ks4[i];
+    }
+    const float sco = attn_score(q_s, kreg2, P.scale);
+    if (p2 < T) sc[p2] = sco;
+    lmax = (p2 < T && sco > lmax) ? sco : lmax;
+  }
+  for (int p = tid + 2 * ATT_KPF; p < T; p += ATT_KPF) {
+    const float4* kr = (p == pos) ? ks4 : reinterpret_cast<const float4*>(kcache + (size_t)p * HD);
     float4 kk4[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) kk4[i] = kr[i];
@@ -882,62 +1005,92 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
     sc[p] = sco;
     lmax = (sco > lmax) ? sco : lmax;
   }
-  // max: x[0] first, strict '>' (tensor/ops.go:321-326): the max of the
-  // non-NaN scores, or NaN when score[0] is NaN.
-  lmax = wave_max_dpp(lmax);
-  if ((tid & 63) == 0) red_m[tid >> 6] = lmax;
-  __syncthreads();
-  float mx = fmax_gt(fmax_gt(fmax_gt(red_m[0], red_m[1]), red_m[2]), red_m[3]);
-  if (sc[0] != sc[0]) mx = sc[0];
-  for (int p = tid; p < T; p += blockDim.x) sc[p] = (float)exp((double)(sc[p] - mx));
-  __syncthreads();
-  if (T <= 64 * SPEC_C) {
-    if (tid < 64) {
-      const float ssum = seq_sum_wave(sc, T);
+
+  // softmax, then V chunk 0 from registers into LDS buffer 0
+  auto softmax = [&]() {
+    // max: x[0] first, strict '>' (tensor/ops.go:321-326): the max of the
+    // non-NaN scores, or NaN when score[0] is NaN.
+    lmax = wave_max_dpp(lmax);
+    if ((tid & 63) == 0) red_m[tid >> 6] = lmax;
+    __syncthreads();
+    float mx = fmax_gt(fmax_gt(fmax_gt(red_m[0], red_m[1]), red_m[2]), red_m[3]);
+    if (sc[0] != sc[0]) mx = sc[0];
+    for (int p = tid; p < T; p += blockDim.x) sc[p] = (float)exp((double)(sc[p] - mx));
+    __syncthreads();
+    if (T <= 64 * SPEC_C) {
+      if (tid < 64) {
+        const float ssum = seq_sum_wave(sc, T);
+        if (tid == 0) inv_slot = 1.0f / ssum;
+      }
+    } else if (tid < 64) {
+      const float ssum = seq_sum_wave_n(sc, T);
       if (tid == 0) inv_slot = 1.0f / ssum;
     }
-  } else if (tid < 64) {
-    const float ssum = seq_sum_wave_n(sc, T);
-    if (tid == 0) inv_slot = 1.0f / ssum;
-  }
 #pragma unroll
-  for (int i = 0; i < VPT; ++i) reinterpret_cast<f32x4_t*>(vbuf)[tid + 256 * i] = vreg[i];
-  __syncthreads();
-  const float inv = inv_slot;
-  for (int p = tid; p < T; p += blockDim.x) sc[p] = sc[p] * inv;
-  __syncthreads();
+    for (int i = 0; i < VPT; ++i) vbuf[(wave + 4 * i) * HD + (tid & 63)] = vreg[i];
+    __syncthreads();
+    const float inv = inv_slot;
+    for (int p = tid; p < T; p += blockDim.x) sc[p] = sc[p] * inv;
+    __syncthreads();
+  };
 
-  // ---- AV: out[d] = fma chain over p of (prob[p], V[p][d]); V[pos] is v_s
+  // ---- AV: out[d] = fma chain over p of (prob[p], V[p][d]); V[pos] is v_s.
   float acc = 0.0f;
   const int d = tid & 63;
-  for (int p0 = 0; p0 < pos; p0 += ATT_CH) {
-    const int np = min(ATT_CH, pos - p0);
-    if (p0 > 0) {
-      __syncthreads();  // previous chunk consumed
+  if (nch <= 1) {
+    softmax();
+    if (tid < HD && nch == 1) acc = av_chain_q(sc, vbuf, pos, d, acc);
+  } else {
+    // Chunk c sits in LDS buffer c & 1; chunk c+1 waits in register set
+    // c % 3.  Chunks 1..3 start loading under the softmax.  Every thread
+    // issues the set loads (wave 0 duplicates wave 1's, unused) and the
+    // staging loop loads unconditionally (indices clamped): with no load
+    // on only one side of a branch the compiler's memory-counter waits
+    // keep three chunks in flight.
+    const int wp = (wave >= 1) ? wave - 1 : 0;  // staging wave index
+    auto load_set = [&](VStage<PER>& st, int c) {
 #pragma unroll
-      for (int i = 0; i < VPT; ++i) {
-        const int f = tid + 256 * i;
-        const int p = min(p0 + (f >> 4), plast);
-        reinterpret_cast<float4*>(vbuf)[f] = reinterpret_cast<const float4*>(vcache + (size_t)p * HD)[f & 15];
+      for (int k = 0; k < PER; ++k) st.r[k] = vquad_load(vcache, min(c * NQ + min(wp + 3 * k, NQ - 1), qlast));
+    };
+    auto store_set = [&](const VStage<PER>& st, int c) {
+#pragma unroll
+      for (int k = 0; k < PER; ++k)
+        if (wp + 3 * k < NQ) vbuf[((c & 1) * NQ + wp + 3 * k) * HD + (tid & 63)] = st.r[k];
+    };
+    VStage<PER> s0, s1, s2;
+    load_set(s0, 1);
+    load_set(s1, min(2, nch - 1));
+    load_set(s2, min(3, nch - 1));
+    softmax();
+    // both roles pass nch barriers, one per chunk; the staging loop runs
+    // whole trips of three unconditional steps, the remainder after it
+    if (tid >= 64) {
+      int c = 0;
+      for (; c + 3 <= nch; c += 3) {
+        store_set(s0, c + 1);
+        load_set(s0, min(c + 4, nch - 1));
+        __syncthreads();
+        store_set(s1, c + 2);
+        load_set(s1, min(c + 5, nch - 1));
+        __syncthreads();
+        store_set(s2, c + 3);
+        load_set(s2, min(c + 6, nch - 1));
+        __syncthreads();
       }
-      __syncthreads();
-    }
-    if (tid < HD) {
-      int p = 0;
-      for (; p + 16 <= np; p += 16) {
-        float vv[16];
-#pragma unroll
-        for (int k = 0; k < 16; ++k) vv[k] = vbuf[(p + k) * HD + d];
-        const float4 s0 = *reinterpret_cast<const float4*>(sc + p0 + p);
-        const float4 s1 = *reinterpret_cast<const float4*>(sc + p0 + p + 4);
-        const float4 s2 = *reinterpret_cast<const float4*>(sc + p0 + p + 8);
-        const float4 s3 = *reinterpret_cast<const float4*>(sc + p0 + p + 12);
-        const float ss[16] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w,
-                              s2.x, s2.y, s2.z, s2.w, s3.x, s3.y, s3.z, s3.w};
-#pragma unroll
-        for (int k = 0; k < 16; ++k) acc = __builtin_fmaf(ss[k], vv[k], acc);
+      if (c < nch) {
+        store_set(s0, c + 1);
+        __syncthreads();
       }
-      for (; p < np; ++p) acc = __builtin_fmaf(sc[p0 + p], vbuf[p * HD + d], acc);
+      if (c + 1 < nch) {
+        store_set(s1, c + 2);
+        __syncthreads();
+      }
+    } else {
+      for (int c = 0; c < nch; ++c) {
+        const int np = min(ATT_CH, pos - c * ATT_CH);
+        acc = av_chain_q(sc + c * ATT_CH, vbuf + (c & 1) * NQ * HD, np, d, acc);
+        __syncthreads();
+      }
     }
   }
   if (tid < HD) {
@@ -957,7 +1110,7 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
 //                   makes the max NaN, tensor/ops.go:321-326), f64 exp, the
 //                   sequential f32 sum (exact speculative form), p = e/sum;
 //   k_attn_av       per output dim the FMA chain over p = 0..pos in order,
-//                   run by wave 0 while waves 1..15 stage V rows and
+//                   run by wave 0 while waves 1..7 stage V quads and
 //                   probabilities through two LDS chunks.
 
 // In decode (store_kv) the workgroup whose block holds pos stores RoPE(k)
@@ -975,7 +1128,7 @@ __global__ void __launch_bounds__(256) k_attn_scores(AttnCoreParams P) {
   const int T = pos + 1;
   const int p0 = blockIdx.x * ATT_SB;
   if (p0 >= T) return;  // uniform: blocks past the context do nothing
-  const size_t head_stride = (size_t)P.max_ctx * HD;
+  const size_t head_stride = (size_t)kv_slot(P.max_ctx) * HD;
   float* kcache = P.kv + ((size_t)P.layer * P.n_kv_heads + g) * head_stride;
   float* vcache = P.kv + (((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * head_stride;
   const int p = p0 + tid;
@@ -1013,7 +1166,7 @@ __global__ void __launch_bounds__(256) k_attn_scores(AttnCoreParams P) {
   __syncthreads();
   if (P.store_kv && tid < HD && pos >= p0 && pos < p0 + ATT_SB && pos < P.max_ctx) {
     kcache[(size_t)pos * HD + tid] = ks[tid];
-    vcache[(size_t)pos * HD + tid] = vn;
+    vcache[vq_index(pos, tid)] = vn;
   }
   if (P.store_kv && p == pos) {
     const float4* ks4 = reinterpret_cast<const float4*>(ks);
@@ -1071,87 +1224,95 @@ __global__ void __launch_bounds__(1024) k_attn_softmax(AttnCoreParams P) {
   for (int p = tid; p < T; p += 1024) s[p] = e[p] * inv;
 }
 
-__global__ void __launch_bounds__(1024) k_attn_av(AttnCoreParams P) {
+// Staging of k_attn_av: chunk j of V quads and probabilities travels
+// global -> registers of set j % 3 -> LDS buffer j & 1 (a plain copy: the
+// cache is quad-major), so three chunks (~190 KB) are in flight while wave
+// 0 chains through the current one.
+template <int PER>
+struct AvStage {
+  f32x4_t r[PER];
+  f32x4_t p;
+};
+
+__global__ void __launch_bounds__(ATT_AV_THREADS) k_attn_av(AttnCoreParams P) {
   constexpr int HD = 64;
-  constexpr int NV4 = ATT_AV_CH * HD / 4;  // float4 of V per chunk
-  constexpr int NP4 = ATT_AV_CH / 4;       // float4 of probabilities per chunk
-  constexpr int NPROD = 1024 - 64;         // staging threads (waves 1..15)
-  constexpr int PER = (NV4 + NP4 + NPROD - 1) / NPROD;
+  constexpr int NQ = ATT_AV_CH / 4;             // quads per chunk (= float4 of probabilities)
+  constexpr int NPW = ATT_AV_THREADS / 64 - 1;  // staging waves
+  constexpr int PER = (NQ + NPW - 1) / NPW;     // quads per staging wave
+  static_assert(NQ == 64, "one probability float4 per lane of a staging wave");
   extern __shared__ __align__(16) unsigned char smem[];
-  float* vb = reinterpret_cast<float*>(smem);  // [2][ATT_AV_CH][64]
-  float* pb = vb + 2 * ATT_AV_CH * HD;         // [2][ATT_AV_CH]
+  f32x4_t* vb = reinterpret_cast<f32x4_t*>(smem);                 // [2][NQ][64] quad-major
+  float* pb = reinterpret_cast<float*>(vb + 2 * NQ * HD);         // [2][ATT_AV_CH]
   const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
   const int h = blockIdx.x, i = blockIdx.y;
   const int ti = P.tok0 + i;
   const int g = h / (P.n_heads / P.n_kv_heads);
   const int pos = P.state->pos + ti;
   const int T = pos + 1;
-  const float* vcache = P.kv + (((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * (size_t)P.max_ctx * HD;
+  const float* vcache = P.kv + (((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * (size_t)kv_slot(P.max_ctx) * HD;
   const float* s = P.sc + ((size_t)i * P.n_heads + h) * P.sc_ld;
   const int nch = (T + ATT_AV_CH - 1) / ATT_AV_CH;
-  const int j = tid - 64;
-  const int plast4 = (T - 1) & ~3;
-  f32x4_t r[PER];
-  // chunk c into registers: V rows c*CH.. (clamped to pos) and their
-  // probabilities (a float4 that starts before T stays inside the row)
-  auto load_chunk = [&](int c) {
-    const int base = c * ATT_AV_CH;
+  const int qlast = pos >> 2;
+  const int plast4 = (T - 1) & ~3;  // a float4 starting there stays inside the row
+  const int wp = wave - 1;
+  auto load_set = [&](AvStage<PER>& st, int c) {
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      const int f = j + NPROD * k;
-      const int pp = min(base + (f >> 4), T - 1);
-      const float* va = vcache + (size_t)pp * HD + 4 * (f & 15);
-      const float* sa = s + min(base + 4 * (f - NV4), plast4);
-      r[k] = *reinterpret_cast<const f32x4_t*>((f < NV4) ? va : sa);
-    }
+    for (int k = 0; k < PER; ++k) st.r[k] = vquad_load(vcache, min(c * NQ + min(wp + NPW * k, NQ - 1), qlast));
+    st.p = *reinterpret_cast<const f32x4_t*>(s + min(c * ATT_AV_CH + 4 * lane, plast4));
   };
-  auto store_chunk = [&](int c) {
-    float* vbb = vb + (c & 1) * ATT_AV_CH * HD;
-    float* pbb = pb + (c & 1) * ATT_AV_CH;
+  auto store_set = [&](const AvStage<PER>& st, int c) {
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      const int f = j + NPROD * k;
-      if (f < NV4)
-        reinterpret_cast<f32x4_t*>(vbb)[f] = r[k];
-      else if (f < NV4 + NP4)
-        reinterpret_cast<f32x4_t*>(pbb)[f - NV4] = r[k];
-    }
+    for (int k = 0; k < PER; ++k)
+      if (wp + NPW * k < NQ) vb[((c & 1) * NQ + wp + NPW * k) * HD + lane] = st.r[k];
+    if (wp == 0) reinterpret_cast<f32x4_t*>(pb + (c & 1) * ATT_AV_CH)[lane] = st.p;
   };
-  if (tid >= 64) {
-    load_chunk(0);
-    store_chunk(0);
-    if (nch > 1) load_chunk(1);
-  }
-  __syncthreads();
+  // Wave 0 chains; waves 1.. stage.  The two roles run separate loops with
+  // the same number of barriers, and the staging loop issues its loads
+  // unconditionally (chunk indices clamped), so the compiler's memory
+  // counter waits keep three chunks in flight.
   float acc = 0.0f;
-  const int d = tid & 63;
-  for (int c = 0; c < nch; ++c) {
-    if (tid < 64) {
-      const float* vbb = vb + (c & 1) * ATT_AV_CH * HD;
-      const float* pbb = pb + (c & 1) * ATT_AV_CH;
-      const int np = min(ATT_AV_CH, T - c * ATT_AV_CH);
-      int p = 0;
-      for (; p + 16 <= np; p += 16) {
-        float vv[16];
-#pragma unroll
-        for (int k = 0; k < 16; ++k) vv[k] = vbb[(p + k) * HD + d];
-        const float4 s0 = *reinterpret_cast<const float4*>(pbb + p);
-        const float4 s1 = *reinterpret_cast<const float4*>(pbb + p + 4);
-        const float4 s2 = *reinterpret_cast<const float4*>(pbb + p + 8);
-        const float4 s3 = *reinterpret_cast<const float4*>(pbb + p + 12);
-        const float ss[16] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w,
-                              s2.x, s2.y, s2.z, s2.w, s3.x, s3.y, s3.z, s3.w};
-#pragma unroll
-        for (int k = 0; k < 16; ++k) acc = __builtin_fmaf(ss[k], vv[k], acc);
-      }
-      for (; p < np; ++p) acc = __builtin_fmaf(pbb[p], vbb[p * HD + d], acc);
-    } else {
-      if (c + 1 < nch) store_chunk(c + 1);
-      if (c + 2 < nch) load_chunk(c + 2);
-    }
+  if (wave > 0) {
+    AvStage<PER> s0, s1, s2;
+    load_set(s0, 0);
+    load_set(s1, min(1, nch - 1));
+    load_set(s2, min(2, nch - 1));
+    store_set(s0, 0);
+    load_set(s0, min(3, nch - 1));
     __syncthreads();
+    // iteration c: chunk c+1 from its set ((c+1) % 3) to LDS, then that set
+    // reloads chunk c+4 (LDS buffer (c+1) & 1 is not the one being chained).
+    // Both roles pass nch barriers, one per chunk: whole trips of three
+    // unconditional steps, the remainder after the loop.
+    int c = 0;
+    for (; c + 3 <= nch; c += 3) {
+      store_set(s1, c + 1);
+      load_set(s1, min(c + 4, nch - 1));
+      __syncthreads();
+      store_set(s2, c + 2);
+      load_set(s2, min(c + 5, nch - 1));
+      __syncthreads();
+      store_set(s0, c + 3);
+      load_set(s0, min(c + 6, nch - 1));
+      __syncthreads();
+    }
+    if (c < nch) {
+      store_set(s1, c + 1);
+      __syncthreads();
+    }
+    if (c + 1 < nch) {
+      store_set(s2, c + 2);
+      __syncthreads();
+    }
+  } else {
+    __syncthreads();
+    for (int c = 0; c < nch; ++c) {
+      const int np = min(ATT_AV_CH, T - c * ATT_AV_CH);
+      acc = av_chain_q(pb + (c & 1) * ATT_AV_CH, vb + (c & 1) * NQ * HD, np, lane, acc);
+      __syncthreads();
+    }
+    P.out[(size_t)ti * P.out_ld + h * HD + lane] = acc;
   }
-  if (tid < 64) P.out[(size_t)ti * P.out_ld + h * HD + d] = acc;
 }
 
 // ------------------------------------------------------- prefill (A17)
@@ -1231,9 +1392,9 @@ __global__ void __launch_bounds__(64) k_pf_rope_store(PFRopeParams P) {
     const float x0 = kr[i], x1 = kr[i + 32];
     kv = (d < 32) ? (x0 * c) - (x1 * sn) : (x0 * sn) + (x1 * c);
   }
-  const size_t head_stride = (size_t)P.max_ctx * 64;
+  const size_t head_stride = (size_t)kv_slot(P.max_ctx) * 64;
   P.kv[((size_t)P.layer * P.n_kv_heads + g) * head_stride + (size_t)pos * 64 + d] = kv;
-  P.kv[(((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * head_stride + (size_t)pos * 64 + d] = vr[d];
+  P.kv[(((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * head_stride + vq_index(pos, d)] = vr[d];
 }
 
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
