@@ -9,10 +9,11 @@ steps are timed.  A step is the reference's generate-loop body
 (c2slm.go:153-222): vocab projection + repetition penalty 1.15 + argmax,
 then Forward(best, pos); only the chosen id crosses to the host each step.
 
-Prints one JSON line (see the contract in the repository's design notes):
-value = K / wall time of the K steps on one GPU, plus the roofline of the
-dominant kernel (the fused vocab projection) and the CPU baseline (the
-oracle on this host's cores, same workload).
+Prints one JSON line: value = K / wall time of the K steps on one GPU, plus
+the roofline of the dominant kernel (the fused vocab projection) and the CPU
+baseline (the oracle on this host's cores, same workload).  `extra` adds,
+outside the timed region, the batched prefill of a 512-token prompt and
+decode at long contexts (512 / 4096 / 32768 positions of N(0,1) K/V).
 """
 from __future__ import annotations
 
@@ -84,6 +85,55 @@ def copy_calibration(ctx, mib: int, reps: int = 5):
           f"({2 * (mib << 20) / (ms * 1e-3) / 1e9:.1f} GB/s read+write)", file=sys.stderr)
 
 
+def prefill_rate(ctx, desc, reps: int = 5):
+    """Batched prefill of a 512-token prompt of uniform random ids at position
+    0 (c2h_prefill: int8 MFMA GEMMs, causal attention, KV population), timed
+    on the host around the synchronous call; effective int8 rate of its
+    projections (floor(cols/256)*256 columns per row, as the reference's
+    K-quant rows are read)."""
+    m = 512
+    toks = np.random.default_rng(SEED + 1).integers(0, desc.n_vocab, m).astype(np.int32)
+    ctx.prefill(toks, 0, want_normx=False)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        ctx.prefill(toks, 0, want_normx=False)
+        ts.append(time.perf_counter() - t0)
+    E, F = desc.n_embd, desc.n_ff
+    KV = desc.n_kv_heads * desc.head_dim
+    ce, cf = E // 256 * 256, F // 256 * 256
+    macs = desc.n_layers * (E * ce + 2 * KV * ce + E * ce + 2 * F * ce + E * cf) * m
+    best = min(ts)
+    return {"tokens": m, "ms": round(best * 1e3, 3), "tok_s": round(m / best, 1),
+            "int8_macs": macs, "effective_int8_tops": round(2 * macs / best / 1e12, 2),
+            "ms_all": [round(t * 1e3, 3) for t in ts]}
+
+
+def long_context(gf, im_end, eos, lengths, steps: int = 16):
+    """Decode at long contexts (the KV cache pre-filled with N(0,1) keys and
+    values, token ids uniform): device-fed greedy steps whose last one
+    attends `n` positions, per n."""
+    from c2slm_amd import _lib as H
+    top = max(lengths)
+    desc = H.desc_from_gguf(gf, max_ctx=max(top, 1024))
+    ctx = H.Ctx(desc)
+    H.load_gguf_into(ctx, gf)
+    rng = np.random.default_rng(SEED + 2)
+    for which in (0, 1):
+        for layer in range(desc.n_layers):
+            for h in range(desc.n_kv_heads):
+                ctx.set_kv(which, layer, h, 0, rng.standard_normal((top, desc.head_dim), dtype=np.float32))
+    ctx.set_token_ids(0, rng.integers(0, desc.n_vocab, top).astype(np.int32))
+    out = {}
+    for n in lengths:
+        pos = n - steps
+        ctx.forward(11, pos - 1, want_normx=False)
+        ms = ctx.time_steps(pos, steps, PENALTY, im_end, eos)
+        out[str(n)] = {"ms_per_step": round(ms, 4), "tok_s": round(1000.0 / ms, 1)}
+    ctx.close()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -96,6 +146,13 @@ def main():
     ap.add_argument("--pipelined-iters", type=int, default=64, help="steps in the pipelined (no host sync) timing")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run plain device copies of this size (counter calibration under rocprofv3 --pmc)")
+    ap.add_argument("--long-context", default="512,4096,32768",
+                    help="context lengths of the long-context decode lines ('' to skip)")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill line")
+    ap.add_argument("--only", choices=["prefill", "long"], default=None,
+                    help="run just the prefill reps or just the long-context decode (profiler runs); "
+                         "prints their JSON object, not the bench line")
+    ap.add_argument("--prefill-reps", type=int, default=5)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported", file=sys.stderr)
@@ -109,12 +166,31 @@ def main():
     if path is None:
         tmpdir = tempfile.mkdtemp(prefix="c2slm_bench_")
         path = os.path.join(tmpdir, "qwen05b_synth.gguf")
+
+    def cleanup():
+        if tmpdir:
+            try:
+                os.remove(path)
+                os.rmdir(tmpdir)
+            except OSError:
+                pass
+
     synth_model(path)
     gf = G.GGUFFile(path)
+    _, im_end, eos = G.special_token_ids(gf)
+    if args.only == "long":
+        lengths = [int(x) for x in args.long_context.split(",") if x]
+        print(json.dumps({"long_context_decode": long_context(gf, im_end, eos, lengths)}))
+        cleanup()
+        return
     desc = H.desc_from_gguf(gf, max_ctx=args.max_ctx)
     ctx = H.Ctx(desc)
     H.load_gguf_into(ctx, gf)
-    _, im_end, eos = G.special_token_ids(gf)
+    if args.only == "prefill":
+        print(json.dumps({"prefill_512": prefill_rate(ctx, desc, args.prefill_reps)}))
+        ctx.close()
+        cleanup()
+        return
     rng = np.random.default_rng(SEED)
     prompt = rng.integers(0, desc.n_vocab, PROMPT_LEN).astype(np.int32)
 
@@ -143,6 +219,10 @@ def main():
     traffic = vocab_traffic()
     if args.copy_calib_mib:
         copy_calibration(ctx, args.copy_calib_mib)
+
+    prefill = None if args.no_prefill else prefill_rate(ctx, desc, args.prefill_reps)
+    lengths = [int(x) for x in args.long_context.split(",") if x]
+    longctx = long_context(gf, im_end, eos, lengths) if lengths else None
 
     base = None
     if not args.no_cpu_baseline:
@@ -173,16 +253,13 @@ def main():
         "cpu_baseline": base,
         "extra": {"vocab_ms_back_to_back": round(vocab_b2b_ms, 5),
                   "pipelined_ms_per_step": round(pipelined_ms, 4),
-                  "pipelined_tok_s": round(1000.0 / pipelined_ms, 1)},
+                  "pipelined_tok_s": round(1000.0 / pipelined_ms, 1),
+                  "prefill_512": prefill,
+                  "long_context_decode": longctx},
     }
     print(json.dumps(line))
     ctx.close()
-    if tmpdir:
-        try:
-            os.remove(path)
-            os.rmdir(tmpdir)
-        except OSError:
-            pass
+    cleanup()
 
 
 if __name__ == "__main__":
