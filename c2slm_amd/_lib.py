@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("C2H_LIB") or os.path.join(HERE, "libc2h.so")
 
 C2H_OK = 0
-F32, Q8_0, Q4_K, Q6_K = 0, 8, 12, 14
+F32, Q5_0, Q8_0, Q4_K, Q6_K = 0, 6, 8, 12, 14
 
 ROLE = dict(TOKEN_EMBD=0, OUTPUT=1, OUTPUT_NORM=2, ATTN_NORM=10, ATTN_Q=11, ATTN_Q_BIAS=12, ATTN_K=13,
             ATTN_K_BIAS=14, ATTN_V=15, ATTN_V_BIAS=16, ATTN_OUT=17, FFN_NORM=18, FFN_GATE=19, FFN_UP=20,

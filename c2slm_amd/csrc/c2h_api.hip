@@ -130,6 +130,7 @@ size_t native_row_bytes(int type, int64_t cols) {
     case C2H_Q4_K: return (size_t)nb_k(cols) * BS_Q4K;
     case C2H_Q6_K: return (size_t)nb_k(cols) * BS_Q6K;
     case C2H_Q8_0: return (size_t)nb8_of(cols) * BS_Q8_0;
+    case C2H_Q5_0: return (size_t)nb8_of(cols) * BS_Q5_0;
     case C2H_F32: return (size_t)cols * 4;
   }
   return 0;
@@ -145,6 +146,7 @@ void packed_parts(int type, int64_t rows, int64_t cols, size_t* qb, size_t* db) 
       *db = (size_t)rows * nb_k(cols) * 2;
       break;
     case C2H_Q8_0: *qb = (size_t)rows * q8_0_row_stride(nb8_of(cols)); break;
+    case C2H_Q5_0: *qb = (size_t)rows * nb8_of(cols) * 24; break;
   }
 }
 
@@ -175,6 +177,22 @@ void pack_host(int type, int64_t rows, int64_t cols, const uint8_t* src, uint8_t
           for (int i = 0; i < 4; ++i) qr[(bq * 8 + j) * 16 + bb * 4 + i] = blk[2 + j + 8 * i];
       }
     }
+  } else if (type == C2H_Q5_0) {
+    // per row: the 16 quant bytes of every block, then (qh u32, d u16, 0 u16) per block
+    (void)ddst;
+    const int nb8 = nb8_of(cols);
+    for (int64_t r = 0; r < rows; ++r) {
+      const uint8_t* row = src + (size_t)r * nb8 * BS_Q5_0;
+      uint8_t* qr = qdst + (size_t)r * nb8 * 24;
+      uint8_t* hr = qr + (size_t)nb8 * 16;
+      for (int b = 0; b < nb8; ++b) {
+        const uint8_t* blk = row + (size_t)b * BS_Q5_0;
+        memcpy(qr + (size_t)b * 16, blk + 6, 16);
+        memcpy(hr + (size_t)b * 8, blk + 2, 4);
+        memcpy(hr + (size_t)b * 8 + 4, blk, 2);
+        hr[b * 8 + 6] = hr[b * 8 + 7] = 0;
+      }
+    }
   }
 }
 
@@ -185,8 +203,8 @@ int check_type_shape(c2h_ctx* c, int type, int64_t rows, int64_t cols) {
     if (nb_k(cols) > LDS_Q8K_BLOCKS) return fail(c, C2H_ERR_UNSUPPORTED, "more than 16384 columns");
     return C2H_OK;
   }
-  if (type == C2H_Q8_0) {
-    if (cols < 32) return fail(c, C2H_ERR_UNSUPPORTED, "Q8_0 rows need at least 32 columns");
+  if (type == C2H_Q8_0 || type == C2H_Q5_0) {
+    if (cols < 32) return fail(c, C2H_ERR_UNSUPPORTED, "Q8_0/Q5_0 rows need at least 32 columns");
     return C2H_OK;
   }
   return fail(c, C2H_ERR_UNSUPPORTED, "ggml type %d is not run by this build", type);
@@ -249,8 +267,13 @@ void add_job(GemvParams& P, int* task, const Tensor& w, const Tensor* w2, int mo
     J.type2 = w.type;
   }
   J.rows = (int)w.rows;
-  J.nb = nb_k(w.cols);
-  J.rpw = 256 / (4 * J.nb);
+  if (w.type == C2H_Q5_0 || w.type == C2H_Q8_0) {  // k_gemv_f: 32-element blocks
+    J.nb = nb8_of(w.cols);
+    J.rpw = (w.type == C2H_Q5_0) ? std::max(1, 256 / J.nb) : 32;
+  } else {
+    J.nb = nb_k(w.cols);
+    J.rpw = 256 / (4 * J.nb);
+  }
   J.n_wg = (J.rows + J.rpw - 1) / J.rpw;
   J.wg_begin = *task;
   *task += J.n_wg;
@@ -292,6 +315,28 @@ GemvKernel gemv_row_kernel(int nb, int pro, int mode) {
     if (pro == PRO_ARGMAX_EMBED_NORM) return k_gemv_row<4, PRO_ARGMAX_EMBED_NORM, MODE_BIAS>;
   }
   return nullptr;
+}
+
+bool float_input(int type) { return type == C2H_Q5_0 || type == C2H_Q8_0; }
+
+// k_gemv_f instance for (prologue, mode); nullptr when none is built.
+GemvKernel gemv_f_kernel(int pro, int mode) {
+  if (mode == MODE_BIAS) {
+    if (pro == PRO_NORM) return k_gemv_f<PRO_NORM, MODE_BIAS>;
+    if (pro == PRO_EMBED_NORM) return k_gemv_f<PRO_EMBED_NORM, MODE_BIAS>;
+    if (pro == PRO_ARGMAX_EMBED_NORM) return k_gemv_f<PRO_ARGMAX_EMBED_NORM, MODE_BIAS>;
+  }
+  if (pro == PRO_NORM && mode == MODE_SWIGLU) return k_gemv_f<PRO_NORM, MODE_SWIGLU>;
+  if (pro == PRO_QUANT && mode == MODE_RESID) return k_gemv_f<PRO_QUANT, MODE_RESID>;
+  if (pro == PRO_QUANT && mode == MODE_STORE) return k_gemv_f<PRO_QUANT, MODE_STORE>;
+  return nullptr;
+}
+
+// A float-input launch over all its jobs (P.n_x = the input length).
+void launch_gemv_f(c2h_ctx* c, GemvParams& P, int total_wg) {
+  GemvKernel k = gemv_f_kernel(P.prologue, P.jobs[0].mode);
+  const size_t lds = (size_t)gemv_f_lds_floats(P.n_x) * sizeof(float);
+  hipLaunchKernelGGL(k, dim3(total_wg), dim3(256), lds, c->stream, P);
 }
 
 // A row-kernel launch over all its jobs (same width and mode); the norm
@@ -374,6 +419,44 @@ void enqueue_attn_long(c2h_ctx* c, const AttnCoreParams& A, int ntok) {
                      A);
 }
 
+// One projection of a layer (w2: the paired up matrix of SwiGLU).
+struct ProjJob {
+  const Tensor* w;
+  const Tensor* w2;
+  float* y;
+  const float* bias;
+};
+
+// The matrices of one projection group launched by input kind: Q4_K/Q6_K
+// read the Q8_K row of x (k_gemv_row), Q5_0/Q8_0 read x as f32 (k_gemv_f),
+// as engine/model.go:250-270 dispatches.  The first launch carries the
+// group's prologue; for layer 0's embed/argmax prologues a second launch
+// normalises the X the first one published.  x: the input (X for the norm
+// prologues), n_x its length.
+void launch_group(c2h_ctx* c, std::initializer_list<ProjJob> jobs, int pro, int mode, const float* x, int n_x,
+                  const float* norm_w) {
+  bool first = true;
+  for (int kind = 0; kind < 2; ++kind) {
+    GemvParams P = base_params(c);
+    int task = 0;
+    for (const ProjJob& j : jobs)
+      if (float_input(j.w->type) == (kind == 1)) add_job(P, &task, *j.w, j.w2, mode, j.y, j.bias, nullptr);
+    if (P.n_jobs == 0) continue;
+    P.prologue = (!first && (pro == PRO_EMBED_NORM || pro == PRO_ARGMAX_EMBED_NORM)) ? PRO_NORM : pro;
+    P.x = x;
+    P.x_out = c->X;
+    P.n_x = n_x;
+    P.n_x_lds = chain_lds_floats(n_x);
+    P.norm_w = norm_w;
+    P.nb_in = kind == 0 ? nb_k(n_x) : nb8_of(n_x);
+    if (kind == 0)
+      launch_gemv_row(c, P, task);
+    else
+      launch_gemv_f(c, P, task);
+    first = false;
+  }
+}
+
 // The 24-layer body of engine.Forward plus the final RMSNorm; layer 0 embeds
 // either state->token (forward) or the argmax of the vocab partials (step).
 // long_attn selects the long-context attention kernels.
@@ -382,21 +465,10 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax, bool long_attn) {
   const int E = D.n_embd;
   for (int l = 0; l < D.n_layers; ++l) {
     Layer& L = c->layers[l];
-    {  // q|k|v = W * Q8_K(RMSNorm(X)) + bias; layer 0 embeds the token first
-      GemvParams P = base_params(c);
-      P.prologue = (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM;
-      P.n_x = E;
-      P.n_x_lds = chain_lds_floats(E);
-      P.x = c->X;
-      P.x_out = c->X;
-      P.norm_w = L.attn_norm;
-      P.nb_in = nb_k(E);
-      int task = 0;
-      add_job(P, &task, L.wq, nullptr, MODE_BIAS, c->q, L.bq, nullptr);
-      add_job(P, &task, L.wk, nullptr, MODE_BIAS, c->k, L.bk, nullptr);
-      add_job(P, &task, L.wv, nullptr, MODE_BIAS, c->v, L.bv, nullptr);
-      launch_gemv_row(c, P, task);
-    }
+    // q|k|v = W * x(RMSNorm(X)) + bias; layer 0 embeds the token first
+    launch_group(c, {{&L.wq, nullptr, c->q, L.bq}, {&L.wk, nullptr, c->k, L.bk}, {&L.wv, nullptr, c->v, L.bv}},
+                 (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM, MODE_BIAS, c->X, E,
+                 L.attn_norm);
     {  // attention: RoPE, KV store, scores, softmax, AV
       AttnCoreParams A = attn_params(c, l);
       A.q = c->q;
@@ -409,36 +481,12 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax, bool long_attn) {
       else
         hipLaunchKernelGGL(k_attn_core, dim3(D.n_heads), dim3(256), c->attn_lds, c->stream, A);
     }
-    {  // attn_out: X += Wo * Q8_K(attn)
-      GemvParams P = base_params(c);
-      P.prologue = PRO_QUANT;
-      P.x = c->attn;
-      P.nb_in = nb_k(E);
-      int task = 0;
-      add_job(P, &task, L.wo, nullptr, MODE_RESID, c->X, nullptr, nullptr);
-      launch_gemv_row(c, P, task);
-    }
-    {  // ffn_in: h = SwiGLU(Wg * n, Wu * n), n = Q8_K(RMSNorm(X))
-      GemvParams P = base_params(c);
-      P.prologue = PRO_NORM;
-      P.n_x = E;
-      P.n_x_lds = chain_lds_floats(E);
-      P.x = c->X;
-      P.norm_w = L.ffn_norm;
-      P.nb_in = nb_k(E);
-      int task = 0;
-      add_job(P, &task, L.wg, &L.wu, MODE_SWIGLU, c->h, nullptr, nullptr);
-      launch_gemv_row(c, P, task);
-    }
-    {  // ffn_out: X += Wd * Q8_K(h)
-      GemvParams P = base_params(c);
-      P.prologue = PRO_QUANT;
-      P.x = c->h;
-      P.nb_in = nb_k(D.n_ff);
-      int task = 0;
-      add_job(P, &task, L.wd, nullptr, MODE_RESID, c->X, nullptr, nullptr);
-      launch_gemv_row(c, P, task);
-    }
+    // attn_out: X += Wo * x(attn)
+    launch_group(c, {{&L.wo, nullptr, c->X, nullptr}}, PRO_QUANT, MODE_RESID, c->attn, E, nullptr);
+    // ffn_in: h = SwiGLU(Wg * n, Wu * n), n = x(RMSNorm(X))
+    launch_group(c, {{&L.wg, &L.wu, c->h, nullptr}}, PRO_NORM, MODE_SWIGLU, c->X, E, L.ffn_norm);
+    // ffn_out: X += Wd * x(h)
+    launch_group(c, {{&L.wd, nullptr, c->X, nullptr}}, PRO_QUANT, MODE_RESID, c->h, D.n_ff, nullptr);
   }
   NormParams N;
   memset(&N, 0, sizeof(N));
@@ -472,11 +520,18 @@ int validate_model(c2h_ctx* c) {
     const Tensor* ts[] = {&L.wq, &L.wk, &L.wv, &L.wo, &L.wg, &L.wu, &L.wd};
     for (const Tensor* t : ts) {
       if (!t->present()) return fail(c, C2H_ERR_STATE, "layer %d projection missing", l);
-      if (t->type != C2H_Q4_K && t->type != C2H_Q6_K)
-        return fail(c, C2H_ERR_UNSUPPORTED, "layer %d: projections must be Q4_K or Q6_K", l);
+      if (t->type != C2H_Q4_K && t->type != C2H_Q6_K && t->type != C2H_Q5_0 && t->type != C2H_Q8_0)
+        return fail(c, C2H_ERR_UNSUPPORTED, "layer %d: projections must be Q4_K, Q6_K, Q5_0 or Q8_0", l);
+      const int64_t want_cols = (t == &L.wd) ? c->desc.n_ff : c->desc.n_embd;
+      if (t->cols != want_cols) return fail(c, C2H_ERR_INVALID, "layer %d: projection has %lld columns, expected %lld", l,
+                                            (long long)t->cols, (long long)want_cols);
+      if (t->type == C2H_Q8_0 && nb8_of(t->cols) > 32)
+        return fail(c, C2H_ERR_UNSUPPORTED, "layer %d: Q8_0 projections run up to 1024 columns", l);
     }
     if (L.wg.cols != L.wu.cols || L.wg.rows != L.wu.rows)
       return fail(c, C2H_ERR_INVALID, "layer %d gate/up shapes differ", l);
+    if (float_input(L.wg.type) != float_input(L.wu.type) || (float_input(L.wg.type) && L.wg.type != L.wu.type))
+      return fail(c, C2H_ERR_UNSUPPORTED, "layer %d: gate and up must both be Q5_0, both Q8_0, or both K-quants", l);
   }
   return C2H_OK;
 }
@@ -1015,6 +1070,10 @@ int c2h_prefill(c2h_ctx* c, const int32_t* tokens, int32_t n, int32_t pos0, floa
   if (pos0 < 0 || (int64_t)pos0 + n > c->desc.max_ctx)
     return fail(c, C2H_ERR_RANGE, "positions [%d, %d) outside [0, %d)", pos0, pos0 + n, c->desc.max_ctx);
   if (n == 0) return C2H_OK;
+  for (const Layer& L : c->layers)
+    for (const Tensor* t : {&L.wq, &L.wk, &L.wv, &L.wo, &L.wg, &L.wu, &L.wd})
+      if (float_input(t->type))
+        return fail(c, C2H_ERR_UNSUPPORTED, "batched prefill runs Q4_K/Q6_K projections; use c2h_forward per token");
   if ((rc = pf_alloc(c))) return rc;
   HIPCHK(c, hipStreamSynchronize(c->stream));
   c->ring_next = 0;
@@ -1214,6 +1273,18 @@ int c2h_gemv_dev(c2h_ctx* c, int32_t type, const void* w_packed, const void* xq,
     HIPCHK(c, hipGetLastError());
     return C2H_OK;
   }
+  if (type == C2H_Q5_0) {  // f32 x, k_gemv_f without a prologue
+    GemvParams P;
+    memset(&P, 0, sizeof(P));
+    P.prologue = PRO_QUANT;
+    P.x = reinterpret_cast<const float*>(xq);
+    P.n_x = nb8_of(cols) * 32;
+    int task = 0;
+    add_job(P, &task, t, nullptr, MODE_STORE, y, nullptr, nullptr);
+    launch_gemv_f(c, P, task);
+    HIPCHK(c, hipGetLastError());
+    return C2H_OK;
+  }
   GemvParams P;
   memset(&P, 0, sizeof(P));
   P.prologue = PRO_Q8K;
@@ -1272,7 +1343,7 @@ int c2h_gemv(c2h_ctx* c, int32_t type, const void* w, const void* xq, int32_t ro
   packed_parts(type, rows, cols, &qb, &db);
   pack_host(type, rows, cols, reinterpret_cast<const uint8_t*>(w), packed.data(), packed.data() + qb);
   (void)nbytes;
-  size_t xbytes = (type == C2H_Q8_0) ? (size_t)cols * 4 : (size_t)nb_k(cols) * BS_Q8K;
+  size_t xbytes = (type == C2H_Q8_0 || type == C2H_Q5_0) ? (size_t)cols * 4 : (size_t)nb_k(cols) * BS_Q8K;
   size_t isz = 0;
   if (isums_out && type == C2H_Q4_K) isz = (size_t)rows * nb_k(cols) * 8 * 4;
   if (isums_out && type == C2H_Q6_K) isz = (size_t)rows * nb_k(cols) * 4;

@@ -17,6 +17,7 @@ constexpr int BS_Q6K_PACKED = 208;  // ql|qh|scales; d lives in a separate fp16 
 constexpr int BS_Q8K = 292;
 constexpr int QK8_0 = 32;
 constexpr int BS_Q8_0 = 34;
+constexpr int BS_Q5_0 = 22;
 constexpr int MAX_Q8K_BLOCKS = 64;  // 16384 columns, the reference pool's Q8_K scratch (engine/pool.go:59)
 
 enum GgmlType : int { T_F32 = 0, T_Q5_0 = 6, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };

@@ -275,6 +275,14 @@ __global__ void k_quantize_q8k(const float* __restrict__ x, int nb, uint8_t* __r
 __global__ void k_gemv_q8k(GemvParams P);
 template <int NB, int PRO, int MODE>
 __global__ void k_gemv_row(GemvParams P);
+// Q5_0 / Q8_0 projections on f32 x (PRO_QUANT here means "x as is").
+template <int PRO, int MODE>
+__global__ void k_gemv_f(GemvParams P);
+constexpr int GF_XPAD = 36;  // floats per 32-element block of x in LDS (Q5_0 reads, bank spread)
+// Dynamic LDS of k_gemv_f, in floats: x padded per block | x permuted | norm chain.
+__host__ __device__ inline int gemv_f_lds_floats(int n_x) {
+  return (n_x / 32) * GF_XPAD + (n_x / 32) * 32 + chain_lds_floats(n_x);
+}
 __global__ void k_rmsnorm(NormParams P);
 __global__ void k_attn_core(AttnCoreParams P);
 __global__ void k_attn_scores(AttnCoreParams P);

@@ -755,6 +755,258 @@ __global__ void __launch_bounds__(256) k_gemv_q8k(GemvParams P) {
   }
 }
 
+// ------------------------------------------------ float-x GEMV (Q5_0, Q8_0)
+//
+// The projections the reference multiplies with f32 x (engine/model.go:
+// 250-270, engine/pool.go:122-154: no Q8_K), for the real-model formats:
+//   Q5_0 (tensor/ops.go:25-74 DotQ5_0): thread = (block b, row r), laid
+//     out block-major so the lanes of a wave share x reads; the block's
+//     products onto a zero start in the reference's order (q0*x[i], then
+//     q1*x[i+16], i = 0..15, each product rounded), term = d*sum with d
+//     decoded as tensor.FP16ToF32; one thread per row adds the terms in
+//     block order onto zero.
+//   Q8_0 (tensor/ops.go:77-95 -> internal/simd/c2_tensor_dot_q8_0_gen.go):
+//     8 lanes per row, the vocab kernel's arithmetic: lane j accumulates
+//     ((w[j]x[j] + w[j+8]x[j+8]) + (w[j+16]x[j+16] + w[j+24]x[j+24]))*d
+//     over the blocks, then (((a0+a1)+a2)+...)+a7.
+// Prologues as the row kernel's (norm, embed, argmax), or x as is; the
+// input lives in LDS twice: padded per block for Q5_0, permuted
+// [b][j][i] = x[32b + j + 8i] for Q8_0.  Epilogues bias / residual /
+// SwiGLU.  Device layouts: Q5_0 rows are [qs 16 B per block][qh u32, d u16,
+// 0 u16 per block]; Q8_0 rows as the vocab table.
+
+struct Q50Item {
+  uint4 qs;
+  uint2 hd;  // qh, d | 0
+};
+
+__device__ __forceinline__ Q50Item load_q50(const WeightRef& w, int nb, int row, int b) {
+  const uint8_t* rowp = w.q + (size_t)row * nb * 24;
+  Q50Item it;
+  it.qs = reinterpret_cast<const uint4*>(rowp)[b];
+  it.hd = reinterpret_cast<const uint2*>(rowp + (size_t)nb * 16)[b];
+  return it;
+}
+
+// d * (block sum) of one Q5_0 block against x[32b .. 32b+32) (padded LDS)
+__device__ __forceinline__ float q50_term(const Q50Item& it, const float* xb) {
+  float xv[32];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float4 t = reinterpret_cast<const float4*>(xb)[k];
+    xv[4 * k] = t.x;
+    xv[4 * k + 1] = t.y;
+    xv[4 * k + 2] = t.z;
+    xv[4 * k + 3] = t.w;
+  }
+  const uint32_t qw[4] = {it.qs.x, it.qs.y, it.qs.z, it.qs.w};
+  const uint32_t qh = it.hd.x;
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t byte = (qw[i >> 2] >> (8 * (i & 3))) & 0xffu;
+    const int q0 = (int)((byte & 15u) | (((qh >> i) & 1u) << 4)) - 16;
+    const int q1 = (int)((byte >> 4) | (((qh >> (i + 16)) & 1u) << 4)) - 16;
+    sum = sum + (float)q0 * xv[i];
+    sum = sum + (float)q1 * xv[i + 16];
+  }
+  return fp16_tensor(it.hd.y & 0xffffu) * sum;
+}
+
+struct Q80Row {
+  uint4 q[8];  // groups of four blocks, this lane's 16 bytes of each
+  uint4 d[4];  // the row's fp16 scales, eight per uint4
+};
+
+__device__ __forceinline__ Q80Row load_q80(const WeightRef& w, int nb8, int row, int j) {
+  const int nq = q8_0_nq(nb8), dpad = q8_0_dpad(nb8);
+  const uint8_t* rowp = w.q + (size_t)row * q8_0_row_stride(nb8);
+  const uint4* dvec = reinterpret_cast<const uint4*>(rowp);
+  const uint4* qrow = reinterpret_cast<const uint4*>(rowp + (size_t)dpad * 2);
+  Q80Row r;
+#pragma unroll
+  for (int bq = 0; bq < 8; ++bq) r.q[bq] = qrow[min(bq, nq - 1) * 8 + j];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) r.d[k] = dvec[min(k, dpad / 8 - 1)];
+  return r;
+}
+
+// lane j's accumulator over the row (nb8 <= 32 blocks), xp permuted
+__device__ __forceinline__ float q80_lane_acc(const Q80Row& w, const float* xp, int nb8, int j) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int bq = 0; bq < 8; ++bq) {
+    const uint4 dv = w.d[bq >> 1];
+    const uint32_t dlo = (bq & 1) ? dv.z : dv.x;
+    const uint32_t dhi = (bq & 1) ? dv.w : dv.y;
+    const uint32_t dd[4] = {dlo & 0xffffu, dlo >> 16, dhi & 0xffffu, dhi >> 16};
+    const uint32_t ww[4] = {w.q[bq].x, w.q[bq].y, w.q[bq].z, w.q[bq].w};
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) {
+      const int b = bq * 4 + bb;
+      if (b < nb8) {
+        const float dsc = q8_0_scale(dd[bb]);
+        const float4 xv = *reinterpret_cast<const float4*>(xp + (b * 8 + j) * 4);
+        const uint32_t q = ww[bb];
+        const float p0 = (float)(int8_t)(q & 0xff) * xv.x;
+        const float p1 = (float)(int8_t)((q >> 8) & 0xff) * xv.y;
+        const float p2 = (float)(int8_t)((q >> 16) & 0xff) * xv.z;
+        const float p3 = (float)(int8_t)(q >> 24) * xv.w;
+        acc = acc + ((p0 + p1) + (p2 + p3)) * dsc;
+      }
+    }
+  }
+  return acc;
+}
+
+// (((((((a0+a1)+a2)+a3)+a4)+a5)+a6)+a7) of the 8 lanes of a row, in every lane
+__device__ __forceinline__ float q80_row_sum(float acc) {
+  const int base = (threadIdx.x & 63) & ~7;
+  float tot = __shfl(acc, base);
+#pragma unroll
+  for (int k = 1; k < 8; ++k) tot = tot + __shfl(acc, base + k);
+  return tot;
+}
+
+template <int PRO, int MODE>
+__global__ void __launch_bounds__(256) k_gemv_f(GemvParams P) {
+  constexpr bool PAIRED = (MODE == MODE_SWIGLU);
+  constexpr bool NORM = (PRO == PRO_NORM || PRO == PRO_EMBED_NORM || PRO == PRO_ARGMAX_EMBED_NORM);
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nb8 = P.n_x / 32;
+  float* xq = reinterpret_cast<float*>(smem);  // [nb8][GF_XPAD]
+  float* xp = xq + nb8 * GF_XPAD;              // [nb8][8][4]
+  float* sq = xp + nb8 * 32;                   // norm chain scratch
+  __shared__ float terms[PAIRED ? 2 : 1][256];
+  __shared__ float inv_slot;
+  __shared__ ArgCand ared[4];
+
+  int ji = 0;
+#pragma unroll
+  for (int j = 1; j < MAX_JOBS; ++j)
+    if (j < P.n_jobs && (int)blockIdx.x >= P.jobs[j].wg_begin) ji = j;
+  const GemvJob& J = P.jobs[ji];
+  const int tid = threadIdx.x;
+  const bool q50 = (J.type == T_Q5_0);
+  const int R = J.rpw;
+  const int row0 = ((int)blockIdx.x - J.wg_begin) * R;
+  // Q5_0: thread = (block b, row r) block-major; Q8_0: row tid/8, lane tid%8
+  const int b5 = tid / R, r5 = tid - (tid / R) * R;
+  const int r_local = q50 ? r5 : (tid >> 3);
+  const int lane8 = tid & 7;
+  const int row = row0 + r_local;
+  const bool active = q50 ? (b5 < nb8 && row < J.rows) : (row < J.rows);
+  const int row_c = min(row, J.rows - 1);
+  const int out_row = min(row0 + min(tid, R - 1), J.rows - 1);
+
+  // ---- loads
+  float4 xa = make_float4(0.0f, 0.0f, 0.0f, 0.0f), nw = xa;
+  int tok = 0;
+  if (PRO == PRO_NORM) {
+    xa = load4(P.x, P.n_x);
+  } else if (NORM) {
+    tok = (PRO == PRO_ARGMAX_EMBED_NORM) ? reduce_argmax_partials(P.part_v, P.part_i, P.n_part, ared)
+                                         : P.state->token;
+    xa = embed4(P.emb, P.n_vocab, P.n_x, tok);
+  }
+  if (NORM) nw = load4(P.norm_w, P.n_x);
+  Q50Item w5a, w5b;
+  Q80Row w8a, w8b;
+  if (q50) {
+    w5a = load_q50(J.w, nb8, row_c, min(b5, nb8 - 1));
+    if (PAIRED) w5b = load_q50(J.w2, nb8, row_c, min(b5, nb8 - 1));
+  } else {
+    w8a = load_q80(J.w, nb8, row_c, lane8);
+    if (PAIRED) w8b = load_q80(J.w2, nb8, row_c, lane8);
+  }
+  float yres = 0.0f;
+  if (MODE == MODE_RESID) yres = J.y[out_row];
+  if (MODE == MODE_BIAS) yres = (J.bias ? J.bias : P.x)[J.bias ? out_row : 0];
+  issue_fence();
+
+  // ---- prologue: x (normalised or as is) into both LDS layouts
+  auto put = [&](int e, float v) {
+    const int b = e >> 5, kk = e & 31;
+    xq[b * GF_XPAD + kk] = v;
+    xp[(b * 8 + (kk & 7)) * 4 + (kk >> 3)] = v;
+  };
+  if (NORM) {
+    if (PRO != PRO_NORM && blockIdx.x == 0) {  // layer 0 publishes the embedded token
+      if (4 * tid < P.n_x) reinterpret_cast<float4*>(P.x_out)[tid] = xa;
+      if (tid == 0) {
+        const int pos = P.state->pos;
+        P.state->token = tok;
+        if (pos >= 0 && pos < P.max_ctx) P.token_ids[pos] = tok;
+      }
+    }
+    const float inv = rms_inv4(xa, P.n_x, P.eps, sq, &inv_slot);
+    const float4 xn = norm4(xa, inv, nw);
+    if (4 * tid < P.n_x) {
+      put(4 * tid, xn.x);
+      put(4 * tid + 1, xn.y);
+      put(4 * tid + 2, xn.z);
+      put(4 * tid + 3, xn.w);
+    }
+  } else {
+    for (int e = tid; e < nb8 * 32; e += 256) put(e, P.x[e]);
+  }
+  __syncthreads();
+
+  // ---- items and the per-row fold
+  float acc = 0.0f, acc2 = 0.0f;
+  if (q50) {
+    if (active) {
+      terms[0][r5 * nb8 + b5] = q50_term(w5a, xq + b5 * GF_XPAD);
+      if (PAIRED) terms[PAIRED ? 1 : 0][r5 * nb8 + b5] = q50_term(w5b, xq + b5 * GF_XPAD);
+    }
+    __syncthreads();
+    if (tid < R) {
+      for (int b = 0; b < nb8; ++b) acc = acc + terms[0][tid * nb8 + b];
+      if (PAIRED)
+        for (int b = 0; b < nb8; ++b) acc2 = acc2 + terms[PAIRED ? 1 : 0][tid * nb8 + b];
+    }
+  } else {
+    acc = q80_row_sum(q80_lane_acc(w8a, xp, nb8, lane8));
+    if (PAIRED) acc2 = q80_row_sum(q80_lane_acc(w8b, xp, nb8, lane8));
+    // the row's value moves to thread r_local (< R = 32) for the epilogue
+    if (lane8 == 0) {
+      terms[0][r_local] = acc;
+      if (PAIRED) terms[PAIRED ? 1 : 0][r_local] = acc2;
+    }
+    __syncthreads();
+    if (tid < R) {
+      acc = terms[0][tid];
+      if (PAIRED) acc2 = terms[PAIRED ? 1 : 0][tid];
+    }
+  }
+
+  // ---- epilogue
+  if (tid < R) {
+    const int r = row0 + tid;
+    if (r < J.rows) {
+      if (PAIRED) {
+        const int n8 = J.rows - (J.rows % 8);
+        J.y[r] = (r < n8) ? swiglu_poly(acc, acc2) : swiglu_tail(acc, acc2);
+      } else if (MODE == MODE_BIAS) {
+        J.y[r] = J.bias ? acc + yres : acc;
+      } else if (MODE == MODE_RESID) {
+        J.y[r] = yres + acc;
+      } else {
+        J.y[r] = acc;
+      }
+    }
+  }
+}
+
+#define C2H_GEMV_F(PRO_, MODE_) template __global__ void k_gemv_f<PRO_, MODE_>(GemvParams);
+C2H_GEMV_F(PRO_NORM, MODE_BIAS)
+C2H_GEMV_F(PRO_EMBED_NORM, MODE_BIAS)
+C2H_GEMV_F(PRO_ARGMAX_EMBED_NORM, MODE_BIAS)
+C2H_GEMV_F(PRO_NORM, MODE_SWIGLU)
+C2H_GEMV_F(PRO_QUANT, MODE_RESID)
+C2H_GEMV_F(PRO_QUANT, MODE_STORE)
+#undef C2H_GEMV_F
+
 // ------------------------------------------------------------- final norm
 
 // normX = RMSNorm(X) * output_norm (engine/forward.go:135); x and w are

@@ -271,7 +271,16 @@ def synth_q8_0(rng: np.random.Generator, n_blocks: int) -> np.ndarray:
     return blk.reshape(-1)
 
 
-SYNTH = {Q4_K: synth_q4_k, Q6_K: synth_q6_k, Q8_0: synth_q8_0}
+def synth_q5_0(rng: np.random.Generator, n_blocks: int) -> np.ndarray:
+    """Q5_0 blocks: d fp16 U(0,0.02), the 32 high bits and the 16 nibble
+    bytes uniform (5-bit quants U[0,31], offset -16)."""
+    blk = rng.integers(0, 256, size=(n_blocks, 22), dtype=np.uint8)
+    d = _fp16_bits(rng.uniform(0.0, 0.02, n_blocks))
+    blk[:, 0:2] = d.view(np.uint8).reshape(n_blocks, 2)
+    return blk.reshape(-1)
+
+
+SYNTH = {Q4_K: synth_q4_k, Q6_K: synth_q6_k, Q8_0: synth_q8_0, Q5_0: synth_q5_0}
 
 
 @dataclasses.dataclass
@@ -300,6 +309,12 @@ class ModelShape:
 
 
 QWEN05B = ModelShape()
+
+# The published Qwen2.5-0.5B-Instruct Q4_K_M file's format mix: 896-column
+# matrices cannot hold K-quant super-blocks whole, so q/k/o/gate/up are Q5_0
+# and attn_v is Q8_0; ffn_down (4864 columns) stays a K-quant
+# (tensor/real_tensor_test.go:26-33,55-66).
+QWEN05B_REAL_FORMATS = ModelShape(t_q=Q5_0, t_k=Q5_0, t_v=Q8_0, t_o=Q5_0, t_gate=Q5_0, t_up=Q5_0, t_down=Q6_K)
 
 # Qwen special ids (tokenizer/bpe_test.go:31-36)
 SPECIAL_TOKENS = {151643: "<|endoftext|>", 151644: "<|im_start|>", 151645: "<|im_end|>"}

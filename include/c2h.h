@@ -28,6 +28,7 @@ extern "C" {
 
 /* ggml tensor types (gguf/reader.go:21-37) */
 #define C2H_F32 0
+#define C2H_Q5_0 6
 #define C2H_Q8_0 8
 #define C2H_Q4_K 12
 #define C2H_Q6_K 14
@@ -92,8 +93,10 @@ const char* c2h_last_error(const c2h_ctx* ctx);
  * is borrowed for the call only.  Quantized rows use the reference's row
  * stride (cols/QK)*blockSize (tensor/ops.go:26,78,121,183), so a 896-wide
  * K-quant row covers 3 super-blocks exactly as the reference reads it;
- * `bytes` must cover rows*stride.  Types: Q4_K/Q6_K projections, Q8_0
- * embedding/output, F32 norms and biases. */
+ * `bytes` must cover rows*stride.  Types: Q4_K/Q6_K/Q5_0/Q8_0 projections
+ * (Q4_K/Q6_K multiply a Q8_K row, Q5_0/Q8_0 the f32 input, as
+ * engine/model.go:250-270 dispatches; Q8_0 projections up to 1024 columns),
+ * Q8_0 embedding/output, F32 norms and biases. */
 int c2h_upload_tensor(c2h_ctx* ctx, int32_t layer, int32_t role, int32_t ggml_type, int64_t rows, int64_t cols,
                       const void* host, size_t bytes);
 
@@ -170,9 +173,10 @@ int c2h_set_kv(c2h_ctx* ctx, int32_t which, int32_t layer, int32_t kv_head, int3
  * 292 bytes (f32 d | int8 qs[256] | int16 bsums[16]) from host x. */
 int c2h_quantize_q8k(c2h_ctx* ctx, const float* x, int32_t cols, void* q8k_out);
 
-/* tensor.GEMVQ4_K_Q8_K / GEMVQ6_K_Q8_K / GEMVQ8_0 (tensor/ops.go:77-203)
- * on host buffers.  w is the reference's native layout (row stride as
- * above); xq is the Q8_K row for Q4_K/Q6_K and the f32 vector for Q8_0.
+/* tensor.GEMVQ4_K_Q8_K / GEMVQ6_K_Q8_K / GEMVQ8_0 / GEMVQ5_0
+ * (tensor/ops.go:25-203) on host buffers.  w is the reference's native
+ * layout (row stride as above); xq is the Q8_K row for Q4_K/Q6_K and the
+ * f32 vector for Q8_0 and Q5_0.
  * isums_out (nullable, K-quants only) receives the integer sums: Q4_K 8 per
  * (row, super-block), the 32-element sums in q8 order; Q6_K 1 per
  * (row, super-block), the scaled super-block sum. */

@@ -37,6 +37,34 @@ def run_ref_dequant(name: str, block: bytes, dense=None):
     return raw[:256], raw[256]
 
 
+def run_ref_q5_0(block: bytes) -> np.ndarray:
+    """The 32 floats oracle/_ref/q5_0 writes for one 22-byte block (driven as
+    tensor/oracle_c_test.go:104-136 drives it: block file in, floats out)."""
+    with tempfile.TemporaryDirectory() as td:
+        fin = os.path.join(td, "in.bin")
+        fo = os.path.join(td, "out.bin")
+        with open(fin, "wb") as f:
+            f.write(bytes(block))
+        subprocess.run([os.path.join(REF_DIR, "q5_0"), fin, fo], check=True, capture_output=True)
+        return np.fromfile(fo, dtype="<f4")[:32]
+
+
+def dequant_q5_0_f64(blocks: np.ndarray) -> np.ndarray:
+    """float64 dequantisation of Q5_0 blocks [n,22] -> [n,32] (layout of
+    tensor/oracle_c_test.go:51-72)."""
+    blocks = np.asarray(blocks, np.uint8).reshape(-1, 22)
+    d = blocks[:, 0:2].copy().view("<f2")[:, 0].astype(np.float64)
+    qh = blocks[:, 2:6].copy().view("<u4")[:, 0].astype(np.int64)
+    qs = blocks[:, 6:22].astype(np.int64)
+    out = np.zeros((len(blocks), 32), np.float64)
+    for j in range(16):
+        h0 = (qh >> j) & 1
+        h1 = (qh >> (j + 16)) & 1
+        out[:, j] = d * (((qs[:, j] & 15) | (h0 << 4)) - 16)
+        out[:, j + 16] = d * (((qs[:, j] >> 4) | (h1 << 4)) - 16)
+    return out
+
+
 def fp16(b0, b1):
     return np.frombuffer(bytes([b0, b1]), dtype="<f2")[0].astype(np.float64)
 

@@ -142,3 +142,32 @@ def test_gemv_q8_0_order_known_answers(ctx):
     cases.append((x, big))
     for x, want in cases:
         assert ctx.gemv(H.Q8_0, one, x, 1, 96)[0] == want
+
+
+@pytest.mark.parametrize("rows,cols", [(896, 896), (128, 896), (4864, 896), (896, 4864), (9, 64)])
+def test_gemv_q5_0_bitexact(ctx, rows, cols):
+    # tensor/ops.go:25-74 on f32 x (the real-model format of 896-wide matrices)
+    rng = np.random.default_rng(rows + cols)
+    w = G.synth_q5_0(rng, rows * (cols // 32))
+    x = rng.normal(size=cols).astype(np.float32)
+    got = ctx.gemv(H.Q5_0, w, x, rows, cols)
+    want = O.gemv(w, G.Q5_0, rows, cols, x=x)
+    assert np.array_equal(bits(got), bits(want))
+
+
+def test_gemv_q5_0_order_known_answers(ctx):
+    from tests.test_oracle import q5_0_block
+    ones = q5_0_block(0x3C00, 0xFFFFFFFF, [0x11] * 16)
+    big = np.float32(2 ** 24)
+    cases = [([0, 16, 1], [1, big, 1], big), ([0, 1, 17], [big, 3, -1], big + 4)]
+    for idx, vals, want in cases:
+        x = np.zeros(32, np.float32)
+        x[idx] = vals
+        assert ctx.gemv(H.Q5_0, ones, x, 1, 32)[0] == want
+    qs = [0x11] * 16
+    qs[0] = 0x3D
+    blk = q5_0_block(0x3C00, 0xFFFFFFFE, qs)
+    x = np.zeros(32, np.float32)
+    x[0] = 1.0
+    x[16] = np.float32(1 + 2 ** -23)
+    assert ctx.gemv(H.Q5_0, blk, x, 1, 32)[0] == np.float32(2.0 ** -21)

@@ -386,6 +386,90 @@ def test_q8_0_reference_fixture_vs_float64():
     assert abs(got - want) <= 1e-5 * max(1.0, abs(want))
 
 
+# ----------------------------------------------------------------- Q5_0
+
+
+def q5_0_block(d_bits: int, qh: int, qs) -> np.ndarray:
+    blk = np.zeros(22, np.uint8)
+    blk[0:2] = [d_bits & 0xFF, d_bits >> 8]
+    blk[2:6] = np.frombuffer(np.uint32(qh).tobytes(), np.uint8)
+    blk[6:22] = np.asarray(qs, np.uint8)
+    return blk
+
+
+def dot_q5_0(w, x):
+    w = np.ascontiguousarray(w, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    return L.orc_dot_q5_0(O.ptr(w, U8P), O.ptr(x, F32P), len(x))
+
+
+@pytest.mark.skipif(not R.ref_available("q5_0"), reason="oracle/_ref not built (needs the reference checkout)")
+def test_q5_0_unit_vectors_vs_reference_c_oracle():
+    # the reference's own fixture (tensor/oracle_c_test.go:118-127), hostile
+    # byte patterns and random blocks, each element through a unit vector
+    rng = np.random.default_rng(50)
+    blocks = [q5_0_block(0x3C00, 0xAAAAAAAA, [(i * 17) & 0xFF for i in range(16)])]
+    for val in (0x00, 0xFF, 0xAA, 0x55):
+        blocks.append(q5_0_block(0x3C00, int.from_bytes(bytes([val] * 4), "little"), [val] * 16))
+    for _ in range(4):
+        b = rng.integers(0, 256, 22, dtype=np.uint8)
+        b[0:2] = np.frombuffer(np.float16(rng.uniform(-2, 2)).tobytes(), np.uint8)
+        blocks.append(b)
+    for blk in blocks:
+        want = R.run_ref_q5_0(blk.tobytes())
+        for i in range(32):
+            x = np.zeros(32, np.float32)
+            x[i] = 1.0
+            got = dot_q5_0(blk, x)
+            assert got == float(want[i]), (i, got, want[i])
+
+
+def test_q5_0_summation_order_known_answers():
+    one = 0x3C00  # d = 1.0
+    # every quant 1: nibbles 1 with the high bit set ((1 | 16) - 16)
+    ones = q5_0_block(one, 0xFFFFFFFF, [0x11] * 16)
+    big = float(2 ** 24)
+    # interleaved i, i+16 (not i = 0..15 then 16..31): x0=1, x16=2^24, x1=1:
+    # ((1 + 2^24) -> 2^24) + 1 -> 2^24; the blocked order would give 2^24+2
+    x = np.zeros(32, np.float32)
+    x[[0, 16, 1]] = [1, big, 1]
+    assert dot_q5_0(ones, x) == big
+    # q0*x[i] before q1*x[i+16]: x0=2^24, x1=3, x17=-1:
+    # ((2^24 + 3) -> 2^24+4) - 1 -> 2^24+4 (tie to even); q1 first: 2^24+2
+    x = np.zeros(32, np.float32)
+    x[[0, 1, 17]] = [big, 3, -1]
+    assert dot_q5_0(ones, x) == big + 4
+    # products rounded before the add (no FMA): q0 = -3 at x0 = 1, q1 = 3 at
+    # x16 = 1 + 2^-23: -3 + round(3 + 3*2^-23) = -3 + (3 + 2^-21) = 2^-21
+    # (a fused multiply-add would give 3*2^-23)
+    qs = [0x11] * 16
+    qs[0] = 0x3D  # low nibble 13 (high bit 0) -> -3, high nibble 3 (high bit 1) -> 3
+    blk = q5_0_block(one, 0xFFFFFFFE, qs)
+    x = np.zeros(32, np.float32)
+    x[0] = 1.0
+    x[16] = np.float32(1 + 2 ** -23)
+    assert dot_q5_0(blk, x) == 2.0 ** -21
+    # the block totals add in block order onto zero: 2^24, 1, 1 -> 2^24
+    three = np.concatenate([ones] * 3)
+    x = np.zeros(96, np.float32)
+    x[[0, 32, 64]] = [big, 1, 1]
+    assert dot_q5_0(three, x) == big
+
+
+def test_q5_0_gemv_vs_float64_dequant():
+    rng = np.random.default_rng(51)
+    from c2slm_amd import gguf as G
+    for rows, cols in [(32, 896), (8, 4864)]:
+        nb = cols // 32
+        w = G.synth_q5_0(rng, rows * nb)
+        x = rng.normal(size=cols).astype(np.float32)
+        y = O.gemv(w, G.Q5_0, rows, cols, x=x)
+        wd = R.dequant_q5_0_f64(w).reshape(rows, cols)
+        want = wd @ x.astype(np.float64)
+        scale = np.abs(wd).sum(1) * np.abs(x).max()
+        assert np.all(np.abs(y - want) <= 1e-5 * scale), (rows, cols)
+
+
 # ----------------------------------------------------------- small ops
 
 
