@@ -83,6 +83,7 @@ struct c2h_ctx {
     bool ready = false;
     float *X = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
     float *g = nullptr, *u = nullptr, *h = nullptr;
+    float* xn = nullptr;  // normalised rows as f32 (Q5_0 / Q8_0 projections)
     int8_t* q8 = nullptr;
     float* q8d = nullptr;
     int32_t* q8bs = nullptr;
@@ -883,6 +884,7 @@ int pf_alloc(c2h_ctx* c) {
   if ((rc = dalloc(c, &p.X, M * E * 4)) || (rc = dalloc(c, &p.q, M * E * 4)) || (rc = dalloc(c, &p.k, M * KV * 4)) ||
       (rc = dalloc(c, &p.v, M * KV * 4)) || (rc = dalloc(c, &p.attn, M * E * 4)) ||
       (rc = dalloc(c, &p.g, M * F * 4)) || (rc = dalloc(c, &p.u, M * F * 4)) || (rc = dalloc(c, &p.h, M * F * 4)) ||
+      (rc = dalloc(c, &p.xn, M * E * 4)) ||
       (rc = dalloc(c, &p.q8, M * p.nbs * QK_K)) || (rc = dalloc(c, &p.q8d, M * p.nbs * 4)) ||
       (rc = dalloc(c, &p.q8bs, M * p.nbs * 16 * 4)) || (rc = dalloc(c, &p.tok, M * 4)))
     return rc;
@@ -896,11 +898,12 @@ PFGemmKernel pf_gemm_kernel(int type, int mode) {
   return mode == MODE_RESID ? k_pf_gemm<T_Q6_K, MODE_RESID> : k_pf_gemm<T_Q6_K, MODE_BIAS>;
 }
 
-// y[t][r] (=|+=) W * q8[t] for the given matrices: one launch per weight
-// type, the matrices of one type as jobs of that launch.
+// y[t][r] (=|+=) W * x[t] for the given matrices: Q4_K / Q6_K on the
+// Q8_K rows (one MFMA launch per type), Q5_0 / Q8_0 on the f32 rows xf
+// (one k_pf_gemm_f launch), as engine/model.go:250-270 dispatches.
 void pf_gemm(c2h_ctx* c, int m, int m_pad, int nb, int mode, std::initializer_list<const Tensor*> ws,
              std::initializer_list<float*> ys, std::initializer_list<const float*> biases,
-             std::initializer_list<int> ldys) {
+             std::initializer_list<int> ldys, const float* xf, int ldxf, int n_x) {
   std::vector<const Tensor*> W(ws);
   std::vector<float*> Y(ys);
   std::vector<const float*> B(biases);
@@ -927,6 +930,33 @@ void pf_gemm(c2h_ctx* c, int m, int m_pad, int nb, int mode, std::initializer_li
     }
     if (P.n_jobs == 0) continue;
     hipLaunchKernelGGL(pf_gemm_kernel(type, mode), dim3(tiles, m_pad / PF_TILE), dim3(256), 0, c->stream, P);
+  }
+  PFGemmFParams F;
+  memset(&F, 0, sizeof(F));
+  F.x = xf;
+  F.ldx = ldxf;
+  F.n_x = n_x;
+  F.m = m;
+  int tiles = 0;
+  const int nb8 = n_x / 32;
+  for (size_t i = 0; i < W.size(); ++i) {
+    if (!float_input(W[i]->type)) continue;
+    PFJob& J = F.jobs[F.n_jobs++];
+    J.w = W[i]->ref();
+    J.type = W[i]->type;
+    J.rows = (int)W[i]->rows;
+    J.tile_begin = tiles;
+    const int R = (J.type == C2H_Q5_0) ? std::max(1, 256 / nb8) : 32;
+    tiles += (J.rows + R - 1) / R;
+    J.mode = mode;
+    J.y = Y[i];
+    J.ldy = L[i];
+    J.bias = B[i];
+  }
+  if (F.n_jobs) {
+    const size_t lds = (size_t)(nb8 * GF_XPAD + nb8 * 32) * sizeof(float);
+    auto k = (mode == MODE_RESID) ? k_pf_gemm_f<MODE_RESID> : k_pf_gemm_f<MODE_BIAS>;
+    hipLaunchKernelGGL(k, dim3(tiles, (m + PF_FT - 1) / PF_FT), dim3(256), lds, c->stream, F);
   }
 }
 
@@ -977,10 +1007,11 @@ int pf_pass(c2h_ctx* c, const int32_t* tokens, int m, int pos0) {
       N.m = m;
       N.nb = nb_k(E);
       N.out = q8;
+      N.xn = p.xn;
       hipLaunchKernelGGL(pf_norm_kernel(nb_k(E)), dim3(m_pad), dim3(256), norm_lds, c->stream, N);
     }
     pf_gemm(c, m, m_pad, nb_k(E), MODE_BIAS, {&L.wq, &L.wk, &L.wv}, {p.q, p.k, p.v}, {L.bq, L.bk, L.bv},
-            {E, KV, KV});
+            {E, KV, KV}, p.xn, E, E);
     {
       PFRopeParams R;
       memset(&R, 0, sizeof(R));
@@ -1023,7 +1054,7 @@ int pf_pass(c2h_ctx* c, const int32_t* tokens, int m, int pos0) {
       PFQuantParams Q{p.attn, E, m, q8};
       hipLaunchKernelGGL(pf_quant_kernel(nb_k(E)), dim3(m_pad), dim3(256), 0, c->stream, Q);
     }
-    pf_gemm(c, m, m_pad, nb_k(E), MODE_RESID, {&L.wo}, {p.X}, {nullptr}, {E});
+    pf_gemm(c, m, m_pad, nb_k(E), MODE_RESID, {&L.wo}, {p.X}, {nullptr}, {E}, p.attn, E, E);
     {
       PFNormParams N;
       memset(&N, 0, sizeof(N));
@@ -1034,15 +1065,16 @@ int pf_pass(c2h_ctx* c, const int32_t* tokens, int m, int pos0) {
       N.m = m;
       N.nb = nb_k(E);
       N.out = q8;
+      N.xn = p.xn;
       hipLaunchKernelGGL(pf_norm_kernel(nb_k(E)), dim3(m_pad), dim3(256), norm_lds, c->stream, N);
     }
-    pf_gemm(c, m, m_pad, nb_k(E), MODE_BIAS, {&L.wg, &L.wu}, {p.g, p.u}, {nullptr, nullptr}, {F, F});
+    pf_gemm(c, m, m_pad, nb_k(E), MODE_BIAS, {&L.wg, &L.wu}, {p.g, p.u}, {nullptr, nullptr}, {F, F}, p.xn, E, E);
     hipLaunchKernelGGL(k_pf_swiglu, dim3((F + 255) / 256, m), dim3(256), 0, c->stream, p.g, p.u, p.h, F, m);
     {
       PFQuantParams Q{p.h, F, m, q8};
       hipLaunchKernelGGL(pf_quant_kernel(nb_k(F)), dim3(m_pad), dim3(256), 0, c->stream, Q);
     }
-    pf_gemm(c, m, m_pad, nb_k(F), MODE_RESID, {&L.wd}, {p.X}, {nullptr}, {E});
+    pf_gemm(c, m, m_pad, nb_k(F), MODE_RESID, {&L.wd}, {p.X}, {nullptr}, {E}, p.h, F, F);
   }
   // normX of the last token (engine/forward.go:135)
   NormParams N;
@@ -1070,10 +1102,6 @@ int c2h_prefill(c2h_ctx* c, const int32_t* tokens, int32_t n, int32_t pos0, floa
   if (pos0 < 0 || (int64_t)pos0 + n > c->desc.max_ctx)
     return fail(c, C2H_ERR_RANGE, "positions [%d, %d) outside [0, %d)", pos0, pos0 + n, c->desc.max_ctx);
   if (n == 0) return C2H_OK;
-  for (const Layer& L : c->layers)
-    for (const Tensor* t : {&L.wq, &L.wk, &L.wv, &L.wo, &L.wg, &L.wu, &L.wd})
-      if (float_input(t->type))
-        return fail(c, C2H_ERR_UNSUPPORTED, "batched prefill runs Q4_K/Q6_K projections; use c2h_forward per token");
   if ((rc = pf_alloc(c))) return rc;
   HIPCHK(c, hipStreamSynchronize(c->stream));
   c->ring_next = 0;

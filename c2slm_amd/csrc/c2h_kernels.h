@@ -211,6 +211,7 @@ struct PFNormParams {
   int m;
   int nb;  // floor(n_x/256) blocks quantised
   PFQ8 out;
+  float* xn;  // optional: the normalised rows [m_pad][n_x] as f32
 };
 
 // Per token: Q8_K of x[t][0 .. nb*256).
@@ -236,6 +237,19 @@ struct PFGemmParams {
   PFQ8 in;
   int nb;  // super-blocks per row
   int m;   // valid tokens
+  int n_jobs;
+  PFJob jobs[3];
+};
+
+// Q5_0 / Q8_0 jobs of a batch on f32 rows x[t*ldx .. + n_x); grid (row
+// tiles of the jobs, ceil(m / PF_FT)); tile_begin counts row tiles of
+// max(1, 256/(n_x/32)) rows (Q5_0) or 32 rows (Q8_0).
+constexpr int PF_FT = 16;  // tokens per k_pf_gemm_f workgroup
+struct PFGemmFParams {
+  const float* x;
+  int ldx;
+  int n_x;
+  int m;
   int n_jobs;
   PFJob jobs[3];
 };
@@ -294,6 +308,8 @@ template <int NB>
 __global__ void k_pf_quant(PFQuantParams P);
 template <int TYPE, int MODE>
 __global__ void k_pf_gemm(PFGemmParams P);
+template <int MODE>
+__global__ void k_pf_gemm_f(PFGemmFParams P);
 __global__ void k_pf_rope_store(PFRopeParams P);
 __global__ void k_pf_swiglu(const float* gate, const float* up, float* h, int n, int m);
 __global__ void k_vocab(VocabParams P);

@@ -1609,7 +1609,10 @@ __global__ void __launch_bounds__(256) k_pf_norm_quant(PFNormParams P) {
   if (P.embed && 4 * tid < P.n_x) reinterpret_cast<float4*>(P.X + (size_t)t * P.n_x)[tid] = x;
   const float inv = rms_inv4(x, P.n_x, P.eps, sq, &inv_slot);
   const int wave = tid >> 6;
-  if (wave < NB) quantize_wave(norm4(x, inv, w), wave, s);
+  const float4 xn = norm4(x, inv, w);
+  // the f32 row too, for the projections that read x as is (Q5_0, Q8_0)
+  if (P.xn && 4 * tid < P.n_x) reinterpret_cast<float4*>(P.xn + (size_t)t * P.n_x)[tid] = xn;
+  if (wave < NB) quantize_wave(xn, wave, s);
   __syncthreads();
   store_q8_row<NB>(s, P.out, t);
 }
@@ -1628,6 +1631,75 @@ __global__ void __launch_bounds__(256) k_pf_quant(PFQuantParams P) {
   quantize_row_waves<NB>(xa, s);
   store_q8_row<NB>(s, P.out, t);
 }
+
+// Q5_0 / Q8_0 projections of a token batch on f32 rows (the decode
+// kernel's per-row arithmetic, k_gemv_f): a workgroup keeps its rows'
+// weights in registers and runs PF_FT tokens one after the other.
+template <int MODE>
+__global__ void __launch_bounds__(256) k_pf_gemm_f(PFGemmFParams P) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nb8 = P.n_x / 32;
+  float* xq = reinterpret_cast<float*>(smem);  // [nb8][GF_XPAD]
+  float* xp = xq + nb8 * GF_XPAD;              // [nb8][8][4]
+  __shared__ float terms[256];
+  int ji = 0;
+#pragma unroll
+  for (int j = 1; j < 3; ++j)
+    if (j < P.n_jobs && (int)blockIdx.x >= P.jobs[j].tile_begin) ji = j;
+  const PFJob& J = P.jobs[ji];
+  const int tid = threadIdx.x;
+  const bool q50 = (J.type == T_Q5_0);
+  const int R = q50 ? max(1, 256 / nb8) : 32;
+  const int row0 = ((int)blockIdx.x - J.tile_begin) * R;
+  const int b5 = tid / R, r5 = tid - (tid / R) * R;
+  const int r_local = q50 ? r5 : (tid >> 3);
+  const int lane8 = tid & 7;
+  const int row = row0 + r_local;
+  const bool active = q50 ? (b5 < nb8 && row < J.rows) : (row < J.rows);
+  const int row_c = min(row, J.rows - 1);
+  const int orow = min(row0 + min(tid, R - 1), J.rows - 1);
+  Q50Item w5;
+  Q80Row w8;
+  if (q50)
+    w5 = load_q50(J.w, nb8, row_c, min(b5, nb8 - 1));
+  else
+    w8 = load_q80(J.w, nb8, row_c, lane8);
+  const float bias = (MODE == MODE_BIAS && J.bias) ? J.bias[orow] : 0.0f;
+  const int t0 = blockIdx.y * PF_FT;
+  for (int tt = 0; tt < PF_FT; ++tt) {
+    const int t = t0 + tt;
+    if (t >= P.m) break;  // uniform
+    __syncthreads();      // the previous token's LDS reads are done
+    for (int e = tid; e < nb8 * 32; e += 256) {
+      const float v = P.x[(size_t)t * P.ldx + e];
+      const int b = e >> 5, kk = e & 31;
+      xq[b * GF_XPAD + kk] = v;
+      xp[(b * 8 + (kk & 7)) * 4 + (kk >> 3)] = v;
+    }
+    __syncthreads();
+    float acc = 0.0f;
+    if (q50) {
+      if (active) terms[r5 * nb8 + b5] = q50_term(w5, xq + b5 * GF_XPAD);
+      __syncthreads();
+      if (tid < R)
+        for (int b = 0; b < nb8; ++b) acc = acc + terms[tid * nb8 + b];
+    } else {
+      acc = q80_row_sum(q80_lane_acc(w8, xp, nb8, lane8));
+      if (lane8 == 0) terms[r_local] = acc;
+      __syncthreads();
+      if (tid < R) acc = terms[tid];
+    }
+    if (tid < R && row0 + tid < J.rows) {
+      float* y = J.y + (size_t)t * J.ldy + row0 + tid;
+      if (MODE == MODE_RESID)
+        *y = *y + acc;
+      else
+        *y = J.bias ? acc + bias : acc;
+    }
+  }
+}
+template __global__ void k_pf_gemm_f<MODE_BIAS>(PFGemmFParams);
+template __global__ void k_pf_gemm_f<MODE_RESID>(PFGemmFParams);
 
 // RoPE of token t's k (tensor/ops.go:262-286, same expressions as the
 // attention kernel) and the K/V store at pos0 + t (engine/kvcache.go:143-157).

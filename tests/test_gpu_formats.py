@@ -77,10 +77,23 @@ def test_real_formats_greedy_stream(real_tiny):
     orc.close()
 
 
-def test_real_formats_reject_batched_prefill(real_tiny):
+def test_real_formats_batched_prefill(real_tiny):
+    # Q5_0 / Q8_0 projections of a token batch (k_pf_gemm_f) with the
+    # K-quant ffn_down on MFMA: KV and normX equal sequential ingest
     gf, ctx, orc, _, _ = open_pair(real_tiny, 256)
-    with pytest.raises(H.C2hError):
-        ctx.prefill(np.arange(8, dtype=np.int32), 0)
+    rng = np.random.default_rng(81)
+    a = rng.integers(0, 4093, 37).astype(np.int32)
+    b = rng.integers(0, 4093, 21).astype(np.int32)
+    ctx.prefill(a, 0, want_normx=False)
+    got = ctx.prefill(b, 37)
+    orc.ingest_from(0, a)
+    want = orc.ingest_from(37, b)
+    assert np.array_equal(bits(got), bits(want))
+    kv = orc.kv()
+    for which in (0, 1):
+        for layer in (0, 1):
+            for h in (0, 1):
+                assert np.array_equal(bits(ctx.kv(which, layer, h, 58)), bits(kv[which, layer, h, :58]))
     ctx.close()
     orc.close()
 
@@ -91,9 +104,7 @@ def test_full_model_real_formats_64_steps(tmp_path_factory):
     gf, ctx, orc, im_end, eos = open_pair(p, 1024)
     rng = np.random.default_rng(80)
     prompt = rng.integers(0, 151936, 32).astype(np.int32)
-    ctx.set_token_ids(0, prompt)
-    for q, t in enumerate(prompt):
-        ctx.forward(int(t), q, want_normx=False)
+    ctx.prefill(prompt, 0, want_normx=False)  # batched: Q5_0 / Q8_0 / Q6_K projections of 32 tokens
     got = []
     pos = len(prompt)
     for _ in range(64):
