@@ -12,8 +12,9 @@ then Forward(best, pos); only the chosen id crosses to the host each step.
 Prints one JSON line: value = K / wall time of the K steps on one GPU, plus
 the roofline of the dominant kernel (the fused vocab projection) and the CPU
 baseline (the oracle on this host's cores, same workload).  `extra` adds,
-outside the timed region, the batched prefill of a 512-token prompt and
-decode at long contexts (512 / 4096 / 32768 positions of N(0,1) K/V).
+outside the timed region, the batched prefill of a 512-token prompt, decode
+at long contexts (512 / 4096 / 32768 positions of N(0,1) K/V), and decode
+and prefill with the real Q4_K_M file's format mix (Q5_0 / Q8_0 / Q6_K).
 """
 from __future__ import annotations
 
@@ -134,6 +135,31 @@ def long_context(gf, im_end, eos, lengths, steps: int = 16):
     return out
 
 
+def real_formats(tmpdir, im_end, eos, steps: int = 64):
+    """The published Qwen2.5-0.5B-Instruct Q4_K_M file's format mix (Q5_0
+    q/k/o/gate/up, Q8_0 attn_v, Q6_K ffn_down) at the same shape, random-init:
+    device-fed greedy steps after a 32-token batched prefill, and the
+    512-token prefill."""
+    from c2slm_amd import _lib as H
+    from c2slm_amd import gguf as G
+    path = os.path.join(tmpdir, "qwen05b_real_formats.gguf")
+    G.write_synthetic_model(path, G.QWEN05B_REAL_FORMATS, seed=SEED + 3)
+    gf = G.GGUFFile(path)
+    desc = H.desc_from_gguf(gf, max_ctx=1024)
+    ctx = H.Ctx(desc)
+    H.load_gguf_into(ctx, gf)
+    prompt = np.random.default_rng(SEED).integers(0, desc.n_vocab, PROMPT_LEN).astype(np.int32)
+    ctx.prefill(prompt, 0, want_normx=False)
+    ms = ctx.time_steps(PROMPT_LEN, steps, PENALTY, im_end, eos)
+    pf = prefill_rate(ctx, desc, 3)
+    ctx.close()
+    del gf
+    os.remove(path)
+    return {"formats": "Q5_0 q/k/o/gate/up, Q8_0 attn_v, Q6_K ffn_down, Q8_0 embedding",
+            "decode_ms_per_step": round(ms, 4), "decode_tok_s": round(1000.0 / ms, 1),
+            "prefill_512_ms": pf["ms"], "prefill_512_tok_s": pf["tok_s"]}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -149,6 +175,7 @@ def main():
     ap.add_argument("--long-context", default="512,4096,32768",
                     help="context lengths of the long-context decode lines ('' to skip)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill line")
+    ap.add_argument("--no-real-formats", action="store_true", help="skip the real-model format line")
     ap.add_argument("--only", choices=["prefill", "long"], default=None,
                     help="run just the prefill reps or just the long-context decode (profiler runs); "
                          "prints their JSON object, not the bench line")
@@ -223,6 +250,12 @@ def main():
     prefill = None if args.no_prefill else prefill_rate(ctx, desc, args.prefill_reps)
     lengths = [int(x) for x in args.long_context.split(",") if x]
     longctx = long_context(gf, im_end, eos, lengths) if lengths else None
+    realf = None
+    if not args.no_real_formats:
+        rdir = tmpdir or tempfile.mkdtemp(prefix="c2slm_bench_")
+        realf = real_formats(rdir, im_end, eos)
+        if rdir != tmpdir:
+            os.rmdir(rdir)
 
     base = None
     if not args.no_cpu_baseline:
@@ -255,7 +288,8 @@ def main():
                   "pipelined_ms_per_step": round(pipelined_ms, 4),
                   "pipelined_tok_s": round(1000.0 / pipelined_ms, 1),
                   "prefill_512": prefill,
-                  "long_context_decode": longctx},
+                  "long_context_decode": longctx,
+                  "real_formats": realf},
     }
     print(json.dumps(line))
     ctx.close()
