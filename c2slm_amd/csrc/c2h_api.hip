@@ -255,7 +255,7 @@ int upload_f32(c2h_ctx* c, float** dst, int64_t n_expected, int type, int64_t ro
 // k_gemv_q8k: the external Q8_K row plus 256 term and 256 scale slots.
 size_t gemv_q8k_lds_bytes() { return sizeof(Q8KLds) + (size_t)512 * sizeof(float); }
 
-void add_job(GemvParams& P, int* task, const Tensor& w, const Tensor* w2, int mode, float* y, const float* bias,
+void add_job(GemvParams& P, const Tensor& w, const Tensor* w2, int mode, float* y, const float* bias,
              int32_t* isums) {
   GemvJob& J = P.jobs[P.n_jobs++];
   J.w = w.ref();
@@ -276,12 +276,17 @@ void add_job(GemvParams& P, int* task, const Tensor& w, const Tensor* w2, int mo
     J.rpw = 256 / (4 * J.nb);
   }
   J.n_wg = (J.rows + J.rpw - 1) / J.rpw;
-  J.wg_begin = *task;
-  *task += J.n_wg;
   J.mode = mode;
   J.y = y;
   J.bias = bias;
   J.isums = isums;
+}
+
+// Grid of a GEMV launch: one row per job, as wide as its widest job.
+dim3 job_grid(const GemvParams& P) {
+  int w = 1;
+  for (int j = 0; j < P.n_jobs; ++j) w = std::max(w, P.jobs[j].n_wg);
+  return dim3(w, P.n_jobs);
 }
 
 typedef void (*GemvKernel)(GemvParams);
@@ -334,19 +339,19 @@ GemvKernel gemv_f_kernel(int pro, int mode) {
 }
 
 // A float-input launch over all its jobs (P.n_x = the input length).
-void launch_gemv_f(c2h_ctx* c, GemvParams& P, int total_wg) {
+void launch_gemv_f(c2h_ctx* c, GemvParams& P) {
   GemvKernel k = gemv_f_kernel(P.prologue, P.jobs[0].mode);
   const size_t lds = (size_t)gemv_f_lds_floats(P.n_x) * sizeof(float);
-  hipLaunchKernelGGL(k, dim3(total_wg), dim3(256), lds, c->stream, P);
+  hipLaunchKernelGGL(k, job_grid(P), dim3(256), lds, c->stream, P);
 }
 
 // A row-kernel launch over all its jobs (same width and mode); the norm
 // prologues need the x*x chain buffer.
-void launch_gemv_row(c2h_ctx* c, GemvParams& P, int total_wg) {
+void launch_gemv_row(c2h_ctx* c, GemvParams& P) {
   const GemvJob& J = P.jobs[0];
   GemvKernel k = gemv_row_kernel(J.nb, P.prologue, J.mode);
   size_t lds = (P.prologue != PRO_QUANT) ? (size_t)P.n_x_lds * sizeof(float) : 0;
-  hipLaunchKernelGGL(k, dim3(total_wg), dim3(256), lds, c->stream, P);
+  hipLaunchKernelGGL(k, job_grid(P), dim3(256), lds, c->stream, P);
 }
 
 GemvParams base_params(c2h_ctx* c) {
@@ -439,9 +444,8 @@ void launch_group(c2h_ctx* c, std::initializer_list<ProjJob> jobs, int pro, int 
   bool first = true;
   for (int kind = 0; kind < 2; ++kind) {
     GemvParams P = base_params(c);
-    int task = 0;
     for (const ProjJob& j : jobs)
-      if (float_input(j.w->type) == (kind == 1)) add_job(P, &task, *j.w, j.w2, mode, j.y, j.bias, nullptr);
+      if (float_input(j.w->type) == (kind == 1)) add_job(P, *j.w, j.w2, mode, j.y, j.bias, nullptr);
     if (P.n_jobs == 0) continue;
     P.prologue = (!first && (pro == PRO_EMBED_NORM || pro == PRO_ARGMAX_EMBED_NORM)) ? PRO_NORM : pro;
     P.x = x;
@@ -451,9 +455,9 @@ void launch_group(c2h_ctx* c, std::initializer_list<ProjJob> jobs, int pro, int 
     P.norm_w = norm_w;
     P.nb_in = kind == 0 ? nb_k(n_x) : nb8_of(n_x);
     if (kind == 0)
-      launch_gemv_row(c, P, task);
+      launch_gemv_row(c, P);
     else
-      launch_gemv_f(c, P, task);
+      launch_gemv_f(c, P);
     first = false;
   }
 }
@@ -1307,9 +1311,8 @@ int c2h_gemv_dev(c2h_ctx* c, int32_t type, const void* w_packed, const void* xq,
     P.prologue = PRO_QUANT;
     P.x = reinterpret_cast<const float*>(xq);
     P.n_x = nb8_of(cols) * 32;
-    int task = 0;
-    add_job(P, &task, t, nullptr, MODE_STORE, y, nullptr, nullptr);
-    launch_gemv_f(c, P, task);
+    add_job(P, t, nullptr, MODE_STORE, y, nullptr, nullptr);
+    launch_gemv_f(c, P);
     HIPCHK(c, hipGetLastError());
     return C2H_OK;
   }
@@ -1318,9 +1321,8 @@ int c2h_gemv_dev(c2h_ctx* c, int32_t type, const void* w_packed, const void* xq,
   P.prologue = PRO_Q8K;
   P.q8k_in = reinterpret_cast<const uint8_t*>(xq);
   P.nb_in = nb_k(cols);
-  int task = 0;
-  add_job(P, &task, t, nullptr, MODE_STORE, y, nullptr, isums_out);
-  hipLaunchKernelGGL(k_gemv_q8k, dim3(task), dim3(256), gemv_q8k_lds_bytes(), c->stream, P);
+  add_job(P, t, nullptr, MODE_STORE, y, nullptr, isums_out);
+  hipLaunchKernelGGL(k_gemv_q8k, job_grid(P), dim3(256), gemv_q8k_lds_bytes(), c->stream, P);
   HIPCHK(c, hipGetLastError());
   return C2H_OK;
 }

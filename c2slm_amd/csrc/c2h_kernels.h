@@ -73,8 +73,7 @@ struct GemvJob {
   int rows;
   int nb;        // super-blocks per row (floor(cols/256))
   int rpw;       // rows per workgroup = floor(256 / (4*nb))
-  int wg_begin;  // first workgroup of this job
-  int n_wg;
+  int n_wg;      // workgroups of this job (grid row blockIdx.y = job)
   int mode;
   float* y;
   const float* bias;

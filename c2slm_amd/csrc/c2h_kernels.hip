@@ -117,14 +117,60 @@ __device__ __forceinline__ void quantize_wave(const float4& v, int b, Row& s) {
 }
 
 // Quantise NB blocks of a row held as float4 per lane: wave w owns blocks
-// w, w+4, ... (v[i] = elements 4l..4l+3 of block w+4i).  Ends with a barrier.
+// w, w+4, ... (v[i] = elements 4l..4l+3 of block w+4i; past the last block
+// a wave holds a copy of block NB-1 and stores nothing).  The blocks of a
+// wave run in lockstep, each step applied to all of them, so their
+// dependent DPP/divide chains overlap.  Ends with a barrier.
 template <int NB, class Row>
 __device__ __forceinline__ void quantize_row_waves(const float4 (&v)[(NB + 3) / 4], Row& s) {
-  const int wave = threadIdx.x >> 6;
+  constexpr int BPW = (NB + 3) / 4;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  int a[BPW];
 #pragma unroll
-  for (int i = 0; i < (NB + 3) / 4; ++i) {
+  for (int i = 0; i < BPW; ++i)
+    a[i] = max(max(amax_bits(v[i].x), amax_bits(v[i].y)), max(amax_bits(v[i].z), amax_bits(v[i].w)));
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp_i<DPP_QUAD_1032>(a[i]));
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp_i<DPP_QUAD_2301>(a[i]));
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp_i<DPP_HALF_MIRROR>(a[i]));
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp_i<DPP_MIRROR>(a[i]));
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp_i<DPP_BCAST15, 0xa>(a[i]));
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp_i<DPP_BCAST31, 0xc>(a[i]));
+  float m[BPW], d[BPW], isc[BPW];
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
+    m[i] = __int_as_float(__builtin_amdgcn_readlane(a[i], 63));
+    // a zero block keeps d = 0 (its quants are 0 through quant1)
+    d[i] = (m[i] != 0.0f) ? m[i] / 127.0f : 0.0f;
+    isc[i] = (m[i] != 0.0f) ? 127.0f / m[i] : 0.0f;
+  }
+  int bsum[BPW];
+  uint32_t packed[BPW];
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
+    const int q0 = quant1(v[i].x, isc[i], m[i]), q1 = quant1(v[i].y, isc[i], m[i]);
+    const int q2 = quant1(v[i].z, isc[i], m[i]), q3 = quant1(v[i].w, isc[i], m[i]);
+    packed[i] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+                ((uint32_t)(q3 & 0xff) << 24);
+    bsum[i] = (q0 + q1) + (q2 + q3);
+  }
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) bsum[i] += dpp_i<DPP_QUAD_1032>(bsum[i]);
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) bsum[i] += dpp_i<DPP_QUAD_2301>(bsum[i]);
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
     const int b = wave + 4 * i;
-    if (b < NB) quantize_wave(v[i], b, s);
+    if (b < NB) {
+      s.q[b][lane] = packed[i];
+      if ((lane & 3) == 0) s.bs[b][lane >> 2] = bsum[i];
+      if (lane == 0) s.d[b] = d[i];
+    }
   }
   __syncthreads();
 }
@@ -174,24 +220,58 @@ __device__ __forceinline__ float wave_incl_scan(float x) {
   x = x + dpp_or0<DPP_BCAST31, 0xc>(x);
   return x;
 }
-__device__ __forceinline__ float wave_shift_up(float x) { return dpp_or0<0x138>(x); }  // wave_shr:1, lane 0 gets 0
+// Lane l receives lane l-1's value (lane 0 gets 0) / lane l+1's value
+// (lane 63 gets 0).  wave_shr:1 / wave_shl:1.
+__device__ __forceinline__ float wave_shift_up(float x) { return dpp_or0<0x138>(x); }
+__device__ __forceinline__ float wave_shift_down(float x) { return dpp_or0<0x130>(x); }
+// Cross-lane values must be computed with the whole wave active: a select
+// around them lets the compiler run the DPP moves under a partial EXEC, where
+// reads from switched-off lanes return 0.  The empty asm pins the value.
+__device__ __forceinline__ float pin_full_wave(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+__device__ __forceinline__ float lane_value(float x, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
 
 // The reference's sequential f32 sum (((0 + a[0]) + a[1]) + ...) + a[n-1]
-// (tensor/ops.go:209-211 RMSNorm, :331-333 Softmax) of n <= 1024 values
-// a[i] >= +0 in LDS, computed by one whole wave and returned in every lane,
-// bit-identical to the one-lane chain but ~6x shorter:
-//   lane l owns chunk [16l, 16l+16); from a start S_l it runs the chunk's
-//   16 dependent adds to R_l.  Lane 0's start is 0 (exact).  If R_l ==
-//   S_{l+1} for every l, each start is by induction the exact sequential
-//   partial sum and R_63 is the exact total.  The starts begin as a
-//   parallel-prefix guess; each round keeps the verified prefix, sets the
-//   first unverified start to its predecessor's (now exact) R, and shifts
-//   the later ones by the accumulated differences, which is exact while
-//   the sums stay in one binade.  Each round extends the exact prefix by at
-//   least one chunk; after SPEC_ROUNDS lane 0 finishes sequentially from
-//   the last exact start.  a must be readable up to round_up(n, 16).
+// (tensor/ops.go:209-211 RMSNorm, :331-333 Softmax) of n values a[i] >= +0
+// computed by one whole wave and returned in every lane, bit-identical to
+// the one-lane chain but several times shorter:
+//   lane l owns chunk l and runs the chunk's dependent adds from a start
+//   S_l to R_l.  Lane 0's start is 0 (exact).  If R_l == S_{l+1} for every
+//   l, each start is by induction the exact sequential partial sum and R_63
+//   is the exact total.  The starts begin as a parallel-prefix guess; each
+//   round keeps the verified prefix, sets the first unverified start to its
+//   predecessor's (now exact) R, and shifts the later ones by the
+//   accumulated differences, which is exact while the sums stay in one
+//   binade.  Each round extends the exact prefix by at least one chunk;
+//   after SPEC_ROUNDS the rest runs sequentially from the last exact start.
 constexpr int SPEC_C = 16;
 constexpr int SPEC_ROUNDS = 10;
+
+// One round: R is this lane's chunk run from its start S.  Returns true with
+// the total once every start is verified; else advances S (and m, the last
+// lane whose start is exact before the update).
+__device__ __forceinline__ bool spec_round(float& S, float R, int& m, float& total) {
+  const int lane = threadIdx.x & 63;
+  const float s_next = pin_full_wave(wave_shift_down(S));
+  const unsigned long long bad = __ballot(lane < 63 && !(R == s_next));
+  if (bad == 0ull) {
+    total = lane_value(R, 63);
+    return true;
+  }
+  m = __builtin_amdgcn_readfirstlane(__ffsll(bad) - 1);  // starts 0..m are exact
+  const float e = (lane < 63) ? (R - s_next) : 0.0f;
+  const float shift = pin_full_wave(wave_shift_up(wave_incl_scan(e)));
+  const float r_prev = pin_full_wave(wave_shift_up(R));
+  S = (lane <= m) ? S : ((lane == m + 1) ? r_prev : S + shift);
+  return false;
+}
+
+// n <= 1024: lane l owns [16l, 16l+16) in registers.  a: LDS readable up to
+// round_up(n, 16).
 __device__ __forceinline__ float seq_sum_wave(const float* a, int n) {
   const int lane = threadIdx.x & 63;
   const int base = lane * SPEC_C;
@@ -212,27 +292,18 @@ __device__ __forceinline__ float seq_sum_wave(const float* a, int n) {
   float cs = 0.0f;
 #pragma unroll
   for (int k = 0; k < SPEC_C; ++k) cs = cs + v[k];
-  float S = (lane == 0) ? 0.0f : wave_shift_up(wave_incl_scan(cs));
-  int m = -1;  // lanes <= m have verified starts
+  float S = pin_full_wave(wave_shift_up(wave_incl_scan(cs)));
+  int m = -1;
+  float total;
   for (int round = 0; round < SPEC_ROUNDS; ++round) {
     float R = S;
 #pragma unroll
     for (int k = 0; k < SPEC_C; ++k) R = R + v[k];
-    const float s_next = __shfl_down(S, 1);
-    const unsigned long long bad = __ballot(lane < 63 && !(R == s_next));
-    if (bad == 0ull) return __shfl(R, 63);
-    m = __ffsll(bad) - 1;  // first lane whose successor's start is wrong; starts 0..m are exact
-    const float e = (lane < 63) ? (R - s_next) : 0.0f;
-    const float shift = (lane == 0) ? 0.0f : wave_shift_up(wave_incl_scan(e));
-    const float r_prev = __shfl_up(R, 1);
-    S = (lane <= m) ? S : ((lane == m + 1) ? r_prev : S + shift);
+    if (spec_round(S, R, m, total)) return total;
   }
-  // starts 0..m+1 are exact: finish sequentially from chunk m+1
-  float s = __shfl(S, m + 1);
-  if (lane == 0) {
-    for (int i = (m + 1) * SPEC_C; i < n; ++i) s = s + a[i];
-  }
-  return __shfl(s, 0);
+  float s = lane_value(S, m + 1);
+  for (int i = (m + 1) * SPEC_C; i < n; ++i) s = s + a[i];
+  return s;
 }
 
 // The same exact sequential sum for any n >= 1 (softmax over long contexts):
@@ -280,22 +351,14 @@ __device__ __forceinline__ float seq_sum_wave_n(const float* a, int n) {
   const int C = (((n + 63) >> 6) + 3) & ~3;
   const int b0 = min(lane * C, n), b1 = min(b0 + C, n);
   const float cs = chunk_chain(a, b0, b1, 0.0f);
-  float S = (lane == 0) ? 0.0f : wave_shift_up(wave_incl_scan(cs));
+  float S = pin_full_wave(wave_shift_up(wave_incl_scan(cs)));
   int m = -1;
+  float total;
   for (int round = 0; round < SPEC_ROUNDS; ++round) {
     const float R = chunk_chain(a, b0, b1, S);
-    const float s_next = __shfl_down(S, 1);
-    const unsigned long long bad = __ballot(lane < 63 && !(R == s_next));
-    if (bad == 0ull) return __shfl(R, 63);
-    m = __ffsll(bad) - 1;
-    const float e = (lane < 63) ? (R - s_next) : 0.0f;
-    const float shift = (lane == 0) ? 0.0f : wave_shift_up(wave_incl_scan(e));
-    const float r_prev = __shfl_up(R, 1);
-    S = (lane <= m) ? S : ((lane == m + 1) ? r_prev : S + shift);
+    if (spec_round(S, R, m, total)) return total;
   }
-  float s = __shfl(S, m + 1);
-  if (lane == 0) s = chunk_chain(a, min((m + 1) * C, n), n, s);
-  return __shfl(s, 0);
+  return chunk_chain(a, min((m + 1) * C, n), n, lane_value(S, m + 1));
 }
 
 // 1/rms of n values (n <= 1024, a multiple of 4) held as elements 4t..4t+3
@@ -577,6 +640,22 @@ __device__ __forceinline__ float4 embed4(const WeightRef& emb, int n_vocab, int 
 
 // ------------------------------------------------------ GEMV (row kernel)
 
+// A GEMV launch covers its jobs as grid rows: job blockIdx.y, workgroup
+// blockIdx.x of it.  The job's fields go through an empty asm together with
+// the launch's x, so they load in one scalar batch instead of a chain of
+// dependent round trips.  The integer fields come out of the asm, which
+// keeps them in SGPRs rather than re-read in the epilogue; the pointers only
+// go in (a pointer out of an asm loses its global address space, and its
+// loads would turn into flat loads with whole-queue waits).
+__device__ __forceinline__ GemvJob launch_job(const GemvParams& P) {
+  GemvJob J = P.jobs[blockIdx.y];
+  asm volatile(""
+               : "+s"(J.type), "+s"(J.type2), "+s"(J.rows), "+s"(J.nb), "+s"(J.rpw), "+s"(J.n_wg), "+s"(J.mode)
+               : "s"(J.w.q), "s"(J.w.d), "s"(J.w2.q), "s"(J.w2.d), "s"(J.y), "s"(J.bias), "s"(J.isums), "s"(P.x),
+                 "s"(P.norm_w), "s"(P.n_x), "s"(P.eps));
+  return J;
+}
+
 // One GEMV of the layer body with its input prologue, for rows of NB
 // super-blocks (weights and input share the width):
 //   PRO_QUANT  Q8_K(x), x = attention output or SwiGLU output;
@@ -602,18 +681,14 @@ __global__ void __launch_bounds__(256) k_gemv_row(GemvParams P) {
   __shared__ float inv_slot;
   __shared__ ArgCand ared[4];
 
-  // the job of this workgroup (uniform)
-  int ji = 0;
-#pragma unroll
-  for (int j = 1; j < MAX_JOBS; ++j)
-    if (j < P.n_jobs && (int)blockIdx.x >= P.jobs[j].wg_begin) ji = j;
-  const GemvJob& J = P.jobs[ji];
+  const GemvJob J = launch_job(P);
+  if ((int)blockIdx.x >= J.n_wg) return;  // uniform: the launch's widest job sets the grid
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int b = tid / (4 * RPW);
   const int r_local = (tid - b * 4 * RPW) >> 2;
   const int u = tid & 3;
-  const int row0 = ((int)blockIdx.x - J.wg_begin) * RPW;
+  const int row0 = (int)blockIdx.x * RPW;
   const int row = row0 + r_local;
   const bool active = (b < NB) && (row < J.rows);
   const int row_c = min(row, J.rows - 1);
@@ -647,7 +722,7 @@ __global__ void __launch_bounds__(256) k_gemv_row(GemvParams P) {
 
   // ---- prologue: the Q8_K input row in LDS
   if (NORM) {
-    if (PRO != PRO_NORM && blockIdx.x == 0) {  // layer 0 publishes the embedded token
+    if (PRO != PRO_NORM && blockIdx.x == 0 && blockIdx.y == 0) {  // layer 0 publishes the embedded token
       if (4 * tid < P.n_x) reinterpret_cast<float4*>(P.x_out)[tid] = xa[0];
       if (tid == 0) {
         const int pos = P.state->pos;
@@ -720,15 +795,14 @@ __global__ void __launch_bounds__(256) k_gemv_q8k(GemvParams P) {
   float* terms = reinterpret_cast<float*>(smem + sizeof(Q8KLds));  // [256]
   float* dq = terms + 256;                                          // [256]
   const int tid = threadIdx.x;
-  int ji = 0;
-  while (ji < P.n_jobs - 1 && (int)blockIdx.x >= P.jobs[ji + 1].wg_begin) ++ji;
-  const GemvJob& J = P.jobs[ji];
+  const GemvJob J = launch_job(P);
+  if ((int)blockIdx.x >= J.n_wg) return;
   const int nb = J.nb;
   const int ipr = 4 * nb;
   const int r_local = tid / ipr;
   const int rem = tid - r_local * ipr;
   const int b = rem >> 2, u = rem & 3;
-  const int row0 = ((int)blockIdx.x - J.wg_begin) * J.rpw;
+  const int row0 = (int)blockIdx.x * J.rpw;
   const int row = row0 + r_local;
   const bool active = (r_local < J.rpw) && (row < J.rows);
   const int row_c = min(row0 + min(r_local, J.rpw - 1), J.rows - 1);
@@ -881,15 +955,12 @@ __global__ void __launch_bounds__(256) k_gemv_f(GemvParams P) {
   __shared__ float inv_slot;
   __shared__ ArgCand ared[4];
 
-  int ji = 0;
-#pragma unroll
-  for (int j = 1; j < MAX_JOBS; ++j)
-    if (j < P.n_jobs && (int)blockIdx.x >= P.jobs[j].wg_begin) ji = j;
-  const GemvJob& J = P.jobs[ji];
+  const GemvJob J = launch_job(P);
+  if ((int)blockIdx.x >= J.n_wg) return;
   const int tid = threadIdx.x;
   const bool q50 = (J.type == T_Q5_0);
   const int R = J.rpw;
-  const int row0 = ((int)blockIdx.x - J.wg_begin) * R;
+  const int row0 = (int)blockIdx.x * R;
   // Q5_0: thread = (block b, row r) block-major; Q8_0: row tid/8, lane tid%8
   const int b5 = tid / R, r5 = tid - (tid / R) * R;
   const int r_local = q50 ? r5 : (tid >> 3);
@@ -931,7 +1002,7 @@ __global__ void __launch_bounds__(256) k_gemv_f(GemvParams P) {
     xp[(b * 8 + (kk & 7)) * 4 + (kk >> 3)] = v;
   };
   if (NORM) {
-    if (PRO != PRO_NORM && blockIdx.x == 0) {  // layer 0 publishes the embedded token
+    if (PRO != PRO_NORM && blockIdx.x == 0 && blockIdx.y == 0) {  // layer 0 publishes the embedded token
       if (4 * tid < P.n_x) reinterpret_cast<float4*>(P.x_out)[tid] = xa;
       if (tid == 0) {
         const int pos = P.state->pos;
