@@ -484,7 +484,8 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax, bool long_attn) {
       if (long_attn)
         enqueue_attn_long(c, A, 1);
       else
-        hipLaunchKernelGGL(k_attn_core, dim3(D.n_heads), dim3(256), c->attn_lds, c->stream, A);
+        hipLaunchKernelGGL(k_attn_core, dim3(D.n_heads / D.n_kv_heads, D.n_kv_heads), dim3(256), c->attn_lds,
+                           c->stream, A);
     }
     // attn_out: X += Wo * x(attn)
     launch_group(c, {{&L.wo, nullptr, c->X, nullptr}}, PRO_QUANT, MODE_RESID, c->attn, E, nullptr);
@@ -1046,7 +1047,7 @@ int pf_pass(c2h_ctx* c, const int32_t* tokens, int m, int pos0) {
       A.store_kv = 0;
       if (pos0 + m <= c->att_split) {
         const size_t lds = (size_t)attn_lds_floats(pos0 + m) * 4;
-        hipLaunchKernelGGL(k_attn_core, dim3(D.n_heads, m), dim3(256), lds, c->stream, A);
+        hipLaunchKernelGGL(k_attn_core, dim3(D.n_heads / D.n_kv_heads, D.n_kv_heads, m), dim3(256), lds, c->stream, A);
       } else {
         for (int t0 = 0; t0 < m; t0 += PF_ATT_SUB) {
           A.tok0 = t0;

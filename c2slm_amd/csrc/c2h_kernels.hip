@@ -116,14 +116,14 @@ __device__ __forceinline__ void quantize_wave(const float4& v, int b, Row& s) {
   if (lane == 0) s.d[b] = d;
 }
 
-// Quantise NB blocks of a row held as float4 per lane: wave w owns blocks
-// w, w+4, ... (v[i] = elements 4l..4l+3 of block w+4i; past the last block
-// a wave holds a copy of block NB-1 and stores nothing).  The blocks of a
-// wave run in lockstep, each step applied to all of them, so their
-// dependent DPP/divide chains overlap.  Ends with a barrier.
-template <int NB, class Row>
-__device__ __forceinline__ void quantize_row_waves(const float4 (&v)[(NB + 3) / 4], Row& s) {
-  constexpr int BPW = (NB + 3) / 4;
+// Quantise NB blocks of a row held as float4 per lane by NW waves: wave w
+// owns blocks w, w+NW, ... (v[i] = elements 4l..4l+3 of block w+NW*i; past
+// the last block a wave holds a copy of block NB-1 and stores nothing).  The
+// blocks of a wave run in lockstep, each step applied to all of them, so
+// their dependent DPP/divide chains overlap.  Ends with a barrier.
+template <int NB, int NW = 4, class Row>
+__device__ __forceinline__ void quantize_row_waves(const float4 (&v)[(NB + NW - 1) / NW], Row& s) {
+  constexpr int BPW = (NB + NW - 1) / NW;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   int a[BPW];
 #pragma unroll
@@ -165,7 +165,7 @@ __device__ __forceinline__ void quantize_row_waves(const float4 (&v)[(NB + 3) / 
   for (int i = 0; i < BPW; ++i) bsum[i] += dpp_i<DPP_QUAD_2301>(bsum[i]);
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
-    const int b = wave + 4 * i;
+    const int b = wave + NW * i;
     if (b < NB) {
       s.q[b][lane] = packed[i];
       if ((lane & 3) == 0) s.bs[b][lane >> 2] = bsum[i];
@@ -668,9 +668,10 @@ __device__ __forceinline__ GemvJob launch_job(const GemvParams& P) {
 // fold runs per row in the reference's order.
 template <int NB, int PRO, int MODE>
 __global__ void __launch_bounds__(256) k_gemv_row(GemvParams P) {
+  constexpr int NW = 4;
   constexpr int IPR = 4 * NB;
   constexpr int RPW = 256 / IPR;
-  constexpr int BPW = (NB + 3) / 4;  // Q8_K blocks quantised per wave
+  constexpr int BPW = (NB + NW - 1) / NW;  // Q8_K blocks quantised per wave
   constexpr bool PAIRED = (MODE == MODE_SWIGLU);
   constexpr bool NORM = (PRO == PRO_NORM || PRO == PRO_EMBED_NORM || PRO == PRO_ARGMAX_EMBED_NORM);
   static_assert(!NORM || NB <= 4, "the norm prologue holds one float4 per thread");
@@ -708,7 +709,7 @@ __global__ void __launch_bounds__(256) k_gemv_row(GemvParams P) {
   } else {
 #pragma unroll
     for (int i = 0; i < BPW; ++i)
-      xa[i] = reinterpret_cast<const float4*>(P.x + min(wave + 4 * i, NB - 1) * QK_K)[lane];
+      xa[i] = reinterpret_cast<const float4*>(P.x + min(wave + NW * i, NB - 1) * QK_K)[lane];
   }
   if (NORM) nw = load4(P.norm_w, P.n_x);
   const ItemW w1 = load_item(J.w, J.type, NB, row_c, b_c, u);
@@ -735,7 +736,7 @@ __global__ void __launch_bounds__(256) k_gemv_row(GemvParams P) {
     if (wave < NB) quantize_wave(xn[0], wave, s);
     __syncthreads();
   } else {
-    quantize_row_waves<NB>(xa, s);
+    quantize_row_waves<NB, NW>(xa, s);
   }
 
   // ---- items
@@ -1173,6 +1174,21 @@ __device__ __forceinline__ f32x4_t vquad_load(const float* vslot, int qi) {
   return reinterpret_cast<const f32x4_t*>(vslot)[(size_t)qi * 64 + (threadIdx.x & 63)];
 }
 
+// A buffer resource over the first nbytes at p (raw, 32-bit elements):
+// lanes whose offset lies past nbytes read zeros and cause no memory traffic,
+// so a fixed-shape prefetch of the cache costs what the stored context holds
+// instead of re-reading a clamped last row.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t cache_rsrc(const float* p, int nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, nbytes, 0x00020000);
+}
+__device__ __forceinline__ f32x4_t cache_ld4(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+// V quad qi of this lane's dimension from a quad-major slot held as a buffer.
+__device__ __forceinline__ f32x4_t vquad_load_buf(__amdgpu_buffer_rsrc_t r, int qi) {
+  return cache_ld4(r, (qi * 64 + (int)(threadIdx.x & 63)) * 16);
+}
+
 // Score of one position (internal/simd/c2_tensor_attn_gen.go:18-50): two
 // 8-lane FMA accumulators over d = 0,16,32,48 (lanes l and 8+l), then
 // ((l0+l1)+(l2+l3))+((l4+l5)+(l6+l7)) of acc0+acc1, times scale.
@@ -1232,42 +1248,54 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   __shared__ float inv_slot;
 
   const int tid = threadIdx.x;
-  const int h = blockIdx.x;
-  const int ti = P.tok0 + blockIdx.y;  // query token of the batch (0 in decode)
-  const int qpkv = P.n_heads / P.n_kv_heads;
-  const int g = h / qpkv;
+  // grid (query heads per KV head, KV heads, query tokens of the batch)
+  const int qpkv = (int)gridDim.x;
+  const int g = (int)blockIdx.y;
+  const int h = g * qpkv + (int)blockIdx.x;
+  const int ti = P.tok0 + (int)blockIdx.z;  // query token of the batch (0 in decode)
+  // the launch's fields in one scalar batch (not a chain of round trips)
+  asm volatile("" ::"s"(P.q), "s"(P.k), "s"(P.v), "s"(P.kv), "s"(P.state), "s"(P.rope_cos), "s"(P.rope_sin),
+               "s"(P.q_ld), "s"(P.kv_ld), "s"(P.tok0), "s"(P.layer), "s"(P.n_layers), "s"(P.n_kv_heads),
+               "s"(P.max_ctx), "s"(P.rope_len));
+  // this head's q and the group's k, v: thread t < 192 holds element t%64
+  // of q_h (t < 64), k_g, v_g.  Issued before the position is read.
+  const int bm = min(tid >> 6, 2);
+  const float* qsrc = P.q + (size_t)ti * P.q_ld + h * HD;
+  const float* ksrc = P.k + (size_t)ti * P.kv_ld + g * HD;
+  const float* vsrc = P.v + (size_t)ti * P.kv_ld + g * HD;
+  const float own = ((bm == 0) ? qsrc : ((bm == 1) ? ksrc : vsrc))[tid & 63];
+  issue_fence();
   const int pos = P.state->pos + ti;
   const int T = pos + 1;
   const size_t head_stride = (size_t)kv_slot(P.max_ctx) * HD;
   float* kcache = P.kv + ((size_t)P.layer * P.n_kv_heads + g) * head_stride;
   float* vcache = P.kv + (((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * head_stride;
-  const int plast = max(min(pos, P.max_ctx) - 1, 0);  // last stored position (clamp target)
-  const int qlast = plast >> 2;                        // its V quad
+  const int nstored = max(min(pos, P.max_ctx), 0);    // cached positions [0, nstored)
   const int nch = (pos + ATT_CH - 1) / ATT_CH;         // V chunks of positions [0, pos)
+  // the stored rows as buffers: prefetch slots past them read zeros for free
+  const __amdgpu_buffer_rsrc_t krs = cache_rsrc(kcache, nstored * HD * 4);
+  const __amdgpu_buffer_rsrc_t vrs = cache_rsrc(vcache, ((nstored + 3) >> 2) * HD * 16);
 
   // ---- loads, in the order they are consumed
-  // thread t < 192 holds element t%64 of q_h (t < 64), k_g, v_g
-  const int bm = min(tid >> 6, 2);
-  const float* src = (bm == 0) ? P.q + (size_t)ti * P.q_ld + h * HD
-                               : ((bm == 1) ? P.k : P.v) + (size_t)ti * P.kv_ld + g * HD;
-  const float own = src[tid & 63];
   const int rp = min(max(pos, 0), P.rope_len - 1);
   const float rcos = P.rope_cos[(size_t)rp * (HD / 2) + (tid & 31)];
   const float rsin = P.rope_sin[(size_t)rp * (HD / 2) + (tid & 31)];
   issue_fence();  // q/k/v and the RoPE row are needed first: issue them first
   float4 kreg[16], kreg2[16];
-  {
-    const float4* kr = reinterpret_cast<const float4*>(kcache + (size_t)min(tid, plast) * HD);
-    const float4* kr2 = reinterpret_cast<const float4*>(kcache + (size_t)min(tid + ATT_KPF, plast) * HD);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) kreg[i] = kr[i];
+  for (int i = 0; i < 16; ++i) {
+    const f32x4_t t = cache_ld4(krs, tid * HD * 4 + i * 16);
+    kreg[i] = make_float4(t.x, t.y, t.z, t.w);
+  }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) kreg2[i] = kr2[i];
+  for (int i = 0; i < 16; ++i) {
+    const f32x4_t t = cache_ld4(krs, (tid + ATT_KPF) * HD * 4 + i * 16);
+    kreg2[i] = make_float4(t.x, t.y, t.z, t.w);
   }
   const int wave = tid >> 6;
   f32x4_t vreg[VPT];  // native vectors: a float4 array copied whole is kept in scratch
 #pragma unroll
-  for (int i = 0; i < VPT; ++i) vreg[i] = vquad_load(vcache, min(wave + 4 * i, qlast));
+  for (int i = 0; i < VPT; ++i) vreg[i] = vquad_load_buf(vrs, wave + 4 * i);
   issue_fence();
 
   if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;
@@ -1288,7 +1316,7 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   __syncthreads();
 
   // (a batch of query tokens has its K/V stored by a kernel before this one)
-  if (P.store_kv && (h % qpkv) == 0 && tid < HD && pos < P.max_ctx) {
+  if (P.store_kv && blockIdx.x == 0 && tid < HD && pos < P.max_ctx) {
     kcache[(size_t)pos * HD + tid] = k_s[tid];
     vcache[vq_index(pos, tid)] = v_s[tid];
   }
@@ -1373,7 +1401,7 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
     const int wp = (wave >= 1) ? wave - 1 : 0;  // staging wave index
     auto load_set = [&](VStage<PER>& st, int c) {
 #pragma unroll
-      for (int k = 0; k < PER; ++k) st.r[k] = vquad_load(vcache, min(c * NQ + min(wp + 3 * k, NQ - 1), qlast));
+      for (int k = 0; k < PER; ++k) st.r[k] = vquad_load_buf(vrs, c * NQ + min(wp + 3 * k, NQ - 1));
     };
     auto store_set = [&](const VStage<PER>& st, int c) {
 #pragma unroll
