@@ -1259,7 +1259,9 @@ int c2h_quantize_q8k_dev(c2h_ctx* c, const float* x, int32_t cols, void* q8k_out
   HIPCHK(c, hipSetDevice(c->device));
   int nb = cols / 256;
   if (nb == 0) return C2H_OK;
-  hipLaunchKernelGGL(k_quantize_q8k, dim3(nb), dim3(256), 0, c->stream, x, nb, reinterpret_cast<uint8_t*>(q8k_out));
+  if (reinterpret_cast<uintptr_t>(x) & 15) return fail(c, C2H_ERR_INVALID, "x must be 16-byte aligned");
+  hipLaunchKernelGGL(k_quantize_q8k, dim3((nb + 3) / 4), dim3(256), 0, c->stream, x, nb,
+                     reinterpret_cast<uint8_t*>(q8k_out));
   HIPCHK(c, hipGetLastError());
   return C2H_OK;
 }

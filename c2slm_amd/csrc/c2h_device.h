@@ -67,16 +67,6 @@ __device__ __forceinline__ float fp16_tensor(uint32_t h) {
   return fp16_simd(h);
 }
 
-// Go int(float32) on amd64 (CVTTSS2SQ): truncation, INT64_MIN for NaN or
-// out-of-range inputs.  Callers clamp to [-127, 127], so only the sign of
-// the out-of-range marker matters.
-__device__ __forceinline__ int go_f32_to_int_clamped127(float t) {
-  if (!(t >= -9223372036854775808.0f && t < 9223372036854775808.0f)) return -127;
-  if (t >= 127.0f) return 127;
-  if (t <= -127.0f) return -127;
-  return (int)t;  // |t| < 127: exact truncation
-}
-
 // archsimd ConvertToInt32 (VCVTTPS2DQ): truncation, INT32_MIN for NaN or
 // out-of-range lanes.
 __device__ __forceinline__ int32_t x86_cvtt_i32(float t) {
@@ -140,6 +130,13 @@ template <int CTRL, int ROW_MASK = 0xf>
 __device__ __forceinline__ int dpp_i(int v) {
   return __builtin_amdgcn_update_dpp(v, v, CTRL, ROW_MASK, 0xf, false);
 }
+// The same move with 0 in lanes the control leaves out: 0 is the identity of
+// the max of non-negative values and of sums, which lets the compiler fold
+// the move into the following VALU op (one v_*_dpp instruction, no copy).
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ int dpp0_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, false);
+}
 template <int CTRL, int ROW_MASK = 0xf>
 __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(dpp_i<CTRL, ROW_MASK>(__float_as_int(v)));
@@ -157,15 +154,6 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
   v = fmax_gt(v, dpp_f<DPP_BCAST15, 0xa>(v));
   v = fmax_gt(v, dpp_f<DPP_BCAST31, 0xc>(v));
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-// Integer sum over each row of 16 lanes; every lane of the row gets it.
-__device__ __forceinline__ int row16_sum_dpp(int v) {
-  v += dpp_i<DPP_QUAD_1032>(v);
-  v += dpp_i<DPP_QUAD_2301>(v);
-  v += dpp_i<DPP_HALF_MIRROR>(v);
-  v += dpp_i<DPP_MIRROR>(v);
-  return v;
 }
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));

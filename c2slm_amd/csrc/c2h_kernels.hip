@@ -55,151 +55,130 @@ __device__ __forceinline__ ArgCand wave_argmax(ArgCand c) {
   return c;
 }
 
-__device__ __forceinline__ float abs_branch(float v) { return (v < 0.0f) ? -v : v; }
-
-// |x| as the quantiser's amax scan sees it (c2_quantize_q8_k_gen.go:26-37):
-// amax starts at +0 and only a strictly larger |x| replaces it, so NaN and
-// -0 never matter.  Mapping them to +0 lets v_max_f32 do the reduction.
-__device__ __forceinline__ float amax_key(float v) {
-  const float a = abs_branch(v);
-  return (a > 0.0f) ? a : 0.0f;
-}
-
 // ------------------------------------------------------------- Q8_K (A1)
 
-// One quant of internal/simd/c2_quantize_q8_k_gen.go:58-74: q = int(x*isc
-// ± 0.5) clamped to ±127, 0 in a zero block (m == 0).  Branch-free: |x*isc|
-// is at most 127(1+2^-23) whenever isc is finite, so only NaN and ±Inf
-// (isc = Inf for a tiny amax) reach Go's out-of-range conversion, whose
-// INT64_MIN result clamps to -127.
-__device__ __forceinline__ int quant1(float x, float isc, float m) {
+// One quant of internal/simd/c2_quantize_q8_k_gen.go:58-74 in a block with
+// amax != 0: q = int(x*isc ± 0.5) clamped to ±127.  The ± 0.5 is a copysign
+// (tq = -0 then gives -0.5 where the reference adds +0.5; both truncate to
+// 0).  Go's conversion truncates, and turns NaN and |r| >= 2^63 into
+// INT64_MIN, -127 after the clamp: the float clamp already sends NaN and
+// r <= -2^63 there, the compare catches r >= 2^63 (only reached with an
+// infinite isc, from an amax below 127/FLT_MAX).
+__device__ __forceinline__ int quant1(float x, float isc) {
   const float tq = x * isc;
-  const float r = (tq >= 0.0f) ? (tq + 0.5f) : (tq - 0.5f);
-  const bool in_range = (r >= -9223372036854775808.0f) && (r < 9223372036854775808.0f);
-  const int q = in_range ? (int)fminf(fmaxf(r, -127.0f), 127.0f) : -127;
-  return (m != 0.0f) ? q : 0;
+  const float r = tq + __builtin_copysignf(0.5f, tq);
+  const int q = (int)fminf(fmaxf(r, -127.0f), 127.0f);
+  return (r < 9223372036854775808.0f) ? q : -127;
 }
 
-// amax_key as int bits: non-negative non-NaN floats order like their bits.
-__device__ __forceinline__ int amax_bits(float v) { return __float_as_int(amax_key(v)); }
+// d = amax/127 rounded once: the product with RN(1/127) corrected by its
+// exact residual.  Equal to the IEEE quotient for every finite amax >= 0
+// (checked exhaustively over all 2^31 such floats); amax = +Inf gives Inf.
+__device__ __forceinline__ float div127(float m) {
+  constexpr float C = 1.0f / 127.0f;
+  const float q0 = m * C;
+  const float r = __builtin_fmaf(-q0, 127.0f, m);
+  const float q1 = __builtin_fmaf(r, C, q0);
+  return (m == __builtin_inff()) ? m : q1;
+}
 
-// Q8_K quantisation of block b by one wave; lane l holds elements 4l..4l+3
-// (internal/simd/c2_quantize_q8_k_gen.go:22-90: amax of branch-|x|,
-// d = amax/127, q = int(x*(127/amax) ± 0.5) clamped to ±127, zero block when
-// amax == 0, bsums over 16 quants).  The whole block stays in one wave:
-// the amax is a DPP reduction, the four quants of a lane pack into the
-// dword q[b][l], a 16-quant bsum is a quad reduction.  No barrier.
-template <class Row>
-__device__ __forceinline__ void quantize_wave(const float4& v, int b, Row& s) {
+// Q8_K quantisation (internal/simd/c2_quantize_q8_k_gen.go:22-90: amax of
+// branch-|x| where NaN and -0 never win, d = amax/127, q = int(x*(127/amax)
+// ± 0.5) clamped to ±127, zero block when amax == 0, bsums over 16 quants)
+// of BPW blocks by one wave, in lockstep so that their dependent DPP and
+// divide chains overlap.  Lane l holds elements 4l..4l+3 of block
+// b0 + step*i in v[i]; blocks at or past nb are computed and not stored.
+// The amax is a maxNum chain from +0 (NaN operands are skipped, -0 never
+// exceeds +0), then a DPP max over the wave's non-negative bit patterns;
+// the four quants of a lane pack into the dword q[b][l]; a 16-quant bsum
+// is a quad reduction.  No barrier.
+template <int BPW, class Row>
+__device__ __forceinline__ void quantize_blocks(const float4 (&v)[BPW], int b0, int step, int nb, Row& s) {
   const int lane = threadIdx.x & 63;
-  int a = max(max(amax_bits(v.x), amax_bits(v.y)), max(amax_bits(v.z), amax_bits(v.w)));
-  a = max(a, dpp_i<DPP_QUAD_1032>(a));
-  a = max(a, dpp_i<DPP_QUAD_2301>(a));
-  a = max(a, dpp_i<DPP_HALF_MIRROR>(a));
-  a = max(a, dpp_i<DPP_MIRROR>(a));
-  a = max(a, dpp_i<DPP_BCAST15, 0xa>(a));
-  a = max(a, dpp_i<DPP_BCAST31, 0xc>(a));
-  const float m = __int_as_float(__builtin_amdgcn_readlane(a, 63));
-  float d = 0.0f, isc = 0.0f;
-  if (m != 0.0f) {
-    d = m / 127.0f;
-    isc = 127.0f / m;
-  }
-  const int q0 = quant1(v.x, isc, m), q1 = quant1(v.y, isc, m);
-  const int q2 = quant1(v.z, isc, m), q3 = quant1(v.w, isc, m);
-  s.q[b][lane] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
-                 ((uint32_t)(q3 & 0xff) << 24);
-  int bsum = (q0 + q1) + (q2 + q3);
-  bsum += dpp_i<DPP_QUAD_1032>(bsum);
-  bsum += dpp_i<DPP_QUAD_2301>(bsum);
-  if ((lane & 3) == 0) s.bs[b][lane >> 2] = bsum;
-  if (lane == 0) s.d[b] = d;
-}
-
-// Quantise NB blocks of a row held as float4 per lane by NW waves: wave w
-// owns blocks w, w+NW, ... (v[i] = elements 4l..4l+3 of block w+NW*i; past
-// the last block a wave holds a copy of block NB-1 and stores nothing).  The
-// blocks of a wave run in lockstep, each step applied to all of them, so
-// their dependent DPP/divide chains overlap.  Ends with a barrier.
-template <int NB, int NW = 4, class Row>
-__device__ __forceinline__ void quantize_row_waves(const float4 (&v)[(NB + NW - 1) / NW], Row& s) {
-  constexpr int BPW = (NB + NW - 1) / NW;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   int a[BPW];
 #pragma unroll
-  for (int i = 0; i < BPW; ++i)
-    a[i] = max(max(amax_bits(v[i].x), amax_bits(v[i].y)), max(amax_bits(v[i].z), amax_bits(v[i].w)));
+  for (int i = 0; i < BPW; ++i) {
+    float am = fmaxf(fmaxf(0.0f, fabsf(v[i].x)), fabsf(v[i].y));
+    am = fmaxf(fmaxf(am, fabsf(v[i].z)), fabsf(v[i].w));
+    a[i] = __float_as_int(am);
+  }
 #pragma unroll
-  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp_i<DPP_QUAD_1032>(a[i]));
+  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp0_i<DPP_QUAD_1032>(a[i]));
 #pragma unroll
-  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp_i<DPP_QUAD_2301>(a[i]));
+  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp0_i<DPP_QUAD_2301>(a[i]));
 #pragma unroll
-  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp_i<DPP_HALF_MIRROR>(a[i]));
+  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp0_i<DPP_HALF_MIRROR>(a[i]));
 #pragma unroll
-  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp_i<DPP_MIRROR>(a[i]));
+  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp0_i<DPP_MIRROR>(a[i]));
 #pragma unroll
-  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp_i<DPP_BCAST15, 0xa>(a[i]));
+  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp0_i<DPP_BCAST15, 0xa>(a[i]));
 #pragma unroll
-  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp_i<DPP_BCAST31, 0xc>(a[i]));
+  for (int i = 0; i < BPW; ++i) a[i] = max(a[i], dpp0_i<DPP_BCAST31, 0xc>(a[i]));
   float m[BPW], d[BPW], isc[BPW];
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
     m[i] = __int_as_float(__builtin_amdgcn_readlane(a[i], 63));
-    // a zero block keeps d = 0 (its quants are 0 through quant1)
-    d[i] = (m[i] != 0.0f) ? m[i] / 127.0f : 0.0f;
+    d[i] = div127(m[i]);  // 0 for a zero block
     isc[i] = (m[i] != 0.0f) ? 127.0f / m[i] : 0.0f;
   }
   int bsum[BPW];
   uint32_t packed[BPW];
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
-    const int q0 = quant1(v[i].x, isc[i], m[i]), q1 = quant1(v[i].y, isc[i], m[i]);
-    const int q2 = quant1(v[i].z, isc[i], m[i]), q3 = quant1(v[i].w, isc[i], m[i]);
-    packed[i] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
-                ((uint32_t)(q3 & 0xff) << 24);
-    bsum[i] = (q0 + q1) + (q2 + q3);
+    const int q0 = quant1(v[i].x, isc[i]), q1 = quant1(v[i].y, isc[i]);
+    const int q2 = quant1(v[i].z, isc[i]), q3 = quant1(v[i].w, isc[i]);
+    const bool live = (m[i] != 0.0f);  // a zero block quantises to zeros
+    packed[i] = live ? ((uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+                        ((uint32_t)(q3 & 0xff) << 24))
+                     : 0u;
+    bsum[i] = live ? (q0 + q1) + (q2 + q3) : 0;
   }
 #pragma unroll
-  for (int i = 0; i < BPW; ++i) bsum[i] += dpp_i<DPP_QUAD_1032>(bsum[i]);
+  for (int i = 0; i < BPW; ++i) bsum[i] += dpp0_i<DPP_QUAD_1032>(bsum[i]);
 #pragma unroll
-  for (int i = 0; i < BPW; ++i) bsum[i] += dpp_i<DPP_QUAD_2301>(bsum[i]);
+  for (int i = 0; i < BPW; ++i) bsum[i] += dpp0_i<DPP_QUAD_2301>(bsum[i]);
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
-    const int b = wave + NW * i;
-    if (b < NB) {
+    const int b = b0 + step * i;
+    if (b < nb) {
       s.q[b][lane] = packed[i];
       if ((lane & 3) == 0) s.bs[b][lane >> 2] = bsum[i];
       if (lane == 0) s.d[b] = d[i];
     }
   }
+}
+
+// Block b of a row by one wave (lane l: elements 4l..4l+3).
+template <class Row>
+__device__ __forceinline__ void quantize_wave(const float4& v, int b, Row& s) {
+  const float4 vv[1] = {v};
+  quantize_blocks<1>(vv, b, 0, b + 1, s);
+}
+
+// NB blocks of a row by NW waves: wave w owns blocks w, w+NW, ... (v[i] =
+// elements 4l..4l+3 of block w+NW*i; past the last block a wave holds a copy
+// of block NB-1).  Ends with a barrier.
+template <int NB, int NW = 4, class Row>
+__device__ __forceinline__ void quantize_row_waves(const float4 (&v)[(NB + NW - 1) / NW], Row& s) {
+  quantize_blocks<(NB + NW - 1) / NW>(v, (int)(threadIdx.x >> 6), NW, NB, s);
   __syncthreads();
 }
 
-// The same quantiser writing the reference's 292-byte Q8_K block: one
-// workgroup (256 threads) per block.
+// The same quantiser writing the reference's 292-byte Q8_K blocks (f32 d,
+// 256 int8 quants, 16 int16 bsums): one wave per block, four blocks per
+// workgroup.
 __global__ void __launch_bounds__(256) k_quantize_q8k(const float* __restrict__ x, int nb, uint8_t* __restrict__ y) {
-  __shared__ float red[4];
-  const int b = blockIdx.x;
-  if (b >= nb) return;
-  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-  const float v = x[(size_t)b * QK_K + t];
-  float m = wave_max_dpp(abs_branch(v));
-  if (lane == 0) red[wave] = m;
+  __shared__ Q8KRow<4> s;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int b = (int)blockIdx.x * 4 + wave;
+  const float4 v[1] = {reinterpret_cast<const float4*>(x + (size_t)min(b, nb - 1) * QK_K)[lane]};
+  quantize_blocks<1>(v, wave, 0, b < nb ? wave + 1 : 0, s);
   __syncthreads();
-  m = fmax_gt(fmax_gt(fmax_gt(red[0], red[1]), red[2]), red[3]);
+  if (b >= nb) return;
   uint8_t* yb = y + (size_t)b * BS_Q8K;
-  int q = 0;
-  float d = 0.0f;
-  if (m != 0.0f) {
-    d = m / 127.0f;
-    float tq = v * (127.0f / m);
-    float r = (tq >= 0.0f) ? (tq + 0.5f) : (tq - 0.5f);
-    q = go_f32_to_int_clamped127(r);
-  }
-  yb[4 + t] = (uint8_t)(int8_t)q;
-  int bsum = row16_sum_dpp(q);
-  if ((t & 15) == 0) reinterpret_cast<int16_t*>(yb + 260)[t >> 4] = (int16_t)bsum;
-  if (t == 0) *reinterpret_cast<float*>(yb) = d;
+  reinterpret_cast<uint32_t*>(yb + 4)[lane] = s.q[wave][lane];
+  if (lane < 16) reinterpret_cast<int16_t*>(yb + 260)[lane] = (int16_t)s.bs[wave][lane];
+  if (lane == 0) *reinterpret_cast<float*>(yb) = s.d[wave];
 }
 
 // ------------------------------------------------------------ RMSNorm (A8)

@@ -193,7 +193,8 @@ int c2h_pack_weights(int32_t ggml_type, int64_t rows, int64_t cols, const void* 
 
 /* Device-pointer forms for device-resident pipelines and measurement; they
  * run on the context stream and return without synchronising
- * (c2h_sync waits).  w_packed is in the c2h_pack_weights layout. */
+ * (c2h_sync waits).  w_packed is in the c2h_pack_weights layout; x of
+ * c2h_quantize_q8k_dev is 16-byte aligned (C2H_ERR_INVALID otherwise). */
 int c2h_quantize_q8k_dev(c2h_ctx* ctx, const float* x, int32_t cols, void* q8k_out);
 int c2h_gemv_dev(c2h_ctx* ctx, int32_t ggml_type, const void* w_packed, const void* xq, int32_t rows, int32_t cols,
                  float* y, int32_t* isums_out);

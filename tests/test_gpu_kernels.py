@@ -45,6 +45,47 @@ def test_quantize_q8k_edge_cases(ctx):
     assert np.array_equal(ctx.quantize_q8k(t), O.quantize_row_q8k(t))
 
 
+def special_blocks():
+    """Blocks that reach every branch of the quantiser: an infinite amax
+    (d = Inf, isc = 0, Inf*0 = NaN quants), a signalling NaN (skipped by the
+    amax like a quiet one), an amax below 127/FLT_MAX (isc = Inf, so x*isc is
+    +-Inf or NaN), an all -0 block (zero block), and exact halves (amax 127,
+    isc 1: x = k + 0.5 rounds away from zero)."""
+    rng = np.random.default_rng(77)
+    blocks = []
+    b = rng.normal(size=256).astype(np.float32)
+    b[3] = np.inf
+    blocks.append(b)
+    b = rng.normal(size=256).astype(np.float32)
+    b[9] = -np.inf
+    b[10] = np.nan
+    blocks.append(b)
+    b = rng.normal(size=256).astype(np.float32)
+    b.view(np.uint32)[17] = 0x7F800001  # signalling NaN
+    b.view(np.uint32)[18] = 0xFFC00001  # negative quiet NaN
+    blocks.append(b)
+    b = (rng.normal(size=256) * 1e-38).astype(np.float32)  # amax ~ 3e-38 < 127/FLT_MAX
+    b[0] = 0.0
+    b[1] = -0.0
+    blocks.append(b)
+    blocks.append(np.full(256, -0.0, np.float32))
+    b = np.clip((np.arange(256, dtype=np.float32) - 128.0) + 0.5, -126.5, 126.5)
+    b[0] = 127.0
+    blocks.append(b.astype(np.float32))
+    b = np.full(256, np.nan, np.float32)  # NaNs only: amax 0, a zero block
+    blocks.append(b)
+    return np.concatenate(blocks)
+
+
+def test_quantize_q8k_special_blocks(ctx):
+    x = special_blocks()
+    assert np.array_equal(ctx.quantize_q8k(x), O.quantize_row_q8k(x))
+    # the same blocks in every position of a four-block workgroup
+    for shift in (1, 2, 3):
+        y = np.concatenate([np.zeros(256 * shift, np.float32), x])
+        assert np.array_equal(ctx.quantize_q8k(y), O.quantize_row_q8k(y))
+
+
 SHAPES_Q4K = [(896, 896), (128, 896), (4864, 896), (896, 4864), (7, 512)]
 
 
