@@ -66,8 +66,9 @@ struct c2h_ctx {
   int32_t* tok_host = nullptr;     // pinned
   unsigned ring_next = 0;
 
-  // graphs [0] attend with k_attn_core, [1] with the long-context kernels
-  hipGraphExec_t g_step[2] = {nullptr, nullptr}, g_fwd[2] = {nullptr, nullptr};
+  // graphs by attention form (AttnForm): k_attn_core for up to 128, up to
+  // 256 and up to att_split positions, the long-context kernels beyond
+  hipGraphExec_t g_step[4] = {}, g_fwd[4] = {};
   bool graphs_ready = false;
   bool use_graphs = true;
   size_t attn_lds = 0;
@@ -112,6 +113,17 @@ int fail(c2h_ctx* c, int code, const char* fmt, ...) {
     hipError_t e_ = (call);                                                                             \
     if (e_ != hipSuccess) return fail((c), C2H_ERR_HIP, "%s failed: %s", #call, hipGetErrorString(e_)); \
   } while (0)
+
+// Host<->device copies go on the context stream and complete before
+// returning: a plain hipMemcpy runs on the null stream, which the
+// (non-blocking) context stream does not wait for, and from pageable memory
+// it may return before its DMA lands -- a kernel launched next on the
+// context stream could read the old bytes.
+inline hipError_t stream_copy(hipStream_t st, void* dst, const void* src, size_t bytes, hipMemcpyKind kind) {
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, st);
+  if (e != hipSuccess) return e;
+  return hipStreamSynchronize(st);
+}
 
 template <class T>
 int dalloc(c2h_ctx* c, T** p, size_t bytes) {
@@ -222,11 +234,11 @@ int upload_quant(c2h_ctx* c, Tensor* t, int type, int64_t rows, int64_t cols, co
   pack_host(type, rows, cols, reinterpret_cast<const uint8_t*>(host), qh.data(), dh.data());
   uint8_t* q;
   if ((rc = dalloc(c, &q, qb))) return rc;
-  HIPCHK(c, hipMemcpy(q, qh.data(), qb, hipMemcpyHostToDevice));
+  HIPCHK(c, stream_copy(c->stream, q, qh.data(), qb, hipMemcpyHostToDevice));
   uint16_t* d = nullptr;
   if (db) {
     if ((rc = dalloc(c, &d, db))) return rc;
-    HIPCHK(c, hipMemcpy(d, dh.data(), db, hipMemcpyHostToDevice));
+    HIPCHK(c, stream_copy(c->stream, d, dh.data(), db, hipMemcpyHostToDevice));
   }
   t->q = q;
   t->d = d;
@@ -245,7 +257,7 @@ int upload_f32(c2h_ctx* c, float** dst, int64_t n_expected, int type, int64_t ro
                 (long long)n_expected);
   int rc;
   if (!*dst && (rc = dalloc(c, dst, (size_t)n_expected * 4))) return rc;
-  HIPCHK(c, hipMemcpy(*dst, host, (size_t)n_expected * 4, hipMemcpyHostToDevice));
+  HIPCHK(c, stream_copy(c->stream, *dst, host, (size_t)n_expected * 4, hipMemcpyHostToDevice));
   c->graphs_ready = false;
   return C2H_OK;
 }
@@ -425,6 +437,27 @@ void enqueue_attn_long(c2h_ctx* c, const AttnCoreParams& A, int ntok) {
                      A);
 }
 
+// Attention forms of a decode step by the positions T it attends to:
+// k_attn_core sized for T <= 128, T <= 256, T <= att_split, and the
+// long-context kernels past the split.
+enum : int { ATT_FORM_128 = 0, ATT_FORM_256 = 1, ATT_FORM_CORE = 2, ATT_FORM_LONG = 3, ATT_FORMS = 4 };
+
+int attn_form(const c2h_ctx* c, int T) {
+  if (c->long_attn && T > c->att_split) return ATT_FORM_LONG;
+  return T <= 128 ? ATT_FORM_128 : (T <= 256 ? ATT_FORM_256 : ATT_FORM_CORE);
+}
+
+// Whether some decode position of this context runs the form.
+bool form_used(const c2h_ctx* c, int form) {
+  const int tmax = c->long_attn ? c->att_split : c->desc.max_ctx;  // largest T of the core forms
+  switch (form) {
+    case ATT_FORM_128: return true;
+    case ATT_FORM_256: return tmax > 128;
+    case ATT_FORM_CORE: return tmax > 256;
+    default: return c->long_attn;
+  }
+}
+
 // One projection of a layer (w2: the paired up matrix of SwiGLU).
 struct ProjJob {
   const Tensor* w;
@@ -464,8 +497,8 @@ void launch_group(c2h_ctx* c, std::initializer_list<ProjJob> jobs, int pro, int 
 
 // The 24-layer body of engine.Forward plus the final RMSNorm; layer 0 embeds
 // either state->token (forward) or the argmax of the vocab partials (step).
-// long_attn selects the long-context attention kernels.
-void enqueue_layers(c2h_ctx* c, bool from_argmax, bool long_attn) {
+// form selects the attention kernels.
+void enqueue_layers(c2h_ctx* c, bool from_argmax, int form) {
   const c2h_model_desc& D = c->desc;
   const int E = D.n_embd;
   for (int l = 0; l < D.n_layers; ++l) {
@@ -481,11 +514,15 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax, bool long_attn) {
       A.v = c->v;
       A.out = c->attn;
       A.store_kv = 1;
-      if (long_attn)
+      const dim3 grid(D.n_heads / D.n_kv_heads, D.n_kv_heads);
+      if (form == ATT_FORM_LONG)
         enqueue_attn_long(c, A, 1);
+      else if (form == ATT_FORM_128)
+        hipLaunchKernelGGL(k_attn_core<ATT_TIER_128>, grid, dim3(256), c->attn_lds, c->stream, A);
+      else if (form == ATT_FORM_256)
+        hipLaunchKernelGGL(k_attn_core<ATT_TIER_256>, grid, dim3(256), c->attn_lds, c->stream, A);
       else
-        hipLaunchKernelGGL(k_attn_core, dim3(D.n_heads / D.n_kv_heads, D.n_kv_heads), dim3(256), c->attn_lds,
-                           c->stream, A);
+        hipLaunchKernelGGL(k_attn_core<ATT_TIER_ANY>, grid, dim3(256), c->attn_lds, c->stream, A);
     }
     // attn_out: X += Wo * x(attn)
     launch_group(c, {{&L.wo, nullptr, c->X, nullptr}}, PRO_QUANT, MODE_RESID, c->attn, E, nullptr);
@@ -508,9 +545,9 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax, bool long_attn) {
   hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), (size_t)N.n_lds * sizeof(float), c->stream, N);
 }
 
-void enqueue_step(c2h_ctx* c, bool long_attn) {
+void enqueue_step(c2h_ctx* c, int form) {
   enqueue_vocab(c, 1, nullptr, 1, nullptr);
-  enqueue_layers(c, true, long_attn);
+  enqueue_layers(c, true, form);
 }
 
 int validate_model(c2h_ctx* c) {
@@ -543,7 +580,7 @@ int validate_model(c2h_ctx* c) {
 }
 
 void destroy_graphs(c2h_ctx* c) {
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < ATT_FORMS; ++t) {
     if (c->g_step[t]) (void)hipGraphExecDestroy(c->g_step[t]);
     if (c->g_fwd[t]) (void)hipGraphExecDestroy(c->g_fwd[t]);
     c->g_step[t] = c->g_fwd[t] = nullptr;
@@ -556,19 +593,20 @@ int build_graphs(c2h_ctx* c) {
   if (rc) return rc;
   destroy_graphs(c);
   if (c->use_graphs) {
-    for (int tier = 0; tier < (c->long_attn ? 2 : 1); ++tier) {
+    for (int form = 0; form < ATT_FORMS; ++form) {
+      if (!form_used(c, form)) continue;
       for (int which = 0; which < 2; ++which) {
         hipGraph_t g;
         HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
         if (which == 0)
-          enqueue_step(c, tier == 1);
+          enqueue_step(c, form);
         else
-          enqueue_layers(c, false, tier == 1);
+          enqueue_layers(c, false, form);
         HIPCHK(c, hipStreamEndCapture(c->stream, &g));
         hipGraphExec_t ge;
         HIPCHK(c, hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
         (void)hipGraphDestroy(g);
-        (which == 0 ? c->g_step : c->g_fwd)[tier] = ge;
+        (which == 0 ? c->g_step : c->g_fwd)[form] = ge;
       }
     }
   }
@@ -586,17 +624,16 @@ int push_state(c2h_ctx* c, const C2hState& s) {
   return C2H_OK;
 }
 
-// Decode at `pos` attends to pos+1 positions: the long-context kernels
-// take over past the split length.
+// Decode at `pos` attends to pos+1 positions.
 int run_graph(c2h_ctx* c, bool step, int pos) {
-  const bool long_attn = c->long_attn && pos + 1 > c->att_split;
+  const int form = attn_form(c, pos + 1);
   if (c->use_graphs) {
-    HIPCHK(c, hipGraphLaunch(step ? c->g_step[long_attn] : c->g_fwd[long_attn], c->stream));
+    HIPCHK(c, hipGraphLaunch(step ? c->g_step[form] : c->g_fwd[form], c->stream));
   } else {
     if (step)
-      enqueue_step(c, long_attn);
+      enqueue_step(c, form);
     else
-      enqueue_layers(c, false, long_attn);
+      enqueue_layers(c, false, form);
     HIPCHK(c, hipGetLastError());
   }
   return C2H_OK;
@@ -630,7 +667,7 @@ int v_rows_copy(c2h_ctx* c, int layer, int kv_head, int pos0, int n, float* rows
   const int q0 = pos0 >> 2, q1 = (pos0 + n + 3) >> 2;
   std::vector<float> quads((size_t)(q1 - q0) * 256);
   float* dev = c->kv + kv_slot_offset(D, 1, layer, kv_head) + (size_t)q0 * 256;
-  HIPCHK(c, hipMemcpy(quads.data(), dev, quads.size() * 4, hipMemcpyDeviceToHost));
+  HIPCHK(c, stream_copy(c->stream, quads.data(), dev, quads.size() * 4, hipMemcpyDeviceToHost));
   for (int p = pos0; p < pos0 + n; ++p)
     for (int d = 0; d < 64; ++d) {
       float& q = quads[vq_index(p, d) - (size_t)q0 * 256];
@@ -640,7 +677,7 @@ int v_rows_copy(c2h_ctx* c, int layer, int kv_head, int pos0, int n, float* rows
       else
         r = q;
     }
-  if (to_device) HIPCHK(c, hipMemcpy(dev, quads.data(), quads.size() * 4, hipMemcpyHostToDevice));
+  if (to_device) HIPCHK(c, stream_copy(c->stream, dev, quads.data(), quads.size() * 4, hipMemcpyHostToDevice));
   return C2H_OK;
 }
 
@@ -715,11 +752,13 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
     return bail(rc);
   size_t kv_bytes = (size_t)2 * D.n_layers * D.n_kv_heads * kv_slot(D.max_ctx) * D.head_dim * 4;
   if ((rc = dalloc(c, &c->kv, kv_bytes))) return bail(rc);
-  if (hipMemset(c->kv, 0, kv_bytes) != hipSuccess) return bail(fail(c, C2H_ERR_HIP, "hipMemset kv"));
   if ((rc = dalloc(c, &c->token_ids, (size_t)D.max_ctx * 4))) return bail(rc);
-  if (hipMemset(c->token_ids, 0, (size_t)D.max_ctx * 4) != hipSuccess) return bail(fail(c, C2H_ERR_HIP, "memset"));
-  if (hipMemset(c->normx[0], 0, E * 4) != hipSuccess || hipMemset(c->normx[1], 0, E * 4) != hipSuccess)
-    return bail(fail(c, C2H_ERR_HIP, "memset"));
+  // cleared on the context stream (before any of its work), finished here
+  if (hipMemsetAsync(c->kv, 0, kv_bytes, c->stream) != hipSuccess ||
+      hipMemsetAsync(c->token_ids, 0, (size_t)D.max_ctx * 4, c->stream) != hipSuccess ||
+      hipMemsetAsync(c->normx[0], 0, E * 4, c->stream) != hipSuccess ||
+      hipMemsetAsync(c->normx[1], 0, E * 4, c->stream) != hipSuccess || hipStreamSynchronize(c->stream) != hipSuccess)
+    return bail(fail(c, C2H_ERR_HIP, "clearing the KV cache and state"));
   // RoPE table, tensor.NewRoPETable (tensor/ops.go:237-257) in float64
   {
     int half = D.head_dim / 2;
@@ -732,8 +771,8 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
         sn[(size_t)p * half + i] = (float)std::sin(val);
       }
     if ((rc = dalloc(c, &c->rope_cos, cs.size() * 4)) || (rc = dalloc(c, &c->rope_sin, sn.size() * 4))) return bail(rc);
-    if (hipMemcpy(c->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(c->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+    if (stream_copy(c->stream, c->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        stream_copy(c->stream, c->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
       return bail(fail(c, C2H_ERR_HIP, "rope upload"));
   }
   int tiles = (D.n_vocab + 31) / 32;
@@ -751,9 +790,13 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   c->att_split = std::min(c->att_split, D.max_ctx);
   c->long_attn = D.max_ctx > c->att_split;
   c->attn_lds = (size_t)attn_lds_floats(c->att_split) * 4;
-  if (hipFuncSetAttribute((const void*)k_attn_core, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->attn_lds) !=
-      hipSuccess)
-    return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
+  {
+    const void* cores[] = {(const void*)k_attn_core<ATT_TIER_128>, (const void*)k_attn_core<ATT_TIER_256>,
+                           (const void*)k_attn_core<ATT_TIER_ANY>};
+    for (const void* k : cores)
+      if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->attn_lds) != hipSuccess)
+        return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
+  }
   if (c->long_attn) {
     if (D.max_ctx > ATT_LONG_MAX_CTX)
       return bail(fail(c, C2H_ERR_UNSUPPORTED, "max_ctx %d above the %d positions of the exact attention kernels",
@@ -847,7 +890,7 @@ int c2h_set_token_ids(c2h_ctx* c, int32_t pos0, const int32_t* ids, int32_t n) {
   if (pos0 < 0 || n < 0 || pos0 + n > c->desc.max_ctx) return fail(c, C2H_ERR_RANGE, "token ids out of range");
   HIPCHK(c, hipSetDevice(c->device));
   HIPCHK(c, hipStreamSynchronize(c->stream));
-  if (n) HIPCHK(c, hipMemcpy(c->token_ids + pos0, ids, (size_t)n * 4, hipMemcpyHostToDevice));
+  if (n) HIPCHK(c, stream_copy(c->stream, c->token_ids + pos0, ids, (size_t)n * 4, hipMemcpyHostToDevice));
   return C2H_OK;
 }
 
@@ -1047,7 +1090,8 @@ int pf_pass(c2h_ctx* c, const int32_t* tokens, int m, int pos0) {
       A.store_kv = 0;
       if (pos0 + m <= c->att_split) {
         const size_t lds = (size_t)attn_lds_floats(pos0 + m) * 4;
-        hipLaunchKernelGGL(k_attn_core, dim3(D.n_heads / D.n_kv_heads, D.n_kv_heads, m), dim3(256), lds, c->stream, A);
+        hipLaunchKernelGGL(k_attn_core<ATT_TIER_ANY>, dim3(D.n_heads / D.n_kv_heads, D.n_kv_heads, m), dim3(256), lds,
+                           c->stream, A);
       } else {
         for (int t0 = 0; t0 < m; t0 += PF_ATT_SUB) {
           A.tok0 = t0;
@@ -1118,7 +1162,8 @@ int c2h_prefill(c2h_ctx* c, const int32_t* tokens, int32_t n, int32_t pos0, floa
     c->seq_len = pos0 + done;
   }
   if (normx_out)
-    HIPCHK(c, hipMemcpy(normx_out, c->normx[c->nx_cur], (size_t)c->desc.n_embd * 4, hipMemcpyDeviceToHost));
+    HIPCHK(c, stream_copy(c->stream, normx_out, c->normx[c->nx_cur], (size_t)c->desc.n_embd * 4,
+                          hipMemcpyDeviceToHost));
   return C2H_OK;
 }
 
@@ -1191,7 +1236,7 @@ int c2h_get_kv(c2h_ctx* c, int32_t which, int32_t layer, int32_t kv_head, int32_
   HIPCHK(c, hipStreamSynchronize(c->stream));
   if (n == 0) return C2H_OK;
   if (which == 1) return v_rows_copy(c, layer, kv_head, 0, n, out, false);
-  HIPCHK(c, hipMemcpy(out, c->kv + kv_slot_offset(D, 0, layer, kv_head), (size_t)n * D.head_dim * 4,
+  HIPCHK(c, stream_copy(c->stream, out, c->kv + kv_slot_offset(D, 0, layer, kv_head), (size_t)n * D.head_dim * 4,
                       hipMemcpyDeviceToHost));
   return C2H_OK;
 }
@@ -1205,7 +1250,7 @@ int c2h_set_kv(c2h_ctx* c, int32_t which, int32_t layer, int32_t kv_head, int32_
   HIPCHK(c, hipStreamSynchronize(c->stream));
   if (n == 0) return C2H_OK;
   if (which == 1) return v_rows_copy(c, layer, kv_head, pos0, n, const_cast<float*>(src), true);
-  HIPCHK(c, hipMemcpy(c->kv + kv_slot_offset(D, 0, layer, kv_head) + (size_t)pos0 * D.head_dim, src,
+  HIPCHK(c, stream_copy(c->stream, c->kv + kv_slot_offset(D, 0, layer, kv_head) + (size_t)pos0 * D.head_dim, src,
                       (size_t)n * D.head_dim * 4, hipMemcpyHostToDevice));
   return C2H_OK;
 }
@@ -1216,7 +1261,7 @@ int c2h_get_token_ids(c2h_ctx* c, int32_t pos0, int32_t n, int32_t* out) {
   if (pos0 < 0 || n < 0 || (int64_t)pos0 + n > c->desc.max_ctx) return fail(c, C2H_ERR_RANGE, "token ids out of range");
   HIPCHK(c, hipSetDevice(c->device));
   HIPCHK(c, hipStreamSynchronize(c->stream));
-  if (n) HIPCHK(c, hipMemcpy(out, c->token_ids + pos0, (size_t)n * 4, hipMemcpyDeviceToHost));
+  if (n) HIPCHK(c, stream_copy(c->stream, out, c->token_ids + pos0, (size_t)n * 4, hipMemcpyDeviceToHost));
   return C2H_OK;
 }
 
@@ -1353,10 +1398,11 @@ int c2h_quantize_q8k(c2h_ctx* c, const float* x, int32_t cols, void* q8k_out) {
     return fail(c, C2H_ERR_HIP, "hipMalloc");
   }
   int rc = C2H_OK;
-  if (hipMemcpy(dx, x, (size_t)nb * 256 * 4, hipMemcpyHostToDevice) != hipSuccess) rc = C2H_ERR_HIP;
+  if (stream_copy(c->stream, dx, x, (size_t)nb * 256 * 4, hipMemcpyHostToDevice) != hipSuccess) rc = C2H_ERR_HIP;
   if (!rc) rc = c2h_quantize_q8k_dev(c, dx, cols, dy);
   if (!rc && hipStreamSynchronize(c->stream) != hipSuccess) rc = C2H_ERR_HIP;
-  if (!rc && hipMemcpy(q8k_out, dy, (size_t)nb * BS_Q8K, hipMemcpyDeviceToHost) != hipSuccess) rc = C2H_ERR_HIP;
+  if (!rc && stream_copy(c->stream, q8k_out, dy, (size_t)nb * BS_Q8K, hipMemcpyDeviceToHost) != hipSuccess)
+    rc = C2H_ERR_HIP;
   (void)hipFree(dx);
   (void)hipFree(dy);
   if (rc == C2H_ERR_HIP) return fail(c, rc, "quantize copy failed");
@@ -1395,14 +1441,14 @@ int c2h_gemv(c2h_ctx* c, int32_t type, const void* w, const void* xq, int32_t ro
     return fail(c, C2H_ERR_HIP, "hipMalloc failed");
   }
   rc = C2H_OK;
-  if (hipMemcpy(dw, packed.data(), pbytes, hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemcpy(dx, xq, xbytes, hipMemcpyHostToDevice) != hipSuccess)
+  if (stream_copy(c->stream, dw, packed.data(), pbytes, hipMemcpyHostToDevice) != hipSuccess ||
+      stream_copy(c->stream, dx, xq, xbytes, hipMemcpyHostToDevice) != hipSuccess)
     rc = fail(c, C2H_ERR_HIP, "copy in failed");
   if (!rc) rc = c2h_gemv_dev(c, type, dw, dx, rows, cols, dy, di);
   if (!rc && c2h_sync(c)) rc = C2H_ERR_HIP;
-  if (!rc && hipMemcpy(y, dy, (size_t)rows * 4, hipMemcpyDeviceToHost) != hipSuccess)
+  if (!rc && stream_copy(c->stream, y, dy, (size_t)rows * 4, hipMemcpyDeviceToHost) != hipSuccess)
     rc = fail(c, C2H_ERR_HIP, "copy out failed");
-  if (!rc && isz && hipMemcpy(isums_out, di, isz, hipMemcpyDeviceToHost) != hipSuccess)
+  if (!rc && isz && stream_copy(c->stream, isums_out, di, isz, hipMemcpyDeviceToHost) != hipSuccess)
     rc = fail(c, C2H_ERR_HIP, "copy out failed");
   cleanup();
   return rc;

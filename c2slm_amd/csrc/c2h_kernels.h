@@ -140,6 +140,13 @@ __host__ __device__ inline size_t vq_index(int p, int d) { return ((size_t)(p >>
 //     one wave runs the FMA chains, the others stage V through LDS).
 constexpr int ATT_CH = 128;   // V positions staged in LDS per pass (chunk 0 prefetched)
 constexpr int ATT_KPF = 256;  // positions whose K row is prefetched (one per thread)
+// k_attn_core instances by the context they prefetch for: up to 128 and up
+// to 256 positions attended (the prefetch covers all of K and V), or any
+// context up to the split length.
+constexpr int ATT_TIER_ANY = 0;
+constexpr int ATT_TIER_128 = 1;
+constexpr int ATT_TIER_256 = 2;
+__host__ __device__ inline int attn_tier(int T) { return T <= 128 ? ATT_TIER_128 : (T <= 256 ? ATT_TIER_256 : ATT_TIER_ANY); }
 constexpr int ATT_SPLIT_T = 1024;  // default split length (positions attended)
 constexpr int ATT_SB = 256;        // positions per k_attn_scores workgroup
 constexpr int ATT_AV_CH = 256;     // positions per k_attn_av LDS chunk
@@ -297,6 +304,7 @@ __host__ __device__ inline int gemv_f_lds_floats(int n_x) {
   return (n_x / 32) * GF_XPAD + (n_x / 32) * 32 + chain_lds_floats(n_x);
 }
 __global__ void k_rmsnorm(NormParams P);
+template <int TIER>
 __global__ void k_attn_core(AttnCoreParams P);
 __global__ void k_attn_scores(AttnCoreParams P);
 __global__ void k_attn_softmax(AttnCoreParams P);

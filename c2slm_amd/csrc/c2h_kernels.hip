@@ -1214,6 +1214,7 @@ struct VStage {
   f32x4_t r[PER];
 };
 
+template <int TIER>
 __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   constexpr int HD = 64;
   constexpr int NQ = ATT_CH / 4;    // quads (four V rows) per chunk
@@ -1260,21 +1261,44 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   const float rcos = P.rope_cos[(size_t)rp * (HD / 2) + (tid & 31)];
   const float rsin = P.rope_sin[(size_t)rp * (HD / 2) + (tid & 31)];
   issue_fence();  // q/k/v and the RoPE row are needed first: issue them first
-  float4 kreg[16], kreg2[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const f32x4_t t = cache_ld4(krs, tid * HD * 4 + i * 16);
-    kreg[i] = make_float4(t.x, t.y, t.z, t.w);
-  }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const f32x4_t t = cache_ld4(krs, (tid + ATT_KPF) * HD * 4 + i * 16);
-    kreg2[i] = make_float4(t.x, t.y, t.z, t.w);
-  }
+  // The prefetch is sized to the tier's context (every thread issues the
+  // same loads, so the compiler's memory-counter waits stay exact):
+  //   ATT_TIER_128: waves 0-1 hold K rows 0..127, waves 2-3 V quads 0..31
+  //                 (V chunk 0);
+  //   ATT_TIER_256: K rows 0..255 and V quads 0..63 (chunks 0 and 1, both
+  //                 LDS buffers);
+  //   ATT_TIER_ANY: K rows 0..511 and V chunk 0, later rows and V chunks
+  //                 streamed.
+  constexpr int VQW = (TIER == ATT_TIER_256) ? 2 * VPT : VPT;  // V quads per wave
   const int wave = tid >> 6;
-  f32x4_t vreg[VPT];  // native vectors: a float4 array copied whole is kept in scratch
+  float4 kreg[16], kreg2[16];
+  f32x4_t vreg[VQW];  // native vectors: a float4 array copied whole is kept in scratch
+  if constexpr (TIER == ATT_TIER_128) {
+    const int uw = __builtin_amdgcn_readfirstlane(wave);
+    const bool kw = uw < 2;
+    const __amdgpu_buffer_rsrc_t rs = kw ? krs : vrs;
 #pragma unroll
-  for (int i = 0; i < VPT; ++i) vreg[i] = vquad_load_buf(vrs, wave + 4 * i);
+    for (int i = 0; i < 16; ++i) {
+      const int off = kw ? tid * HD * 4 + i * 16 : (((uw - 2) + 2 * i) * 64 + (tid & 63)) * 16;
+      const f32x4_t t = cache_ld4(rs, off);
+      kreg[i] = make_float4(t.x, t.y, t.z, t.w);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const f32x4_t t = cache_ld4(krs, tid * HD * 4 + i * 16);
+      kreg[i] = make_float4(t.x, t.y, t.z, t.w);
+    }
+    if constexpr (TIER == ATT_TIER_ANY) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const f32x4_t t = cache_ld4(krs, (tid + ATT_KPF) * HD * 4 + i * 16);
+        kreg2[i] = make_float4(t.x, t.y, t.z, t.w);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VQW; ++i) vreg[i] = vquad_load_buf(vrs, wave + 4 * i);
+  }
   issue_fence();
 
   if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;
@@ -1316,7 +1340,7 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
     if (tid < T) sc[tid] = sco;
     lmax = (tid < T && sco > lmax) ? sco : lmax;
   }
-  {
+  if constexpr (TIER == ATT_TIER_ANY) {
     const int p2 = tid + ATT_KPF;
     if (p2 == pos) {
 #pragma unroll
@@ -1326,7 +1350,7 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
     if (p2 < T) sc[p2] = sco;
     lmax = (p2 < T && sco > lmax) ? sco : lmax;
   }
-  for (int p = tid + 2 * ATT_KPF; p < T; p += ATT_KPF) {
+  for (int p = tid + 2 * ATT_KPF; TIER == ATT_TIER_ANY && p < T; p += ATT_KPF) {
     const float4* kr = (p == pos) ? ks4 : reinterpret_cast<const float4*>(kcache + (size_t)p * HD);
     float4 kk4[16];
 #pragma unroll
@@ -1356,8 +1380,19 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
       const float ssum = seq_sum_wave_n(sc, T);
       if (tid == 0) inv_slot = 1.0f / ssum;
     }
+    if constexpr (TIER == ATT_TIER_128) {
+      if (wave >= 2) {
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) vbuf[(wave + 4 * i) * HD + (tid & 63)] = vreg[i];
+        for (int i = 0; i < 16; ++i) {
+          const float4 t = kreg[i];
+          f32x4_t q4 = {t.x, t.y, t.z, t.w};
+          vbuf[((wave - 2) + 2 * i) * HD + (tid & 63)] = q4;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < VQW; ++i) vbuf[(wave + 4 * i) * HD + (tid & 63)] = vreg[i];
+    }
     __syncthreads();
     const float inv = inv_slot;
     for (int p = tid; p < T; p += blockDim.x) sc[p] = sc[p] * inv;
@@ -1367,9 +1402,9 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   // ---- AV: out[d] = fma chain over p of (prob[p], V[p][d]); V[pos] is v_s.
   float acc = 0.0f;
   const int d = tid & 63;
-  if (nch <= 1) {
+  if (TIER != ATT_TIER_ANY || nch <= 1) {  // V[0, pos) already in LDS
     softmax();
-    if (tid < HD && nch == 1) acc = av_chain_q(sc, vbuf, pos, d, acc);
+    if (tid < HD && pos > 0) acc = av_chain_q(sc, vbuf, pos, d, acc);
   } else {
     // Chunk c sits in LDS buffer c & 1; chunk c+1 waits in register set
     // c % 3.  Chunks 1..3 start loading under the softmax.  Every thread
@@ -1428,6 +1463,9 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
     P.out[(size_t)ti * P.out_ld + h * HD + d] = acc;
   }
 }
+template __global__ void k_attn_core<ATT_TIER_128>(AttnCoreParams);
+template __global__ void k_attn_core<ATT_TIER_256>(AttnCoreParams);
+template __global__ void k_attn_core<ATT_TIER_ANY>(AttnCoreParams);
 
 
 // ------------------------------------------- attention, long contexts

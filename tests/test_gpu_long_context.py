@@ -85,6 +85,19 @@ def check_decode(ctx, orc, pos, im_end, eos, steps):
     assert np.array_equal(bits(ctx.normx()), bits(nx))
 
 
+# ---- the short-context forms of k_attn_core: prefetch sized for up to 128
+# and up to 256 attended positions, and the general form; decode crosses
+# each boundary mid-stream (tiny model, default split)
+
+@pytest.mark.parametrize("n0", [124, 252])
+def test_core_forms_cross_their_limits(tiny_model_path, n0):
+    gf, ctx, orc, im_end, eos = open_pair(tiny_model_path, max_ctx=1024)
+    fill_cache(ctx, orc, n0, seed=n0)
+    check_decode(ctx, orc, n0, im_end, eos, steps=8)  # T = n0+1 .. n0+9
+    ctx.close()
+    orc.close()
+
+
 # ---- the long-context kernels at small sizes (tiny model, split moved down)
 
 def test_long_kernels_decode_small_split(tiny_model_path):
