@@ -360,10 +360,16 @@ void launch_gemv_f(c2h_ctx* c, GemvParams& P) {
 // A row-kernel launch over all its jobs (same width and mode); the norm
 // prologues need the x*x chain buffer.
 void launch_gemv_row(c2h_ctx* c, GemvParams& P) {
+  const int nt = row_threads(P.jobs[0].nb, P.prologue);
+  for (int j = 0; j < P.n_jobs; ++j) {  // rows per workgroup at this width
+    GemvJob& J = P.jobs[j];
+    J.rpw = nt / (4 * J.nb);
+    J.n_wg = (J.rows + J.rpw - 1) / J.rpw;
+  }
   const GemvJob& J = P.jobs[0];
   GemvKernel k = gemv_row_kernel(J.nb, P.prologue, J.mode);
   size_t lds = (P.prologue != PRO_QUANT) ? (size_t)P.n_x_lds * sizeof(float) : 0;
-  hipLaunchKernelGGL(k, job_grid(P), dim3(256), lds, c->stream, P);
+  hipLaunchKernelGGL(k, job_grid(P), dim3(nt), lds, c->stream, P);
 }
 
 GemvParams base_params(c2h_ctx* c) {

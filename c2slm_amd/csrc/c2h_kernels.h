@@ -82,6 +82,12 @@ struct GemvJob {
 
 constexpr int MAX_JOBS = 4;
 
+// Threads of a row-kernel workgroup.  A wide Q8_K input (12 or more
+// super-blocks, quantised by every workgroup) runs on 8 waves: its blocks
+// quantise at most three per wave with two waves per SIMD, and the
+// workgroup takes twice the rows, which halves the redundant quantisations.
+__host__ __device__ constexpr int row_threads(int nb, int pro) { return (pro == PRO_QUANT && nb >= 12) ? 512 : 256; }
+
 struct GemvParams {
   int prologue;
   int nb_in;

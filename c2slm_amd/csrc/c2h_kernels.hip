@@ -646,10 +646,11 @@ __device__ __forceinline__ GemvJob launch_job(const GemvParams& P) {
 // read the same block of the Q8_K row (broadcast, no bank conflicts).  The
 // fold runs per row in the reference's order.
 template <int NB, int PRO, int MODE>
-__global__ void __launch_bounds__(256) k_gemv_row(GemvParams P) {
-  constexpr int NW = 4;
+__global__ void __launch_bounds__(row_threads(NB, PRO)) k_gemv_row(GemvParams P) {
+  constexpr int NT = row_threads(NB, PRO);
+  constexpr int NW = NT / 64;
   constexpr int IPR = 4 * NB;
-  constexpr int RPW = 256 / IPR;
+  constexpr int RPW = NT / IPR;
   constexpr int BPW = (NB + NW - 1) / NW;  // Q8_K blocks quantised per wave
   constexpr bool PAIRED = (MODE == MODE_SWIGLU);
   constexpr bool NORM = (PRO == PRO_NORM || PRO == PRO_EMBED_NORM || PRO == PRO_ARGMAX_EMBED_NORM);
