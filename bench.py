@@ -244,6 +244,8 @@ def main():
     vocab_b2b_ms = ctx.time_vocab(args.vocab_iters, pos, in_step=False)
     achieved = VOCAB_BYTES / (vocab_ms * 1e-3) / 1e9
     traffic = vocab_traffic()
+    # per-kernel floor of dependent launches in a graph (empty kernels)
+    floor_us = ctx.launch_floor(240, 256, 5)
     if args.copy_calib_mib:
         copy_calibration(ctx, args.copy_calib_mib)
 
@@ -285,6 +287,7 @@ def main():
                      "ms_per_launch": round(vocab_ms, 5)},
         "cpu_baseline": base,
         "extra": {"vocab_ms_back_to_back": round(vocab_b2b_ms, 5),
+                  "launch_floor_us_per_kernel": round(floor_us, 3),
                   "pipelined_ms_per_step": round(pipelined_ms, 4),
                   "pipelined_tok_s": round(1000.0 / pipelined_ms, 1),
                   "prefill_512": prefill,

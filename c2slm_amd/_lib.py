@@ -80,6 +80,7 @@ def lib():
             "c2h_sync": (C.c_int, [VP]),
             "c2h_time_vocab": (C.c_int, [VP, I32, I32, I32, C.POINTER(C.c_float)]),
             "c2h_copy_bench": (C.c_int, [VP, C.c_int64, I32, C.POINTER(C.c_float)]),
+            "c2h_launch_floor": (C.c_int, [VP, I32, I32, I32, C.POINTER(C.c_float)]),
             "c2h_time_steps": (C.c_int, [VP, I32, I32, C.c_float, I32, I32, C.POINTER(C.c_float)]),
         }
         for name, (res, args) in sig.items():
@@ -198,6 +199,12 @@ class Ctx:
         ms = C.c_float()
         self._chk(lib().c2h_copy_bench(self.h, nbytes, reps, C.byref(ms)))
         return ms.value
+
+    def launch_floor(self, n=240, grid=256, reps=5):
+        """Device µs per kernel of a graph of n dependent empty launches."""
+        us = C.c_float()
+        self._chk(lib().c2h_launch_floor(self.h, n, grid, reps, C.byref(us)))
+        return us.value
 
     def time_steps(self, pos: int, iters: int, penalty: float, im_end: int, eos: int) -> float:
         ms = C.c_float()

@@ -328,5 +328,6 @@ __global__ void k_pf_swiglu(const float* gate, const float* up, float* h, int n,
 __global__ void k_vocab(VocabParams P);
 __global__ void k_argmax_final(const float* pv, const int* pi, int n, C2hState* state);
 __global__ void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16);
+__global__ void k_empty(const int* __restrict__ flag, int* __restrict__ out);
 
 }  // namespace c2h

@@ -218,6 +218,12 @@ int c2h_time_vocab(c2h_ctx* ctx, int32_t iters, int32_t pos, int32_t in_step, fl
  * traffic calibrates the memory counters of a profiler run. */
 int c2h_copy_bench(c2h_ctx* ctx, int64_t bytes, int32_t reps, float* ms_per_copy);
 
+/* Measurement aid with no counterpart in the reference: the device time
+ * (µs) per kernel of a captured graph of `n` dependent launches of an empty
+ * kernel (`grid` workgroups of 256 threads), best of `reps` replays -- the
+ * floor a chain of decode kernels pays per launch. */
+int c2h_launch_floor(c2h_ctx* ctx, int32_t n, int32_t grid, int32_t reps, float* us_per_kernel);
+
 /* Average device time (ms) of `iters` decode steps (graph replays) at
  * positions pos, pos+1, ...; tokens are fed back on the device. */
 int c2h_time_steps(c2h_ctx* ctx, int32_t pos, int32_t iters, float penalty, int32_t im_end, int32_t eos,
