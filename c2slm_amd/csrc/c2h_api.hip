@@ -389,6 +389,44 @@ GemvParams base_params(c2h_ctx* c) {
 
 const Tensor& out_weight(c2h_ctx* c) { return c->output.present() ? c->output : c->embd; }
 
+typedef void (*VocabKernel)(VocabParams);
+
+// The vocab kernel instance for rows of nb8 Q8_0 blocks (nullptr outside
+// the instantiated widths) and its dynamic LDS (x permuted).
+VocabKernel vocab_kernel(int nb8) {
+  switch (nb8) {
+    case 24: return k_vocab<24>;
+    case 25: return k_vocab<25>;
+    case 26: return k_vocab<26>;
+    case 27: return k_vocab<27>;
+    case 28: return k_vocab<28>;
+    case 29: return k_vocab<29>;
+    case 30: return k_vocab<30>;
+    case 31: return k_vocab<31>;
+    case 32: return k_vocab<32>;
+    default: return nullptr;
+  }
+}
+size_t vocab_lds(int64_t cols) { return (size_t)nq_of((int)cols) * 4 * 32 * sizeof(float); }
+
+// Grid of the vocab kernel for a rows x cols Q8_0 matrix: two workgroups
+// per CU (fewer if the occupancy is lower), at most one per 32-row tile.
+// Measured over 1..18 per CU for the 151,936 x 896 matrix: two per CU
+// keeps the most of the matrix streaming under the arithmetic; more
+// workgroups add per-workgroup set-up and first-tile waits.
+int vocab_grid(c2h_ctx* c, int64_t rows, int64_t cols, int* grid) {
+  VocabKernel k = vocab_kernel(nb8_of(cols));
+  if (!k)
+    return fail(c, C2H_ERR_UNSUPPORTED, "Q8_0 vocab rows of %lld columns (this build: %d..%d)", (long long)cols,
+                32 * VOCAB_MIN_NB8, 32 * VOCAB_MAX_NB8);
+  int per_cu = 0, n_cu = 0;
+  HIPCHK(c, hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, 256, vocab_lds(cols)));
+  HIPCHK(c, hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, c->device));
+  const int64_t tiles = (rows + 31) / 32;
+  *grid = (int)std::max<int64_t>(1, std::min<int64_t>(tiles, (int64_t)std::min(std::max(per_cu, 1), 2) * std::max(n_cu, 1)));
+  return C2H_OK;
+}
+
 void enqueue_vocab(c2h_ctx* c, int apply_penalty, float* logits_out, int x_sel, const float* x) {
   VocabParams V;
   memset(&V, 0, sizeof(V));
@@ -405,8 +443,8 @@ void enqueue_vocab(c2h_ctx* c, int apply_penalty, float* logits_out, int x_sel, 
   V.part_v = c->part_v;
   V.part_i = c->part_i;
   V.state = c->state_dev;
-  size_t lds = (size_t)nq_of(c->desc.n_embd) * 4 * 32 * sizeof(float);
-  hipLaunchKernelGGL(k_vocab, dim3(c->n_part), dim3(256), lds, c->stream, V);
+  hipLaunchKernelGGL(vocab_kernel(nb8_of(c->desc.n_embd)), dim3(c->n_part), dim3(256), vocab_lds(c->desc.n_embd),
+                     c->stream, V);
 }
 
 AttnCoreParams attn_params(c2h_ctx* c, int layer) {
@@ -781,8 +819,7 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
         stream_copy(c->stream, c->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
       return bail(fail(c, C2H_ERR_HIP, "rope upload"));
   }
-  int tiles = (D.n_vocab + 31) / 32;
-  c->n_part = (tiles + VOCAB_TILES - 1) / VOCAB_TILES;
+  if ((rc = vocab_grid(c, D.n_vocab, D.n_embd, &c->n_part))) return bail(rc);
   if ((rc = dalloc(c, &c->part_v, (size_t)c->n_part * 4)) || (rc = dalloc(c, &c->part_i, (size_t)c->n_part * 4)) ||
       (rc = dalloc(c, &c->logits, (size_t)D.n_vocab * 4)))
     return bail(rc);
@@ -1331,35 +1368,8 @@ int c2h_gemv_dev(c2h_ctx* c, int32_t type, const void* w_packed, const void* xq,
   t.type = type;
   t.rows = rows;
   t.cols = cols;
-  if (type == C2H_Q8_0) {
-    // the vocab kernel without penalty, logits to y
-    int tiles = (rows + 31) / 32;
-    int n_part = (tiles + VOCAB_TILES - 1) / VOCAB_TILES;
-    // scratch for the argmax candidates
-    float* pv = nullptr;
-    int* pi = nullptr;
-    HIPCHK(c, hipMalloc(&pv, (size_t)n_part * 4 + 256));
-    c->scratch.push_back(pv);
-    HIPCHK(c, hipMalloc(&pi, (size_t)n_part * 4 + 256));
-    c->scratch.push_back(pi);
-    VocabParams V;
-    memset(&V, 0, sizeof(V));
-    V.w = t.ref();
-    V.n_vocab = rows;
-    V.n_embd = cols;
-    V.x = reinterpret_cast<const float*>(xq);
-    V.token_ids = nullptr;
-    V.apply_penalty = 0;
-    V.logits_out = y;
-    V.part_v = pv;
-    V.part_i = pi;
-    V.state = c->state_dev;
-    size_t lds = (size_t)nq_of(cols) * 4 * 32 * sizeof(float);
-    hipLaunchKernelGGL(k_vocab, dim3(n_part), dim3(256), lds, c->stream, V);
-    HIPCHK(c, hipGetLastError());
-    return C2H_OK;
-  }
-  if (type == C2H_Q5_0) {  // f32 x, k_gemv_f without a prologue
+  if (type == C2H_Q8_0 && nb8_of(cols) > 32) return fail(c, C2H_ERR_UNSUPPORTED, "Q8_0 rows run up to 1024 columns");
+  if (type == C2H_Q5_0 || type == C2H_Q8_0) {  // f32 x: k_gemv_f without a prologue
     GemvParams P;
     memset(&P, 0, sizeof(P));
     P.prologue = PRO_QUANT;

@@ -280,7 +280,6 @@ struct PFRopeParams {
   int layer, n_layers, n_kv_heads, max_ctx;
 };
 
-constexpr int VOCAB_TILES = 1;  // 32-row tiles per vocab workgroup
 
 struct VocabParams {
   WeightRef w;
@@ -325,7 +324,9 @@ template <int MODE>
 __global__ void k_pf_gemm_f(PFGemmFParams P);
 __global__ void k_pf_rope_store(PFRopeParams P);
 __global__ void k_pf_swiglu(const float* gate, const float* up, float* h, int n, int m);
+template <int NB8>
 __global__ void k_vocab(VocabParams P);
+constexpr int VOCAB_MIN_NB8 = 24, VOCAB_MAX_NB8 = 32;  // instantiated widths (Q8_0 blocks per row)
 __global__ void k_argmax_final(const float* pv, const int* pi, int n, C2hState* state);
 __global__ void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16);
 __global__ void k_empty(const int* __restrict__ flag, int* __restrict__ out);

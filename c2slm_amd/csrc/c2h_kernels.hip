@@ -2089,77 +2089,70 @@ template __global__ void k_pf_gemm<T_Q6_K, MODE_RESID>(PFGemmParams);
 // internal/simd/c2_tensor_dot_q8_0_gen.go:79-102 (lane j of a row owns
 // acc[j]), repetition penalty (c2slm.go:157-170) and per-workgroup argmax
 // candidates (c2slm.go:173-180).  256 threads = 32 rows x 8 lanes; rows of
-// up to VOCAB_NQ*4 blocks (1024 columns).  x, the penalty window and the
-// row's weights are loaded at entry (clamped, unconditional).
-constexpr int VOCAB_NQ = 8;
+// NB8 = 24..32 blocks (768..1024 columns), one instance per width.
 
-__global__ void __launch_bounds__(256) k_vocab(VocabParams P) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  float* xp = reinterpret_cast<float*>(smem);  // x permuted: [b][j][i] = x[32b + j + 8i]
-  __shared__ int win[64];
-  __shared__ ArgCand red[4];
+// One 32-row tile of the vocab projection: 8 lanes per row, lane j holding
+// bytes j, j+8, j+16, j+24 of each block (the packed layout), and the row's
+// scales.  Loads of rows past the matrix are clamped to its last row.
+// Every loaded dword is used: a load whose result is partly dead lets the
+// register allocator put a temporary into its dead part, and the write then
+// waits for the load (a WAW wait that serialises the double buffering).
+template <int NB8>
+struct VocabTile {
+  static constexpr int NQ = (NB8 + 3) / 4;  // 16-byte quant groups per lane
+  static constexpr int ND = NQ / 2;         // 16-byte scale groups (two quant groups each)
+  static constexpr int NT = NQ % 2;         // an 8-byte scale group for an odd last quant group
+  uint4 q[NQ];
+  uint4 d[ND > 0 ? ND : 1];
+  uint2 dt[NT > 0 ? NT : 1];
+};
 
+template <int NB8>
+__device__ __forceinline__ void vocab_load(VocabTile<NB8>& t, const VocabParams& P, int tile) {
+  constexpr int DPAD = ((NB8 + 31) / 32) * 32;
+  const int j = threadIdx.x & 7, rl = threadIdx.x >> 3;
+  const int row_c = min(tile * 32 + rl, P.n_vocab - 1);
+  const uint8_t* rowp = P.w.q + (size_t)row_c * q8_0_row_stride(NB8);
+  const uint4* dvec = reinterpret_cast<const uint4*>(rowp);
+  const uint4* qrow = reinterpret_cast<const uint4*>(rowp + (size_t)DPAD * 2);
+#pragma unroll
+  for (int bq = 0; bq < VocabTile<NB8>::NQ; ++bq) t.q[bq] = ld_nt(qrow + bq * 8 + j);
+#pragma unroll
+  for (int k = 0; k < VocabTile<NB8>::ND; ++k) t.d[k] = dvec[k];
+  if constexpr (VocabTile<NB8>::NT > 0) t.dt[0] = reinterpret_cast<const uint2*>(dvec)[2 * VocabTile<NB8>::ND];
+}
+
+// The row of this lane group: the reference's 8-lane sum
+// acc[j] += ((p0+p1)+(p2+p3))*d over the blocks, then the lanes left to
+// right; the logit (optional output), the penalty per occurrence of the row
+// id in the window, and the candidate (NaN never wins the scan except at
+// id 0, where it ends it).
+template <int NB8>
+__device__ __forceinline__ void vocab_row(const VocabTile<NB8>& t, const VocabParams& P, const float* xp,
+                                          const int* win, int nwin, int tile, int im_end, int eos, float penalty,
+                                          ArgCand& best) {
   const int tid = threadIdx.x;
   const int j = tid & 7;
-  const int rl = tid >> 3;
-  const int E = P.n_embd;
-  const int nb8 = E / QK8_0;
-  const int nq = q8_0_nq(nb8);
-  const int dpad = q8_0_dpad(nb8);
-  const size_t stride = q8_0_row_stride(nb8);
-  const int row = blockIdx.x * 32 + rl;
-  const int row_c = min(row, P.n_vocab - 1);
-  const int pos = P.state->pos;
-  const int wstart = max(pos - 64, 0);
-  const int nwin = (P.apply_penalty && pos > 0) ? (pos - wstart) : 0;
-
-  // ---- loads: x, the penalty window, then the row
-  const float* x = P.x_sel ? P.x_buf[P.state->nx_in] : P.x;
-  float xr[VOCAB_NQ / 2];
-#pragma unroll
-  for (int k = 0; k < VOCAB_NQ / 2; ++k) xr[k] = x[min(tid + 256 * k, nb8 * 32 - 1)];
-  // without the penalty token_ids may be absent: read a valid dummy instead
-  const int32_t* wsrc = P.apply_penalty ? P.token_ids + wstart : P.part_i;
-  const int wid = wsrc[P.apply_penalty ? min(tid & 63, max(nwin - 1, 0)) : 0];
-  uint4 wq[VOCAB_NQ], wd[VOCAB_NQ / 2];
-  {
-    const uint8_t* rowp = P.w.q + (size_t)row_c * stride;
-    const uint4* dvec = reinterpret_cast<const uint4*>(rowp);
-    const uint4* qrow = reinterpret_cast<const uint4*>(rowp + (size_t)dpad * 2);
-#pragma unroll
-    for (int bq = 0; bq < VOCAB_NQ; ++bq) wq[bq] = ld_nt(qrow + min(bq, nq - 1) * 8 + j);
-#pragma unroll
-    for (int k = 0; k < VOCAB_NQ / 2; ++k) wd[k] = dvec[min(k, dpad / 8 - 1)];
-  }
-  issue_fence();
-#pragma unroll
-  for (int k = 0; k < VOCAB_NQ / 2; ++k) {
-    const int e = tid + 256 * k;
-    if (e < nb8 * 32) {
-      int b = e >> 5, kk = e & 31;
-      int jj = kk & 7, ii = kk >> 3;
-      xp[(b * 8 + jj) * 4 + ii] = xr[k];
-    }
-  }
-  if (tid < 64) win[tid] = wid;
-  __syncthreads();
-
-  const int im_end = P.state->im_end, eos = P.state->eos;
-  const float penalty = P.state->penalty;
-  const bool valid = row < P.n_vocab;
+  const int row = tile * 32 + (tid >> 3);
   float acc = 0.0f;
 #pragma unroll
-  for (int bq = 0; bq < VOCAB_NQ; ++bq) {
-    if (bq < nq) {
-      const uint4 dv = wd[bq >> 1];
-      const uint32_t dlo = (bq & 1) ? dv.z : dv.x;
-      const uint32_t dhi = (bq & 1) ? dv.w : dv.y;
+  for (int bq = 0; bq < VocabTile<NB8>::NQ; ++bq) {
+    {
+      uint32_t dlo, dhi;
+      if (bq < 2 * VocabTile<NB8>::ND) {
+        const uint4 dv = t.d[bq >> 1];
+        dlo = (bq & 1) ? dv.z : dv.x;
+        dhi = (bq & 1) ? dv.w : dv.y;
+      } else {
+        dlo = t.dt[0].x;
+        dhi = t.dt[0].y;
+      }
       const uint32_t dd[4] = {dlo & 0xffffu, dlo >> 16, dhi & 0xffffu, dhi >> 16};
-      const uint32_t ww[4] = {wq[bq].x, wq[bq].y, wq[bq].z, wq[bq].w};
+      const uint32_t ww[4] = {t.q[bq].x, t.q[bq].y, t.q[bq].z, t.q[bq].w};
 #pragma unroll
       for (int bb = 0; bb < 4; ++bb) {
         const int b = bq * 4 + bb;
-        if (b < nb8) {
+        if (b < NB8) {
           const float dsc = q8_0_scale(dd[bb]);
           const float4 xv = *reinterpret_cast<const float4*>(xp + (b * 8 + j) * 4);
           const uint32_t q = ww[bb];
@@ -2172,28 +2165,92 @@ __global__ void __launch_bounds__(256) k_vocab(VocabParams P) {
       }
     }
   }
-  // (((((((a0+a1)+a2)+a3)+a4)+a5)+a6)+a7) into lane j == 0
+  // (((((((a0+a1)+a2)+a3)+a4)+a5)+a6)+a7) into every lane of the row
   const int base = tid & ~7;
   float tot = __shfl(acc, base);
 #pragma unroll
   for (int k = 1; k < 8; ++k) tot = tot + __shfl(acc, base + k);
-  // occurrences of this row id in the penalty window
+  // occurrences of the row id in the window; most tiles hold none of the
+  // window's ids, which one ballot over the wave's tile shows
   int cnt = 0;
-  for (int e = j; e < nwin; e += 8) cnt += (win[e] == row) ? 1 : 0;
-  cnt += __shfl_xor(cnt, 1);
-  cnt += __shfl_xor(cnt, 2);
-  cnt += __shfl_xor(cnt, 4);
-  ArgCand best;
-  best.v = -__builtin_inff();
-  best.i = 0x7fffffff;
-  if (valid && j == 0) {
+  const bool hit = (tid & 63) < nwin && (win[tid & 63] >> 5) == tile;
+  if (__ballot(hit) != 0ull) {
+    for (int e = j; e < nwin; e += 8) cnt += (win[e] == row) ? 1 : 0;
+    cnt += __shfl_xor(cnt, 1);
+    cnt += __shfl_xor(cnt, 2);
+    cnt += __shfl_xor(cnt, 4);
+  }
+  if (row < P.n_vocab && j == 0) {
     if (P.logits_out) P.logits_out[row] = tot;
     if (row != im_end && row != eos) {
       for (int c = 0; c < cnt; ++c) tot = (tot > 0.0f) ? (tot / penalty) : (tot * penalty);
     }
-    // NaN never wins the scan except at id 0, where it ends it
-    best.v = (tot != tot) ? ((row == 0) ? __builtin_inff() : -__builtin_inff()) : tot;
-    best.i = row;
+    ArgCand cand;
+    cand.v = (tot != tot) ? ((row == 0) ? __builtin_inff() : -__builtin_inff()) : tot;
+    cand.i = row;
+    best = arg_better(best, cand);
+  }
+}
+
+// Vocab projection + penalty + argmax candidates.  A fixed grid (the
+// resident workgroups of the GPU) walks the 32-row tiles with stride
+// gridDim.x, two tiles per trip: the next tile's rows load while the
+// current one computes, so each wave keeps the matrix streaming under its
+// own arithmetic.  x is permuted into LDS once per workgroup.  Workgroup w
+// leaves its best (value, lowest index) in part_v/part_i[w].
+template <int NB8>
+__global__ void __launch_bounds__(256) k_vocab(VocabParams P) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* xp = reinterpret_cast<float*>(smem);  // x permuted: [b][j][i] = x[32b + j + 8i]
+  __shared__ int win[64];
+  __shared__ ArgCand red[4];
+
+  const int tid = threadIdx.x;
+  constexpr int nb8 = NB8;
+  const int n_tiles = (P.n_vocab + 31) / 32;
+  const int G = (int)gridDim.x;
+  const int trips = ((n_tiles + G - 1) / G + 1) / 2;  // tile pairs per workgroup
+  const int pos = P.state->pos;
+  const int wstart = max(pos - 64, 0);
+  const int nwin = (P.apply_penalty && pos > 0) ? (pos - wstart) : 0;
+
+  // ---- loads: x, the penalty window, then the first tile
+  const float* x = P.x_sel ? P.x_buf[P.state->nx_in] : P.x;
+  constexpr int XR = (NB8 + 7) / 8;  // x elements per thread
+  float xr[XR];
+#pragma unroll
+  for (int k = 0; k < XR; ++k) xr[k] = x[min(tid + 256 * k, nb8 * 32 - 1)];
+  // without the penalty token_ids may be absent: read a valid dummy instead
+  const int32_t* wsrc = P.apply_penalty ? P.token_ids + wstart : P.part_i;
+  const int wid = wsrc[P.apply_penalty ? min(tid & 63, max(nwin - 1, 0)) : 0];
+  VocabTile<NB8> ta, tb;
+  vocab_load(ta, P, blockIdx.x);
+  issue_fence();
+#pragma unroll
+  for (int k = 0; k < XR; ++k) {
+    const int e = tid + 256 * k;
+    if (e < nb8 * 32) {
+      int b = e >> 5, kk = e & 31;
+      int jj = kk & 7, ii = kk >> 3;
+      xp[(b * 8 + jj) * 4 + ii] = xr[k];
+    }
+  }
+  if (tid < 64) win[tid] = wid;
+  __syncthreads();
+
+  const int im_end = P.state->im_end, eos = P.state->eos;
+  const float penalty = P.state->penalty;
+  ArgCand best;
+  best.v = -__builtin_inff();
+  best.i = 0x7fffffff;
+  for (int k = 0; k < trips; ++k) {
+    const int t0 = (int)blockIdx.x + 2 * k * G;
+    vocab_load(tb, P, t0 + G);
+    __builtin_amdgcn_sched_barrier(0);
+    vocab_row(ta, P, xp, win, nwin, t0, im_end, eos, penalty, best);
+    vocab_load(ta, P, t0 + 2 * G);  // the next trip's first tile
+    __builtin_amdgcn_sched_barrier(0);
+    vocab_row(tb, P, xp, win, nwin, t0 + G, im_end, eos, penalty, best);
   }
   best = wave_argmax(best);
   if ((tid & 63) == 0) red[tid >> 6] = best;
@@ -2205,6 +2262,17 @@ __global__ void __launch_bounds__(256) k_vocab(VocabParams P) {
     P.part_i[blockIdx.x] = r.i;
   }
 }
+#define C2H_VOCAB(NB8_) template __global__ void k_vocab<NB8_>(VocabParams);
+C2H_VOCAB(24)
+C2H_VOCAB(25)
+C2H_VOCAB(26)
+C2H_VOCAB(27)
+C2H_VOCAB(28)
+C2H_VOCAB(29)
+C2H_VOCAB(30)
+C2H_VOCAB(31)
+C2H_VOCAB(32)
+#undef C2H_VOCAB
 
 // Final reduction for standalone argmax calls (no following layer kernel).
 __global__ void __launch_bounds__(256) k_argmax_final(const float* pv, const int* pi, int n, C2hState* state) {
