@@ -82,6 +82,10 @@ def lib():
             "c2h_copy_bench": (C.c_int, [VP, C.c_int64, I32, C.POINTER(C.c_float)]),
             "c2h_launch_floor": (C.c_int, [VP, I32, I32, I32, C.POINTER(C.c_float)]),
             "c2h_time_steps": (C.c_int, [VP, I32, I32, C.c_float, I32, I32, C.POINTER(C.c_float)]),
+            "c2h_gemv_f32": (C.c_int, [VP, I32, VP, VP, I32, I32, VP]),
+            "c2h_gemv_f32_dev": (C.c_int, [VP, I32, VP, VP, I32, I32, VP]),
+            "c2h_logits_ids": (C.c_int, [VP, VP, I32, VP]),
+            "c2h_logits_ids_dev": (C.c_int, [VP, VP, I32, VP]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -152,6 +156,16 @@ class Ctx:
     def logits(self) -> np.ndarray:
         out = np.empty(self.desc.n_vocab, np.float32)
         self._chk(lib().c2h_logits(self.h, _p(out)))
+        return out
+
+    def logits_ids(self, ids, out: np.ndarray | None = None) -> np.ndarray:
+        """engine.ComputeLogits with a target list: out[id] for each id in
+        range; the other entries of out keep their values."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        if out is None:
+            out = np.zeros(self.desc.n_vocab, np.float32)
+        assert out.dtype == np.float32 and out.flags.c_contiguous and len(out) == self.desc.n_vocab
+        self._chk(lib().c2h_logits_ids(self.h, _p(ids) if len(ids) else None, len(ids), _p(out)))
         return out
 
     def step(self, pos: int, penalty: float, im_end: int, eos: int) -> int:
@@ -230,6 +244,16 @@ class Ctx:
         self._chk(lib().c2h_gemv(self.h, ggml_type, _p(w), _p(xq), rows, cols, _p(y),
                                  _p(isums) if isums is not None else None))
         return (y, isums) if want_isums else y
+
+
+    def gemv_f32(self, ggml_type: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int) -> np.ndarray:
+        """engine.DispatchGEMV without a pool: y = W·x on f32 x."""
+        w = np.ascontiguousarray(w)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        assert len(x) >= cols
+        y = np.empty(rows, np.float32)
+        self._chk(lib().c2h_gemv_f32(self.h, ggml_type, _p(w), _p(x), rows, cols, _p(y)))
+        return y
 
 
 def packed_size(ggml_type: int, rows: int, cols: int) -> int:

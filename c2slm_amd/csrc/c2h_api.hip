@@ -94,6 +94,11 @@ struct c2h_ctx {
 
   // kernel-only scratch (c2h_gemv / c2h_quantize_q8k host forms)
   std::vector<void*> scratch;
+
+  // restricted-logits staging (c2h_logits_ids): ids in, compact logits out
+  int32_t* ids_dev = nullptr;
+  float* ids_y = nullptr;
+  int ids_cap = 0;
 };
 
 namespace {
@@ -873,6 +878,8 @@ void c2h_destroy(c2h_ctx* c) {
   destroy_graphs(c);
   for (void* p : c->allocs) (void)hipFree(p);
   for (void* p : c->scratch) (void)hipFree(p);
+  if (c->ids_dev) (void)hipFree(c->ids_dev);
+  if (c->ids_y) (void)hipFree(c->ids_y);
   if (c->state_ring) (void)hipHostFree(c->state_ring);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
@@ -1388,6 +1395,150 @@ int c2h_gemv_dev(c2h_ctx* c, int32_t type, const void* w_packed, const void* xq,
   add_job(P, t, nullptr, MODE_STORE, y, nullptr, isums_out);
   hipLaunchKernelGGL(k_gemv_q8k, job_grid(P), dim3(256), gemv_q8k_lds_bytes(), c->stream, P);
   HIPCHK(c, hipGetLastError());
+  return C2H_OK;
+}
+
+namespace {
+
+bool float_x_type(int type) {
+  return type == C2H_Q4_K || type == C2H_Q6_K || type == C2H_Q8_0 || type == C2H_Q5_0;
+}
+
+// Super-blocks (K-quants) or blocks (Q8_0 / Q5_0) per row: the reference's
+// row functions floor cols to them, and zero of them gives zero dots.
+int64_t float_x_blocks(int type, int64_t cols) {
+  return (type == C2H_Q4_K || type == C2H_Q6_K) ? cols / 256 : cols / 32;
+}
+
+void launch_dot_rows(c2h_ctx* c, int type, WeightRef w, int rows, int cols, const float* x, const int32_t* ids, int n,
+                     int scatter, float* y) {
+  DotRowsParams P;
+  memset(&P, 0, sizeof(P));
+  P.w = w;
+  P.rows = rows;
+  P.cols = cols;
+  P.x = x;
+  P.ids = ids;
+  P.n = n;
+  P.scatter = scatter;
+  P.y = y;
+  const dim3 grid((n + DOT_ROWS_PER_WG - 1) / DOT_ROWS_PER_WG), block(256);
+  switch (type) {
+    case C2H_Q4_K: hipLaunchKernelGGL(k_dot_rows<T_Q4_K>, grid, block, 0, c->stream, P); break;
+    case C2H_Q6_K: hipLaunchKernelGGL(k_dot_rows<T_Q6_K>, grid, block, 0, c->stream, P); break;
+    case C2H_Q8_0: hipLaunchKernelGGL(k_dot_rows<T_Q8_0>, grid, block, 0, c->stream, P); break;
+    default: hipLaunchKernelGGL(k_dot_rows<T_Q5_0>, grid, block, 0, c->stream, P); break;
+  }
+}
+
+// Weight view of a c2h_pack_weights buffer.
+WeightRef packed_ref(int type, int64_t rows, int64_t cols, const void* w_packed) {
+  size_t qb, db;
+  packed_parts(type, rows, cols, &qb, &db);
+  WeightRef w;
+  w.q = reinterpret_cast<const uint8_t*>(w_packed);
+  w.d = db ? reinterpret_cast<const uint16_t*>(w.q + qb) : nullptr;
+  return w;
+}
+
+}  // namespace
+
+int c2h_gemv_f32_dev(c2h_ctx* c, int32_t type, const void* w_packed, const float* x, int32_t rows, int32_t cols,
+                     float* y) {
+  if (!c || !x || !y || rows <= 0 || cols <= 0) return C2H_ERR_INVALID;
+  HIPCHK(c, hipSetDevice(c->device));
+  if (!float_x_type(type) || float_x_blocks(type, cols) == 0) {  // DispatchGEMV's zero fallback / empty rows
+    HIPCHK(c, hipMemsetAsync(y, 0, (size_t)rows * 4, c->stream));
+    return C2H_OK;
+  }
+  if (!w_packed) return C2H_ERR_INVALID;
+  if (reinterpret_cast<uintptr_t>(x) & 15) return fail(c, C2H_ERR_INVALID, "x must be 16-byte aligned");
+  launch_dot_rows(c, type, packed_ref(type, rows, cols, w_packed), rows, cols, x, nullptr, rows, 0, y);
+  HIPCHK(c, hipGetLastError());
+  return C2H_OK;
+}
+
+int c2h_gemv_f32(c2h_ctx* c, int32_t type, const void* w, const float* x, int32_t rows, int32_t cols, float* y) {
+  if (!c || !x || !y || rows <= 0 || cols <= 0) return C2H_ERR_INVALID;
+  HIPCHK(c, hipSetDevice(c->device));
+  if (!float_x_type(type) || float_x_blocks(type, cols) == 0) {
+    memset(y, 0, (size_t)rows * 4);
+    return C2H_OK;
+  }
+  if (!w) return C2H_ERR_INVALID;
+  const size_t pbytes = c2h_packed_size(type, rows, cols);
+  std::vector<uint8_t> packed(pbytes);
+  size_t qb, db;
+  packed_parts(type, rows, cols, &qb, &db);
+  pack_host(type, rows, cols, reinterpret_cast<const uint8_t*>(w), packed.data(), packed.data() + qb);
+  uint8_t* dw = nullptr;
+  float *dx = nullptr, *dy = nullptr;
+  auto cleanup = [&]() {
+    if (dw) (void)hipFree(dw);
+    if (dx) (void)hipFree(dx);
+    if (dy) (void)hipFree(dy);
+  };
+  if (hipMalloc(&dw, pbytes) != hipSuccess || hipMalloc(&dx, (size_t)cols * 4) != hipSuccess ||
+      hipMalloc(&dy, (size_t)rows * 4) != hipSuccess) {
+    cleanup();
+    return fail(c, C2H_ERR_HIP, "hipMalloc failed");
+  }
+  int rc = C2H_OK;
+  if (stream_copy(c->stream, dw, packed.data(), pbytes, hipMemcpyHostToDevice) != hipSuccess ||
+      stream_copy(c->stream, dx, x, (size_t)cols * 4, hipMemcpyHostToDevice) != hipSuccess)
+    rc = fail(c, C2H_ERR_HIP, "copy in failed");
+  if (!rc) rc = c2h_gemv_f32_dev(c, type, dw, dx, rows, cols, dy);
+  if (!rc && hipStreamSynchronize(c->stream) != hipSuccess) rc = fail(c, C2H_ERR_HIP, "kernel failed");
+  if (!rc && stream_copy(c->stream, y, dy, (size_t)rows * 4, hipMemcpyDeviceToHost) != hipSuccess)
+    rc = fail(c, C2H_ERR_HIP, "copy out failed");
+  cleanup();
+  return rc;
+}
+
+int c2h_logits_ids_dev(c2h_ctx* c, const int32_t* ids, int32_t n_ids, float* logits) {
+  if (!c || !logits || n_ids < 0 || (n_ids > 0 && !ids)) return C2H_ERR_INVALID;
+  if (!c->has_model) return fail(c, C2H_ERR_STATE, "kernel-only context");
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = validate_model(c);
+  if (rc) return rc;
+  if (n_ids == 0) {  // an empty target list projects the whole vocabulary (engine/forward.go:174,185-190)
+    enqueue_vocab(c, 0, logits, 0, c->normx[c->nx_cur]);
+    HIPCHK(c, hipGetLastError());
+    return C2H_OK;
+  }
+  const Tensor& t = out_weight(c);
+  launch_dot_rows(c, t.type, t.ref(), (int)t.rows, (int)t.cols, c->normx[c->nx_cur], ids, n_ids, 1, logits);
+  HIPCHK(c, hipGetLastError());
+  return C2H_OK;
+}
+
+int c2h_logits_ids(c2h_ctx* c, const int32_t* ids, int32_t n_ids, float* logits_out) {
+  if (!c || !logits_out || n_ids < 0 || (n_ids > 0 && !ids)) return C2H_ERR_INVALID;
+  if (n_ids == 0) return c2h_logits(c, logits_out);
+  if (!c->has_model) return fail(c, C2H_ERR_STATE, "kernel-only context");
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = validate_model(c);
+  if (rc) return rc;
+  if (n_ids > c->ids_cap) {
+    if (c->ids_dev) (void)hipFree(c->ids_dev);
+    if (c->ids_y) (void)hipFree(c->ids_y);
+    c->ids_dev = nullptr;
+    c->ids_y = nullptr;
+    c->ids_cap = 0;
+    const int cap = n_ids < 1024 ? 1024 : n_ids;
+    HIPCHK(c, hipMalloc(&c->ids_dev, (size_t)cap * 4));
+    HIPCHK(c, hipMalloc(&c->ids_y, (size_t)cap * 4));
+    c->ids_cap = cap;
+  }
+  HIPCHK(c, stream_copy(c->stream, c->ids_dev, ids, (size_t)n_ids * 4, hipMemcpyHostToDevice));
+  const Tensor& t = out_weight(c);
+  launch_dot_rows(c, t.type, t.ref(), (int)t.rows, (int)t.cols, c->normx[c->nx_cur], c->ids_dev, n_ids, 0, c->ids_y);
+  HIPCHK(c, hipGetLastError());
+  std::vector<float> y((size_t)n_ids);
+  HIPCHK(c, stream_copy(c->stream, y.data(), c->ids_y, (size_t)n_ids * 4, hipMemcpyDeviceToHost));
+  const int vocab = c->desc.n_vocab;
+  for (int i = 0; i < n_ids; ++i)  // out-of-range ids are skipped (engine/forward.go:177-179)
+    if (ids[i] >= 0 && ids[i] < vocab) logits_out[ids[i]] = y[(size_t)i];
   return C2H_OK;
 }
 

@@ -327,6 +327,22 @@ __global__ void k_pf_swiglu(const float* gate, const float* up, float* h, int n,
 template <int NB8>
 __global__ void k_vocab(VocabParams P);
 constexpr int VOCAB_MIN_NB8 = 24, VOCAB_MAX_NB8 = 32;  // instantiated widths (Q8_0 blocks per row)
+// One f32 dot per output (float-x order of each format).  Output i is row
+// ids[i] when ids is given (ids outside [0, rows) are skipped), else row i;
+// it is stored to y[ids[i]] when scatter is set, else to y[i].  x is 16-byte
+// aligned and holds cols floats.
+struct DotRowsParams {
+  WeightRef w;
+  int rows, cols;
+  const float* x;
+  const int32_t* ids;
+  int n;
+  int scatter;
+  float* y;
+};
+template <int TYPE>
+__global__ void k_dot_rows(DotRowsParams P);
+constexpr int DOT_ROWS_PER_WG = 32;
 __global__ void k_argmax_final(const float* pv, const int* pi, int n, C2hState* state);
 __global__ void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16);
 __global__ void k_empty(const int* __restrict__ flag, int* __restrict__ out);

@@ -2281,17 +2281,215 @@ __global__ void __launch_bounds__(256) k_argmax_final(const float* pv, const int
   if (threadIdx.x == 0) state->token = tok;
 }
 
-// Plain 16-byte copy (grid-stride), the calibration load for the memory
-// traffic counters: it reads and writes exactly n16*16 bytes.
 // A kernel that does no work (one flag read, a write that never happens):
 // its launches in a graph measure the per-launch floor.
 __global__ void __launch_bounds__(256) k_empty(const int* __restrict__ flag, int* __restrict__ out) {
   if (threadIdx.x == 0 && blockIdx.x == 0 && flag[0] == 0x5eed) out[0] = 1;
 }
 
+// Plain 16-byte copy (grid-stride), the calibration load for the memory
+// traffic counters: it reads and writes exactly n16*16 bytes.
 __global__ void __launch_bounds__(256) k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
 }
+
+// ------------------------------------------------------- float-x row dots
+// One f32 dot per output row, in each format's float-x order: the
+// non-pooled DispatchGEMV (engine/model.go:250-270 -> tensor.GEMVQ5_0 /
+// GEMVQ8_0 / GEMVQ6_K / GEMVQ4_K) and the restricted-token logits
+// (engine/forward.go:171-212, one DotQ* per requested id).  Eight lanes per
+// row are the reference's eight accumulators:
+//   Q8_0 (internal/simd/c2_tensor_dot_q8_0_gen.go): lane l adds
+//     ((q[l]x[l] + q[l+8]x[l+8]) + (q[l+16]x[l+16] + q[l+24]x[l+24])) * d
+//     per block;
+//   Q4_K (internal/simd/c2_tensor_dot_q4_k_gen.go:9-100): per 32-element
+//     sub-block with scale sc and min m, lane l adds
+//     a*(d*sc) - s*(dmin*m), a the pair-sum of its four products, s the
+//     pair-sum of its four x;
+//   Q6_K (internal/simd/c2_tensor_dot_q6_k_gen.go:9-81): per half, four
+//     quarter partials take (q*dk)*x pair sums for k = 0, 1, then the lane
+//     adds (s0 + s1) + (s2 + s3);
+//   then (((((((a0+a1)+a2)+a3)+a4)+a5)+a6)+a7).
+//   Q5_0 (tensor/ops.go:40-74) is one sequential chain over the blocks of
+//     d * (block sum); lane l forms the block sums of blocks l, l+8, ... and
+//     the chain adds them in block order.
+// The K-quant super-blocks of the 8 rows of a wave are staged through LDS
+// with 16-byte loads (the 144 / 208 byte blocks of the device layout are
+// 16-byte aligned), the next block's loads in flight while the current one
+// is consumed.  x is read from global memory (all rows share it).
+
+template <int TYPE>
+struct DotStage {
+  static constexpr int PIECES = (TYPE == T_Q4_K) ? BS_Q4K / 16 : BS_Q6K_PACKED / 16;  // uint4 per block
+  static constexpr int PER_WAVE = 8 * PIECES;                                        // 72 or 104
+  static constexpr int LOADS = (PER_WAVE + 63) / 64;                                 // 2
+};
+
+__device__ __forceinline__ float dot_lane_sum(float acc) { return q80_row_sum(acc); }
+
+template <int TYPE>
+__global__ void __launch_bounds__(256) k_dot_rows(DotRowsParams P) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l = tid & 7;
+  const int i = (int)blockIdx.x * 32 + (tid >> 3);
+  int r = -1;
+  if (i < P.n) r = P.ids ? P.ids[i] : i;
+  const bool valid = (r >= 0 && r < P.rows);
+  const int rc = valid ? r : 0;  // rows of empty slots are read but never stored
+  float acc = 0.0f;
+
+  if (TYPE == T_Q4_K || TYPE == T_Q6_K) {
+    typedef DotStage<TYPE> S;
+    constexpr int BS = (TYPE == T_Q4_K) ? BS_Q4K : BS_Q6K_PACKED;
+    __shared__ uint4 stage[4][S::PER_WAVE];
+    const int nb = P.cols / 256;
+    // the two pieces this lane fetches per block: slot row, byte offset
+    const uint8_t* src[S::LOADS];
+    bool live[S::LOADS];
+#pragma unroll
+    for (int k = 0; k < S::LOADS; ++k) {
+      const int p = lane + 64 * k;
+      live[k] = p < S::PER_WAVE;
+      const int pc = live[k] ? p : 0;
+      const int slot = pc / S::PIECES, piece = pc - slot * S::PIECES;
+      const int srow = __shfl(rc, slot * 8);
+      src[k] = P.w.q + ((size_t)srow * nb) * BS + 16 * piece;
+    }
+    uint4 nxt[S::LOADS];
+#pragma unroll
+    for (int k = 0; k < S::LOADS; ++k) nxt[k] = live[k] ? *reinterpret_cast<const uint4*>(src[k]) : make_uint4(0, 0, 0, 0);
+    const uint8_t* sb = reinterpret_cast<const uint8_t*>(&stage[wave][(tid >> 3 & 7) * S::PIECES]);
+    for (int b = 0; b < nb; ++b) {
+      __syncthreads();  // the previous block is consumed
+#pragma unroll
+      for (int k = 0; k < S::LOADS; ++k)
+        if (live[k]) stage[wave][lane + 64 * k] = nxt[k];
+      __syncthreads();
+      if (b + 1 < nb) {
+#pragma unroll
+        for (int k = 0; k < S::LOADS; ++k)
+          if (live[k]) nxt[k] = *reinterpret_cast<const uint4*>(src[k] + (size_t)(b + 1) * BS);
+      }
+      const float* xs = P.x + b * 256;
+      if (TYPE == T_Q4_K) {
+        const uint4 hdr = *reinterpret_cast<const uint4*>(sb);
+        const float d = fp16_simd(hdr.x & 0xffffu), dmin = fp16_simd(hdr.x >> 16);
+        const uint32_t sw[3] = {hdr.y, hdr.z, hdr.w};  // scale bytes 0..11
+        auto sbyte = [&](int k) { return (sw[k >> 2] >> (8 * (k & 3))) & 0xffu; };
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const int is = 2 * j + half;
+            uint32_t sc, mn;
+            if (is < 4) {
+              sc = sbyte(is) & 63u;
+              mn = sbyte(is + 4) & 63u;
+            } else {
+              sc = (sbyte(is + 4) & 15u) | ((sbyte(is - 4) >> 6) << 4);
+              mn = (sbyte(is + 4) >> 4) | ((sbyte(is) >> 6) << 4);
+            }
+            const float dsc = d * (float)sc;
+            const float dmm = dmin * (float)mn;
+            const float* xb = xs + 64 * j + 32 * half + l;
+            const uint8_t* qb = sb + 16 + 32 * j + l;
+            const int sh = 4 * half;
+            const float x0 = xb[0], x1 = xb[8], x2 = xb[16], x3 = xb[24];
+            const float p0 = (float)((qb[0] >> sh) & 15) * x0;
+            const float p1 = (float)((qb[8] >> sh) & 15) * x1;
+            const float p2 = (float)((qb[16] >> sh) & 15) * x2;
+            const float p3 = (float)((qb[24] >> sh) & 15) * x3;
+            const float a = (p0 + p1) + (p2 + p3);
+            const float sx = (x0 + x1) + (x2 + x3);
+            const float t = sx * dmm;
+            acc = acc + (a * dsc - t);
+          }
+        }
+      } else {
+        const float d = fp16_simd(P.w.d[(size_t)rc * nb + b]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint8_t* ql = sb + 64 * h;
+          const uint8_t* qh = sb + 128 + 32 * h;
+          const int8_t* scl = reinterpret_cast<const int8_t*>(sb + 192 + 8 * h);
+          const float* xb = xs + 128 * h;
+          float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const float dk0 = d * (float)scl[k], dk1 = d * (float)scl[k + 2];
+            const float dk2 = d * (float)scl[k + 4], dk3 = d * (float)scl[k + 6];
+            float pr[4][2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+              const int o = 16 * k + 8 * t + l;
+              const uint32_t a = ql[o], c = ql[32 + o], hb = qh[o];
+              const int v0 = (int)((a & 15u) | ((hb & 3u) << 4)) - 32;
+              const int v1 = (int)((c & 15u) | (((hb >> 2) & 3u) << 4)) - 32;
+              const int v2 = (int)((a >> 4) | (((hb >> 4) & 3u) << 4)) - 32;
+              const int v3 = (int)((c >> 4) | (((hb >> 6) & 3u) << 4)) - 32;
+              pr[0][t] = ((float)v0 * dk0) * xb[o];
+              pr[1][t] = ((float)v1 * dk1) * xb[32 + o];
+              pr[2][t] = ((float)v2 * dk2) * xb[64 + o];
+              pr[3][t] = ((float)v3 * dk3) * xb[96 + o];
+            }
+            s0 = s0 + (pr[0][0] + pr[0][1]);
+            s1 = s1 + (pr[1][0] + pr[1][1]);
+            s2 = s2 + (pr[2][0] + pr[2][1]);
+            s3 = s3 + (pr[3][0] + pr[3][1]);
+          }
+          acc = acc + ((s0 + s1) + (s2 + s3));
+        }
+      }
+    }
+    acc = dot_lane_sum(acc);
+  } else if (TYPE == T_Q8_0) {
+    const int nb8 = P.cols / 32, nq = q8_0_nq(nb8);
+    const uint8_t* rowp = P.w.q + (size_t)rc * q8_0_row_stride(nb8);
+    const uint16_t* dr = reinterpret_cast<const uint16_t*>(rowp);
+    const uint4* qrow = reinterpret_cast<const uint4*>(rowp + (size_t)q8_0_dpad(nb8) * 2);
+    for (int bq = 0; bq < nq; ++bq) {
+      const uint4 qv = qrow[bq * 8 + l];
+      const uint32_t ww[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+      for (int bb = 0; bb < 4; ++bb) {
+        const int b = bq * 4 + bb;
+        if (b < nb8) {
+          const float dsc = q8_0_scale(dr[b]);
+          const float* xb = P.x + 32 * b + l;
+          const uint32_t q = ww[bb];
+          const float p0 = (float)(int8_t)(q & 0xff) * xb[0];
+          const float p1 = (float)(int8_t)((q >> 8) & 0xff) * xb[8];
+          const float p2 = (float)(int8_t)((q >> 16) & 0xff) * xb[16];
+          const float p3 = (float)(int8_t)(q >> 24) * xb[24];
+          acc = acc + ((p0 + p1) + (p2 + p3)) * dsc;
+        }
+      }
+    }
+    acc = dot_lane_sum(acc);
+  } else {  // T_Q5_0
+    const int nb8 = P.cols / 32;
+    const uint8_t* rowp = P.w.q + (size_t)rc * nb8 * 24;
+    const int base = lane & ~7;
+    for (int b0 = 0; b0 < nb8; b0 += 8) {
+      const int b = min(b0 + l, nb8 - 1);
+      Q50Item it;
+      it.qs = reinterpret_cast<const uint4*>(rowp)[b];
+      it.hd = reinterpret_cast<const uint2*>(rowp + (size_t)nb8 * 16)[b];
+      const float term = q50_term(it, P.x + 32 * b);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float tk = __shfl(term, base + k);
+        if (b0 + k < nb8) acc = acc + tk;
+      }
+    }
+  }
+  if (valid && l == 0) P.y[(P.ids && P.scatter) ? r : i] = acc;
+}
+
+template __global__ void k_dot_rows<T_Q4_K>(DotRowsParams);
+template __global__ void k_dot_rows<T_Q6_K>(DotRowsParams);
+template __global__ void k_dot_rows<T_Q8_0>(DotRowsParams);
+template __global__ void k_dot_rows<T_Q5_0>(DotRowsParams);
 
 }  // namespace c2h

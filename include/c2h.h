@@ -200,6 +200,31 @@ int c2h_gemv_dev(c2h_ctx* ctx, int32_t ggml_type, const void* w_packed, const vo
                  float* y, int32_t* isums_out);
 int c2h_sync(c2h_ctx* ctx);
 
+/* engine.DispatchGEMV with a nil pool (engine/model.go:250-270): y = W·x on
+ * the f32 vector x through each format's float row function --
+ * tensor.GEMVQ4_K / GEMVQ6_K (DotQ4_K / DotQ6_K, tensor/ops.go:112-168),
+ * GEMVQ8_0 and GEMVQ5_0 (tensor/ops.go:25-110) -- over floor(cols/256)
+ * super-blocks or floor(cols/32) blocks per row.  Any other ggml type, or a
+ * row with no whole block, yields zeros (the reference's fallback).  Host
+ * buffers; w in the native layout, x holds cols floats. */
+int c2h_gemv_f32(c2h_ctx* ctx, int32_t ggml_type, const void* w, const float* x, int32_t rows, int32_t cols,
+                 float* y);
+/* Device-pointer form: w_packed in the c2h_pack_weights layout, x 16-byte
+ * aligned; runs on the context stream without synchronising. */
+int c2h_gemv_f32_dev(c2h_ctx* ctx, int32_t ggml_type, const void* w_packed, const float* x, int32_t rows,
+                     int32_t cols, float* y);
+
+/* engine.ComputeLogits(m, a, normX, out, targetTokens) with a target list
+ * (engine/forward.go:171-212) on the current normX: for each id of ids in
+ * [0, n_vocab), logits_out[id] = DotQ8_0(row id of the output matrix, normX);
+ * out-of-range ids are skipped and every other entry of logits_out (n_vocab
+ * floats) is left as it was.  n_ids == 0 projects the whole vocabulary like
+ * c2h_logits (the reference's empty-list branch). */
+int c2h_logits_ids(c2h_ctx* ctx, const int32_t* ids, int32_t n_ids, float* logits_out);
+/* Device-pointer form (ids and logits in device memory, logits n_vocab
+ * floats); runs on the context stream without synchronising. */
+int c2h_logits_ids_dev(c2h_ctx* ctx, const int32_t* ids, int32_t n_ids, float* logits);
+
 /* ---- measurement --------------------------------------------------------- */
 
 /* Average device time (ms) of `iters` launches of the fused vocab projection

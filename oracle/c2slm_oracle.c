@@ -290,6 +290,109 @@ float orc_dot_q8_0(const uint8_t* w, const float* x, int cols) {
   return ((((((acc[0] + acc[1]) + acc[2]) + acc[3]) + acc[4]) + acc[5]) + acc[6]) + acc[7];
 }
 
+/* Q4_K scales and mins of one super-block (get_scale_min_k4), as the float
+ * dot unpacks them: internal/simd/c2_tensor_dot_q4_k_gen.go:28-44. */
+static void q4k_scales(const uint8_t* s, uint8_t sc[8], uint8_t mn[8]) {
+  for (int i = 0; i < 4; ++i) {
+    sc[i] = s[i] & 63;
+    mn[i] = s[i + 4] & 63;
+    sc[i + 4] = (uint8_t)((s[i + 8] & 15) | ((s[i] >> 6) << 4));
+    mn[i + 4] = (uint8_t)((s[i + 8] >> 4) | ((s[i + 4] >> 6) << 4));
+  }
+}
+
+/* The float-x Q4_K dot (tensor/ops.go:165 DotQ4_K ->
+ * internal/simd/c2_tensor_dot_q4_k_gen.go:9-100, AVX2 path): eight lane
+ * accumulators; per 32-element sub-block with scale pair (sc, m), lane l
+ * forms a = (q[l]x[l] + q[l+8]x[l+8]) + (q[l+16]x[l+16] + q[l+24]x[l+24]),
+ * s = (x[l] + x[l+8]) + (x[l+16] + x[l+24]) and adds
+ * a·(d·sc) − s·(dmin·m) (products and the difference rounded separately);
+ * the low nibbles of the pair's 32 bytes are sub-block 2j, the high ones
+ * 2j+1; then (((((((a0+a1)+a2)+a3)+a4)+a5)+a6)+a7). */
+float orc_dot_q4k_f32(const uint8_t* w, const float* x, int cols) {
+  int nb = cols / QK_K;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int b = 0; b < nb; ++b) {
+    const uint8_t* blk = w + (long)b * BS_Q4K;
+    float d = orc_fp16_simd(rd_u16(blk));
+    float dmin = orc_fp16_simd(rd_u16(blk + 2));
+    uint8_t sc[8], mn[8];
+    q4k_scales(blk + 4, sc, mn);
+    for (int j = 0; j < 4; ++j) {
+      const uint8_t* q = blk + 16 + 32 * j;
+      for (int half = 0; half < 2; ++half) {
+        const int is = 2 * j + half;
+        const float* xb = x + b * QK_K + 64 * j + 32 * half;
+        const float dsc = d * (float)sc[is];
+        const float dmm = dmin * (float)mn[is];
+        for (int l = 0; l < 8; ++l) {
+          const int sh = 4 * half;
+          float p0 = (float)((q[l] >> sh) & 15) * xb[l];
+          float p1 = (float)((q[l + 8] >> sh) & 15) * xb[l + 8];
+          float p2 = (float)((q[l + 16] >> sh) & 15) * xb[l + 16];
+          float p3 = (float)((q[l + 24] >> sh) & 15) * xb[l + 24];
+          float a = (p0 + p1) + (p2 + p3);
+          float sx = (xb[l] + xb[l + 8]) + (xb[l + 16] + xb[l + 24]);
+          float t = sx * dmm;
+          float v = a * dsc - t;
+          acc[l] = acc[l] + v;
+        }
+      }
+    }
+  }
+  return ((((((acc[0] + acc[1]) + acc[2]) + acc[3]) + acc[4]) + acc[5]) + acc[6]) + acc[7];
+}
+
+/* The float-x Q6_K dot (tensor/ops.go:114 DotQ6_K ->
+ * internal/simd/c2_tensor_dot_q6_k_gen.go:9-81, AVX2 path): per half h of a
+ * super-block, four 8-lane partial vectors s0..s3 (quants of x offsets
+ * 0, 32, 64, 96 within the half) each take, for k = 0, 1, the pair sum
+ * (q[16k+l]·dk·x[16k+l]) + (q[16k+8+l]·dk·x[16k+8+l]) with
+ * dk = d·scale[k + 2i] for partial i, products in that order; then
+ * acc += (s0 + s1) + (s2 + s3), and the lanes are summed left to right. */
+float orc_dot_q6k_f32(const uint8_t* w, const float* x, int cols) {
+  int nb = cols / QK_K;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int b = 0; b < nb; ++b) {
+    const uint8_t* blk = w + (long)b * BS_Q6K;
+    float d = orc_fp16_simd(rd_u16(blk + 208));
+    for (int h = 0; h < 2; ++h) {
+      const uint8_t* ql = blk + 64 * h;
+      const uint8_t* qh = blk + 128 + 32 * h;
+      const int8_t* scl = (const int8_t*)(blk + 192 + 8 * h);
+      const float* xb = x + b * QK_K + 128 * h;
+      float s[4][8];
+      for (int i = 0; i < 4; ++i)
+        for (int l = 0; l < 8; ++l) s[i][l] = 0.0f;
+      for (int k = 0; k < 2; ++k) {
+        float dk[4];
+        for (int i = 0; i < 4; ++i) dk[i] = d * (float)scl[k + 2 * i];
+        for (int i = 0; i < 4; ++i) {
+          for (int l = 0; l < 8; ++l) {
+            float pr[2];
+            for (int t = 0; t < 2; ++t) {
+              const int o = 16 * k + 8 * t + l;
+              const uint8_t a = ql[o], c = ql[32 + o], hb = qh[o];
+              int v;
+              switch (i) {
+                case 0: v = (a & 15) | ((hb & 3) << 4); break;
+                case 1: v = (c & 15) | (((hb >> 2) & 3) << 4); break;
+                case 2: v = (a >> 4) | (((hb >> 4) & 3) << 4); break;
+                default: v = (c >> 4) | (((hb >> 6) & 3) << 4); break;
+              }
+              const float qv = (float)(v - 32);
+              pr[t] = (qv * dk[i]) * xb[32 * i + o];
+            }
+            s[i][l] = s[i][l] + (pr[0] + pr[1]);
+          }
+        }
+      }
+      for (int l = 0; l < 8; ++l) acc[l] = acc[l] + ((s[0][l] + s[1][l]) + (s[2][l] + s[3][l]));
+    }
+  }
+  return ((((((acc[0] + acc[1]) + acc[2]) + acc[3]) + acc[4]) + acc[5]) + acc[6]) + acc[7];
+}
+
 /* tensor/ops.go:40-74 (DotQ5_0, plain float loop; real-model format). */
 float orc_dot_q5_0(const uint8_t* w, const float* x, int cols) {
   float total = 0.0f;

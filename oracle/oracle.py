@@ -59,6 +59,8 @@ def lib():
             "orc_dot_q6k_q8k": (C.c_float, [U8P, U8P, C.c_int]),
             "orc_dot_q8_0": (C.c_float, [U8P, F32P, C.c_int]),
             "orc_dot_q5_0": (C.c_float, [U8P, F32P, C.c_int]),
+            "orc_dot_q4k_f32": (C.c_float, [U8P, F32P, C.c_int]),
+            "orc_dot_q6k_f32": (C.c_float, [U8P, F32P, C.c_int]),
             "orc_dequant_row_q8_0": (None, [F32P, U8P, C.c_int]),
             "orc_rmsnorm": (None, [F32P, F32P, F32P, C.c_int, C.c_float]),
             "orc_rope_table": (None, [F32P, F32P, C.c_int, C.c_int, C.c_float]),
@@ -106,14 +108,23 @@ def quantize_row_q8k(x: np.ndarray, y_len: int | None = None) -> np.ndarray:
 
 
 def gemv(w: np.ndarray, ggml_type: int, rows: int, cols: int, x: np.ndarray | None = None,
-         q8k: np.ndarray | None = None) -> np.ndarray:
-    """y = W·x for the reference's row functions (row stride with floor semantics)."""
+         q8k: np.ndarray | None = None, float_x: bool = False) -> np.ndarray:
+    """y = W·x for the reference's row functions (row stride with floor semantics).
+    K-quants take the Q8_K row of x (GEMVQ*_K_Q8_K), or with float_x the f32
+    x itself (GEMVQ4_K / GEMVQ6_K, engine/model.go:250-270 without a pool)."""
     from c2slm_amd import gguf as G
     L = lib()
     w = np.ascontiguousarray(w, dtype=np.uint8)
     rb = G.row_bytes(ggml_type, cols)
     y = np.empty(rows, dtype=np.float32)
-    if ggml_type in (G.Q4_K, G.Q6_K):
+    if ggml_type in (G.Q4_K, G.Q6_K) and float_x:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        fn = L.orc_dot_q4k_f32 if ggml_type == G.Q4_K else L.orc_dot_q6k_f32
+        base = w.ctypes.data
+        xp = ptr(x, F32P)
+        for r in range(rows):
+            y[r] = fn(C.cast(base + r * rb, U8P), xp, cols)
+    elif ggml_type in (G.Q4_K, G.Q6_K):
         if q8k is None:
             q8k = quantize_row_q8k(x)
         q8k = np.ascontiguousarray(q8k, dtype=np.uint8)

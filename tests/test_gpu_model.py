@@ -62,6 +62,29 @@ def test_logits_bitexact(tiny):
     assert np.array_equal(bits(ctx.logits()), bits(orc.compute_logits(nx)))
 
 
+def test_logits_ids_bitexact(tiny):
+    # engine.ComputeLogits with a target list (engine/forward.go:171-183):
+    # only the listed ids in range are written
+    gf, ctx, orc, _, _ = tiny
+    ctx.forward(29, 0)
+    nx = orc.forward(29, 0)
+    full = orc.compute_logits(nx)
+    V = ctx.desc.n_vocab
+    ids = np.array([5, 0, V - 1, 17, 17, -3, V, 2 ** 30, 1234 % V], np.int32)
+    out = np.full(V, 7.25, np.float32)
+    got = ctx.logits_ids(ids, out)
+    valid = ids[(ids >= 0) & (ids < V)]
+    assert np.array_equal(bits(got[valid]), bits(full[valid]))
+    rest = np.ones(V, bool)
+    rest[valid] = False
+    assert np.all(got[rest] == 7.25)
+    # a long list (every 7th id) and the empty list (the whole vocabulary)
+    many = np.arange(0, V, 7, dtype=np.int32)[::-1].copy()
+    got = ctx.logits_ids(many, np.zeros(V, np.float32))
+    assert np.array_equal(bits(got[many]), bits(full[many]))
+    assert np.array_equal(bits(ctx.logits_ids([], np.zeros(V, np.float32))), bits(full))
+
+
 def gpu_generate(ctx, prompt, max_new, im_end, eos, penalty=PENALTY):
     """The c2slm.go:92-117 ingest and :144-226 loop over the C ABI."""
     ctx.set_token_ids(0, prompt)

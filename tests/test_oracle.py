@@ -330,6 +330,178 @@ def test_q6k_gemv_vs_float64_dequant():
         assert np.all(np.abs(y - want) <= 1e-5 * scale)
 
 
+# ------------------------------------------------------------------ float-x K-quant dots
+# DotQ4_K / DotQ6_K (tensor/ops.go:112-168) take the f32 vector itself: the
+# non-pooled DispatchGEMV (engine/model.go:250-270) and the restricted-token
+# logits (engine/forward.go:171-212) use them.
+
+
+def onehot_f32(i, n=256):
+    x = np.zeros(n, np.float32)
+    x[i] = 1.0
+    return x
+
+
+def dot_f32(fn, blk, x):
+    x = np.ascontiguousarray(x, np.float32)
+    return fn(O.ptr(np.ascontiguousarray(blk), U8P), O.ptr(x, F32P), len(x))
+
+
+@pytest.mark.skipif(not R.ref_available("q4_k"), reason="oracle/_ref not built (needs the reference checkout)")
+def test_q4k_f32_unit_vectors_vs_reference_c_oracle():
+    # x = e_i leaves one product per lane: the dot is the dequantised weight
+    # q*(d*sc) - dmin*m, which the reference's C oracle writes out.
+    blocks = [q4k_fixture_block()] + hostile_blocks(144, [(0, [0x00, 0x3C]), (2, [0x00, 0x38])])
+    for blk in blocks:
+        want, _ = R.run_ref_dequant("q4_k", blk.tobytes())
+        for i in range(256):
+            assert dot_f32(L.orc_dot_q4k_f32, blk, onehot_f32(i)) == float(want[i]), i
+
+
+@pytest.mark.skipif(not R.ref_available("q6_k"), reason="oracle/_ref not built (needs the reference checkout)")
+def test_q6k_f32_unit_vectors_vs_reference_c_oracle():
+    blocks = [q6k_fixture_block()] + hostile_blocks(210, [(208, [0x00, 0x3C])])
+    for blk in blocks:
+        want, _ = R.run_ref_dequant("q6_k", blk.tobytes())
+        for i in range(256):
+            assert dot_f32(L.orc_dot_q6k_f32, blk, onehot_f32(i)) == float(want[i]), i
+
+
+@pytest.mark.skipif(not R.ref_available("q4_k"), reason="oracle/_ref not built (needs the reference checkout)")
+def test_kquant_f32_dense_dot_vs_reference_c_oracle():
+    # the C oracles' own dense dot (a different summation order) on the fixture blocks
+    rng = np.random.default_rng(3)
+    for name, blk, fn in (("q4_k", q4k_fixture_block(), L.orc_dot_q4k_f32),
+                          ("q6_k", q6k_fixture_block(), L.orc_dot_q6k_f32)):
+        for _ in range(4):
+            x = rng.normal(size=256).astype(np.float32)
+            deq, ref_dot = R.run_ref_dequant(name, blk.tobytes(), x)
+            got = dot_f32(fn, blk, x)
+            scale = float(np.abs(deq.astype(np.float64) * x).sum())
+            assert abs(got - float(ref_dot)) <= 4e-6 * scale, (name, got, ref_dot)
+
+
+def q4k_ones_block(d_bits=0x3C00, dmin_bits=0x0000, nib=0x11):
+    # every scale 1 and every min 0: the dot is the plain sum of x in the kernel's order
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = [d_bits & 0xFF, d_bits >> 8]
+    blk[2:4] = [dmin_bits & 0xFF, dmin_bits >> 8]
+    blk[4:16] = [1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1]
+    blk[16:144] = nib
+    return blk
+
+
+def q6k_ones_block():
+    # (0x1 | 2 << 4) - 32 = 1 in every position, every scale 1, d = 1
+    blk = np.zeros(210, np.uint8)
+    blk[0:128] = 0x11
+    blk[128:192] = 0xAA
+    blk[192:208] = 1
+    blk[208:210] = [0x00, 0x3C]
+    return blk
+
+
+def test_q4k_f32_order_known_answers():
+    big = float(2 ** 24)
+    ones = q4k_ones_block()
+    two = np.concatenate([ones, ones])
+    cases = [
+        # (x0*q0 + x8*q8) + (x16*q16 + x24*q24): the pair sums round first
+        ({0: big, 8: 1, 16: 1, 24: 1}, big + 2, ones),
+        # lanes summed left to right at the end
+        ({0: big, **{i: 1 for i in range(1, 8)}}, big, ones),
+        # each sub-block's term is added to its lane in turn
+        ({0: big, 32: 1, 64: 1}, big, ones),
+        ({0: big, 32: 1, 256: 1}, big, two),
+        # high nibbles are the odd sub-block (x offset +32): nibble 1 there too
+        ({32: big, 40: 1, 48: 1, 56: 1}, big + 2, ones),
+    ]
+    for xs, want, blk in cases:
+        x = np.zeros(len(blk) // 144 * 256, np.float32)
+        for k, v in xs.items():
+            x[k] = v
+        assert dot_f32(L.orc_dot_q4k_f32, blk, x) == want, xs
+    # the min term: a*(d*sc) - (x0+x8+x16+x24)*(dmin*m), products rounded apart
+    blk = q4k_ones_block(dmin_bits=0x3C00, nib=0x33)
+    blk[4:16] = [1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1]  # sc = m = 1 for sub-blocks 0..3, m(4..7) = 1 | 0 = 1
+    x = np.zeros(256, np.float32)
+    x[0] = np.float32(1 + 2 ** -23)
+    # 3*x0 rounds up to 3 + 2**-21 before x0 is subtracted: 2 + 2**-21, not the exact 2*x0 = 2 + 2**-22
+    assert dot_f32(L.orc_dot_q4k_f32, blk, x) == np.float32(np.float32(3) * x[0]) - x[0]
+
+
+def test_q6k_f32_order_known_answers():
+    big = float(2 ** 24)
+    ones = q6k_ones_block()
+    two = np.concatenate([ones, ones])
+    cases = [
+        # pair (16k+l, 16k+8+l) first, then added to the partial of its quarter
+        ({0: big, 16: 1, 24: 1}, big + 2, ones),
+        ({0: big, 8: 1, 16: 1}, big, ones),
+        # the four quarter partials as (s0 + s1) + (s2 + s3)
+        ({0: big, 32: 1, 64: 1, 96: 1}, big + 2, ones),
+        # halves and blocks add to the lane in turn; lanes left to right
+        ({0: big, 128: 1, 256: 1}, big, two),
+        ({0: big, **{i: 1 for i in range(1, 8)}}, big, ones),
+    ]
+    for xs, want, blk in cases:
+        x = np.zeros(len(blk) // 210 * 256, np.float32)
+        for k, v in xs.items():
+            x[k] = v
+        assert dot_f32(L.orc_dot_q6k_f32, blk, x) == want, xs
+    # (q * (d*sc)) * x with q = 3, sc = 3: 9 * x0 = 9 + 2**-20, where q * ((d*sc) * x0) gives 9 + 2**-19
+    blk = q6k_ones_block()
+    blk[0:128] = 0x33  # q = (3 | 2 << 4) - 32 = 3
+    blk[192:208] = 3
+    x = np.zeros(256, np.float32)
+    x[0] = np.float32(1 + 2 ** -23)
+    assert dot_f32(L.orc_dot_q6k_f32, blk, x) == np.float32(np.float32(9) * x[0])
+
+
+@pytest.mark.parametrize("kind", ["q4_k", "q6_k"])
+def test_kquant_f32_gemv_vs_float64_dequant(kind):
+    from c2slm_amd import gguf as G
+    rng = np.random.default_rng(21)
+    typ, synth, deq = ((G.Q4_K, G.synth_q4_k, R.dequant_q4k_f64) if kind == "q4_k"
+                       else (G.Q6_K, G.synth_q6_k, R.dequant_q6k_f64))
+    for rows, cols in [(48, 896), (16, 4864), (8, 1024)]:
+        nb = cols // 256
+        w = synth(rng, rows * nb)
+        x = rng.normal(size=cols).astype(np.float32)
+        y = O.gemv(w, typ, rows, cols, x=x, float_x=True)
+        wd = deq(w).reshape(rows, nb * 256)
+        xd = x[:nb * 256].astype(np.float64)  # floor(cols/256) super-blocks
+        want = wd @ xd
+        scale = np.abs(wd).sum(1) * np.abs(xd).max()
+        assert np.all(np.abs(y - want) <= 1e-5 * scale), (kind, rows, cols)
+
+
+def test_kquant_f32_reference_fixtures_vs_float64():
+    # internal/simd/c2_tensor_dot_q4_k_test.go:64-84 and c2_tensor_dot_q6_k_test.go:66-90
+    # (their golden values come from a C oracle absent from the checkout)
+    w4 = np.zeros(2 * 144, np.uint8)
+    for b in range(2):
+        blk = w4[b * 144:(b + 1) * 144]
+        blk[0:4] = [0x00, 0x3C, 0x00, 0x38]
+        blk[4:16] = [(b * 37 + i * 19 + 17) & 0xFF for i in range(12)]
+        blk[16:144] = [(b * 13 + i * 7 + 3) & 0xFF for i in range(128)]
+    x4 = np.array([((i % 17) - 8) * 0.125 for i in range(512)], np.float32)
+    w6 = np.zeros(2 * 210, np.uint8)
+    for b in range(2):
+        blk = w6[b * 210:(b + 1) * 210]
+        blk[0:128] = [(b * 23 + i * 11 + 5) & 0xFF for i in range(128)]
+        blk[128:192] = [(b * 17 + i * 7 + 1) & 0xFF for i in range(64)]
+        blk[192:208] = np.array([(i % 7) - 3 for i in range(16)], np.int8).view(np.uint8)
+        blk[208:210] = [0x00, 0x3C]
+    x6 = np.array([np.float32((i % 13) - 6) * np.float32(0.1) for i in range(512)], np.float32)
+    for fn, w, x, deq in ((L.orc_dot_q4k_f32, w4, x4, R.dequant_q4k_f64),
+                          (L.orc_dot_q6k_f32, w6, x6, R.dequant_q6k_f64)):
+        got = dot_f32(fn, w, x)
+        wd = deq(w).reshape(-1)
+        want = float(wd @ x.astype(np.float64))
+        assert abs(got - want) <= 1e-5 * float(np.abs(wd * x).sum()), (got, want)
+
+
 # ------------------------------------------------------------------ Q8_0
 
 
