@@ -110,6 +110,36 @@ def prefill_rate(ctx, desc, reps: int = 5):
             "ms_all": [round(t * 1e3, 3) for t in ts]}
 
 
+def float_x_dots(ctx, iters: int = 20, flush_mib: int = 512):
+    """The float-x row dots (c2h_gemv_f32: DispatchGEMV without a pool;
+    c2h_logits_ids: ComputeLogits with a target list) over a 151936 x 896
+    matrix of each format (random blocks; K-quant rows floor to 768
+    columns), the matrix evicted from the last-level cache by a 512 MiB copy
+    before each launch; plus a 64-id restricted-logits launch on the Q8_0
+    matrix.  GB/s counts the matrix bytes the dots read."""
+    from c2slm_amd import _lib as H
+    from c2slm_amd import gguf as G
+    rng = np.random.default_rng(SEED + 3)
+    V, E = 151936, 896
+    x = rng.normal(size=E).astype(np.float32)
+    out = {}
+    q8 = None
+    for name, typ, synth, qk, bs in (("q8_0", H.Q8_0, G.synth_q8_0, 32, 34), ("q6_k", H.Q6_K, G.synth_q6_k, 256, 210),
+                                     ("q4_k", H.Q4_K, G.synth_q4_k, 256, 144), ("q5_0", H.Q5_0, G.synth_q5_0, 32, 22)):
+        nb = E // qk
+        w = synth(rng, V * nb)
+        ms, _ = ctx.time_dot_rows(typ, w, x, V, E, iters=iters, flush_bytes=flush_mib << 20)
+        nbytes = V * nb * bs
+        out[name] = {"ms": round(ms, 4), "matrix_bytes": nbytes, "gb_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        if typ == H.Q8_0:
+            q8 = w
+    ids = rng.integers(0, V, 64).astype(np.int32)
+    ms, _ = ctx.time_dot_rows(H.Q8_0, q8, x, V, E, ids=ids, iters=iters, flush_bytes=flush_mib << 20)
+    out["logits_64_ids_q8_0_us"] = round(ms * 1e3, 2)
+    return out
+
+
 def long_context(gf, im_end, eos, lengths, steps: int = 16):
     """Decode at long contexts (the KV cache pre-filled with N(0,1) keys and
     values, token ids uniform): device-fed greedy steps whose last one
@@ -176,7 +206,8 @@ def main():
                     help="context lengths of the long-context decode lines ('' to skip)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill line")
     ap.add_argument("--no-real-formats", action="store_true", help="skip the real-model format line")
-    ap.add_argument("--only", choices=["prefill", "long"], default=None,
+    ap.add_argument("--no-float-dots", action="store_true", help="skip the float-x row-dot timings")
+    ap.add_argument("--only", choices=["prefill", "long", "float-dots"], default=None,
                     help="run just the prefill reps or just the long-context decode (profiler runs); "
                          "prints their JSON object, not the bench line")
     ap.add_argument("--prefill-reps", type=int, default=5)
@@ -205,6 +236,12 @@ def main():
     synth_model(path)
     gf = G.GGUFFile(path)
     _, im_end, eos = G.special_token_ids(gf)
+    if args.only == "float-dots":
+        ctx = H.Ctx(None)
+        print(json.dumps({"float_x_dots": float_x_dots(ctx)}))
+        ctx.close()
+        cleanup()
+        return
     if args.only == "long":
         lengths = [int(x) for x in args.long_context.split(",") if x]
         print(json.dumps({"long_context_decode": long_context(gf, im_end, eos, lengths)}))
@@ -259,6 +296,8 @@ def main():
         if rdir != tmpdir:
             os.rmdir(rdir)
 
+    fdots = None if args.no_float_dots else float_x_dots(ctx)
+
     base = None
     if not args.no_cpu_baseline:
         base = cpu_baseline(gf, prompt, args.steps, im_end, eos)
@@ -292,7 +331,8 @@ def main():
                   "pipelined_tok_s": round(1000.0 / pipelined_ms, 1),
                   "prefill_512": prefill,
                   "long_context_decode": longctx,
-                  "real_formats": realf},
+                  "real_formats": realf,
+                  "float_x_dots": fdots},
     }
     print(json.dumps(line))
     ctx.close()

@@ -86,6 +86,8 @@ def lib():
             "c2h_gemv_f32_dev": (C.c_int, [VP, I32, VP, VP, I32, I32, VP]),
             "c2h_logits_ids": (C.c_int, [VP, VP, I32, VP]),
             "c2h_logits_ids_dev": (C.c_int, [VP, VP, I32, VP]),
+            "c2h_time_dot_rows": (C.c_int, [VP, I32, VP, VP, I32, I32, VP, I32, I32, C.c_int64, VP,
+                                            C.POINTER(C.c_float)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -245,6 +247,23 @@ class Ctx:
                                  _p(isums) if isums is not None else None))
         return (y, isums) if want_isums else y
 
+
+    def time_dot_rows(self, ggml_type: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int, ids=None,
+                      n: int | None = None, iters: int = 20, flush_bytes: int = 0):
+        """(ms per launch, results) of the float-x row dots: rows 0..n-1, or
+        the listed ids."""
+        w = np.ascontiguousarray(w)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if ids is not None:
+            ids = np.ascontiguousarray(ids, dtype=np.int32)
+            n = len(ids)
+        n = rows if n is None else n
+        y = np.empty(n, np.float32)
+        ms = C.c_float()
+        self._chk(lib().c2h_time_dot_rows(self.h, ggml_type, _p(w), _p(x), rows, cols,
+                                          _p(ids) if ids is not None else None, n, iters, flush_bytes, _p(y),
+                                          C.byref(ms)))
+        return ms.value, y
 
     def gemv_f32(self, ggml_type: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int) -> np.ndarray:
         """engine.DispatchGEMV without a pool: y = W·x on f32 x."""

@@ -99,6 +99,8 @@ struct c2h_ctx {
   int32_t* ids_dev = nullptr;
   float* ids_y = nullptr;
   int ids_cap = 0;
+  bool dot_attr = false;  // k_dot_rows LDS limit raised
+  uint8_t* vq8k = nullptr;  // Q8_K row of normX for a K-quant output.weight
 };
 
 namespace {
@@ -432,7 +434,60 @@ int vocab_grid(c2h_ctx* c, int64_t rows, int64_t cols, int* grid) {
   return C2H_OK;
 }
 
+XSel plain_x(const float* x) {
+  XSel X;
+  memset(&X, 0, sizeof(X));
+  X.x = x;
+  return X;
+}
+
+void launch_dot_rows(c2h_ctx* c, int type, WeightRef w, int rows, int cols, XSel X, const int32_t* ids, int n,
+                     int scatter, float* y);
+int dot_rows_ready(c2h_ctx* c, int64_t cols);
+
+// The vocab projection of the step: the fused Q8_0 kernel (logits, penalty
+// and argmax candidates in one pass), or for the other output formats the
+// pooled DispatchGEMV (engine/pool.go:122-154: Q4_K / Q6_K on the Q8_K row
+// of normX, Q5_0 on f32 normX) into logits_out (else the context's logits
+// buffer), then k_logits_pick for the penalty and the candidates.
 void enqueue_vocab(c2h_ctx* c, int apply_penalty, float* logits_out, int x_sel, const float* x) {
+  const Tensor& ow = out_weight(c);
+  if (ow.type != C2H_Q8_0) {
+    XSel X;
+    memset(&X, 0, sizeof(X));
+    X.x = x;
+    X.buf[0] = c->normx[0];
+    X.buf[1] = c->normx[1];
+    X.state = c->state_dev;
+    X.sel = x_sel;
+    float* y = logits_out ? logits_out : c->logits;
+    if (ow.type == C2H_Q5_0) {
+      launch_dot_rows(c, ow.type, ow.ref(), (int)ow.rows, (int)ow.cols, X, nullptr, (int)ow.rows, 0, y);
+    } else {
+      const int nb = nb_k(ow.cols);
+      hipLaunchKernelGGL(k_quantize_q8k_sel, dim3((nb + 3) / 4), dim3(256), 0, c->stream, X, nb, c->vq8k);
+      GemvParams P;
+      memset(&P, 0, sizeof(P));
+      P.prologue = PRO_Q8K;
+      P.q8k_in = c->vq8k;
+      P.nb_in = nb;
+      add_job(P, ow, nullptr, MODE_STORE, y, nullptr, nullptr);
+      hipLaunchKernelGGL(k_gemv_q8k, job_grid(P), dim3(256), gemv_q8k_lds_bytes(), c->stream, P);
+    }
+    if (apply_penalty || !logits_out) {
+      PickParams K;
+      memset(&K, 0, sizeof(K));
+      K.logits = y;
+      K.n_vocab = c->desc.n_vocab;
+      K.token_ids = c->token_ids;
+      K.apply_penalty = apply_penalty;
+      K.state = c->state_dev;
+      K.part_v = c->part_v;
+      K.part_i = c->part_i;
+      hipLaunchKernelGGL(k_logits_pick, dim3(c->n_part), dim3(256), 0, c->stream, K);
+    }
+    return;
+  }
   VocabParams V;
   memset(&V, 0, sizeof(V));
   V.w = out_weight(c).ref();
@@ -603,8 +658,10 @@ int validate_model(c2h_ctx* c) {
   if (!c->has_model) return fail(c, C2H_ERR_STATE, "context has no model");
   if (!c->embd.present() || c->embd.type != C2H_Q8_0)
     return fail(c, C2H_ERR_STATE, "token_embd (Q8_0) not uploaded");
-  if (c->output.present() && c->output.type != C2H_Q8_0)
-    return fail(c, C2H_ERR_UNSUPPORTED, "output.weight must be Q8_0");
+  if (c->output.present() && c->output.type == C2H_Q5_0) {
+    int rc = dot_rows_ready(c, c->output.cols);
+    if (rc) return rc;
+  }
   if (!c->output_norm) return fail(c, C2H_ERR_STATE, "output_norm not uploaded");
   for (int l = 0; l < c->desc.n_layers; ++l) {
     Layer& L = c->layers[l];
@@ -826,7 +883,8 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   }
   if ((rc = vocab_grid(c, D.n_vocab, D.n_embd, &c->n_part))) return bail(rc);
   if ((rc = dalloc(c, &c->part_v, (size_t)c->n_part * 4)) || (rc = dalloc(c, &c->part_i, (size_t)c->n_part * 4)) ||
-      (rc = dalloc(c, &c->logits, (size_t)D.n_vocab * 4)))
+      (rc = dalloc(c, &c->logits, (size_t)D.n_vocab * 4)) ||
+      (rc = dalloc(c, &c->vq8k, (size_t)nb_k(D.n_embd) * BS_Q8K)))
     return bail(rc);
   // Attention: k_attn_core while a token attends to at most att_split
   // positions (staged V | all scores in LDS, within the 160 KB of a gfx950
@@ -911,7 +969,7 @@ int c2h_upload_tensor(c2h_ctx* c, int32_t layer, int32_t role, int32_t type, int
   }
   if (role == C2H_ROLE_OUTPUT) {
     if ((rc = want(V, E))) return rc;
-    if (type != C2H_Q8_0) return fail(c, C2H_ERR_UNSUPPORTED, "output.weight must be Q8_0");
+    // Q8_0 runs the fused vocab kernel; Q4_K / Q6_K / Q5_0 the pooled GEMV and k_logits_pick
     return upload_quant(c, &c->output, type, rows, cols, host, bytes);
   }
   if (role == C2H_ROLE_OUTPUT_NORM) return upload_f32(c, &c->output_norm, E, type, rows, cols, host, bytes);
@@ -1410,25 +1468,41 @@ int64_t float_x_blocks(int type, int64_t cols) {
   return (type == C2H_Q4_K || type == C2H_Q6_K) ? cols / 256 : cols / 32;
 }
 
-void launch_dot_rows(c2h_ctx* c, int type, WeightRef w, int rows, int cols, const float* x, const int32_t* ids, int n,
+void launch_dot_rows(c2h_ctx* c, int type, WeightRef w, int rows, int cols, XSel X, const int32_t* ids, int n,
                      int scatter, float* y) {
   DotRowsParams P;
   memset(&P, 0, sizeof(P));
   P.w = w;
   P.rows = rows;
   P.cols = cols;
-  P.x = x;
+  P.X = X;
   P.ids = ids;
   P.n = n;
   P.scatter = scatter;
   P.y = y;
   const dim3 grid((n + DOT_ROWS_PER_WG - 1) / DOT_ROWS_PER_WG), block(256);
+  const size_t lds = dot_rows_lds_bytes(type, cols);
   switch (type) {
-    case C2H_Q4_K: hipLaunchKernelGGL(k_dot_rows<T_Q4_K>, grid, block, 0, c->stream, P); break;
-    case C2H_Q6_K: hipLaunchKernelGGL(k_dot_rows<T_Q6_K>, grid, block, 0, c->stream, P); break;
-    case C2H_Q8_0: hipLaunchKernelGGL(k_dot_rows<T_Q8_0>, grid, block, 0, c->stream, P); break;
-    default: hipLaunchKernelGGL(k_dot_rows<T_Q5_0>, grid, block, 0, c->stream, P); break;
+    case C2H_Q4_K: hipLaunchKernelGGL(k_dot_rows<T_Q4_K>, grid, block, lds, c->stream, P); break;
+    case C2H_Q6_K: hipLaunchKernelGGL(k_dot_rows<T_Q6_K>, grid, block, lds, c->stream, P); break;
+    case C2H_Q8_0: hipLaunchKernelGGL(k_dot_rows<T_Q8_0>, grid, block, lds, c->stream, P); break;
+    default: hipLaunchKernelGGL(k_dot_rows<T_Q5_0>, grid, block, lds, c->stream, P); break;
   }
+}
+
+// Shape checks of the float-x row dots, and (once per context) their LDS
+// limit: x is staged whole, up to DOT_MAX_COLS floats.
+int dot_rows_ready(c2h_ctx* c, int64_t cols) {
+  if (cols > DOT_MAX_COLS) return fail(c, C2H_ERR_UNSUPPORTED, "float-x rows run up to %d columns", DOT_MAX_COLS);
+  if (!c->dot_attr) {
+    const void* ks[] = {(const void*)k_dot_rows<T_Q4_K>, (const void*)k_dot_rows<T_Q6_K>,
+                        (const void*)k_dot_rows<T_Q8_0>, (const void*)k_dot_rows<T_Q5_0>};
+    for (const void* k : ks)
+      if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, DOT_MAX_COLS * 4) != hipSuccess)
+        return fail(c, C2H_ERR_HIP, "row-dot LDS attribute");
+    c->dot_attr = true;
+  }
+  return C2H_OK;
 }
 
 // Weight view of a c2h_pack_weights buffer.
@@ -1453,7 +1527,9 @@ int c2h_gemv_f32_dev(c2h_ctx* c, int32_t type, const void* w_packed, const float
   }
   if (!w_packed) return C2H_ERR_INVALID;
   if (reinterpret_cast<uintptr_t>(x) & 15) return fail(c, C2H_ERR_INVALID, "x must be 16-byte aligned");
-  launch_dot_rows(c, type, packed_ref(type, rows, cols, w_packed), rows, cols, x, nullptr, rows, 0, y);
+  int rc = dot_rows_ready(c, cols);
+  if (rc) return rc;
+  launch_dot_rows(c, type, packed_ref(type, rows, cols, w_packed), rows, cols, plain_x(x), nullptr, rows, 0, y);
   HIPCHK(c, hipGetLastError());
   return C2H_OK;
 }
@@ -1466,6 +1542,7 @@ int c2h_gemv_f32(c2h_ctx* c, int32_t type, const void* w, const float* x, int32_
     return C2H_OK;
   }
   if (!w) return C2H_ERR_INVALID;
+  if (int rc0 = dot_rows_ready(c, cols)) return rc0;
   const size_t pbytes = c2h_packed_size(type, rows, cols);
   std::vector<uint8_t> packed(pbytes);
   size_t qb, db;
@@ -1507,7 +1584,8 @@ int c2h_logits_ids_dev(c2h_ctx* c, const int32_t* ids, int32_t n_ids, float* log
     return C2H_OK;
   }
   const Tensor& t = out_weight(c);
-  launch_dot_rows(c, t.type, t.ref(), (int)t.rows, (int)t.cols, c->normx[c->nx_cur], ids, n_ids, 1, logits);
+  if ((rc = dot_rows_ready(c, t.cols))) return rc;
+  launch_dot_rows(c, t.type, t.ref(), (int)t.rows, (int)t.cols, plain_x(c->normx[c->nx_cur]), ids, n_ids, 1, logits);
   HIPCHK(c, hipGetLastError());
   return C2H_OK;
 }
@@ -1532,7 +1610,9 @@ int c2h_logits_ids(c2h_ctx* c, const int32_t* ids, int32_t n_ids, float* logits_
   }
   HIPCHK(c, stream_copy(c->stream, c->ids_dev, ids, (size_t)n_ids * 4, hipMemcpyHostToDevice));
   const Tensor& t = out_weight(c);
-  launch_dot_rows(c, t.type, t.ref(), (int)t.rows, (int)t.cols, c->normx[c->nx_cur], c->ids_dev, n_ids, 0, c->ids_y);
+  if ((rc = dot_rows_ready(c, t.cols))) return rc;
+  launch_dot_rows(c, t.type, t.ref(), (int)t.rows, (int)t.cols, plain_x(c->normx[c->nx_cur]), c->ids_dev, n_ids, 0,
+                  c->ids_y);
   HIPCHK(c, hipGetLastError());
   std::vector<float> y((size_t)n_ids);
   HIPCHK(c, stream_copy(c->stream, y.data(), c->ids_y, (size_t)n_ids * 4, hipMemcpyDeviceToHost));
@@ -1731,6 +1811,70 @@ int c2h_time_vocab(c2h_ctx* c, int32_t iters, int32_t pos, int32_t in_step, floa
     if (e != hipSuccess) rc = fail(c, C2H_ERR_HIP, "vocab timing: %s", hipGetErrorString(e));
   }
   for (auto& e : ev) (void)hipEventDestroy(e);
+  if (rc) return rc;
+  *ms = (float)(total / iters);
+  return C2H_OK;
+}
+
+int c2h_time_dot_rows(c2h_ctx* c, int32_t type, const void* w, const float* x, int32_t rows, int32_t cols,
+                      const int32_t* ids, int32_t n, int32_t iters, int64_t flush_bytes, float* y_out, float* ms) {
+  if (!c || !w || !x || !ms || rows <= 0 || cols <= 0 || n <= 0 || iters <= 0 || iters > 4096 || flush_bytes < 0)
+    return C2H_ERR_INVALID;
+  if (!float_x_type(type) || float_x_blocks(type, cols) == 0) return fail(c, C2H_ERR_UNSUPPORTED, "no float row dot");
+  if (!ids && n > rows) return fail(c, C2H_ERR_INVALID, "n > rows without ids");
+  HIPCHK(c, hipSetDevice(c->device));
+  if (int rc0 = dot_rows_ready(c, cols)) return rc0;
+  const size_t pbytes = c2h_packed_size(type, rows, cols), n16 = (size_t)flush_bytes / 16;
+  std::vector<uint8_t> packed(pbytes);
+  size_t qb, db;
+  packed_parts(type, rows, cols, &qb, &db);
+  pack_host(type, rows, cols, reinterpret_cast<const uint8_t*>(w), packed.data(), packed.data() + qb);
+  uint8_t* dw = nullptr;
+  float *dx = nullptr, *dy = nullptr;
+  int32_t* di = nullptr;
+  uint4* fl = nullptr;
+  std::vector<hipEvent_t> ev(2 * (size_t)iters, nullptr);
+  auto cleanup = [&]() {
+    (void)hipStreamSynchronize(c->stream);
+    for (auto& e : ev)
+      if (e) (void)hipEventDestroy(e);
+    for (void* p : {(void*)dw, (void*)dx, (void*)dy, (void*)di, (void*)fl})
+      if (p) (void)hipFree(p);
+  };
+  int rc = C2H_OK;
+  if (hipMalloc(&dw, pbytes) != hipSuccess || hipMalloc(&dx, (size_t)cols * 4) != hipSuccess ||
+      hipMalloc(&dy, (size_t)n * 4) != hipSuccess || (ids && hipMalloc(&di, (size_t)n * 4) != hipSuccess) ||
+      (n16 && hipMalloc(&fl, 2 * n16 * 16) != hipSuccess))
+    rc = fail(c, C2H_ERR_HIP, "hipMalloc failed");
+  if (!rc && (stream_copy(c->stream, dw, packed.data(), pbytes, hipMemcpyHostToDevice) != hipSuccess ||
+              stream_copy(c->stream, dx, x, (size_t)cols * 4, hipMemcpyHostToDevice) != hipSuccess ||
+              (ids && stream_copy(c->stream, di, ids, (size_t)n * 4, hipMemcpyHostToDevice) != hipSuccess)))
+    rc = fail(c, C2H_ERR_HIP, "copy in failed");
+  for (auto& e : ev)
+    if (!rc && hipEventCreate(&e) != hipSuccess) rc = fail(c, C2H_ERR_HIP, "hipEventCreate");
+  const WeightRef wr = packed_ref(type, rows, cols, dw);
+  if (!rc) launch_dot_rows(c, type, wr, rows, cols, plain_x(dx), di, n, 0, dy);  // warm-up
+  for (int i = 0; i < iters && rc == C2H_OK; ++i) {
+    // copying flush_bytes (2x that touched) between launches evicts the matrix from the last-level cache
+    if (n16) hipLaunchKernelGGL(k_copy16, dim3(1024), dim3(256), 0, c->stream, fl, fl + n16, n16);
+    (void)hipEventRecord(ev[2 * i], c->stream);
+    launch_dot_rows(c, type, wr, rows, cols, plain_x(dx), di, n, 0, dy);
+    (void)hipEventRecord(ev[2 * i + 1], c->stream);
+  }
+  if (!rc && hipGetLastError() != hipSuccess) rc = fail(c, C2H_ERR_HIP, "launch failed");
+  double total = 0;
+  if (!rc) {
+    hipError_t e = hipEventSynchronize(ev.back());
+    for (int i = 0; i < iters && e == hipSuccess; ++i) {
+      float t = 0;
+      e = hipEventElapsedTime(&t, ev[2 * i], ev[2 * i + 1]);
+      total += t;
+    }
+    if (e != hipSuccess) rc = fail(c, C2H_ERR_HIP, "dot timing: %s", hipGetErrorString(e));
+  }
+  if (!rc && y_out && stream_copy(c->stream, y_out, dy, (size_t)n * 4, hipMemcpyDeviceToHost) != hipSuccess)
+    rc = fail(c, C2H_ERR_HIP, "copy out failed");
+  cleanup();
   if (rc) return rc;
   *ms = (float)(total / iters);
   return C2H_OK;

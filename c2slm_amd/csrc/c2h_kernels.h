@@ -327,6 +327,27 @@ __global__ void k_pf_swiglu(const float* gate, const float* up, float* h, int n,
 template <int NB8>
 __global__ void k_vocab(VocabParams P);
 constexpr int VOCAB_MIN_NB8 = 24, VOCAB_MAX_NB8 = 32;  // instantiated widths (Q8_0 blocks per row)
+// An f32 input vector: x itself, or (sel) the normX buffer the step state
+// names, for kernels inside replayed graphs.
+struct XSel {
+  const float* x;
+  const float* buf[2];
+  const C2hState* state;
+  int sel;
+};
+
+struct PickParams {
+  const float* logits;
+  int n_vocab;
+  const int32_t* token_ids;
+  int apply_penalty;
+  const C2hState* state;
+  float* part_v;
+  int* part_i;
+};
+__global__ void k_logits_pick(PickParams P);
+__global__ void k_quantize_q8k_sel(XSel X, int nb, uint8_t* __restrict__ y);
+
 // One f32 dot per output (float-x order of each format).  Output i is row
 // ids[i] when ids is given (ids outside [0, rows) are skipped), else row i;
 // it is stored to y[ids[i]] when scatter is set, else to y[i].  x is 16-byte
@@ -334,7 +355,7 @@ constexpr int VOCAB_MIN_NB8 = 24, VOCAB_MAX_NB8 = 32;  // instantiated widths (Q
 struct DotRowsParams {
   WeightRef w;
   int rows, cols;
-  const float* x;
+  XSel X;
   const int32_t* ids;
   int n;
   int scatter;
@@ -343,6 +364,11 @@ struct DotRowsParams {
 template <int TYPE>
 __global__ void k_dot_rows(DotRowsParams P);
 constexpr int DOT_ROWS_PER_WG = 32;
+constexpr int DOT_MAX_COLS = 32768;  // x staged in LDS: 128 KB
+// Dynamic LDS of k_dot_rows: x of the row's whole groups (32 floats each).
+__host__ __device__ inline int dot_rows_lds_bytes(int type, int cols) {
+  return (type == 12 || type == 14) ? (cols / 256) * 256 * 4 : (cols / 32) * 32 * 4;  // Q4_K, Q6_K: whole super-blocks
+}
 __global__ void k_argmax_final(const float* pv, const int* pi, int n, C2hState* state);
 __global__ void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16);
 __global__ void k_empty(const int* __restrict__ flag, int* __restrict__ out);

@@ -167,7 +167,7 @@ __device__ __forceinline__ void quantize_row_waves(const float4 (&v)[(NB + NW - 
 // The same quantiser writing the reference's 292-byte Q8_K blocks (f32 d,
 // 256 int8 quants, 16 int16 bsums): one wave per block, four blocks per
 // workgroup.
-__global__ void __launch_bounds__(256) k_quantize_q8k(const float* __restrict__ x, int nb, uint8_t* __restrict__ y) {
+__device__ __forceinline__ void quantize_q8k_wg(const float* __restrict__ x, int nb, uint8_t* __restrict__ y) {
   __shared__ Q8KRow<4> s;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int b = (int)blockIdx.x * 4 + wave;
@@ -179,6 +179,15 @@ __global__ void __launch_bounds__(256) k_quantize_q8k(const float* __restrict__ 
   reinterpret_cast<uint32_t*>(yb + 4)[lane] = s.q[wave][lane];
   if (lane < 16) reinterpret_cast<int16_t*>(yb + 260)[lane] = (int16_t)s.bs[wave][lane];
   if (lane == 0) *reinterpret_cast<float*>(yb) = s.d[wave];
+}
+
+__global__ void __launch_bounds__(256) k_quantize_q8k(const float* __restrict__ x, int nb, uint8_t* __restrict__ y) {
+  quantize_q8k_wg(x, nb, y);
+}
+
+// The same on the normX buffer the step state names (graph replays).
+__global__ void __launch_bounds__(256) k_quantize_q8k_sel(XSel X, int nb, uint8_t* __restrict__ y) {
+  quantize_q8k_wg(X.sel ? X.buf[X.state->nx_in] : X.x, nb, y);
 }
 
 // ------------------------------------------------------------ RMSNorm (A8)
@@ -2281,6 +2290,47 @@ __global__ void __launch_bounds__(256) k_argmax_final(const float* pv, const int
   if (threadIdx.x == 0) state->token = tok;
 }
 
+// Repetition penalty and argmax candidates over a logits vector (the
+// vocab projections other than the fused Q8_0 one): c2slm.go:157-183 as the
+// fused kernel applies it -- each occurrence of a row id among the window's
+// TokenIDs[max(0, pos-64), pos) divides a positive logit by the penalty or
+// multiplies a non-positive one, im_end and eos exempt; NaN never wins
+// except at id 0.  Workgroup w leaves its best in part_v/part_i[w].
+__global__ void __launch_bounds__(256) k_logits_pick(PickParams P) {
+  __shared__ int win[64];
+  __shared__ ArgCand red[4];
+  const int tid = threadIdx.x;
+  const int pos = P.state->pos;
+  const int wstart = max(pos - 64, 0);
+  const int nwin = (P.apply_penalty && pos > 0) ? (pos - wstart) : 0;
+  if (tid < 64) win[tid] = (tid < nwin) ? P.token_ids[wstart + tid] : -1;
+  __syncthreads();
+  const int im_end = P.state->im_end, eos = P.state->eos;
+  const float penalty = P.state->penalty;
+  ArgCand best;
+  best.v = -__builtin_inff();
+  best.i = 0x7fffffff;
+  for (int row = (int)blockIdx.x * 256 + tid; row < P.n_vocab; row += (int)gridDim.x * 256) {
+    float v = P.logits[row];
+    if (row != im_end && row != eos)
+      for (int e = 0; e < nwin; ++e)
+        if (win[e] == row) v = (v > 0.0f) ? (v / penalty) : (v * penalty);
+    ArgCand cand;
+    cand.v = (v != v) ? ((row == 0) ? __builtin_inff() : -__builtin_inff()) : v;
+    cand.i = row;
+    best = arg_better(best, cand);
+  }
+  best = wave_argmax(best);
+  if ((tid & 63) == 0) red[tid >> 6] = best;
+  __syncthreads();
+  if (tid == 0) {
+    ArgCand r = red[0];
+    for (int w = 1; w < 4; ++w) r = arg_better(r, red[w]);
+    P.part_v[blockIdx.x] = r.v;
+    P.part_i[blockIdx.x] = r.i;
+  }
+}
+
 // A kernel that does no work (one flag read, a write that never happens):
 // its launches in a graph measure the per-launch floor.
 __global__ void __launch_bounds__(256) k_empty(const int* __restrict__ flag, int* __restrict__ out) {
@@ -2314,10 +2364,12 @@ __global__ void __launch_bounds__(256) k_copy16(const uint4* __restrict__ src, u
 //   Q5_0 (tensor/ops.go:40-74) is one sequential chain over the blocks of
 //     d * (block sum); lane l forms the block sums of blocks l, l+8, ... and
 //     the chain adds them in block order.
-// The K-quant super-blocks of the 8 rows of a wave are staged through LDS
-// with 16-byte loads (the 144 / 208 byte blocks of the device layout are
-// 16-byte aligned), the next block's loads in flight while the current one
-// is consumed.  x is read from global memory (all rows share it).
+// x sits in LDS permuted per 32-element group g: float4 [g][l] holds
+// x[32g + l + 8i] for i = 0..3, the four values lane l of every format
+// needs from that group (one 16-byte LDS read).  The K-quant super-blocks
+// of a wave's 8 rows are staged through wave-private LDS with 16-byte loads
+// (the 144 / 208 byte blocks of the device layout are 16-byte aligned),
+// the next block's loads in flight while the current one is consumed.
 
 template <int TYPE>
 struct DotStage {
@@ -2326,27 +2378,39 @@ struct DotStage {
   static constexpr int LOADS = (PER_WAVE + 63) / 64;                                 // 2
 };
 
-__device__ __forceinline__ float dot_lane_sum(float acc) { return q80_row_sum(acc); }
+// LDS ordering among the lanes of one wave (LDS serves a wave's accesses in
+// issue order; this keeps the compiler from moving them across).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ float f4c(const float4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
 template <int TYPE>
 __global__ void __launch_bounds__(256) k_dot_rows(DotRowsParams P) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float4* xs = reinterpret_cast<float4*>(smem);  // [groups][8]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l = tid & 7;
-  const int i = (int)blockIdx.x * 32 + (tid >> 3);
+  const int i = (int)blockIdx.x * DOT_ROWS_PER_WG + (tid >> 3);
   int r = -1;
   if (i < P.n) r = P.ids ? P.ids[i] : i;
   const bool valid = (r >= 0 && r < P.rows);
   const int rc = valid ? r : 0;  // rows of empty slots are read but never stored
   float acc = 0.0f;
+  constexpr bool KQ = (TYPE == T_Q4_K || TYPE == T_Q6_K);
+  const int nb = KQ ? P.cols / 256 : P.cols / 32;  // super-blocks or blocks
+  const int groups = KQ ? nb * 8 : nb;
 
-  if (TYPE == T_Q4_K || TYPE == T_Q6_K) {
-    typedef DotStage<TYPE> S;
-    constexpr int BS = (TYPE == T_Q4_K) ? BS_Q4K : BS_Q6K_PACKED;
-    __shared__ uint4 stage[4][S::PER_WAVE];
-    const int nb = P.cols / 256;
-    // the two pieces this lane fetches per block: slot row, byte offset
-    const uint8_t* src[S::LOADS];
-    bool live[S::LOADS];
+  // weight loads first (their latency overlaps the x staging)
+  typedef DotStage<TYPE> S;
+  constexpr int BS = (TYPE == T_Q4_K) ? BS_Q4K : BS_Q6K_PACKED;
+  const uint8_t* src[S::LOADS];
+  bool live[S::LOADS];
+  uint4 nxt[S::LOADS];
+  if constexpr (KQ) {
 #pragma unroll
     for (int k = 0; k < S::LOADS; ++k) {
       const int p = lane + 64 * k;
@@ -2355,30 +2419,60 @@ __global__ void __launch_bounds__(256) k_dot_rows(DotRowsParams P) {
       const int slot = pc / S::PIECES, piece = pc - slot * S::PIECES;
       const int srow = __shfl(rc, slot * 8);
       src[k] = P.w.q + ((size_t)srow * nb) * BS + 16 * piece;
+      nxt[k] = live[k] ? *reinterpret_cast<const uint4*>(src[k]) : make_uint4(0, 0, 0, 0);
     }
-    uint4 nxt[S::LOADS];
+  }
+  // Q8_0: the first batch of eight 4-block groups; Q5_0: this lane's first block
+  uint4 qv[8], dv[4];
+  const uint8_t* rowp = P.w.q + (size_t)rc * (TYPE == T_Q8_0 ? q8_0_row_stride(nb) : (size_t)nb * 24);
+  const int nq = q8_0_nq(nb);
+  const uint4* dvec = reinterpret_cast<const uint4*>(rowp);  // Q8_0: eight fp16 scales per uint4
+  const uint4* qrow = reinterpret_cast<const uint4*>(rowp + (size_t)q8_0_dpad(nb) * 2);
+  auto q80_batch = [&](int q0) {
 #pragma unroll
-    for (int k = 0; k < S::LOADS; ++k) nxt[k] = live[k] ? *reinterpret_cast<const uint4*>(src[k]) : make_uint4(0, 0, 0, 0);
-    const uint8_t* sb = reinterpret_cast<const uint8_t*>(&stage[wave][(tid >> 3 & 7) * S::PIECES]);
+    for (int bq = 0; bq < 8; ++bq) qv[bq] = qrow[min(q0 + bq, nq - 1) * 8 + l];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) dv[k] = dvec[q0 / 2 + k];  // within the padded scale vector
+  };
+  uint4 qs5;
+  uint2 hd5;
+  auto q50_block = [&](int b) {
+    qs5 = reinterpret_cast<const uint4*>(rowp)[b];
+    hd5 = reinterpret_cast<const uint2*>(rowp + (size_t)nb * 16)[b];
+  };
+  if constexpr (TYPE == T_Q8_0) q80_batch(0);
+  if constexpr (TYPE == T_Q5_0) q50_block(min(l, nb - 1));
+  const float* x = P.X.sel ? P.X.buf[P.X.state->nx_in] : P.X.x;
+  for (int e = tid; e < groups * 32; e += 256) {
+    const int g = e >> 5, kk = e & 31;
+    reinterpret_cast<float*>(xs)[(g * 8 + (kk & 7)) * 4 + (kk >> 3)] = x[e];
+  }
+  __syncthreads();
+
+  if constexpr (KQ) {
+    __shared__ uint4 stage[4][2][S::PER_WAVE];
     for (int b = 0; b < nb; ++b) {
-      __syncthreads();  // the previous block is consumed
+      uint4* st = stage[wave][b & 1];
 #pragma unroll
       for (int k = 0; k < S::LOADS; ++k)
-        if (live[k]) stage[wave][lane + 64 * k] = nxt[k];
-      __syncthreads();
+        if (live[k]) st[lane + 64 * k] = nxt[k];
+      wave_lds_sync();
       if (b + 1 < nb) {
 #pragma unroll
         for (int k = 0; k < S::LOADS; ++k)
           if (live[k]) nxt[k] = *reinterpret_cast<const uint4*>(src[k] + (size_t)(b + 1) * BS);
       }
-      const float* xs = P.x + b * 256;
-      if (TYPE == T_Q4_K) {
+      const uint8_t* sb = reinterpret_cast<const uint8_t*>(&st[(lane >> 3) * S::PIECES]);
+      const float4* xg = xs + (size_t)b * 64 + l;  // group (8b + s) at xg[8s]
+      if constexpr (TYPE == T_Q4_K) {
         const uint4 hdr = *reinterpret_cast<const uint4*>(sb);
         const float d = fp16_simd(hdr.x & 0xffffu), dmin = fp16_simd(hdr.x >> 16);
         const uint32_t sw[3] = {hdr.y, hdr.z, hdr.w};  // scale bytes 0..11
         auto sbyte = [&](int k) { return (sw[k >> 2] >> (8 * (k & 3))) & 0xffu; };
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
+          const uint8_t* qb = sb + 16 + 32 * j + l;
+          const uint32_t qq[4] = {qb[0], qb[8], qb[16], qb[24]};
 #pragma unroll
           for (int half = 0; half < 2; ++half) {
             const int is = 2 * j + half;
@@ -2392,16 +2486,14 @@ __global__ void __launch_bounds__(256) k_dot_rows(DotRowsParams P) {
             }
             const float dsc = d * (float)sc;
             const float dmm = dmin * (float)mn;
-            const float* xb = xs + 64 * j + 32 * half + l;
-            const uint8_t* qb = sb + 16 + 32 * j + l;
+            const float4 xv = xg[8 * is];
             const int sh = 4 * half;
-            const float x0 = xb[0], x1 = xb[8], x2 = xb[16], x3 = xb[24];
-            const float p0 = (float)((qb[0] >> sh) & 15) * x0;
-            const float p1 = (float)((qb[8] >> sh) & 15) * x1;
-            const float p2 = (float)((qb[16] >> sh) & 15) * x2;
-            const float p3 = (float)((qb[24] >> sh) & 15) * x3;
+            const float p0 = (float)((qq[0] >> sh) & 15u) * xv.x;
+            const float p1 = (float)((qq[1] >> sh) & 15u) * xv.y;
+            const float p2 = (float)((qq[2] >> sh) & 15u) * xv.z;
+            const float p3 = (float)((qq[3] >> sh) & 15u) * xv.w;
             const float a = (p0 + p1) + (p2 + p3);
-            const float sx = (x0 + x1) + (x2 + x3);
+            const float sx = (xv.x + xv.y) + (xv.z + xv.w);
             const float t = sx * dmm;
             acc = acc + (a * dsc - t);
           }
@@ -2413,7 +2505,9 @@ __global__ void __launch_bounds__(256) k_dot_rows(DotRowsParams P) {
           const uint8_t* ql = sb + 64 * h;
           const uint8_t* qh = sb + 128 + 32 * h;
           const int8_t* scl = reinterpret_cast<const int8_t*>(sb + 192 + 8 * h);
-          const float* xb = xs + 128 * h;
+          float4 xv[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) xv[q] = xg[8 * (4 * h + q)];
           float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
 #pragma unroll
           for (int k = 0; k < 2; ++k) {
@@ -2428,10 +2522,10 @@ __global__ void __launch_bounds__(256) k_dot_rows(DotRowsParams P) {
               const int v1 = (int)((c & 15u) | (((hb >> 2) & 3u) << 4)) - 32;
               const int v2 = (int)((a >> 4) | (((hb >> 4) & 3u) << 4)) - 32;
               const int v3 = (int)((c >> 4) | (((hb >> 6) & 3u) << 4)) - 32;
-              pr[0][t] = ((float)v0 * dk0) * xb[o];
-              pr[1][t] = ((float)v1 * dk1) * xb[32 + o];
-              pr[2][t] = ((float)v2 * dk2) * xb[64 + o];
-              pr[3][t] = ((float)v3 * dk3) * xb[96 + o];
+              pr[0][t] = ((float)v0 * dk0) * f4c(xv[0], 2 * k + t);
+              pr[1][t] = ((float)v1 * dk1) * f4c(xv[1], 2 * k + t);
+              pr[2][t] = ((float)v2 * dk2) * f4c(xv[2], 2 * k + t);
+              pr[3][t] = ((float)v3 * dk3) * f4c(xv[3], 2 * k + t);
             }
             s0 = s0 + (pr[0][0] + pr[0][1]);
             s1 = s1 + (pr[1][0] + pr[1][1]);
@@ -2442,45 +2536,60 @@ __global__ void __launch_bounds__(256) k_dot_rows(DotRowsParams P) {
         }
       }
     }
-    acc = dot_lane_sum(acc);
-  } else if (TYPE == T_Q8_0) {
-    const int nb8 = P.cols / 32, nq = q8_0_nq(nb8);
-    const uint8_t* rowp = P.w.q + (size_t)rc * q8_0_row_stride(nb8);
-    const uint16_t* dr = reinterpret_cast<const uint16_t*>(rowp);
-    const uint4* qrow = reinterpret_cast<const uint4*>(rowp + (size_t)q8_0_dpad(nb8) * 2);
-    for (int bq = 0; bq < nq; ++bq) {
-      const uint4 qv = qrow[bq * 8 + l];
-      const uint32_t ww[4] = {qv.x, qv.y, qv.z, qv.w};
+    acc = q80_row_sum(acc);
+  } else if constexpr (TYPE == T_Q8_0) {
+    // batches of eight 4-block groups (32 blocks): all loads of a batch in flight together
+    for (int q0 = 0; q0 < nq; q0 += 8) {
+      if (q0 > 0) q80_batch(q0);
 #pragma unroll
-      for (int bb = 0; bb < 4; ++bb) {
-        const int b = bq * 4 + bb;
-        if (b < nb8) {
-          const float dsc = q8_0_scale(dr[b]);
-          const float* xb = P.x + 32 * b + l;
-          const uint32_t q = ww[bb];
-          const float p0 = (float)(int8_t)(q & 0xff) * xb[0];
-          const float p1 = (float)(int8_t)((q >> 8) & 0xff) * xb[8];
-          const float p2 = (float)(int8_t)((q >> 16) & 0xff) * xb[16];
-          const float p3 = (float)(int8_t)(q >> 24) * xb[24];
-          acc = acc + ((p0 + p1) + (p2 + p3)) * dsc;
+      for (int bq = 0; bq < 8; ++bq) {
+        const uint4 dd4 = dv[bq >> 1];
+        const uint32_t dlo = (bq & 1) ? dd4.z : dd4.x;
+        const uint32_t dhi = (bq & 1) ? dd4.w : dd4.y;
+        const uint32_t dd[4] = {dlo & 0xffffu, dlo >> 16, dhi & 0xffffu, dhi >> 16};
+        const uint32_t ww[4] = {qv[bq].x, qv[bq].y, qv[bq].z, qv[bq].w};
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+          const int blk = (q0 + bq) * 4 + bb;
+          if (blk < nb) {
+            const float dsc = q8_0_scale(dd[bb]);
+            const float4 xv = xs[blk * 8 + l];
+            const uint32_t q = ww[bb];
+            const float p0 = (float)(int8_t)(q & 0xff) * xv.x;
+            const float p1 = (float)(int8_t)((q >> 8) & 0xff) * xv.y;
+            const float p2 = (float)(int8_t)((q >> 16) & 0xff) * xv.z;
+            const float p3 = (float)(int8_t)(q >> 24) * xv.w;
+            acc = acc + ((p0 + p1) + (p2 + p3)) * dsc;
+          }
         }
       }
     }
-    acc = dot_lane_sum(acc);
+    acc = q80_row_sum(acc);
   } else {  // T_Q5_0
-    const int nb8 = P.cols / 32;
-    const uint8_t* rowp = P.w.q + (size_t)rc * nb8 * 24;
     const int base = lane & ~7;
-    for (int b0 = 0; b0 < nb8; b0 += 8) {
-      const int b = min(b0 + l, nb8 - 1);
-      Q50Item it;
-      it.qs = reinterpret_cast<const uint4*>(rowp)[b];
-      it.hd = reinterpret_cast<const uint2*>(rowp + (size_t)nb8 * 16)[b];
-      const float term = q50_term(it, P.x + 32 * b);
+    for (int b0 = 0; b0 < nb; b0 += 8) {
+      const int b = min(b0 + l, nb - 1);
+      if (b0 > 0) q50_block(b);
+      const uint4 qs = qs5;
+      const uint2 hd = hd5;
+      float4 xv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xv[j] = xs[b * 8 + j];  // x[32b + j + 8i] in component i
+      const uint32_t qw[4] = {qs.x, qs.y, qs.z, qs.w};
+      float sum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t byte = (qw[e >> 2] >> (8 * (e & 3))) & 0xffu;
+        const int q0 = (int)((byte & 15u) | (((hd.x >> e) & 1u) << 4)) - 16;
+        const int q1 = (int)((byte >> 4) | (((hd.x >> (e + 16)) & 1u) << 4)) - 16;
+        sum = sum + (float)q0 * f4c(xv[e & 7], e >> 3);
+        sum = sum + (float)q1 * f4c(xv[e & 7], (e >> 3) + 2);
+      }
+      const float term = fp16_tensor(hd.y & 0xffffu) * sum;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const float tk = __shfl(term, base + k);
-        if (b0 + k < nb8) acc = acc + tk;
+        if (b0 + k < nb) acc = acc + tk;
       }
     }
   }

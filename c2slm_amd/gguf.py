@@ -302,6 +302,7 @@ class ModelShape:
     t_up: int = Q4_K
     t_down: int = Q6_K
     t_embd: int = Q8_0
+    t_out: Optional[int] = None  # an untied output.weight of this type (None: tied to token_embd)
 
     @property
     def head_dim(self) -> int:
@@ -353,6 +354,8 @@ def write_synthetic_model(path: str, shape: ModelShape = QWEN05B, seed: int = 20
 
     quant("token_embd.weight", shape.t_embd, V, E)
     f32("output_norm.weight", np.ones(E, np.float32))
+    if shape.t_out is not None:
+        quant("output.weight", shape.t_out, V, E)
     for i in range(L):
         f32(f"blk.{i}.attn_norm.weight", np.ones(E, np.float32))
         quant(f"blk.{i}.attn_q.weight", shape.t_q, E, E)

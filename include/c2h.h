@@ -96,7 +96,10 @@ const char* c2h_last_error(const c2h_ctx* ctx);
  * `bytes` must cover rows*stride.  Types: Q4_K/Q6_K/Q5_0/Q8_0 projections
  * (Q4_K/Q6_K multiply a Q8_K row, Q5_0/Q8_0 the f32 input, as
  * engine/model.go:250-270 dispatches; Q8_0 projections up to 1024 columns),
- * Q8_0 embedding/output, F32 norms and biases. */
+ * Q8_0 embedding, Q8_0/Q4_K/Q6_K/Q5_0 output (the vocab projection:
+ * Q8_0 through the fused projection + penalty + argmax kernel, the others
+ * as ParallelGEMV computes them, engine/pool.go:122-154), F32 norms and
+ * biases. */
 int c2h_upload_tensor(c2h_ctx* ctx, int32_t layer, int32_t role, int32_t ggml_type, int64_t rows, int64_t cols,
                       const void* host, size_t bytes);
 
@@ -216,7 +219,9 @@ int c2h_gemv_f32_dev(c2h_ctx* ctx, int32_t ggml_type, const void* w_packed, cons
 
 /* engine.ComputeLogits(m, a, normX, out, targetTokens) with a target list
  * (engine/forward.go:171-212) on the current normX: for each id of ids in
- * [0, n_vocab), logits_out[id] = DotQ8_0(row id of the output matrix, normX);
+ * [0, n_vocab), logits_out[id] = DotQ*(row id of the output matrix, normX)
+ * (computeSingleTokenLogit: the float-x dot of the output's format, also
+ * for K-quants, whose full projection uses the Q8_K row instead);
  * out-of-range ids are skipped and every other entry of logits_out (n_vocab
  * floats) is left as it was.  n_ids == 0 projects the whole vocabulary like
  * c2h_logits (the reference's empty-list branch). */
@@ -236,6 +241,18 @@ int c2h_logits_ids_dev(c2h_ctx* ctx, const int32_t* ids, int32_t n_ids, float* l
  * pos and the non-current normX buffer.  With in_step == 0 the launches run
  * back to back. */
 int c2h_time_vocab(c2h_ctx* ctx, int32_t iters, int32_t pos, int32_t in_step, float* ms_per_launch);
+
+/* Measurement aid with no counterpart in the reference: average device time
+ * (ms) of `iters` launches of the float-x row dots behind c2h_gemv_f32 and
+ * c2h_logits_ids, each bracketed by HIP events on the context stream.  Host
+ * inputs (w in the native layout, x of cols floats, ids nullable) are
+ * uploaded first; without ids rows 0..n-1 are computed, with ids the n
+ * listed rows.  With flush_bytes > 0 a device copy of flush_bytes bytes runs
+ * before each launch (not timed), so the matrix comes from HBM rather than
+ * the last-level cache.  y_out (nullable) receives the n results. */
+int c2h_time_dot_rows(c2h_ctx* ctx, int32_t ggml_type, const void* w, const float* x, int32_t rows, int32_t cols,
+                      const int32_t* ids, int32_t n, int32_t iters, int64_t flush_bytes, float* y_out,
+                      float* ms_per_launch);
 
 /* Measurement aid with no counterpart in the reference: `reps` plain
  * device-to-device copies of `bytes` (a multiple of 16) between two scratch

@@ -40,6 +40,9 @@ CASES = [
     (H.Q5_0, 896, 896),
     (H.Q5_0, 41, 4864),
     (H.Q5_0, 3, 96),
+    (H.Q4_K, 9, 16384),
+    (H.Q6_K, 5, 32768),    # the largest row the kernels stage
+    (H.Q8_0, 3, 32768),
 ]
 
 
@@ -52,6 +55,11 @@ def test_gemv_f32_bitexact(ctx, typ, rows, cols):
     got = ctx.gemv_f32(typ, w, x, rows, cols)
     want = O.gemv(w, typ, rows, cols, x=x, float_x=True)
     assert np.array_equal(bits(got), bits(want))
+
+
+def test_gemv_f32_rejects_rows_beyond_the_lds_limit(ctx):
+    with pytest.raises(H.C2hError):
+        ctx.gemv_f32(H.Q8_0, np.zeros(3 * 1026 * 34, np.uint8), np.zeros(32832, np.float32), 3, 32832)
 
 
 def test_gemv_f32_zero_fallbacks(ctx):
@@ -107,3 +115,16 @@ def test_gemv_f32_unit_vectors_vs_reference_c_oracle(ctx):
             # x = e_i: the dot is the i-th dequantised weight
             got = np.array([ctx.gemv_f32(typ, blk, eye[i], 1, 256)[0] for i in range(256)], np.float32)
             assert np.array_equal(got, want.astype(np.float32)), name
+
+
+def test_time_dot_rows_matches_plain_calls(ctx):
+    rng = np.random.default_rng(8)
+    rows, cols = 300, 896
+    w = G.synth_q8_0(rng, rows * 28)
+    x = rng.normal(size=cols).astype(np.float32)
+    want = ctx.gemv_f32(H.Q8_0, w, x, rows, cols)
+    ms, y = ctx.time_dot_rows(H.Q8_0, w, x, rows, cols, iters=3, flush_bytes=1 << 20)
+    assert ms > 0 and np.array_equal(bits(y), bits(want))
+    ids = np.array([7, 0, 299, 7, 150], np.int32)
+    ms, y = ctx.time_dot_rows(H.Q8_0, w, x, rows, cols, ids=ids, iters=2)
+    assert ms > 0 and np.array_equal(bits(y), bits(want[ids]))

@@ -139,3 +139,34 @@ def test_position_bounds_rejected(tiny):
         ctx.forward(1, 512)
     with pytest.raises(H.C2hError):
         ctx.forward(1, -1)
+
+
+@pytest.mark.parametrize("t_out", [G.Q6_K, G.Q4_K, G.Q5_0])
+def test_untied_output_formats(tmp_path, t_out):
+    """An untied output.weight in a K-quant or Q5_0: the full projection as
+    ParallelGEMV computes it (K-quants on the Q8_K row of normX), the penalty
+    and argmax after it, and the restricted logits through the float-x dots
+    (computeSingleTokenLogit), all against the oracle."""
+    path = str(tmp_path / f"out{t_out}.gguf")
+    G.write_synthetic_model(path, G.ModelShape(n_layers=2, n_vocab=4096, t_out=t_out), seed=99)
+    gf, ctx, orc, im_end, eos = open_pair(path, 256)
+    try:
+        nx = orc.forward(3, 0)
+        ctx.forward(3, 0)
+        full = orc.compute_logits(nx)
+        assert np.array_equal(bits(ctx.logits()), bits(full))
+        V = ctx.desc.n_vocab
+        ids = np.array([0, 9, V - 1, 2048, -1], np.int32)
+        got = ctx.logits_ids(ids, np.zeros(V, np.float32))
+        w = np.asarray(gf.tensor_map["output.weight"].data)
+        rb = G.row_bytes(t_out, ctx.desc.n_embd)
+        for t in ids[:4]:
+            want = O.gemv(w[t * rb:(t + 1) * rb], t_out, 1, ctx.desc.n_embd, x=nx, float_x=True)[0]
+            assert bits(got[t]) == bits(want), t
+        prompt = np.array([5, 77, 300, 5, 77], np.int32)
+        a = gpu_generate(ctx, prompt, 20, im_end, eos)
+        b = oracle_generate(orc, prompt, 20, im_end, eos)
+        assert np.array_equal(a, b)
+    finally:
+        ctx.close()
+        orc.close()
