@@ -207,7 +207,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill line")
     ap.add_argument("--no-real-formats", action="store_true", help="skip the real-model format line")
     ap.add_argument("--no-float-dots", action="store_true", help="skip the float-x row-dot timings")
-    ap.add_argument("--only", choices=["prefill", "long", "float-dots"], default=None,
+    ap.add_argument("--only", choices=["prefill", "long", "float-dots", "real-formats"], default=None,
                     help="run just the prefill reps or just the long-context decode (profiler runs); "
                          "prints their JSON object, not the bench line")
     ap.add_argument("--prefill-reps", type=int, default=5)
@@ -236,6 +236,12 @@ def main():
     synth_model(path)
     gf = G.GGUFFile(path)
     _, im_end, eos = G.special_token_ids(gf)
+    if args.only == "real-formats":
+        rdir = tempfile.mkdtemp(prefix="c2slm_bench_")
+        print(json.dumps({"real_formats": real_formats(rdir, im_end, eos)}))
+        os.rmdir(rdir)
+        cleanup()
+        return
     if args.only == "float-dots":
         ctx = H.Ctx(None)
         print(json.dumps({"float_x_dots": float_x_dots(ctx)}))

@@ -537,7 +537,8 @@ void enqueue_attn_long(c2h_ctx* c, const AttnCoreParams& A, int ntok) {
   hipLaunchKernelGGL(k_attn_scores, dim3(c->att_n_blk, D.n_kv_heads, ntok), dim3(256), 0, c->stream, A);
   hipLaunchKernelGGL(k_attn_softmax, dim3(D.n_heads, ntok), dim3(1024),
                      (size_t)attn_softmax_lds_floats(D.max_ctx) * 4, c->stream, A);
-  hipLaunchKernelGGL(k_attn_av, dim3(D.n_heads, ntok), dim3(ATT_AV_THREADS), (size_t)ATT_AV_LDS_FLOATS * 4, c->stream,
+  hipLaunchKernelGGL(k_attn_av, dim3(D.n_kv_heads * ATT_AV_SLICES, ntok), dim3(ATT_AV_THREADS),
+                     (size_t)ATT_AV_LDS_FLOATS * 4, c->stream,
                      A);
 }
 

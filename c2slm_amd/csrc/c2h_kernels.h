@@ -142,8 +142,9 @@ __host__ __device__ inline size_t vq_index(int p, int d) { return ((size_t)(p >>
 //     workgroup per query head does everything with the scores in LDS;
 //   long contexts: k_attn_scores (workgroups over position blocks, one K
 //     row read for all query heads of a group) -> k_attn_softmax (one
-//     workgroup per head, exps in LDS) -> k_attn_av (one workgroup per head:
-//     one wave runs the FMA chains, the others stage V through LDS).
+//     workgroup per head, exps in LDS) -> k_attn_av (one workgroup per KV
+//     head and 16-dim slice: two waves run the FMA chains of all the group's
+//     query heads, the others stage the V slice through LDS).
 constexpr int ATT_CH = 128;   // V positions staged in LDS per pass (chunk 0 prefetched)
 constexpr int ATT_KPF = 256;  // positions whose K row is prefetched (one per thread)
 // k_attn_core instances by the context they prefetch for: up to 128 and up
@@ -156,7 +157,10 @@ __host__ __device__ inline int attn_tier(int T) { return T <= 128 ? ATT_TIER_128
 constexpr int ATT_SPLIT_T = 1024;  // default split length (positions attended)
 constexpr int ATT_SB = 256;        // positions per k_attn_scores workgroup
 constexpr int ATT_AV_CH = 256;     // positions per k_attn_av LDS chunk
-constexpr int ATT_AV_THREADS = 512;  // k_attn_av: one chain wave, seven staging waves
+constexpr int ATT_AV_THREADS = 512;  // k_attn_av: two chain waves, six staging waves
+constexpr int ATT_AV_DSL = 16;       // k_attn_av: dims of a head per workgroup
+constexpr int ATT_AV_SLICES = 64 / ATT_AV_DSL;
+constexpr int ATT_AV_ITEMS = 4;      // 16-byte staging items per staging lane and chunk
 constexpr int ATT_MAX_QPKV = 8;    // query heads per KV head the long form handles
 constexpr int ATT_LONG_MAX_CTX = 36864;  // exps of one head in LDS (k_attn_softmax)
 // grid (n_heads, tokens) for k_attn_core / k_attn_softmax / k_attn_av and
@@ -194,7 +198,7 @@ __host__ __device__ inline int attn_lds_floats(int max_ctx) { return 2 * ATT_CH 
 // Dynamic LDS of k_attn_softmax (exps of up to max_ctx positions) and of
 // k_attn_av (two chunks of V quads and probabilities), in floats.
 __host__ __device__ inline int attn_softmax_lds_floats(int max_ctx) { return (max_ctx + 3) & ~3; }
-constexpr int ATT_AV_LDS_FLOATS = 2 * ATT_AV_CH * (64 + 1);
+constexpr int ATT_AV_LDS_FLOATS = 2 * ATT_AV_CH * ATT_AV_DSL + 2 * ATT_MAX_QPKV * ATT_AV_CH;
 
 // ---- batched prefill (a prompt of up to PF_MAX tokens per pass)
 

@@ -1101,11 +1101,12 @@ __device__ __forceinline__ float fma4(float acc, const float4& p, const f32x4_t&
   return acc;
 }
 
-// the last n % 16 positions, by quads (p readable to round_up(n, 4))
-template <typename PLOAD>
+// the last n % 16 positions, by quads (p readable to round_up(n, 4));
+// quad q of dim d at vq[q * STRIDE + d]
+template <int STRIDE = 64, typename PLOAD>
 __device__ __forceinline__ float av_tail_q(PLOAD pl, const f32x4_t* vq, int i, int n, int d, float acc) {
   for (; i < n; i += 4) {
-    const f32x4_t v = vq[(i >> 2) * 64 + d];
+    const f32x4_t v = vq[(i >> 2) * STRIDE + d];
     const float4 p = pl(i);
     acc = __builtin_fmaf(p.x, v.x, acc);
     if (i + 1 < n) acc = __builtin_fmaf(p.y, v.y, acc);
@@ -1139,6 +1140,58 @@ __device__ __forceinline__ float av_batches(BLOAD load, int nb, float acc) {
     for (int k = 0; k < 4; ++k) acc = fma4(acc, pa[k], va[k]);
   }
   return acc;
+}
+
+// Batches of sixteen with two batches of loads in flight (three register
+// sets), for chains long enough to meet LDS latency on every step.
+template <typename BLOAD>
+__device__ __forceinline__ float av_batches3(BLOAD load, int nb, float acc) {
+  f32x4_t v0[4], v1[4], v2[4];
+  float4 p0[4], p1[4], p2[4];
+  load(0, v0, p0);
+  load(min(1, nb - 1), v1, p1);
+  int b = 0;
+  for (; b + 3 <= nb; b += 3) {  // v0/p0 hold batch b, v1/p1 batch b+1
+    load(min(b + 2, nb - 1), v2, p2);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc = fma4(acc, p0[k], v0[k]);
+    load(min(b + 3, nb - 1), v0, p0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc = fma4(acc, p1[k], v1[k]);
+    load(min(b + 4, nb - 1), v1, p1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc = fma4(acc, p2[k], v2[k]);
+  }
+  if (b < nb) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc = fma4(acc, p0[k], v0[k]);
+  }
+  if (b + 1 < nb) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc = fma4(acc, p1[k], v1[k]);
+  }
+  return acc;
+}
+
+// The chain over n positions of one dim with the quads STRIDE apart.
+template <int STRIDE>
+__device__ __forceinline__ float av_chain_q3(const float* p, const f32x4_t* vq, int n, int d, float acc) {
+  const int nb = n >> 4;
+  const float4* p4 = reinterpret_cast<const float4*>(p);
+  if (nb > 0)
+    acc = av_batches3(
+        [&](int b, f32x4_t(&v)[4], float4(&pp)[4]) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            v[k] = vq[(4 * b + k) * STRIDE + d];
+            pp[k] = p4[4 * b + k];
+          }
+        },
+        nb, acc);
+  return av_tail_q<STRIDE>([&](int i) { return p4[i >> 2]; }, vq, nb * 16, n, d, acc);
 }
 
 __device__ __forceinline__ float av_chain_q(const float* p, const f32x4_t* vq, int n, int d, float acc) {
@@ -1606,90 +1659,117 @@ __global__ void __launch_bounds__(1024) k_attn_softmax(AttnCoreParams P) {
 // global -> registers of set j % 3 -> LDS buffer j & 1 (a plain copy: the
 // cache is quad-major), so three chunks (~190 KB) are in flight while wave
 // 0 chains through the current one.
-template <int PER>
+// The AV chains of long contexts (c2_tensor_attn_gen.go:85-117: per query
+// head and dim, out[d] = fma(p, V[p][d], out[d]) for p = 0..pos in order).
+// A workgroup takes one KV head and a 16-dim slice of it for all the KV
+// head's query heads: two chain waves, lane = (query head j, dim), and six
+// staging waves that bring each 256-position chunk of the V slice (16 KB)
+// and the heads' probabilities into LDS, three chunks of loads in flight.
+// Slicing the dims keeps the V stream per CU at a quarter of a head's rows,
+// so the staging stays ahead of the chains; the V slice is read once for
+// all query heads of the group.
 struct AvStage {
-  f32x4_t r[PER];
-  f32x4_t p;
+  f32x4_t r[ATT_AV_ITEMS];
 };
 
 __global__ void __launch_bounds__(ATT_AV_THREADS) k_attn_av(AttnCoreParams P) {
   constexpr int HD = 64;
-  constexpr int NQ = ATT_AV_CH / 4;             // quads per chunk (= float4 of probabilities)
-  constexpr int NPW = ATT_AV_THREADS / 64 - 1;  // staging waves
-  constexpr int PER = (NQ + NPW - 1) / NPW;     // quads per staging wave
-  static_assert(NQ == 64, "one probability float4 per lane of a staging wave");
+  constexpr int DS = ATT_AV_DSL;                       // dims per slice
+  constexpr int NQ = ATT_AV_CH / 4;                    // quads per chunk
+  constexpr int NV = NQ * DS;                          // V items (16 B) per chunk
+  constexpr int NP = ATT_MAX_QPKV * (ATT_AV_CH / 4);   // probability items per chunk
+  constexpr int NS = ATT_AV_THREADS - 128;             // staging lanes
+  static_assert(ATT_AV_ITEMS * NS >= NV + NP, "staging covers a chunk");
   extern __shared__ __align__(16) unsigned char smem[];
-  f32x4_t* vb = reinterpret_cast<f32x4_t*>(smem);                 // [2][NQ][64] quad-major
-  float* pb = reinterpret_cast<float*>(vb + 2 * NQ * HD);         // [2][ATT_AV_CH]
+  f32x4_t* vb = reinterpret_cast<f32x4_t*>(smem);      // [2][NQ][DS]: quad q of dim dd
+  float* pb = reinterpret_cast<float*>(vb + 2 * NV);   // [2][ATT_MAX_QPKV][ATT_AV_CH]
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int h = blockIdx.x, i = blockIdx.y;
+  const int wave = tid >> 6;
+  const int qpkv = P.n_heads / P.n_kv_heads;
+  const int g = (int)blockIdx.x / ATT_AV_SLICES, sl = (int)blockIdx.x % ATT_AV_SLICES;
+  const int i = blockIdx.y;
   const int ti = P.tok0 + i;
-  const int g = h / (P.n_heads / P.n_kv_heads);
   const int pos = P.state->pos + ti;
   const int T = pos + 1;
-  const float* vcache = P.kv + (((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * (size_t)kv_slot(P.max_ctx) * HD;
-  const float* s = P.sc + ((size_t)i * P.n_heads + h) * P.sc_ld;
+  const f32x4_t* vcache = reinterpret_cast<const f32x4_t*>(
+      P.kv + (((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * (size_t)kv_slot(P.max_ctx) * HD);
+  const float* s0 = P.sc + ((size_t)i * P.n_heads + (size_t)g * qpkv) * P.sc_ld;  // head j at + j*sc_ld
   const int nch = (T + ATT_AV_CH - 1) / ATT_AV_CH;
   const int qlast = pos >> 2;
   const int plast4 = (T - 1) & ~3;  // a float4 starting there stays inside the row
-  const int wp = wave - 1;
-  auto load_set = [&](AvStage<PER>& st, int c) {
+  const int sidx = tid - 128;       // staging lane
+  // item it of a chunk: V (quad it/DS, dim it%DS) for it < NV, then the
+  // probabilities of head (it-NV)/(ATT_AV_CH/4), float4 (it-NV)%(ATT_AV_CH/4)
+  auto load_set = [&](AvStage& st, int c) {
 #pragma unroll
-    for (int k = 0; k < PER; ++k) st.r[k] = vquad_load(vcache, min(c * NQ + min(wp + NPW * k, NQ - 1), qlast));
-    st.p = *reinterpret_cast<const f32x4_t*>(s + min(c * ATT_AV_CH + 4 * lane, plast4));
+    for (int k = 0; k < ATT_AV_ITEMS; ++k) {
+      const int it = sidx + NS * k;
+      if (it < NV) {
+        const int q = min(c * NQ + it / DS, qlast);
+        st.r[k] = vcache[(size_t)q * HD + sl * DS + (it % DS)];
+      } else {
+        const int e = min(it - NV, NP - 1);
+        const int j = min(e / (ATT_AV_CH / 4), qpkv - 1);
+        st.r[k] = *reinterpret_cast<const f32x4_t*>(s0 + (size_t)j * P.sc_ld +
+                                                     min(c * ATT_AV_CH + 4 * (e % (ATT_AV_CH / 4)), plast4));
+      }
+    }
   };
-  auto store_set = [&](const AvStage<PER>& st, int c) {
+  auto store_set = [&](const AvStage& st, int c) {
 #pragma unroll
-    for (int k = 0; k < PER; ++k)
-      if (wp + NPW * k < NQ) vb[((c & 1) * NQ + wp + NPW * k) * HD + lane] = st.r[k];
-    if (wp == 0) reinterpret_cast<f32x4_t*>(pb + (c & 1) * ATT_AV_CH)[lane] = st.p;
+    for (int k = 0; k < ATT_AV_ITEMS; ++k) {
+      const int it = sidx + NS * k;
+      if (it < NV)
+        vb[(c & 1) * NV + it] = st.r[k];
+      else if (it < NV + NP)
+        reinterpret_cast<f32x4_t*>(pb + (c & 1) * ATT_MAX_QPKV * ATT_AV_CH)[it - NV] = st.r[k];
+    }
   };
-  // Wave 0 chains; waves 1.. stage.  The two roles run separate loops with
-  // the same number of barriers, and the staging loop issues its loads
-  // unconditionally (chunk indices clamped), so the compiler's memory
-  // counter waits keep three chunks in flight.
-  float acc = 0.0f;
-  if (wave > 0) {
-    AvStage<PER> s0, s1, s2;
-    load_set(s0, 0);
-    load_set(s1, min(1, nch - 1));
-    load_set(s2, min(2, nch - 1));
-    store_set(s0, 0);
-    load_set(s0, min(3, nch - 1));
+  // Waves 0-1 chain; waves 2.. stage.  The two roles run separate loops with
+  // the same number of barriers (one per chunk, plus the first), and the
+  // staging loop issues its loads unconditionally (chunk indices clamped).
+  if (wave >= 2) {
+    AvStage a, b, d;
+    load_set(a, 0);
+    load_set(b, min(1, nch - 1));
+    load_set(d, min(2, nch - 1));
+    store_set(a, 0);
+    load_set(a, min(3, nch - 1));
     __syncthreads();
-    // iteration c: chunk c+1 from its set ((c+1) % 3) to LDS, then that set
-    // reloads chunk c+4 (LDS buffer (c+1) & 1 is not the one being chained).
-    // Both roles pass nch barriers, one per chunk: whole trips of three
-    // unconditional steps, the remainder after the loop.
+    // iteration c: chunk c+1 from its set to LDS buffer (c+1)&1 (the chains
+    // read buffer c&1), then that set reloads chunk c+4
     int c = 0;
     for (; c + 3 <= nch; c += 3) {
-      store_set(s1, c + 1);
-      load_set(s1, min(c + 4, nch - 1));
+      store_set(b, c + 1);
+      load_set(b, min(c + 4, nch - 1));
       __syncthreads();
-      store_set(s2, c + 2);
-      load_set(s2, min(c + 5, nch - 1));
+      store_set(d, c + 2);
+      load_set(d, min(c + 5, nch - 1));
       __syncthreads();
-      store_set(s0, c + 3);
-      load_set(s0, min(c + 6, nch - 1));
+      store_set(a, c + 3);
+      load_set(a, min(c + 6, nch - 1));
       __syncthreads();
     }
     if (c < nch) {
-      store_set(s1, c + 1);
+      store_set(b, c + 1);
       __syncthreads();
     }
     if (c + 1 < nch) {
-      store_set(s2, c + 2);
+      store_set(d, c + 2);
       __syncthreads();
     }
   } else {
+    const int cl = tid;  // chain lane: query head j, dim dd of the slice
+    const int j = cl / DS, dd = cl % DS;
+    const int jc = min(j, qpkv - 1);
+    float acc = 0.0f;
     __syncthreads();
     for (int c = 0; c < nch; ++c) {
       const int np = min(ATT_AV_CH, T - c * ATT_AV_CH);
-      acc = av_chain_q(pb + (c & 1) * ATT_AV_CH, vb + (c & 1) * NQ * HD, np, lane, acc);
+      acc = av_chain_q3<DS>(pb + ((c & 1) * ATT_MAX_QPKV + jc) * ATT_AV_CH, vb + (c & 1) * NV, np, dd, acc);
       __syncthreads();
     }
-    P.out[(size_t)ti * P.out_ld + h * HD + lane] = acc;
+    if (j < qpkv) P.out[(size_t)ti * P.out_ld + (size_t)(g * qpkv + j) * HD + sl * DS + dd] = acc;
   }
 }
 
