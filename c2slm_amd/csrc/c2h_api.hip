@@ -903,6 +903,10 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
     for (const void* k : cores)
       if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->attn_lds) != hipSuccess)
         return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
+    const void* pff[] = {(const void*)k_pf_gemm_f<MODE_BIAS>, (const void*)k_pf_gemm_f<MODE_RESID>};
+    for (const void* k : pff)
+      if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, PF_F_LDS_MAX) != hipSuccess)
+        return bail(fail(c, C2H_ERR_HIP, "prefill GEMM LDS attribute"));
   }
   if (c->long_attn) {
     if (D.max_ctx > ATT_LONG_MAX_CTX)
@@ -1111,7 +1115,8 @@ void pf_gemm(c2h_ctx* c, int m, int m_pad, int nb, int mode, std::initializer_li
     J.bias = B[i];
   }
   if (F.n_jobs) {
-    const size_t lds = (size_t)(nb8 * GF_XPAD + nb8 * 32) * sizeof(float);
+    // one launch for all float-input jobs: the Q8_0 v rows overlap the Q5_0 q/k rows
+    const size_t lds = (size_t)pf_gemm_f_lds_bytes(n_x);
     auto k = (mode == MODE_RESID) ? k_pf_gemm_f<MODE_RESID> : k_pf_gemm_f<MODE_BIAS>;
     hipLaunchKernelGGL(k, dim3(tiles, (m + PF_FT - 1) / PF_FT), dim3(256), lds, c->stream, F);
   }

@@ -1847,7 +1847,6 @@ __global__ void __launch_bounds__(256) k_pf_gemm_f(PFGemmFParams P) {
   const int nb8 = P.n_x / 32;
   float* xq = reinterpret_cast<float*>(smem);  // [nb8][GF_XPAD]
   float* xp = xq + nb8 * GF_XPAD;              // [nb8][8][4]
-  __shared__ float terms[256];
   int ji = 0;
 #pragma unroll
   for (int j = 1; j < 3; ++j)
@@ -1864,14 +1863,85 @@ __global__ void __launch_bounds__(256) k_pf_gemm_f(PFGemmFParams P) {
   const bool active = q50 ? (b5 < nb8 && row < J.rows) : (row < J.rows);
   const int row_c = min(row, J.rows - 1);
   const int orow = min(row0 + min(tid, R - 1), J.rows - 1);
+  __shared__ float terms[256];
   Q50Item w5;
   Q80Row w8;
   if (q50)
     w5 = load_q50(J.w, nb8, row_c, min(b5, nb8 - 1));
   else
     w8 = load_q80(J.w, nb8, row_c, lane8);
-  const float bias = (MODE == MODE_BIAS && J.bias) ? J.bias[orow] : 0.0f;
   const int t0 = blockIdx.y * PF_FT;
+  if (q50 && nb8 <= PF_Q50_MAXB) {
+    // Q5_0 rows of up to 1,024 columns: the thread's block decoded once to
+    // floats, x of all the workgroup's tokens staged together, every
+    // (token, block) term into LDS, then one thread per (token, row) folds
+    // the row's terms in block order -- two barriers for the 16 tokens.
+    float* xs = reinterpret_cast<float*>(smem);  // [PF_FT][nb8][GF_XPAD]
+    float* tm = xs + PF_FT * nb8 * GF_XPAD;      // [PF_FT][256]
+    const int nt = min(PF_FT, P.m - t0);
+    float qf[32];
+    {
+      const uint32_t qw[4] = {w5.qs.x, w5.qs.y, w5.qs.z, w5.qs.w};
+      const uint32_t qh = w5.hd.x;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t byte = (qw[e >> 2] >> (8 * (e & 3))) & 0xffu;
+        qf[e] = (float)((int)((byte & 15u) | (((qh >> e) & 1u) << 4)) - 16);
+        qf[e + 16] = (float)((int)((byte >> 4) | (((qh >> (e + 16)) & 1u) << 4)) - 16);
+      }
+    }
+    const float dq = fp16_tensor(w5.hd.y & 0xffffu);
+    for (int e = tid; e < nt * nb8 * 32; e += 256) {
+      const int tt = e / (nb8 * 32), r = e - tt * (nb8 * 32);
+      xs[(tt * nb8 + (r >> 5)) * GF_XPAD + (r & 31)] = P.x[(size_t)(t0 + tt) * P.ldx + r];
+    }
+    __syncthreads();
+    if (active) {
+      for (int tt = 0; tt < nt; ++tt) {
+        const float4* xb = reinterpret_cast<const float4*>(xs + (tt * nb8 + b5) * GF_XPAD);
+        float xv[32];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float4 v = xb[k];
+          xv[4 * k] = v.x;
+          xv[4 * k + 1] = v.y;
+          xv[4 * k + 2] = v.z;
+          xv[4 * k + 3] = v.w;
+        }
+        float sum = 0.0f;  // q50_term's order
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          sum = sum + qf[e] * xv[e];
+          sum = sum + qf[e + 16] * xv[e + 16];
+        }
+        tm[tt * 256 + r5 * nb8 + b5] = dq * sum;
+      }
+    }
+    __syncthreads();
+    if (tid < nt * R) {
+      const int tt = tid / R, r = tid - (tid / R) * R;
+      if (row0 + r < J.rows) {
+        const float* tr = tm + tt * 256 + r * nb8;
+        float acc = 0.0f;
+#pragma unroll
+        for (int h = 0; h < PF_Q50_MAXB; h += 16) {  // sixteen terms per LDS round trip
+          float tv[16];
+#pragma unroll
+          for (int b = 0; b < 16; ++b) tv[b] = tr[min(h + b, nb8 - 1)];
+#pragma unroll
+          for (int b = 0; b < 16; ++b)
+            if (h + b < nb8) acc = acc + tv[b];
+        }
+        float* y = J.y + (size_t)(t0 + tt) * J.ldy + row0 + r;
+        if (MODE == MODE_RESID)
+          *y = *y + acc;
+        else
+          *y = J.bias ? acc + J.bias[row0 + r] : acc;
+      }
+    }
+    return;
+  }
+  const float bias = (MODE == MODE_BIAS && J.bias) ? J.bias[orow] : 0.0f;
   for (int tt = 0; tt < PF_FT; ++tt) {
     const int t = t0 + tt;
     if (t >= P.m) break;  // uniform
