@@ -416,11 +416,13 @@ VocabKernel vocab_kernel(int nb8) {
 }
 size_t vocab_lds(int64_t cols) { return (size_t)nq_of((int)cols) * 4 * 32 * sizeof(float); }
 
-// Grid of the vocab kernel for a rows x cols Q8_0 matrix: two workgroups
-// per CU (fewer if the occupancy is lower), at most one per 32-row tile.
-// Measured over 1..18 per CU for the 151,936 x 896 matrix: two per CU
-// keeps the most of the matrix streaming under the arithmetic; more
-// workgroups add per-workgroup set-up and first-tile waits.
+// Grid of the vocab kernel for a rows x cols Q8_0 matrix: up to two
+// workgroups per CU (fewer if the occupancy is lower), at most one per
+// 32-row tile, then trimmed so every workgroup walks the same number of
+// tiles (151,936 x 896: 475 workgroups of 10 tiles rather than 512 of 9 or
+// 10).  Measured over 1..18 per CU and 6..12 tiles per workgroup: two per
+// CU keeps the most of the matrix streaming under the arithmetic, and equal
+// walks remove a last round in which most of the GPU waits.
 int vocab_grid(c2h_ctx* c, int64_t rows, int64_t cols, int* grid) {
   VocabKernel k = vocab_kernel(nb8_of(cols));
   if (!k)
@@ -430,7 +432,13 @@ int vocab_grid(c2h_ctx* c, int64_t rows, int64_t cols, int* grid) {
   HIPCHK(c, hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, 256, vocab_lds(cols)));
   HIPCHK(c, hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, c->device));
   const int64_t tiles = (rows + 31) / 32;
-  *grid = (int)std::max<int64_t>(1, std::min<int64_t>(tiles, (int64_t)std::min(std::max(per_cu, 1), 2) * std::max(n_cu, 1)));
+  const int64_t g0 = std::max<int64_t>(1, std::min<int64_t>(tiles, (int64_t)std::min(std::max(per_cu, 1), 2) * std::max(n_cu, 1)));
+  // as few workgroups as give every one the same number of tiles (up to one
+  // less for the last): no final round with most of the GPU idle
+  int64_t per_wg = (tiles + g0 - 1) / g0;
+  // C2H_VOCAB_TILES_PER_WG overrides the tiles per workgroup (measurement aid)
+  if (const char* e = getenv("C2H_VOCAB_TILES_PER_WG")) per_wg = std::max(1, atoi(e));
+  *grid = (int)((tiles + per_wg - 1) / per_wg);
   return C2H_OK;
 }
 
