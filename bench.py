@@ -207,7 +207,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill line")
     ap.add_argument("--no-real-formats", action="store_true", help="skip the real-model format line")
     ap.add_argument("--no-float-dots", action="store_true", help="skip the float-x row-dot timings")
-    ap.add_argument("--only", choices=["prefill", "long", "float-dots", "real-formats"], default=None,
+    ap.add_argument("--only", choices=["prefill", "long", "float-dots", "real-formats", "vocab"], default=None,
                     help="run just the prefill reps or just the long-context decode (profiler runs); "
                          "prints their JSON object, not the bench line")
     ap.add_argument("--prefill-reps", type=int, default=5)
@@ -263,6 +263,18 @@ def main():
         return
     rng = np.random.default_rng(SEED)
     prompt = rng.integers(0, desc.n_vocab, PROMPT_LEN).astype(np.int32)
+    if args.only == "vocab":  # the roofline kernel alone (profiler runs)
+        ctx.set_token_ids(0, prompt)
+        for p, t in enumerate(prompt):
+            ctx.forward(int(t), p, want_normx=False)
+        ms = ctx.time_vocab(args.vocab_iters, PROMPT_LEN, in_step=2)
+        if args.copy_calib_mib:
+            copy_calibration(ctx, args.copy_calib_mib)
+        print(json.dumps({"vocab_ms_alternating": round(ms, 5),
+                          "achieved_gbs": round(VOCAB_BYTES / (ms * 1e-3) / 1e9, 1)}))
+        ctx.close()
+        cleanup()
+        return
 
     ctx.set_token_ids(0, prompt)
     for p, t in enumerate(prompt):
@@ -283,8 +295,14 @@ def main():
     pipelined_ms = ctx.time_steps(pos, args.pipelined_iters, PENALTY, im_end, eos)
     # In-step timing: a forward pass between launches streams the layer
     # weights, so the vocab rows come from HBM as they do inside a step.
-    vocab_ms = ctx.time_vocab(args.vocab_iters, pos, in_step=True)
-    vocab_b2b_ms = ctx.time_vocab(args.vocab_iters, pos, in_step=False)
+    # Roofline timing: launches back to back alternating between the matrix
+    # and a device copy (twice 145 MB in flight, beyond the 256 MB last-level
+    # cache), so each reads its rows from HBM; one pair of HIP events around
+    # them all.  In-step: a forward pass between launches, each launch
+    # bracketed by its own events (which add its dispatch).
+    vocab_ms = ctx.time_vocab(args.vocab_iters, pos, in_step=2)
+    vocab_step_ms = ctx.time_vocab(args.vocab_iters, pos, in_step=1)
+    vocab_b2b_ms = ctx.time_vocab(args.vocab_iters, pos, in_step=0)
     achieved = VOCAB_BYTES / (vocab_ms * 1e-3) / 1e9
     traffic = vocab_traffic()
     # per-kernel floor of dependent launches in a graph (empty kernels)
@@ -332,6 +350,7 @@ def main():
                      "ms_per_launch": round(vocab_ms, 5)},
         "cpu_baseline": base,
         "extra": {"vocab_ms_back_to_back": round(vocab_b2b_ms, 5),
+                  "vocab_ms_in_step_events": round(vocab_step_ms, 5),
                   "launch_floor_us_per_kernel": round(floor_us, 3),
                   "pipelined_ms_per_step": round(pipelined_ms, 4),
                   "pipelined_tok_s": round(1000.0 / pipelined_ms, 1),

@@ -206,7 +206,7 @@ class Ctx:
     def set_seq(self, n: int):
         self._chk(lib().c2h_set_seq(self.h, n))
 
-    def time_vocab(self, iters: int, pos: int, in_step: bool = True) -> float:
+    def time_vocab(self, iters: int, pos: int, in_step: int = 1) -> float:
         ms = C.c_float()
         self._chk(lib().c2h_time_vocab(self.h, iters, pos, int(in_step), C.byref(ms)))
         return ms.value

@@ -458,7 +458,8 @@ int dot_rows_ready(c2h_ctx* c, int64_t cols);
 // pooled DispatchGEMV (engine/pool.go:122-154: Q4_K / Q6_K on the Q8_K row
 // of normX, Q5_0 on f32 normX) into logits_out (else the context's logits
 // buffer), then k_logits_pick for the penalty and the candidates.
-void enqueue_vocab(c2h_ctx* c, int apply_penalty, float* logits_out, int x_sel, const float* x) {
+void enqueue_vocab(c2h_ctx* c, int apply_penalty, float* logits_out, int x_sel, const float* x,
+                   const uint8_t* q8_rows = nullptr) {
   const Tensor& ow = out_weight(c);
   if (ow.type != C2H_Q8_0) {
     XSel X;
@@ -499,6 +500,7 @@ void enqueue_vocab(c2h_ctx* c, int apply_penalty, float* logits_out, int x_sel, 
   VocabParams V;
   memset(&V, 0, sizeof(V));
   V.w = out_weight(c).ref();
+  if (q8_rows) V.w.q = q8_rows;  // a copy of the packed Q8_0 matrix (measurement)
   V.n_vocab = c->desc.n_vocab;
   V.n_embd = c->desc.n_embd;
   V.x_sel = x_sel;
@@ -1803,6 +1805,37 @@ int c2h_time_vocab(c2h_ctx* c, int32_t iters, int32_t pos, int32_t in_step, floa
   s.nx_out = c->nx_cur ^ 1;
   if ((rc = push_state(c, s))) return rc;
   enqueue_vocab(c, 1, nullptr, 1, nullptr);  // warm-up
+  if (in_step == 2) {
+    // launches back to back, alternating between the matrix and a copy of
+    // it: a working set of twice the matrix, above the last-level cache, so
+    // each launch streams its rows from HBM; one pair of events around all
+    const Tensor& ow = out_weight(c);
+    if (ow.type != C2H_Q8_0) return fail(c, C2H_ERR_UNSUPPORTED, "alternating timing needs the Q8_0 vocab kernel");
+    const size_t bytes = (size_t)ow.rows * q8_0_row_stride(nb8_of(ow.cols));
+    uint8_t* cp = nullptr;
+    HIPCHK(c, hipMalloc(&cp, bytes));
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    rc = C2H_OK;
+    if (hipMemcpyAsync(cp, ow.q, bytes, hipMemcpyDeviceToDevice, c->stream) != hipSuccess ||
+        hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+      rc = fail(c, C2H_ERR_HIP, "vocab copy");
+    if (rc == C2H_OK) {
+      enqueue_vocab(c, 1, nullptr, 1, nullptr, cp);  // warm-up of the copy's launch
+      (void)hipEventRecord(e0, c->stream);
+      for (int i = 0; i < iters; ++i) enqueue_vocab(c, 1, nullptr, 1, nullptr, (i & 1) ? cp : nullptr);
+      (void)hipEventRecord(e1, c->stream);
+      float t = 0;
+      if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&t, e0, e1) != hipSuccess)
+        rc = fail(c, C2H_ERR_HIP, "vocab timing");
+      else
+        *ms = t / iters;
+    }
+    (void)hipStreamSynchronize(c->stream);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipFree(cp);
+    return rc;
+  }
   std::vector<hipEvent_t> ev(2 * (size_t)iters, nullptr);
   for (auto& e : ev) HIPCHK(c, hipEventCreate(&e));
   rc = C2H_OK;

@@ -239,7 +239,10 @@ int c2h_logits_ids_dev(c2h_ctx* ctx, const int32_t* ids, int32_t n_ids, float* l
  * 144 MB matrix is read from HBM as inside a decode step rather than from
  * the 256 MB last-level cache; that forward pass overwrites the KV entry at
  * pos and the non-current normX buffer.  With in_step == 0 the launches run
- * back to back. */
+ * back to back.  With in_step == 2 they run back to back alternating
+ * between the matrix and a device copy of it (twice the matrix in flight,
+ * more than the last-level cache holds, so every launch reads its rows from
+ * HBM), timed by one pair of events around all of them. */
 int c2h_time_vocab(c2h_ctx* ctx, int32_t iters, int32_t pos, int32_t in_step, float* ms_per_launch);
 
 /* Measurement aid with no counterpart in the reference: average device time
