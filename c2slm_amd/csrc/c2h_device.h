@@ -160,10 +160,4 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 
-// 16-byte streaming load (weights are read once per step).
-__device__ __forceinline__ uint4 ld_nt(const uint4* p) {
-  u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-
 }  // namespace c2h

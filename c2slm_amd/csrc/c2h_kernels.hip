@@ -407,9 +407,9 @@ __device__ __forceinline__ ItemW load_item(const WeightRef& W, int type, int nb,
   const int ie = q4 ? 0 : 24 + n;  // in 8-byte units: scales start at byte 192
   const uint16_t* dp = q4 ? reinterpret_cast<const uint16_t*>(base) : (W.d + blk_idx);
   ItemW it;
-  it.a = ld_nt(p + ia);
-  it.b = ld_nt(p + ib);
-  it.c = ld_nt(p + ic);
+  it.a = p[ia];
+  it.b = p[ib];
+  it.c = p[ic];
   it.e = reinterpret_cast<const uint2*>(base)[ie];
   it.d = *dp;
   return it;
@@ -2275,7 +2275,7 @@ __device__ __forceinline__ void vocab_load(VocabTile<NB8>& t, const VocabParams&
   const uint4* dvec = reinterpret_cast<const uint4*>(rowp);
   const uint4* qrow = reinterpret_cast<const uint4*>(rowp + (size_t)DPAD * 2);
 #pragma unroll
-  for (int bq = 0; bq < VocabTile<NB8>::NQ; ++bq) t.q[bq] = ld_nt(qrow + bq * 8 + j);
+  for (int bq = 0; bq < VocabTile<NB8>::NQ; ++bq) t.q[bq] = qrow[bq * 8 + j];
 #pragma unroll
   for (int k = 0; k < VocabTile<NB8>::ND; ++k) t.d[k] = dvec[k];
   if constexpr (VocabTile<NB8>::NT > 0) t.dt[0] = reinterpret_cast<const uint2*>(dvec)[2 * VocabTile<NB8>::ND];
