@@ -157,6 +157,14 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
 }
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte non-temporal load: for the vocab matrix, which is read once per
+// step and would otherwise push the layer weights out of the last-level
+// cache (the layer kernels use plain loads so that cache keeps them).
+__device__ __forceinline__ uint4 ld_nt(const uint4* p) {
+  u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 

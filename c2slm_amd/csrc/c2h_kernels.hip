@@ -2275,7 +2275,7 @@ __device__ __forceinline__ void vocab_load(VocabTile<NB8>& t, const VocabParams&
   const uint4* dvec = reinterpret_cast<const uint4*>(rowp);
   const uint4* qrow = reinterpret_cast<const uint4*>(rowp + (size_t)DPAD * 2);
 #pragma unroll
-  for (int bq = 0; bq < VocabTile<NB8>::NQ; ++bq) t.q[bq] = qrow[bq * 8 + j];
+  for (int bq = 0; bq < VocabTile<NB8>::NQ; ++bq) t.q[bq] = ld_nt(qrow + bq * 8 + j);
 #pragma unroll
   for (int k = 0; k < VocabTile<NB8>::ND; ++k) t.d[k] = dvec[k];
   if constexpr (VocabTile<NB8>::NT > 0) t.dt[0] = reinterpret_cast<const uint2*>(dvec)[2 * VocabTile<NB8>::ND];
