@@ -21,7 +21,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libc2h.so")
 ARCH = os.environ.get("C2H_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["c2h_kernels.hip", "c2h_api.hip", "engine.cpp", "gguf_reader.cpp"]
+SOURCES = ["c2h_kernels.hip", "c2h_api.hip"]
 
 
 def hipcc() -> str:
@@ -41,10 +41,9 @@ def build(verbose: bool = False) -> str:
     for src in SOURCES:
         path = os.path.join(CSRC, src)
         if not os.path.exists(path):
-            continue
+            raise FileNotFoundError(path)
         obj = os.path.join(bdir, src + ".o")
-        lang = [] if src.endswith(".hip") else ["-x", "hip"]
-        cmd = [hipcc(), *flags, *lang, "-c", path, "-o", obj]
+        cmd = [hipcc(), *flags, "-c", path, "-o", obj]
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             sys.stderr.write(res.stdout + res.stderr)

@@ -25,7 +25,9 @@ def test_full_model_greedy_64_steps(full_model_path):
     got = gpu_generate(ctx, prompt, 64, im_end, eos)
     print("first tokens", got[:8])
     want = oracle_generate(orc, prompt, 64, im_end, eos)
-    assert len(got) == len(want) and np.array_equal(got, want)
+    # north star: an identical greedy stream for at least 64 steps (no early EOS on either side)
+    assert len(want) == 64 and len(got) == 64
+    assert np.array_equal(got, want)
     nx = np.ctypeslib.as_array(O.lib().orc_state_normx(orc.state), shape=(896,)).copy()
     assert np.array_equal(bits(ctx.normx()), bits(nx))
     lg = ctx.logits()
@@ -64,6 +66,7 @@ def test_full_model_prefill_512_then_128_steps(full_model_path):
         if t in (im_end, eos):
             break
     want = orc.generate(128, im_end, eos, 1.15)
+    assert len(want) == 128 and len(got) == 128
     assert np.array_equal(np.array(got, np.int32), want)
     ctx.close()
     orc.close()
