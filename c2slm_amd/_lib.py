@@ -15,6 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("C2H_LIB") or os.path.join(HERE, "libc2h.so")
 
 C2H_OK = 0
+NOALLOC_MAX_COLS = 16384  # C2H_NOALLOC_MAX_COLS
 F32, Q5_0, Q8_0, Q4_K, Q6_K = 0, 6, 8, 12, 14
 
 ROLE = dict(TOKEN_EMBD=0, OUTPUT=1, OUTPUT_NORM=2, ATTN_NORM=10, ATTN_Q=11, ATTN_Q_BIAS=12, ATTN_K=13,
@@ -72,6 +73,7 @@ def lib():
             "c2h_get_token_ids": (C.c_int, [VP, I32, I32, VP]),
             "c2h_get_seq": (C.c_int, [VP, C.POINTER(I32)]),
             "c2h_quantize_q8k": (C.c_int, [VP, VP, I32, VP]),
+            "c2h_quantize_q8k_noalloc": (C.c_int, [VP, VP, I32, VP]),
             "c2h_gemv": (C.c_int, [VP, I32, VP, VP, I32, I32, VP, VP]),
             "c2h_packed_size": (C.c_size_t, [I32, I64, I64]),
             "c2h_pack_weights": (C.c_int, [I32, I64, I64, VP, C.c_size_t, VP, C.c_size_t]),
@@ -232,6 +234,13 @@ class Ctx:
         x = np.ascontiguousarray(x, dtype=np.float32)
         out = np.zeros((len(x) // 256) * 292, np.uint8)
         self._chk(lib().c2h_quantize_q8k(self.h, _p(x), len(x), _p(out)))
+        return out
+
+    def quantize_q8k_noalloc(self, x: np.ndarray) -> np.ndarray:
+        """c2h_quantize_q8k through the entry point that allocates nothing."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros((len(x) // 256) * 292, np.uint8)
+        self._chk(lib().c2h_quantize_q8k_noalloc(self.h, _p(x), len(x), _p(out)))
         return out
 
     def gemv(self, ggml_type: int, w: np.ndarray, xq: np.ndarray, rows: int, cols: int, want_isums: bool = False):

@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <initializer_list>
 #include <cstdio>
+#include <mutex>
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -92,16 +93,24 @@ struct c2h_ctx {
     int nbs = 0;
   } pf;
 
-  // kernel-only scratch (c2h_gemv / c2h_quantize_q8k host forms)
-  std::vector<void*> scratch;
-
   // restricted-logits staging (c2h_logits_ids): ids in, compact logits out
   int32_t* ids_dev = nullptr;
   float* ids_y = nullptr;
   int ids_cap = 0;
   bool dot_attr = false;  // k_dot_rows LDS limit raised
   uint8_t* vq8k = nullptr;  // Q8_K row of normX for a K-quant output.weight
+  uint8_t* noalloc = nullptr;  // this device's copy of `scratch` (c2h_quantize_q8k_noalloc)
 };
+
+// Device scratch of c2h_quantize_q8k_noalloc, which calls no allocator:
+// the staged f32 row (C2H_NOALLOC_MAX_COLS floats) followed by the Q8_K
+// blocks the kernel writes (C2H_NOALLOC_MAX_COLS/256 blocks of 292 bytes).
+// Every GPU holds its own copy until the process ends.  In host code the
+// name is a host-side stand-in, never a device address: host code uses
+// only the address hipGetSymbolAddress returned for the device (ctx->noalloc).
+constexpr size_t kNoAllocX = (size_t)C2H_NOALLOC_MAX_COLS * 4;
+constexpr size_t kNoAllocY = (size_t)(C2H_NOALLOC_MAX_COLS / 256) * 292;
+static __device__ __align__(256) uint8_t scratch[kNoAllocX + kNoAllocY];
 
 namespace {
 
@@ -758,6 +767,27 @@ int run_graph(c2h_ctx* c, bool step, int pos) {
 
 thread_local std::string g_create_err;
 
+// `scratch`'s address on each device, looked up once per device (with that
+// device current) by the first c2h_create on it.
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+uint8_t* g_noalloc[kMaxDevices] = {};
+
+int noalloc_setup(c2h_ctx* c) {
+  if (c->device < 0 || c->device >= kMaxDevices)
+    return fail(c, C2H_ERR_UNSUPPORTED, "device %d beyond the %d this build tracks", c->device, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (!g_noalloc[c->device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(c, C2H_ERR_HIP, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+    g_noalloc[c->device] = reinterpret_cast<uint8_t*>(p);
+  }
+  c->noalloc = g_noalloc[c->device];
+  return C2H_OK;
+}
+
 }  // namespace
 
 namespace {
@@ -832,6 +862,7 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   c->state_ring = reinterpret_cast<C2hState*>(pinned);
   c->tok_host = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(pinned) + sizeof(C2hState) * kStateRing);
   int rc;
+  if ((rc = noalloc_setup(c))) return bail(rc);
   if ((rc = dalloc(c, &c->state_dev, sizeof(C2hState)))) return bail(rc);
   if (!desc) {
     C2hState s0;
@@ -950,7 +981,6 @@ void c2h_destroy(c2h_ctx* c) {
   if (c->stream) (void)hipStreamSynchronize(c->stream);
   destroy_graphs(c);
   for (void* p : c->allocs) (void)hipFree(p);
-  for (void* p : c->scratch) (void)hipFree(p);
   if (c->ids_dev) (void)hipFree(c->ids_dev);
   if (c->ids_y) (void)hipFree(c->ids_y);
   if (c->state_ring) (void)hipHostFree(c->state_ring);
@@ -1642,9 +1672,6 @@ int c2h_sync(c2h_ctx* c) {
   if (!c) return C2H_ERR_INVALID;
   HIPCHK(c, hipSetDevice(c->device));
   HIPCHK(c, hipStreamSynchronize(c->stream));
-  // kernel-only scratch from c2h_gemv_dev is released once the stream drained
-  for (void* p : c->scratch) (void)hipFree(p);
-  c->scratch.clear();
   return C2H_OK;
 }
 
@@ -1670,6 +1697,27 @@ int c2h_quantize_q8k(c2h_ctx* c, const float* x, int32_t cols, void* q8k_out) {
   (void)hipFree(dy);
   if (rc == C2H_ERR_HIP) return fail(c, rc, "quantize copy failed");
   return rc;
+}
+
+int c2h_quantize_q8k_noalloc(c2h_ctx* c, const float* x, int32_t cols, void* q8k_out) {
+  if (!c || !x || !q8k_out || cols < 0) return C2H_ERR_INVALID;
+  if (cols > C2H_NOALLOC_MAX_COLS)
+    return fail(c, C2H_ERR_INVALID, "%d columns exceed the no-alloc scratch (%d)", cols, C2H_NOALLOC_MAX_COLS);
+  HIPCHK(c, hipSetDevice(c->device));
+  const int nb = cols / 256;
+  if (nb == 0) return C2H_OK;
+  if (!c->noalloc) return fail(c, C2H_ERR_STATE, "no-alloc scratch not set up");
+  float* dx = reinterpret_cast<float*>(c->noalloc);
+  uint8_t* dy = c->noalloc + kNoAllocX;
+  // the same stream orders this copy after any earlier call's read-back of
+  // the scratch; every byte the kernel writes is rewritten, nothing needs
+  // clearing
+  HIPCHK(c, hipMemcpyAsync(dx, x, (size_t)nb * 256 * 4, hipMemcpyHostToDevice, c->stream));
+  hipLaunchKernelGGL(k_quantize_q8k, dim3((nb + 3) / 4), dim3(256), 0, c->stream, dx, nb, dy);
+  HIPCHK(c, hipGetLastError());
+  HIPCHK(c, hipMemcpyAsync(q8k_out, dy, (size_t)nb * BS_Q8K, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return C2H_OK;
 }
 
 int c2h_gemv(c2h_ctx* c, int32_t type, const void* w, const void* xq, int32_t rows, int32_t cols, float* y,

@@ -176,6 +176,17 @@ int c2h_set_kv(c2h_ctx* ctx, int32_t which, int32_t layer, int32_t kv_head, int3
  * 292 bytes (f32 d | int8 qs[256] | int16 bsums[16]) from host x. */
 int c2h_quantize_q8k(c2h_ctx* ctx, const float* x, int32_t cols, void* q8k_out);
 
+/* No counterpart in the reference: c2h_quantize_q8k for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, results and
+ * errors, but it calls no allocator: x and the Q8_K blocks are staged in a
+ * fixed device scratch, one per GPU, set up by c2h_create.  cols above
+ * C2H_NOALLOC_MAX_COLS returns C2H_ERR_INVALID.  Every context on a GPU
+ * shares that GPU's scratch: calls that overlap on one GPU (several
+ * threads, or contexts on different streams) race. */
+#define C2H_NOALLOC_MAX_COLS 16384 /* 64 super-blocks, the reference's Q8_K scratch (engine/pool.go:59) */
+int c2h_quantize_q8k_noalloc(c2h_ctx* ctx, const float* x, int32_t cols, void* q8k_out);
+
 /* tensor.GEMVQ4_K_Q8_K / GEMVQ6_K_Q8_K / GEMVQ8_0 / GEMVQ5_0
  * (tensor/ops.go:25-203) on host buffers.  w is the reference's native
  * layout (row stride as above); xq is the Q8_K row for Q4_K/Q6_K and the
