@@ -25,11 +25,19 @@
  *   attention          textbook float64 attention, FMA-order known answers
  *   SwiGLU             c2_tensor_swiglu_test.go:34 precision, extremes
  *   penalty/argmax     brute force, ties, NaN at id 0
- * Parity unpinned (needs the Go toolchain, absent here): the last ulp of Go's
- * float64 math.Exp / Pow / Cos / Sin (glibc is used; after the f32 rounding
- * they differ only in rare double-rounding cases), archsimd ConvertToInt32 in
- * SwiGLU (truncation assumed; the reference pins it to 1e-4), and the
- * reference's own end-to-end stream.
+ *   forward / ingest / float64 Qwen2 decoder written from the model's
+ *   logits / generate  mathematics (tests/qwen2_f64.py, tests/test_oracle_model.py):
+ *                      normX, K/V and logits within 1e-3 (seen: 1e-6), the
+ *                      greedy stream wherever decided; planted mistakes are
+ *                      caught (tests/test_oracle_mutants.py)
+ *   f64 exp / pow /    every input whose f32 result two <=1-ulp libraries could
+ *   cos / sin          round differently is listed (tests/golden/f32_stability.json):
+ *                      one exp input of 1.1e9; RoPE entries only from position 2,387
+ * Parity unpinned (needs the Go toolchain, absent here): the f32 results of
+ * Go's math.Exp at t = -14.56709 (0xc16912cd) and of Go's Pow/Cos/Sin at the
+ * listed RoPE entries (positions >= 2,387), archsimd ConvertToInt32 in SwiGLU
+ * (truncation assumed; the reference pins it to 1e-4), and the reference's
+ * own bits of the end-to-end stream beyond these pins.
  */
 #include <math.h>
 #include <stdint.h>
@@ -645,6 +653,10 @@ typedef struct {
   float* kv; /* [2][L][KVH][max_ctx][HD], engine/kvcache.go:31 */
   int32_t* token_ids;
   int32_t seq_len;
+  /* test hook: every Q8_K row dispatch_gemv produces, appended in call
+     order (tests/qwen2_f64.py checks each against its own activation) */
+  uint8_t* trace;
+  long trace_cap, trace_len;
 } orc_state;
 
 static long kv_off(const orc_state* s, int is_v, int layer, int head, int pos) {
@@ -700,7 +712,12 @@ static int n_workers(const orc_state* s) {
  * Q8_K once per call; rows are split over the workers, inline below 256
  * rows.  The split does not change any row's arithmetic. */
 static void dispatch_gemv(orc_state* s, float* y, const uint8_t* w, int type, const float* x, int rows, int cols) {
-  if (type == T_Q4_K || type == T_Q6_K) orc_quantize_row_q8k(x, s->q8k, cols, (16384 / 256) * BS_Q8K);
+  if (type == T_Q4_K || type == T_Q6_K) {
+    orc_quantize_row_q8k(x, s->q8k, cols, (16384 / 256) * BS_Q8K);
+    long nbytes = (long)(cols / QK_K) * BS_Q8K;
+    if (s->trace && s->trace_len + nbytes <= s->trace_cap) memcpy(s->trace + s->trace_len, s->q8k, (size_t)nbytes);
+    s->trace_len += nbytes;
+  }
   int nw = (rows < 256) ? 1 : n_workers(s);
   const uint8_t* q8k = s->q8k;
   long rb;
@@ -847,3 +864,7 @@ float* orc_state_kv(orc_state* s) { return s->kv; }
 int32_t* orc_state_token_ids(orc_state* s) { return s->token_ids; }
 int32_t orc_state_seq_len(orc_state* s) { return s->seq_len; }
 void orc_state_set_seq_len(orc_state* s, int32_t n) { s->seq_len = n; }
+/* test hook: record the Q8_K rows into buf (cap bytes); the length counts
+   every byte produced since the last call, so len > cap means truncation */
+void orc_state_trace(orc_state* s, uint8_t* buf, long cap) { s->trace = buf; s->trace_cap = cap; s->trace_len = 0; }
+long orc_state_trace_len(orc_state* s) { return s->trace_len; }

@@ -38,15 +38,16 @@ def build():
     subprocess.run(["make", "-C", HERE, "-s"], check=True)
 
 
-_lib = None
+_libs: dict = {}
 
 
-def lib():
-    global _lib
-    if _lib is None:
-        if not os.path.exists(LIB_PATH):
+def lib(path: str | None = None):
+    """The oracle library (another build of the same source with `path`)."""
+    path = path or LIB_PATH
+    if path not in _libs:
+        if path == LIB_PATH and not os.path.exists(LIB_PATH):
             build()
-        L = C.CDLL(LIB_PATH)
+        L = C.CDLL(path)
         sig = {
             "orc_fp16_simd": (C.c_float, [C.c_uint16]),
             "orc_fp16_tensor": (C.c_float, [C.c_uint16]),
@@ -82,13 +83,15 @@ def lib():
             "orc_state_token_ids": (I32P, [C.c_void_p]),
             "orc_state_seq_len": (C.c_int32, [C.c_void_p]),
             "orc_state_set_seq_len": (None, [C.c_void_p, C.c_int32]),
+            "orc_state_trace": (None, [C.c_void_p, U8P, C.c_long]),
+            "orc_state_trace_len": (C.c_long, [C.c_void_p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
-        _lib = L
-    return _lib
+        _libs[path] = L
+    return _libs[path]
 
 
 def ptr(a: np.ndarray, typ):
@@ -150,8 +153,9 @@ class OracleEngine:
     """The reference's Engine state (model + KV cache + arena) over a GGUF file,
     computed by the oracle on the host CPU."""
 
-    def __init__(self, gf, max_ctx: int = 1024, n_threads: int = 1):
+    def __init__(self, gf, max_ctx: int = 1024, n_threads: int = 1, lib_path: str | None = None):
         from c2slm_amd import gguf as G
+        self._L = lib(lib_path)
         self.gf = gf
         md = gf
         def u32(k2, k3, dflt):
@@ -212,13 +216,13 @@ class OracleEngine:
         self.model = m
         self.n_embd, self.n_vocab, self.max_ctx = E, V, max_ctx
         self.n_layers, self.n_kv_heads, self.head_dim = L, KVH, E // H
-        self.state = lib().orc_state_new(C.byref(m))
+        self.state = self._L.orc_state_new(C.byref(m))
         if not self.state:
             raise MemoryError("oracle state allocation failed")
 
     def close(self):
         if self.state:
-            lib().orc_state_free(self.state)
+            self._L.orc_state_free(self.state)
             self.state = None
 
     def __del__(self):
@@ -226,11 +230,11 @@ class OracleEngine:
 
     def forward(self, token: int, pos: int) -> np.ndarray:
         out = np.empty(self.n_embd, dtype=np.float32)
-        lib().orc_forward(self.state, token, pos, ptr(out, F32P))
+        self._L.orc_forward(self.state, token, pos, ptr(out, F32P))
         return out
 
     def compute_logits(self, normx: np.ndarray | None = None) -> np.ndarray:
-        L = lib()
+        L = self._L
         nx = np.ctypeslib.as_array(L.orc_state_normx(self.state), shape=(self.n_embd,)).copy() \
             if normx is None else np.ascontiguousarray(normx, dtype=np.float32)
         out = np.empty(self.n_vocab, dtype=np.float32)
@@ -240,20 +244,20 @@ class OracleEngine:
     def ingest_from(self, pos: int, tokens) -> np.ndarray:
         t = np.ascontiguousarray(tokens, dtype=np.int32)
         out = np.empty(self.n_embd, dtype=np.float32)
-        lib().orc_ingest_from(self.state, pos, ptr(t, I32P), len(t), ptr(out, F32P))
+        self._L.orc_ingest_from(self.state, pos, ptr(t, I32P), len(t), ptr(out, F32P))
         return out
 
     def generate(self, max_new: int, im_end: int, eos: int, penalty: float = 1.15) -> np.ndarray:
         out = np.empty(max_new, dtype=np.int32)
-        n = lib().orc_generate(self.state, max_new, im_end, eos, penalty, ptr(out, I32P))
+        n = self._L.orc_generate(self.state, max_new, im_end, eos, penalty, ptr(out, I32P))
         return out[:n]
 
     @property
     def seq_len(self) -> int:
-        return lib().orc_state_seq_len(self.state)
+        return self._L.orc_state_seq_len(self.state)
 
     def token_ids(self) -> np.ndarray:
-        return np.ctypeslib.as_array(lib().orc_state_token_ids(self.state), shape=(self.max_ctx,)).copy()
+        return np.ctypeslib.as_array(self._L.orc_state_token_ids(self.state), shape=(self.max_ctx,)).copy()
 
     def kv(self) -> np.ndarray:
         return self.kv_view().copy()
@@ -261,12 +265,26 @@ class OracleEngine:
     def kv_view(self) -> np.ndarray:
         """Writable view of the KV cache [2][L][KVH][max_ctx][HD] (for pre-filling)."""
         n = 2 * self.n_layers * self.n_kv_heads * self.max_ctx * self.head_dim
-        a = np.ctypeslib.as_array(lib().orc_state_kv(self.state), shape=(n,))
+        a = np.ctypeslib.as_array(self._L.orc_state_kv(self.state), shape=(n,))
         return a.reshape(2, self.n_layers, self.n_kv_heads, self.max_ctx, self.head_dim)
 
     def set_token_ids(self, pos0: int, ids) -> None:
         ids = np.asarray(ids, np.int32)
-        np.ctypeslib.as_array(lib().orc_state_token_ids(self.state), shape=(self.max_ctx,))[pos0:pos0 + len(ids)] = ids
+        np.ctypeslib.as_array(self._L.orc_state_token_ids(self.state), shape=(self.max_ctx,))[pos0:pos0 + len(ids)] = ids
 
     def set_seq_len(self, n: int) -> None:
-        lib().orc_state_set_seq_len(self.state, n)
+        self._L.orc_state_set_seq_len(self.state, n)
+
+    def start_q8k_trace(self, cap: int = 1 << 24) -> None:
+        """Record every Q8_K row the pooled GEMV quantises from now on."""
+        self._trace = np.zeros(cap, np.uint8)
+        self._L.orc_state_trace(self.state, ptr(self._trace, U8P), cap)
+
+    def take_q8k_trace(self) -> np.ndarray:
+        """The Q8_K bytes recorded since the last start/take, in call order."""
+        n = self._L.orc_state_trace_len(self.state)
+        if n > len(self._trace):
+            raise RuntimeError("Q8_K trace truncated")
+        out = self._trace[:n].copy()
+        self._L.orc_state_trace(self.state, ptr(self._trace, U8P), len(self._trace))
+        return out
