@@ -9,12 +9,17 @@ steps are timed.  A step is the reference's generate-loop body
 (c2slm.go:153-222): vocab projection + repetition penalty 1.15 + argmax,
 then Forward(best, pos); only the chosen id crosses to the host each step.
 
-Prints one JSON line: value = K / wall time of the K steps on one GPU, plus
-the roofline of the dominant kernel (the fused vocab projection) and the CPU
-baseline (the oracle on this host's cores, same workload).  `extra` adds,
-outside the timed region, the batched prefill of a 512-token prompt, decode
-at long contexts (512 / 4096 / 32768 positions of N(0,1) K/V), and decode
-and prefill with the real Q4_K_M file's format mix (Q5_0 / Q8_0 / Q6_K).
+Prints one JSON line: value = K / wall time of the K steps on one GPU; the
+roofline of the kernel with the largest share of the step's time (each
+decode kernel timed in back-to-back launches over the 24 layers' weights);
+and the CPU baseline (the oracle on this host's cores, same workload).
+`extra` adds, outside the timed region: every decode kernel's time, bytes
+and GB/s and the step's bytes and GB/s; the vocab kernel from HBM; the
+operator microbench of the layer shapes (Q4_K/Q6_K x Q8_K GEMV and the Q8_K
+quantiser, hot and with the weights rotated through 1 GiB of copies); the
+batched prefill of a 512-token prompt; decode at long contexts (512 / 4096 /
+32768 positions of N(0,1) K/V); and decode and prefill with the real Q4_K_M
+file's format mix (Q5_0 / Q8_0 / Q6_K).
 """
 from __future__ import annotations
 
@@ -46,35 +51,172 @@ def synth_model(path: str):
     return path
 
 
-def cpu_baseline(gf, prompt, steps, im_end, eos):
-    """The oracle (C restatement of the reference's CPU path) on this host:
-    same prompt ingest, `steps` greedy steps timed."""
-    from oracle import oracle as O
-    threads = min(os.cpu_count() or 1, 16)
-    orc = O.OracleEngine(gf, max_ctx=512, n_threads=threads)
-    orc.ingest_from(0, prompt)
-    t0 = time.perf_counter()
-    toks = orc.generate(steps, -1, -1, PENALTY)  # run exactly `steps` steps
-    dt = time.perf_counter() - t0
-    orc.close()
-    return {"value": round(len(toks) / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"oracle/c2slm_oracle.c (OpenMP, {threads} threads): {PROMPT_LEN}-token prompt ingest "
-                      f"untimed, then {len(toks)} greedy steps timed ({dt:.1f} s)"}
-
-
-def vocab_traffic():
-    """HBM bytes per vocab launch as measured by the rocprofv3 --pmc passes
-    (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration) recorded
-    in profiles/k_vocab_traffic.txt; None when that record is absent."""
-    path = os.path.join(ROOT, "profiles", "k_vocab_traffic.txt")
+def cpu_model() -> str:
     try:
-        with open(path, encoding="utf-8") as f:
+        with open("/proc/cpuinfo", encoding="utf-8") as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch"):
-                    return int(line.split("=", 1)[1].strip())
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
+    return "unknown"
+
+
+def cpu_threads() -> int:
+    """The reference's pool size nw = min(GOMAXPROCS, 32) (engine/pool.go:47-53)
+    over the cores this process may use: its affinity set, or the thread
+    count the host grants it (OMP_NUM_THREADS) when that is smaller."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, min(32, n))
+
+
+def cpu_baseline(gf, prompt, steps, im_end, eos, runs: int = 5, single_steps: int = 16):
+    """The oracle (plain-C restatement of the reference's CPU path; scalar
+    integer dots, not the reference's VPMADDUBSW/VPMADDWD kernels) on this
+    host: after an untimed prompt ingest, `steps` greedy steps timed, the
+    median of `runs` runs with the reference's pool size, plus one run of
+    `single_steps` steps on one thread."""
+    from oracle import oracle as O
+    threads = cpu_threads()
+
+    def rate(nt, n):
+        orc = O.OracleEngine(gf, max_ctx=512, n_threads=nt)
+        orc.ingest_from(0, prompt)
+        t0 = time.perf_counter()
+        toks = orc.generate(n, -1, -1, PENALTY)  # run exactly n steps
+        dt = time.perf_counter() - t0
+        orc.close()
+        return len(toks) / dt, dt
+
+    rs = [rate(threads, steps) for _ in range(runs)]
+    med = float(np.median([r for r, _ in rs]))
+    one, one_dt = rate(1, single_steps)
+    return {"value": round(med, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"oracle/c2slm_oracle.c, plain C with scalar integer dots (OpenMP, {threads} threads = "
+                      f"min(32, cores granted)): {PROMPT_LEN}-token prompt ingest untimed, then {steps} greedy "
+                      f"steps timed, median of {runs} runs ({sum(d for _, d in rs):.1f} s)",
+            "single_thread_tok_s": round(one, 3), "single_thread_sample": f"{single_steps} steps ({one_dt:.1f} s)",
+            "nproc": os.cpu_count(), "cpu_model": cpu_model(), "runs_tok_s": [round(r, 3) for r, _ in rs]}
+
+
+def profiled_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` as measured by the rocprofv3 --pmc
+    passes (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration)
+    recorded in profiles/*_traffic.txt; None when no record names it."""
+    import glob
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_traffic.txt"))):
+        try:
+            with open(path, encoding="utf-8") as f:
+                for line in f:
+                    if not line.startswith("traffic_bytes_per_launch") or "=" not in line:
+                        continue
+                    head, val = line.split("=", 1)
+                    name = head.strip()[len("traffic_bytes_per_launch"):].strip()
+                    if name == f"[{kernel}]" or (not name and kernel == "vocab"):
+                        return int(val.strip())
+        except OSError:
+            pass
     return None
+
+
+def kernel_bytes(gf, desc, T: float) -> dict:
+    """Algorithmic bytes per launch of each decode kernel at T attended
+    positions (the reference's floor semantics: a K-quant row of 896 columns
+    is 3 super-blocks): weights + inputs + outputs + parameters."""
+    from c2slm_amd import gguf as G
+    tm = gf.tensor_map
+    E, F, KVd = desc.n_embd, desc.n_ff, desc.n_kv_heads * desc.head_dim
+
+    def w(name):
+        ti = tm[name]
+        return G.row_bytes(ti.ggml_type, int(ti.dims[0])) * int(ti.dims[1])
+
+    def avg(fn):
+        return sum(fn(i) for i in range(desc.n_layers)) / desc.n_layers
+
+    q = avg(lambda i: w(f"blk.{i}.attn_q.weight") + w(f"blk.{i}.attn_k.weight") + w(f"blk.{i}.attn_v.weight"))
+    o = avg(lambda i: w(f"blk.{i}.attn_output.weight"))
+    gu = avg(lambda i: w(f"blk.{i}.ffn_gate.weight") + w(f"blk.{i}.ffn_up.weight"))
+    dn = avg(lambda i: w(f"blk.{i}.ffn_down.weight"))
+    out = tm.get("output.weight", tm["token_embd.weight"])
+    vocab_w = G.row_bytes(out.ggml_type, int(out.dims[0])) * int(out.dims[1])
+    return {
+        "qkv": int(q + 4 * (E + E + 2 * (E + 2 * KVd))),          # + x, norm w, bias, q|k|v out
+        "attn": int(4 * 2 * KVd * T + 4 * (2 * (E + 2 * KVd) + E)),  # K,V rows + q|k|v in, K/V store, out
+        "attn_out": int(o + 4 * (E + 2 * E)),                      # + attn in, X read and written
+        "ffn_in": int(gu + 4 * (E + E + F)),                       # + x, norm w, h out
+        "ffn_out": int(dn + 4 * (F + 2 * E)),                      # + h in, X read and written
+        "final_norm": int(4 * 3 * E),
+        "vocab": int(vocab_w + 4 * E + 4 * 64 + 4),                # + normX, window ids, chosen id
+    }
+
+
+KERNEL_NAMES = {"qkv": "k_gemv_row<3, PRO_NORM, MODE_BIAS>", "attn": "k_attn_core",
+                "attn_out": "k_gemv_row<3, PRO_QUANT, MODE_RESID>", "ffn_in": "k_gemv_row<3, PRO_NORM, MODE_SWIGLU>",
+                "ffn_out": "k_gemv_row<19, PRO_QUANT, MODE_RESID>", "final_norm": "k_rmsnorm",
+                "vocab": "k_vocab<28>"}
+
+
+def decode_kernels(ctx, gf, desc, vocab_ms, step_ms, T, iters: int = 96):
+    """Each decode kernel's device time per launch (c2h_time_layer_kernel:
+    `iters` launches back to back over the layers' weights, one pair of HIP
+    events; `us` from eager launches -- the form a rocprofv3 trace of this
+    command times -- and `us_graph` from the same launches captured in one
+    graph), its algorithmic bytes and GB/s, and its share of the step."""
+    nbytes = kernel_bytes(gf, desc, T)
+    per_step = {k: desc.n_layers for k in ("qkv", "attn", "attn_out", "ffn_in", "ffn_out")}
+    per_step.update(final_norm=1, vocab=1)
+    out = {}
+    for k in ctx.KERNELS:
+        us = ctx.time_layer_kernel(k, iters) * 1e3
+        usg = ctx.time_layer_kernel(k, iters, captured=True) * 1e3
+        out[k] = {"us": round(us, 3), "us_graph": round(usg, 3)}
+    out["vocab"] = {"us": round(vocab_ms * 1e3, 3)}
+    for k, v in out.items():
+        gbs = nbytes[k] / (v["us"] * 1e-6) / 1e9
+        v.update(bytes=nbytes[k], gb_s=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4),
+                 launches_per_step=per_step[k],
+                 share_of_step=round(v["us"] * per_step[k] / (step_ms * 1e3), 4), kernel=KERNEL_NAMES[k])
+    return out
+
+
+def layer_microbench(ctx, iters: int = 200, rotate_mib: int = 1024):
+    """The operator GEMVs at every layer shape (tensor/ops_test.go:143-171's
+    benchmark shapes; BASELINE distributions) and the Q8_K quantiser, hot
+    (one copy, from the caches) and cold (rotating over 1 GiB of copies, from
+    HBM).  Bytes as the reference reads them: W + Q8_K row + y; the
+    quantiser reads x and writes its Q8_K blocks."""
+    from c2slm_amd import _lib as H
+    from c2slm_amd import gguf as G
+    rng = np.random.default_rng(SEED + 5)
+    out = {}
+    shapes = [("q4k_896x896", H.Q4_K, 896, 896), ("q4k_128x896", H.Q4_K, 128, 896),
+              ("q4k_4864x896", H.Q4_K, 4864, 896), ("q4k_896x4864", H.Q4_K, 896, 4864),
+              ("q6k_896x4864", H.Q6_K, 896, 4864)]
+    for name, t, rows, cols in shapes:
+        nb = cols // 256
+        w = (G.synth_q4_k if t == H.Q4_K else G.synth_q6_k)(rng, rows * nb)
+        xq = ctx.quantize_q8k(rng.standard_normal(cols).astype(np.float32))
+        nbytes = rows * nb * (144 if t == H.Q4_K else 210) + nb * 292 + rows * 4
+        rec = {"rows": rows, "cols": cols, "bytes": nbytes}
+        for mode, rot in (("hot", 0), ("cold", rotate_mib << 20)):
+            ms = ctx.time_gemv(t, w, xq, rows, cols, iters, rot)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            rec[mode] = {"us": round(ms * 1e3, 3), "gb_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        out[name] = rec
+    for cols in (896, 4864):
+        x = rng.standard_normal(cols).astype(np.float32)
+        nb = cols // 256
+        nbytes = nb * 256 * 4 + nb * 292
+        rec = {"cols": cols, "bytes": nbytes}
+        for mode, rot in (("hot", 0), ("cold", rotate_mib << 20)):
+            ms = ctx.time_quantize_q8k(x, iters, rot)
+            rec[mode] = {"us": round(ms * 1e3, 3), "gb_s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+        out[f"quantize_q8k_{cols}"] = rec
+    return out
 
 
 def copy_calibration(ctx, mib: int, reps: int = 5):
@@ -207,7 +349,11 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill line")
     ap.add_argument("--no-real-formats", action="store_true", help="skip the real-model format line")
     ap.add_argument("--no-float-dots", action="store_true", help="skip the float-x row-dot timings")
-    ap.add_argument("--only", choices=["prefill", "long", "float-dots", "real-formats", "vocab"], default=None,
+    ap.add_argument("--no-microbench", action="store_true", help="skip the layer-shape operator microbench")
+    ap.add_argument("--kernel-iters", type=int, default=96, help="launches in each decode-kernel timing")
+    ap.add_argument("--only", choices=["prefill", "long", "float-dots", "real-formats", "vocab", "microbench",
+                                       "kernels"],
+                    default=None,
                     help="run just the prefill reps or just the long-context decode (profiler runs); "
                          "prints their JSON object, not the bench line")
     ap.add_argument("--prefill-reps", type=int, default=5)
@@ -242,9 +388,12 @@ def main():
         os.rmdir(rdir)
         cleanup()
         return
-    if args.only == "float-dots":
+    if args.only in ("float-dots", "microbench"):
         ctx = H.Ctx(None)
-        print(json.dumps({"float_x_dots": float_x_dots(ctx)}))
+        if args.only == "float-dots":
+            print(json.dumps({"float_x_dots": float_x_dots(ctx)}))
+        else:
+            print(json.dumps({"layer_microbench": layer_microbench(ctx)}))
         ctx.close()
         cleanup()
         return
@@ -263,7 +412,19 @@ def main():
         return
     rng = np.random.default_rng(SEED)
     prompt = rng.integers(0, desc.n_vocab, PROMPT_LEN).astype(np.int32)
-    if args.only == "vocab":  # the roofline kernel alone (profiler runs)
+    if args.only == "kernels":  # the decode kernels alone (profiler runs)
+        ctx.set_token_ids(0, prompt)
+        for p, t in enumerate(prompt):
+            ctx.forward(int(t), p, want_normx=False)
+        out = {k: [round(ctx.time_layer_kernel(k, args.kernel_iters, captured=g) * 1e3, 3) for g in (False, True)]
+               for k in ctx.KERNELS}
+        if args.copy_calib_mib:
+            copy_calibration(ctx, args.copy_calib_mib)
+        print(json.dumps({"decode_kernels_us_eager_graph": out}))
+        ctx.close()
+        cleanup()
+        return
+    if args.only == "vocab":  # the vocab kernel alone (profiler runs)
         ctx.set_token_ids(0, prompt)
         for p, t in enumerate(prompt):
             ctx.forward(int(t), p, want_normx=False)
@@ -291,6 +452,20 @@ def main():
     dt = time.perf_counter() - t0
     ms_per_step = dt * 1000.0 / args.steps
     value = args.steps / dt
+    t_first, t_last = PROMPT_LEN + args.warmup + 1, pos  # positions attended by the timed steps
+    t_avg = 0.5 * (t_first + t_last)
+
+    # the vocab kernel from HBM: launches back to back alternating between the
+    # matrix and a device copy (twice 145 MB in flight, beyond the 256 MB
+    # last-level cache), one pair of HIP events around them all
+    vocab_ms = ctx.time_vocab(args.vocab_iters, pos, in_step=2)
+    # every decode kernel, at the next position (attending pos + 1)
+    kern = decode_kernels(ctx, gf, desc, vocab_ms, ms_per_step, pos + 1, args.kernel_iters)
+    step_bytes = sum(v["bytes"] * v["launches_per_step"] for k, v in kern.items() if k != "attn")
+    step_bytes += desc.n_layers * kernel_bytes(gf, desc, t_avg)["attn"]
+    dom = max(kern, key=lambda k: kern[k]["share_of_step"])
+    dk = kern[dom]
+    achieved = dk["bytes"] / (dk["us"] * 1e-6) / 1e9
 
     pipelined_ms = ctx.time_steps(pos, args.pipelined_iters, PENALTY, im_end, eos)
     # In-step timing: a forward pass between launches streams the layer
@@ -300,11 +475,9 @@ def main():
     # cache), so each reads its rows from HBM; one pair of HIP events around
     # them all.  In-step: a forward pass between launches, each launch
     # bracketed by its own events (which add its dispatch).
-    vocab_ms = ctx.time_vocab(args.vocab_iters, pos, in_step=2)
     vocab_step_ms = ctx.time_vocab(args.vocab_iters, pos, in_step=1)
     vocab_b2b_ms = ctx.time_vocab(args.vocab_iters, pos, in_step=0)
-    achieved = VOCAB_BYTES / (vocab_ms * 1e-3) / 1e9
-    traffic = vocab_traffic()
+    vocab_gbs = VOCAB_BYTES / (vocab_ms * 1e-3) / 1e9
     # per-kernel floor of dependent launches in a graph (empty kernels)
     floor_us = ctx.launch_floor(240, 256, 5)
     if args.copy_calib_mib:
@@ -321,6 +494,7 @@ def main():
             os.rmdir(rdir)
 
     fdots = None if args.no_float_dots else float_x_dots(ctx)
+    micro = None if args.no_microbench else layer_microbench(ctx)
 
     base = None
     if not args.no_cpu_baseline:
@@ -345,11 +519,19 @@ def main():
                                f"repetition penalty {PENALTY}",
                    "batch": 1, "prompt_len": PROMPT_LEN, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "k_vocab (151936x896 Q8_0 + penalty + argmax)",
-                     "ms_per_launch": round(vocab_ms, 5)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(dom),
+                     "kernel": f"{dom}: {dk['kernel']} (largest share of the step: {dk['share_of_step']:.0%})",
+                     "bytes_per_launch": dk["bytes"], "us_per_launch": dk["us"]},
         "cpu_baseline": base,
-        "extra": {"vocab_ms_back_to_back": round(vocab_b2b_ms, 5),
+        "extra": {"step": {"bytes": int(step_bytes), "gb_s": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+                           "hbm_frac": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                           "attended_positions": [t_first, t_last]},
+                  "decode_kernels": kern,
+                  "vocab_from_hbm": {"ms": round(vocab_ms, 5), "gb_s": round(vocab_gbs, 1),
+                                     "hbm_frac": round(vocab_gbs / HBM_PEAK_GBS, 4),
+                                     "traffic": profiled_traffic("vocab")},
+                  "layer_microbench": micro,
+                  "vocab_ms_back_to_back": round(vocab_b2b_ms, 5),
                   "vocab_ms_in_step_events": round(vocab_step_ms, 5),
                   "launch_floor_us_per_kernel": round(floor_us, 3),
                   "pipelined_ms_per_step": round(pipelined_ms, 4),

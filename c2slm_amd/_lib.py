@@ -74,6 +74,9 @@ def lib():
             "c2h_get_seq": (C.c_int, [VP, C.POINTER(I32)]),
             "c2h_quantize_q8k": (C.c_int, [VP, VP, I32, VP]),
             "c2h_quantize_q8k_noalloc": (C.c_int, [VP, VP, I32, VP]),
+            "c2h_time_layer_kernel": (C.c_int, [VP, I32, I32, I32, C.POINTER(C.c_float)]),
+            "c2h_time_gemv": (C.c_int, [VP, I32, VP, VP, I32, I32, I32, I64, C.POINTER(C.c_float)]),
+            "c2h_time_quantize_q8k": (C.c_int, [VP, VP, I32, I32, I64, C.POINTER(C.c_float)]),
             "c2h_gemv": (C.c_int, [VP, I32, VP, VP, I32, I32, VP, VP]),
             "c2h_packed_size": (C.c_size_t, [I32, I64, I64]),
             "c2h_pack_weights": (C.c_int, [I32, I64, I64, VP, C.c_size_t, VP, C.c_size_t]),
@@ -227,6 +230,30 @@ class Ctx:
     def time_steps(self, pos: int, iters: int, penalty: float, im_end: int, eos: int) -> float:
         ms = C.c_float()
         self._chk(lib().c2h_time_steps(self.h, pos, iters, penalty, im_end, eos, C.byref(ms)))
+        return ms.value
+
+    KERNELS = ("qkv", "attn", "attn_out", "ffn_in", "ffn_out", "final_norm")  # C2H_KERNEL_*
+
+    def time_layer_kernel(self, kernel: str, iters: int, captured: bool = False) -> float:
+        """ms per launch of one decoder-layer kernel (c2h_time_layer_kernel):
+        eager launches, or one captured graph."""
+        ms = C.c_float()
+        self._chk(lib().c2h_time_layer_kernel(self.h, self.KERNELS.index(kernel), iters, int(captured), C.byref(ms)))
+        return ms.value
+
+    def time_gemv(self, ggml_type: int, w: np.ndarray, xq: np.ndarray, rows: int, cols: int, iters: int,
+                  rotate_bytes: int = 0) -> float:
+        w = np.ascontiguousarray(w)
+        xq = np.ascontiguousarray(xq)
+        ms = C.c_float()
+        self._chk(lib().c2h_time_gemv(self.h, ggml_type, _p(w), _p(xq), rows, cols, iters, rotate_bytes,
+                                      C.byref(ms)))
+        return ms.value
+
+    def time_quantize_q8k(self, x: np.ndarray, iters: int, rotate_bytes: int = 0) -> float:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        ms = C.c_float()
+        self._chk(lib().c2h_time_quantize_q8k(self.h, _p(x), len(x), iters, rotate_bytes, C.byref(ms)))
         return ms.value
 
     # ---- operators (host buffers)

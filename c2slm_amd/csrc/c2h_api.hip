@@ -619,54 +619,81 @@ void launch_group(c2h_ctx* c, std::initializer_list<ProjJob> jobs, int pro, int 
   }
 }
 
-// The 24-layer body of engine.Forward plus the final RMSNorm; layer 0 embeds
-// either state->token (forward) or the argmax of the vocab partials (step).
-// form selects the attention kernels.
-void enqueue_layers(c2h_ctx* c, bool from_argmax, int form) {
+// The launches of one decoder layer (engine/forward.go:65-131), each on its
+// own so the measurement entry points can time them one by one.
+// q|k|v = W * x(RMSNorm(X)) + bias; layer 0 embeds the token first (pro).
+void enqueue_qkv(c2h_ctx* c, int l, int pro) {
+  Layer& L = c->layers[l];
+  launch_group(c, {{&L.wq, nullptr, c->q, L.bq}, {&L.wk, nullptr, c->k, L.bk}, {&L.wv, nullptr, c->v, L.bv}}, pro,
+               MODE_BIAS, c->X, c->desc.n_embd, L.attn_norm);
+}
+
+// attention: RoPE, KV store, scores, softmax, AV
+void enqueue_attn(c2h_ctx* c, int l, int form) {
   const c2h_model_desc& D = c->desc;
-  const int E = D.n_embd;
-  for (int l = 0; l < D.n_layers; ++l) {
-    Layer& L = c->layers[l];
-    // q|k|v = W * x(RMSNorm(X)) + bias; layer 0 embeds the token first
-    launch_group(c, {{&L.wq, nullptr, c->q, L.bq}, {&L.wk, nullptr, c->k, L.bk}, {&L.wv, nullptr, c->v, L.bv}},
-                 (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM, MODE_BIAS, c->X, E,
-                 L.attn_norm);
-    {  // attention: RoPE, KV store, scores, softmax, AV
-      AttnCoreParams A = attn_params(c, l);
-      A.q = c->q;
-      A.k = c->k;
-      A.v = c->v;
-      A.out = c->attn;
-      A.store_kv = 1;
-      const dim3 grid(D.n_heads / D.n_kv_heads, D.n_kv_heads);
-      if (form == ATT_FORM_LONG)
-        enqueue_attn_long(c, A, 1);
-      else if (form == ATT_FORM_128)
-        hipLaunchKernelGGL(k_attn_core<ATT_TIER_128>, grid, dim3(256), c->attn_lds, c->stream, A);
-      else if (form == ATT_FORM_256)
-        hipLaunchKernelGGL(k_attn_core<ATT_TIER_256>, grid, dim3(256), c->attn_lds, c->stream, A);
-      else
-        hipLaunchKernelGGL(k_attn_core<ATT_TIER_ANY>, grid, dim3(256), c->attn_lds, c->stream, A);
-    }
-    // attn_out: X += Wo * x(attn)
-    launch_group(c, {{&L.wo, nullptr, c->X, nullptr}}, PRO_QUANT, MODE_RESID, c->attn, E, nullptr);
-    // ffn_in: h = SwiGLU(Wg * n, Wu * n), n = x(RMSNorm(X))
-    launch_group(c, {{&L.wg, &L.wu, c->h, nullptr}}, PRO_NORM, MODE_SWIGLU, c->X, E, L.ffn_norm);
-    // ffn_out: X += Wd * x(h)
-    launch_group(c, {{&L.wd, nullptr, c->X, nullptr}}, PRO_QUANT, MODE_RESID, c->h, D.n_ff, nullptr);
-  }
+  AttnCoreParams A = attn_params(c, l);
+  A.q = c->q;
+  A.k = c->k;
+  A.v = c->v;
+  A.out = c->attn;
+  A.store_kv = 1;
+  const dim3 grid(D.n_heads / D.n_kv_heads, D.n_kv_heads);
+  if (form == ATT_FORM_LONG)
+    enqueue_attn_long(c, A, 1);
+  else if (form == ATT_FORM_128)
+    hipLaunchKernelGGL(k_attn_core<ATT_TIER_128>, grid, dim3(256), c->attn_lds, c->stream, A);
+  else if (form == ATT_FORM_256)
+    hipLaunchKernelGGL(k_attn_core<ATT_TIER_256>, grid, dim3(256), c->attn_lds, c->stream, A);
+  else
+    hipLaunchKernelGGL(k_attn_core<ATT_TIER_ANY>, grid, dim3(256), c->attn_lds, c->stream, A);
+}
+
+// attn_out: X += Wo * x(attn)
+void enqueue_attn_out(c2h_ctx* c, int l) {
+  launch_group(c, {{&c->layers[l].wo, nullptr, c->X, nullptr}}, PRO_QUANT, MODE_RESID, c->attn, c->desc.n_embd,
+               nullptr);
+}
+
+// ffn_in: h = SwiGLU(Wg * n, Wu * n), n = x(RMSNorm(X))
+void enqueue_ffn_in(c2h_ctx* c, int l) {
+  Layer& L = c->layers[l];
+  launch_group(c, {{&L.wg, &L.wu, c->h, nullptr}}, PRO_NORM, MODE_SWIGLU, c->X, c->desc.n_embd, L.ffn_norm);
+}
+
+// ffn_out: X += Wd * x(h)
+void enqueue_ffn_out(c2h_ctx* c, int l) {
+  launch_group(c, {{&c->layers[l].wd, nullptr, c->X, nullptr}}, PRO_QUANT, MODE_RESID, c->h, c->desc.n_ff, nullptr);
+}
+
+// the final RMSNorm into the normX buffer the step state names
+void enqueue_final_norm(c2h_ctx* c) {
+  const c2h_model_desc& D = c->desc;
   NormParams N;
   memset(&N, 0, sizeof(N));
   N.x = c->X;
   N.w = c->output_norm;
   N.eps = D.rms_eps;
-  N.n = E;
+  N.n = D.n_embd;
   N.out_sel = 1;
   N.out_buf[0] = c->normx[0];
   N.out_buf[1] = c->normx[1];
   N.state = c->state_dev;
-  N.n_lds = chain_lds_floats(E);
+  N.n_lds = chain_lds_floats(D.n_embd);
   hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), (size_t)N.n_lds * sizeof(float), c->stream, N);
+}
+
+// The 24-layer body of engine.Forward plus the final RMSNorm; layer 0 embeds
+// either state->token (forward) or the argmax of the vocab partials (step).
+// form selects the attention kernels.
+void enqueue_layers(c2h_ctx* c, bool from_argmax, int form) {
+  for (int l = 0; l < c->desc.n_layers; ++l) {
+    enqueue_qkv(c, l, (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM);
+    enqueue_attn(c, l, form);
+    enqueue_attn_out(c, l);
+    enqueue_ffn_in(c, l);
+    enqueue_ffn_out(c, l);
+  }
+  enqueue_final_norm(c);
 }
 
 void enqueue_step(c2h_ctx* c, int form) {
@@ -2008,6 +2035,182 @@ int c2h_time_steps(c2h_ctx* c, int32_t pos, int32_t iters, float penalty, int32_
   HIPCHK(c, hipEventElapsedTime(&t, e0, e1));
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
+  *ms = t / iters;
+  return C2H_OK;
+}
+
+
+int c2h_time_layer_kernel(c2h_ctx* c, int32_t kernel, int32_t iters, int32_t captured, float* ms) {
+  if (!c || !ms || iters <= 0 || iters > 100000 || kernel < 0 || kernel > C2H_KERNEL_FINAL_NORM) return C2H_ERR_INVALID;
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = build_graphs(c);
+  if (rc) return rc;
+  const c2h_model_desc& D = c->desc;
+  const int pos = std::min(c->seq_len, D.max_ctx - 1);
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  c->ring_next = 0;
+  C2hState s;
+  memset(&s, 0, sizeof(s));
+  s.pos = pos;
+  s.penalty = 1.15f;
+  s.im_end = -1;
+  s.eos = -1;
+  s.nx_in = c->nx_cur;
+  s.nx_out = c->nx_cur ^ 1;
+  if ((rc = push_state(c, s))) return rc;
+  const int form = attn_form(c, pos + 1);
+  // the residual kernels update X: it is restored afterwards
+  float* saved = nullptr;
+  HIPCHK(c, hipMalloc(&saved, (size_t)D.n_embd * 4));
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  auto one = [&](int i) {
+    const int l = i % D.n_layers;
+    switch (kernel) {
+      case C2H_KERNEL_QKV: enqueue_qkv(c, l, PRO_NORM); break;
+      case C2H_KERNEL_ATTN: enqueue_attn(c, l, form); break;
+      case C2H_KERNEL_ATTN_OUT: enqueue_attn_out(c, l); break;
+      case C2H_KERNEL_FFN_IN: enqueue_ffn_in(c, l); break;
+      case C2H_KERNEL_FFN_OUT: enqueue_ffn_out(c, l); break;
+      default: enqueue_final_norm(c); break;
+    }
+  };
+  if (hipMemcpyAsync(saved, c->X, (size_t)D.n_embd * 4, hipMemcpyDeviceToDevice, c->stream) != hipSuccess ||
+      hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+    rc = fail(c, C2H_ERR_HIP, "kernel timing set-up failed");
+  float t = 0.0f;
+  hipGraph_t g = nullptr;
+  hipGraphExec_t ge = nullptr;
+  if (!rc) {
+    for (int i = 0; i < D.n_layers; ++i) one(i);  // warm-up: every layer once
+    // captured: the timed launches replay as one graph (as the decode step
+    // does), so the host's launch rate does not pace them; eager when the
+    // context runs without graphs (C2H_NO_GRAPH=1)
+    hipError_t e = hipSuccess;
+    if (captured && c->use_graphs) {
+      e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+      if (e == hipSuccess) {
+        for (int i = 0; i < iters; ++i) one(i);
+        e = hipStreamEndCapture(c->stream, &g);
+      }
+      if (e == hipSuccess) e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+      if (e == hipSuccess) e = hipGraphLaunch(ge, c->stream);  // warm-up replay
+    }
+    if (e == hipSuccess) e = hipEventRecord(e0, c->stream);
+    if (e == hipSuccess) {
+      if (ge)
+        e = hipGraphLaunch(ge, c->stream);
+      else
+        for (int i = 0; i < iters; ++i) one(i);
+    }
+    if (e == hipSuccess) e = hipEventRecord(e1, c->stream);
+    if (e == hipSuccess) e = hipGetLastError();
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipEventElapsedTime(&t, e0, e1);
+    if (e != hipSuccess) rc = fail(c, C2H_ERR_HIP, "kernel timing failed: %s", hipGetErrorString(e));
+  }
+  if (ge) (void)hipGraphExecDestroy(ge);
+  if (g) (void)hipGraphDestroy(g);
+  if (!rc && hipMemcpyAsync(c->X, saved, (size_t)D.n_embd * 4, hipMemcpyDeviceToDevice, c->stream) != hipSuccess)
+    rc = fail(c, C2H_ERR_HIP, "restoring X failed");
+  (void)hipStreamSynchronize(c->stream);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  (void)hipFree(saved);
+  if (rc) return rc;
+  *ms = t / iters;
+  return C2H_OK;
+}
+
+int c2h_time_gemv(c2h_ctx* c, int32_t type, const void* w, const void* xq, int32_t rows, int32_t cols, int32_t iters,
+                  int64_t rotate_bytes, float* ms) {
+  if (!c || !w || !xq || !ms || iters <= 0 || iters > 100000 || rotate_bytes < 0) return C2H_ERR_INVALID;
+  int rc = check_type_shape(c, type, rows, cols);
+  if (rc) return rc;
+  if (type == C2H_Q8_0 && nb8_of(cols) > 32) return fail(c, C2H_ERR_UNSUPPORTED, "Q8_0 rows run up to 1024 columns");
+  HIPCHK(c, hipSetDevice(c->device));
+  const size_t pbytes = c2h_packed_size(type, rows, cols);
+  const int64_t ncopy = std::min<int64_t>(65536, std::max<int64_t>(1, (rotate_bytes + (int64_t)pbytes - 1) / (int64_t)pbytes));
+  std::vector<uint8_t> packed(pbytes);
+  size_t qb, db;
+  packed_parts(type, rows, cols, &qb, &db);
+  pack_host(type, rows, cols, reinterpret_cast<const uint8_t*>(w), packed.data(), packed.data() + qb);
+  const bool fx = (type == C2H_Q8_0 || type == C2H_Q5_0);
+  const size_t xbytes = fx ? (size_t)cols * 4 : (size_t)nb_k(cols) * BS_Q8K;
+  uint8_t *dw = nullptr, *dx = nullptr;
+  float* dy = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (hipMalloc(&dw, pbytes * (size_t)ncopy) != hipSuccess || hipMalloc(&dx, xbytes) != hipSuccess ||
+      hipMalloc(&dy, (size_t)rows * 4) != hipSuccess || hipEventCreate(&e0) != hipSuccess ||
+      hipEventCreate(&e1) != hipSuccess)
+    rc = fail(c, C2H_ERR_HIP, "gemv timing: allocation failed");
+  if (!rc && (stream_copy(c->stream, dw, packed.data(), pbytes, hipMemcpyHostToDevice) != hipSuccess ||
+              stream_copy(c->stream, dx, xq, xbytes, hipMemcpyHostToDevice) != hipSuccess))
+    rc = fail(c, C2H_ERR_HIP, "gemv timing: upload failed");
+  for (int64_t i = 1; !rc && i < ncopy; ++i)
+    if (hipMemcpyAsync(dw + (size_t)i * pbytes, dw, pbytes, hipMemcpyDeviceToDevice, c->stream) != hipSuccess)
+      rc = fail(c, C2H_ERR_HIP, "gemv timing: copies failed");
+  float t = 0.0f;
+  if (!rc) {
+    auto launch = [&](int64_t i) {
+      rc = rc ? rc : c2h_gemv_dev(c, type, dw + (size_t)(i % ncopy) * pbytes, dx, rows, cols, dy, nullptr);
+    };
+    for (int i = 0; i < 20; ++i) launch(ncopy - 1 - i % ncopy);  // warm-up (clocks up, code loaded)
+    (void)hipEventRecord(e0, c->stream);
+    for (int i = 0; i < iters; ++i) launch(i);
+    (void)hipEventRecord(e1, c->stream);
+    if (!rc && (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&t, e0, e1) != hipSuccess))
+      rc = fail(c, C2H_ERR_HIP, "gemv timing failed");
+  }
+  (void)hipStreamSynchronize(c->stream);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  for (void* p : {(void*)dw, (void*)dx, (void*)dy})
+    if (p) (void)hipFree(p);
+  if (rc) return rc;
+  *ms = t / iters;
+  return C2H_OK;
+}
+
+int c2h_time_quantize_q8k(c2h_ctx* c, const float* x, int32_t cols, int32_t iters, int64_t rotate_bytes, float* ms) {
+  if (!c || !x || !ms || cols < 256 || cols > 16384 || iters <= 0 || iters > 100000 || rotate_bytes < 0)
+    return C2H_ERR_INVALID;
+  HIPCHK(c, hipSetDevice(c->device));
+  const int nb = cols / 256;
+  const size_t xbytes = (size_t)nb * 1024;  // 16-byte aligned rows of the f32 input
+  const int64_t ncopy = std::min<int64_t>(65536, std::max<int64_t>(1, (rotate_bytes + (int64_t)xbytes - 1) / (int64_t)xbytes));
+  float* dx = nullptr;
+  uint8_t* dy = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = C2H_OK;
+  if (hipMalloc(&dx, xbytes * (size_t)ncopy) != hipSuccess || hipMalloc(&dy, (size_t)nb * BS_Q8K) != hipSuccess ||
+      hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+    rc = fail(c, C2H_ERR_HIP, "quantise timing: allocation failed");
+  if (!rc && stream_copy(c->stream, dx, x, xbytes, hipMemcpyHostToDevice) != hipSuccess)
+    rc = fail(c, C2H_ERR_HIP, "quantise timing: upload failed");
+  for (int64_t i = 1; !rc && i < ncopy; ++i)
+    if (hipMemcpyAsync(reinterpret_cast<uint8_t*>(dx) + (size_t)i * xbytes, dx, xbytes, hipMemcpyDeviceToDevice,
+                       c->stream) != hipSuccess)
+      rc = fail(c, C2H_ERR_HIP, "quantise timing: copies failed");
+  float t = 0.0f;
+  if (!rc) {
+    auto launch = [&](int64_t i) {
+      const float* xi = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(dx) + (size_t)(i % ncopy) * xbytes);
+      hipLaunchKernelGGL(k_quantize_q8k, dim3((nb + 3) / 4), dim3(256), 0, c->stream, xi, nb, dy);
+    };
+    for (int i = 0; i < 20; ++i) launch(ncopy - 1 - i % ncopy);  // warm-up
+    (void)hipEventRecord(e0, c->stream);
+    for (int i = 0; i < iters; ++i) launch(i);
+    (void)hipEventRecord(e1, c->stream);
+    if (hipGetLastError() != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+        hipEventElapsedTime(&t, e0, e1) != hipSuccess)
+      rc = fail(c, C2H_ERR_HIP, "quantise timing failed");
+  }
+  (void)hipStreamSynchronize(c->stream);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (dx) (void)hipFree(dx);
+  if (dy) (void)hipFree(dy);
+  if (rc) return rc;
   *ms = t / iters;
   return C2H_OK;
 }

@@ -280,6 +280,42 @@ int c2h_copy_bench(c2h_ctx* ctx, int64_t bytes, int32_t reps, float* ms_per_copy
  * floor a chain of decode kernels pays per launch. */
 int c2h_launch_floor(c2h_ctx* ctx, int32_t n, int32_t grid, int32_t reps, float* us_per_kernel);
 
+/* Kernels of one decoder layer, for c2h_time_layer_kernel. */
+#define C2H_KERNEL_QKV 0        /* RMSNorm + Q8_K + q|k|v GEMV + bias */
+#define C2H_KERNEL_ATTN 1       /* RoPE, KV store, scores, softmax, AV */
+#define C2H_KERNEL_ATTN_OUT 2   /* Q8_K(attn) + o GEMV + residual */
+#define C2H_KERNEL_FFN_IN 3     /* RMSNorm + Q8_K + gate|up GEMV + SwiGLU */
+#define C2H_KERNEL_FFN_OUT 4    /* Q8_K(h) + down GEMV + residual */
+#define C2H_KERNEL_FINAL_NORM 5 /* the final RMSNorm */
+
+/* Measurement aid with no counterpart in the reference: average device time
+ * (ms) of one decoder-layer kernel, `iters` launches back to back on the
+ * context stream between one pair of HIP events (captured != 0: as one
+ * captured graph, replayed once untimed first, unless the context runs
+ * without graphs (C2H_NO_GRAPH=1); 0: eager launches), layer
+ * i % n_layers on launch i (so each launch reads another layer's weights,
+ * as inside a step), after one untimed round over the layers.  The q|k|v kernel runs the
+ * later layers' prologue (RMSNorm of X) on every layer.  Inputs are the
+ * context's current buffers, at position SeqLen (clamped to max_ctx-1): the
+ * attention kernel writes the KV entries of that position; X, which the
+ * residual kernels update, is restored afterwards. */
+int c2h_time_layer_kernel(c2h_ctx* ctx, int32_t kernel, int32_t iters, int32_t captured, float* ms_per_launch);
+
+/* Measurement aid with no counterpart in the reference: average device time
+ * (ms) of the operator GEMV behind c2h_gemv_dev (tensor.GEMVQ4_K_Q8_K /
+ * GEMVQ6_K_Q8_K / GEMVQ8_0 / GEMVQ5_0), `iters` launches between one pair of
+ * HIP events.  Host inputs: w in the native layout, xq the Q8_K row (K-quants)
+ * or the f32 vector.  With rotate_bytes > 0 the launches rotate over enough
+ * device copies of w to cover rotate_bytes (more than the 256 MB last-level
+ * cache: each launch reads w from HBM); with 0 they reuse one copy. */
+int c2h_time_gemv(c2h_ctx* ctx, int32_t ggml_type, const void* w, const void* xq, int32_t rows, int32_t cols,
+                  int32_t iters, int64_t rotate_bytes, float* ms_per_launch);
+
+/* The same for the quantiser behind c2h_quantize_q8k_dev on cols (256..16384)
+ * host floats x. */
+int c2h_time_quantize_q8k(c2h_ctx* ctx, const float* x, int32_t cols, int32_t iters, int64_t rotate_bytes,
+                          float* ms_per_launch);
+
 /* Average device time (ms) of `iters` decode steps (graph replays) at
  * positions pos, pos+1, ...; tokens are fed back on the device. */
 int c2h_time_steps(c2h_ctx* ctx, int32_t pos, int32_t iters, float penalty, int32_t im_end, int32_t eos,

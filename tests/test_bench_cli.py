@@ -18,6 +18,29 @@ def test_more_than_one_gpu_is_refused():
 def test_traffic_record_is_read():
     sys.path.insert(0, ROOT)
     import bench
-    t = bench.vocab_traffic()
+    t = bench.profiled_traffic("vocab")
     assert isinstance(t, int)
     assert 1.0 <= t / bench.VOCAB_BYTES < 1.1
+
+
+def test_kernel_bytes_match_the_algorithmic_table():
+    """Per-launch bytes at the bench's shape (reference floor semantics):
+    qkv 539,392; attn_out 397,824; ffn_in 4,229,120; ffn_out 3,601,664;
+    vocab 144,646,916; attention 1,024 per attended position plus its
+    vectors."""
+    sys.path.insert(0, ROOT)
+    import tempfile
+    import bench
+    from c2slm_amd import _lib as H
+    from c2slm_amd import gguf as G
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "m.gguf")
+        G.write_synthetic_model(path, G.ModelShape(n_layers=2, n_vocab=151936), seed=3)
+        gf = G.GGUFFile(path)
+        desc = H.desc_from_gguf(gf, max_ctx=1024)
+        b = bench.kernel_bytes(gf, desc, 100)
+        b0 = bench.kernel_bytes(gf, desc, 0)
+    assert b["qkv"] == 539_392 and b["attn_out"] == 397_824
+    assert b["ffn_in"] == 4_229_120 and b["ffn_out"] == 3_601_664
+    assert b["vocab"] == bench.VOCAB_BYTES
+    assert b["attn"] - b0["attn"] == 1_024 * 100
