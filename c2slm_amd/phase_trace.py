@@ -1,0 +1,194 @@
+"""Per-phase cycle stamps of the decode layer kernels (measurement tool).
+
+`build` writes an instrumented copy of the kernel sources into
+c2slm_amd/_build/phase/ with `s_memtime` stamps at the phase boundaries of
+k_gemv_row (qkv, attn_out, ffn_in, ffn_out) and k_attn_core<ATT_TIER_128>,
+and links it as c2slm_amd/libc2h_phase.so (same C ABI plus
+c2h_phase_read).  Lane 0 of every wave of the first and the last workgroup
+of each launch stores its stamp per phase into a device array; every later
+launch of the same kernel overwrites it, so a read after a run holds the
+last launch's stamps.  The product library is untouched.
+
+`run` (GPU) loads that library (C2H_LIB), runs the decode workload -- a
+synthetic Qwen2.5-0.5B-shaped model, a 32-token prefill, 16 greedy steps --
+and prints the table: per phase, the latest wave's stamp minus wave 0's
+entry stamp, in shader clocks.
+
+    python -m c2slm_amd.phase_trace build      # CPU: hipcc cross-compiles
+    python -m c2slm_amd.phase_trace run        # GPU
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+OUT_LIB = os.path.join(HERE, "libc2h_phase.so")
+N_WAVES, N_SLOTS = 8, 12
+GEMV_KINDS = ["qkv", "attn_out", "ffn_in", "ffn_out"]
+GEMV_PHASES = ["entry", "args", "issued", "x", "norm_end", "quant", "w", "items", "end", "norm_start"]
+ATTN_PHASES = ["entry", "args", "issued", "qkv", "rope", "scores", "softmax", "av", "end"]
+
+_STAMPS = r"""namespace c2h {
+__device__ long long g_phase[5][2][8][12];
+template <int NB, int PRO, int MODE>
+__device__ __forceinline__ int phase_kind() {
+  return (PRO == PRO_NORM && MODE == MODE_BIAS)                 ? 0
+         : (PRO == PRO_QUANT && MODE == MODE_RESID && NB <= 8)  ? 1
+         : (PRO == PRO_NORM && MODE == MODE_SWIGLU)             ? 2
+         : (PRO == PRO_QUANT && MODE == MODE_RESID)             ? 3
+                                                                : -1;
+}
+#define PH_G(k) do { const int kd_ = phase_kind<NB, PRO, MODE>(); \
+  if (kd_ >= 0 && (threadIdx.x & 63) == 0 && blockIdx.y == 0 && (blockIdx.x == 0 || blockIdx.x == gridDim.x - 1)) \
+    g_phase[kd_][blockIdx.x == 0 ? 0 : 1][threadIdx.x >> 6][k] = __builtin_amdgcn_s_memtime(); } while (0)
+#define PH_A(k) do { const bool f_ = blockIdx.x == 0 && blockIdx.y == 0; \
+  const bool l_ = blockIdx.x == gridDim.x - 1 && blockIdx.y == gridDim.y - 1; \
+  if (TIER == ATT_TIER_128 && (threadIdx.x & 63) == 0 && blockIdx.z == 0 && (f_ || l_)) \
+    g_phase[4][f_ ? 0 : 1][threadIdx.x >> 6][k] = __builtin_amdgcn_s_memtime(); } while (0)
+"""
+
+
+def _patch(text: str, start: str, end: str, edits) -> str:
+    i0, i1 = text.index(start), text.index(end)
+    body = text[i0:i1]
+    for old, new in edits:
+        if body.count(old) != 1:
+            raise RuntimeError(f"phase site not found once: {old[:70]!r}")
+        body = body.replace(old, new)
+    body = body.rstrip()
+    if not body.endswith("}"):
+        raise RuntimeError("kernel body does not end in '}'")
+    return text[:i0] + body[:-1] + "  PH_END;\n}\n\n" + text[i1:]
+
+
+def instrument(kernels: str) -> str:
+    s = kernels.replace("namespace c2h {\n", _STAMPS, 1)
+    s = _patch(s, "__global__ void __launch_bounds__(row_threads(NB, PRO)) k_gemv_row(GemvParams P) {",
+               "#define C2H_GEMV_ROW(NB_, PRO_, MODE_)", [
+                   ("  const GemvJob J = launch_job(P);", "  PH_G(0);\n  const GemvJob J = launch_job(P);"),
+                   ("  if ((int)blockIdx.x >= J.n_wg) return;  // uniform: the launch's widest job sets the grid\n",
+                    "  if ((int)blockIdx.x >= J.n_wg) return;  // uniform: the launch's widest job sets the grid\n"
+                    "  PH_G(1);\n"),
+                   ("  issue_fence();\n", "  issue_fence();\n  PH_G(2);\n  asm volatile(\"\" ::\"v\"(xa[0].x));\n"
+                    "  PH_G(3);\n"),
+                   ("    const float inv = rms_inv4(", "    PH_G(9);\n    const float inv = rms_inv4("),
+                   ("    const float4 xn[1] = {norm4(", "    PH_G(4);\n    const float4 xn[1] = {norm4("),
+                   ("  // ---- items\n", "  PH_G(5);\n  asm volatile(\"\" ::\"v\"(w1.a.x), \"v\"(w1.c.w));\n"
+                    "  PH_G(6);\n  // ---- items\n"),
+                   ("  // ---- per-row fold in the reference's order, then the epilogue\n",
+                    "  PH_G(7);\n  // ---- per-row fold in the reference's order, then the epilogue\n"),
+               ]).replace("PH_END;", "PH_G(8);", 1)
+    s = _patch(s, "template <int TIER>\n__global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {",
+               "template __global__ void k_attn_core<ATT_TIER_128>(AttnCoreParams);", [
+                   ("  const int tid = threadIdx.x;\n  // grid", "  PH_A(0);\n  const int tid = threadIdx.x;\n  // grid"),
+                   ('"s"(P.max_ctx), "s"(P.rope_len));\n', '"s"(P.max_ctx), "s"(P.rope_len));\n  PH_A(1);\n'),
+                   ("  issue_fence();\n\n  if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;\n  __syncthreads();\n",
+                    "  issue_fence();\n  PH_A(2);\n\n  if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;\n"
+                    "  __syncthreads();\n  PH_A(3);\n"),
+                   ("  __syncthreads();\n\n  // (a batch of query tokens",
+                    "  __syncthreads();\n  PH_A(4);\n\n  // (a batch of query tokens"),
+                   ("  // softmax, then V chunk 0 from registers into LDS buffer 0\n",
+                    "  PH_A(5);\n  // softmax, then V chunk 0 from registers into LDS buffer 0\n"),
+                   ("    softmax();\n    if (tid < HD && pos > 0) acc = av_chain_q(sc, vbuf, pos, d, acc);\n",
+                    "    softmax();\n    PH_A(6);\n    if (tid < HD && pos > 0) acc = av_chain_q(sc, vbuf, pos, d, acc);\n"
+                    "    PH_A(7);\n"),
+               ]).replace("PH_END;", "PH_A(8);", 1)
+    return s
+
+
+_READER = r"""
+namespace c2h { extern __device__ long long g_phase[5][2][8][12]; }
+extern "C" int c2h_phase_read(long long* out) {
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(c2h::g_phase), sizeof(long long) * 5 * 2 * 8 * 12) == hipSuccess ? 0 : -1;
+}
+"""
+
+
+def build() -> str:
+    from c2slm_amd import build as B
+    bdir = os.path.join(HERE, "_build", "phase")
+    shutil.rmtree(bdir, ignore_errors=True)
+    src = os.path.join(bdir, "k", "csrc")  # the sources include ../../include/c2h.h
+    os.makedirs(src)
+    os.symlink(os.path.abspath(os.path.join(HERE, "..", "include")), os.path.join(bdir, "include"))
+    for f in os.listdir(B.CSRC):
+        if os.path.isfile(os.path.join(B.CSRC, f)):
+            shutil.copy(os.path.join(B.CSRC, f), src)
+    kp = os.path.join(src, "c2h_kernels.hip")
+    with open(kp) as f:
+        text = instrument(f.read())
+    with open(kp, "w") as f:
+        f.write(text)
+    with open(os.path.join(src, "c2h_api.hip"), "a") as f:
+        f.write(_READER)
+    flags = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={B.ARCH}", "-ffp-contract=off", "-fgpu-rdc",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I", os.path.join(HERE, "..", "include")]
+    objs = []
+    for name in B.SOURCES:
+        obj = os.path.join(bdir, name + ".o")
+        res = subprocess.run([B.hipcc(), *flags, "-c", os.path.join(src, name), "-o", obj], capture_output=True,
+                             text=True)
+        if res.returncode:
+            sys.stderr.write(res.stderr[-4000:])
+            raise RuntimeError(f"hipcc failed on the instrumented {name}")
+        objs.append(obj)
+    res = subprocess.run([B.hipcc(), "-shared", "-fPIC", "-fgpu-rdc", "--hip-link", f"--offload-arch={B.ARCH}",
+                          *objs, "-o", OUT_LIB], capture_output=True, text=True)
+    if res.returncode:
+        sys.stderr.write(res.stderr[-4000:])
+        raise RuntimeError("link of the instrumented library failed")
+    return OUT_LIB
+
+
+def run(path: str = "/tmp/c2h_phase_q05.gguf") -> None:
+    if os.environ.get("C2H_LIB") != OUT_LIB:  # the library path is fixed when _lib loads
+        env = dict(os.environ, C2H_LIB=OUT_LIB)
+        sys.exit(subprocess.run([sys.executable, "-u", "-m", "c2slm_amd.phase_trace", "run"], env=env,
+                                cwd=os.path.dirname(HERE)).returncode)
+    import ctypes as C
+
+    import numpy as np
+
+    from c2slm_amd import _lib as H
+    from c2slm_amd import gguf as G
+    if not os.path.exists(path):
+        G.write_synthetic_model(path, G.QWEN05B, seed=20261201)
+    gf = G.GGUFFile(path)
+    ctx = H.Ctx(H.desc_from_gguf(gf, max_ctx=1024))
+    H.load_gguf_into(ctx, gf)
+    prompt = np.random.default_rng(20261201).integers(0, gf.tensor_map["token_embd.weight"].dims[1], 32)
+    ctx.prefill(prompt.astype(np.int32), 0)
+    _, im_end, eos = G.special_token_ids(gf)
+    for p in range(32, 48):
+        ctx.step(p, 1.15, im_end, eos)
+    buf = (C.c_longlong * (5 * 2 * N_WAVES * N_SLOTS))()
+    fn = H.lib().c2h_phase_read
+    fn.argtypes = [C.c_void_p]
+    if fn(buf) != 0:
+        raise RuntimeError("c2h_phase_read failed")
+    a = np.array(buf, dtype=np.int64).reshape(5, 2, N_WAVES, N_SLOTS)
+    print("last launch of each kernel (layer 23 of the 16th step, T = 48); shader clocks from wave 0's entry,"
+          " latest wave")
+    for k, name in enumerate(GEMV_KINDS + ["attn"]):
+        cols = ATTN_PHASES if name == "attn" else GEMV_PHASES
+        print(f"{name:9s} {'wg':5s} " + " ".join(f"{p:>10s}" for p in cols))
+        for wg in range(2):
+            t0 = a[k, wg, 0, 0]
+            vals = []
+            for i in range(len(cols)):
+                v = [int(a[k, wg, w, i] - t0) for w in range(N_WAVES) if a[k, wg, w, i]]
+                vals.append(max(v) if v else -1)
+            print(f"{name:9s} {('first', 'last')[wg]:5s} " + " ".join(f"{v:10d}" for v in vals))
+    ctx.close()
+
+
+if __name__ == "__main__":
+    if len(sys.argv) != 2 or sys.argv[1] not in ("build", "run"):
+        sys.exit("usage: python -m c2slm_amd.phase_trace build|run")
+    if sys.argv[1] == "build":
+        print(build())
+    else:
+        run()
