@@ -20,12 +20,13 @@ F32, Q5_0, Q8_0, Q4_K, Q6_K = 0, 6, 8, 12, 14
 
 ROLE = dict(TOKEN_EMBD=0, OUTPUT=1, OUTPUT_NORM=2, ATTN_NORM=10, ATTN_Q=11, ATTN_Q_BIAS=12, ATTN_K=13,
             ATTN_K_BIAS=14, ATTN_V=15, ATTN_V_BIAS=16, ATTN_OUT=17, FFN_NORM=18, FFN_GATE=19, FFN_UP=20,
-            FFN_DOWN=21)
+            FFN_DOWN=21, ATTN_Q_NORM=22, ATTN_K_NORM=23)
 
 LAYER_TENSORS = {
     "attn_norm.weight": "ATTN_NORM", "attn_q.weight": "ATTN_Q", "attn_q.bias": "ATTN_Q_BIAS",
     "attn_k.weight": "ATTN_K", "attn_k.bias": "ATTN_K_BIAS", "attn_v.weight": "ATTN_V",
     "attn_v.bias": "ATTN_V_BIAS", "attn_output.weight": "ATTN_OUT", "ffn_norm.weight": "FFN_NORM",
+    "attn_q_norm.weight": "ATTN_Q_NORM", "attn_k_norm.weight": "ATTN_K_NORM",
     "ffn_gate.weight": "FFN_GATE", "ffn_up.weight": "FFN_UP", "ffn_down.weight": "FFN_DOWN",
 }
 

@@ -35,6 +35,7 @@ struct Tensor {
 
 struct Layer {
   float *attn_norm = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr, *ffn_norm = nullptr;
+  float *q_norm = nullptr, *k_norm = nullptr;  // Qwen3 per-head QK-norm weights (head_dim each)
   Tensor wq, wk, wv, wo, wg, wu, wd;
 };
 
@@ -328,6 +329,8 @@ GemvKernel gemv_row_kernel(int nb, int pro, int mode) {
       case 4: return k_gemv_row<4, PRO_QUANT, MODE_RESID>;
       case 12: return k_gemv_row<12, PRO_QUANT, MODE_RESID>;
       case 19: return k_gemv_row<19, PRO_QUANT, MODE_RESID>;
+      case 8: return k_gemv_row<8, PRO_QUANT, MODE_RESID>;
+      case 24: return k_gemv_row<24, PRO_QUANT, MODE_RESID>;
       default: return nullptr;
     }
   }
@@ -335,6 +338,7 @@ GemvKernel gemv_row_kernel(int nb, int pro, int mode) {
     switch (nb) {
       case 3: return k_gemv_row<3, PRO_NORM, MODE_SWIGLU>;
       case 4: return k_gemv_row<4, PRO_NORM, MODE_SWIGLU>;
+      case 8: return k_gemv_row<8, PRO_NORM, MODE_SWIGLU>;
       default: return nullptr;
     }
   }
@@ -347,6 +351,11 @@ GemvKernel gemv_row_kernel(int nb, int pro, int mode) {
     if (pro == PRO_NORM) return k_gemv_row<4, PRO_NORM, MODE_BIAS>;
     if (pro == PRO_EMBED_NORM) return k_gemv_row<4, PRO_EMBED_NORM, MODE_BIAS>;
     if (pro == PRO_ARGMAX_EMBED_NORM) return k_gemv_row<4, PRO_ARGMAX_EMBED_NORM, MODE_BIAS>;
+  }
+  if (mode == MODE_BIAS && nb == 8) {
+    if (pro == PRO_NORM) return k_gemv_row<8, PRO_NORM, MODE_BIAS>;
+    if (pro == PRO_EMBED_NORM) return k_gemv_row<8, PRO_EMBED_NORM, MODE_BIAS>;
+    if (pro == PRO_ARGMAX_EMBED_NORM) return k_gemv_row<8, PRO_ARGMAX_EMBED_NORM, MODE_BIAS>;
   }
   return nullptr;
 }
@@ -420,6 +429,7 @@ VocabKernel vocab_kernel(int nb8) {
     case 30: return k_vocab<30>;
     case 31: return k_vocab<31>;
     case 32: return k_vocab<32>;
+    case 64: return k_vocab<64>;
     default: return nullptr;
   }
 }
@@ -435,8 +445,8 @@ size_t vocab_lds(int64_t cols) { return (size_t)nq_of((int)cols) * 4 * 32 * size
 int vocab_grid(c2h_ctx* c, int64_t rows, int64_t cols, int* grid) {
   VocabKernel k = vocab_kernel(nb8_of(cols));
   if (!k)
-    return fail(c, C2H_ERR_UNSUPPORTED, "Q8_0 vocab rows of %lld columns (this build: %d..%d)", (long long)cols,
-                32 * VOCAB_MIN_NB8, 32 * VOCAB_MAX_NB8);
+    return fail(c, C2H_ERR_UNSUPPORTED, "Q8_0 vocab rows of %lld columns (this build: %d..%d and 2048)",
+                (long long)cols, 32 * VOCAB_MIN_NB8, 32 * VOCAB_MAX_NB8);
   int per_cu = 0, n_cu = 0;
   HIPCHK(c, hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, 256, vocab_lds(cols)));
   HIPCHK(c, hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, c->device));
@@ -540,6 +550,9 @@ AttnCoreParams attn_params(c2h_ctx* c, int layer) {
   A.n_kv_heads = D.n_kv_heads;
   A.max_ctx = D.max_ctx;
   A.scale = (float)(1.0 / std::sqrt((double)D.head_dim));
+  A.eps = D.rms_eps;
+  A.q_norm = c->layers[layer].q_norm;
+  A.k_norm = c->layers[layer].k_norm;
   A.state = c->state_dev;
   A.sc = c->att_sc;
   A.bmax = c->att_bmax;
@@ -567,12 +580,14 @@ void enqueue_attn_long(c2h_ctx* c, const AttnCoreParams& A, int ntok) {
 enum : int { ATT_FORM_128 = 0, ATT_FORM_256 = 1, ATT_FORM_CORE = 2, ATT_FORM_LONG = 3, ATT_FORMS = 4 };
 
 int attn_form(const c2h_ctx* c, int T) {
+  if (c->desc.head_dim == 128) return ATT_FORM_128;  // k_attn_h128 serves every T
   if (c->long_attn && T > c->att_split) return ATT_FORM_LONG;
   return T <= 128 ? ATT_FORM_128 : (T <= 256 ? ATT_FORM_256 : ATT_FORM_CORE);
 }
 
 // Whether some decode position of this context runs the form.
 bool form_used(const c2h_ctx* c, int form) {
+  if (c->desc.head_dim == 128) return form == ATT_FORM_128;
   const int tmax = c->long_attn ? c->att_split : c->desc.max_ctx;  // largest T of the core forms
   switch (form) {
     case ATT_FORM_128: return true;
@@ -638,7 +653,9 @@ void enqueue_attn(c2h_ctx* c, int l, int form) {
   A.out = c->attn;
   A.store_kv = 1;
   const dim3 grid(D.n_heads / D.n_kv_heads, D.n_kv_heads);
-  if (form == ATT_FORM_LONG)
+  if (D.head_dim == 128)
+    hipLaunchKernelGGL(k_attn_h128, grid, dim3(256), c->attn_lds, c->stream, A);
+  else if (form == ATT_FORM_LONG)
     enqueue_attn_long(c, A, 1);
   else if (form == ATT_FORM_128)
     hipLaunchKernelGGL(k_attn_core<ATT_TIER_128>, grid, dim3(256), c->attn_lds, c->stream, A);
@@ -665,6 +682,9 @@ void enqueue_ffn_out(c2h_ctx* c, int l) {
   launch_group(c, {{&c->layers[l].wd, nullptr, c->X, nullptr}}, PRO_QUANT, MODE_RESID, c->h, c->desc.n_ff, nullptr);
 }
 
+// k_rmsnorm holds one float4 per thread
+int norm_threads(int n) { return n <= 1024 ? 256 : 512; }
+
 // the final RMSNorm into the normX buffer the step state names
 void enqueue_final_norm(c2h_ctx* c) {
   const c2h_model_desc& D = c->desc;
@@ -679,7 +699,7 @@ void enqueue_final_norm(c2h_ctx* c) {
   N.out_buf[1] = c->normx[1];
   N.state = c->state_dev;
   N.n_lds = chain_lds_floats(D.n_embd);
-  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), (size_t)N.n_lds * sizeof(float), c->stream, N);
+  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(norm_threads(D.n_embd)), (size_t)N.n_lds * sizeof(float), c->stream, N);
 }
 
 // The 24-layer body of engine.Forward plus the final RMSNorm; layer 0 embeds
@@ -713,6 +733,8 @@ int validate_model(c2h_ctx* c) {
   for (int l = 0; l < c->desc.n_layers; ++l) {
     Layer& L = c->layers[l];
     if (!L.attn_norm || !L.ffn_norm) return fail(c, C2H_ERR_STATE, "layer %d norms missing", l);
+    if ((L.q_norm || L.k_norm) && c->desc.head_dim != 128)
+      return fail(c, C2H_ERR_UNSUPPORTED, "layer %d: QK-norm runs with head_dim 128", l);
     const Tensor* ts[] = {&L.wq, &L.wk, &L.wv, &L.wo, &L.wg, &L.wu, &L.wd};
     for (const Tensor* t : ts) {
       if (!t->present()) return fail(c, C2H_ERR_STATE, "layer %d projection missing", l);
@@ -723,6 +745,8 @@ int validate_model(c2h_ctx* c) {
                                             (long long)t->cols, (long long)want_cols);
       if (t->type == C2H_Q8_0 && nb8_of(t->cols) > 32)
         return fail(c, C2H_ERR_UNSUPPORTED, "layer %d: Q8_0 projections run up to 1024 columns", l);
+      if (float_input(t->type) && t != &L.wd && c->desc.n_embd > 1024)
+        return fail(c, C2H_ERR_UNSUPPORTED, "layer %d: Q5_0/Q8_0 projections need n_embd <= 1024", l);
     }
     if (L.wg.cols != L.wu.cols || L.wg.rows != L.wu.rows)
       return fail(c, C2H_ERR_INVALID, "layer %d gate/up shapes differ", l);
@@ -838,14 +862,15 @@ int check_kv_args(c2h_ctx* c, int which, int layer, int kv_head, int pos0, int n
 // whole and are (re)ordered on the host.
 int v_rows_copy(c2h_ctx* c, int layer, int kv_head, int pos0, int n, float* rows, bool to_device) {
   const c2h_model_desc& D = c->desc;
+  const int hd = D.head_dim, qf = 4 * hd;  // floats per quad
   const int q0 = pos0 >> 2, q1 = (pos0 + n + 3) >> 2;
-  std::vector<float> quads((size_t)(q1 - q0) * 256);
-  float* dev = c->kv + kv_slot_offset(D, 1, layer, kv_head) + (size_t)q0 * 256;
+  std::vector<float> quads((size_t)(q1 - q0) * qf);
+  float* dev = c->kv + kv_slot_offset(D, 1, layer, kv_head) + (size_t)q0 * qf;
   HIPCHK(c, stream_copy(c->stream, quads.data(), dev, quads.size() * 4, hipMemcpyDeviceToHost));
   for (int p = pos0; p < pos0 + n; ++p)
-    for (int d = 0; d < 64; ++d) {
-      float& q = quads[vq_index(p, d) - (size_t)q0 * 256];
-      float& r = rows[(size_t)(p - pos0) * 64 + d];
+    for (int d = 0; d < hd; ++d) {
+      float& q = quads[vq_index(p, d, hd) - (size_t)q0 * qf];
+      float& r = rows[(size_t)(p - pos0) * hd + d];
       if (to_device)
         q = r;
       else
@@ -905,17 +930,20 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   if (D.n_layers <= 0 || D.n_embd <= 0 || D.n_heads <= 0 || D.n_kv_heads <= 0 || D.n_ff <= 0 || D.n_vocab <= 0 ||
       D.max_ctx <= 0)
     return bail(fail(c, C2H_ERR_INVALID, "model dimensions must be positive"));
-  if (D.head_dim != 64 || D.n_embd != D.n_heads * D.head_dim || D.n_heads % D.n_kv_heads)
-    return bail(fail(c, C2H_ERR_UNSUPPORTED, "this build runs head_dim 64 with n_embd = n_heads*64"));
+  // engine/model.go:137: head_dim = n_embd / n_heads (64 for Qwen2.5-0.5B,
+  // 128 for Qwen3-1.7B)
+  if ((D.head_dim != 64 && D.head_dim != 128) || D.n_embd != D.n_heads * D.head_dim || D.n_heads % D.n_kv_heads)
+    return bail(fail(c, C2H_ERR_UNSUPPORTED, "this build runs head_dim 64 or 128 with n_embd = n_heads*head_dim"));
   if (D.n_embd < 256 || D.n_ff < 256)
     return bail(fail(c, C2H_ERR_UNSUPPORTED, "K-quant projections need n_embd and n_ff of at least 256"));
-  if (D.n_embd % 32 || D.n_embd > 1024 || D.n_ff % 4 || D.n_ff > 16384)
-    return bail(fail(c, C2H_ERR_UNSUPPORTED, "n_embd must be a multiple of 32 up to 1024, n_ff up to 16384"));
+  if (D.n_embd % 32 || D.n_embd > 2048 || D.n_ff % 4 || D.n_ff > 16384)
+    return bail(fail(c, C2H_ERR_UNSUPPORTED, "n_embd must be a multiple of 32 up to 2048, n_ff up to 16384"));
   if (!gemv_row_kernel(nb_k(D.n_embd), PRO_NORM, MODE_BIAS) || !gemv_row_kernel(nb_k(D.n_embd), PRO_QUANT, MODE_RESID) ||
       !gemv_row_kernel(nb_k(D.n_embd), PRO_NORM, MODE_SWIGLU) ||
       !gemv_row_kernel(nb_k(D.n_ff), PRO_QUANT, MODE_RESID))
     return bail(fail(c, C2H_ERR_UNSUPPORTED,
-                     "no kernel instance for n_embd %d / n_ff %d (built: n_embd/256 in {3,4}, n_ff/256 in {3,4,12,19})",
+                     "no kernel instance for n_embd %d / n_ff %d (built: n_embd/256 in {3,4,8}, n_ff/256 in "
+                     "{3,4,12,19,24})",
                      D.n_embd, D.n_ff));
   c->desc = D;
   c->has_model = true;
@@ -959,39 +987,49 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   // positions (staged V | all scores in LDS, within the 160 KB of a gfx950
   // workgroup, 8 KB kept for static shared data), the long-context kernels
   // beyond.  C2H_ATT_SPLIT overrides the split length (measurement aid).
-  c->att_split = ATT_SPLIT_T;
-  if (const char* sp = getenv("C2H_ATT_SPLIT")) c->att_split = std::max(1, atoi(sp));
-  while (c->att_split > 1 && (size_t)attn_lds_floats(c->att_split) * 4 > 152u * 1024) --c->att_split;
-  c->att_split = std::min(c->att_split, D.max_ctx);
-  c->long_attn = D.max_ctx > c->att_split;
-  c->attn_lds = (size_t)attn_lds_floats(c->att_split) * 4;
-  {
-    const void* cores[] = {(const void*)k_attn_core<ATT_TIER_128>, (const void*)k_attn_core<ATT_TIER_256>,
-                           (const void*)k_attn_core<ATT_TIER_ANY>};
-    for (const void* k : cores)
-      if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->attn_lds) != hipSuccess)
-        return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
-    const void* pff[] = {(const void*)k_pf_gemm_f<MODE_BIAS>, (const void*)k_pf_gemm_f<MODE_RESID>};
-    for (const void* k : pff)
-      if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, PF_F_LDS_MAX) != hipSuccess)
-        return bail(fail(c, C2H_ERR_HIP, "prefill GEMM LDS attribute"));
-  }
-  if (c->long_attn) {
-    if (D.max_ctx > ATT_LONG_MAX_CTX)
-      return bail(fail(c, C2H_ERR_UNSUPPORTED, "max_ctx %d above the %d positions of the exact attention kernels",
-                       D.max_ctx, ATT_LONG_MAX_CTX));
-    if (D.n_heads / D.n_kv_heads > ATT_MAX_QPKV)
-      return bail(fail(c, C2H_ERR_UNSUPPORTED, "more than %d query heads per KV head", ATT_MAX_QPKV));
-    c->att_sc_ld = (D.max_ctx + 3) & ~3;
-    c->att_n_blk = (D.max_ctx + ATT_SB - 1) / ATT_SB;
-    if ((rc = dalloc(c, &c->att_sc, (size_t)PF_ATT_SUB * D.n_heads * c->att_sc_ld * 4)) ||
-        (rc = dalloc(c, &c->att_bmax, (size_t)PF_ATT_SUB * D.n_heads * c->att_n_blk * 4)))
-      return bail(rc);
-    if (hipFuncSetAttribute((const void*)k_attn_softmax, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            attn_softmax_lds_floats(D.max_ctx) * 4) != hipSuccess ||
-        hipFuncSetAttribute((const void*)k_attn_av, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            ATT_AV_LDS_FLOATS * 4) != hipSuccess)
-      return bail(fail(c, C2H_ERR_HIP, "long attention LDS attribute"));
+  if (D.head_dim == 128) {  // k_attn_h128 at every T: the scores of max_ctx positions in LDS
+    c->attn_lds = (size_t)attn_h128_lds_floats(D.max_ctx) * 4;
+    if (c->attn_lds > 152u * 1024)
+      return bail(fail(c, C2H_ERR_UNSUPPORTED, "head_dim 128 runs up to %d positions", 152 * 256 - 64));
+    if (hipFuncSetAttribute((const void*)k_attn_h128, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)c->attn_lds) != hipSuccess)
+      return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
+    c->att_split = D.max_ctx;
+  } else {
+    c->att_split = ATT_SPLIT_T;
+    if (const char* sp = getenv("C2H_ATT_SPLIT")) c->att_split = std::max(1, atoi(sp));
+    while (c->att_split > 1 && (size_t)attn_lds_floats(c->att_split) * 4 > 152u * 1024) --c->att_split;
+    c->att_split = std::min(c->att_split, D.max_ctx);
+    c->long_attn = D.max_ctx > c->att_split;
+    c->attn_lds = (size_t)attn_lds_floats(c->att_split) * 4;
+    {
+      const void* cores[] = {(const void*)k_attn_core<ATT_TIER_128>, (const void*)k_attn_core<ATT_TIER_256>,
+                             (const void*)k_attn_core<ATT_TIER_ANY>};
+      for (const void* k : cores)
+        if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->attn_lds) != hipSuccess)
+          return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
+      const void* pff[] = {(const void*)k_pf_gemm_f<MODE_BIAS>, (const void*)k_pf_gemm_f<MODE_RESID>};
+      for (const void* k : pff)
+        if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, PF_F_LDS_MAX) != hipSuccess)
+          return bail(fail(c, C2H_ERR_HIP, "prefill GEMM LDS attribute"));
+    }
+    if (c->long_attn) {
+      if (D.max_ctx > ATT_LONG_MAX_CTX)
+        return bail(fail(c, C2H_ERR_UNSUPPORTED, "max_ctx %d above the %d positions of the exact attention kernels",
+                         D.max_ctx, ATT_LONG_MAX_CTX));
+      if (D.n_heads / D.n_kv_heads > ATT_MAX_QPKV)
+        return bail(fail(c, C2H_ERR_UNSUPPORTED, "more than %d query heads per KV head", ATT_MAX_QPKV));
+      c->att_sc_ld = (D.max_ctx + 3) & ~3;
+      c->att_n_blk = (D.max_ctx + ATT_SB - 1) / ATT_SB;
+      if ((rc = dalloc(c, &c->att_sc, (size_t)PF_ATT_SUB * D.n_heads * c->att_sc_ld * 4)) ||
+          (rc = dalloc(c, &c->att_bmax, (size_t)PF_ATT_SUB * D.n_heads * c->att_n_blk * 4)))
+        return bail(rc);
+      if (hipFuncSetAttribute((const void*)k_attn_softmax, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              attn_softmax_lds_floats(D.max_ctx) * 4) != hipSuccess ||
+          hipFuncSetAttribute((const void*)k_attn_av, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              ATT_AV_LDS_FLOATS * 4) != hipSuccess)
+        return bail(fail(c, C2H_ERR_HIP, "long attention LDS attribute"));
+    }
   }
   C2hState s0;
   memset(&s0, 0, sizeof(s0));
@@ -1053,6 +1091,8 @@ int c2h_upload_tensor(c2h_ctx* c, int32_t layer, int32_t role, int32_t type, int
     case C2H_ROLE_ATTN_Q_BIAS: return upload_f32(c, &L.bq, E, type, rows, cols, host, bytes);
     case C2H_ROLE_ATTN_K_BIAS: return upload_f32(c, &L.bk, KV, type, rows, cols, host, bytes);
     case C2H_ROLE_ATTN_V_BIAS: return upload_f32(c, &L.bv, KV, type, rows, cols, host, bytes);
+    case C2H_ROLE_ATTN_Q_NORM: return upload_f32(c, &L.q_norm, D.head_dim, type, rows, cols, host, bytes);
+    case C2H_ROLE_ATTN_K_NORM: return upload_f32(c, &L.k_norm, D.head_dim, type, rows, cols, host, bytes);
     case C2H_ROLE_ATTN_Q: if ((rc = want(E, E))) return rc; return upload_quant(c, &L.wq, type, rows, cols, host, bytes);
     case C2H_ROLE_ATTN_K: if ((rc = want(KV, E))) return rc; return upload_quant(c, &L.wk, type, rows, cols, host, bytes);
     case C2H_ROLE_ATTN_V: if ((rc = want(KV, E))) return rc; return upload_quant(c, &L.wv, type, rows, cols, host, bytes);
@@ -1315,7 +1355,7 @@ int pf_pass(c2h_ctx* c, const int32_t* tokens, int m, int pos0) {
   N.n = E;
   N.out = c->normx[c->nx_cur ^ 1];
   N.n_lds = chain_lds_floats(E);
-  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), (size_t)N.n_lds * sizeof(float), c->stream, N);
+  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(norm_threads(E)), (size_t)N.n_lds * sizeof(float), c->stream, N);
   HIPCHK(c, hipGetLastError());
   c->nx_prev = c->nx_cur;
   c->nx_cur ^= 1;
@@ -1332,15 +1372,35 @@ int c2h_prefill(c2h_ctx* c, const int32_t* tokens, int32_t n, int32_t pos0, floa
   if (pos0 < 0 || (int64_t)pos0 + n > c->desc.max_ctx)
     return fail(c, C2H_ERR_RANGE, "positions [%d, %d) outside [0, %d)", pos0, pos0 + n, c->desc.max_ctx);
   if (n == 0) return C2H_OK;
-  if ((rc = pf_alloc(c))) return rc;
-  HIPCHK(c, hipStreamSynchronize(c->stream));
-  c->ring_next = 0;
-  for (int done = 0; done < n;) {
-    const int m = std::min(n - done, PF_MAX);
-    if ((rc = pf_pass(c, tokens + done, m, pos0 + done))) return rc;
-    HIPCHK(c, hipStreamSynchronize(c->stream));  // tokens are copied from the caller's buffer
-    done += m;
-    c->seq_len = pos0 + done;
+  if (c->desc.head_dim != 64) {
+    // no batched prefill kernels at this head_dim: one forward graph per
+    // token, as engine.IngestFrom runs Forward per token (c2slm.go:103-114)
+    if ((rc = build_graphs(c))) return rc;
+    for (int i = 0; i < n; ++i) {
+      C2hState s;
+      memset(&s, 0, sizeof(s));
+      s.pos = pos0 + i;
+      s.token = tokens[i];
+      s.penalty = 1.15f;
+      s.nx_in = c->nx_cur;
+      s.nx_out = c->nx_cur ^ 1;
+      if ((rc = push_state(c, s)) || (rc = run_graph(c, false, pos0 + i))) return rc;
+      c->nx_prev = c->nx_cur;
+      c->nx_cur ^= 1;
+      c->seq_len = pos0 + i + 1;
+    }
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+  } else {
+    if ((rc = pf_alloc(c))) return rc;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    c->ring_next = 0;
+    for (int done = 0; done < n;) {
+      const int m = std::min(n - done, PF_MAX);
+      if ((rc = pf_pass(c, tokens + done, m, pos0 + done))) return rc;
+      HIPCHK(c, hipStreamSynchronize(c->stream));  // tokens are copied from the caller's buffer
+      done += m;
+      c->seq_len = pos0 + done;
+    }
   }
   if (normx_out)
     HIPCHK(c, stream_copy(c->stream, normx_out, c->normx[c->nx_cur], (size_t)c->desc.n_embd * 4,

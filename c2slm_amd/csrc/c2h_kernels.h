@@ -86,7 +86,11 @@ constexpr int MAX_JOBS = 4;
 // super-blocks, quantised by every workgroup) runs on 8 waves: its blocks
 // quantise at most three per wave with two waves per SIMD, and the
 // workgroup takes twice the rows, which halves the redundant quantisations.
-__host__ __device__ constexpr int row_threads(int nb, int pro) { return (pro == PRO_QUANT && nb >= 12) ? 512 : 256; }
+// The norm prologues hold one float4 of x per thread, so rows of more than
+// 1024 values (up to 2048) run on 8 waves as well.
+__host__ __device__ constexpr int row_threads(int nb, int pro) {
+  return ((pro == PRO_QUANT && nb >= 12) || (pro >= PRO_NORM && nb > 4)) ? 512 : 256;
+}
 
 struct GemvParams {
   int prologue;
@@ -128,13 +132,16 @@ struct NormParams {
   C2hState* state;
 };
 
-// KV cache: [K|V][layer][kv head][kv_slot(max_ctx)][64] floats.  K rows are
-// position-major (row p at p*64); V is quad-major within a head slot:
-// element (p, d) at vq_index(p, d), so positions 4q..4q+3 of dim d are 16
-// contiguous bytes and quad q (all dims) is 1 KB.  The attention chains
-// read four positions per 16-byte access and V chunks copy to LDS as is.
+// KV cache: [K|V][layer][kv head][kv_slot(max_ctx)][hd] floats.  K rows are
+// position-major (row p at p*hd); V is quad-major within a head slot:
+// element (p, d) at vq_index(p, d, hd), so positions 4q..4q+3 of dim d are
+// 16 contiguous bytes and quad q (all dims) is 16*hd bytes.  The attention
+// chains read four positions per 16-byte access and V chunks copy to LDS as
+// is.
 __host__ __device__ inline int kv_slot(int max_ctx) { return (max_ctx + 3) & ~3; }
-__host__ __device__ inline size_t vq_index(int p, int d) { return ((size_t)(p >> 2) * 64 + d) * 4 + (p & 3); }
+__host__ __device__ inline size_t vq_index(int p, int d, int hd = 64) {
+  return ((size_t)(p >> 2) * hd + d) * 4 + (p & 3);
+}
 
 // Attention of one layer over the q|k|v the QKV GEMV wrote: RoPE, KV store,
 // scores, softmax, AV.  Two exact forms with the same arithmetic:
@@ -167,9 +174,12 @@ constexpr int ATT_LONG_MAX_CTX = 36864;  // exps of one head in LDS (k_attn_soft
 // (blocks, n_kv_heads, tokens) for k_attn_scores: query token i of a launch
 // sits at position state->pos + tok0 + i; decode launches one token.
 struct AttnCoreParams {
-  const float* q;  // [tokens][q_ld]: n_heads*64, bias added, before RoPE
-  const float* k;  // [tokens][kv_ld]: n_kv_heads*64
+  const float* q;  // [tokens][q_ld]: n_heads*hd, bias added, before QK-norm and RoPE
+  const float* k;  // [tokens][kv_ld]: n_kv_heads*hd
   const float* v;
+  const float* q_norm;  // per-head QK-norm weights (hd floats each), nullptr: none
+  const float* k_norm;
+  float eps;
   float* out;      // attention output [tokens][out_ld]
   int q_ld, kv_ld, out_ld;
   int store_kv;    // 1: K/V of pos come from k/v and are stored by this launch
@@ -192,6 +202,10 @@ struct AttnCoreParams {
   int sc_ld;
   int n_blk;
 };
+
+// Dynamic LDS of k_attn_h128 (head_dim 128), in floats: the scores of every
+// position up to max_ctx.
+__host__ __device__ inline int attn_h128_lds_floats(int max_ctx) { return chain_lds_floats(max_ctx); }
 
 // Dynamic LDS of k_attn_core, in floats: two staged V chunks | scores.
 __host__ __device__ inline int attn_lds_floats(int max_ctx) { return 2 * ATT_CH * 64 + chain_lds_floats(max_ctx); }
@@ -328,6 +342,7 @@ __global__ void k_attn_core(AttnCoreParams P);
 __global__ void k_attn_scores(AttnCoreParams P);
 __global__ void k_attn_softmax(AttnCoreParams P);
 __global__ void k_attn_av(AttnCoreParams P);
+__global__ void k_attn_h128(AttnCoreParams P);
 template <int NB>
 __global__ void k_pf_norm_quant(PFNormParams P);
 template <int NB>
@@ -340,7 +355,7 @@ __global__ void k_pf_rope_store(PFRopeParams P);
 __global__ void k_pf_swiglu(const float* gate, const float* up, float* h, int n, int m);
 template <int NB8>
 __global__ void k_vocab(VocabParams P);
-constexpr int VOCAB_MIN_NB8 = 24, VOCAB_MAX_NB8 = 32;  // instantiated widths (Q8_0 blocks per row)
+constexpr int VOCAB_MIN_NB8 = 24, VOCAB_MAX_NB8 = 32;  // instantiated widths (Q8_0 blocks per row), and 64
 // An f32 input vector: x itself, or (sel) the normX buffer the step state
 // names, for kernels inside replayed graphs.
 struct XSel {

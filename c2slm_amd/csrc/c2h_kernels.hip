@@ -349,16 +349,16 @@ __device__ __forceinline__ float seq_sum_wave_n(const float* a, int n) {
   return chunk_chain(a, min((m + 1) * C, n), n, lane_value(S, m + 1));
 }
 
-// 1/rms of n values (n <= 1024, a multiple of 4) held as elements 4t..4t+3
-// by thread t < n/4, tensor/ops.go:207-218: sequential f32 sum of x*x,
-// inv = f32(1/sqrt(f64(sum/n + eps))).  sq: LDS scratch of
+// 1/rms of n values (n <= 4*blockDim.x, a multiple of 4) held as elements
+// 4t..4t+3 by thread t < n/4, tensor/ops.go:207-218: sequential f32 sum of
+// x*x, inv = f32(1/sqrt(f64(sum/n + eps))).  sq: LDS scratch of
 // chain_lds_floats(n) floats.
 __device__ __forceinline__ float rms_inv4(const float4& x, int n, float eps, float* sq, float* inv_slot) {
   const int tid = threadIdx.x;
   if (4 * tid < n) reinterpret_cast<float4*>(sq)[tid] = make_float4(x.x * x.x, x.y * x.y, x.z * x.z, x.w * x.w);
   __syncthreads();
   if (tid < 64) {
-    const float s = seq_sum_wave(sq, n);
+    const float s = (n <= 64 * SPEC_C) ? seq_sum_wave(sq, n) : seq_sum_wave_n(sq, n);
     if (tid == 0) *inv_slot = (float)(1.0 / sqrt((double)(s / (float)n + eps)));
   }
   __syncthreads();
@@ -663,13 +663,13 @@ __global__ void __launch_bounds__(row_threads(NB, PRO)) k_gemv_row(GemvParams P)
   constexpr int BPW = (NB + NW - 1) / NW;  // Q8_K blocks quantised per wave
   constexpr bool PAIRED = (MODE == MODE_SWIGLU);
   constexpr bool NORM = (PRO == PRO_NORM || PRO == PRO_EMBED_NORM || PRO == PRO_ARGMAX_EMBED_NORM);
-  static_assert(!NORM || NB <= 4, "the norm prologue holds one float4 per thread");
+  static_assert(!NORM || NB <= NW, "the norm prologue holds one float4 per thread, one block per wave");
   extern __shared__ __align__(16) unsigned char smem[];
   float* sq = reinterpret_cast<float*>(smem);  // [n_x_lds] (norm prologues only)
   __shared__ Q8KRow<NB> s;
   __shared__ __align__(16) float terms[PAIRED ? 2 : 1][RPW * IPR];
   __shared__ float inv_slot;
-  __shared__ ArgCand ared[4];
+  __shared__ ArgCand ared[NW];  // one slot per wave (reduce_argmax_partials)
 
   const GemvJob J = launch_job(P);
   if ((int)blockIdx.x >= J.n_wg) return;  // uniform: the launch's widest job sets the grid
@@ -758,14 +758,20 @@ C2H_GEMV_ROW(3, PRO_QUANT, MODE_RESID)
 C2H_GEMV_ROW(4, PRO_QUANT, MODE_RESID)
 C2H_GEMV_ROW(12, PRO_QUANT, MODE_RESID)
 C2H_GEMV_ROW(19, PRO_QUANT, MODE_RESID)
+C2H_GEMV_ROW(8, PRO_QUANT, MODE_RESID)   // Qwen3-1.7B: attn_out (2048 columns)
+C2H_GEMV_ROW(24, PRO_QUANT, MODE_RESID)  // Qwen3-1.7B: ffn_down (6144 columns)
 C2H_GEMV_ROW(3, PRO_NORM, MODE_SWIGLU)
 C2H_GEMV_ROW(4, PRO_NORM, MODE_SWIGLU)
+C2H_GEMV_ROW(8, PRO_NORM, MODE_SWIGLU)
 C2H_GEMV_ROW(3, PRO_NORM, MODE_BIAS)
 C2H_GEMV_ROW(4, PRO_NORM, MODE_BIAS)
+C2H_GEMV_ROW(8, PRO_NORM, MODE_BIAS)
 C2H_GEMV_ROW(3, PRO_EMBED_NORM, MODE_BIAS)
 C2H_GEMV_ROW(4, PRO_EMBED_NORM, MODE_BIAS)
+C2H_GEMV_ROW(8, PRO_EMBED_NORM, MODE_BIAS)
 C2H_GEMV_ROW(3, PRO_ARGMAX_EMBED_NORM, MODE_BIAS)
 C2H_GEMV_ROW(4, PRO_ARGMAX_EMBED_NORM, MODE_BIAS)
+C2H_GEMV_ROW(8, PRO_ARGMAX_EMBED_NORM, MODE_BIAS)
 #undef C2H_GEMV_ROW
 
 // ------------------------------------------- GEMV on an external Q8_K row
@@ -1071,8 +1077,9 @@ C2H_GEMV_F(PRO_QUANT, MODE_STORE)
 // ------------------------------------------------------------- final norm
 
 // normX = RMSNorm(X) * output_norm (engine/forward.go:135); x and w are
-// loaded up front, rows of up to 1024 values (a multiple of 4).
-__global__ void __launch_bounds__(256) k_rmsnorm(NormParams P) {
+// loaded up front, rows of up to 4*blockDim.x values (a multiple of 4;
+// 256 threads up to 1024 values, 512 up to 2048).
+__global__ void __launch_bounds__(512) k_rmsnorm(NormParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
   float* sq = reinterpret_cast<float*>(smem);
   __shared__ float inv_slot;
@@ -1529,6 +1536,166 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
 template __global__ void k_attn_core<ATT_TIER_128>(AttnCoreParams);
 template __global__ void k_attn_core<ATT_TIER_256>(AttnCoreParams);
 template __global__ void k_attn_core<ATT_TIER_ANY>(AttnCoreParams);
+
+// ------------------------------------------------ attention, head_dim 128
+
+// Score of one position for head_dim 128 (internal/simd/c2_tensor_attn_gen.go:
+// 18-50 with hd = 128): two 8-lane FMA accumulators over d = 0,16,..,112
+// (lanes l and 8+l), then ((l0+l1)+(l2+l3))+((l4+l5)+(l6+l7)) of acc0+acc1,
+// times scale.  kr: the K row (cache or LDS), read as 32 float4.
+__device__ __forceinline__ float attn_score_h128(const float* q_s, const float* kr, float scale) {
+  const float4* k4 = reinterpret_cast<const float4*>(kr);
+  float4 kk[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) kk[i] = k4[i];
+  float a0[8], a1[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l) {
+    a0[l] = 0.0f;
+    a1[l] = 0.0f;
+  }
+#pragma unroll
+  for (int d = 0; d < 128; d += 16) {
+    const float4 c0 = kk[d / 4], c1 = kk[d / 4 + 1], c2 = kk[d / 4 + 2], c3 = kk[d / 4 + 3];
+    const float k16[16] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w,
+                           c2.x, c2.y, c2.z, c2.w, c3.x, c3.y, c3.z, c3.w};
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      a0[l] = __builtin_fmaf(q_s[d + l], k16[l], a0[l]);
+      a1[l] = __builtin_fmaf(q_s[d + 8 + l], k16[8 + l], a1[l]);
+    }
+  }
+  float v[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l) v[l] = a0[l] + a1[l];
+  const float sco = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+  return sco * scale;
+}
+
+// Attention of one query head per workgroup for head_dim 128 (Qwen3;
+// engine/forward.go:66-106 from the q|k|v rows on, for that head):
+//   per-head QK-RMSNorm of q_h and k_g when the layer has the weights
+//     (engine/forward.go:80-91 -> tensor/ops.go:207-218 over the head's 128
+//     values: exact sequential sum of x*x, one wave per vector);
+//   RoPE (tensor/ops.go:262-286, pairs (i, i+64));
+//   KV store (engine/kvcache.go:143-157) by the group's first head;
+//   scores in the two-accumulator FMA order (attn_score_h128), softmax with
+//     f64 exp and an exact sequential f32 sum (tensor/ops.go:317-339);
+//   per output dimension one FMA chain over the positions
+//     (c2_tensor_attn_gen.go:85-117, the hd % 64 == 0 path), V read from
+//     the quad-major cache, four positions per 16-byte load; position pos
+//     uses this launch's v.
+// The scores of every position sit in LDS (attn_h128_lds_floats(max_ctx)).
+// Grid (query heads per KV head, KV heads, query tokens); 256 threads.
+__global__ void __launch_bounds__(256) k_attn_h128(AttnCoreParams P) {
+  constexpr int HD = 128;
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* sc = reinterpret_cast<float*>(smem);
+  __shared__ __align__(16) float qkv_s[3][HD];
+  __shared__ __align__(16) float sq_s[2][HD];  // x*x of q_h and of k_g
+  __shared__ float red_m[4];
+  __shared__ float inv_s[3];
+
+  const int tid = threadIdx.x;
+  const int qpkv = (int)gridDim.x;
+  const int g = (int)blockIdx.y;
+  const int h = g * qpkv + (int)blockIdx.x;
+  const int ti = P.tok0 + (int)blockIdx.z;  // query token of the batch (0 in decode)
+  const int e = tid & (HD - 1);
+  const int role = tid >> 7;  // 0: this thread holds q_h[e], 1: k_g[e]
+  const bool has_q_norm = P.q_norm != nullptr, has_k_norm = P.k_norm != nullptr;
+  // ---- loads: q_h / k_g element, v_g element, the head-norm weight, then
+  // the position and the RoPE row
+  const float* src = role == 0 ? P.q + (size_t)ti * P.q_ld + h * HD : P.k + (size_t)ti * P.kv_ld + g * HD;
+  const float own = src[e];
+  const float vown = P.v[(size_t)ti * P.kv_ld + g * HD + e];
+  const float* nsrc = role == 0 ? P.q_norm : P.k_norm;
+  const float nwt = nsrc ? nsrc[e] : 1.0f;
+  issue_fence();
+  const int pos = P.state->pos + ti;
+  const int T = pos + 1;
+  const size_t head_stride = (size_t)kv_slot(P.max_ctx) * HD;
+  float* kcache = P.kv + ((size_t)P.layer * P.n_kv_heads + g) * head_stride;
+  float* vcache = P.kv + (((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * head_stride;
+  const int rp = min(max(pos, 0), P.rope_len - 1);
+  const float rcos = P.rope_cos[(size_t)rp * (HD / 2) + (tid & 63)];
+  const float rsin = P.rope_sin[(size_t)rp * (HD / 2) + (tid & 63)];
+  issue_fence();
+
+  qkv_s[role][e] = own;
+  if (role == 0) qkv_s[2][e] = vown;
+  sq_s[role][e] = own * own;
+  __syncthreads();
+  float* q_s = qkv_s[0];
+  float* k_s = qkv_s[1];
+  float* v_s = qkv_s[2];
+
+  // ---- QK-norm: wave 0 sums q_h's squares, wave 2 k_g's
+  if (has_q_norm || has_k_norm) {
+    if (tid < 64 && has_q_norm) {
+      const float s = seq_sum_wave(sq_s[0], HD);
+      if (tid == 0) inv_s[0] = (float)(1.0 / sqrt((double)(s / (float)HD + P.eps)));
+    }
+    if (tid >= 128 && tid < 192 && has_k_norm) {
+      const float s = seq_sum_wave(sq_s[1], HD);
+      if (tid == 128) inv_s[1] = (float)(1.0 / sqrt((double)(s / (float)HD + P.eps)));
+    }
+    __syncthreads();
+    if (role == 0 ? has_q_norm : has_k_norm) qkv_s[role][e] = (own * inv_s[role]) * nwt;
+    __syncthreads();
+  }
+
+  // ---- RoPE: threads 0..63 turn q's pairs, 64..127 k's
+  if (pos >= 0 && pos < P.rope_len && tid < HD) {
+    float* r = (tid < 64) ? q_s : k_s;
+    const int i = tid & 63;
+    const float x0 = r[i], x1 = r[i + 64];
+    r[i] = (x0 * rcos) - (x1 * rsin);
+    r[i + 64] = (x0 * rsin) + (x1 * rcos);
+  }
+  __syncthreads();
+
+  if (P.store_kv && blockIdx.x == 0 && tid < HD && pos < P.max_ctx) {
+    kcache[(size_t)pos * HD + tid] = k_s[tid];
+    vcache[vq_index(pos, tid, HD)] = v_s[tid];
+  }
+  if (T > P.max_ctx) return;  // rejected on the host; kept as a guard
+
+  // ---- scores; position pos uses this launch's k
+  float lmax = -__builtin_inff();
+  for (int p = tid; p < T; p += 256) {
+    const float* kr = (p == pos) ? k_s : kcache + (size_t)p * HD;
+    const float sco = attn_score_h128(q_s, kr, P.scale);
+    sc[p] = sco;
+    lmax = (sco > lmax) ? sco : lmax;
+  }
+  // ---- softmax: max (x[0] first, strict '>': the max of the non-NaN
+  // scores, or NaN when score[0] is NaN), f32(exp(f64(x - max))), the exact
+  // sequential sum, times f32(1/sum)
+  lmax = wave_max_dpp(lmax);
+  if ((tid & 63) == 0) red_m[tid >> 6] = lmax;
+  __syncthreads();
+  float mx = fmax_gt(fmax_gt(fmax_gt(red_m[0], red_m[1]), red_m[2]), red_m[3]);
+  if (sc[0] != sc[0]) mx = sc[0];
+  for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));
+  __syncthreads();
+  if (tid < 64) {
+    const float ssum = (T <= 64 * SPEC_C) ? seq_sum_wave(sc, T) : seq_sum_wave_n(sc, T);
+    if (tid == 0) inv_s[2] = 1.0f / ssum;
+  }
+  __syncthreads();
+  const float inv = inv_s[2];
+  for (int p = tid; p < T; p += 256) sc[p] = sc[p] * inv;
+  __syncthreads();
+
+  // ---- AV: out[d] = fma chain over p of (prob[p], V[p][d])
+  if (tid < HD) {
+    float acc = 0.0f;
+    if (pos > 0) acc = av_chain_q3<HD>(sc, reinterpret_cast<const f32x4_t*>(vcache), pos, tid, acc);
+    acc = __builtin_fmaf(sc[pos], v_s[tid], acc);
+    P.out[(size_t)ti * P.out_ld + h * HD + tid] = acc;
+  }
+}
 
 
 // ------------------------------------------- attention, long contexts
@@ -2431,6 +2598,7 @@ C2H_VOCAB(29)
 C2H_VOCAB(30)
 C2H_VOCAB(31)
 C2H_VOCAB(32)
+C2H_VOCAB(64)  // Qwen3-1.7B: 2048 columns
 #undef C2H_VOCAB
 
 // Final reduction for standalone argmax calls (no following layer kernel).

@@ -303,6 +303,9 @@ class ModelShape:
     t_down: int = Q6_K
     t_embd: int = Q8_0
     t_out: Optional[int] = None  # an untied output.weight of this type (None: tied to token_embd)
+    # Qwen3 files: qwen3.* metadata keys, per-head attn_q_norm / attn_k_norm
+    # weights (engine/forward.go:80-91) and no q/k/v biases
+    arch: str = "qwen2"
 
     @property
     def head_dim(self) -> int:
@@ -310,6 +313,11 @@ class ModelShape:
 
 
 QWEN05B = ModelShape()
+
+# Qwen3-1.7B's dimensions (engine/model_config_test.go:18-33: 28 layers,
+# 16/8 heads, head_dim 2048/16 = 128; FFN 6144, tied embedding) in the
+# Q4_K_M mix of the other shapes.
+QWEN3_1_7B = ModelShape(n_layers=28, n_embd=2048, n_heads=16, n_kv_heads=8, n_ff=6144, arch="qwen3")
 
 # The published Qwen2.5-0.5B-Instruct Q4_K_M file's format mix: 896-column
 # matrices cannot hold K-quant super-blocks whole, so q/k/o/gate/up are Q5_0
@@ -356,32 +364,40 @@ def write_synthetic_model(path: str, shape: ModelShape = QWEN05B, seed: int = 20
     f32("output_norm.weight", np.ones(E, np.float32))
     if shape.t_out is not None:
         quant("output.weight", shape.t_out, V, E)
+    qwen3 = shape.arch == "qwen3"
     for i in range(L):
         f32(f"blk.{i}.attn_norm.weight", np.ones(E, np.float32))
         quant(f"blk.{i}.attn_q.weight", shape.t_q, E, E)
-        f32(f"blk.{i}.attn_q.bias", rng.normal(0.0, bias_std, E).astype(np.float32))
+        if not qwen3:
+            f32(f"blk.{i}.attn_q.bias", rng.normal(0.0, bias_std, E).astype(np.float32))
         quant(f"blk.{i}.attn_k.weight", shape.t_k, KV, E)
-        f32(f"blk.{i}.attn_k.bias", rng.normal(0.0, bias_std, KV).astype(np.float32))
+        if not qwen3:
+            f32(f"blk.{i}.attn_k.bias", rng.normal(0.0, bias_std, KV).astype(np.float32))
         quant(f"blk.{i}.attn_v.weight", shape.t_v, KV, E)
-        f32(f"blk.{i}.attn_v.bias", rng.normal(0.0, bias_std, KV).astype(np.float32))
+        if not qwen3:
+            f32(f"blk.{i}.attn_v.bias", rng.normal(0.0, bias_std, KV).astype(np.float32))
+        else:  # per-head QK-norm weights near 1, distinct for q and k
+            f32(f"blk.{i}.attn_q_norm.weight", rng.uniform(0.5, 1.5, shape.head_dim).astype(np.float32))
+            f32(f"blk.{i}.attn_k_norm.weight", rng.uniform(0.5, 1.5, shape.head_dim).astype(np.float32))
         quant(f"blk.{i}.attn_output.weight", shape.t_o, E, E)
         f32(f"blk.{i}.ffn_norm.weight", np.ones(E, np.float32))
         quant(f"blk.{i}.ffn_gate.weight", shape.t_gate, F, E)
         quant(f"blk.{i}.ffn_up.weight", shape.t_up, F, E)
         quant(f"blk.{i}.ffn_down.weight", shape.t_down, E, F)
 
+    a = shape.arch
     md = [
-        ("general.architecture", T_STR, "qwen2"),
-        ("general.name", T_STR, "synthetic-qwen2.5-0.5b-shape"),
+        ("general.architecture", T_STR, a),
+        ("general.name", T_STR, "synthetic-qwen3-shape" if qwen3 else "synthetic-qwen2.5-0.5b-shape"),
         ("general.alignment", T_U32, 32),
-        ("qwen2.block_count", T_U32, L),
-        ("qwen2.context_length", T_U32, 32768),
-        ("qwen2.embedding_length", T_U32, E),
-        ("qwen2.feed_forward_length", T_U32, F),
-        ("qwen2.attention.head_count", T_U32, shape.n_heads),
-        ("qwen2.attention.head_count_kv", T_U32, shape.n_kv_heads),
-        ("qwen2.rope.freq_base", T_F32, shape.rope_theta),
-        ("qwen2.attention.layer_norm_rms_epsilon", T_F32, shape.rms_eps),
+        (f"{a}.block_count", T_U32, L),
+        (f"{a}.context_length", T_U32, 40960 if qwen3 else 32768),
+        (f"{a}.embedding_length", T_U32, E),
+        (f"{a}.feed_forward_length", T_U32, F),
+        (f"{a}.attention.head_count", T_U32, shape.n_heads),
+        (f"{a}.attention.head_count_kv", T_U32, shape.n_kv_heads),
+        (f"{a}.rope.freq_base", T_F32, shape.rope_theta),
+        (f"{a}.attention.layer_norm_rms_epsilon", T_F32, shape.rms_eps),
         ("tokenizer.ggml.model", T_STR, "gpt2"),
         ("tokenizer.ggml.tokens", T_ARR, (T_STR, token_list(V))),
     ]

@@ -50,20 +50,22 @@ enum c2h_role {
   C2H_ROLE_FFN_NORM = 18,
   C2H_ROLE_FFN_GATE = 19,
   C2H_ROLE_FFN_UP = 20,
-  C2H_ROLE_FFN_DOWN = 21
+  C2H_ROLE_FFN_DOWN = 21,
+  C2H_ROLE_ATTN_Q_NORM = 22, /* Qwen3 blk.N.attn_q_norm.weight (head_dim floats, engine/model.go:168-170) */
+  C2H_ROLE_ATTN_K_NORM = 23  /* Qwen3 blk.N.attn_k_norm.weight (engine/model.go:177-179) */
 };
 
 /* Model dimensions, as engine.LoadModel resolves them (engine/model.go:64-145). */
 typedef struct c2h_model_desc {
-  int32_t n_layers;   /* qwen2.block_count (24) */
-  int32_t n_embd;     /* qwen2.embedding_length (896) */
-  int32_t n_heads;    /* qwen2.attention.head_count (14) */
-  int32_t n_kv_heads; /* qwen2.attention.head_count_kv (2) */
-  int32_t head_dim;   /* n_embd / n_heads (64) */
-  int32_t n_ff;       /* qwen2.feed_forward_length (4864) */
+  int32_t n_layers;   /* qwen2.block_count, else qwen3.block_count (24; Qwen3-1.7B 28) */
+  int32_t n_embd;     /* *.embedding_length (896; 2048) */
+  int32_t n_heads;    /* *.attention.head_count (14; 16) */
+  int32_t n_kv_heads; /* *.attention.head_count_kv (2; 8) */
+  int32_t head_dim;   /* n_embd / n_heads (64; 128), engine/model.go:137 */
+  int32_t n_ff;       /* *.feed_forward_length (4864; 6144) */
   int32_t n_vocab;    /* token_embd dims[1] (151936) */
   int32_t max_ctx;    /* KV positions; engine.MaxContextLen = 16384 (engine/kvcache.go:11);
-                         this build runs up to 36864 */
+                         this build runs up to 36864 at head_dim 64, 38848 at 128 */
   float rms_eps;      /* 1e-6 */
   float rope_theta;   /* 1e6 */
   int32_t reserved[6];

@@ -631,6 +631,7 @@ typedef struct {
   const float *attn_norm, *bq, *bk, *bv, *ffn_norm;
   const uint8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
   int32_t tq, tk, tv, to, tg, tu, td;
+  const float *q_norm, *k_norm; /* Qwen3 attn_q_norm / attn_k_norm (head_dim), NULL when absent */
 } orc_layer;
 
 typedef struct {
@@ -787,6 +788,11 @@ void orc_forward(orc_state* s, int32_t tok, int pos, float* normx_out) {
     if (L->bk) orc_add_bias(s->k, L->bk, KV);
     dispatch_gemv(s, s->v, L->wv, L->tv, s->normx, KV, E);
     if (L->bv) orc_add_bias(s->v, L->bv, KV);
+    /* engine/forward.go:80-91: per-head QK-RMSNorm (Qwen3), before RoPE */
+    if (L->q_norm)
+      for (int h = 0; h < m->n_heads; ++h) orc_rmsnorm(s->q + h * hd, s->q + h * hd, L->q_norm, hd, m->eps);
+    if (L->k_norm)
+      for (int h = 0; h < m->n_kv_heads; ++h) orc_rmsnorm(s->k + h * hd, s->k + h * hd, L->k_norm, hd, m->eps);
     orc_rope_apply(s->q, E, m->n_heads, pos, s->cosb, s->sinb, m->max_ctx, hd);
     orc_rope_apply(s->k, KV, m->n_kv_heads, pos, s->cosb, s->sinb, m->max_ctx, hd);
     if (pos >= 0 && pos < m->max_ctx) { /* engine/kvcache.go:143-157 */

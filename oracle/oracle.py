@@ -23,7 +23,8 @@ I32P = C.POINTER(C.c_int32)
 class OrcLayer(C.Structure):
     _fields_ = [(n, F32P) for n in ("attn_norm", "bq", "bk", "bv", "ffn_norm")] + \
                [(n, U8P) for n in ("wq", "wk", "wv", "wo", "wg", "wu", "wd")] + \
-               [(n, C.c_int32) for n in ("tq", "tk", "tv", "to", "tg", "tu", "td")]
+               [(n, C.c_int32) for n in ("tq", "tk", "tv", "to", "tg", "tu", "td")] + \
+               [(n, F32P) for n in ("q_norm", "k_norm")]
 
 
 class OrcModel(C.Structure):
@@ -198,6 +199,7 @@ class OracleEngine:
             ly.attn_norm, ly.bq, ly.bk, ly.bv, ly.ffn_norm = (
                 fp(g("attn_norm.weight")), fp(g("attn_q.bias")), fp(g("attn_k.bias")), fp(g("attn_v.bias")),
                 fp(g("ffn_norm.weight")))
+            ly.q_norm, ly.k_norm = fp(g("attn_q_norm.weight")), fp(g("attn_k_norm.weight"))
             for fld, nm in (("wq", "attn_q"), ("wk", "attn_k"), ("wv", "attn_v"), ("wo", "attn_output"),
                             ("wg", "ffn_gate"), ("wu", "ffn_up"), ("wd", "ffn_down")):
                 ti = g(nm + ".weight")

@@ -11,6 +11,9 @@ every matrix product, norm, rotation, softmax and activation is float64:
   per layer:
     n    = x / sqrt(mean(x^2) + eps) * attn_norm
     q,k,v = Wq n + bq, Wk n + bk, Wv n + bv
+    (Qwen3: no biases; every head of q and of k divided by its own
+     sqrt(mean(head^2) + eps) and scaled by attn_q_norm / attn_k_norm,
+     engine/forward.go:80-91)
     rotate-half RoPE on every head: pair (i, i + hd/2) turned by
          pos * theta^(-2i/hd)
     per query head h, KV head h // (H/KVH): softmax(q.K^T / sqrt(hd)) V
@@ -83,14 +86,15 @@ def q8k_round_trip(x: np.ndarray) -> np.ndarray:
 
 class Qwen2F64:
     def __init__(self, gf: G.GGUFFile, max_ctx: int = 1024):
-        md = gf
-        self.E = md.get_u32("qwen2.embedding_length")
-        self.L = md.get_u32("qwen2.block_count")
-        self.H = md.get_u32("qwen2.attention.head_count")
-        self.KVH = md.get_u32("qwen2.attention.head_count_kv")
-        self.F = md.get_u32("qwen2.feed_forward_length")
-        self.theta = float(np.float32(md.get_f32("qwen2.rope.freq_base")))
-        self.eps = float(np.float32(md.get_f32("qwen2.attention.layer_norm_rms_epsilon")))
+        arch = gf.metadata.get("general.architecture", "qwen2")
+        u32 = lambda k: gf.get_u32(f"{arch}.{k}")
+        self.E = u32("embedding_length")
+        self.L = u32("block_count")
+        self.H = u32("attention.head_count")
+        self.KVH = u32("attention.head_count_kv")
+        self.F = u32("feed_forward_length")
+        self.theta = float(np.float32(gf.get_f32(f"{arch}.rope.freq_base")))
+        self.eps = float(np.float32(gf.get_f32(f"{arch}.attention.layer_norm_rms_epsilon")))
         self.hd = self.E // self.H
         tm = gf.tensor_map
         self.types = {}
@@ -120,6 +124,8 @@ class Qwen2F64:
                 ly[k] = vec(p + k + ".weight")
             for k in ("attn_q", "attn_k", "attn_v"):
                 ly[k + ".bias"] = vec(p + k + ".bias")
+            for k in ("attn_q_norm", "attn_k_norm"):
+                ly[k] = vec(p + k + ".weight")
             self.layers.append(ly)
         self.max_ctx = max_ctx
         kv = self.KVH * self.hd
@@ -175,6 +181,10 @@ class Qwen2F64:
     def _rmsnorm(self, x, w):
         return x / np.sqrt(np.mean(x * x) + self.eps) * w
 
+    def _head_norm(self, v, w):
+        hd = self.hd
+        return np.concatenate([self._rmsnorm(v[i:i + hd], w) for i in range(0, len(v), hd)])
+
     def _matvec(self, w, t, x):
         if t in (G.Q4_K, G.Q6_K):
             return w @ self._q8k_row(x, w.shape[1] // 256)
@@ -204,6 +214,10 @@ class Qwen2F64:
                 b = ly[name + ".bias"]
                 if b is not None:
                     arr += b
+            if ly["attn_q_norm"] is not None:
+                q = self._head_norm(q, ly["attn_q_norm"])
+            if ly["attn_k_norm"] is not None:
+                k = self._head_norm(k, ly["attn_k_norm"])
             q, k = self._rope(q, pos), self._rope(k, pos)
             self.K[li, pos], self.Vc[li, pos] = k, v
             att = np.zeros(E)
@@ -276,7 +290,9 @@ def write_pin_model(path: str, shape: G.ModelShape, seed: int, bias_std: float =
     (the bench's Q4_K draw is all-positive, mean weight ~ +1, so outputs are
     small differences of large sums), every norm weight vector distinct
     (U(norm_lo, norm_hi)), biases N(0, bias_std^2) comparable to the
-    projections, so a swapped norm vector or a dropped bias shows."""
+    projections, so a swapped norm vector or a dropped bias shows.  A
+    shape with arch "qwen3" has no biases and distinct attn_q_norm /
+    attn_k_norm vectors (U(norm_lo, norm_hi), head_dim long)."""
     rng = np.random.default_rng(seed)
     E, F, V, L = shape.n_embd, shape.n_ff, shape.n_vocab, shape.n_layers
     KV = shape.n_kv_heads * shape.head_dim
@@ -292,6 +308,7 @@ def write_pin_model(path: str, shape: G.ModelShape, seed: int, bias_std: float =
     def f32(name, values):
         tensors.append((name, [len(values)], G.F32, np.asarray(values, dtype="<f4").view(np.uint8)))
 
+    qwen3 = shape.arch == "qwen3"
     quant("token_embd.weight", shape.t_embd, V, E)
     f32("output_norm.weight", rng.uniform(norm_lo, norm_hi, E))
     if shape.t_out is not None:
@@ -299,26 +316,33 @@ def write_pin_model(path: str, shape: G.ModelShape, seed: int, bias_std: float =
     for i in range(L):
         f32(f"blk.{i}.attn_norm.weight", rng.uniform(norm_lo, norm_hi, E))
         quant(f"blk.{i}.attn_q.weight", shape.t_q, E, E)
-        f32(f"blk.{i}.attn_q.bias", rng.normal(0.0, bias_std, E))
+        if not qwen3:
+            f32(f"blk.{i}.attn_q.bias", rng.normal(0.0, bias_std, E))
         quant(f"blk.{i}.attn_k.weight", shape.t_k, KV, E)
-        f32(f"blk.{i}.attn_k.bias", rng.normal(0.0, bias_std, KV))
+        if not qwen3:
+            f32(f"blk.{i}.attn_k.bias", rng.normal(0.0, bias_std, KV))
         quant(f"blk.{i}.attn_v.weight", shape.t_v, KV, E)
-        f32(f"blk.{i}.attn_v.bias", rng.normal(0.0, bias_std, KV))
+        if not qwen3:
+            f32(f"blk.{i}.attn_v.bias", rng.normal(0.0, bias_std, KV))
+        else:
+            f32(f"blk.{i}.attn_q_norm.weight", rng.uniform(norm_lo, norm_hi, shape.head_dim))
+            f32(f"blk.{i}.attn_k_norm.weight", rng.uniform(norm_lo, norm_hi, shape.head_dim))
         quant(f"blk.{i}.attn_output.weight", shape.t_o, E, E)
         f32(f"blk.{i}.ffn_norm.weight", rng.uniform(norm_lo, norm_hi, E))
         quant(f"blk.{i}.ffn_gate.weight", shape.t_gate, F, E)
         quant(f"blk.{i}.ffn_up.weight", shape.t_up, F, E)
         quant(f"blk.{i}.ffn_down.weight", shape.t_down, E, F)
+    a = shape.arch
     md = [
-        ("general.architecture", G.T_STR, "qwen2"),
+        ("general.architecture", G.T_STR, a),
         ("general.alignment", G.T_U32, 32),
-        ("qwen2.block_count", G.T_U32, L),
-        ("qwen2.embedding_length", G.T_U32, E),
-        ("qwen2.feed_forward_length", G.T_U32, F),
-        ("qwen2.attention.head_count", G.T_U32, shape.n_heads),
-        ("qwen2.attention.head_count_kv", G.T_U32, shape.n_kv_heads),
-        ("qwen2.rope.freq_base", G.T_F32, shape.rope_theta),
-        ("qwen2.attention.layer_norm_rms_epsilon", G.T_F32, shape.rms_eps),
+        (f"{a}.block_count", G.T_U32, L),
+        (f"{a}.embedding_length", G.T_U32, E),
+        (f"{a}.feed_forward_length", G.T_U32, F),
+        (f"{a}.attention.head_count", G.T_U32, shape.n_heads),
+        (f"{a}.attention.head_count_kv", G.T_U32, shape.n_kv_heads),
+        (f"{a}.rope.freq_base", G.T_F32, shape.rope_theta),
+        (f"{a}.attention.layer_norm_rms_epsilon", G.T_F32, shape.rms_eps),
         ("tokenizer.ggml.model", G.T_STR, "gpt2"),
         ("tokenizer.ggml.tokens", G.T_ARR, (G.T_STR, G.token_list(V))),
     ]

@@ -21,7 +21,9 @@ The pin models (tests/qwen2_f64.py, write_pin_model) carry distinct norm
 weight vectors and biases comparable to the projections, so a swapped norm
 vector, a dropped bias, a wrong RoPE pairing or GQA head map, a missing
 residual or a penalty on the wrong ids moves these outputs by far more than
-the tolerance; float32 rounding moves them by ~1e-6.  The bench's own
+the tolerance; float32 rounding moves them by ~1e-6.  The Qwen3 case
+(engine/forward.go:80-91) adds per-head QK-norm vectors of their own, so a
+skipped or swapped QK-norm shows the same way.  The bench's own
 synthetic draw (all-positive Q4_K weights) is checked as well."""
 import numpy as np
 import pytest
@@ -50,6 +52,9 @@ SHAPES = {
     # untied K-quant output.weight (the vocab projection on the Q8_K row)
     "untied_q6k": G.ModelShape(n_layers=2, n_vocab=V, t_out=G.Q6_K),
     "untied_q4k": G.ModelShape(n_layers=2, n_vocab=V, t_out=G.Q4_K),
+    # Qwen3: head_dim 128, per-head QK-norm before RoPE, no biases
+    "qwen3_hd128": G.ModelShape(n_layers=2, n_embd=512, n_heads=4, n_kv_heads=2, n_ff=768, n_vocab=V,
+                                arch="qwen3"),
 }
 CASES = sorted(SHAPES) + ["bench_draw"]
 

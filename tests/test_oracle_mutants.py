@@ -33,14 +33,20 @@ MUTANTS = [
     ("ingest clamp dropped", "if (pos > s->seq_len) pos = s->seq_len;", "", "ingest"),
     ("im_end not exempt", "t != im_end && t != eos", "t != eos", "penalty"),
     ("penalty window one short", "int start = pos - 64;", "int start = pos - 63;", "penalty_window"),
+    ("k QK-norm skipped", "if (L->k_norm)\n", "if (0)\n", "forward_qwen3"),
+    ("q QK-norm with the k weights", "orc_rmsnorm(s->q + h * hd, s->q + h * hd, L->q_norm, hd, m->eps)",
+     "orc_rmsnorm(s->q + h * hd, s->q + h * hd, L->k_norm, hd, m->eps)", "forward_qwen3"),
 ]
 
 
 @pytest.fixture(scope="module")
-def model(tmp_path_factory):
-    path = str(tmp_path_factory.mktemp("mut") / "pin.gguf")
-    write_pin_model(path, T.SHAPES["q4k_mix"], seed=31)
-    return G.GGUFFile(path)
+def models(tmp_path_factory):
+    out = {}
+    for key, shape in (("qwen2", "q4k_mix"), ("qwen3", "qwen3_hd128")):
+        path = str(tmp_path_factory.mktemp("mut") / f"{key}.gguf")
+        write_pin_model(path, T.SHAPES[shape], seed=31)
+        out[key] = G.GGUFFile(path)
+    return out
 
 
 def build_variant(tmp, name, old, new):
@@ -61,7 +67,7 @@ def run_pin(gf, so, which):
     orc.start_q8k_trace()
     ref = Qwen2F64(gf, max_ctx=256)
     try:
-        if which == "forward":
+        if which in ("forward", "forward_qwen3"):
             rng = np.random.default_rng(5)
             for p, t in enumerate(rng.integers(0, T.V, 6)):
                 got = orc.forward(int(t), p)
@@ -104,14 +110,18 @@ def check_window_edge(gf, orc, ref):
     assert int(got[0]) == int(np.argmax(want))
 
 
-def test_unmodified_copy_passes_every_pin(model, tmp_path):
+def model_for(models, which):
+    return models["qwen3" if which.endswith("qwen3") else "qwen2"]
+
+
+def test_unmodified_copy_passes_every_pin(models, tmp_path):
     so = build_variant(tmp_path, "unmodified", None, None)
-    for which in ("forward", "ingest", "penalty", "penalty_window"):
-        run_pin(model, so, which)
+    for which in ("forward", "ingest", "penalty", "penalty_window", "forward_qwen3"):
+        run_pin(model_for(models, which), so, which)
 
 
 @pytest.mark.parametrize("name,old,new,which", MUTANTS, ids=[m[0] for m in MUTANTS])
-def test_pin_catches_planted_mistake(model, tmp_path, name, old, new, which):
+def test_pin_catches_planted_mistake(models, tmp_path, name, old, new, which):
     so = build_variant(tmp_path, name, old, new)
     with pytest.raises(AssertionError):
-        run_pin(model, so, which)
+        run_pin(model_for(models, which), so, which)
