@@ -18,8 +18,9 @@ and GB/s and the step's bytes and GB/s; the vocab kernel from HBM; the
 operator microbench of the layer shapes (Q4_K/Q6_K x Q8_K GEMV and the Q8_K
 quantiser, hot and with the weights rotated through 1 GiB of copies); the
 batched prefill of a 512-token prompt; decode at long contexts (512 / 4096 /
-32768 positions of N(0,1) K/V); and decode and prefill with the real Q4_K_M
-file's format mix (Q5_0 / Q8_0 / Q6_K).
+32768 positions of N(0,1) K/V); decode and prefill with the real Q4_K_M
+file's format mix (Q5_0 / Q8_0 / Q6_K); and decode of the Qwen3-1.7B shape
+(head_dim 128, QK-norm).
 """
 from __future__ import annotations
 
@@ -332,6 +333,48 @@ def real_formats(tmpdir, im_end, eos, steps: int = 64):
             "prefill_512_ms": pf["ms"], "prefill_512_tok_s": pf["tok_s"]}
 
 
+def qwen3_decode(tmpdir, im_end, eos, steps: int = 64):
+    """The Qwen3-1.7B shape (28 layers, hidden 2048, 16/8 heads of 128, FFN
+    6144, per-head QK-norm, tied Q8_0 embedding; Q4_K / Q6_K projections),
+    random-init: a 32-token prompt (one forward per token at head_dim 128),
+    then greedy steps timed on the host around synchronous c2h_step calls,
+    as the main line, and device-fed (c2h_time_steps); algorithmic bytes of
+    a step at the mean attended position."""
+    from c2slm_amd import _lib as H
+    from c2slm_amd import gguf as G
+    path = os.path.join(tmpdir, "qwen3_1_7b_synth.gguf")
+    G.write_synthetic_model(path, G.QWEN3_1_7B, seed=SEED + 7)
+    gf = G.GGUFFile(path)
+    desc = H.desc_from_gguf(gf, max_ctx=1024)
+    ctx = H.Ctx(desc)
+    H.load_gguf_into(ctx, gf)
+    prompt = np.random.default_rng(SEED).integers(0, desc.n_vocab, PROMPT_LEN).astype(np.int32)
+    ctx.set_token_ids(0, prompt)
+    ctx.prefill(prompt, 0, want_normx=False)
+    pos = PROMPT_LEN
+    for _ in range(8):
+        ctx.step(pos, PENALTY, im_end, eos)
+        pos += 1
+    ctx.normx()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ctx.step(pos, PENALTY, im_end, eos)
+        pos += 1
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    fed_ms = ctx.time_steps(pos, steps, PENALTY, im_end, eos)
+    kb = kernel_bytes(gf, desc, pos - steps / 2)
+    step_bytes = (desc.n_layers * sum(kb[k] for k in ("qkv", "attn", "attn_out", "ffn_in", "ffn_out"))
+                  + kb["final_norm"] + kb["vocab"])
+    ctx.close()
+    del gf
+    os.remove(path)
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    return {"shape": "Qwen3-1.7B: 28 layers, hidden 2048, 16/8 heads x 128, FFN 6144, QK-norm, vocab 151936",
+            "ms_per_step": round(ms, 4), "tok_s": round(1000.0 / ms, 1),
+            "device_fed_ms_per_step": round(fed_ms, 4), "device_fed_tok_s": round(1000.0 / fed_ms, 1),
+            "step_bytes": int(step_bytes), "gb_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -350,9 +393,10 @@ def main():
     ap.add_argument("--no-real-formats", action="store_true", help="skip the real-model format line")
     ap.add_argument("--no-float-dots", action="store_true", help="skip the float-x row-dot timings")
     ap.add_argument("--no-microbench", action="store_true", help="skip the layer-shape operator microbench")
+    ap.add_argument("--no-qwen3", action="store_true", help="skip the Qwen3-1.7B-shape decode line")
     ap.add_argument("--kernel-iters", type=int, default=96, help="launches in each decode-kernel timing")
     ap.add_argument("--only", choices=["prefill", "long", "float-dots", "real-formats", "vocab", "microbench",
-                                       "kernels"],
+                                       "kernels", "qwen3"],
                     default=None,
                     help="run just the prefill reps or just the long-context decode (profiler runs); "
                          "prints their JSON object, not the bench line")
@@ -385,6 +429,12 @@ def main():
     if args.only == "real-formats":
         rdir = tempfile.mkdtemp(prefix="c2slm_bench_")
         print(json.dumps({"real_formats": real_formats(rdir, im_end, eos)}))
+        os.rmdir(rdir)
+        cleanup()
+        return
+    if args.only == "qwen3":
+        rdir = tempfile.mkdtemp(prefix="c2slm_bench_")
+        print(json.dumps({"qwen3_1_7b_decode": qwen3_decode(rdir, im_end, eos)}))
         os.rmdir(rdir)
         cleanup()
         return
@@ -480,6 +530,7 @@ def main():
     vocab_gbs = VOCAB_BYTES / (vocab_ms * 1e-3) / 1e9
     # per-kernel floor of dependent launches in a graph (empty kernels)
     floor_us = ctx.launch_floor(240, 256, 5)
+    floor_by_grid = {g: round(ctx.launch_floor(240, g, 5), 3) for g in (1, 64, 256, 1024, 4096)}
     if args.copy_calib_mib:
         copy_calibration(ctx, args.copy_calib_mib)
 
@@ -493,6 +544,12 @@ def main():
         if rdir != tmpdir:
             os.rmdir(rdir)
 
+    qwen3 = None
+    if not args.no_qwen3:
+        rdir = tmpdir or tempfile.mkdtemp(prefix="c2slm_bench_")
+        qwen3 = qwen3_decode(rdir, im_end, eos)
+        if rdir != tmpdir:
+            os.rmdir(rdir)
     fdots = None if args.no_float_dots else float_x_dots(ctx)
     micro = None if args.no_microbench else layer_microbench(ctx)
 
@@ -534,11 +591,13 @@ def main():
                   "vocab_ms_back_to_back": round(vocab_b2b_ms, 5),
                   "vocab_ms_in_step_events": round(vocab_step_ms, 5),
                   "launch_floor_us_per_kernel": round(floor_us, 3),
+                  "launch_floor_us_by_grid": floor_by_grid,
                   "pipelined_ms_per_step": round(pipelined_ms, 4),
                   "pipelined_tok_s": round(1000.0 / pipelined_ms, 1),
                   "prefill_512": prefill,
                   "long_context_decode": longctx,
                   "real_formats": realf,
+                  "qwen3_1_7b_decode": qwen3,
                   "float_x_dots": fdots},
     }
     print(json.dumps(line))
