@@ -75,6 +75,7 @@ struct c2h_ctx {
   bool use_graphs = true;
   size_t attn_lds = 0;
   int att_split = 0;     // positions attended up to which k_attn_core runs
+  int pfa_max_pos = 0;   // prefill passes ending at or below this many positions run k_pf_attn
   bool long_attn = false;
   float* att_sc = nullptr;  // [PF_ATT_SUB][n_heads][sc_ld] scores / probabilities
   float* att_bmax = nullptr;
@@ -1012,6 +1013,12 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
       for (const void* k : pff)
         if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, PF_F_LDS_MAX) != hipSuccess)
           return bail(fail(c, C2H_ERR_HIP, "prefill GEMM LDS attribute"));
+      // k_pf_attn keeps the scores of up to att_split positions per token in LDS
+      c->pfa_max_pos = c->att_split;
+      while (c->pfa_max_pos > 1 && (size_t)pfa_lds_floats(c->pfa_max_pos - 1) * 4 > 152u * 1024) --c->pfa_max_pos;
+      if (hipFuncSetAttribute((const void*)k_pf_attn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              pfa_lds_floats(c->pfa_max_pos - 1) * 4) != hipSuccess)
+        return bail(fail(c, C2H_ERR_HIP, "prefill attention LDS attribute"));
     }
     if (c->long_attn) {
       if (D.max_ctx > ATT_LONG_MAX_CTX)
@@ -1309,7 +1316,13 @@ int pf_pass(c2h_ctx* c, const int32_t* tokens, int m, int pos0) {
       A.kv_ld = KV;
       A.out_ld = E;
       A.store_kv = 0;
-      if (pos0 + m <= c->att_split) {
+      if (pos0 + m <= c->att_split && pos0 + m <= c->pfa_max_pos) {
+        // blocks of 16 query tokens per head, K/V chunks shared by the block
+        A.n_tok = m;
+        A.sc_ld = pfa_sc_ld(pos0 + m - 1);
+        hipLaunchKernelGGL(k_pf_attn, dim3(D.n_heads, (m + PFA_TB - 1) / PFA_TB), dim3(256),
+                           (size_t)pfa_lds_floats(pos0 + m - 1) * 4, c->stream, A);
+      } else if (pos0 + m <= c->att_split) {
         const size_t lds = (size_t)attn_lds_floats(pos0 + m) * 4;
         hipLaunchKernelGGL(k_attn_core<ATT_TIER_ANY>, dim3(D.n_heads / D.n_kv_heads, D.n_kv_heads, m), dim3(256), lds,
                            c->stream, A);

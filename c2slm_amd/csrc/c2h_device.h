@@ -8,7 +8,22 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace c2h {
+
+// f(std::integral_constant<int, i>) for i = 0..N-1, expanded in the source:
+// arrays indexed by i are promoted to registers even when they stay live
+// across a loop (an unrolled `for` can leave such an array in scratch memory).
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 constexpr int QK_K = 256;
 constexpr int BS_Q4K = 144;

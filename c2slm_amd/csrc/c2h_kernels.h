@@ -199,9 +199,22 @@ struct AttnCoreParams {
   // launch token i, block maxima bmax[(i*n_heads + h)*n_blk + b]
   float* sc;
   float* bmax;
-  int sc_ld;
+  int sc_ld;    // (k_pf_attn: the row stride of its LDS scores, pfa_sc_ld)
   int n_blk;
+  int n_tok;    // k_pf_attn: query tokens of the prefill pass
 };
+
+// Causal attention of a prefill pass (k_pf_attn): one workgroup per query
+// head and block of PFA_TB query tokens, K and V staged through LDS in
+// chunks of PFA_CH positions shared by the block's tokens.
+constexpr int PFA_TB = 16;
+constexpr int PFA_CH = 128;
+constexpr int PFA_KPAD = 68;  // floats per staged K row (64 + 4: conflict-free row reads)
+// Row stride (floats) of the block's scores for positions up to pmax.
+__host__ __device__ inline int pfa_sc_ld(int pmax) { return ((pmax + 1 + 63) & ~63) + 4; }
+// Dynamic LDS of k_pf_attn, in floats: K chunk (V chunk aliases it) | q of
+// the block's tokens | scores.
+__host__ __device__ inline int pfa_lds_floats(int pmax) { return PFA_CH * PFA_KPAD + PFA_TB * 64 + PFA_TB * pfa_sc_ld(pmax); }
 
 // Dynamic LDS of k_attn_h128 (head_dim 128), in floats: the scores of every
 // position up to max_ctx.
@@ -343,6 +356,7 @@ __global__ void k_attn_scores(AttnCoreParams P);
 __global__ void k_attn_softmax(AttnCoreParams P);
 __global__ void k_attn_av(AttnCoreParams P);
 __global__ void k_attn_h128(AttnCoreParams P);
+__global__ void k_pf_attn(AttnCoreParams P);
 template <int NB>
 __global__ void k_pf_norm_quant(PFNormParams P);
 template <int NB>

@@ -2164,6 +2164,208 @@ __global__ void __launch_bounds__(64) k_pf_rope_store(PFRopeParams P) {
   P.kv[(((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * head_stride + vq_index(pos, d)] = vr[d];
 }
 
+// Causal attention of a prefill pass: workgroup (query head h, block of
+// PFA_TB query tokens), token i at position pos0 + i attending positions
+// 0..pos0+i, all of whose K/V rows are in the cache.  Per (token, head) the
+// arithmetic is k_attn_core's, bit for bit:
+//   RoPE of q (tensor/ops.go:262-286);
+//   scores in the two-accumulator FMA order (attn_score), times scale;
+//   softmax (tensor/ops.go:317-339): the max of the non-NaN scores (NaN
+//     when score 0 is NaN), f32(exp(f64(s - max))), the exact sequential
+//     f32 sum, times f32(1/sum);
+//   per output dim one FMA chain over positions 0..pos in order
+//     (c2_tensor_attn_gen.go:85-117).
+// Sharing: the K rows of a PFA_CH-position chunk are read from the cache
+// once per block (coalesced, into LDS rows padded to PFA_KPAD floats) and
+// serve the block's 16 tokens; likewise the V quads.  Thread roles:
+//   scores     position c0 + (t % 128) of the chunk, tokens 8*(t/128)..+7;
+//   sums       lanes 0..15 of wave 0, one token each: the sequential sum is
+//              one dependent chain per token, so the 16 chains run side by
+//              side (lanes past a token's last position add +0, exactly);
+//   AV         dim t % 64 of tokens 4*(t/64)..+3: four independent chains.
+// (LDS limits a CU to two of these workgroups: two waves per SIMD, the VGPR budget of that occupancy)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) k_pf_attn(AttnCoreParams P) {
+  constexpr int HD = 64;
+  constexpr int KP = PFA_KPAD;
+  constexpr int KL = PFA_CH * 16 / 256;       // 16-byte K loads per thread and chunk
+  constexpr int VL = PFA_CH / 4 * 64 / 256;   // V quads per thread and chunk
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* kbuf = reinterpret_cast<float*>(smem);        // [PFA_CH][KP]   (scores phase)
+  f32x4_t* vbuf = reinterpret_cast<f32x4_t*>(smem);    // [PFA_CH/4][64] (AV phase)
+  float* q_s = kbuf + PFA_CH * KP;                     // [PFA_TB][64]
+  float* sc = q_s + PFA_TB * HD;                       // [PFA_TB][P.sc_ld]
+  __shared__ float red_m[4][8];
+  __shared__ float mx_s[PFA_TB], inv_s[PFA_TB];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int h = (int)blockIdx.x;
+  const int g = h / (P.n_heads / P.n_kv_heads);
+  const int t0 = (int)blockIdx.y * PFA_TB;
+  const int nt = min(PFA_TB, P.n_tok - t0);  // tokens of this block
+  const int ld = P.sc_ld;
+  const int pos0 = P.state->pos;
+  const int pmax = pos0 + t0 + nt - 1;       // last position the block attends
+  const size_t head_stride = (size_t)kv_slot(P.max_ctx) * HD;
+  const float* kcache = P.kv + ((size_t)P.layer * P.n_kv_heads + g) * head_stride;
+  const f32x4_t* vcache =
+      reinterpret_cast<const f32x4_t*>(P.kv + (((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * head_stride);
+  // A chunk's K rows / V quads are read 16 bytes per thread and load,
+  // coalesced; rows past pmax repeat row pmax (read, never used), so the
+  // loads of the chunk after the last are harmless and need no branch.
+
+  // ---- loads: q of the block's tokens, K chunk 0
+  float4 qv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  {
+    const int tk = tid >> 4, c = tid & 15;
+    if (tk < nt) qv = reinterpret_cast<const float4*>(P.q + (size_t)(t0 + tk) * P.q_ld + h * HD)[c];
+  }
+  f32x4_t kn[KL];  // native vectors: a float4 array copied whole is kept in scratch
+  static_for<KL>([&](auto k) {
+    const int i = tid + 256 * k;
+    kn[k] = reinterpret_cast<const f32x4_t*>(kcache + (size_t)min(i >> 4, pmax) * HD)[i & 15];
+  });
+  reinterpret_cast<float4*>(q_s)[tid] = qv;
+  __syncthreads();
+  {  // RoPE (pairs i, i+32) at each token's position
+    const int tk = tid >> 4;
+    const int pos = pos0 + t0 + tk;
+    if (tk < nt && pos >= 0 && pos < P.rope_len) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int i = (tid & 15) * 2 + e;
+        const float rc = P.rope_cos[(size_t)pos * (HD / 2) + i], rs = P.rope_sin[(size_t)pos * (HD / 2) + i];
+        float* qr = q_s + tk * HD;
+        const float x0 = qr[i], x1 = qr[i + 32];
+        qr[i] = (x0 * rc) - (x1 * rs);
+        qr[i + 32] = (x0 * rs) + (x1 * rc);
+      }
+    }
+  }
+
+  // ---- scores, chunk by chunk of K rows; the next chunk loads meanwhile
+  const int th = tid >> 7, pl = tid & 127;
+  float lmax[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) lmax[j] = -__builtin_inff();
+  for (int c0 = 0; c0 <= pmax; c0 += PFA_CH) {
+    __syncthreads();  // the previous chunk's rows are read (and, first time, q is turned)
+    static_for<KL>([&](auto k) {
+      const int i = tid + 256 * k;
+      reinterpret_cast<f32x4_t*>(kbuf + (i >> 4) * KP)[i & 15] = kn[k];
+    });
+    static_for<KL>([&](auto k) {  // the next chunk
+      const int i = tid + 256 * k;
+      kn[k] = reinterpret_cast<const f32x4_t*>(kcache + (size_t)min(c0 + PFA_CH + (i >> 4), pmax) * HD)[i & 15];
+    });
+    __syncthreads();
+    const int p = c0 + pl;
+    if (p <= pmax) {
+      float4 kk4[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) kk4[i] = reinterpret_cast<const float4*>(kbuf + pl * KP)[i];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int tk = th * 8 + j;
+        if (tk < nt && p <= pos0 + t0 + tk) {
+          const float sco = attn_score(q_s + tk * HD, kk4, P.scale);
+          sc[tk * ld + p] = sco;
+          lmax[j] = (sco > lmax[j]) ? sco : lmax[j];
+        }
+      }
+    }
+  }
+  // ---- max per token: waves 2th, 2th+1 hold tokens 8th..8th+7
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float m = wave_max_dpp(lmax[j]);
+    if (lane == 0) red_m[wave][j] = m;
+  }
+  __syncthreads();
+  if (tid < nt) {
+    const int w0 = 2 * (tid >> 3), j = tid & 7;
+    float m = fmax_gt(red_m[w0][j], red_m[w0 + 1][j]);
+    const float s0 = sc[tid * ld];
+    if (s0 != s0) m = s0;
+    mx_s[tid] = m;
+  }
+  __syncthreads();
+  // ---- exps
+  for (int tk = 0; tk < nt; ++tk) {
+    const float m = mx_s[tk];
+    for (int p = tid; p <= pos0 + t0 + tk; p += 256) sc[tk * ld + p] = (float)exp((double)(sc[tk * ld + p] - m));
+  }
+  f32x4_t vn[VL];  // V chunk 0 lands under the sums
+  static_for<VL>([&](auto k) {
+    const int i = tid + 256 * k;
+    vn[k] = vcache[(size_t)min(i >> 6, pmax >> 2) * 64 + (i & 63)];
+  });
+  __syncthreads();
+  // ---- sequential sums: lane tk of wave 0 runs token tk's chain (reads 16 ahead)
+  if (tid < 64) {
+    const int tk = min(lane, nt - 1);
+    const float s = chunk_chain(sc + tk * ld, 0, pos0 + t0 + tk + 1, 0.0f);
+    if (lane < nt) inv_s[lane] = 1.0f / s;
+  }
+  __syncthreads();
+  for (int tk = 0; tk < nt; ++tk) {
+    const float iv = inv_s[tk];
+    for (int p = tid; p <= pos0 + t0 + tk; p += 256) sc[tk * ld + p] = sc[tk * ld + p] * iv;
+  }
+
+  // ---- AV: four chains per thread (dim lane, tokens 4*wave..+3), V quads by chunk
+  const float4* sc4[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sc4[j] = reinterpret_cast<const float4*>(sc + min(wave * 4 + j, PFA_TB - 1) * ld);
+  const int last0 = pos0 + t0 + wave * 4;  // every token of the wave attends [0, last0]
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c0 = 0; c0 <= pmax; c0 += PFA_CH) {
+    __syncthreads();  // K rows (first time) / the previous V chunk are read
+    static_for<VL>([&](auto k) { vbuf[tid + 256 * k] = vn[k]; });
+    static_for<VL>([&](auto k) {  // the next chunk
+      const int i = tid + 256 * k;
+      vn[k] = vcache[(size_t)min(((c0 + PFA_CH) >> 2) + (i >> 6), pmax >> 2) * 64 + (i & 63)];
+    });
+    __syncthreads();
+    const int nq = min(PFA_CH, pmax + 1 - c0 + 3) >> 2;               // quads of the chunk up to pmax
+    const int nfull = max(min((last0 + 1 - c0) >> 2, nq), 0);          // quads all four tokens use whole
+    int qd = 0;
+    for (; qd + 4 <= nfull; qd += 4) {  // sixteen positions: every read issued before the FMAs
+      f32x4_t v[4];
+      float4 pr[4][4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[k] = vbuf[(qd + k) * 64 + lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pr[j][k] = sc4[j][(c0 >> 2) + qd + k];
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = fma4(acc[j], pr[j][k], v[k]);
+    }
+    for (; qd < nq; ++qd) {  // the rest, position by position against each token's last
+      const f32x4_t v = vbuf[qd * 64 + lane];
+      const int p = c0 + 4 * qd;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int last = last0 + j;
+        if (p <= last) {
+          const float4 pr = sc4[j][p >> 2];
+          acc[j] = __builtin_fmaf(pr.x, v.x, acc[j]);
+          if (p + 1 <= last) acc[j] = __builtin_fmaf(pr.y, v.y, acc[j]);
+          if (p + 2 <= last) acc[j] = __builtin_fmaf(pr.z, v.z, acc[j]);
+          if (p + 3 <= last) acc[j] = __builtin_fmaf(pr.w, v.w, acc[j]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int tk = wave * 4 + j;
+    if (tk < nt) P.out[(size_t)(t0 + tk) * P.out_ld + h * HD + lane] = acc[j];
+  }
+}
+
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 // One super-block of one weight row as the MFMA A operand needs it: lane
