@@ -258,45 +258,6 @@ __device__ __forceinline__ bool spec_round(float& S, float R, int& m, float& tot
   return false;
 }
 
-// n <= 1024: lane l owns [16l, 16l+16) in registers.  a: LDS readable up to
-// round_up(n, 16).
-__device__ __forceinline__ float seq_sum_wave(const float* a, int n) {
-  const int lane = threadIdx.x & 63;
-  const int base = lane * SPEC_C;
-  float v[SPEC_C];
-  {
-    const float4* a4 = reinterpret_cast<const float4*>(a + min(base, (n - 1) & ~(SPEC_C - 1)));
-#pragma unroll
-    for (int k = 0; k < SPEC_C / 4; ++k) {
-      const float4 t = a4[k];
-      v[4 * k + 0] = t.x;
-      v[4 * k + 1] = t.y;
-      v[4 * k + 2] = t.z;
-      v[4 * k + 3] = t.w;
-    }
-#pragma unroll
-    for (int k = 0; k < SPEC_C; ++k) v[k] = (base + k < n) ? v[k] : 0.0f;  // +0 adds are exact no-ops
-  }
-  float cs = 0.0f;
-#pragma unroll
-  for (int k = 0; k < SPEC_C; ++k) cs = cs + v[k];
-  float S = pin_full_wave(wave_shift_up(wave_incl_scan(cs)));
-  int m = -1;
-  float total;
-  for (int round = 0; round < SPEC_ROUNDS; ++round) {
-    float R = S;
-#pragma unroll
-    for (int k = 0; k < SPEC_C; ++k) R = R + v[k];
-    if (spec_round(S, R, m, total)) return total;
-  }
-  float s = lane_value(S, m + 1);
-  for (int i = (m + 1) * SPEC_C; i < n; ++i) s = s + a[i];
-  return s;
-}
-
-// The same exact sequential sum for any n >= 1 (softmax over long contexts):
-// lane l owns [l*C, l*C + C), C = ceil(n/64) rounded up to a multiple of 4,
-// and re-reads its chunk from LDS each round.  a: 16-byte aligned LDS.
 // Sequential adds of a[b0 .. b1) onto s; the LDS reads of the next 16
 // values are issued before the adds of the current 16, so the chain runs at
 // add latency.
@@ -334,6 +295,45 @@ __device__ __forceinline__ float chunk_chain(const float* a, int b0, int b1, flo
   return s;
 }
 
+
+// n <= 1024: lane l owns [16l, 16l+16) in registers.  a: LDS readable up to
+// round_up(n, 16).
+__device__ __forceinline__ float seq_sum_wave(const float* a, int n) {
+  const int lane = threadIdx.x & 63;
+  const int base = lane * SPEC_C;
+  float v[SPEC_C];
+  {
+    const float4* a4 = reinterpret_cast<const float4*>(a + min(base, (n - 1) & ~(SPEC_C - 1)));
+#pragma unroll
+    for (int k = 0; k < SPEC_C / 4; ++k) {
+      const float4 t = a4[k];
+      v[4 * k + 0] = t.x;
+      v[4 * k + 1] = t.y;
+      v[4 * k + 2] = t.z;
+      v[4 * k + 3] = t.w;
+    }
+#pragma unroll
+    for (int k = 0; k < SPEC_C; ++k) v[k] = (base + k < n) ? v[k] : 0.0f;  // +0 adds are exact no-ops
+  }
+  float cs = 0.0f;
+#pragma unroll
+  for (int k = 0; k < SPEC_C; ++k) cs = cs + v[k];
+  float S = pin_full_wave(wave_shift_up(wave_incl_scan(cs)));
+  int m = -1;
+  float total;
+  for (int round = 0; round < SPEC_ROUNDS; ++round) {
+    float R = S;
+#pragma unroll
+    for (int k = 0; k < SPEC_C; ++k) R = R + v[k];
+    if (spec_round(S, R, m, total)) return total;
+  }
+  // the rest in order from the last exact start, reads issued 16 ahead
+  return chunk_chain(a, (m + 1) * SPEC_C, n, lane_value(S, m + 1));
+}
+
+// The same exact sequential sum for any n >= 1 (softmax over long contexts):
+// lane l owns [l*C, l*C + C), C = ceil(n/64) rounded up to a multiple of 4,
+// and re-reads its chunk from LDS each round.  a: 16-byte aligned LDS.
 __device__ __forceinline__ float seq_sum_wave_n(const float* a, int n) {
   const int lane = threadIdx.x & 63;
   const int C = (((n + 63) >> 6) + 3) & ~3;
