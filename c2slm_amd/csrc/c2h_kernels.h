@@ -153,7 +153,8 @@ __host__ __device__ inline size_t vq_index(int p, int d, int hd = 64) {
 //     head and 16-dim slice: two waves run the FMA chains of all the group's
 //     query heads, the others stage the V slice through LDS).
 constexpr int ATT_CH = 128;   // V positions staged in LDS per pass (chunk 0 prefetched)
-constexpr int ATT_KPF = 256;  // positions whose K row is prefetched (one per thread)
+constexpr int ATT_KPF = 256;  // K rows per LDS chunk of the scores (one per thread)
+constexpr int ATT_KPAD = 68;  // floats per staged K row (64 + 4: conflict-free row reads)
 // k_attn_core instances by the context they prefetch for: up to 128 and up
 // to 256 positions attended (the prefetch covers all of K and V), or any
 // context up to the split length.
@@ -220,8 +221,13 @@ __host__ __device__ inline int pfa_lds_floats(int pmax) { return PFA_CH * PFA_KP
 // position up to max_ctx.
 __host__ __device__ inline int attn_h128_lds_floats(int max_ctx) { return chain_lds_floats(max_ctx); }
 
-// Dynamic LDS of k_attn_core, in floats: two staged V chunks | scores.
-__host__ __device__ inline int attn_lds_floats(int max_ctx) { return 2 * ATT_CH * 64 + chain_lds_floats(max_ctx); }
+// Dynamic LDS of k_attn_core, in floats: the staged K rows of the scores
+// (ATT_KPF padded rows), which the two staged V chunks of the AV chains
+// later reuse | the scores.
+__host__ __device__ constexpr int attn_kv_lds_floats() {
+  return ATT_KPF * ATT_KPAD > 2 * ATT_CH * 64 ? ATT_KPF * ATT_KPAD : 2 * ATT_CH * 64;
+}
+__host__ __device__ inline int attn_lds_floats(int max_ctx) { return attn_kv_lds_floats() + chain_lds_floats(max_ctx); }
 // Dynamic LDS of k_attn_softmax (exps of up to max_ctx positions) and of
 // k_attn_av (two chunks of V quads and probabilities), in floats.
 __host__ __device__ inline int attn_softmax_lds_floats(int max_ctx) { return (max_ctx + 3) & ~3; }

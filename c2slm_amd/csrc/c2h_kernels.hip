@@ -1275,10 +1275,13 @@ __device__ __forceinline__ float attn_score(const float* q_s, const float4 (&kk4
 //   softmax with f64 exp and a sequential f32 sum (tensor/ops.go:317-339),
 //   and one FMA chain over positions per output dim
 //   (c2_tensor_attn_gen.go:85-117) with V staged through LDS.
-// Every load (q/k/v, RoPE row, the K rows of positions tid and tid+256, the
-// V rows of the first ATT_CH positions) is issued at entry.  Past the first
-// chunk, waves 1..3 stage V chunk by chunk (three chunks in flight in
-// registers, two in LDS) while wave 0 runs the chains.
+// Every load (q/k/v, RoPE row, the first chunk of K rows, the V rows of the
+// first ATT_CH positions) is issued at entry.  K rows are read in chunks of
+// ATT_KPF positions, coalesced (a wave reads 1 KB contiguous per load), into
+// LDS rows padded to ATT_KPAD floats; thread t scores the chunk's position t
+// from its LDS row while the next chunk loads.  Past the first V chunk,
+// waves 1..3 stage V chunk by chunk (three chunks in flight in registers,
+// two in LDS) while wave 0 runs the chains.
 template <int PER>
 struct VStage {
   f32x4_t r[PER];
@@ -1291,8 +1294,9 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   constexpr int VPT = NQ / 4;       // quads of chunk 0 per wave
   constexpr int PER = (NQ + 2) / 3;  // quads per staging wave (waves 1..3)
   extern __shared__ __align__(16) unsigned char smem[];
-  f32x4_t* vbuf = reinterpret_cast<f32x4_t*>(smem);               // [2][NQ][64] quad-major
-  float* sc = reinterpret_cast<float*>(vbuf + 2 * NQ * HD);       // [chain_lds_floats(split)]
+  f32x4_t* vbuf = reinterpret_cast<f32x4_t*>(smem);              // [2][NQ][64] quad-major (softmax, AV)
+  float* kbuf = reinterpret_cast<float*>(smem);                  // [ATT_KPF][ATT_KPAD] K rows (scores)
+  float* sc = reinterpret_cast<float*>(smem) + attn_kv_lds_floats();  // [chain_lds_floats(split)]
   __shared__ __align__(16) float qkv_s[3][HD];
   __shared__ float red_m[4];
   __shared__ float inv_slot;
@@ -1331,44 +1335,19 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   const float rcos = P.rope_cos[(size_t)rp * (HD / 2) + (tid & 31)];
   const float rsin = P.rope_sin[(size_t)rp * (HD / 2) + (tid & 31)];
   issue_fence();  // q/k/v and the RoPE row are needed first: issue them first
-  // The prefetch is sized to the tier's context (every thread issues the
-  // same loads, so the compiler's memory-counter waits stay exact):
-  //   ATT_TIER_128: waves 0-1 hold K rows 0..127, waves 2-3 V quads 0..31
-  //                 (V chunk 0);
-  //   ATT_TIER_256: K rows 0..255 and V quads 0..63 (chunks 0 and 1, both
-  //                 LDS buffers);
-  //   ATT_TIER_ANY: K rows 0..511 and V chunk 0, later rows and V chunks
-  //                 streamed.
+  // K chunk 0, coalesced: 16-byte piece i = tid + 256k of the chunk is row
+  // i/16, columns 4(i%16)..+3 (ATT_TIER_128 reads the 128 rows it can need);
+  // V chunk 0 (ATT_TIER_256: chunks 0 and 1): wave w holds quads w + 4i.
+  // Rows past the stored context read zeros at no cost (buffer bounds).
+  constexpr int KL = (TIER == ATT_TIER_128) ? 8 : 16;           // K pieces per thread and chunk
   constexpr int VQW = (TIER == ATT_TIER_256) ? 2 * VPT : VPT;  // V quads per wave
   const int wave = tid >> 6;
-  float4 kreg[16], kreg2[16];
-  f32x4_t vreg[VQW];  // native vectors: a float4 array copied whole is kept in scratch
-  if constexpr (TIER == ATT_TIER_128) {
-    const int uw = __builtin_amdgcn_readfirstlane(wave);
-    const bool kw = uw < 2;
-    const __amdgpu_buffer_rsrc_t rs = kw ? krs : vrs;
+  f32x4_t kc[KL];  // native vectors: a float4 array copied whole is kept in scratch
+  f32x4_t vreg[VQW];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int off = kw ? tid * HD * 4 + i * 16 : (((uw - 2) + 2 * i) * 64 + (tid & 63)) * 16;
-      const f32x4_t t = cache_ld4(rs, off);
-      kreg[i] = make_float4(t.x, t.y, t.z, t.w);
-    }
-  } else {
+  for (int k = 0; k < KL; ++k) kc[k] = cache_ld4(krs, (tid + 256 * k) * 16);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const f32x4_t t = cache_ld4(krs, tid * HD * 4 + i * 16);
-      kreg[i] = make_float4(t.x, t.y, t.z, t.w);
-    }
-    if constexpr (TIER == ATT_TIER_ANY) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const f32x4_t t = cache_ld4(krs, (tid + ATT_KPF) * HD * 4 + i * 16);
-        kreg2[i] = make_float4(t.x, t.y, t.z, t.w);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < VQW; ++i) vreg[i] = vquad_load_buf(vrs, wave + 4 * i);
-  }
+  for (int i = 0; i < VQW; ++i) vreg[i] = vquad_load_buf(vrs, wave + 4 * i);
   issue_fence();
 
   if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;
@@ -1395,40 +1374,34 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   }
   if (T > P.max_ctx) return;  // rejected on the host; kept as a guard
 
-  // ---- scores; position pos uses this launch's k (not yet visible in the cache)
-  // (both prefetched rows are consumed on every path: a load left pending
-  // on one path would make the compiler wait for all later loads before
-  // reusing its registers)
+  // ---- scores, chunk by chunk of K rows; position pos uses this launch's k
+  // (not yet visible in the cache)
   const float4* ks4 = reinterpret_cast<const float4*>(k_s);
   float lmax = -__builtin_inff();
-  {
-    if (tid == pos) {
+  for (int c0 = 0; c0 < T; c0 += ATT_KPF) {  // one chunk below 257 positions
+    if (c0 > 0) __syncthreads();              // the previous chunk's rows are read
 #pragma unroll
-      for (int i = 0; i < 16; ++i) kreg[i] = ks4[i];
+    for (int k = 0; k < KL; ++k) {
+      const int i = tid + 256 * k;
+      *reinterpret_cast<f32x4_t*>(kbuf + (i >> 4) * ATT_KPAD + 4 * (i & 15)) = kc[k];
     }
-    const float sco = attn_score(q_s, kreg, P.scale);
-    if (tid < T) sc[tid] = sco;
-    lmax = (tid < T && sco > lmax) ? sco : lmax;
-  }
-  if constexpr (TIER == ATT_TIER_ANY) {
-    const int p2 = tid + ATT_KPF;
-    if (p2 == pos) {
+    if (TIER == ATT_TIER_ANY && c0 + ATT_KPF < T) {  // the next chunk loads under this one's scores
 #pragma unroll
-      for (int i = 0; i < 16; ++i) kreg2[i] = ks4[i];
+      for (int k = 0; k < KL; ++k) kc[k] = cache_ld4(krs, (c0 + ATT_KPF) * HD * 4 + (tid + 256 * k) * 16);
     }
-    const float sco = attn_score(q_s, kreg2, P.scale);
-    if (p2 < T) sc[p2] = sco;
-    lmax = (p2 < T && sco > lmax) ? sco : lmax;
-  }
-  for (int p = tid + 2 * ATT_KPF; TIER == ATT_TIER_ANY && p < T; p += ATT_KPF) {
-    const float4* kr = (p == pos) ? ks4 : reinterpret_cast<const float4*>(kcache + (size_t)p * HD);
-    float4 kk4[16];
+    __syncthreads();
+    const int p = c0 + tid;
+    if (p < T) {
+      float4 kk4[16];
+      const float4* kr = (p == pos) ? ks4 : reinterpret_cast<const float4*>(kbuf + tid * ATT_KPAD);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) kk4[i] = kr[i];
-    const float sco = attn_score(q_s, kk4, P.scale);
-    sc[p] = sco;
-    lmax = (sco > lmax) ? sco : lmax;
+      for (int i = 0; i < 16; ++i) kk4[i] = kr[i];
+      const float sco = attn_score(q_s, kk4, P.scale);
+      sc[p] = sco;
+      lmax = (sco > lmax) ? sco : lmax;
+    }
   }
+  // (softmax's first barrier comes before V chunk 0 takes the K rows' LDS)
 
   // softmax, then V chunk 0 from registers into LDS buffer 0
   auto softmax = [&]() {
@@ -1450,19 +1423,8 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
       const float ssum = seq_sum_wave_n(sc, T);
       if (tid == 0) inv_slot = 1.0f / ssum;
     }
-    if constexpr (TIER == ATT_TIER_128) {
-      if (wave >= 2) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float4 t = kreg[i];
-          f32x4_t q4 = {t.x, t.y, t.z, t.w};
-          vbuf[((wave - 2) + 2 * i) * HD + (tid & 63)] = q4;
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < VQW; ++i) vbuf[(wave + 4 * i) * HD + (tid & 63)] = vreg[i];
-    }
+    for (int i = 0; i < VQW; ++i) vbuf[(wave + 4 * i) * HD + (tid & 63)] = vreg[i];
     __syncthreads();
     const float inv = inv_slot;
     for (int p = tid; p < T; p += blockDim.x) sc[p] = sc[p] * inv;
