@@ -1436,7 +1436,7 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   const int d = tid & 63;
   if (TIER != ATT_TIER_ANY || nch <= 1) {  // V[0, pos) already in LDS
     softmax();
-    if (tid < HD && pos > 0) acc = av_chain_q(sc, vbuf, pos, d, acc);
+    if (tid < HD && pos > 0) acc = (TIER == ATT_TIER_ANY) ? av_chain_q3<64>(sc, vbuf, pos, d, acc) : av_chain_q(sc, vbuf, pos, d, acc);
   } else {
     // Chunk c sits in LDS buffer c & 1; chunk c+1 waits in register set
     // c % 3.  Chunks 1..3 start loading under the softmax.  Every thread
@@ -1485,7 +1485,7 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
     } else {
       for (int c = 0; c < nch; ++c) {
         const int np = min(ATT_CH, pos - c * ATT_CH);
-        acc = av_chain_q(sc + c * ATT_CH, vbuf + (c & 1) * NQ * HD, np, d, acc);
+        acc = av_chain_q3<64>(sc + c * ATT_CH, vbuf + (c & 1) * NQ * HD, np, d, acc);
         __syncthreads();
       }
     }
