@@ -68,9 +68,10 @@ struct c2h_ctx {
   int32_t* tok_host = nullptr;     // pinned
   unsigned ring_next = 0;
 
-  // graphs by attention form (AttnForm): k_attn_core for up to 128, up to
-  // 256 and up to att_split positions, the long-context kernels beyond
-  hipGraphExec_t g_step[4] = {}, g_fwd[4] = {};
+  // graphs by attention form (attn_form): k_attn_core's tiers of 32, 64,
+  // 96, 128 and 256 positions, its any tier up to att_split positions, the
+  // long-context kernels beyond
+  hipGraphExec_t g_step[7] = {}, g_fwd[7] = {};
   bool graphs_ready = false;
   bool use_graphs = true;
   size_t attn_lds = 0;
@@ -576,25 +577,39 @@ void enqueue_attn_long(c2h_ctx* c, const AttnCoreParams& A, int ntok) {
 }
 
 // Attention forms of a decode step by the positions T it attends to:
-// k_attn_core sized for T <= 128, T <= 256, T <= att_split, and the
-// long-context kernels past the split.
-enum : int { ATT_FORM_128 = 0, ATT_FORM_256 = 1, ATT_FORM_CORE = 2, ATT_FORM_LONG = 3, ATT_FORMS = 4 };
+// k_attn_core sized for T <= 32, 64, 96, 128, 256 (the tiers), for
+// T <= att_split, and the long-context kernels past the split.
+enum : int {
+  ATT_FORM_32 = 0, ATT_FORM_64, ATT_FORM_96, ATT_FORM_128, ATT_FORM_256, ATT_FORM_CORE, ATT_FORM_LONG, ATT_FORMS
+};
+constexpr int kFormTier[ATT_FORM_CORE] = {ATT_TIER_32, ATT_TIER_64, ATT_TIER_96, ATT_TIER_128, ATT_TIER_256};
+static_assert(sizeof(c2h_ctx::g_step) / sizeof(hipGraphExec_t) == ATT_FORMS, "one graph per attention form");
 
 int attn_form(const c2h_ctx* c, int T) {
-  if (c->desc.head_dim == 128) return ATT_FORM_128;  // k_attn_h128 serves every T
+  if (c->desc.head_dim == 128) return ATT_FORM_32;  // k_attn_h128 serves every T
   if (c->long_attn && T > c->att_split) return ATT_FORM_LONG;
-  return T <= 128 ? ATT_FORM_128 : (T <= 256 ? ATT_FORM_256 : ATT_FORM_CORE);
+  for (int f = 0; f < ATT_FORM_CORE; ++f)
+    if (T <= kFormTier[f]) return f;
+  return ATT_FORM_CORE;
 }
 
 // Whether some decode position of this context runs the form.
 bool form_used(const c2h_ctx* c, int form) {
-  if (c->desc.head_dim == 128) return form == ATT_FORM_128;
+  if (c->desc.head_dim == 128) return form == ATT_FORM_32;
   const int tmax = c->long_attn ? c->att_split : c->desc.max_ctx;  // largest T of the core forms
+  if (form == ATT_FORM_LONG) return c->long_attn;
+  return form == 0 || tmax > kFormTier[form - 1];
+}
+
+// The k_attn_core instance of a core form.
+decltype(&k_attn_core<ATT_TIER_ANY>) attn_core_kernel(int form) {
   switch (form) {
-    case ATT_FORM_128: return true;
-    case ATT_FORM_256: return tmax > 128;
-    case ATT_FORM_CORE: return tmax > 256;
-    default: return c->long_attn;
+    case ATT_FORM_32: return k_attn_core<ATT_TIER_32>;
+    case ATT_FORM_64: return k_attn_core<ATT_TIER_64>;
+    case ATT_FORM_96: return k_attn_core<ATT_TIER_96>;
+    case ATT_FORM_128: return k_attn_core<ATT_TIER_128>;
+    case ATT_FORM_256: return k_attn_core<ATT_TIER_256>;
+    default: return k_attn_core<ATT_TIER_ANY>;
   }
 }
 
@@ -658,12 +673,11 @@ void enqueue_attn(c2h_ctx* c, int l, int form) {
     hipLaunchKernelGGL(k_attn_h128, grid, dim3(256), c->attn_lds, c->stream, A);
   else if (form == ATT_FORM_LONG)
     enqueue_attn_long(c, A, 1);
-  else if (form == ATT_FORM_128)
-    hipLaunchKernelGGL(k_attn_core<ATT_TIER_128>, grid, dim3(256), c->attn_lds, c->stream, A);
-  else if (form == ATT_FORM_256)
-    hipLaunchKernelGGL(k_attn_core<ATT_TIER_256>, grid, dim3(256), c->attn_lds, c->stream, A);
-  else
-    hipLaunchKernelGGL(k_attn_core<ATT_TIER_ANY>, grid, dim3(256), c->attn_lds, c->stream, A);
+  else {
+    A.xcd_map = D.n_kv_heads <= ATT_XCDS ? 1 : 0;
+    const dim3 xgrid(ATT_XCDS * (D.n_heads / D.n_kv_heads));
+    hipLaunchKernelGGL(attn_core_kernel(form), A.xcd_map ? xgrid : grid, dim3(256), c->attn_lds, c->stream, A);
+  }
 }
 
 // attn_out: X += Wo * x(attn)
@@ -1004,10 +1018,9 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
     c->long_attn = D.max_ctx > c->att_split;
     c->attn_lds = (size_t)attn_lds_floats(c->att_split) * 4;
     {
-      const void* cores[] = {(const void*)k_attn_core<ATT_TIER_128>, (const void*)k_attn_core<ATT_TIER_256>,
-                             (const void*)k_attn_core<ATT_TIER_ANY>};
-      for (const void* k : cores)
-        if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->attn_lds) != hipSuccess)
+      for (int form = 0; form <= ATT_FORM_CORE; ++form)
+        if (hipFuncSetAttribute((const void*)attn_core_kernel(form), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)c->attn_lds) != hipSuccess)
           return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
       const void* pff[] = {(const void*)k_pf_gemm_f<MODE_BIAS>, (const void*)k_pf_gemm_f<MODE_RESID>};
       for (const void* k : pff)

@@ -75,6 +75,7 @@ struct GemvJob {
   int rpw;       // rows per workgroup = floor(256 / (4*nb))
   int n_wg;      // workgroups of this job (grid row blockIdx.y = job)
   int mode;
+  int spare;     // (unused: named so that the fields load as one scalar batch)
   float* y;
   const float* bias;
   int32_t* isums;  // optional integer sums (Q4_K: 8 per row-block; Q6_K: 1)
@@ -155,13 +156,21 @@ __host__ __device__ inline size_t vq_index(int p, int d, int hd = 64) {
 constexpr int ATT_CH = 128;   // V positions staged in LDS per pass (chunk 0 prefetched)
 constexpr int ATT_KPF = 256;  // K rows per LDS chunk of the scores (one per thread)
 constexpr int ATT_KPAD = 68;  // floats per staged K row (64 + 4: conflict-free row reads)
-// k_attn_core instances by the context they prefetch for: up to 128 and up
-// to 256 positions attended (the prefetch covers all of K and V), or any
-// context up to the split length.
+// k_attn_core instances by the context they prefetch for: a tier of N
+// positions serves T <= N positions attended and reads the first N rows of
+// K and of V whole (a CU's loads issue at ~32-44 B/clk whether or not a
+// row lies past the stored context, so the tiers step by 32 rows); the any
+// tier serves any context up to the split length, K in chunks of ATT_KPF.
 constexpr int ATT_TIER_ANY = 0;
-constexpr int ATT_TIER_128 = 1;
-constexpr int ATT_TIER_256 = 2;
-__host__ __device__ inline int attn_tier(int T) { return T <= 128 ? ATT_TIER_128 : (T <= 256 ? ATT_TIER_256 : ATT_TIER_ANY); }
+constexpr int ATT_TIER_32 = 32;
+constexpr int ATT_TIER_64 = 64;
+constexpr int ATT_TIER_96 = 96;
+constexpr int ATT_TIER_128 = 128;
+constexpr int ATT_TIER_256 = 256;
+__host__ __device__ inline int attn_tier(int T) {
+  return T <= 32 ? ATT_TIER_32 : T <= 64 ? ATT_TIER_64 : T <= 96 ? ATT_TIER_96 : T <= 128 ? ATT_TIER_128
+         : T <= 256 ? ATT_TIER_256 : ATT_TIER_ANY;
+}
 constexpr int ATT_SPLIT_T = 1024;  // default split length (positions attended)
 constexpr int ATT_SB = 256;        // positions per k_attn_scores workgroup
 constexpr int ATT_AV_CH = 256;     // positions per k_attn_av LDS chunk
@@ -203,7 +212,14 @@ struct AttnCoreParams {
   int sc_ld;    // (k_pf_attn: the row stride of its LDS scores, pfa_sc_ld)
   int n_blk;
   int n_tok;    // k_pf_attn: query tokens of the prefill pass
+  // k_attn_core: 1 = the grid is (ATT_XCDS * qpkv, 1, tokens), n_kv_heads
+  // <= ATT_XCDS, and workgroup L serves KV head L % ATT_XCDS, query head
+  // L / ATT_XCDS, so the workgroups of one KV head share an XCD and its L2
+  // (workgroups go to the XCDs round robin); the workgroups left over exit
+  // at once.  0 = the grid is (qpkv, n_kv_heads, tokens).
+  int xcd_map;
 };
+constexpr int ATT_XCDS = 8;
 
 // Causal attention of a prefill pass (k_pf_attn): one workgroup per query
 // head and block of PFA_TB query tokens, K and V staged through LDS in

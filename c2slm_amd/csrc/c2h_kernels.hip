@@ -639,8 +639,8 @@ __device__ __forceinline__ GemvJob launch_job(const GemvParams& P) {
   GemvJob J = P.jobs[blockIdx.y];
   asm volatile(""
                : "+s"(J.type), "+s"(J.type2), "+s"(J.rows), "+s"(J.nb), "+s"(J.rpw), "+s"(J.n_wg), "+s"(J.mode)
-               : "s"(J.w.q), "s"(J.w.d), "s"(J.w2.q), "s"(J.w2.d), "s"(J.y), "s"(J.bias), "s"(J.isums), "s"(P.x),
-                 "s"(P.norm_w), "s"(P.n_x), "s"(P.eps));
+               : "s"(J.spare), "s"(J.w.q), "s"(J.w.d), "s"(J.w2.q), "s"(J.w2.d), "s"(J.y), "s"(J.bias), "s"(J.isums),
+                 "s"(P.x), "s"(P.norm_w), "s"(P.n_x), "s"(P.eps));
   return J;
 }
 
@@ -1217,6 +1217,21 @@ __device__ __forceinline__ float av_chain_q(const float* p, const f32x4_t* vq, i
   return av_tail_q([&](int i) { return p4[i >> 2]; }, vq, nb * 16, n, d, acc);
 }
 
+// The chain over nb whole batches of sixteen positions (callers pad the
+// probabilities and V with zeros past the last position).
+__device__ __forceinline__ float av_chain_pad(const float* p, const f32x4_t* vq, int nb, int d, float acc) {
+  const float4* p4 = reinterpret_cast<const float4*>(p);
+  return av_batches(
+      [&](int b, f32x4_t(&v)[4], float4(&pp)[4]) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          v[k] = vq[(4 * b + k) * 64 + d];
+          pp[k] = p4[4 * b + k];
+        }
+      },
+      nb, acc);
+}
+
 // Quad qi of a head slot's V (positions 4qi..4qi+3, all dims, 1 KB):
 // lane l's 16 bytes are dim l.
 __device__ __forceinline__ f32x4_t vquad_load(const float* vslot, int qi) {
@@ -1275,13 +1290,19 @@ __device__ __forceinline__ float attn_score(const float* q_s, const float4 (&kk4
 //   softmax with f64 exp and a sequential f32 sum (tensor/ops.go:317-339),
 //   and one FMA chain over positions per output dim
 //   (c2_tensor_attn_gen.go:85-117) with V staged through LDS.
-// Every load (q/k/v, RoPE row, the first chunk of K rows, the V rows of the
-// first ATT_CH positions) is issued at entry.  K rows are read in chunks of
-// ATT_KPF positions, coalesced (a wave reads 1 KB contiguous per load), into
-// LDS rows padded to ATT_KPAD floats; thread t scores the chunk's position t
-// from its LDS row while the next chunk loads.  Past the first V chunk,
-// waves 1..3 stage V chunk by chunk (three chunks in flight in registers,
-// two in LDS) while wave 0 runs the chains.
+// Every load (q/k/v, the RoPE row, the first chunk of K rows, the first V
+// rows: the tier's, or the first ATT_CH positions) is issued at entry.  A
+// tier reads whole batches of its rows, so that its issue time (a CU issues
+// ~32-44 B/clk, rows past the stored context included) follows the
+// context in steps of 32 positions.  K rows are read in chunks of ATT_KPF
+// positions, coalesced (a wave reads 1 KB contiguous per load), into LDS rows
+// padded to ATT_KPAD floats; thread t scores the chunk's position t from its
+// LDS row while the next chunk loads.  A tier's chain runs whole batches of
+// sixteen positions: past pos its V rows are zeroed in LDS and its
+// probabilities are zero, and each such step, fma(p, 0, acc), returns acc
+// unchanged (acc starts at +0 and an fma never turns it into -0).  Past the
+// first V chunk (the any tier), waves 1..3 stage V chunk by chunk (three
+// chunks in flight in registers, two in LDS) while wave 0 runs the chains.
 template <int PER>
 struct VStage {
   f32x4_t r[PER];
@@ -1290,6 +1311,8 @@ struct VStage {
 template <int TIER>
 __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   constexpr int HD = 64;
+  constexpr bool ANY = (TIER == ATT_TIER_ANY);
+  static_assert(ANY || (TIER % 32 == 0 && TIER <= ATT_KPF), "a tier reads whole batches of K and V rows");
   constexpr int NQ = ATT_CH / 4;    // quads (four V rows) per chunk
   constexpr int VPT = NQ / 4;       // quads of chunk 0 per wave
   constexpr int PER = (NQ + 2) / 3;  // quads per staging wave (waves 1..3)
@@ -1301,16 +1324,22 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   __shared__ float red_m[4];
   __shared__ float inv_slot;
 
-  const int tid = threadIdx.x;
-  // grid (query heads per KV head, KV heads, query tokens of the batch)
-  const int qpkv = (int)gridDim.x;
-  const int g = (int)blockIdx.y;
-  const int h = g * qpkv + (int)blockIdx.x;
-  const int ti = P.tok0 + (int)blockIdx.z;  // query token of the batch (0 in decode)
   // the launch's fields in one scalar batch (not a chain of round trips)
   asm volatile("" ::"s"(P.q), "s"(P.k), "s"(P.v), "s"(P.kv), "s"(P.state), "s"(P.rope_cos), "s"(P.rope_sin),
                "s"(P.q_ld), "s"(P.kv_ld), "s"(P.tok0), "s"(P.layer), "s"(P.n_layers), "s"(P.n_kv_heads),
-               "s"(P.max_ctx), "s"(P.rope_len));
+               "s"(P.max_ctx), "s"(P.rope_len), "s"(P.xcd_map), "s"(gridDim.x));
+  const int tid = threadIdx.x;
+  // grid (query heads per KV head, KV heads, query tokens of the batch), or
+  // the XCD-grouped order of xcd_map (at most ATT_XCDS KV heads)
+  int qpkv = (int)gridDim.x, g = (int)blockIdx.y, hx = (int)blockIdx.x;
+  if (P.xcd_map) {
+    qpkv = (int)gridDim.x / ATT_XCDS;
+    g = (int)blockIdx.x % ATT_XCDS;
+    hx = (int)blockIdx.x / ATT_XCDS;
+    if (g >= P.n_kv_heads) return;  // uniform: a spare workgroup of the grid
+  }
+  const int h = g * qpkv + hx;
+  const int ti = P.tok0 + (int)blockIdx.z;  // query token of the batch (0 in decode)
   // this head's q and the group's k, v: thread t < 192 holds element t%64
   // of q_h (t < 64), k_g, v_g.  Issued before the position is read.
   const int bm = min(tid >> 6, 2);
@@ -1326,7 +1355,8 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   float* vcache = P.kv + (((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * head_stride;
   const int nstored = max(min(pos, P.max_ctx), 0);    // cached positions [0, nstored)
   const int nch = (pos + ATT_CH - 1) / ATT_CH;         // V chunks of positions [0, pos)
-  // the stored rows as buffers: prefetch slots past them read zeros for free
+  // the stored rows as buffers: prefetch slots past them read zeros without
+  // memory traffic
   const __amdgpu_buffer_rsrc_t krs = cache_rsrc(kcache, nstored * HD * 4);
   const __amdgpu_buffer_rsrc_t vrs = cache_rsrc(vcache, ((nstored + 3) >> 2) * HD * 16);
 
@@ -1336,11 +1366,10 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   const float rsin = P.rope_sin[(size_t)rp * (HD / 2) + (tid & 31)];
   issue_fence();  // q/k/v and the RoPE row are needed first: issue them first
   // K chunk 0, coalesced: 16-byte piece i = tid + 256k of the chunk is row
-  // i/16, columns 4(i%16)..+3 (ATT_TIER_128 reads the 128 rows it can need);
-  // V chunk 0 (ATT_TIER_256: chunks 0 and 1): wave w holds quads w + 4i.
-  // Rows past the stored context read zeros at no cost (buffer bounds).
-  constexpr int KL = (TIER == ATT_TIER_128) ? 8 : 16;           // K pieces per thread and chunk
-  constexpr int VQW = (TIER == ATT_TIER_256) ? 2 * VPT : VPT;  // V quads per wave
+  // i/16, columns 4(i%16)..+3 (a tier reads its TIER rows); V: wave w holds
+  // quads w + 4i of the tier's rows, or of chunk 0.
+  constexpr int KL = ANY ? ATT_KPF / 16 : TIER / 16;  // K pieces per thread and chunk
+  constexpr int VQW = ANY ? VPT : TIER / 16;          // V quads per wave
   const int wave = tid >> 6;
   f32x4_t kc[KL];  // native vectors: a float4 array copied whole is kept in scratch
   f32x4_t vreg[VQW];
@@ -1368,7 +1397,7 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   __syncthreads();
 
   // (a batch of query tokens has its K/V stored by a kernel before this one)
-  if (P.store_kv && blockIdx.x == 0 && tid < HD && pos < P.max_ctx) {
+  if (P.store_kv && hx == 0 && tid < HD && pos < P.max_ctx) {
     kcache[(size_t)pos * HD + tid] = k_s[tid];
     vcache[vq_index(pos, tid)] = v_s[tid];
   }
@@ -1385,7 +1414,7 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
       const int i = tid + 256 * k;
       *reinterpret_cast<f32x4_t*>(kbuf + (i >> 4) * ATT_KPAD + 4 * (i & 15)) = kc[k];
     }
-    if (TIER == ATT_TIER_ANY && c0 + ATT_KPF < T) {  // the next chunk loads under this one's scores
+    if (ANY && c0 + ATT_KPF < T) {  // the next chunk loads under this one's scores
 #pragma unroll
       for (int k = 0; k < KL; ++k) kc[k] = cache_ld4(krs, (c0 + ATT_KPF) * HD * 4 + (tid + 256 * k) * 16);
     }
@@ -1402,6 +1431,7 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
     }
   }
   // (softmax's first barrier comes before V chunk 0 takes the K rows' LDS)
+  const int nbat = (pos + 15) >> 4;  // a tier's whole batches of sixteen positions
 
   // softmax, then V chunk 0 from registers into LDS buffer 0
   auto softmax = [&]() {
@@ -1424,19 +1454,34 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
       if (tid == 0) inv_slot = 1.0f / ssum;
     }
 #pragma unroll
-    for (int i = 0; i < VQW; ++i) vbuf[(wave + 4 * i) * HD + (tid & 63)] = vreg[i];
+    for (int i = 0; i < VQW; ++i) {
+      f32x4_t vv = vreg[i];
+      if (!ANY) {  // positions pos and past (stale or zero rows) -> 0
+        const int p0 = 4 * (wave + 4 * i);
+        vv.x = (p0 < pos) ? vv.x : 0.0f;
+        vv.y = (p0 + 1 < pos) ? vv.y : 0.0f;
+        vv.z = (p0 + 2 < pos) ? vv.z : 0.0f;
+        vv.w = (p0 + 3 < pos) ? vv.w : 0.0f;
+      }
+      vbuf[(wave + 4 * i) * HD + (tid & 63)] = vv;
+    }
     __syncthreads();
     const float inv = inv_slot;
     for (int p = tid; p < T; p += blockDim.x) sc[p] = sc[p] * inv;
+    if (!ANY)
+      for (int p = T + tid; p < 16 * nbat; p += blockDim.x) sc[p] = 0.0f;
     __syncthreads();
   };
 
   // ---- AV: out[d] = fma chain over p of (prob[p], V[p][d]); V[pos] is v_s.
   float acc = 0.0f;
   const int d = tid & 63;
-  if (TIER != ATT_TIER_ANY || nch <= 1) {  // V[0, pos) already in LDS
+  if (!ANY) {  // V[0, pos) in LDS, zero rows up to the batch end
     softmax();
-    if (tid < HD && pos > 0) acc = (TIER == ATT_TIER_ANY) ? av_chain_q3<64>(sc, vbuf, pos, d, acc) : av_chain_q(sc, vbuf, pos, d, acc);
+    if (tid < HD && nbat > 0) acc = av_chain_pad(sc, vbuf, nbat, d, acc);
+  } else if (nch <= 1) {
+    softmax();
+    if (tid < HD && pos > 0) acc = av_chain_q3<64>(sc, vbuf, pos, d, acc);
   } else {
     // Chunk c sits in LDS buffer c & 1; chunk c+1 waits in register set
     // c % 3.  Chunks 1..3 start loading under the softmax.  Every thread
@@ -1495,6 +1540,9 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
     P.out[(size_t)ti * P.out_ld + h * HD + d] = acc;
   }
 }
+template __global__ void k_attn_core<ATT_TIER_32>(AttnCoreParams);
+template __global__ void k_attn_core<ATT_TIER_64>(AttnCoreParams);
+template __global__ void k_attn_core<ATT_TIER_96>(AttnCoreParams);
 template __global__ void k_attn_core<ATT_TIER_128>(AttnCoreParams);
 template __global__ void k_attn_core<ATT_TIER_256>(AttnCoreParams);
 template __global__ void k_attn_core<ATT_TIER_ANY>(AttnCoreParams);

@@ -2,7 +2,7 @@
 
 `build` writes an instrumented copy of the kernel sources into
 c2slm_amd/_build/phase/ with `s_memtime` stamps at the phase boundaries of
-k_gemv_row (qkv, attn_out, ffn_in, ffn_out) and k_attn_core<ATT_TIER_128>,
+k_gemv_row (qkv, attn_out, ffn_in, ffn_out) and the tiers of k_attn_core,
 and links it as c2slm_amd/libc2h_phase.so (same C ABI plus
 c2h_phase_read).  Lane 0 of every wave of the first and the last workgroup
 of each launch stores its stamp per phase into a device array; every later
@@ -26,13 +26,13 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 OUT_LIB = os.path.join(HERE, "libc2h_phase.so")
-N_WAVES, N_SLOTS = 8, 12
+N_WAVES, N_SLOTS = 8, 16
 GEMV_KINDS = ["qkv", "attn_out", "ffn_in", "ffn_out"]
 GEMV_PHASES = ["entry", "args", "issued", "x", "norm_end", "quant", "w", "items", "end", "norm_start"]
-ATTN_PHASES = ["entry", "args", "issued", "qkv", "rope", "scores", "softmax", "av", "end"]
+ATTN_PHASES = ["entry", "args", "issued", "qkv", "rope", "scores", "softmax", "av", "end", "pos", "k_in", "v_in", "max", "exp", "sum"]
 
 _STAMPS = r"""namespace c2h {
-__device__ long long g_phase[5][2][8][12];
+__device__ long long g_phase[5][2][8][16];
 template <int NB, int PRO, int MODE>
 __device__ __forceinline__ int phase_kind() {
   return (PRO == PRO_NORM && MODE == MODE_BIAS)                 ? 0
@@ -44,10 +44,11 @@ __device__ __forceinline__ int phase_kind() {
 #define PH_G(k) do { const int kd_ = phase_kind<NB, PRO, MODE>(); \
   if (kd_ >= 0 && (threadIdx.x & 63) == 0 && blockIdx.y == 0 && (blockIdx.x == 0 || blockIdx.x == gridDim.x - 1)) \
     g_phase[kd_][blockIdx.x == 0 ? 0 : 1][threadIdx.x >> 6][k] = __builtin_amdgcn_s_memtime(); } while (0)
-#define PH_A(k) do { const bool f_ = blockIdx.x == 0 && blockIdx.y == 0; \
-  const bool l_ = blockIdx.x == gridDim.x - 1 && blockIdx.y == gridDim.y - 1; \
-  if (TIER == ATT_TIER_128 && (threadIdx.x & 63) == 0 && blockIdx.z == 0 && (f_ || l_)) \
-    g_phase[4][f_ ? 0 : 1][threadIdx.x >> 6][k] = __builtin_amdgcn_s_memtime(); } while (0)
+#define PH_AT(k, t) do { const bool f_ = h == 0; \
+  const bool l_ = h == P.n_heads - 1; \
+  if (TIER != ATT_TIER_ANY && (threadIdx.x & 63) == 0 && blockIdx.z == 0 && (f_ || l_)) \
+    g_phase[4][f_ ? 0 : 1][threadIdx.x >> 6][k] = (t); } while (0)
+#define PH_A(k) PH_AT(k, __builtin_amdgcn_s_memtime())
 """
 
 
@@ -82,9 +83,23 @@ def instrument(kernels: str) -> str:
                     "  PH_G(7);\n  // ---- per-row fold in the reference's order, then the epilogue\n"),
                ]).replace("PH_END;", "PH_G(8);", 1)
     s = _patch(s, "template <int TIER>\n__global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {",
-               "template __global__ void k_attn_core<ATT_TIER_128>(AttnCoreParams);", [
-                   ("  const int tid = threadIdx.x;\n  // grid", "  PH_A(0);\n  const int tid = threadIdx.x;\n  // grid"),
-                   ('"s"(P.max_ctx), "s"(P.rope_len));\n', '"s"(P.max_ctx), "s"(P.rope_len));\n  PH_A(1);\n'),
+               "template __global__ void k_attn_core<ATT_TIER_32>(AttnCoreParams);", [
+                   ("  // the launch's fields in one scalar batch (not a chain of round trips)\n  asm volatile",
+                    "  const long long ph_entry_ = __builtin_amdgcn_s_memtime();\n"
+                    "  // the launch's fields in one scalar batch (not a chain of round trips)\n  asm volatile"),
+                   ('"s"(P.xcd_map), "s"(gridDim.x));\n', '"s"(P.xcd_map), "s"(gridDim.x));\n'
+                    '  const long long ph_args_ = __builtin_amdgcn_s_memtime();\n'),
+                   ("  const int h = g * qpkv + hx;\n", "  const int h = g * qpkv + hx;\n  PH_AT(0, ph_entry_);\n"
+                    "  PH_AT(1, ph_args_);\n"),
+                   ("  const int T = pos + 1;\n", "  asm volatile(\"\" ::\"s\"(pos));\n  PH_A(9);\n  const int T = pos + 1;\n"),
+                   ("    __syncthreads();\n    const int p = c0 + tid;\n",
+                    "    PH_A(10);\n    __syncthreads();\n    const int p = c0 + tid;\n"),
+                   ("    __syncthreads();\n    const float inv = inv_slot;\n",
+                    "    PH_A(11);\n    __syncthreads();\n    const float inv = inv_slot;\n"),
+                   ("    if (sc[0] != sc[0]) mx = sc[0];\n    for (int p = tid; p < T; p += blockDim.x) sc[p] = (float)exp((double)(sc[p] - mx));\n    __syncthreads();\n",
+                    "    if (sc[0] != sc[0]) mx = sc[0];\n    PH_A(12);\n    for (int p = tid; p < T; p += blockDim.x) sc[p] = (float)exp((double)(sc[p] - mx));\n    __syncthreads();\n    PH_A(13);\n"),
+                   ("#pragma unroll\n    for (int i = 0; i < VQW; ++i) {\n      f32x4_t vv = vreg[i];",
+                    "    PH_A(14);\n#pragma unroll\n    for (int i = 0; i < VQW; ++i) {\n      f32x4_t vv = vreg[i];"),
                    ("  issue_fence();\n\n  if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;\n  __syncthreads();\n",
                     "  issue_fence();\n  PH_A(2);\n\n  if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;\n"
                     "  __syncthreads();\n  PH_A(3);\n"),
@@ -92,17 +107,17 @@ def instrument(kernels: str) -> str:
                     "  __syncthreads();\n  PH_A(4);\n\n  // (a batch of query tokens"),
                    ("  // softmax, then V chunk 0 from registers into LDS buffer 0\n",
                     "  PH_A(5);\n  // softmax, then V chunk 0 from registers into LDS buffer 0\n"),
-                   ("    softmax();\n    if (tid < HD && pos > 0) acc = av_chain_q(sc, vbuf, pos, d, acc);\n",
-                    "    softmax();\n    PH_A(6);\n    if (tid < HD && pos > 0) acc = av_chain_q(sc, vbuf, pos, d, acc);\n"
+                   ("    softmax();\n    if (tid < HD && nbat > 0) acc = av_chain_pad(sc, vbuf, nbat, d, acc);\n",
+                    "    softmax();\n    PH_A(6);\n    if (tid < HD && nbat > 0) acc = av_chain_pad(sc, vbuf, nbat, d, acc);\n"
                     "    PH_A(7);\n"),
                ]).replace("PH_END;", "PH_A(8);", 1)
     return s
 
 
 _READER = r"""
-namespace c2h { extern __device__ long long g_phase[5][2][8][12]; }
+namespace c2h { extern __device__ long long g_phase[5][2][8][16]; }
 extern "C" int c2h_phase_read(long long* out) {
-  return hipMemcpyFromSymbol(out, HIP_SYMBOL(c2h::g_phase), sizeof(long long) * 5 * 2 * 8 * 12) == hipSuccess ? 0 : -1;
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(c2h::g_phase), sizeof(long long) * 5 * 2 * 8 * 16) == hipSuccess ? 0 : -1;
 }
 """
 
