@@ -387,10 +387,11 @@ void launch_gemv_f(c2h_ctx* c, GemvParams& P) {
 // A row-kernel launch over all its jobs (same width and mode); the norm
 // prologues need the x*x chain buffer.
 void launch_gemv_row(c2h_ctx* c, GemvParams& P) {
-  const int nt = row_threads(P.jobs[0].nb, P.prologue);
+  const int nt = row_threads(P.jobs[0].nb, P.prologue, P.jobs[0].mode);
+  const int ni = row_item_threads(P.jobs[0].nb, P.prologue, P.jobs[0].mode);
   for (int j = 0; j < P.n_jobs; ++j) {  // rows per workgroup at this width
     GemvJob& J = P.jobs[j];
-    J.rpw = nt / (4 * J.nb);
+    J.rpw = ni / (4 * J.nb);
     J.n_wg = (J.rows + J.rpw - 1) / J.rpw;
   }
   const GemvJob& J = P.jobs[0];

@@ -88,9 +88,16 @@ constexpr int MAX_JOBS = 4;
 // quantise at most three per wave with two waves per SIMD, and the
 // workgroup takes twice the rows, which halves the redundant quantisations.
 // The norm prologues hold one float4 of x per thread, so rows of more than
-// 1024 values (up to 2048) run on 8 waves as well.
-__host__ __device__ constexpr int row_threads(int nb, int pro) {
-  return ((pro == PRO_QUANT && nb >= 12) || (pro >= PRO_NORM && nb > 4)) ? 512 : 256;
+// 1024 values (up to 2048) run on 8 waves as well.  The SwiGLU pair of
+// narrow rows (up to 4 super-blocks) runs on 8 waves with the gate items on
+// the first half and the up items on the second, one item per thread.
+__host__ __device__ constexpr int row_threads(int nb, int pro, int mode) {
+  return ((pro == PRO_QUANT && nb >= 12) || (pro >= PRO_NORM && nb > 4) || (mode == MODE_SWIGLU && nb <= 4)) ? 512
+                                                                                                            : 256;
+}
+// Threads holding the items of one matrix (rows per workgroup = this / (4 nb)).
+__host__ __device__ constexpr int row_item_threads(int nb, int pro, int mode) {
+  return (mode == MODE_SWIGLU && nb <= 4) ? row_threads(nb, pro, mode) / 2 : row_threads(nb, pro, mode);
 }
 
 struct GemvParams {

@@ -58,17 +58,17 @@ __device__ __forceinline__ ArgCand wave_argmax(ArgCand c) {
 // ------------------------------------------------------------- Q8_K (A1)
 
 // One quant of internal/simd/c2_quantize_q8_k_gen.go:58-74 in a block with
-// amax != 0: q = int(x*isc ± 0.5) clamped to ±127.  The ± 0.5 is a copysign
-// (tq = -0 then gives -0.5 where the reference adds +0.5; both truncate to
-// 0).  Go's conversion truncates, and turns NaN and |r| >= 2^63 into
-// INT64_MIN, -127 after the clamp: the float clamp already sends NaN and
-// r <= -2^63 there, the compare catches r >= 2^63 (only reached with an
-// infinite isc, from an amax below 127/FLT_MAX).
+// a finite isc: q = int(x*isc ± 0.5) clamped to ±127 (|x*isc| <= 127 up to
+// rounding).  The ± 0.5 is a copysign (tq = -0 then gives -0.5 where the
+// reference adds +0.5; both truncate to 0), Go's conversion truncates, and
+// a NaN x goes to -127 through the clamp, as Go's NaN -> INT64_MIN does.
+// A block whose amax is below 127/FLT_MAX has isc = +Inf: x*isc is then
+// +-Inf or NaN for every x, which Go turns into INT64_MIN, so the block is
+// all -127 (quantize_blocks selects that per block).
 __device__ __forceinline__ int quant1(float x, float isc) {
   const float tq = x * isc;
   const float r = tq + __builtin_copysignf(0.5f, tq);
-  const int q = (int)fminf(fmaxf(r, -127.0f), 127.0f);
-  return (r < 9223372036854775808.0f) ? q : -127;
+  return (int)fminf(fmaxf(r, -127.0f), 127.0f);
 }
 
 // d = amax/127 rounded once: the product with RN(1/127) corrected by its
@@ -127,11 +127,12 @@ __device__ __forceinline__ void quantize_blocks(const float4 (&v)[BPW], int b0, 
   for (int i = 0; i < BPW; ++i) {
     const int q0 = quant1(v[i].x, isc[i]), q1 = quant1(v[i].y, isc[i]);
     const int q2 = quant1(v[i].z, isc[i]), q3 = quant1(v[i].w, isc[i]);
-    const bool live = (m[i] != 0.0f);  // a zero block quantises to zeros
-    packed[i] = live ? ((uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
-                        ((uint32_t)(q3 & 0xff) << 24))
-                     : 0u;
-    bsum[i] = live ? (q0 + q1) + (q2 + q3) : 0;
+    const bool live = (m[i] != 0.0f);         // a zero block quantises to zeros
+    const bool inf_isc = (isc[i] == __builtin_inff());  // all -127 (see quant1)
+    const uint32_t pk = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+                        ((uint32_t)(q3 & 0xff) << 24);
+    packed[i] = live ? (inf_isc ? 0x81818181u : pk) : 0u;
+    bsum[i] = live ? (inf_isc ? -4 * 127 : (q0 + q1) + (q2 + q3)) : 0;
   }
 #pragma unroll
   for (int i = 0; i < BPW; ++i) bsum[i] += dpp0_i<DPP_QUAD_1032>(bsum[i]);
@@ -749,13 +750,16 @@ __device__ __forceinline__ GemvJob launch_job(const GemvParams& P) {
 // read the same block of the Q8_K row (broadcast, no bank conflicts).  The
 // fold runs per row in the reference's order.
 template <int NB, int PRO, int MODE>
-__global__ void __launch_bounds__(row_threads(NB, PRO)) k_gemv_row(GemvParams P) {
-  constexpr int NT = row_threads(NB, PRO);
+__global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(GemvParams P) {
+  constexpr int NT = row_threads(NB, PRO, MODE);
+  constexpr int NI = row_item_threads(NB, PRO, MODE);  // threads per matrix's items
   constexpr int NW = NT / 64;
   constexpr int IPR = 4 * NB;
-  constexpr int RPW = NT / IPR;
+  constexpr int RPW = NI / IPR;
   constexpr int BPW = (NB + NW - 1) / NW;  // Q8_K blocks quantised per wave
   constexpr bool PAIRED = (MODE == MODE_SWIGLU);
+  constexpr bool SPLIT = PAIRED && NI < NT;  // gate items on threads [0, NI), up items on [NI, 2 NI)
+  static_assert(!SPLIT || (NI & (NI - 1)) == 0, "the split takes the item index modulo NI");
   constexpr bool NORM = (PRO == PRO_NORM || PRO == PRO_EMBED_NORM || PRO == PRO_ARGMAX_EMBED_NORM);
   static_assert(!NORM || NB <= NW, "the norm prologue holds one float4 per thread, one block per wave");
   extern __shared__ __align__(16) unsigned char smem[];
@@ -769,9 +773,11 @@ __global__ void __launch_bounds__(row_threads(NB, PRO)) k_gemv_row(GemvParams P)
   if ((int)blockIdx.x >= J.n_wg) return;  // uniform: the launch's widest job sets the grid
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  const int b = tid / (4 * RPW);
-  const int r_local = (tid - b * 4 * RPW) >> 2;
-  const int u = tid & 3;
+  const int it = SPLIT ? (tid & (NI - 1)) : tid;  // item index within its matrix
+  const int half = SPLIT ? tid / NI : 0;           // 0: gate (w), 1: up (w2); wave-uniform
+  const int b = it / (4 * RPW);
+  const int r_local = (it - b * 4 * RPW) >> 2;
+  const int u = it & 3;
   const int row0 = (int)blockIdx.x * RPW;
   const int row = row0 + r_local;
   const bool active = (b < NB) && (row < J.rows);
@@ -795,9 +801,10 @@ __global__ void __launch_bounds__(row_threads(NB, PRO)) k_gemv_row(GemvParams P)
       xa[i] = reinterpret_cast<const float4*>(P.x + min(wave + NW * i, NB - 1) * QK_K)[lane];
   }
   if (NORM) nw = load4(P.norm_w, P.n_x);
-  const ItemW w1 = load_item(J.w, J.type, NB, row_c, b_c, u);
+  const int type1 = (SPLIT && half) ? J.type2 : J.type;
+  const ItemW w1 = load_item((SPLIT && half) ? J.w2 : J.w, type1, NB, row_c, b_c, u);
   ItemW w2;
-  if (PAIRED) w2 = load_item(J.w2, J.type2, NB, row_c, b_c, u);
+  if (PAIRED && !SPLIT) w2 = load_item(J.w2, J.type2, NB, row_c, b_c, u);
   float yres = 0.0f;
   if (MODE == MODE_RESID) yres = J.y[out_row];
   // an absent bias reads x instead (a valid address) and is not added
@@ -824,8 +831,9 @@ __global__ void __launch_bounds__(row_threads(NB, PRO)) k_gemv_row(GemvParams P)
 
   // ---- items
   if (active) {
-    store_item(&terms[0][r_local * IPR], J.type, b, u, item_value(w1, J.type, s, b, u));
-    if (PAIRED) store_item(&terms[PAIRED ? 1 : 0][r_local * IPR], J.type2, b, u, item_value(w2, J.type2, s, b, u));
+    store_item(&terms[PAIRED ? half : 0][r_local * IPR], type1, b, u, item_value(w1, type1, s, b, u));
+    if (PAIRED && !SPLIT)
+      store_item(&terms[PAIRED ? 1 : 0][r_local * IPR], J.type2, b, u, item_value(w2, J.type2, s, b, u));
   }
   __syncthreads();
 

@@ -67,7 +67,7 @@ def _patch(text: str, start: str, end: str, edits) -> str:
 
 def instrument(kernels: str) -> str:
     s = kernels.replace("namespace c2h {\n", _STAMPS, 1)
-    s = _patch(s, "__global__ void __launch_bounds__(row_threads(NB, PRO)) k_gemv_row(GemvParams P) {",
+    s = _patch(s, "__global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(GemvParams P) {",
                "#define C2H_GEMV_ROW(NB_, PRO_, MODE_)", [
                    ("  const GemvJob J = launch_job(P);", "  PH_G(0);\n  const GemvJob J = launch_job(P);"),
                    ("  if ((int)blockIdx.x >= J.n_wg) return;  // uniform: the launch's widest job sets the grid\n",
