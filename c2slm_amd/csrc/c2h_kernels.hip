@@ -665,12 +665,15 @@ __device__ __forceinline__ float fold_terms(int type, const float* row_terms) {
 
 // ------------------------------------------------------------- prologues
 
-// Argmax over the vocab kernel's per-workgroup candidates.
+// Argmax over the vocab kernel's per-workgroup candidates, by a workgroup of
+// NT threads (a constant: blockDim.x would be one more scalar load to wait
+// for before the first candidate load).
+template <int NT>
 __device__ int reduce_argmax_partials(const float* __restrict__ pv, const int* __restrict__ pi, int n, ArgCand* red) {
   ArgCand c;
   c.v = -__builtin_inff();
   c.i = 0x7fffffff;
-  for (int k = threadIdx.x; k < n; k += blockDim.x) {
+  for (int k = threadIdx.x; k < n; k += NT) {
     ArgCand t;
     t.v = pv[k];
     t.i = pi[k];
@@ -682,7 +685,7 @@ __device__ int reduce_argmax_partials(const float* __restrict__ pv, const int* _
   __syncthreads();
   if (threadIdx.x == 0) {
     ArgCand r = red[0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = arg_better(r, red[w]);
+    for (int w = 1; w < NT / 64; ++w) r = arg_better(r, red[w]);
     red[0] = r;
   }
   __syncthreads();
@@ -792,7 +795,7 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(GemvPar
   if (PRO == PRO_NORM) {
     xa[0] = load4(P.x, P.n_x);
   } else if (NORM) {  // layer 0: the token's embedding row
-    tok = (PRO == PRO_ARGMAX_EMBED_NORM) ? reduce_argmax_partials(P.part_v, P.part_i, P.n_part, ared)
+    tok = (PRO == PRO_ARGMAX_EMBED_NORM) ? reduce_argmax_partials<NT>(P.part_v, P.part_i, P.n_part, ared)
                                          : P.state->token;
     xa[0] = embed4(P.emb, P.n_vocab, P.n_x, tok);
   } else {
@@ -1074,7 +1077,7 @@ __global__ void __launch_bounds__(256) k_gemv_f(GemvParams P) {
   if (PRO == PRO_NORM) {
     xa = load4(P.x, P.n_x);
   } else if (NORM) {
-    tok = (PRO == PRO_ARGMAX_EMBED_NORM) ? reduce_argmax_partials(P.part_v, P.part_i, P.n_part, ared)
+    tok = (PRO == PRO_ARGMAX_EMBED_NORM) ? reduce_argmax_partials<256>(P.part_v, P.part_i, P.n_part, ared)
                                          : P.state->token;
     xa = embed4(P.emb, P.n_vocab, P.n_x, tok);
   }
@@ -1426,10 +1429,13 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   __shared__ float red_m[4];
   __shared__ float inv_slot;
 
-  // the launch's fields in one scalar batch (not a chain of round trips)
+  // the launch's fields in one scalar batch (not a chain of round trips;
+  // and a scalar load still in flight would make every later LDS wait,
+  // which shares its counter, wait for memory too)
   asm volatile("" ::"s"(P.q), "s"(P.k), "s"(P.v), "s"(P.kv), "s"(P.state), "s"(P.rope_cos), "s"(P.rope_sin),
                "s"(P.q_ld), "s"(P.kv_ld), "s"(P.tok0), "s"(P.layer), "s"(P.n_layers), "s"(P.n_kv_heads),
-               "s"(P.max_ctx), "s"(P.rope_len), "s"(P.xcd_map), "s"(gridDim.x));
+               "s"(P.max_ctx), "s"(P.rope_len), "s"(P.xcd_map), "s"(gridDim.x), "s"(P.out), "s"(P.out_ld),
+               "s"(P.scale), "s"(P.store_kv));
   const int tid = threadIdx.x;
   // grid (query heads per KV head, KV heads, query tokens of the batch), or
   // the XCD-grouped order of xcd_map (at most ATT_XCDS KV heads)
@@ -1544,7 +1550,7 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
     __syncthreads();
     float mx = fmax_gt(fmax_gt(fmax_gt(red_m[0], red_m[1]), red_m[2]), red_m[3]);
     if (sc[0] != sc[0]) mx = sc[0];
-    for (int p = tid; p < T; p += blockDim.x) sc[p] = (float)exp((double)(sc[p] - mx));
+    for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));
     __syncthreads();
     if (T <= 64 * SPEC_C) {
       if (tid < 64) {
@@ -1569,9 +1575,9 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
     }
     __syncthreads();
     const float inv = inv_slot;
-    for (int p = tid; p < T; p += blockDim.x) sc[p] = sc[p] * inv;
+    for (int p = tid; p < T; p += 256) sc[p] = sc[p] * inv;
     if (!ANY)
-      for (int p = T + tid; p < 16 * nbat; p += blockDim.x) sc[p] = 0.0f;
+      for (int p = T + tid; p < 16 * nbat; p += 256) sc[p] = 0.0f;
     __syncthreads();
   };
 
@@ -1708,6 +1714,11 @@ __global__ void __launch_bounds__(256) k_attn_h128(AttnCoreParams P) {
   __shared__ float red_m[4];
   __shared__ float inv_s[3];
 
+  // the launch's fields in one scalar batch (see k_attn_core)
+  asm volatile("" ::"s"(P.q), "s"(P.k), "s"(P.v), "s"(P.q_norm), "s"(P.k_norm), "s"(P.eps), "s"(P.out),
+               "s"(P.q_ld), "s"(P.kv_ld), "s"(P.out_ld), "s"(P.store_kv), "s"(P.kv), "s"(P.rope_cos),
+               "s"(P.rope_sin), "s"(P.rope_len), "s"(P.layer), "s"(P.n_layers), "s"(P.n_kv_heads), "s"(P.max_ctx),
+               "s"(P.scale), "s"(P.state), "s"(P.tok0), "s"(gridDim.x));
   const int tid = threadIdx.x;
   const int qpkv = (int)gridDim.x;
   const int g = (int)blockIdx.y;
@@ -2918,7 +2929,7 @@ C2H_VOCAB(64)  // Qwen3-1.7B: 2048 columns
 // Final reduction for standalone argmax calls (no following layer kernel).
 __global__ void __launch_bounds__(256) k_argmax_final(const float* pv, const int* pi, int n, C2hState* state) {
   __shared__ ArgCand red[4];
-  int tok = reduce_argmax_partials(pv, pi, n, red);
+  int tok = reduce_argmax_partials<256>(pv, pi, n, red);
   if (threadIdx.x == 0) state->token = tok;
 }
 

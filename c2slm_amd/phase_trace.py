@@ -84,10 +84,10 @@ def instrument(kernels: str) -> str:
                ]).replace("PH_END;", "PH_G(8);", 1)
     s = _patch(s, "template <int TIER>\n__global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {",
                "template __global__ void k_attn_core<ATT_TIER_32>(AttnCoreParams);", [
-                   ("  // the launch's fields in one scalar batch (not a chain of round trips)\n  asm volatile",
-                    "  const long long ph_entry_ = __builtin_amdgcn_s_memtime();\n"
-                    "  // the launch's fields in one scalar batch (not a chain of round trips)\n  asm volatile"),
-                   ('"s"(P.xcd_map), "s"(gridDim.x));\n', '"s"(P.xcd_map), "s"(gridDim.x));\n'
+                   ('  asm volatile("" ::"s"(P.q), "s"(P.k), "s"(P.v), "s"(P.kv),',
+                    '  const long long ph_entry_ = __builtin_amdgcn_s_memtime();\n'
+                    '  asm volatile("" ::"s"(P.q), "s"(P.k), "s"(P.v), "s"(P.kv),'),
+                   ('"s"(P.scale), "s"(P.store_kv));\n', '"s"(P.scale), "s"(P.store_kv));\n'
                     '  const long long ph_args_ = __builtin_amdgcn_s_memtime();\n'),
                    ("  const int h = g * qpkv + hx;\n", "  const int h = g * qpkv + hx;\n  PH_AT(0, ph_entry_);\n"
                     "  PH_AT(1, ph_args_);\n"),
@@ -96,8 +96,8 @@ def instrument(kernels: str) -> str:
                     "    PH_A(10);\n    __syncthreads();\n    const int p = c0 + tid;\n"),
                    ("    __syncthreads();\n    const float inv = inv_slot;\n",
                     "    PH_A(11);\n    __syncthreads();\n    const float inv = inv_slot;\n"),
-                   ("    if (sc[0] != sc[0]) mx = sc[0];\n    for (int p = tid; p < T; p += blockDim.x) sc[p] = (float)exp((double)(sc[p] - mx));\n    __syncthreads();\n",
-                    "    if (sc[0] != sc[0]) mx = sc[0];\n    PH_A(12);\n    for (int p = tid; p < T; p += blockDim.x) sc[p] = (float)exp((double)(sc[p] - mx));\n    __syncthreads();\n    PH_A(13);\n"),
+                   ("    if (sc[0] != sc[0]) mx = sc[0];\n    for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));\n    __syncthreads();\n",
+                    "    if (sc[0] != sc[0]) mx = sc[0];\n    PH_A(12);\n    for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));\n    __syncthreads();\n    PH_A(13);\n"),
                    ("#pragma unroll\n    for (int i = 0; i < VQW; ++i) {\n      f32x4_t vv = vreg[i];",
                     "    PH_A(14);\n#pragma unroll\n    for (int i = 0; i < VQW; ++i) {\n      f32x4_t vv = vreg[i];"),
                    ("  issue_fence();\n\n  if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;\n  __syncthreads();\n",
