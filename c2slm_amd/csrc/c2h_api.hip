@@ -65,7 +65,8 @@ struct c2h_ctx {
   float* logits = nullptr;
   C2hState* state_dev = nullptr;
   C2hState* state_ring = nullptr;  // pinned
-  int32_t* tok_host = nullptr;     // pinned
+  int32_t* tok_host = nullptr;     // pinned: {token, seq} written by a step's layer 0
+  unsigned step_seq = 0;           // last step number handed to the device
   unsigned ring_next = 0;
 
   // graphs by attention form (attn_form): k_attn_core's tiers of 32, 64,
@@ -637,6 +638,7 @@ void launch_group(c2h_ctx* c, std::initializer_list<ProjJob> jobs, int pro, int 
       if (float_input(j.w->type) == (kind == 1)) add_job(P, *j.w, j.w2, mode, j.y, j.bias, nullptr);
     if (P.n_jobs == 0) continue;
     P.prologue = (!first && (pro == PRO_EMBED_NORM || pro == PRO_ARGMAX_EMBED_NORM)) ? PRO_NORM : pro;
+    if (P.prologue == PRO_ARGMAX_EMBED_NORM) P.tok_out = c->tok_host;
     P.x = x;
     P.x_out = c->X;
     P.n_x = n_x;
@@ -929,6 +931,8 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   if (hipHostMalloc(&pinned, sizeof(C2hState) * kStateRing + 64, hipHostMallocDefault) != hipSuccess) return bail(C2H_ERR_HIP);
   c->state_ring = reinterpret_cast<C2hState*>(pinned);
   c->tok_host = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(pinned) + sizeof(C2hState) * kStateRing);
+  c->tok_host[0] = 0;
+  c->tok_host[1] = -1;
   int rc;
   if ((rc = noalloc_setup(c))) return bail(rc);
   if ((rc = dalloc(c, &c->state_dev, sizeof(C2hState)))) return bail(rc);
@@ -1469,15 +1473,32 @@ int c2h_step(c2h_ctx* c, int32_t pos, float penalty, int32_t im_end, int32_t eos
   s.penalty = penalty;
   s.nx_in = c->nx_cur;
   s.nx_out = c->nx_cur ^ 1;
+  s.seq = (int32_t)(++c->step_seq % 0x7ffffffeu) + 1;  // never 0 (other launches) or -1 (initial)
   if ((rc = push_state(c, s))) return rc;
   if ((rc = run_graph(c, true, pos))) return rc;
   c->nx_prev = c->nx_cur;
   c->nx_cur ^= 1;
   c->seq_len = pos + 1;
-  HIPCHK(c, hipMemcpyAsync(c->tok_host, &c->state_dev->token, 4, hipMemcpyDeviceToHost, c->stream));
-  HIPCHK(c, hipStreamSynchronize(c->stream));
-  if (next_token) *next_token = *c->tok_host;
-  return C2H_OK;
+  // The token is the argmax layer 0 takes at the start of the step: it
+  // arrives in pinned memory (with s.seq) while the forward of that token
+  // still runs, and everything that later reads the step's results is
+  // ordered after it on the stream.  If the stream stops without it (an
+  // error), the stream's status is reported.
+  const volatile int32_t* tk = c->tok_host;
+  for (unsigned spin = 1;; ++spin) {
+    if (__atomic_load_n(&tk[1], __ATOMIC_ACQUIRE) == s.seq) {
+      if (next_token) *next_token = tk[0];
+      return C2H_OK;
+    }
+    if ((spin & 1023u) == 0u) {
+      const hipError_t q = hipStreamQuery(c->stream);
+      if (q != hipErrorNotReady && __atomic_load_n(&tk[1], __ATOMIC_ACQUIRE) != s.seq) {
+        HIPCHK(c, hipStreamSynchronize(c->stream));
+        if (q != hipSuccess) return fail(c, C2H_ERR_HIP, "step: %s", hipGetErrorString(q));
+        return fail(c, C2H_ERR_HIP, "step %d ended without handing over its token", s.seq);
+      }
+    }
+  }
 }
 
 int c2h_restore_normx(c2h_ctx* c) {

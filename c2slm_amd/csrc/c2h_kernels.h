@@ -15,7 +15,7 @@ struct C2hState {
   float penalty;    // 1.15 in the reference (c2slm.go:165,167)
   int32_t nx_in;    // normX buffer read by the vocab projection
   int32_t nx_out;   // normX buffer written by the final RMSNorm
-  int32_t pad;
+  int32_t seq;      // step number, handed to the host with the step's token
 };
 
 // Q8_K row as the GEMVs keep it in LDS: quants packed four per dword, the
@@ -120,6 +120,10 @@ struct GemvParams {
   int32_t* token_ids;
   int max_ctx;
   C2hState* state;
+  // step graphs: the chosen token and state->seq, written by layer 0's
+  // prologue into host-pinned memory (system scope) so that the host has
+  // the token while the rest of the step runs (nullptr: none)
+  int32_t* tok_out;
   int n_jobs;
   GemvJob jobs[MAX_JOBS];
 };

@@ -742,6 +742,15 @@ __device__ __forceinline__ GemvJob launch_job(const GemvParams& P) {
   return J;
 }
 
+// The step's token to the host: the token, then (system-scope release, so
+// that the token is visible first) the step number the host waits for.
+__device__ __forceinline__ void publish_token(const GemvParams& P, int tok) {
+  if (P.tok_out != nullptr) {
+    P.tok_out[0] = tok;
+    __hip_atomic_store(&P.tok_out[1], P.state->seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
 // One GEMV of the layer body with its input prologue, for rows of NB
 // super-blocks (weights and input share the width):
 //   PRO_QUANT  Q8_K(x), x = attention output or SwiGLU output;
@@ -822,6 +831,7 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(GemvPar
         const int pos = P.state->pos;
         P.state->token = tok;
         if (pos >= 0 && pos < P.max_ctx) P.token_ids[pos] = tok;
+        publish_token(P, tok);
       }
     }
     const float inv = rms_inv4(xa[0], P.n_x, P.eps, sq, &inv_slot);
@@ -1109,6 +1119,7 @@ __global__ void __launch_bounds__(256) k_gemv_f(GemvParams P) {
         const int pos = P.state->pos;
         P.state->token = tok;
         if (pos >= 0 && pos < P.max_ctx) P.token_ids[pos] = tok;
+        publish_token(P, tok);
       }
     }
     const float inv = rms_inv4(xa, P.n_x, P.eps, sq, &inv_slot);
