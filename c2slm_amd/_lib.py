@@ -184,6 +184,11 @@ class Ctx:
     def restore_normx(self):
         self._chk(lib().c2h_restore_normx(self.h))
 
+    def sync(self):
+        """Wait for all work queued on the context (a step's call returns with
+        its token while the forward of that token still runs)."""
+        self._chk(lib().c2h_sync(self.h))
+
     def normx(self) -> np.ndarray:
         out = np.empty(self.desc.n_embd, np.float32)
         self._chk(lib().c2h_get_normx(self.h, _p(out)))

@@ -151,7 +151,11 @@ int c2h_logits(c2h_ctx* ctx, float* logits_out);
  * engine.Forward(best, pos) and TokenIDs[pos] = best.  Only the chosen id
  * crosses to the host.  The new normX becomes current; c2h_restore_normx
  * undoes that for a caller that rejects the token (stop strings,
- * c2slm.go:205-216). */
+ * c2slm.go:205-216).  The call returns once the chosen id is known (the
+ * step's first layer hands it over through pinned memory); the forward of
+ * that token then completes on the context's stream, before any later call
+ * on the context reads or writes device state, so results are the same as
+ * if the call had waited (c2h_sync waits for it explicitly). */
 int c2h_step(c2h_ctx* ctx, int32_t pos, float penalty, int32_t im_end, int32_t eos, int32_t* next_token);
 
 /* Makes the normX that was current before the last c2h_step current again. */
