@@ -67,6 +67,10 @@ struct c2h_ctx {
   C2hState* state_ring = nullptr;  // pinned
   int32_t* tok_host = nullptr;     // pinned: {token, seq} written by a step's layer 0
   unsigned step_seq = 0;           // last step number handed to the device
+  // the state a completed step graph leaves on the device (its final norm
+  // advances pos, seq and the normX buffers); valid until the next push
+  C2hState state_pred{};
+  bool state_pred_valid = false;
   unsigned ring_next = 0;
 
   // graphs by attention form (attn_form): k_attn_core's tiers of 32, 64,
@@ -703,8 +707,9 @@ void enqueue_ffn_out(c2h_ctx* c, int l) {
 // k_rmsnorm holds one float4 per thread
 int norm_threads(int n) { return n <= 1024 ? 256 : 512; }
 
-// the final RMSNorm into the normX buffer the step state names
-void enqueue_final_norm(c2h_ctx* c) {
+// the final RMSNorm into the normX buffer the step state names; a step
+// graph's also leaves the next step's state (advance)
+void enqueue_final_norm(c2h_ctx* c, int advance = 0) {
   const c2h_model_desc& D = c->desc;
   NormParams N;
   memset(&N, 0, sizeof(N));
@@ -717,6 +722,7 @@ void enqueue_final_norm(c2h_ctx* c) {
   N.out_buf[1] = c->normx[1];
   N.state = c->state_dev;
   N.n_lds = chain_lds_floats(D.n_embd);
+  N.advance = advance;
   hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(norm_threads(D.n_embd)), (size_t)N.n_lds * sizeof(float), c->stream, N);
 }
 
@@ -731,7 +737,7 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax, int form) {
     enqueue_ffn_in(c, l);
     enqueue_ffn_out(c, l);
   }
-  enqueue_final_norm(c);
+  enqueue_final_norm(c, from_argmax ? 1 : 0);
 }
 
 void enqueue_step(c2h_ctx* c, int form) {
@@ -812,6 +818,7 @@ int build_graphs(c2h_ctx* c) {
 // Writes the per-launch state through a ring of pinned slots; the stream
 // orders the copy before the graph.  Slots are reused only after a sync.
 int push_state(c2h_ctx* c, const C2hState& s) {
+  c->state_pred_valid = false;
   unsigned slot = c->ring_next++ % kStateRing;
   if (slot == 0 && c->ring_next > 1) HIPCHK(c, hipStreamSynchronize(c->stream));
   c->state_ring[slot] = s;
@@ -1474,8 +1481,19 @@ int c2h_step(c2h_ctx* c, int32_t pos, float penalty, int32_t im_end, int32_t eos
   s.nx_in = c->nx_cur;
   s.nx_out = c->nx_cur ^ 1;
   s.seq = (int32_t)(++c->step_seq % 0x7ffffffeu) + 1;  // never 0 (other launches) or -1 (initial)
-  if ((rc = push_state(c, s))) return rc;
+  // the state the previous step left on the device, when it is this one,
+  // needs no copy (the token field is not read by a step graph)
+  const C2hState& pr = c->state_pred;
+  const bool same = c->state_pred_valid && pr.pos == s.pos && pr.im_end == s.im_end && pr.eos == s.eos &&
+                    pr.penalty == s.penalty && pr.nx_in == s.nx_in && pr.nx_out == s.nx_out && pr.seq == s.seq;
+  if (!same && (rc = push_state(c, s))) return rc;
   if ((rc = run_graph(c, true, pos))) return rc;
+  c->state_pred = s;
+  c->state_pred.pos = s.pos + 1;
+  c->state_pred.seq = s.seq % 0x7ffffffe + 1;
+  c->state_pred.nx_in = s.nx_out;
+  c->state_pred.nx_out = s.nx_out ^ 1;
+  c->state_pred_valid = true;  // eager launches run the same final norm
   c->nx_prev = c->nx_cur;
   c->nx_cur ^= 1;
   c->seq_len = pos + 1;

@@ -142,6 +142,7 @@ struct NormParams {
   float* out;
   float* out_buf[2];
   C2hState* state;
+  int advance;  // step graphs: leave the state of the next step (pos, seq, normX buffers)
 };
 
 // KV cache: [K|V][layer][kv head][kv_slot(max_ctx)][hd] floats.  K rows are

@@ -1199,12 +1199,25 @@ __global__ void __launch_bounds__(512) k_rmsnorm(NormParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
   float* sq = reinterpret_cast<float*>(smem);
   __shared__ float inv_slot;
+  asm volatile("" ::"s"(P.x), "s"(P.w), "s"(P.n), "s"(P.eps), "s"(P.out_sel), "s"(P.out), "s"(P.out_buf[0]),
+               "s"(P.out_buf[1]), "s"(P.state), "s"(P.advance));
   const float4 x = load4(P.x, P.n);
   const float4 w = load4(P.w, P.n);
+  const int nx_out = P.out_sel ? P.state->nx_out : 0;  // with the loads, not after the sum
   issue_fence();
   const float inv = rms_inv4(x, P.n, P.eps, sq, &inv_slot);
-  float* out = P.out_sel ? P.out_buf[P.state->nx_out] : P.out;
+  float* out = P.out_sel ? P.out_buf[nx_out] : P.out;
   if (4 * (int)threadIdx.x < P.n) reinterpret_cast<float4*>(out)[threadIdx.x] = norm4(x, inv, w);
+  if (P.advance) {
+    __syncthreads();  // every thread has read the state
+    if (threadIdx.x == 0) {
+      C2hState* st = P.state;
+      st->pos = st->pos + 1;
+      st->seq = st->seq % 0x7ffffffe + 1;
+      st->nx_in = nx_out;
+      st->nx_out = nx_out ^ 1;
+    }
+  }
 }
 
 // ------------------------------------------------------- attention block
