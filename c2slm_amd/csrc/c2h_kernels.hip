@@ -1616,11 +1616,14 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
     if (tid < HD && pos > 0) acc = av_chain_q3<64>(sc, vbuf, pos, d, acc);
   } else {
     // Chunk c sits in LDS buffer c & 1; chunk c+1 waits in register set
-    // c % 3.  Chunks 1..3 start loading under the softmax.  Every thread
-    // issues the set loads (wave 0 duplicates wave 1's, unused) and the
-    // staging loop loads unconditionally (indices clamped): with no load
-    // on only one side of a branch the compiler's memory-counter waits
-    // keep three chunks in flight.
+    // c % 3.  The staging waves (1..3) issue their loads after the softmax,
+    // inside their own branch: issued before it they held every wave at the
+    // softmax's barriers (a CU takes ~30 clk per 1 KB load), and the chain
+    // wave issues none.  The staging loop loads unconditionally (indices
+    // clamped, whole trips of three steps, the remainder after it), so the
+    // compiler's memory-counter waits keep three chunks in flight; with at
+    // most four chunks the three register sets hold all of them and there
+    // is no loop.
     const int wp = (wave >= 1) ? wave - 1 : 0;  // staging wave index
     auto load_set = [&](VStage<PER>& st, int c) {
 #pragma unroll
@@ -1631,33 +1634,46 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
       for (int k = 0; k < PER; ++k)
         if (wp + 3 * k < NQ) vbuf[((c & 1) * NQ + wp + 3 * k) * HD + (tid & 63)] = st.r[k];
     };
-    VStage<PER> s0, s1, s2;
-    load_set(s0, 1);
-    load_set(s1, min(2, nch - 1));
-    load_set(s2, min(3, nch - 1));
     softmax();
-    // both roles pass nch barriers, one per chunk; the staging loop runs
-    // whole trips of three unconditional steps, the remainder after it
+    // both roles pass nch barriers, one per chunk
     if (tid >= 64) {
-      int c = 0;
-      for (; c + 3 <= nch; c += 3) {
-        store_set(s0, c + 1);
-        load_set(s0, min(c + 4, nch - 1));
+      VStage<PER> s0, s1, s2;
+      load_set(s0, 1);
+      load_set(s1, min(2, nch - 1));
+      load_set(s2, min(3, nch - 1));
+      if (nch <= 4) {
+        store_set(s0, 1);
         __syncthreads();
-        store_set(s1, c + 2);
-        load_set(s1, min(c + 5, nch - 1));
+        if (nch > 2) {
+          store_set(s1, 2);
+          __syncthreads();
+        }
+        if (nch > 3) {
+          store_set(s2, 3);
+          __syncthreads();
+        }
         __syncthreads();
-        store_set(s2, c + 3);
-        load_set(s2, min(c + 6, nch - 1));
-        __syncthreads();
-      }
-      if (c < nch) {
-        store_set(s0, c + 1);
-        __syncthreads();
-      }
-      if (c + 1 < nch) {
-        store_set(s1, c + 2);
-        __syncthreads();
+      } else {
+        int c = 0;
+        for (; c + 3 <= nch; c += 3) {
+          store_set(s0, c + 1);
+          load_set(s0, min(c + 4, nch - 1));
+          __syncthreads();
+          store_set(s1, c + 2);
+          load_set(s1, min(c + 5, nch - 1));
+          __syncthreads();
+          store_set(s2, c + 3);
+          load_set(s2, min(c + 6, nch - 1));
+          __syncthreads();
+        }
+        if (c < nch) {
+          store_set(s0, c + 1);
+          __syncthreads();
+        }
+        if (c + 1 < nch) {
+          store_set(s1, c + 2);
+          __syncthreads();
+        }
       }
     } else {
       for (int c = 0; c < nch; ++c) {

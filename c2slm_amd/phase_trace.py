@@ -32,7 +32,7 @@ GEMV_PHASES = ["entry", "args", "issued", "x", "norm_end", "quant", "w", "items"
 ATTN_PHASES = ["entry", "args", "issued", "qkv", "rope", "scores", "softmax", "av", "end", "pos", "k_in", "v_in", "max", "exp", "sum"]
 
 _STAMPS = r"""namespace c2h {
-__device__ long long g_phase[5][2][8][16];
+__device__ long long g_phase[6][2][8][16];
 template <int NB, int PRO, int MODE>
 __device__ __forceinline__ int phase_kind() {
   return (PRO == PRO_NORM && MODE == MODE_BIAS)                 ? 0
@@ -46,8 +46,8 @@ __device__ __forceinline__ int phase_kind() {
     g_phase[kd_][blockIdx.x == 0 ? 0 : 1][threadIdx.x >> 6][k] = __builtin_amdgcn_s_memtime(); } while (0)
 #define PH_AT(k, t) do { const bool f_ = h == 0; \
   const bool l_ = h == P.n_heads - 1; \
-  if (TIER != ATT_TIER_ANY && (threadIdx.x & 63) == 0 && blockIdx.z == 0 && (f_ || l_)) \
-    g_phase[4][f_ ? 0 : 1][threadIdx.x >> 6][k] = (t); } while (0)
+  if ((threadIdx.x & 63) == 0 && blockIdx.z == 0 && (f_ || l_)) \
+    g_phase[TIER == ATT_TIER_ANY ? 5 : 4][f_ ? 0 : 1][threadIdx.x >> 6][k] = (t); } while (0)
 #define PH_A(k) PH_AT(k, __builtin_amdgcn_s_memtime())
 """
 
@@ -108,16 +108,19 @@ def instrument(kernels: str) -> str:
                    ("  // softmax, then V chunk 0 from registers into LDS buffer 0\n",
                     "  PH_A(5);\n  // softmax, then V chunk 0 from registers into LDS buffer 0\n"),
                    ("    softmax();\n    if (tid < HD && nbat > 0) acc = av_chain_pad(sc, vbuf, nbat, d, acc);\n",
-                    "    softmax();\n    PH_A(6);\n    if (tid < HD && nbat > 0) acc = av_chain_pad(sc, vbuf, nbat, d, acc);\n"
-                    "    PH_A(7);\n"),
+                    "    softmax();\n    PH_A(6);\n    if (tid < HD && nbat > 0) acc = av_chain_pad(sc, vbuf, nbat, d, acc);\n"),
+                   ("    softmax();\n    // both roles pass nch barriers, one per chunk\n",
+                    "    softmax();\n    PH_A(6);\n    // both roles pass nch barriers, one per chunk\n"),
+                   ("  if (tid < HD) {\n    acc = __builtin_fmaf(sc[pos], v_s[d], acc);\n",
+                    "  PH_A(7);\n  if (tid < HD) {\n    acc = __builtin_fmaf(sc[pos], v_s[d], acc);\n"),
                ]).replace("PH_END;", "PH_A(8);", 1)
     return s
 
 
 _READER = r"""
-namespace c2h { extern __device__ long long g_phase[5][2][8][16]; }
+namespace c2h { extern __device__ long long g_phase[6][2][8][16]; }
 extern "C" int c2h_phase_read(long long* out) {
-  return hipMemcpyFromSymbol(out, HIP_SYMBOL(c2h::g_phase), sizeof(long long) * 5 * 2 * 8 * 16) == hipSuccess ? 0 : -1;
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(c2h::g_phase), sizeof(long long) * 6 * 2 * 8 * 16) == hipSuccess ? 0 : -1;
 }
 """
 
@@ -179,12 +182,12 @@ def run(path: str = "/tmp/c2h_phase_q05.gguf") -> None:
     _, im_end, eos = G.special_token_ids(gf)
     for p in range(32, 48):
         ctx.step(p, 1.15, im_end, eos)
-    buf = (C.c_longlong * (5 * 2 * N_WAVES * N_SLOTS))()
+    buf = (C.c_longlong * (6 * 2 * N_WAVES * N_SLOTS))()
     fn = H.lib().c2h_phase_read
     fn.argtypes = [C.c_void_p]
     if fn(buf) != 0:
         raise RuntimeError("c2h_phase_read failed")
-    a = np.array(buf, dtype=np.int64).reshape(5, 2, N_WAVES, N_SLOTS)
+    a = np.array(buf, dtype=np.int64).reshape(6, 2, N_WAVES, N_SLOTS)
     print("last launch of each kernel (layer 23 of the 16th step, T = 48); shader clocks from wave 0's entry,"
           " latest wave")
     for k, name in enumerate(GEMV_KINDS + ["attn"]):
