@@ -1566,25 +1566,15 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   const int nbat = (pos + 15) >> 4;  // a tier's whole batches of sixteen positions
 
   // softmax, then V chunk 0 from registers into LDS buffer 0
-  auto softmax = [&]() {
+  // waves 1..3 run while_summing during wave 0's exact sum
+  auto softmax = [&](auto&& while_summing) {
     // max: x[0] first, strict '>' (tensor/ops.go:321-326): the max of the
     // non-NaN scores, or NaN when score[0] is NaN.
     lmax = wave_max_dpp(lmax);
     if ((tid & 63) == 0) red_m[tid >> 6] = lmax;
     __syncthreads();
-    float mx = fmax_gt(fmax_gt(fmax_gt(red_m[0], red_m[1]), red_m[2]), red_m[3]);
-    if (sc[0] != sc[0]) mx = sc[0];
-    for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));
-    __syncthreads();
-    if (T <= 64 * SPEC_C) {
-      if (tid < 64) {
-        const float ssum = seq_sum_wave(sc, T);
-        if (tid == 0) inv_slot = 1.0f / ssum;
-      }
-    } else if (tid < 64) {
-      const float ssum = seq_sum_wave_n(sc, T);
-      if (tid == 0) inv_slot = 1.0f / ssum;
-    }
+    // every score has read its K row: V (the tier's rows, or chunk 0) takes
+    // their LDS, before any later load is issued
 #pragma unroll
     for (int i = 0; i < VQW; ++i) {
       f32x4_t vv = vreg[i];
@@ -1596,6 +1586,16 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
         vv.w = (p0 + 3 < pos) ? vv.w : 0.0f;
       }
       vbuf[(wave + 4 * i) * HD + (tid & 63)] = vv;
+    }
+    float mx = fmax_gt(fmax_gt(fmax_gt(red_m[0], red_m[1]), red_m[2]), red_m[3]);
+    if (sc[0] != sc[0]) mx = sc[0];
+    for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));
+    __syncthreads();
+    if (tid < 64) {
+      const float ssum = (T <= 64 * SPEC_C) ? seq_sum_wave(sc, T) : seq_sum_wave_n(sc, T);
+      if (tid == 0) inv_slot = 1.0f / ssum;
+    } else {
+      while_summing();
     }
     __syncthreads();
     const float inv = inv_slot;
@@ -1609,17 +1609,17 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   float acc = 0.0f;
   const int d = tid & 63;
   if (!ANY) {  // V[0, pos) in LDS, zero rows up to the batch end
-    softmax();
+    softmax([] {});
     if (tid < HD && nbat > 0) acc = av_chain_pad(sc, vbuf, nbat, d, acc);
   } else if (nch <= 1) {
-    softmax();
+    softmax([] {});
     if (tid < HD && pos > 0) acc = av_chain_q3<64>(sc, vbuf, pos, d, acc);
   } else {
     // Chunk c sits in LDS buffer c & 1; chunk c+1 waits in register set
-    // c % 3.  The staging waves (1..3) issue their loads after the softmax,
-    // inside their own branch: issued before it they held every wave at the
-    // softmax's barriers (a CU takes ~30 clk per 1 KB load), and the chain
-    // wave issues none.  The staging loop loads unconditionally (indices
+    // c % 3.  The staging waves (1..3) issue the loads of chunks 1..3 while
+    // wave 0 runs the softmax's sum: issued before the softmax they held
+    // every wave at its barriers (a CU takes ~30 clk per 1 KB load), and the
+    // chain wave issues none.  The staging loop loads unconditionally (indices
     // clamped, whole trips of three steps, the remainder after it), so the
     // compiler's memory-counter waits keep three chunks in flight; with at
     // most four chunks the three register sets hold all of them and there
@@ -1634,13 +1634,14 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
       for (int k = 0; k < PER; ++k)
         if (wp + 3 * k < NQ) vbuf[((c & 1) * NQ + wp + 3 * k) * HD + (tid & 63)] = st.r[k];
     };
-    softmax();
-    // both roles pass nch barriers, one per chunk
-    if (tid >= 64) {
-      VStage<PER> s0, s1, s2;
+    VStage<PER> s0, s1, s2;
+    softmax([&] {
       load_set(s0, 1);
       load_set(s1, min(2, nch - 1));
       load_set(s2, min(3, nch - 1));
+    });
+    // both roles pass nch barriers, one per chunk
+    if (tid >= 64) {
       if (nch <= 4) {
         store_set(s0, 1);
         __syncthreads();

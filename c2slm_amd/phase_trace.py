@@ -98,8 +98,8 @@ def instrument(kernels: str) -> str:
                     "    PH_A(11);\n    __syncthreads();\n    const float inv = inv_slot;\n"),
                    ("    if (sc[0] != sc[0]) mx = sc[0];\n    for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));\n    __syncthreads();\n",
                     "    if (sc[0] != sc[0]) mx = sc[0];\n    PH_A(12);\n    for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));\n    __syncthreads();\n    PH_A(13);\n"),
-                   ("#pragma unroll\n    for (int i = 0; i < VQW; ++i) {\n      f32x4_t vv = vreg[i];",
-                    "    PH_A(14);\n#pragma unroll\n    for (int i = 0; i < VQW; ++i) {\n      f32x4_t vv = vreg[i];"),
+                   ("      while_summing();\n    }\n",
+                    "      while_summing();\n    }\n    PH_A(14);\n"),
                    ("  issue_fence();\n\n  if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;\n  __syncthreads();\n",
                     "  issue_fence();\n  PH_A(2);\n\n  if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;\n"
                     "  __syncthreads();\n  PH_A(3);\n"),
