@@ -107,10 +107,10 @@ def instrument(kernels: str) -> str:
                     "  __syncthreads();\n  PH_A(4);\n\n  // (a batch of query tokens"),
                    ("  // softmax, then V chunk 0 from registers into LDS buffer 0\n",
                     "  PH_A(5);\n  // softmax, then V chunk 0 from registers into LDS buffer 0\n"),
-                   ("    softmax();\n    if (tid < HD && nbat > 0) acc = av_chain_pad(sc, vbuf, nbat, d, acc);\n",
-                    "    softmax();\n    PH_A(6);\n    if (tid < HD && nbat > 0) acc = av_chain_pad(sc, vbuf, nbat, d, acc);\n"),
-                   ("    softmax();\n    // both roles pass nch barriers, one per chunk\n",
-                    "    softmax();\n    PH_A(6);\n    // both roles pass nch barriers, one per chunk\n"),
+                   ("    softmax([] {});\n    if (tid < HD && nbat > 0) acc = av_chain_pad(sc, vbuf, nbat, d, acc);\n",
+                    "    softmax([] {});\n    PH_A(6);\n    if (tid < HD && nbat > 0) acc = av_chain_pad(sc, vbuf, nbat, d, acc);\n"),
+                   ("    });\n    // both roles pass nch barriers, one per chunk\n",
+                    "    });\n    PH_A(6);\n    // both roles pass nch barriers, one per chunk\n"),
                    ("  if (tid < HD) {\n    acc = __builtin_fmaf(sc[pos], v_s[d], acc);\n",
                     "  PH_A(7);\n  if (tid < HD) {\n    acc = __builtin_fmaf(sc[pos], v_s[d], acc);\n"),
                ]).replace("PH_END;", "PH_A(8);", 1)
