@@ -530,9 +530,13 @@ def main():
     vocab_step_ms = ctx.time_vocab(args.vocab_iters, pos, in_step=1)
     vocab_b2b_ms = ctx.time_vocab(args.vocab_iters, pos, in_step=0)
     vocab_gbs = VOCAB_BYTES / (vocab_ms * 1e-3) / 1e9
-    # per-kernel floor of dependent launches in a graph (empty kernels)
-    floor_us = ctx.launch_floor(240, 256, 5)
-    floor_by_grid = {g: round(ctx.launch_floor(240, g, 5), 3) for g in (1, 64, 256, 1024, 4096)}
+    # per-kernel floor of dependent launches in a graph (empty kernels); not
+    # with C2H_NO_GRAPH=1 (eager runs, e.g. under a kernel-trace profiler)
+    if os.environ.get("C2H_NO_GRAPH") == "1":
+        floor_us, floor_by_grid = None, None
+    else:
+        floor_us = ctx.launch_floor(240, 256, 5)
+        floor_by_grid = {g: round(ctx.launch_floor(240, g, 5), 3) for g in (1, 64, 256, 1024, 4096)}
     if args.copy_calib_mib:
         copy_calibration(ctx, args.copy_calib_mib)
 
@@ -592,7 +596,7 @@ def main():
                   "layer_microbench": micro,
                   "vocab_ms_back_to_back": round(vocab_b2b_ms, 5),
                   "vocab_ms_in_step_events": round(vocab_step_ms, 5),
-                  "launch_floor_us_per_kernel": round(floor_us, 3),
+                  "launch_floor_us_per_kernel": None if floor_us is None else round(floor_us, 3),
                   "launch_floor_us_by_grid": floor_by_grid,
                   "pipelined_ms_per_step": round(pipelined_ms, 4),
                   "pipelined_tok_s": round(1000.0 / pipelined_ms, 1),
