@@ -396,6 +396,9 @@ def main():
     ap.add_argument("--no-microbench", action="store_true", help="skip the layer-shape operator microbench")
     ap.add_argument("--no-qwen3", action="store_true", help="skip the Qwen3-1.7B-shape decode line")
     ap.add_argument("--kernel-iters", type=int, default=96, help="launches in each decode-kernel timing")
+    ap.add_argument("--kernel-pos", type=int, default=None,
+                    help="with --only kernels: greedy steps after the prompt up to this position, so attention "
+                         "covers pos+1 positions (default: the decode line's last position, prompt + warmup + steps)")
     ap.add_argument("--only", choices=["prefill", "long", "float-dots", "real-formats", "vocab", "microbench",
                                        "kernels", "qwen3"],
                     default=None,
@@ -467,8 +470,13 @@ def main():
         ctx.set_token_ids(0, prompt)
         for p, t in enumerate(prompt):
             ctx.forward(int(t), p, want_normx=False)
+        kpos = PROMPT_LEN + args.warmup + args.steps if args.kernel_pos is None else args.kernel_pos
+        for p in range(PROMPT_LEN, kpos):
+            ctx.step(p, PENALTY, im_end, eos)
+        ctx.sync()
         out = {k: [round(ctx.time_layer_kernel(k, args.kernel_iters, captured=g) * 1e3, 3) for g in (False, True)]
                for k in ctx.KERNELS}
+        out["attended_positions"] = ctx.seq_len + 1
         if args.copy_calib_mib:
             copy_calibration(ctx, args.copy_calib_mib)
         print(json.dumps({"decode_kernels_us_eager_graph": out}))

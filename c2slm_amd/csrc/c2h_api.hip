@@ -2141,15 +2141,17 @@ int c2h_time_steps(c2h_ctx* c, int32_t pos, int32_t iters, float penalty, int32_
   HIPCHK(c, hipEventCreate(&e1));
   HIPCHK(c, hipEventRecord(e0, c->stream));
   for (int i = 0; i < iters; ++i) {
-    C2hState s;
-    memset(&s, 0, sizeof(s));
-    s.pos = pos + i;
-    s.im_end = im_end;
-    s.eos = eos;
-    s.penalty = penalty;
-    s.nx_in = c->nx_cur;
-    s.nx_out = c->nx_cur ^ 1;
-    if ((rc = push_state(c, s))) return rc;
+    if (i == 0) {  // later steps run on the state the previous step's final norm advanced
+      C2hState s;
+      memset(&s, 0, sizeof(s));
+      s.pos = pos;
+      s.im_end = im_end;
+      s.eos = eos;
+      s.penalty = penalty;
+      s.nx_in = c->nx_cur;
+      s.nx_out = c->nx_cur ^ 1;
+      if ((rc = push_state(c, s))) return rc;
+    }
     if ((rc = run_graph(c, true, pos + i))) return rc;
     c->nx_prev = c->nx_cur;
     c->nx_cur ^= 1;

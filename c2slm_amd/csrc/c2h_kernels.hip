@@ -244,9 +244,13 @@ __device__ __forceinline__ float lane_value(float x, int l) {
 // over the lanes' window-to-window maps finds how far the exact chain
 // reaches.  The first round stays plain.  On activation rows of 896 values
 // this takes 2.3 rounds on average where plain rounds take 5.9.
+// The rounds cost ~1,000-1,900 clk at any n (measured); one lane's chain
+// (chain_sum) ~10-12 clk per value, so attention over at most SUM_DIRECT_N
+// positions runs that instead.
 constexpr int SPEC_C = 16;
 constexpr int SPEC_ROUNDS = 10;
 constexpr int WIN_MIN_N = 256;
+constexpr int SUM_DIRECT_N = 64;
 
 // One round: R is this lane's chunk run from its start S.  Returns true with
 // the total once every start is verified; else advances S (and m, the last
@@ -365,6 +369,33 @@ __device__ __forceinline__ float chunk_chain(const float* a, int b0, int b1, flo
   return s;
 }
 
+// The whole chain (((0 + a[0]) + a[1]) + ...) + a[n-1] in one lane, n >= 1,
+// over whole blocks of 16: a[n .. round_up(n, 16)) must hold -0, which
+// leaves every sum unchanged.  Two register sets alternate, each block's
+// reads issued one block ahead and unconditionally, so every wait covers
+// only the block about to be added.
+__device__ __forceinline__ float chain_sum(const float* a, int n) {
+  const int nb = (n + 15) >> 4;
+  float s = 0.0f;
+  float4 A[4], B[4];
+  load16(A, a);
+  int b = 0;
+  for (; b + 2 <= nb; b += 2) {  // A holds block b
+    load16(B, a + 16 * (b + 1));
+    __builtin_amdgcn_sched_barrier(0);
+    s = add16(s, A);
+    load16(A, a + 16 * min(b + 2, nb - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    s = add16(s, B);
+  }
+  if (b < nb) s = add16(s, A);
+  return s;
+}
+// -0 into a[n .. round_up(n, 16)) by threads 0..15 (chain_sum's padding).
+__device__ __forceinline__ void pad_chain(float* a, int n) {
+  const int p = n + (int)threadIdx.x;
+  if (threadIdx.x < 16 && p < ((n + 15) & ~15)) a[p] = -0.0f;
+}
 
 // n <= 1024: lane l owns [16l, 16l+16) in registers.  a: LDS readable up to
 // round_up(n, 16).
@@ -1590,9 +1621,17 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
     float mx = fmax_gt(fmax_gt(fmax_gt(red_m[0], red_m[1]), red_m[2]), red_m[3]);
     if (sc[0] != sc[0]) mx = sc[0];
     for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));
+    if constexpr (!ANY && TIER <= SUM_DIRECT_N) pad_chain(sc, T);
     __syncthreads();
     if (tid < 64) {
-      const float ssum = (T <= 64 * SPEC_C) ? seq_sum_wave(sc, T) : seq_sum_wave_n(sc, T);
+      // a tier knows its bound at compile time: no code for longer sums
+      float ssum;
+      if constexpr (!ANY && TIER <= SUM_DIRECT_N)
+        ssum = chain_sum(sc, T);
+      else if constexpr (!ANY)
+        ssum = seq_sum_wave(sc, T);
+      else
+        ssum = (T <= 64 * SPEC_C) ? seq_sum_wave(sc, T) : seq_sum_wave_n(sc, T);
       if (tid == 0) inv_slot = 1.0f / ssum;
     } else {
       while_summing();

@@ -9,13 +9,16 @@ of each launch stores its stamp per phase into a device array; every later
 launch of the same kernel overwrites it, so a read after a run holds the
 last launch's stamps.  The product library is untouched.
 
-`run` (GPU) loads that library (C2H_LIB), runs the decode workload -- a
-synthetic Qwen2.5-0.5B-shaped model, a 32-token prefill, 16 greedy steps --
-and prints the table: per phase, the latest wave's stamp minus wave 0's
-entry stamp, in shader clocks.
+`run [T]` (GPU) loads that library (C2H_LIB), runs the decode workload -- a
+synthetic Qwen2.5-0.5B-shaped model, a prefill of T-16 tokens, 16 greedy
+steps, the last one attending over T positions (default 48) -- and prints
+the table: per phase, the latest wave's stamp minus wave 0's entry stamp, in
+shader clocks.  Above 256 positions it prints the any-length attention
+tier's stamps wave by wave instead.
 
     python -m c2slm_amd.phase_trace build      # CPU: hipcc cross-compiles
     python -m c2slm_amd.phase_trace run        # GPU
+    python -m c2slm_amd.phase_trace run 512    # GPU, long-context attention
 """
 from __future__ import annotations
 
@@ -96,8 +99,8 @@ def instrument(kernels: str) -> str:
                     "    PH_A(10);\n    __syncthreads();\n    const int p = c0 + tid;\n"),
                    ("    __syncthreads();\n    const float inv = inv_slot;\n",
                     "    PH_A(11);\n    __syncthreads();\n    const float inv = inv_slot;\n"),
-                   ("    if (sc[0] != sc[0]) mx = sc[0];\n    for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));\n    __syncthreads();\n",
-                    "    if (sc[0] != sc[0]) mx = sc[0];\n    PH_A(12);\n    for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));\n    __syncthreads();\n    PH_A(13);\n"),
+                   ("    if (sc[0] != sc[0]) mx = sc[0];\n    for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));\n    if constexpr (!ANY && TIER <= SUM_DIRECT_N) pad_chain(sc, T);\n    __syncthreads();\n",
+                    "    if (sc[0] != sc[0]) mx = sc[0];\n    PH_A(12);\n    for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));\n    if constexpr (!ANY && TIER <= SUM_DIRECT_N) pad_chain(sc, T);\n    __syncthreads();\n    PH_A(13);\n"),
                    ("      while_summing();\n    }\n",
                     "      while_summing();\n    }\n    PH_A(14);\n"),
                    ("  issue_fence();\n\n  if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;\n  __syncthreads();\n",
@@ -161,11 +164,18 @@ def build() -> str:
     return OUT_LIB
 
 
-def run(path: str = "/tmp/c2h_phase_q05.gguf") -> None:
+def run(last: int = 48, path: str = "/tmp/c2h_phase_q05.gguf") -> None:
+    """Prefill last-16 tokens, take 16 greedy steps, print the stamps of the last launches.
+
+    At last <= 256 the table covers every kernel (first and last workgroup, latest wave); above
+    256 the attention launch runs the any-length tier, and the table lists its waves one by one.
+    """
     if os.environ.get("C2H_LIB") != OUT_LIB:  # the library path is fixed when _lib loads
         env = dict(os.environ, C2H_LIB=OUT_LIB)
-        sys.exit(subprocess.run([sys.executable, "-u", "-m", "c2slm_amd.phase_trace", "run"], env=env,
+        sys.exit(subprocess.run([sys.executable, "-u", "-m", "c2slm_amd.phase_trace", "run", str(last)], env=env,
                                 cwd=os.path.dirname(HERE)).returncode)
+    if not 17 <= last <= 1024:
+        raise ValueError("last must lie in 17..1024")
     import ctypes as C
 
     import numpy as np
@@ -177,19 +187,31 @@ def run(path: str = "/tmp/c2h_phase_q05.gguf") -> None:
     gf = G.GGUFFile(path)
     ctx = H.Ctx(H.desc_from_gguf(gf, max_ctx=1024))
     H.load_gguf_into(ctx, gf)
-    prompt = np.random.default_rng(20261201).integers(0, gf.tensor_map["token_embd.weight"].dims[1], 32)
+    prompt = np.random.default_rng(20261201).integers(0, gf.tensor_map["token_embd.weight"].dims[1], last - 16)
     ctx.prefill(prompt.astype(np.int32), 0)
     _, im_end, eos = G.special_token_ids(gf)
-    for p in range(32, 48):
+    for p in range(last - 16, last):
         ctx.step(p, 1.15, im_end, eos)
+    ctx.sync()
     buf = (C.c_longlong * (6 * 2 * N_WAVES * N_SLOTS))()
     fn = H.lib().c2h_phase_read
     fn.argtypes = [C.c_void_p]
     if fn(buf) != 0:
         raise RuntimeError("c2h_phase_read failed")
     a = np.array(buf, dtype=np.int64).reshape(6, 2, N_WAVES, N_SLOTS)
-    print("last launch of each kernel (layer 23 of the 16th step, T = 48); shader clocks from wave 0's entry,"
-          " latest wave")
+    if last > 256:
+        print(f"attention, any-length tier, layer 23 of the 16th step, T = {last}; shader clocks from wave 0's"
+              " entry, per wave")
+        print(f"{'wg':5s} {'wave':4s} " + " ".join(f"{p:>8s}" for p in ATTN_PHASES))
+        for wg in range(2):
+            t0 = a[5, wg, 0, 0]
+            for w in range(4):
+                print(f"{('first', 'last')[wg]:5s} {w:4d} " + " ".join(
+                    f"{int(a[5, wg, w, i] - t0) if a[5, wg, w, i] else -1:8d}" for i in range(len(ATTN_PHASES))))
+        ctx.close()
+        return
+    print(f"last launch of each kernel (layer 23 of the 16th step, T = {last}); shader clocks from wave 0's"
+          " entry, latest wave")
     for k, name in enumerate(GEMV_KINDS + ["attn"]):
         cols = ATTN_PHASES if name == "attn" else GEMV_PHASES
         print(f"{name:9s} {'wg':5s} " + " ".join(f"{p:>10s}" for p in cols))
@@ -204,9 +226,10 @@ def run(path: str = "/tmp/c2h_phase_q05.gguf") -> None:
 
 
 if __name__ == "__main__":
-    if len(sys.argv) != 2 or sys.argv[1] not in ("build", "run"):
-        sys.exit("usage: python -m c2slm_amd.phase_trace build|run")
+    if len(sys.argv) not in (2, 3) or sys.argv[1] not in ("build", "run") or (
+            len(sys.argv) == 3 and (sys.argv[1] != "run" or not sys.argv[2].isdigit())):
+        sys.exit("usage: python -m c2slm_amd.phase_trace build | run [positions]")
     if sys.argv[1] == "build":
         print(build())
     else:
-        run()
+        run(int(sys.argv[2]) if len(sys.argv) == 3 else 48)

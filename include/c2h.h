@@ -323,7 +323,8 @@ int c2h_time_quantize_q8k(c2h_ctx* ctx, const float* x, int32_t cols, int32_t it
                           float* ms_per_launch);
 
 /* Average device time (ms) of `iters` decode steps (graph replays) at
- * positions pos, pos+1, ...; tokens are fed back on the device. */
+ * positions pos, pos+1, ...; tokens are fed back on the device, and the
+ * state is copied once: each step's final norm advances it for the next. */
 int c2h_time_steps(c2h_ctx* ctx, int32_t pos, int32_t iters, float penalty, int32_t im_end, int32_t eos,
                    float* ms_per_step);
 

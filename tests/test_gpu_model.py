@@ -119,6 +119,36 @@ def test_greedy_stream_tiny(tiny):
     orc2.close()
 
 
+def test_device_fed_steps_match_host_loop(tiny):
+    # c2h_time_steps copies the state once and lets each step's final norm
+    # advance it; its tokens, KV and normX must equal those of c2h_step
+    # calls, and c2h_step must continue from where it stopped
+    gf, ctx, orc, im_end, eos = tiny
+    prompt = np.random.default_rng(33).integers(0, 4096, 32).astype(np.int32)
+
+    def ingest():
+        ctx.set_token_ids(0, prompt)
+        for p, t in enumerate(prompt):
+            ctx.forward(int(t), p, want_normx=False)
+
+    ingest()
+    host = [ctx.step(32 + i, PENALTY, im_end, eos) for i in range(24)]
+    ctx.sync()
+    want_ids = ctx.token_ids(32, 24)
+    want_kv = [ctx.kv(w, l, h, 56) for w in (0, 1) for l in range(2) for h in range(2)]
+    want_nx = ctx.normx()
+    assert np.array_equal(want_ids, np.array(host, np.int32))
+    ingest()
+    ctx.time_steps(32, 20, PENALTY, im_end, eos)
+    tail = [ctx.step(52 + i, PENALTY, im_end, eos) for i in range(4)]
+    ctx.sync()
+    assert tail == host[20:]
+    assert np.array_equal(ctx.token_ids(32, 24), want_ids)
+    for got, want in zip([ctx.kv(w, l, h, 56) for w in (0, 1) for l in range(2) for h in range(2)], want_kv):
+        assert np.array_equal(bits(got), bits(want))
+    assert np.array_equal(bits(ctx.normx()), bits(want_nx))
+
+
 def test_session_differential_ingestion(tiny):
     # c2slm_test.go:60-105: prefix then suffix == one shot, bit for bit
     gf, ctx, orc, _, _ = tiny
