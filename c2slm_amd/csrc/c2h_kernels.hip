@@ -678,20 +678,74 @@ __device__ __forceinline__ void store_item(float* row_terms, int type, int b, in
   if (type == T_Q4_K || u == 0) row_terms[4 * b + u] = v;
 }
 
+// A row's 4*NB term slots (16-byte aligned) into registers, read whole
+// whatever the type: every read is issued before the first add, and a
+// second row's reads with them (a read after the type branch was a second
+// LDS round trip per row).
+template <int NB>
+struct RowTerms {
+  float4 t[NB];
+};
+template <int NB>
+__device__ __forceinline__ RowTerms<NB> read_terms(const float* row_terms) {
+  RowTerms<NB> r;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) r.t[b] = reinterpret_cast<const float4*>(row_terms)[b];
+  return r;
+}
+// Uses every slot unconditionally, so the compiler keeps the reads ahead of
+// the type branch instead of sinking the ones a type needs into it.
+template <int NB>
+__device__ __forceinline__ void pin_terms(RowTerms<NB>& r) {
+#pragma unroll
+  for (int b = 0; b < NB; ++b) asm volatile("" : "+v"(r.t[b].x), "+v"(r.t[b].y), "+v"(r.t[b].z), "+v"(r.t[b].w));
+}
 // Fold of one row in the reference's order: Q4_K acc += term over (block,
 // pair), c2_tensor_dot_q4_k_q8_k_gen.go:85; Q6_K acc += f32(isum)*(d*q8d)
 // over blocks, c2_tensor_gemv2_q6_k_q8_k_gen.go:208-209.
 template <int NB>
-__device__ __forceinline__ float fold_terms(int type, const float* row_terms) {
+__device__ __forceinline__ float fold_terms(int type, const RowTerms<NB>& r) {
   float acc = 0.0f;
   if (type == T_Q4_K) {
 #pragma unroll
-    for (int i = 0; i < 4 * NB; ++i) acc = acc + row_terms[i];
+    for (int b = 0; b < NB; ++b) {
+      acc = acc + r.t[b].x;
+      acc = acc + r.t[b].y;
+      acc = acc + r.t[b].z;
+      acc = acc + r.t[b].w;
+    }
   } else {
 #pragma unroll
-    for (int b = 0; b < NB; ++b) acc = acc + row_terms[4 * b];
+    for (int b = 0; b < NB; ++b) acc = acc + r.t[b].x;
   }
   return acc;
+}
+// Two rows of one type (gate and up): the two chains in one branch, so
+// their adds interleave.
+template <int NB>
+__device__ __forceinline__ void fold_terms2(int type, const RowTerms<NB>& r, const RowTerms<NB>& q, float& a,
+                                            float& c) {
+  a = 0.0f;
+  c = 0.0f;
+  if (type == T_Q4_K) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      a = a + r.t[b].x;
+      c = c + q.t[b].x;
+      a = a + r.t[b].y;
+      c = c + q.t[b].y;
+      a = a + r.t[b].z;
+      c = c + q.t[b].z;
+      a = a + r.t[b].w;
+      c = c + q.t[b].w;
+    }
+  } else {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      a = a + r.t[b].x;
+      c = c + q.t[b].x;
+    }
+  }
 }
 
 // ------------------------------------------------------------- prologues
@@ -885,9 +939,19 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(GemvPar
   if (tid < RPW) {
     const int r = row0 + tid;
     if (r < J.rows) {
-      const float acc = fold_terms<NB>(J.type, &terms[0][tid * IPR]);
+      RowTerms<NB> tg = read_terms<NB>(&terms[0][tid * IPR]);
+      RowTerms<NB> tu;
+      if (PAIRED) tu = read_terms<NB>(&terms[PAIRED ? 1 : 0][tid * IPR]);
+      pin_terms(tg);
+      if (PAIRED) pin_terms(tu);
+      float acc, up = 0.0f;
+      if (PAIRED && J.type == J.type2) {
+        fold_terms2<NB>(J.type, tg, tu, acc, up);
+      } else {
+        acc = fold_terms<NB>(J.type, tg);
+        if (PAIRED) up = fold_terms<NB>(J.type2, tu);
+      }
       if (PAIRED) {
-        const float up = fold_terms<NB>(J.type2, &terms[PAIRED ? 1 : 0][tid * IPR]);
         const int n8 = J.rows - (J.rows % 8);
         J.y[r] = (r < n8) ? swiglu_poly(acc, up) : swiglu_tail(acc, up);
       } else if (MODE == MODE_BIAS) {
