@@ -87,6 +87,8 @@ def lib():
             "c2h_time_vocab": (C.c_int, [VP, I32, I32, I32, C.POINTER(C.c_float)]),
             "c2h_copy_bench": (C.c_int, [VP, C.c_int64, I32, C.POINTER(C.c_float)]),
             "c2h_launch_floor": (C.c_int, [VP, I32, I32, I32, C.POINTER(C.c_float)]),
+            "c2h_check_rms_scale": (C.c_int, [VP, C.c_uint32, C.c_uint64, C.POINTER(C.c_uint64),
+                                              C.POINTER(C.c_uint32)]),
             "c2h_time_steps": (C.c_int, [VP, I32, I32, C.c_float, I32, I32, C.POINTER(C.c_float)]),
             "c2h_gemv_f32": (C.c_int, [VP, I32, VP, VP, I32, I32, VP]),
             "c2h_gemv_f32_dev": (C.c_int, [VP, I32, VP, VP, I32, I32, VP]),
@@ -232,6 +234,13 @@ class Ctx:
         us = C.c_float()
         self._chk(lib().c2h_launch_floor(self.h, n, grid, reps, C.byref(us)))
         return us.value
+
+    def check_rms_scale(self, lo: int, hi: int) -> tuple[int, int]:
+        """(mismatches, lowest mismatching bit pattern) of the kernels' RMSNorm
+        scale against the IEEE sqrt and division over patterns [lo, hi)."""
+        bad, first = C.c_uint64(), C.c_uint32()
+        self._chk(lib().c2h_check_rms_scale(self.h, lo, hi, C.byref(bad), C.byref(first)))
+        return bad.value, first.value
 
     def time_steps(self, pos: int, iters: int, penalty: float, im_end: int, eos: int) -> float:
         ms = C.c_float()

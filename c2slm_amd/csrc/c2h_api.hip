@@ -1949,6 +1949,32 @@ int c2h_copy_bench(c2h_ctx* c, int64_t bytes, int32_t reps, float* ms) {
   return C2H_OK;
 }
 
+int c2h_check_rms_scale(c2h_ctx* c, uint32_t lo, uint64_t hi, uint64_t* mismatches, uint32_t* first_bits) {
+  if (!c || !mismatches || !first_bits || hi > (1ull << 32) || hi < lo) return C2H_ERR_INVALID;
+  HIPCHK(c, hipSetDevice(c->device));
+  unsigned long long* bad = nullptr;
+  hipError_t e = hipMalloc(&bad, 16);
+  uint32_t* first = reinterpret_cast<uint32_t*>(bad + 1);
+  if (e == hipSuccess) e = hipMemsetAsync(bad, 0, 8, c->stream);
+  if (e == hipSuccess) e = hipMemsetAsync(first, 0xff, 4, c->stream);
+  constexpr uint64_t kChunk = 1ull << 28;  // patterns per launch (2^20 workgroups)
+  for (uint64_t b = lo; e == hipSuccess && b < hi; b += kChunk) {
+    const uint32_t n = (uint32_t)std::min<uint64_t>(kChunk, hi - b);
+    hipLaunchKernelGGL(k_check_rms_scale, dim3((n + 255) / 256), dim3(256), 0, c->stream, (uint32_t)b, n, bad, first);
+    e = hipGetLastError();
+  }
+  unsigned long long nb = 0;
+  uint32_t fb = 0;
+  if (e == hipSuccess) e = hipMemcpyAsync(&nb, bad, 8, hipMemcpyDeviceToHost, c->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(&fb, first, 4, hipMemcpyDeviceToHost, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (bad) (void)hipFree(bad);
+  if (e != hipSuccess) return fail(c, C2H_ERR_HIP, "rms scale check: %s", hipGetErrorString(e));
+  *mismatches = nb;
+  *first_bits = fb;
+  return C2H_OK;
+}
+
 int c2h_launch_floor(c2h_ctx* c, int32_t n, int32_t grid, int32_t reps, float* us) {
   if (!c || !us || n <= 0 || n > 4096 || grid <= 0 || grid > 65536 || reps <= 0) return C2H_ERR_INVALID;
   HIPCHK(c, hipSetDevice(c->device));

@@ -449,5 +449,6 @@ __host__ __device__ inline int dot_rows_lds_bytes(int type, int cols) {
 __global__ void k_argmax_final(const float* pv, const int* pi, int n, C2hState* state);
 __global__ void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16);
 __global__ void k_empty(const int* __restrict__ flag, int* __restrict__ out);
+__global__ void k_check_rms_scale(uint32_t lo, uint32_t n, unsigned long long* bad, uint32_t* first);
 
 }  // namespace c2h

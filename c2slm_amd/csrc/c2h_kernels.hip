@@ -475,6 +475,39 @@ __device__ __forceinline__ float seq_sum_wave_n(const float* a, int n) {
   return chunk_chain(a, min((m + 1) * C, n), n, lane_value(S, m + 1));
 }
 
+// f32(1/sqrt(f64(v))), the RMSNorm scale of tensor/ops.go:207-218 (and of
+// the Qwen3 QK-norm).  For a normal positive v: the f64 reciprocal square
+// root estimate, one Newton step, rounded to f32 -- equal to the IEEE square
+// root and division it replaces for every normal positive float (checked
+// over all of them by c2h_check_rms_scale; the estimate alone differs for
+// 9 % of them), ~8 dependent operations instead of ~30.  Other v (zero,
+// subnormal, infinite, NaN, negative) take the IEEE operations.
+__device__ __forceinline__ float rms_scale(float v) {
+  if (v >= __FLT_MIN__ && v <= __FLT_MAX__) {
+    const double x = (double)v;
+    const double y = __builtin_amdgcn_rsq(x);
+    const double r = __builtin_fma(-(x * y), 0.5 * y, 0.5);
+    return (float)__builtin_fma(y, r, y);
+  }
+  return (float)(1.0 / sqrt((double)v));
+}
+
+// rms_scale against the IEEE operations over the bit patterns [lo, lo + n);
+// mismatches counted in *bad, the lowest mismatching pattern in *first.
+__global__ void __launch_bounds__(256) k_check_rms_scale(uint32_t lo, uint32_t n, unsigned long long* bad,
+                                                         uint32_t* first) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t bits = lo + i;
+  const float v = __uint_as_float(bits);
+  const float want = (float)(1.0 / sqrt((double)v));
+  const float got = rms_scale(v);
+  if (__float_as_uint(want) != __float_as_uint(got) && !(want != want && got != got)) {
+    atomicAdd(bad, 1ull);
+    atomicMin(first, bits);
+  }
+}
+
 // 1/rms of n values (n <= 4*blockDim.x, a multiple of 4) held as elements
 // 4t..4t+3 by thread t < n/4, tensor/ops.go:207-218: sequential f32 sum of
 // x*x, inv = f32(1/sqrt(f64(sum/n + eps))).  sq: LDS scratch of
@@ -485,7 +518,7 @@ __device__ __forceinline__ float rms_inv4(const float4& x, int n, float eps, flo
   __syncthreads();
   if (tid < 64) {
     const float s = (n <= 64 * SPEC_C) ? seq_sum_wave(sq, n) : seq_sum_wave_n(sq, n);
-    if (tid == 0) *inv_slot = (float)(1.0 / sqrt((double)(s / (float)n + eps)));
+    if (tid == 0) *inv_slot = rms_scale(s / (float)n + eps);
   }
   __syncthreads();
   return *inv_slot;
@@ -1901,11 +1934,11 @@ __global__ void __launch_bounds__(256) k_attn_h128(AttnCoreParams P) {
   if (has_q_norm || has_k_norm) {
     if (tid < 64 && has_q_norm) {
       const float s = seq_sum_wave(sq_s[0], HD);
-      if (tid == 0) inv_s[0] = (float)(1.0 / sqrt((double)(s / (float)HD + P.eps)));
+      if (tid == 0) inv_s[0] = rms_scale(s / (float)HD + P.eps);
     }
     if (tid >= 128 && tid < 192 && has_k_norm) {
       const float s = seq_sum_wave(sq_s[1], HD);
-      if (tid == 128) inv_s[1] = (float)(1.0 / sqrt((double)(s / (float)HD + P.eps)));
+      if (tid == 128) inv_s[1] = rms_scale(s / (float)HD + P.eps);
     }
     __syncthreads();
     if (role == 0 ? has_q_norm : has_k_norm) qkv_s[role][e] = (own * inv_s[role]) * nwt;

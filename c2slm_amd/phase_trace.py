@@ -44,13 +44,25 @@ __device__ __forceinline__ int phase_kind() {
          : (PRO == PRO_QUANT && MODE == MODE_RESID)             ? 3
                                                                 : -1;
 }
-#define PH_G(k) do { const int kd_ = phase_kind<NB, PRO, MODE>(); \
+// Stamps go to LDS (lane 0 of each wave, its own row) and are copied to
+// g_phase once, at the kernel's end: a global store per stamp would be
+// counted by vmcnt, and the kernel's own waits for its loads would then
+// wait for the stamps' stores too.
+#define PH_DECL \
+  __shared__ long long ph_s_[8][16]; \
+  if ((threadIdx.x & 63) == 0) \
+    for (int k_ = 0; k_ < 16; ++k_) ph_s_[threadIdx.x >> 6][k_] = 0
+#define PH_G(k) do { if ((threadIdx.x & 63) == 0) ph_s_[threadIdx.x >> 6][k] = __builtin_amdgcn_s_memtime(); } while (0)
+#define PH_G_END do { const int kd_ = phase_kind<NB, PRO, MODE>(); \
   if (kd_ >= 0 && (threadIdx.x & 63) == 0 && blockIdx.y == 0 && (blockIdx.x == 0 || blockIdx.x == gridDim.x - 1)) \
-    g_phase[kd_][blockIdx.x == 0 ? 0 : 1][threadIdx.x >> 6][k] = __builtin_amdgcn_s_memtime(); } while (0)
-#define PH_AT(k, t) do { const bool f_ = h == 0; \
+    for (int k_ = 0; k_ < 16; ++k_) \
+      g_phase[kd_][blockIdx.x == 0 ? 0 : 1][threadIdx.x >> 6][k_] = ph_s_[threadIdx.x >> 6][k_]; } while (0)
+#define PH_AT(k, t) do { if ((threadIdx.x & 63) == 0) ph_s_[threadIdx.x >> 6][k] = (t); } while (0)
+#define PH_A_END do { const bool f_ = h == 0; \
   const bool l_ = h == P.n_heads - 1; \
   if ((threadIdx.x & 63) == 0 && blockIdx.z == 0 && (f_ || l_)) \
-    g_phase[TIER == ATT_TIER_ANY ? 5 : 4][f_ ? 0 : 1][threadIdx.x >> 6][k] = (t); } while (0)
+    for (int k_ = 0; k_ < 16; ++k_) \
+      g_phase[TIER == ATT_TIER_ANY ? 5 : 4][f_ ? 0 : 1][threadIdx.x >> 6][k_] = ph_s_[threadIdx.x >> 6][k_]; } while (0)
 #define PH_A(k) PH_AT(k, __builtin_amdgcn_s_memtime())
 """
 
@@ -72,6 +84,8 @@ def instrument(kernels: str) -> str:
     s = kernels.replace("namespace c2h {\n", _STAMPS, 1)
     s = _patch(s, "__global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(GemvParams P) {",
                "#define C2H_GEMV_ROW(NB_, PRO_, MODE_)", [
+                   ("  constexpr int NT = row_threads(NB, PRO, MODE);\n",
+                    "  PH_DECL;\n  constexpr int NT = row_threads(NB, PRO, MODE);\n"),
                    ("  const GemvJob J = launch_job(P);", "  PH_G(0);\n  const GemvJob J = launch_job(P);"),
                    ("  if ((int)blockIdx.x >= J.n_wg) return;  // uniform: the launch's widest job sets the grid\n",
                     "  if ((int)blockIdx.x >= J.n_wg) return;  // uniform: the launch's widest job sets the grid\n"
@@ -84,11 +98,11 @@ def instrument(kernels: str) -> str:
                     "  PH_G(6);\n  // ---- items\n"),
                    ("  // ---- per-row fold in the reference's order, then the epilogue\n",
                     "  PH_G(7);\n  // ---- per-row fold in the reference's order, then the epilogue\n"),
-               ]).replace("PH_END;", "PH_G(8);", 1)
+               ]).replace("PH_END;", "PH_G(8);\n  PH_G_END;", 1)
     s = _patch(s, "template <int TIER>\n__global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {",
                "template __global__ void k_attn_core<ATT_TIER_32>(AttnCoreParams);", [
                    ('  asm volatile("" ::"s"(P.q), "s"(P.k), "s"(P.v), "s"(P.kv),',
-                    '  const long long ph_entry_ = __builtin_amdgcn_s_memtime();\n'
+                    '  PH_DECL;\n  const long long ph_entry_ = __builtin_amdgcn_s_memtime();\n'
                     '  asm volatile("" ::"s"(P.q), "s"(P.k), "s"(P.v), "s"(P.kv),'),
                    ('"s"(P.scale), "s"(P.store_kv));\n', '"s"(P.scale), "s"(P.store_kv));\n'
                     '  const long long ph_args_ = __builtin_amdgcn_s_memtime();\n'),
@@ -116,7 +130,7 @@ def instrument(kernels: str) -> str:
                     "    });\n    PH_A(6);\n    // both roles pass nch barriers, one per chunk\n"),
                    ("  if (tid < HD) {\n    acc = __builtin_fmaf(sc[pos], v_s[d], acc);\n",
                     "  PH_A(7);\n  if (tid < HD) {\n    acc = __builtin_fmaf(sc[pos], v_s[d], acc);\n"),
-               ]).replace("PH_END;", "PH_A(8);", 1)
+               ]).replace("PH_END;", "PH_A(8);\n  PH_A_END;", 1)
     return s
 
 

@@ -286,6 +286,15 @@ int c2h_copy_bench(c2h_ctx* ctx, int64_t bytes, int32_t reps, float* ms_per_copy
  * floor a chain of decode kernels pays per launch. */
 int c2h_launch_floor(c2h_ctx* ctx, int32_t n, int32_t grid, int32_t reps, float* us_per_kernel);
 
+/* Self-check with no counterpart in the reference: the RMSNorm scale
+ * f32(1/sqrt(f64(v))) as the kernels compute it (a reciprocal square root
+ * estimate and one Newton step for normal positive v) against the IEEE
+ * square root and division, for every float whose bit pattern lies in
+ * [lo, hi) (hi <= 2^32); *mismatches receives their number (0 expected, NaN
+ * results of either form equal) and *first_bits the lowest mismatching
+ * pattern (0xffffffff if none). */
+int c2h_check_rms_scale(c2h_ctx* ctx, uint32_t lo, uint64_t hi, uint64_t* mismatches, uint32_t* first_bits);
+
 /* Kernels of one decoder layer, for c2h_time_layer_kernel. */
 #define C2H_KERNEL_QKV 0        /* RMSNorm + Q8_K + q|k|v GEMV + bias */
 #define C2H_KERNEL_ATTN 1       /* RoPE, KV store, scores, softmax, AV */

@@ -23,6 +23,15 @@ def bits(a):
     return np.asarray(a, np.float32).view(np.uint32)
 
 
+def test_rms_scale_every_float(ctx):
+    # The RMSNorm scale f32(1/sqrt(f64(v))) of tensor/ops.go:212-214 as the
+    # kernels compute it (for normal positive v a reciprocal square root
+    # estimate and one Newton step) equals the IEEE square root and division
+    # for every one of the 2^32 bit patterns.
+    bad, first = ctx.check_rms_scale(0, 1 << 32)
+    assert bad == 0, f"{bad} mismatches, first at {first:#010x}"
+
+
 @pytest.mark.parametrize("cols", [256, 512, 896, 4864, 16384])
 def test_quantize_q8k_bitexact(ctx, cols):
     rng = np.random.default_rng(cols)
