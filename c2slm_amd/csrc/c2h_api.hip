@@ -59,6 +59,7 @@ struct c2h_ctx {
   float* kv = nullptr;
   int32_t* token_ids = nullptr;
   float *rope_cos = nullptr, *rope_sin = nullptr;
+  std::vector<float> rope_cos_h, rope_sin_h;  // head_dim 64: host copies for the state's RoPE row
   float* part_v = nullptr;
   int* part_i = nullptr;
   int n_part = 0;
@@ -723,6 +724,11 @@ void enqueue_final_norm(c2h_ctx* c, int advance = 0) {
   N.state = c->state_dev;
   N.n_lds = chain_lds_floats(D.n_embd);
   N.advance = advance;
+  if (D.head_dim == 64) {  // the advance leaves the next position's RoPE row in the state
+    N.rope_cos = c->rope_cos;
+    N.rope_sin = c->rope_sin;
+    N.rope_len = D.max_ctx;
+  }
   hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(norm_threads(D.n_embd)), (size_t)N.n_lds * sizeof(float), c->stream, N);
 }
 
@@ -821,7 +827,13 @@ int push_state(c2h_ctx* c, const C2hState& s) {
   c->state_pred_valid = false;
   unsigned slot = c->ring_next++ % kStateRing;
   if (slot == 0 && c->ring_next > 1) HIPCHK(c, hipStreamSynchronize(c->stream));
-  c->state_ring[slot] = s;
+  C2hState& t = c->state_ring[slot];
+  t = s;
+  if (!c->rope_cos_h.empty()) {  // the RoPE row of pos, as the decode attention tiers read it
+    const int rp = std::min(std::max(s.pos, 0), c->desc.max_ctx - 1);
+    memcpy(t.rope, &c->rope_cos_h[(size_t)rp * 32], 32 * 4);
+    memcpy(t.rope + 32, &c->rope_sin_h[(size_t)rp * 32], 32 * 4);
+  }
   HIPCHK(c, hipMemcpyAsync(c->state_dev, &c->state_ring[slot], sizeof(C2hState), hipMemcpyHostToDevice, c->stream));
   return C2H_OK;
 }
@@ -1004,6 +1016,10 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
     if (stream_copy(c->stream, c->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
         stream_copy(c->stream, c->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
       return bail(fail(c, C2H_ERR_HIP, "rope upload"));
+    if (half == 32) {
+      c->rope_cos_h = std::move(cs);
+      c->rope_sin_h = std::move(sn);
+    }
   }
   if ((rc = vocab_grid(c, D.n_vocab, D.n_embd, &c->n_part))) return bail(rc);
   if ((rc = dalloc(c, &c->part_v, (size_t)c->n_part * 4)) || (rc = dalloc(c, &c->part_i, (size_t)c->n_part * 4)) ||

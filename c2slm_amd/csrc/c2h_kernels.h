@@ -16,6 +16,9 @@ struct C2hState {
   int32_t nx_in;    // normX buffer read by the vocab projection
   int32_t nx_out;   // normX buffer written by the final RMSNorm
   int32_t seq;      // step number, handed to the host with the step's token
+  // head_dim 64: the RoPE row of pos (cos at [0, 32), sin at [32, 64)), so
+  // that decode attention reads it with pos instead of after it
+  float rope[64];
 };
 
 // Q8_K row as the GEMVs keep it in LDS: quants packed four per dword, the
@@ -142,7 +145,10 @@ struct NormParams {
   float* out;
   float* out_buf[2];
   C2hState* state;
-  int advance;  // step graphs: leave the state of the next step (pos, seq, normX buffers)
+  int advance;  // step graphs: leave the state of the next step (pos, seq, normX buffers, RoPE row)
+  const float* rope_cos;  // head_dim 64: the RoPE table the advance takes the next row from (else nullptr)
+  const float* rope_sin;
+  int rope_len;
 };
 
 // KV cache: [K|V][layer][kv head][kv_slot(max_ctx)][hd] floats.  K rows are

@@ -1328,19 +1328,34 @@ __global__ void __launch_bounds__(512) k_rmsnorm(NormParams P) {
   float* sq = reinterpret_cast<float*>(smem);
   __shared__ float inv_slot;
   asm volatile("" ::"s"(P.x), "s"(P.w), "s"(P.n), "s"(P.eps), "s"(P.out_sel), "s"(P.out), "s"(P.out_buf[0]),
-               "s"(P.out_buf[1]), "s"(P.state), "s"(P.advance));
+               "s"(P.out_buf[1]), "s"(P.state), "s"(P.advance), "s"(P.rope_cos), "s"(P.rope_sin), "s"(P.rope_len));
   const float4 x = load4(P.x, P.n);
   const float4 w = load4(P.w, P.n);
   const int nx_out = P.out_sel ? P.state->nx_out : 0;  // with the loads, not after the sum
+  const int pos = P.advance ? P.state->pos : 0;
   issue_fence();
+  // the next position's RoPE row, loaded by wave 1 (idle during wave 0's
+  // sum) and stored with the rest of the advance
+  const int rt = (int)threadIdx.x - 64;
+  const bool rope_lane = P.advance && P.rope_cos != nullptr && rt >= 0 && rt < 32;
+  float rc = 0.0f, rs = 0.0f;
+  if (rope_lane) {
+    const int rp = min(max(pos + 1, 0), P.rope_len - 1);
+    rc = P.rope_cos[(size_t)rp * 32 + rt];
+    rs = P.rope_sin[(size_t)rp * 32 + rt];
+  }
   const float inv = rms_inv4(x, P.n, P.eps, sq, &inv_slot);
   float* out = P.out_sel ? P.out_buf[nx_out] : P.out;
   if (4 * (int)threadIdx.x < P.n) reinterpret_cast<float4*>(out)[threadIdx.x] = norm4(x, inv, w);
   if (P.advance) {
     __syncthreads();  // every thread has read the state
+    C2hState* st = P.state;
+    if (rope_lane) {
+      st->rope[rt] = rc;
+      st->rope[32 + rt] = rs;
+    }
     if (threadIdx.x == 0) {
-      C2hState* st = P.state;
-      st->pos = st->pos + 1;
+      st->pos = pos + 1;
       st->seq = st->seq % 0x7ffffffe + 1;
       st->nx_in = nx_out;
       st->nx_out = nx_out ^ 1;
@@ -1607,24 +1622,18 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   const float* ksrc = P.k + (size_t)ti * P.kv_ld + g * HD;
   const float* vsrc = P.v + (size_t)ti * P.kv_ld + g * HD;
   const float own = ((bm == 0) ? qsrc : ((bm == 1) ? ksrc : vsrc))[tid & 63];
+  // the position, and for a tier its RoPE row from the state: issued now,
+  // first used (waited for) after a tier's K/V loads are issued
+  int pos_state = P.state->pos;
+  float rcos = 0.0f, rsin = 0.0f;
+  if constexpr (!ANY) {
+    rcos = P.state->rope[tid & 31];
+    rsin = P.state->rope[32 + (tid & 31)];
+  }
   issue_fence();
-  const int pos = P.state->pos + ti;
-  const int T = pos + 1;
   const size_t head_stride = (size_t)kv_slot(P.max_ctx) * HD;
   float* kcache = P.kv + ((size_t)P.layer * P.n_kv_heads + g) * head_stride;
   float* vcache = P.kv + (((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * head_stride;
-  const int nstored = max(min(pos, P.max_ctx), 0);    // cached positions [0, nstored)
-  const int nch = (pos + ATT_CH - 1) / ATT_CH;         // V chunks of positions [0, pos)
-  // the stored rows as buffers: prefetch slots past them read zeros without
-  // memory traffic
-  const __amdgpu_buffer_rsrc_t krs = cache_rsrc(kcache, nstored * HD * 4);
-  const __amdgpu_buffer_rsrc_t vrs = cache_rsrc(vcache, ((nstored + 3) >> 2) * HD * 16);
-
-  // ---- loads, in the order they are consumed
-  const int rp = min(max(pos, 0), P.rope_len - 1);
-  const float rcos = P.rope_cos[(size_t)rp * (HD / 2) + (tid & 31)];
-  const float rsin = P.rope_sin[(size_t)rp * (HD / 2) + (tid & 31)];
-  issue_fence();  // q/k/v and the RoPE row are needed first: issue them first
   // K chunk 0, coalesced: 16-byte piece i = tid + 256k of the chunk is row
   // i/16, columns 4(i%16)..+3 (a tier reads its TIER rows); V: wave w holds
   // quads w + 4i of the tier's rows, or of chunk 0.
@@ -1633,11 +1642,43 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   const int wave = tid >> 6;
   f32x4_t kc[KL];  // native vectors: a float4 array copied whole is kept in scratch
   f32x4_t vreg[VQW];
+  if constexpr (!ANY) {
+    // A tier's rows are issued before the position is read (a load of the
+    // device state, ~1,000 clk): their buffers span the head's whole cache.
+    // Rows at and past pos hold an earlier sequence's values, or none, and
+    // are never used: the scores stop at T (the row at pos is this
+    // launch's k) and V is zeroed past pos before the chain.
+    const int nall = kv_slot(P.max_ctx);
+    const __amdgpu_buffer_rsrc_t krs0 = cache_rsrc(kcache, nall * HD * 4);
+    const __amdgpu_buffer_rsrc_t vrs0 = cache_rsrc(vcache, (nall >> 2) * HD * 16);
 #pragma unroll
-  for (int k = 0; k < KL; ++k) kc[k] = cache_ld4(krs, (tid + 256 * k) * 16);
+    for (int k = 0; k < KL; ++k) kc[k] = cache_ld4(krs0, (tid + 256 * k) * 16);
 #pragma unroll
-  for (int i = 0; i < VQW; ++i) vreg[i] = vquad_load_buf(vrs, wave + 4 * i);
-  issue_fence();
+    for (int i = 0; i < VQW; ++i) vreg[i] = vquad_load_buf(vrs0, wave + 4 * i);
+    issue_fence();
+  }
+  asm volatile("" : "+v"(pos_state));
+  const int pos = __builtin_amdgcn_readfirstlane(pos_state) + ti;
+  const int T = pos + 1;
+  const int nstored = max(min(pos, P.max_ctx), 0);    // cached positions [0, nstored)
+  const int nch = (pos + ATT_CH - 1) / ATT_CH;         // V chunks of positions [0, pos)
+  // the any tier's rows: the stored ones as buffers, whose slots past them
+  // read zeros without memory traffic
+  const __amdgpu_buffer_rsrc_t krs = cache_rsrc(kcache, nstored * HD * 4);
+  const __amdgpu_buffer_rsrc_t vrs = cache_rsrc(vcache, ((nstored + 3) >> 2) * HD * 16);
+
+  // ---- loads, in the order they are consumed
+  if constexpr (ANY) {  // a batch of query tokens: each its own row of the table
+    const int rp = min(max(pos, 0), P.rope_len - 1);
+    rcos = P.rope_cos[(size_t)rp * (HD / 2) + (tid & 31)];
+    rsin = P.rope_sin[(size_t)rp * (HD / 2) + (tid & 31)];
+    issue_fence();  // q/k/v and the RoPE row are needed first: issue them first
+#pragma unroll
+    for (int k = 0; k < KL; ++k) kc[k] = cache_ld4(krs, (tid + 256 * k) * 16);
+#pragma unroll
+    for (int i = 0; i < VQW; ++i) vreg[i] = vquad_load_buf(vrs, wave + 4 * i);
+    issue_fence();
+  }
 
   if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;
   __syncthreads();

@@ -117,8 +117,8 @@ def instrument(kernels: str) -> str:
                     "    if (sc[0] != sc[0]) mx = sc[0];\n    PH_A(12);\n    for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));\n    if constexpr (!ANY && TIER <= SUM_DIRECT_N) pad_chain(sc, T);\n    __syncthreads();\n    PH_A(13);\n"),
                    ("      while_summing();\n    }\n",
                     "      while_summing();\n    }\n    PH_A(14);\n"),
-                   ("  issue_fence();\n\n  if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;\n  __syncthreads();\n",
-                    "  issue_fence();\n  PH_A(2);\n\n  if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;\n"
+                   ("\n\n  if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;\n  __syncthreads();\n",
+                    "\n  PH_A(2);\n\n  if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;\n"
                     "  __syncthreads();\n  PH_A(3);\n"),
                    ("  __syncthreads();\n\n  // (a batch of query tokens",
                     "  __syncthreads();\n  PH_A(4);\n\n  // (a batch of query tokens"),
