@@ -26,10 +26,10 @@ struct C2hState {
 // Block rows are padded to 68 dwords so that neighbouring blocks start in
 // different LDS banks.
 template <int NB>
-struct Q8KRow {
+struct alignas(16) Q8KRow {
   uint32_t q[NB][68];
+  int32_t bs[NB][16];  // 16-byte aligned rows (an item reads its sums whole)
   float d[NB];
-  int32_t bs[NB][16];
 };
 constexpr int LDS_Q8K_BLOCKS = 64;  // 16384 columns (the reference's Q8_K scratch, engine/pool.go:59)
 typedef Q8KRow<LDS_Q8K_BLOCKS> Q8KLds;

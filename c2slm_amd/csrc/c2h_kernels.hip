@@ -580,12 +580,40 @@ __device__ __forceinline__ uint32_t u4get(const uint4& v, int i) {
 
 __device__ __forceinline__ uint32_t byte_of(const uint4& v, int i) { return (u4get(v, i >> 2) >> (8 * (i & 3))) & 0xffu; }
 
+// The LDS operands of one item, read whole at its start (16-byte reads, one
+// round trip, where reads placed by the compiler next to their uses took
+// three): the Q8_K quants (Q4_K: 16u .. 16u+15; Q6_K: half n = u>>1, lanes
+// [16c, 16c+16) with c = u&1, quants 32n + 4c + 8k .. +3 for k = 0..3),
+// the block sums (Q4_K: 4u .. 4u+3; Q6_K: 8n .. 8n+7) and the scale of
+// block b.  Both formats read the same amount (addresses by arithmetic).
+struct ItemQ8 {
+  uint4 q[4];
+  int4 bs[2];
+  float d;
+};
+template <class Row>
+__device__ __forceinline__ ItemQ8 read_item_q8(const Row& s, int type, int b, int u) {
+  const bool q4 = (type == T_Q4_K);
+  // in 16-byte units of the block's row (rows are 16-byte aligned)
+  const uint4* qrow = reinterpret_cast<const uint4*>(s.q[b]);
+  const int4* brow = reinterpret_cast<const int4*>(s.bs[b]);
+  const int qi = q4 ? 4 * u : 8 * (u >> 1) + (u & 1);
+  const int qs = q4 ? 1 : 2;
+  const int bi = q4 ? u : 2 * (u >> 1);
+  ItemQ8 r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) r.q[k] = qrow[qi + qs * k];
+  r.bs[0] = brow[bi];
+  r.bs[1] = brow[min(bi + 1, 3)];  // Q6_K's second four
+  r.d = s.d[b];
+  return r;
+}
+
 // Q4_K pair term (c2_tensor_dot_q4_k_q8_k_gen.go:38-85): s_lo, s_hi of pair u
 // of super-block b, folded with the block scales exactly as the reference.
-template <class Row>
-__device__ __forceinline__ float q4k_item(const ItemW& it, const Row& s, int b, int u, int32_t* lo_out,
+__device__ __forceinline__ float q4k_item(const ItemW& it, const ItemQ8& r, int u, int32_t* lo_out,
                                           int32_t* hi_out) {
-  const float q8d = s.d[b];
+  const float q8d = r.d;
   const float dW = fp16_simd_nb(it.a.x & 0xffffu) * q8d;
   const float mW = fp16_simd_nb(it.a.x >> 16) * q8d;
   // scale/min pairs 2u, 2u+1 (gen.go:47-61), branch-free in u: the scale
@@ -603,24 +631,23 @@ __device__ __forceinline__ float q4k_item(const ItemW& it, const Row& s, int b, 
                                  __builtin_amdgcn_ubfe(S0, o1, 6));
   const uint32_t m1 = blend_u32(hi_pair, __builtin_amdgcn_ubfe(S2, o1 + 4, 4) | (__builtin_amdgcn_ubfe(S1, o1 + 6, 2) << 4),
                                 __builtin_amdgcn_ubfe(S1, o1, 6));
-  const uint32_t* q8 = s.q[b] + 16 * u;
-  int lo = 0, hi = 0;
+  int lo = 0, hi = 0;  // quants i, 8+i (it.b) then 4+i, 12+i (it.c)
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     uint32_t q = u4get(it.b, i);
-    lo = sdot4((int)(q & 0x0f0f0f0fu), (int)q8[i], lo);
-    hi = sdot4((int)((q >> 4) & 0x0f0f0f0fu), (int)q8[8 + i], hi);
+    lo = sdot4((int)(q & 0x0f0f0f0fu), (int)u4get(r.q[0], i), lo);
+    hi = sdot4((int)((q >> 4) & 0x0f0f0f0fu), (int)u4get(r.q[2], i), hi);
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     uint32_t q = u4get(it.c, i);
-    lo = sdot4((int)(q & 0x0f0f0f0fu), (int)q8[4 + i], lo);
-    hi = sdot4((int)((q >> 4) & 0x0f0f0f0fu), (int)q8[12 + i], hi);
+    lo = sdot4((int)(q & 0x0f0f0f0fu), (int)u4get(r.q[1], i), lo);
+    hi = sdot4((int)((q >> 4) & 0x0f0f0f0fu), (int)u4get(r.q[3], i), hi);
   }
   *lo_out = lo;
   *hi_out = hi;
-  const float bA = (float)(s.bs[b][4 * u] + s.bs[b][4 * u + 1]);
-  const float bB = (float)(s.bs[b][4 * u + 2] + s.bs[b][4 * u + 3]);
+  const float bA = (float)(r.bs[0].x + r.bs[0].y);
+  const float bB = (float)(r.bs[0].z + r.bs[0].w);
   return (((float)lo * (dW * (float)sc0)) - (bA * (mW * (float)m0))) +
          (((float)hi * (dW * (float)sc1)) - (bB * (mW * (float)m1)));
 }
@@ -629,27 +656,30 @@ __device__ __forceinline__ float q4k_item(const ItemW& it, const Row& s, int b, 
 // with c = u&1 (c2_tensor_gemv2_q6_k_q8_k_gen.go:104-207): four (n,k) sums
 // s, each contributing (s - 32*bsum)*scale.  The four partials of a block
 // add up (exactly) to the reference's isum.
-template <class Row>
-__device__ __forceinline__ int32_t q6k_item(const ItemW& it, const Row& s, int b, int u) {
-  const int n = u >> 1, c = u & 1;
+__device__ __forceinline__ int32_t q6k_item(const ItemW& it, const ItemQ8& r, int u) {
+  const int c = u & 1;
   int32_t part = 0;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const uint4& ql = (k & 1) ? it.b : it.a;
-    const uint32_t* q8 = s.q[b] + 32 * n + 8 * k + 4 * c;
     int sum = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t qlv = u4get(ql, i);
       uint32_t lo = (k < 2) ? (qlv & 0x0f0f0f0fu) : ((qlv >> 4) & 0x0f0f0f0fu);
       uint32_t hi = ((u4get(it.c, i) >> (2 * k)) & 0x03030303u) << 4;
-      sum = sdot4((int)(lo | hi), (int)q8[i], sum);
+      sum = sdot4((int)(lo | hi), (int)u4get(r.q[k], i), sum);
     }
-    const int j = 8 * n + 2 * k + c;
+    // block sum 8n + 2k + c of the row: components fixed by k, a value
+    // select by c (an indexed pick would put the operands in scratch)
+    const int4 bv = (k < 2) ? r.bs[0] : r.bs[1];
+    const int b_c0 = (k & 1) ? bv.z : bv.x;
+    const int b_c1 = (k & 1) ? bv.w : bv.y;
+    const int bsum = c ? b_c1 : b_c0;
     const int jj = 2 * k + c;  // byte of scales[8n .. 8n+8)
     const uint32_t sw = (jj < 4) ? it.e.x : it.e.y;
     const int sc = (int)(int8_t)((sw >> (8 * (jj & 3))) & 0xffu);
-    part += (sum - 32 * s.bs[b][j]) * sc;
+    part += (sum - 32 * bsum) * sc;
   }
   return part;
 }
@@ -659,16 +689,17 @@ __device__ __forceinline__ int32_t q6k_item(const ItemW& it, const Row& s, int b
 template <class Row>
 __device__ __forceinline__ void run_item(const ItemW& it, int type, const Row& s, int b, int u, float* term_slot,
                                          float* dq_slot, int32_t* isums, size_t isum_base) {
+  const ItemQ8 r = read_item_q8(s, type, b, u);
   if (type == T_Q4_K) {
     int32_t lo, hi;
-    *term_slot = q4k_item(it, s, b, u, &lo, &hi);
+    *term_slot = q4k_item(it, r, u, &lo, &hi);
     if (isums) {
       isums[isum_base + 2 * u] = lo;
       isums[isum_base + 2 * u + 1] = hi;
     }
   } else {
-    *reinterpret_cast<int32_t*>(term_slot) = q6k_item(it, s, b, u);
-    if (u == 0) *dq_slot = fp16_simd(it.d) * s.d[b];
+    *reinterpret_cast<int32_t*>(term_slot) = q6k_item(it, r, u);
+    if (u == 0) *dq_slot = fp16_simd(it.d) * r.d;
   }
 }
 
@@ -696,14 +727,15 @@ __device__ __forceinline__ float fold_row(int type, const float* terms, const fl
 // always active together.
 template <class Row>
 __device__ __forceinline__ float item_value(const ItemW& it, int type, const Row& s, int b, int u) {
+  const ItemQ8 r = read_item_q8(s, type, b, u);
   if (type == T_Q4_K) {
     int32_t lo, hi;
-    return q4k_item(it, s, b, u, &lo, &hi);
+    return q4k_item(it, r, u, &lo, &hi);
   }
-  int32_t part = q6k_item(it, s, b, u);
+  int32_t part = q6k_item(it, r, u);
   part += dpp_i<DPP_QUAD_1032>(part);
   part += dpp_i<DPP_QUAD_2301>(part);
-  return (float)part * (fp16_simd_nb(it.d) * s.d[b]);
+  return (float)part * (fp16_simd_nb(it.d) * r.d);
 }
 
 // Item value into the row's term slots [4b + u] (Q6_K: once per block, at u == 0).
