@@ -728,6 +728,9 @@ __device__ __forceinline__ float fold_row(int type, const float* terms, const fl
 template <class Row>
 __device__ __forceinline__ float item_value(const ItemW& it, int type, const Row& s, int b, int u) {
   const ItemQ8 r = read_item_q8(s, type, b, u);
+  // the LDS reads go out before the weights' waits (the scheduler would
+  // otherwise hoist the nibble extraction, and its waits, above them)
+  __builtin_amdgcn_sched_barrier(0);
   if (type == T_Q4_K) {
     int32_t lo, hi;
     return q4k_item(it, r, u, &lo, &hi);
@@ -936,7 +939,9 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(GemvPar
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int it = SPLIT ? (tid & (NI - 1)) : tid;  // item index within its matrix
-  const int half = SPLIT ? tid / NI : 0;           // 0: gate (w), 1: up (w2); wave-uniform
+  // 0: gate (w), 1: up (w2); wave-uniform, and scalar so that the type
+  // tests on it branch on SCC, not per lane
+  const int half = SPLIT ? __builtin_amdgcn_readfirstlane(tid / NI) : 0;
   const int b = it / (4 * RPW);
   const int r_local = (it - b * 4 * RPW) >> 2;
   const int u = it & 3;
