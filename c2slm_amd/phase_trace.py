@@ -4,10 +4,11 @@
 c2slm_amd/_build/phase/ with `s_memtime` stamps at the phase boundaries of
 k_gemv_row (qkv, attn_out, ffn_in, ffn_out) and the tiers of k_attn_core,
 and links it as c2slm_amd/libc2h_phase.so (same C ABI plus
-c2h_phase_read).  Lane 0 of every wave of the first and the last workgroup
-of each launch stores its stamp per phase into a device array; every later
-launch of the same kernel overwrites it, so a read after a run holds the
-last launch's stamps.  The product library is untouched.
+c2h_phase_read).  Lane 0 of every wave writes its stamp per phase into LDS;
+at the kernel's end the first and the last workgroup of each launch copy
+their stamps into a device array, which every later launch of the same
+kernel overwrites, so a read after a run holds the last launch's stamps.
+The product library is untouched.
 
 `run [T]` (GPU) loads that library (C2H_LIB), runs the decode workload -- a
 synthetic Qwen2.5-0.5B-shaped model, a prefill of T-16 tokens, 16 greedy
