@@ -397,25 +397,12 @@ __device__ __forceinline__ void pad_chain(float* a, int n) {
   if (threadIdx.x < 16 && p < ((n + 15) & ~15)) a[p] = -0.0f;
 }
 
-// n <= 1024: lane l owns [16l, 16l+16) in registers.  a: LDS readable up to
-// round_up(n, 16).
-__device__ __forceinline__ float seq_sum_wave(const float* a, int n) {
-  const int lane = threadIdx.x & 63;
-  const int base = lane * SPEC_C;
-  float v[SPEC_C];
-  {
-    const float4* a4 = reinterpret_cast<const float4*>(a + min(base, (n - 1) & ~(SPEC_C - 1)));
-#pragma unroll
-    for (int k = 0; k < SPEC_C / 4; ++k) {
-      const float4 t = a4[k];
-      v[4 * k + 0] = t.x;
-      v[4 * k + 1] = t.y;
-      v[4 * k + 2] = t.z;
-      v[4 * k + 3] = t.w;
-    }
-#pragma unroll
-    for (int k = 0; k < SPEC_C; ++k) v[k] = (base + k < n) ? v[k] : 0.0f;  // +0 adds are exact no-ops
-  }
+// n <= 1024 values, lane l holding [16l, 16l+16) in v (+0 past n: +0 adds
+// are exact no-ops, the sums being >= +0 or NaN).  tail(c, E): the rest of
+// the chain in order from chunk c, E the exact start of chunk c (after
+// SPEC_ROUNDS rounds without a verified total).
+template <class Tail>
+__device__ __forceinline__ float seq_sum_v(const float (&v)[SPEC_C], int n, Tail tail) {
   float cs = 0.0f;
 #pragma unroll
   for (int k = 0; k < SPEC_C; ++k) cs = cs + v[k];
@@ -429,7 +416,7 @@ __device__ __forceinline__ float seq_sum_wave(const float* a, int n) {
       for (int k = 0; k < SPEC_C; ++k) R = R + v[k];
       if (spec_round(S, R, m, total)) return total;
     }
-    return chunk_chain(a, (m + 1) * SPEC_C, n, lane_value(S, m + 1));
+    return tail(m + 1, lane_value(S, m + 1));
   }
   // round 1 plain: its starts are the prefix guess, off by many ulps, so a
   // window would not reach further; it leaves starts that windows follow
@@ -453,8 +440,26 @@ __device__ __forceinline__ float seq_sum_wave(const float* a, int n) {
     }
     if (win_round(S, u, Rm, R0, Rp, f, E, total)) return total;
   }
+  return tail(f, E);
+}
+
+// The same over values in LDS: a readable up to round_up(n, 16).
+__device__ __forceinline__ float seq_sum_wave(const float* a, int n) {
+  const int base = (threadIdx.x & 63) * SPEC_C;
+  float v[SPEC_C];
+  const float4* a4 = reinterpret_cast<const float4*>(a + min(base, (n - 1) & ~(SPEC_C - 1)));
+#pragma unroll
+  for (int k = 0; k < SPEC_C / 4; ++k) {
+    const float4 t = a4[k];
+    v[4 * k + 0] = t.x;
+    v[4 * k + 1] = t.y;
+    v[4 * k + 2] = t.z;
+    v[4 * k + 3] = t.w;
+  }
+#pragma unroll
+  for (int k = 0; k < SPEC_C; ++k) v[k] = (base + k < n) ? v[k] : 0.0f;
   // the rest in order from the last exact start, reads issued 16 ahead
-  return chunk_chain(a, f * SPEC_C, n, E);
+  return seq_sum_v(v, n, [&](int c, float E) { return chunk_chain(a, c * SPEC_C, n, E); });
 }
 
 // The same exact sequential sum for any n >= 1 (softmax over long contexts):
@@ -522,6 +527,32 @@ __device__ __forceinline__ float rms_inv4(const float4& x, int n, float eps, flo
   }
   __syncthreads();
   return *inv_slot;
+}
+
+// The same 1/rms by one wave alone, from x[16l, 16l+16) in lane l's xs
+// (n <= 1024, a multiple of 4): no LDS and no barrier, so each wave that
+// needs the scale computes it as soon as its own loads arrive.
+__device__ __forceinline__ float rms_inv_regs(const float4 (&xs)[SPEC_C / 4], int n, float eps) {
+  const int base = (threadIdx.x & 63) * SPEC_C;
+  float v[SPEC_C];
+#pragma unroll
+  for (int k = 0; k < SPEC_C / 4; ++k) {
+    v[4 * k + 0] = xs[k].x * xs[k].x;
+    v[4 * k + 1] = xs[k].y * xs[k].y;
+    v[4 * k + 2] = xs[k].z * xs[k].z;
+    v[4 * k + 3] = xs[k].w * xs[k].w;
+  }
+#pragma unroll
+  for (int k = 0; k < SPEC_C; ++k) v[k] = (base + k < n) ? v[k] : 0.0f;
+  const float s = seq_sum_v(v, n, [&](int c, float E) {
+    float t = E;  // lanes c.. in order, their values read across the wave
+    for (int j = c; j < 64; ++j) {
+#pragma unroll
+      for (int k = 0; k < SPEC_C; ++k) t = t + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[k]), j));
+    }
+    return t;
+  });
+  return rms_scale(s / (float)n + eps);
 }
 
 // Keeps the instruction scheduler from sinking the loads issued above below
@@ -956,7 +987,18 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(GemvPar
   float4 xa[BPW];
   float4 nw = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   int tok = 0;
+  // PRO_NORM, n_x <= 1024: the waves that quantise (w < NB) each sum x*x
+  // themselves, lane l from x[16l, 16l+16)
+  const bool sum_regs = (PRO == PRO_NORM) && P.n_x <= 64 * SPEC_C;
+  const int swave = __builtin_amdgcn_readfirstlane(wave);
+  float4 xs[SPEC_C / 4];
   if (PRO == PRO_NORM) {
+    if (sum_regs && swave < NB) {
+      const float4* x4 = reinterpret_cast<const float4*>(P.x);
+      const int last4 = (P.n_x >> 2) - 1;
+#pragma unroll
+      for (int k = 0; k < SPEC_C / 4; ++k) xs[k] = x4[min(4 * lane + k, last4)];
+    }
     xa[0] = load4(P.x, P.n_x);
   } else if (NORM) {  // layer 0: the token's embedding row
     tok = (PRO == PRO_ARGMAX_EMBED_NORM) ? reduce_argmax_partials<NT>(P.part_v, P.part_i, P.n_part, ared)
@@ -989,7 +1031,12 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(GemvPar
         publish_token(P, tok);
       }
     }
-    const float inv = rms_inv4(xa[0], P.n_x, P.eps, sq, &inv_slot);
+    float inv = 0.0f;  // (unused by the waves past NB on the register path)
+    if (PRO == PRO_NORM && sum_regs) {
+      if (swave < NB) inv = rms_inv_regs(xs, P.n_x, P.eps);
+    } else {
+      inv = rms_inv4(xa[0], P.n_x, P.eps, sq, &inv_slot);
+    }
     const float4 xn[1] = {norm4(xa[0], inv, nw)};  // wave w holds block w
     if (wave < NB) quantize_wave(xn[0], wave, s);
     __syncthreads();

@@ -93,7 +93,7 @@ def instrument(kernels: str) -> str:
                     "  PH_G(1);\n"),
                    ("  issue_fence();\n", "  issue_fence();\n  PH_G(2);\n  asm volatile(\"\" ::\"v\"(xa[0].x));\n"
                     "  PH_G(3);\n"),
-                   ("    const float inv = rms_inv4(", "    PH_G(9);\n    const float inv = rms_inv4("),
+                   ("    float inv = 0.0f;  //", "    PH_G(9);\n    float inv = 0.0f;  //"),
                    ("    const float4 xn[1] = {norm4(", "    PH_G(4);\n    const float4 xn[1] = {norm4("),
                    ("  // ---- items\n", "  PH_G(5);\n  asm volatile(\"\" ::\"v\"(w1.a.x), \"v\"(w1.c.w));\n"
                     "  PH_G(6);\n  // ---- items\n"),
