@@ -31,9 +31,18 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
+# Kernel-argument preload (gfx950): the first two arguments of every kernel
+# whose leading arguments are scalars or pointers arrive in SGPRs at wave
+# start (k_gemv_row: x and n_x), so the first loads of the input row do not
+# wait for a read of the kernel arguments from memory.  The code object
+# starts with a block that loads them the usual way, for firmware without
+# the feature; the firmware that has it enters past that block.
+PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=2"]
+
+
 def build(verbose: bool = False) -> str:
     flags = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off",
-             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", *PRELOAD,
              "-Wall", "-Wno-unused-function", "-I", os.path.join(HERE, "..", "include")]
     objs = []
     bdir = os.path.join(HERE, "_build")

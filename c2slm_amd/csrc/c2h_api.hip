@@ -326,7 +326,8 @@ dim3 job_grid(const GemvParams& P) {
   return dim3(w, P.n_jobs);
 }
 
-typedef void (*GemvKernel)(GemvParams);
+typedef void (*GemvKernel)(const float*, int, GemvParams);  // k_gemv_row
+typedef void (*GemvFKernel)(GemvParams);                     // k_gemv_f
 
 // Row-kernel instance for (super-blocks per row, prologue, mode); nullptr
 // when this build has none for that width.
@@ -371,7 +372,7 @@ GemvKernel gemv_row_kernel(int nb, int pro, int mode) {
 bool float_input(int type) { return type == C2H_Q5_0 || type == C2H_Q8_0; }
 
 // k_gemv_f instance for (prologue, mode); nullptr when none is built.
-GemvKernel gemv_f_kernel(int pro, int mode) {
+GemvFKernel gemv_f_kernel(int pro, int mode) {
   if (mode == MODE_BIAS) {
     if (pro == PRO_NORM) return k_gemv_f<PRO_NORM, MODE_BIAS>;
     if (pro == PRO_EMBED_NORM) return k_gemv_f<PRO_EMBED_NORM, MODE_BIAS>;
@@ -385,7 +386,7 @@ GemvKernel gemv_f_kernel(int pro, int mode) {
 
 // A float-input launch over all its jobs (P.n_x = the input length).
 void launch_gemv_f(c2h_ctx* c, GemvParams& P) {
-  GemvKernel k = gemv_f_kernel(P.prologue, P.jobs[0].mode);
+  GemvFKernel k = gemv_f_kernel(P.prologue, P.jobs[0].mode);
   const size_t lds = (size_t)gemv_f_lds_floats(P.n_x) * sizeof(float);
   hipLaunchKernelGGL(k, job_grid(P), dim3(256), lds, c->stream, P);
 }
@@ -403,7 +404,7 @@ void launch_gemv_row(c2h_ctx* c, GemvParams& P) {
   const GemvJob& J = P.jobs[0];
   GemvKernel k = gemv_row_kernel(J.nb, P.prologue, J.mode);
   size_t lds = (P.prologue != PRO_QUANT) ? (size_t)P.n_x_lds * sizeof(float) : 0;
-  hipLaunchKernelGGL(k, job_grid(P), dim3(nt), lds, c->stream, P);
+  hipLaunchKernelGGL(k, job_grid(P), dim3(nt), lds, c->stream, P.x, P.n_x, P);
 }
 
 GemvParams base_params(c2h_ctx* c) {

@@ -371,7 +371,7 @@ struct VocabParams {
 __global__ void k_quantize_q8k(const float* __restrict__ x, int nb, uint8_t* __restrict__ y);
 __global__ void k_gemv_q8k(GemvParams P);
 template <int NB, int PRO, int MODE>
-__global__ void k_gemv_row(GemvParams P);
+__global__ void k_gemv_row(const float* xp, int n_xp, GemvParams P);  // xp, n_xp: P.x, P.n_x
 // Q5_0 / Q8_0 projections on f32 x (PRO_QUANT here means "x as is").
 template <int PRO, int MODE>
 __global__ void k_gemv_f(GemvParams P);

@@ -926,6 +926,18 @@ __device__ __forceinline__ GemvJob launch_job(const GemvParams& P) {
   return J;
 }
 
+// The same fields for k_gemv_row, whose x and n_x come as leading kernel
+// arguments (preloaded into SGPRs at wave start where the firmware supports
+// it) and are not waited for here.
+__device__ __forceinline__ GemvJob launch_job_rows(const GemvParams& P) {
+  GemvJob J = P.jobs[blockIdx.y];
+  asm volatile(""
+               : "+s"(J.type), "+s"(J.type2), "+s"(J.rows), "+s"(J.nb), "+s"(J.rpw), "+s"(J.n_wg), "+s"(J.mode)
+               : "s"(J.spare), "s"(J.w.q), "s"(J.w.d), "s"(J.w2.q), "s"(J.w2.d), "s"(J.y), "s"(J.bias), "s"(J.isums),
+                 "s"(P.norm_w), "s"(P.eps));
+  return J;
+}
+
 // The step's token to the host: the token, then (system-scope release, so
 // that the token is visible first) the step number the host waits for.
 __device__ __forceinline__ void publish_token(const GemvParams& P, int tok) {
@@ -946,7 +958,7 @@ __device__ __forceinline__ void publish_token(const GemvParams& P, int tok) {
 // read the same block of the Q8_K row (broadcast, no bank conflicts).  The
 // fold runs per row in the reference's order.
 template <int NB, int PRO, int MODE>
-__global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(GemvParams P) {
+__global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(const float* __restrict__ xp, int n_xp, GemvParams P) {
   constexpr int NT = row_threads(NB, PRO, MODE);
   constexpr int NI = row_item_threads(NB, PRO, MODE);  // threads per matrix's items
   constexpr int NW = NT / 64;
@@ -965,10 +977,30 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(GemvPar
   __shared__ float inv_slot;
   __shared__ ArgCand ared[NW];  // one slot per wave (reduce_argmax_partials)
 
-  const GemvJob J = launch_job(P);
-  if ((int)blockIdx.x >= J.n_wg) return;  // uniform: the launch's widest job sets the grid
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
+  // ---- the input row's loads first: they need only xp and n_xp
+  float4 xa[BPW];
+  // PRO_NORM, n_x <= 1024: the waves that quantise (w < NB) each sum x*x
+  // themselves, lane l from x[16l, 16l+16)
+  const bool sum_regs = (PRO == PRO_NORM) && n_xp <= 64 * SPEC_C;
+  const int swave = __builtin_amdgcn_readfirstlane(wave);
+  float4 xs[SPEC_C / 4];
+  if (PRO == PRO_NORM) {
+    if (sum_regs && swave < NB) {
+      const float4* x4 = reinterpret_cast<const float4*>(xp);
+      const int last4 = (n_xp >> 2) - 1;
+#pragma unroll
+      for (int k = 0; k < SPEC_C / 4; ++k) xs[k] = x4[min(4 * lane + k, last4)];
+    }
+    xa[0] = load4(xp, n_xp);
+  } else if (!NORM) {
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) xa[i] = reinterpret_cast<const float4*>(xp + min(wave + NW * i, NB - 1) * QK_K)[lane];
+  }
+  issue_fence();
+  const GemvJob J = launch_job_rows(P);
+  if ((int)blockIdx.x >= J.n_wg) return;  // uniform: the launch's widest job sets the grid
   const int it = SPLIT ? (tid & (NI - 1)) : tid;  // item index within its matrix
   // 0: gate (w), 1: up (w2); wave-uniform, and scalar so that the type
   // tests on it branch on SCC, not per lane
@@ -983,33 +1015,15 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(GemvPar
   const int b_c = min(b, NB - 1);
   const int out_row = min(row0 + min(tid, RPW - 1), J.rows - 1);  // epilogue row of thread tid < RPW
 
-  // ---- loads, in the order they are consumed
-  float4 xa[BPW];
+  // ---- the other loads, in the order they are consumed
   float4 nw = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   int tok = 0;
-  // PRO_NORM, n_x <= 1024: the waves that quantise (w < NB) each sum x*x
-  // themselves, lane l from x[16l, 16l+16)
-  const bool sum_regs = (PRO == PRO_NORM) && P.n_x <= 64 * SPEC_C;
-  const int swave = __builtin_amdgcn_readfirstlane(wave);
-  float4 xs[SPEC_C / 4];
-  if (PRO == PRO_NORM) {
-    if (sum_regs && swave < NB) {
-      const float4* x4 = reinterpret_cast<const float4*>(P.x);
-      const int last4 = (P.n_x >> 2) - 1;
-#pragma unroll
-      for (int k = 0; k < SPEC_C / 4; ++k) xs[k] = x4[min(4 * lane + k, last4)];
-    }
-    xa[0] = load4(P.x, P.n_x);
-  } else if (NORM) {  // layer 0: the token's embedding row
+  if (NORM && PRO != PRO_NORM) {  // layer 0: the token's embedding row
     tok = (PRO == PRO_ARGMAX_EMBED_NORM) ? reduce_argmax_partials<NT>(P.part_v, P.part_i, P.n_part, ared)
                                          : P.state->token;
-    xa[0] = embed4(P.emb, P.n_vocab, P.n_x, tok);
-  } else {
-#pragma unroll
-    for (int i = 0; i < BPW; ++i)
-      xa[i] = reinterpret_cast<const float4*>(P.x + min(wave + NW * i, NB - 1) * QK_K)[lane];
+    xa[0] = embed4(P.emb, P.n_vocab, n_xp, tok);
   }
-  if (NORM) nw = load4(P.norm_w, P.n_x);
+  if (NORM) nw = load4(P.norm_w, n_xp);
   const int type1 = (SPLIT && half) ? J.type2 : J.type;
   const ItemW w1 = load_item((SPLIT && half) ? J.w2 : J.w, type1, NB, row_c, b_c, u);
   ItemW w2;
@@ -1017,13 +1031,13 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(GemvPar
   float yres = 0.0f;
   if (MODE == MODE_RESID) yres = J.y[out_row];
   // an absent bias reads x instead (a valid address) and is not added
-  if (MODE == MODE_BIAS) yres = (J.bias ? J.bias : P.x)[J.bias ? out_row : 0];
+  if (MODE == MODE_BIAS) yres = (J.bias ? J.bias : xp)[J.bias ? out_row : 0];
   issue_fence();
 
   // ---- prologue: the Q8_K input row in LDS
   if (NORM) {
     if (PRO != PRO_NORM && blockIdx.x == 0 && blockIdx.y == 0) {  // layer 0 publishes the embedded token
-      if (4 * tid < P.n_x) reinterpret_cast<float4*>(P.x_out)[tid] = xa[0];
+      if (4 * tid < n_xp) reinterpret_cast<float4*>(P.x_out)[tid] = xa[0];
       if (tid == 0) {
         const int pos = P.state->pos;
         P.state->token = tok;
@@ -1033,9 +1047,9 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(GemvPar
     }
     float inv = 0.0f;  // (unused by the waves past NB on the register path)
     if (PRO == PRO_NORM && sum_regs) {
-      if (swave < NB) inv = rms_inv_regs(xs, P.n_x, P.eps);
+      if (swave < NB) inv = rms_inv_regs(xs, n_xp, P.eps);
     } else {
-      inv = rms_inv4(xa[0], P.n_x, P.eps, sq, &inv_slot);
+      inv = rms_inv4(xa[0], n_xp, P.eps, sq, &inv_slot);
     }
     const float4 xn[1] = {norm4(xa[0], inv, nw)};  // wave w holds block w
     if (wave < NB) quantize_wave(xn[0], wave, s);
@@ -1080,7 +1094,8 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(GemvPar
   }
 }
 
-#define C2H_GEMV_ROW(NB_, PRO_, MODE_) template __global__ void k_gemv_row<NB_, PRO_, MODE_>(GemvParams);
+#define C2H_GEMV_ROW(NB_, PRO_, MODE_) \
+  template __global__ void k_gemv_row<NB_, PRO_, MODE_>(const float*, int, GemvParams);
 C2H_GEMV_ROW(3, PRO_QUANT, MODE_RESID)
 C2H_GEMV_ROW(4, PRO_QUANT, MODE_RESID)
 C2H_GEMV_ROW(12, PRO_QUANT, MODE_RESID)

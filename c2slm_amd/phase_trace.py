@@ -83,16 +83,18 @@ def _patch(text: str, start: str, end: str, edits) -> str:
 
 def instrument(kernels: str) -> str:
     s = kernels.replace("namespace c2h {\n", _STAMPS, 1)
-    s = _patch(s, "__global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(GemvParams P) {",
+    s = _patch(s, "__global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(const float* __restrict__ xp, int n_xp,",
                "#define C2H_GEMV_ROW(NB_, PRO_, MODE_)", [
                    ("  constexpr int NT = row_threads(NB, PRO, MODE);\n",
                     "  PH_DECL;\n  constexpr int NT = row_threads(NB, PRO, MODE);\n"),
-                   ("  const GemvJob J = launch_job(P);", "  PH_G(0);\n  const GemvJob J = launch_job(P);"),
+                   ("  const int tid = threadIdx.x;\n  const int wave = tid >> 6, lane = tid & 63;\n  // ---- the input",
+                    "  PH_G(0);\n  const int tid = threadIdx.x;\n  const int wave = tid >> 6, lane = tid & 63;\n"
+                    "  // ---- the input"),
                    ("  if ((int)blockIdx.x >= J.n_wg) return;  // uniform: the launch's widest job sets the grid\n",
                     "  if ((int)blockIdx.x >= J.n_wg) return;  // uniform: the launch's widest job sets the grid\n"
                     "  PH_G(1);\n"),
-                   ("  issue_fence();\n", "  issue_fence();\n  PH_G(2);\n  asm volatile(\"\" ::\"v\"(xa[0].x));\n"
-                    "  PH_G(3);\n"),
+                   ("  issue_fence();\n\n  // ---- prologue", "  issue_fence();\n  PH_G(2);\n"
+                    "  asm volatile(\"\" ::\"v\"(xa[0].x));\n  PH_G(3);\n\n  // ---- prologue"),
                    ("    float inv = 0.0f;  //", "    PH_G(9);\n    float inv = 0.0f;  //"),
                    ("    const float4 xn[1] = {norm4(", "    PH_G(4);\n    const float4 xn[1] = {norm4("),
                    ("  // ---- items\n", "  PH_G(5);\n  asm volatile(\"\" ::\"v\"(w1.a.x), \"v\"(w1.c.w));\n"
@@ -161,7 +163,7 @@ def build() -> str:
     with open(os.path.join(src, "c2h_api.hip"), "a") as f:
         f.write(_READER)
     flags = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={B.ARCH}", "-ffp-contract=off", "-fgpu-rdc",
-             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I", os.path.join(HERE, "..", "include")]
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", *B.PRELOAD, "-I", os.path.join(HERE, "..", "include")]
     objs = []
     for name in B.SOURCES:
         obj = os.path.join(bdir, name + ".o")
