@@ -31,13 +31,14 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-# Kernel-argument preload (gfx950): the first two arguments of every kernel
-# whose leading arguments are scalars or pointers arrive in SGPRs at wave
-# start (k_gemv_row: x and n_x), so the first loads of the input row do not
-# wait for a read of the kernel arguments from memory.  The code object
-# starts with a block that loads them the usual way, for firmware without
-# the feature; the firmware that has it enters past that block.
-PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=2"]
+# Kernel-argument preload (gfx950): the leading scalar and pointer
+# arguments of a kernel (up to seven) arrive in SGPRs at wave start
+# (k_gemv_row: x and n_x; k_attn_core: the state, cache and q/k/v pointers
+# and two packed integers), so the first loads do not wait for a read of the
+# kernel arguments from memory.  The code object starts with a block that
+# loads them the usual way, for firmware without the feature; the firmware
+# that has it enters past that block.
+PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=7"]
 
 
 def build(verbose: bool = False) -> str:

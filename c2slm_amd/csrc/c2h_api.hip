@@ -685,7 +685,8 @@ void enqueue_attn(c2h_ctx* c, int l, int form) {
   else {
     A.xcd_map = D.n_kv_heads <= ATT_XCDS ? 1 : 0;
     const dim3 xgrid(ATT_XCDS * (D.n_heads / D.n_kv_heads));
-    hipLaunchKernelGGL(attn_core_kernel(form), A.xcd_map ? xgrid : grid, dim3(256), c->attn_lds, c->stream, A);
+    hipLaunchKernelGGL(attn_core_kernel(form), A.xcd_map ? xgrid : grid, dim3(256), c->attn_lds, c->stream, A.state,
+                       A.kv, A.q, A.k, A.v, attn_dims(A, D.n_heads / D.n_kv_heads), A.max_ctx, A);
   }
 }
 
@@ -970,6 +971,7 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   if (D.n_layers <= 0 || D.n_embd <= 0 || D.n_heads <= 0 || D.n_kv_heads <= 0 || D.n_ff <= 0 || D.n_vocab <= 0 ||
       D.max_ctx <= 0)
     return bail(fail(c, C2H_ERR_INVALID, "model dimensions must be positive"));
+  if (D.n_layers > 255) return bail(fail(c, C2H_ERR_UNSUPPORTED, "this build runs up to 255 layers"));
   // engine/model.go:137: head_dim = n_embd / n_heads (64 for Qwen2.5-0.5B,
   // 128 for Qwen3-1.7B)
   if ((D.head_dim != 64 && D.head_dim != 128) || D.n_embd != D.n_heads * D.head_dim || D.n_heads % D.n_kv_heads)
@@ -1367,7 +1369,7 @@ int pf_pass(c2h_ctx* c, const int32_t* tokens, int m, int pos0) {
       } else if (pos0 + m <= c->att_split) {
         const size_t lds = (size_t)attn_lds_floats(pos0 + m) * 4;
         hipLaunchKernelGGL(k_attn_core<ATT_TIER_ANY>, dim3(D.n_heads / D.n_kv_heads, D.n_kv_heads, m), dim3(256), lds,
-                           c->stream, A);
+                           c->stream, A.state, A.kv, A.q, A.k, A.v, attn_dims(A, D.n_heads / D.n_kv_heads), A.max_ctx, A);
       } else {
         for (int t0 = 0; t0 < m; t0 += PF_ATT_SUB) {
           A.tok0 = t0;

@@ -391,7 +391,12 @@ __host__ __device__ inline int gemv_f_lds_floats(int n_x) {
 }
 __global__ void k_rmsnorm(NormParams P);
 template <int TIER>
-__global__ void k_attn_core(AttnCoreParams P);
+__global__ void k_attn_core(C2hState* st, float* kv, const float* qg, const float* kg, const float* vg, int dims,
+                            int max_ctx, AttnCoreParams P);  // (P.state, P.kv, P.q, P.k, P.v, attn_dims, P.max_ctx)
+// layer | n_layers << 8 | n_kv_heads << 16 | xcd_map << 23 | query heads per KV head << 24
+inline int attn_dims(const AttnCoreParams& A, int qpkv) {
+  return A.layer | (A.n_layers << 8) | (A.n_kv_heads << 16) | ((A.xcd_map ? 1 : 0) << 23) | (qpkv << 24);
+}
 __global__ void k_attn_scores(AttnCoreParams P);
 __global__ void k_attn_softmax(AttnCoreParams P);
 __global__ void k_attn_av(AttnCoreParams P);

@@ -1680,7 +1680,9 @@ struct VStage {
 };
 
 template <int TIER>
-__global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
+__global__ void __launch_bounds__(256)
+    k_attn_core(C2hState* __restrict__ st, float* __restrict__ kv, const float* __restrict__ qg,
+                const float* __restrict__ kg, const float* __restrict__ vg, int dims, int max_ctx, AttnCoreParams P) {
   constexpr int HD = 64;
   constexpr bool ANY = (TIER == ATT_TIER_ANY);
   static_assert(ANY || (TIER % 32 == 0 && TIER <= ATT_KPF), "a tier reads whole batches of K and V rows");
@@ -1695,44 +1697,47 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   __shared__ float red_m[4];
   __shared__ float inv_slot;
 
-  // the launch's fields in one scalar batch (not a chain of round trips;
-  // and a scalar load still in flight would make every later LDS wait,
-  // which shares its counter, wait for memory too)
-  asm volatile("" ::"s"(P.q), "s"(P.k), "s"(P.v), "s"(P.kv), "s"(P.state), "s"(P.rope_cos), "s"(P.rope_sin),
-               "s"(P.q_ld), "s"(P.kv_ld), "s"(P.tok0), "s"(P.layer), "s"(P.n_layers), "s"(P.n_kv_heads),
-               "s"(P.max_ctx), "s"(P.rope_len), "s"(P.xcd_map), "s"(gridDim.x), "s"(P.out), "s"(P.out_ld),
-               "s"(P.scale), "s"(P.store_kv));
+  // st, kv, qg, kg, vg (P.state, P.kv, P.q, P.k, P.v), dims (attn_dims: layer,
+  // n_layers, n_kv_heads, xcd_map, query heads per KV head) and max_ctx
+  // arrive in SGPRs (kernel-argument preload): the loads of a decode tier
+  // issue at wave start, before the other fields are read from memory
   const int tid = threadIdx.x;
+  const int layer = dims & 0xff, n_layers = (dims >> 8) & 0xff, n_kv = (dims >> 16) & 0x7f;
+  const int qpkv = (dims >> 24) & 0xff;
   // grid (query heads per KV head, KV heads, query tokens of the batch), or
   // the XCD-grouped order of xcd_map (at most ATT_XCDS KV heads)
-  int qpkv = (int)gridDim.x, g = (int)blockIdx.y, hx = (int)blockIdx.x;
-  if (P.xcd_map) {
-    qpkv = (int)gridDim.x / ATT_XCDS;
+  int g = (int)blockIdx.y, hx = (int)blockIdx.x;
+  if ((dims >> 23) & 1) {
     g = (int)blockIdx.x % ATT_XCDS;
     hx = (int)blockIdx.x / ATT_XCDS;
-    if (g >= P.n_kv_heads) return;  // uniform: a spare workgroup of the grid
+    if (g >= n_kv) return;  // uniform: a spare workgroup of the grid
   }
   const int h = g * qpkv + hx;
-  const int ti = P.tok0 + (int)blockIdx.z;  // query token of the batch (0 in decode)
+  // query token of the batch (the tiers serve decode: one token, row 0)
+  const int ti = ANY ? P.tok0 + (int)blockIdx.z : 0;
   // this head's q and the group's k, v: thread t < 192 holds element t%64
   // of q_h (t < 64), k_g, v_g.  Issued before the position is read.
   const int bm = min(tid >> 6, 2);
-  const float* qsrc = P.q + (size_t)ti * P.q_ld + h * HD;
-  const float* ksrc = P.k + (size_t)ti * P.kv_ld + g * HD;
-  const float* vsrc = P.v + (size_t)ti * P.kv_ld + g * HD;
+  const float* qsrc = qg + (ANY ? (size_t)ti * P.q_ld : 0) + h * HD;
+  const float* ksrc = kg + (ANY ? (size_t)ti * P.kv_ld : 0) + g * HD;
+  const float* vsrc = vg + (ANY ? (size_t)ti * P.kv_ld : 0) + g * HD;
   const float own = ((bm == 0) ? qsrc : ((bm == 1) ? ksrc : vsrc))[tid & 63];
   // the position, and for a tier its RoPE row from the state: issued now,
   // first used (waited for) after a tier's K/V loads are issued
-  int pos_state = P.state->pos;
+  // a vector load (a VGPR offset): as a scalar load its wait would also
+  // wait for the kernel-argument loads, which share the scalar counter
+  int zero_v = 0;
+  asm volatile("" : "+v"(zero_v));
+  int pos_state = (&st->pos)[zero_v];
   float rcos = 0.0f, rsin = 0.0f;
   if constexpr (!ANY) {
-    rcos = P.state->rope[tid & 31];
-    rsin = P.state->rope[32 + (tid & 31)];
+    rcos = st->rope[tid & 31];
+    rsin = st->rope[32 + (tid & 31)];
   }
   issue_fence();
-  const size_t head_stride = (size_t)kv_slot(P.max_ctx) * HD;
-  float* kcache = P.kv + ((size_t)P.layer * P.n_kv_heads + g) * head_stride;
-  float* vcache = P.kv + (((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * head_stride;
+  const size_t head_stride = (size_t)kv_slot(max_ctx) * HD;
+  float* kcache = kv + ((size_t)layer * n_kv + g) * head_stride;
+  float* vcache = kv + (((size_t)n_layers + layer) * n_kv + g) * head_stride;
   // K chunk 0, coalesced: 16-byte piece i = tid + 256k of the chunk is row
   // i/16, columns 4(i%16)..+3 (a tier reads its TIER rows); V: wave w holds
   // quads w + 4i of the tier's rows, or of chunk 0.
@@ -1747,7 +1752,7 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
     // Rows at and past pos hold an earlier sequence's values, or none, and
     // are never used: the scores stop at T (the row at pos is this
     // launch's k) and V is zeroed past pos before the chain.
-    const int nall = kv_slot(P.max_ctx);
+    const int nall = kv_slot(max_ctx);
     const __amdgpu_buffer_rsrc_t krs0 = cache_rsrc(kcache, nall * HD * 4);
     const __amdgpu_buffer_rsrc_t vrs0 = cache_rsrc(vcache, (nall >> 2) * HD * 16);
 #pragma unroll
@@ -1756,10 +1761,17 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
     for (int i = 0; i < VQW; ++i) vreg[i] = vquad_load_buf(vrs0, wave + 4 * i);
     issue_fence();
   }
+  // the other fields in one scalar batch (a scalar load still in flight
+  // would make every later LDS wait, which shares its counter, wait too)
+  asm volatile("" ::"s"(P.rope_cos), "s"(P.rope_sin), "s"(P.q_ld), "s"(P.kv_ld), "s"(P.tok0), "s"(P.rope_len),
+               "s"(P.out), "s"(P.out_ld), "s"(P.scale), "s"(P.store_kv));
   asm volatile("" : "+v"(pos_state));
+  // the RoPE row is used here, so its loads stay ahead of the K/V loads
+  // (used only under the rotation's branch, they would be sunk behind them)
+  if constexpr (!ANY) asm volatile("" ::"v"(rcos), "v"(rsin));
   const int pos = __builtin_amdgcn_readfirstlane(pos_state) + ti;
   const int T = pos + 1;
-  const int nstored = max(min(pos, P.max_ctx), 0);    // cached positions [0, nstored)
+  const int nstored = max(min(pos, max_ctx), 0);    // cached positions [0, nstored)
   const int nch = (pos + ATT_CH - 1) / ATT_CH;         // V chunks of positions [0, pos)
   // the any tier's rows: the stored ones as buffers, whose slots past them
   // read zeros without memory traffic
@@ -1779,7 +1791,9 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
     issue_fence();
   }
 
-  if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;
+  // every thread stores (threads 192.. repeat v_g): a store under a branch
+  // would let the compiler sink the load of own into it, behind the K/V loads
+  qkv_s[bm][tid & 63] = own;
   __syncthreads();
 
   float* q_s = qkv_s[0];
@@ -1797,11 +1811,11 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
   __syncthreads();
 
   // (a batch of query tokens has its K/V stored by a kernel before this one)
-  if (P.store_kv && hx == 0 && tid < HD && pos < P.max_ctx) {
+  if (P.store_kv && hx == 0 && tid < HD && pos < max_ctx) {
     kcache[(size_t)pos * HD + tid] = k_s[tid];
     vcache[vq_index(pos, tid)] = v_s[tid];
   }
-  if (T > P.max_ctx) return;  // rejected on the host; kept as a guard
+  if (T > max_ctx) return;  // rejected on the host; kept as a guard
 
   // ---- scores, chunk by chunk of K rows; position pos uses this launch's k
   // (not yet visible in the cache)
@@ -1965,12 +1979,18 @@ __global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {
     P.out[(size_t)ti * P.out_ld + h * HD + d] = acc;
   }
 }
-template __global__ void k_attn_core<ATT_TIER_32>(AttnCoreParams);
-template __global__ void k_attn_core<ATT_TIER_64>(AttnCoreParams);
-template __global__ void k_attn_core<ATT_TIER_96>(AttnCoreParams);
-template __global__ void k_attn_core<ATT_TIER_128>(AttnCoreParams);
-template __global__ void k_attn_core<ATT_TIER_256>(AttnCoreParams);
-template __global__ void k_attn_core<ATT_TIER_ANY>(AttnCoreParams);
+template __global__ void k_attn_core<ATT_TIER_32>(C2hState*, float*, const float*, const float*, const float*, int, int,
+                                                   AttnCoreParams);
+template __global__ void k_attn_core<ATT_TIER_64>(C2hState*, float*, const float*, const float*, const float*, int, int,
+                                                   AttnCoreParams);
+template __global__ void k_attn_core<ATT_TIER_96>(C2hState*, float*, const float*, const float*, const float*, int, int,
+                                                   AttnCoreParams);
+template __global__ void k_attn_core<ATT_TIER_128>(C2hState*, float*, const float*, const float*, const float*, int, int,
+                                                   AttnCoreParams);
+template __global__ void k_attn_core<ATT_TIER_256>(C2hState*, float*, const float*, const float*, const float*, int, int,
+                                                   AttnCoreParams);
+template __global__ void k_attn_core<ATT_TIER_ANY>(C2hState*, float*, const float*, const float*, const float*, int, int,
+                                                   AttnCoreParams);
 
 // ------------------------------------------------ attention, head_dim 128
 

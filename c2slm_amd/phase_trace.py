@@ -102,15 +102,14 @@ def instrument(kernels: str) -> str:
                    ("  // ---- per-row fold in the reference's order, then the epilogue\n",
                     "  PH_G(7);\n  // ---- per-row fold in the reference's order, then the epilogue\n"),
                ]).replace("PH_END;", "PH_G(8);\n  PH_G_END;", 1)
-    s = _patch(s, "template <int TIER>\n__global__ void __launch_bounds__(256) k_attn_core(AttnCoreParams P) {",
-               "template __global__ void k_attn_core<ATT_TIER_32>(AttnCoreParams);", [
-                   ('  asm volatile("" ::"s"(P.q), "s"(P.k), "s"(P.v), "s"(P.kv),',
-                    '  PH_DECL;\n  const long long ph_entry_ = __builtin_amdgcn_s_memtime();\n'
-                    '  asm volatile("" ::"s"(P.q), "s"(P.k), "s"(P.v), "s"(P.kv),'),
+    s = _patch(s, "template <int TIER>\n__global__ void __launch_bounds__(256)\n    k_attn_core(C2hState* __restrict__ st,",
+               "template __global__ void k_attn_core<ATT_TIER_32>(", [
+                   ("  const int tid = threadIdx.x;\n  const int layer = dims & 0xff",
+                    "  PH_DECL;\n  const long long ph_entry_ = __builtin_amdgcn_s_memtime();\n"
+                    "  const int tid = threadIdx.x;\n  const int layer = dims & 0xff"),
                    ('"s"(P.scale), "s"(P.store_kv));\n', '"s"(P.scale), "s"(P.store_kv));\n'
-                    '  const long long ph_args_ = __builtin_amdgcn_s_memtime();\n'),
-                   ("  const int h = g * qpkv + hx;\n", "  const int h = g * qpkv + hx;\n  PH_AT(0, ph_entry_);\n"
-                    "  PH_AT(1, ph_args_);\n"),
+                    '  PH_A(1);\n'),
+                   ("  const int h = g * qpkv + hx;\n", "  const int h = g * qpkv + hx;\n  PH_AT(0, ph_entry_);\n"),
                    ("  const int T = pos + 1;\n", "  asm volatile(\"\" ::\"s\"(pos));\n  PH_A(9);\n  const int T = pos + 1;\n"),
                    ("    __syncthreads();\n    const int p = c0 + tid;\n",
                     "    PH_A(10);\n    __syncthreads();\n    const int p = c0 + tid;\n"),
@@ -120,9 +119,8 @@ def instrument(kernels: str) -> str:
                     "    if (sc[0] != sc[0]) mx = sc[0];\n    PH_A(12);\n    for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));\n    if constexpr (!ANY && TIER <= SUM_DIRECT_N) pad_chain(sc, T);\n    __syncthreads();\n    PH_A(13);\n"),
                    ("      while_summing();\n    }\n",
                     "      while_summing();\n    }\n    PH_A(14);\n"),
-                   ("\n\n  if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;\n  __syncthreads();\n",
-                    "\n  PH_A(2);\n\n  if (tid < 3 * HD) qkv_s[bm][tid & 63] = own;\n"
-                    "  __syncthreads();\n  PH_A(3);\n"),
+                   ("  qkv_s[bm][tid & 63] = own;\n  __syncthreads();\n",
+                    "  PH_A(2);\n  qkv_s[bm][tid & 63] = own;\n  __syncthreads();\n  PH_A(3);\n"),
                    ("  __syncthreads();\n\n  // (a batch of query tokens",
                     "  __syncthreads();\n  PH_A(4);\n\n  // (a batch of query tokens"),
                    ("  // softmax, then V chunk 0 from registers into LDS buffer 0\n",
