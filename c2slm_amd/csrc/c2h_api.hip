@@ -424,7 +424,7 @@ GemvParams base_params(c2h_ctx* c) {
 
 const Tensor& out_weight(c2h_ctx* c) { return c->output.present() ? c->output : c->embd; }
 
-typedef void (*VocabKernel)(VocabParams);
+typedef void (*VocabKernel)(const uint8_t*, C2hState*, const float*, const float*, int, VocabParams);
 
 // The vocab kernel instance for rows of nb8 Q8_0 blocks (nullptr outside
 // the instantiated widths) and its dynamic LDS (x permuted).
@@ -543,7 +543,7 @@ void enqueue_vocab(c2h_ctx* c, int apply_penalty, float* logits_out, int x_sel, 
   V.part_i = c->part_i;
   V.state = c->state_dev;
   hipLaunchKernelGGL(vocab_kernel(nb8_of(c->desc.n_embd)), dim3(c->n_part), dim3(256), vocab_lds(c->desc.n_embd),
-                     c->stream, V);
+                     c->stream, V.w.q, V.state, x_sel ? V.x_buf[0] : V.x, x_sel ? V.x_buf[1] : V.x, V.n_vocab, V);
 }
 
 AttnCoreParams attn_params(c2h_ctx* c, int layer) {

@@ -413,7 +413,8 @@ __global__ void k_pf_gemm_f(PFGemmFParams P);
 __global__ void k_pf_rope_store(PFRopeParams P);
 __global__ void k_pf_swiglu(const float* gate, const float* up, float* h, int n, int m);
 template <int NB8>
-__global__ void k_vocab(VocabParams P);
+__global__ void k_vocab(const uint8_t* wq, C2hState* st, const float* xb0, const float* xb1, int n_vocab,
+                        VocabParams P);  // (P.w.q, P.state, x_buf[0] or x, x_buf[1] or x, P.n_vocab)
 constexpr int VOCAB_MIN_NB8 = 24, VOCAB_MAX_NB8 = 32;  // instantiated widths (Q8_0 blocks per row), and 64
 // An f32 input vector: x itself, or (sel) the normX buffer the step state
 // names, for kernels inside replayed graphs.

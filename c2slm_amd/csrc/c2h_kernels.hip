@@ -3096,11 +3096,11 @@ struct VocabTile {
 };
 
 template <int NB8>
-__device__ __forceinline__ void vocab_load(VocabTile<NB8>& t, const VocabParams& P, int tile) {
+__device__ __forceinline__ void vocab_load(VocabTile<NB8>& t, const uint8_t* wq, int n_vocab, int tile) {
   constexpr int DPAD = ((NB8 + 31) / 32) * 32;
   const int j = threadIdx.x & 7, rl = threadIdx.x >> 3;
-  const int row_c = min(tile * 32 + rl, P.n_vocab - 1);
-  const uint8_t* rowp = P.w.q + (size_t)row_c * q8_0_row_stride(NB8);
+  const int row_c = min(tile * 32 + rl, n_vocab - 1);
+  const uint8_t* rowp = wq + (size_t)row_c * q8_0_row_stride(NB8);
   const uint4* dvec = reinterpret_cast<const uint4*>(rowp);
   const uint4* qrow = reinterpret_cast<const uint4*>(rowp + (size_t)DPAD * 2);
 #pragma unroll
@@ -3187,7 +3187,9 @@ __device__ __forceinline__ void vocab_row(const VocabTile<NB8>& t, const VocabPa
 // own arithmetic.  x is permuted into LDS once per workgroup.  Workgroup w
 // leaves its best (value, lowest index) in part_v/part_i[w].
 template <int NB8>
-__global__ void __launch_bounds__(256) k_vocab(VocabParams P) {
+__global__ void __launch_bounds__(256)
+    k_vocab(const uint8_t* __restrict__ wq, C2hState* __restrict__ st, const float* xb0, const float* xb1, int n_vocab,
+            VocabParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
   float* xp = reinterpret_cast<float*>(smem);  // x permuted: [b][j][i] = x[32b + j + 8i]
   __shared__ int win[64];
@@ -3195,15 +3197,23 @@ __global__ void __launch_bounds__(256) k_vocab(VocabParams P) {
 
   const int tid = threadIdx.x;
   constexpr int nb8 = NB8;
-  const int n_tiles = (P.n_vocab + 31) / 32;
+  // wq, st, n_vocab (P.w.q, P.state, P.n_vocab) and x's buffers (xb0, xb1:
+  // x_buf[0..1], or x twice) are preloaded kernel arguments: the first tile
+  // and the step state are read at wave start.  State fields as vector loads
+  // (a VGPR offset): a scalar load's wait would also wait for the other
+  // kernel arguments, which share the scalar counter.
+  int zero_v = 0;
+  asm volatile("" : "+v"(zero_v));
+  const int pos = (&st->pos)[zero_v];
+  const int nx_in = (&st->nx_in)[zero_v];
+  const int n_tiles = (n_vocab + 31) / 32;
   const int G = (int)gridDim.x;
   const int trips = ((n_tiles + G - 1) / G + 1) / 2;  // tile pairs per workgroup
-  const int pos = P.state->pos;
   const int wstart = max(pos - 64, 0);
   const int nwin = (P.apply_penalty && pos > 0) ? (pos - wstart) : 0;
 
   // ---- loads: x, the penalty window, then the first tile
-  const float* x = P.x_sel ? P.x_buf[P.state->nx_in] : P.x;
+  const float* x = nx_in ? xb1 : xb0;
   constexpr int XR = (NB8 + 7) / 8;  // x elements per thread
   float xr[XR];
 #pragma unroll
@@ -3212,7 +3222,7 @@ __global__ void __launch_bounds__(256) k_vocab(VocabParams P) {
   const int32_t* wsrc = P.apply_penalty ? P.token_ids + wstart : P.part_i;
   const int wid = wsrc[P.apply_penalty ? min(tid & 63, max(nwin - 1, 0)) : 0];
   VocabTile<NB8> ta, tb;
-  vocab_load(ta, P, blockIdx.x);
+  vocab_load(ta, wq, n_vocab, blockIdx.x);
   issue_fence();
 #pragma unroll
   for (int k = 0; k < XR; ++k) {
@@ -3226,17 +3236,17 @@ __global__ void __launch_bounds__(256) k_vocab(VocabParams P) {
   if (tid < 64) win[tid] = wid;
   __syncthreads();
 
-  const int im_end = P.state->im_end, eos = P.state->eos;
-  const float penalty = P.state->penalty;
+  const int im_end = st->im_end, eos = st->eos;
+  const float penalty = st->penalty;
   ArgCand best;
   best.v = -__builtin_inff();
   best.i = 0x7fffffff;
   for (int k = 0; k < trips; ++k) {
     const int t0 = (int)blockIdx.x + 2 * k * G;
-    vocab_load(tb, P, t0 + G);
+    vocab_load(tb, wq, n_vocab, t0 + G);
     __builtin_amdgcn_sched_barrier(0);
     vocab_row(ta, P, xp, win, nwin, t0, im_end, eos, penalty, best);
-    vocab_load(ta, P, t0 + 2 * G);  // the next trip's first tile
+    vocab_load(ta, wq, n_vocab, t0 + 2 * G);  // the next trip's first tile
     __builtin_amdgcn_sched_barrier(0);
     vocab_row(tb, P, xp, win, nwin, t0 + G, im_end, eos, penalty, best);
   }
@@ -3250,7 +3260,8 @@ __global__ void __launch_bounds__(256) k_vocab(VocabParams P) {
     P.part_i[blockIdx.x] = r.i;
   }
 }
-#define C2H_VOCAB(NB8_) template __global__ void k_vocab<NB8_>(VocabParams);
+#define C2H_VOCAB(NB8_) \
+  template __global__ void k_vocab<NB8_>(const uint8_t*, C2hState*, const float*, const float*, int, VocabParams);
 C2H_VOCAB(24)
 C2H_VOCAB(25)
 C2H_VOCAB(26)
