@@ -926,16 +926,14 @@ __device__ __forceinline__ GemvJob launch_job(const GemvParams& P) {
   return J;
 }
 
-// The same fields for k_gemv_row, whose x and n_x come as leading kernel
-// arguments (preloaded into SGPRs at wave start where the firmware supports
-// it) and are not waited for here.
-__device__ __forceinline__ GemvJob launch_job_rows(const GemvParams& P) {
-  GemvJob J = P.jobs[blockIdx.y];
+// The same fields for k_gemv_row (read by the caller, pinned here), whose x
+// and n_x come as leading kernel arguments (preloaded into SGPRs at wave
+// start where the firmware supports it) and are not waited for here.
+__device__ __forceinline__ void pin_job_rows(GemvJob& J, const GemvParams& P) {
   asm volatile(""
                : "+s"(J.type), "+s"(J.type2), "+s"(J.rows), "+s"(J.nb), "+s"(J.rpw), "+s"(J.n_wg), "+s"(J.mode)
                : "s"(J.spare), "s"(J.w.q), "s"(J.w.d), "s"(J.w2.q), "s"(J.w2.d), "s"(J.y), "s"(J.bias), "s"(J.isums),
                  "s"(P.norm_w), "s"(P.eps));
-  return J;
 }
 
 // The step's token to the host: the token, then (system-scope release, so
@@ -977,6 +975,9 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(const f
   __shared__ float inv_slot;
   __shared__ ArgCand ared[NW];  // one slot per wave (reduce_argmax_partials)
 
+  // the job's fields: their scalar loads are issued first and waited for
+  // after the input row's loads are out
+  GemvJob J = P.jobs[blockIdx.y];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   // ---- the input row's loads first: they need only xp and n_xp
@@ -999,7 +1000,7 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(const f
     for (int i = 0; i < BPW; ++i) xa[i] = reinterpret_cast<const float4*>(xp + min(wave + NW * i, NB - 1) * QK_K)[lane];
   }
   issue_fence();
-  const GemvJob J = launch_job_rows(P);
+  pin_job_rows(J, P);
   if ((int)blockIdx.x >= J.n_wg) return;  // uniform: the launch's widest job sets the grid
   const int it = SPLIT ? (tid & (NI - 1)) : tid;  // item index within its matrix
   // 0: gate (w), 1: up (w2); wave-uniform, and scalar so that the type
