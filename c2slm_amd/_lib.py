@@ -249,11 +249,13 @@ class Ctx:
 
     KERNELS = ("qkv", "attn", "attn_out", "ffn_in", "ffn_out", "final_norm")  # C2H_KERNEL_*
 
-    def time_layer_kernel(self, kernel: str, iters: int, captured: bool = False) -> float:
+    def time_layer_kernel(self, kernel: str, iters: int, captured: bool = False, per_launch: bool = False) -> float:
         """ms per launch of one decoder-layer kernel (c2h_time_layer_kernel):
-        eager launches, or one captured graph."""
+        eager launches between one pair of events, one captured graph, or
+        (per_launch) eager launches each between its own pair of events."""
         ms = C.c_float()
-        self._chk(lib().c2h_time_layer_kernel(self.h, self.KERNELS.index(kernel), iters, int(captured), C.byref(ms)))
+        mode = 2 if per_launch else int(captured)
+        self._chk(lib().c2h_time_layer_kernel(self.h, self.KERNELS.index(kernel), iters, mode, C.byref(ms)))
         return ms.value
 
     def time_gemv(self, ggml_type: int, w: np.ndarray, xq: np.ndarray, rows: int, cols: int, iters: int,

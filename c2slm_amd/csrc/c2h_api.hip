@@ -862,6 +862,7 @@ thread_local std::string g_create_err;
 constexpr int kMaxDevices = 64;
 std::mutex g_noalloc_mu;
 uint8_t* g_noalloc[kMaxDevices] = {};
+std::mutex g_noalloc_call_mu[kMaxDevices];  // held by c2h_quantize_q8k_noalloc per device
 
 int noalloc_setup(c2h_ctx* c) {
   if (c->device < 0 || c->device >= kMaxDevices)
@@ -1506,13 +1507,8 @@ int c2h_step(c2h_ctx* c, int32_t pos, float penalty, int32_t im_end, int32_t eos
   const bool same = c->state_pred_valid && pr.pos == s.pos && pr.im_end == s.im_end && pr.eos == s.eos &&
                     pr.penalty == s.penalty && pr.nx_in == s.nx_in && pr.nx_out == s.nx_out && pr.seq == s.seq;
   if (!same && (rc = push_state(c, s))) return rc;
+  c->state_pred_valid = false;  // until the step's token has arrived
   if ((rc = run_graph(c, true, pos))) return rc;
-  c->state_pred = s;
-  c->state_pred.pos = s.pos + 1;
-  c->state_pred.seq = s.seq % 0x7ffffffe + 1;
-  c->state_pred.nx_in = s.nx_out;
-  c->state_pred.nx_out = s.nx_out ^ 1;
-  c->state_pred_valid = true;  // eager launches run the same final norm
   c->nx_prev = c->nx_cur;
   c->nx_cur ^= 1;
   c->seq_len = pos + 1;
@@ -1520,11 +1516,20 @@ int c2h_step(c2h_ctx* c, int32_t pos, float penalty, int32_t im_end, int32_t eos
   // arrives in pinned memory (with s.seq) while the forward of that token
   // still runs, and everything that later reads the step's results is
   // ordered after it on the stream.  If the stream stops without it (an
-  // error), the stream's status is reported.
+  // error), the stream's status is reported and the device state is not
+  // trusted by the next step (it copies the state again).
   const volatile int32_t* tk = c->tok_host;
   for (unsigned spin = 1;; ++spin) {
     if (__atomic_load_n(&tk[1], __ATOMIC_ACQUIRE) == s.seq) {
       if (next_token) *next_token = tk[0];
+      // the state this step's final norm leaves on the device (eager
+      // launches run the same final norm)
+      c->state_pred = s;
+      c->state_pred.pos = s.pos + 1;
+      c->state_pred.seq = s.seq % 0x7ffffffe + 1;
+      c->state_pred.nx_in = s.nx_out;
+      c->state_pred.nx_out = s.nx_out ^ 1;
+      c->state_pred_valid = true;
       return C2H_OK;
     }
     if ((spin & 1023u) == 0u) {
@@ -1881,9 +1886,10 @@ int c2h_quantize_q8k_noalloc(c2h_ctx* c, const float* x, int32_t cols, void* q8k
   if (!c->noalloc) return fail(c, C2H_ERR_STATE, "no-alloc scratch not set up");
   float* dx = reinterpret_cast<float*>(c->noalloc);
   uint8_t* dy = c->noalloc + kNoAllocX;
-  // the same stream orders this copy after any earlier call's read-back of
-  // the scratch; every byte the kernel writes is rewritten, nothing needs
-  // clearing
+  // One call at a time per GPU in this process, from the copy in to the
+  // copy out: every context on the GPU shares its scratch.  Every byte the
+  // kernel writes is rewritten, nothing needs clearing.
+  std::lock_guard<std::mutex> lock(g_noalloc_call_mu[c->device]);
   HIPCHK(c, hipMemcpyAsync(dx, x, (size_t)nb * 256 * 4, hipMemcpyHostToDevice, c->stream));
   hipLaunchKernelGGL(k_quantize_q8k, dim3((nb + 3) / 4), dim3(256), 0, c->stream, dx, nb, dy);
   HIPCHK(c, hipGetLastError());
@@ -2195,6 +2201,11 @@ int c2h_time_steps(c2h_ctx* c, int32_t pos, int32_t iters, float penalty, int32_
       s.penalty = penalty;
       s.nx_in = c->nx_cur;
       s.nx_out = c->nx_cur ^ 1;
+      // step numbers come from the context's counter, as c2h_step's do: the
+      // graphs publish seq .. seq+iters-1 to the token slot c2h_step polls,
+      // and the counter moves past them so the next c2h_step's number is new
+      s.seq = (int32_t)(++c->step_seq % 0x7ffffffeu) + 1;
+      c->step_seq += (unsigned)(iters - 1);
       if ((rc = push_state(c, s))) return rc;
     }
     if ((rc = run_graph(c, true, pos + i))) return rc;
@@ -2219,7 +2230,11 @@ int c2h_time_layer_kernel(c2h_ctx* c, int32_t kernel, int32_t iters, int32_t cap
   int rc = build_graphs(c);
   if (rc) return rc;
   const c2h_model_desc& D = c->desc;
-  const int pos = std::min(c->seq_len, D.max_ctx - 1);
+  // the attention kernel stores K/V at pos: only a position past the cached
+  // rows may be written (a timing call must not change what a caller reads)
+  if (c->seq_len >= D.max_ctx)
+    return fail(c, C2H_ERR_RANGE, "SeqLen %d leaves no free position below max_ctx %d", c->seq_len, D.max_ctx);
+  const int pos = c->seq_len;
   HIPCHK(c, hipStreamSynchronize(c->stream));
   c->ring_next = 0;
   C2hState s;
@@ -2232,9 +2247,11 @@ int c2h_time_layer_kernel(c2h_ctx* c, int32_t kernel, int32_t iters, int32_t cap
   s.nx_out = c->nx_cur ^ 1;
   if ((rc = push_state(c, s))) return rc;
   const int form = attn_form(c, pos + 1);
-  // the residual kernels update X: it is restored afterwards
+  // the residual kernels update X and the final norm writes normX[nx_out]:
+  // both are restored afterwards
   float* saved = nullptr;
-  HIPCHK(c, hipMalloc(&saved, (size_t)D.n_embd * 4));
+  HIPCHK(c, hipMalloc(&saved, (size_t)D.n_embd * 8));
+  float* const nx_out = c->normx[s.nx_out];
   hipEvent_t e0 = nullptr, e1 = nullptr;
   auto one = [&](int i) {
     const int l = i % D.n_layers;
@@ -2248,12 +2265,40 @@ int c2h_time_layer_kernel(c2h_ctx* c, int32_t kernel, int32_t iters, int32_t cap
     }
   };
   if (hipMemcpyAsync(saved, c->X, (size_t)D.n_embd * 4, hipMemcpyDeviceToDevice, c->stream) != hipSuccess ||
+      hipMemcpyAsync(saved + D.n_embd, nx_out, (size_t)D.n_embd * 4, hipMemcpyDeviceToDevice, c->stream) !=
+          hipSuccess ||
       hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
     rc = fail(c, C2H_ERR_HIP, "kernel timing set-up failed");
   float t = 0.0f;
   hipGraph_t g = nullptr;
   hipGraphExec_t ge = nullptr;
-  if (!rc) {
+  if (!rc && captured == 2) {
+    // one pair of events around each eager launch: the sum of the pairs'
+    // times, the per-dispatch duration a kernel trace of the same launches
+    // records (no overlap of a launch's set-up with the previous kernel)
+    for (int i = 0; i < D.n_layers; ++i) one(i);  // warm-up: every layer once
+    std::vector<hipEvent_t> ev(2 * (size_t)iters, nullptr);
+    hipError_t e = hipSuccess;
+    for (auto& x : ev)
+      if (e == hipSuccess) e = hipEventCreate(&x);
+    for (int i = 0; e == hipSuccess && i < iters; ++i) {
+      e = hipEventRecord(ev[2 * i], c->stream);
+      one(i);
+      if (e == hipSuccess) e = hipEventRecord(ev[2 * i + 1], c->stream);
+    }
+    if (e == hipSuccess) e = hipGetLastError();
+    if (e == hipSuccess) e = hipEventSynchronize(ev.back());
+    double total = 0.0;
+    for (int i = 0; e == hipSuccess && i < iters; ++i) {
+      float ms1 = 0.0f;
+      e = hipEventElapsedTime(&ms1, ev[2 * i], ev[2 * i + 1]);
+      total += ms1;
+    }
+    for (auto& x : ev)
+      if (x) (void)hipEventDestroy(x);
+    if (e != hipSuccess) rc = fail(c, C2H_ERR_HIP, "kernel timing failed: %s", hipGetErrorString(e));
+    t = (float)total;
+  } else if (!rc) {
     for (int i = 0; i < D.n_layers; ++i) one(i);  // warm-up: every layer once
     // captured: the timed launches replay as one graph (as the decode step
     // does), so the host's launch rate does not pace them; eager when the
@@ -2283,8 +2328,10 @@ int c2h_time_layer_kernel(c2h_ctx* c, int32_t kernel, int32_t iters, int32_t cap
   }
   if (ge) (void)hipGraphExecDestroy(ge);
   if (g) (void)hipGraphDestroy(g);
-  if (!rc && hipMemcpyAsync(c->X, saved, (size_t)D.n_embd * 4, hipMemcpyDeviceToDevice, c->stream) != hipSuccess)
-    rc = fail(c, C2H_ERR_HIP, "restoring X failed");
+  if (!rc && (hipMemcpyAsync(c->X, saved, (size_t)D.n_embd * 4, hipMemcpyDeviceToDevice, c->stream) != hipSuccess ||
+              hipMemcpyAsync(nx_out, saved + D.n_embd, (size_t)D.n_embd * 4, hipMemcpyDeviceToDevice, c->stream) !=
+                  hipSuccess))
+    rc = fail(c, C2H_ERR_HIP, "restoring X / normX failed");
   (void)hipStreamSynchronize(c->stream);
   if (e0) (void)hipEventDestroy(e0);
   if (e1) (void)hipEventDestroy(e1);

@@ -188,9 +188,10 @@ int c2h_quantize_q8k(c2h_ctx* ctx, const float* x, int32_t cols, void* q8k_out);
  * errors, but it calls no allocator: x and the Q8_K blocks are staged in a
  * fixed device scratch, one per GPU, set up by c2h_create.  cols above
  * C2H_NOALLOC_MAX_COLS returns C2H_ERR_INVALID.  Every context on a GPU
- * shares that GPU's scratch: calls that overlap on one GPU (several
- * threads, or contexts on different streams) race. */
-#define C2H_NOALLOC_MAX_COLS 16384 /* 64 super-blocks, the reference's Q8_K scratch (engine/pool.go:59) */
+ * shares that GPU's scratch.  Calls from one process take a per-GPU lock
+ * from the copy in to the copy out, so they run one after another; calls
+ * from different processes on one GPU each have their own scratch. */
+#define C2H_NOALLOC_MAX_COLS 16384 /* 64 Q8_K super-blocks: 84 KB of device scratch per GPU */
 int c2h_quantize_q8k_noalloc(c2h_ctx* ctx, const float* x, int32_t cols, void* q8k_out);
 
 /* tensor.GEMVQ4_K_Q8_K / GEMVQ6_K_Q8_K / GEMVQ8_0 / GEMVQ5_0
@@ -305,15 +306,19 @@ int c2h_check_rms_scale(c2h_ctx* ctx, uint32_t lo, uint64_t hi, uint64_t* mismat
 
 /* Measurement aid with no counterpart in the reference: average device time
  * (ms) of one decoder-layer kernel, `iters` launches back to back on the
- * context stream between one pair of HIP events (captured != 0: as one
+ * context stream between one pair of HIP events (captured == 1: as one
  * captured graph, replayed once untimed first, unless the context runs
- * without graphs (C2H_NO_GRAPH=1); 0: eager launches), layer
+ * without graphs (C2H_NO_GRAPH=1); 0: eager launches; 2: eager launches,
+ * each between its own pair of events, the pairs' times summed), layer
  * i % n_layers on launch i (so each launch reads another layer's weights,
  * as inside a step), after one untimed round over the layers.  The q|k|v kernel runs the
  * later layers' prologue (RMSNorm of X) on every layer.  Inputs are the
- * context's current buffers, at position SeqLen (clamped to max_ctx-1): the
- * attention kernel writes the KV entries of that position; X, which the
- * residual kernels update, is restored afterwards. */
+ * context's current buffers, at position SeqLen, which must be below
+ * max_ctx (else C2H_ERR_RANGE): the attention kernel writes the KV entries
+ * of that position, which no later read depends on until a forward or step
+ * at SeqLen rewrites them; X, which the residual kernels update, is restored
+ * afterwards, and so is the normX buffer the final-norm kernel writes (the
+ * one c2h_restore_normx switches back to). */
 int c2h_time_layer_kernel(c2h_ctx* ctx, int32_t kernel, int32_t iters, int32_t captured, float* ms_per_launch);
 
 /* Measurement aid with no counterpart in the reference: average device time

@@ -1,10 +1,10 @@
 """Per-phase cycle stamps of the decode layer kernels (measurement tool).
 
 `build` writes an instrumented copy of the kernel sources into
-c2slm_amd/_build/phase/ with `s_memtime` stamps at the phase boundaries of
-k_gemv_row (qkv, attn_out, ffn_in, ffn_out) and the tiers of k_attn_core,
-and links it as c2slm_amd/libc2h_phase.so (same C ABI plus
-c2h_phase_read).  Lane 0 of every wave writes its stamp per phase into LDS;
+_build/phase/ at the repository root, with `s_memtime` stamps at the phase
+boundaries of k_gemv_row (qkv, attn_out, ffn_in, ffn_out) and the tiers of
+k_attn_core, and links it as _build/phase/libc2h_phase.so (same C ABI plus
+c2h_phase_read).  Nothing is written into the c2slm_amd package.  Lane 0 of every wave writes its stamp per phase into LDS;
 at the kernel's end the first and the last workgroup of each launch copy
 their stamps into a device array, which every later launch of the same
 kernel overwrites, so a read after a run holds the last launch's stamps.
@@ -17,9 +17,9 @@ the table: per phase, the latest wave's stamp minus wave 0's entry stamp, in
 shader clocks.  Above 256 positions it prints the any-length attention
 tier's stamps wave by wave instead.
 
-    python -m c2slm_amd.phase_trace build      # CPU: hipcc cross-compiles
-    python -m c2slm_amd.phase_trace run        # GPU
-    python -m c2slm_amd.phase_trace run 512    # GPU, long-context attention
+    python phase_trace.py build      # CPU: hipcc cross-compiles
+    python phase_trace.py run        # GPU
+    python phase_trace.py run 512    # GPU, long-context attention
 """
 from __future__ import annotations
 
@@ -28,8 +28,11 @@ import shutil
 import subprocess
 import sys
 
-HERE = os.path.dirname(os.path.abspath(__file__))
-OUT_LIB = os.path.join(HERE, "libc2h_phase.so")
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+BDIR = os.path.join(ROOT, "_build", "phase")
+OUT_LIB = os.path.join(BDIR, "libc2h_phase.so")
 N_WAVES, N_SLOTS = 8, 16
 GEMV_KINDS = ["qkv", "attn_out", "ffn_in", "ffn_out"]
 GEMV_PHASES = ["entry", "args", "issued", "x", "norm_end", "quant", "w", "items", "end", "norm_start"]
@@ -145,11 +148,11 @@ extern "C" int c2h_phase_read(long long* out) {
 
 def build() -> str:
     from c2slm_amd import build as B
-    bdir = os.path.join(HERE, "_build", "phase")
+    bdir = BDIR
     shutil.rmtree(bdir, ignore_errors=True)
     src = os.path.join(bdir, "k", "csrc")  # the sources include ../../include/c2h.h
     os.makedirs(src)
-    os.symlink(os.path.abspath(os.path.join(HERE, "..", "include")), os.path.join(bdir, "include"))
+    os.symlink(os.path.join(ROOT, "include"), os.path.join(bdir, "include"))
     for f in os.listdir(B.CSRC):
         if os.path.isfile(os.path.join(B.CSRC, f)):
             shutil.copy(os.path.join(B.CSRC, f), src)
@@ -161,7 +164,7 @@ def build() -> str:
     with open(os.path.join(src, "c2h_api.hip"), "a") as f:
         f.write(_READER)
     flags = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={B.ARCH}", "-ffp-contract=off", "-fgpu-rdc",
-             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", *B.PRELOAD, "-I", os.path.join(HERE, "..", "include")]
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", *B.PRELOAD, "-I", os.path.join(ROOT, "include")]
     objs = []
     for name in B.SOURCES:
         obj = os.path.join(bdir, name + ".o")
@@ -187,8 +190,8 @@ def run(last: int = 48, path: str = "/tmp/c2h_phase_q05.gguf") -> None:
     """
     if os.environ.get("C2H_LIB") != OUT_LIB:  # the library path is fixed when _lib loads
         env = dict(os.environ, C2H_LIB=OUT_LIB)
-        sys.exit(subprocess.run([sys.executable, "-u", "-m", "c2slm_amd.phase_trace", "run", str(last)], env=env,
-                                cwd=os.path.dirname(HERE)).returncode)
+        sys.exit(subprocess.run([sys.executable, "-u", os.path.join(ROOT, "phase_trace.py"), "run", str(last)], env=env,
+                                cwd=ROOT).returncode)
     if not 17 <= last <= 1024:
         raise ValueError("last must lie in 17..1024")
     import ctypes as C
@@ -243,7 +246,7 @@ def run(last: int = 48, path: str = "/tmp/c2h_phase_q05.gguf") -> None:
 if __name__ == "__main__":
     if len(sys.argv) not in (2, 3) or sys.argv[1] not in ("build", "run") or (
             len(sys.argv) == 3 and (sys.argv[1] != "run" or not sys.argv[2].isdigit())):
-        sys.exit("usage: python -m c2slm_amd.phase_trace build | run [positions]")
+        sys.exit("usage: python phase_trace.py build | run [positions]")
     if sys.argv[1] == "build":
         print(build())
     else:

@@ -63,9 +63,10 @@ def fill_cache(ctx, orc, n, seed):
     orc.set_seq_len(n)
 
 
-def check_decode(ctx, orc, pos, im_end, eos, steps):
+def check_decode(ctx, orc, pos, im_end, eos, steps, full_len=False):
     """Forward(11, pos) as ingest does it, then greedy steps: normX, logits
-    and the stream equal the oracle's."""
+    and the stream equal the oracle's (full_len: all `steps` steps ran, no
+    EOS / im_end ended the stream early)."""
     tok = np.array([11], np.int32)
     got = ctx.forward(int(tok[0]), pos)
     want = orc.ingest_from(pos, tok)
@@ -81,6 +82,8 @@ def check_decode(ctx, orc, pos, im_end, eos, steps):
             break
     ref = orc.generate(steps, im_end, eos, PENALTY)
     assert np.array_equal(np.array(stream, np.int32), ref)
+    if full_len:
+        assert len(stream) == steps
     nx = np.ctypeslib.as_array(O.lib().orc_state_normx(orc.state), shape=(ctx.desc.n_embd,))
     assert np.array_equal(bits(ctx.normx()), bits(nx))
 
@@ -158,13 +161,16 @@ def test_long_kernels_nan_score_zero(tiny_model_path):
 
 @pytest.mark.parametrize("n_ctx", [512, 4096, 32768])
 def test_full_model_long_context(full_model_path, n_ctx):
-    # Forward at pos attends n_ctx positions; the greedy steps after it run
-    # on to pos + steps (the last one attends all 32768 at the largest size)
+    # Forward at pos = n_ctx - 65 after pos cached positions, then 64 greedy
+    # steps (c2slm.go:144-226): the last step forwards its token at
+    # n_ctx - 1 and attends all n_ctx positions.  The 64-token stream, the
+    # final normX and the logits at pos equal the oracle's bit for bit.
     gf, ctx, orc, im_end, eos = open_pair(full_model_path, max_ctx=32768)
-    steps = 4 if n_ctx == 32768 else 8
-    pos = n_ctx - 1 - (steps if n_ctx == 32768 else 0)
+    steps = 64
+    pos = n_ctx - 1 - steps
     fill_cache(ctx, orc, pos, seed=n_ctx)
-    check_decode(ctx, orc, pos, im_end, eos, steps=steps)
+    check_decode(ctx, orc, pos, im_end, eos, steps=steps, full_len=True)
+    assert ctx.seq_len == n_ctx
     ctx.close()
     orc.close()
 

@@ -149,6 +149,64 @@ def test_device_fed_steps_match_host_loop(tiny):
     assert np.array_equal(bits(ctx.normx()), bits(want_nx))
 
 
+def test_device_fed_steps_then_step_on_fresh_context(tiny_model_path, tiny):
+    # A fresh context's first c2h_step after c2h_time_steps(iters=3): the
+    # step numbers the device-fed graphs publish must not be one the next
+    # c2h_step waits for, or it would return a token of the earlier steps
+    _, ctx_h, _, im_end, eos = tiny
+    prompt = np.random.default_rng(35).integers(0, 4096, 32).astype(np.int32)
+
+    def ingest(c):
+        c.set_token_ids(0, prompt)
+        for p, t in enumerate(prompt):
+            c.forward(int(t), p, want_normx=False)
+
+    ingest(ctx_h)
+    host = [ctx_h.step(32 + i, PENALTY, im_end, eos) for i in range(6)]
+    ctx_h.sync()
+    gf = G.GGUFFile(tiny_model_path)
+    ctx = H.Ctx(H.desc_from_gguf(gf, max_ctx=512))
+    try:
+        H.load_gguf_into(ctx, gf)
+        ingest(ctx)
+        ctx.time_steps(32, 3, PENALTY, im_end, eos)
+        tail = [ctx.step(35 + i, PENALTY, im_end, eos) for i in range(3)]
+        ctx.sync()
+        assert tail == host[3:]
+        assert np.array_equal(ctx.token_ids(32, 6), np.array(host, np.int32))
+    finally:
+        ctx.close()
+
+
+def test_layer_kernel_timing_leaves_state(tiny):
+    # c2h_time_layer_kernel writes KV only at SeqLen and restores X and the
+    # normX buffer its final norm writes: a step after it, and after
+    # c2h_restore_normx, equals one without it
+    gf, ctx, orc, im_end, eos = tiny
+    prompt = np.random.default_rng(36).integers(0, 4096, 16).astype(np.int32)
+    ctx.set_token_ids(0, prompt)
+    for p, t in enumerate(prompt):
+        ctx.forward(int(t), p, want_normx=False)
+    nx0 = ctx.normx()
+    ctx.restore_normx()
+    prev = ctx.normx()
+    ctx.forward(int(prompt[-1]), 15, want_normx=False)
+    for k in H.Ctx.KERNELS:
+        ctx.time_layer_kernel(k, 4)
+    assert np.array_equal(bits(ctx.normx()), bits(nx0))
+    ctx.restore_normx()
+    assert np.array_equal(bits(ctx.normx()), bits(prev))
+    ctx.forward(int(prompt[-1]), 15, want_normx=False)
+    a = ctx.step(16, PENALTY, im_end, eos)
+    ctx.sync()
+    orc.ingest_from(0, prompt)
+    assert a == int(orc.generate(1, im_end, eos, PENALTY)[0])
+    ctx.set_seq(512)
+    with pytest.raises(H.C2hError):
+        ctx.time_layer_kernel("qkv", 4)
+    ctx.set_seq(17)
+
+
 def test_session_differential_ingestion(tiny):
     # c2slm_test.go:60-105: prefix then suffix == one shot, bit for bit
     gf, ctx, orc, _, _ = tiny
