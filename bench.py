@@ -11,10 +11,10 @@ then Forward(best, pos); only the chosen id crosses to the host each step.
 
 Prints one JSON line: value = K / wall time of the K steps on one GPU; the
 roofline of ffn_in, the layer kernel that moves the most bytes (RMSNorm +
-Q8_K + gate/up Q4_K GEMV + SwiGLU; each launch timed between its own pair of
-HIP events, over the 24 layers' weights, as a kernel trace times a
-dispatch); and the CPU baseline (the oracle on this host's cores, same
-workload).
+Q8_K + gate/up Q4_K GEMV + SwiGLU; eager launches back to back over the 24
+layers' weights, paced by the GPU, between one pair of HIP events: the
+per-dispatch time a kernel trace of `bench.py --only roofline` records);
+and the CPU baseline (the oracle on this host's cores, same workload).
 `extra` adds, outside the timed region: every decode kernel's time, bytes
 and GB/s and the step's bytes and GB/s; the vocab kernel from HBM; the
 operator microbench of the layer shapes (Q4_K/Q6_K x Q8_K GEMV and the Q8_K
@@ -108,9 +108,12 @@ def cpu_baseline(gf, prompt, steps, im_end, eos, runs: int = 5, single_steps: in
 def profiled_traffic(kernel: str):
     """HBM bytes per launch of `kernel` as measured by the rocprofv3 --pmc
     passes (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration)
-    recorded in profiles/*_traffic.txt; None when no record names it."""
+    recorded in profiles/roofline_*.md (the roofline command's own passes)
+    or profiles/*_traffic.txt; None when no record names it."""
     import glob
-    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_traffic.txt"))):
+    paths = sorted(glob.glob(os.path.join(ROOT, "profiles", "roofline_*.md")))
+    paths += sorted(glob.glob(os.path.join(ROOT, "profiles", "*_traffic.txt")))
+    for path in paths:
         try:
             with open(path, encoding="utf-8") as f:
                 for line in f:
@@ -170,27 +173,60 @@ KERNEL_NAMES = {"qkv": "k_gemv_row<3, PRO_NORM, MODE_BIAS>", "attn": "k_attn_cor
 
 def decode_kernels(ctx, gf, desc, vocab_ms, step_ms, T, iters: int = 96):
     """Each decode kernel's device time per launch (c2h_time_layer_kernel,
-    `iters` launches over the layers' weights): `us` each eager launch
-    between its own pair of HIP events (the per-dispatch duration a
-    rocprofv3 kernel trace records), `us_b2b` eager launches back to back
-    between one pair of events, `us_graph` the same launches captured in
-    one graph (the figure a step's replay sees); its algorithmic bytes and
-    GB/s at `us`, and its share of the step at `us_graph`."""
+    `iters` launches over the layers' weights, one pair of HIP events):
+    `us` eager launches back to back, paced by the GPU (the host enqueues
+    them all behind a short wait on the device; a rocprofv3 kernel trace of
+    the same launches records per-dispatch durations within a few per cent
+    of it), `us_graph` the same launches captured in one graph (the figure a
+    step's replay sees); its algorithmic bytes and GB/s at `us`, and its
+    share of the step at `us_graph`."""
     nbytes = kernel_bytes(gf, desc, T)
     per_step = {k: desc.n_layers for k in ("qkv", "attn", "attn_out", "ffn_in", "ffn_out")}
     per_step.update(final_norm=1, vocab=1)
     out = {}
     for k in ctx.KERNELS:
-        us = ctx.time_layer_kernel(k, iters, per_launch=True) * 1e3
-        usb = ctx.time_layer_kernel(k, iters) * 1e3
+        us = ctx.time_layer_kernel(k, iters) * 1e3
         usg = ctx.time_layer_kernel(k, iters, captured=True) * 1e3
-        out[k] = {"us": round(us, 3), "us_b2b": round(usb, 3), "us_graph": round(usg, 3)}
+        out[k] = {"us": round(us, 3), "us_graph": round(usg, 3)}
     out["vocab"] = {"us": round(vocab_ms * 1e3, 3), "us_graph": round(vocab_ms * 1e3, 3)}
     for k, v in out.items():
         gbs = nbytes[k] / (v["us"] * 1e-6) / 1e9
         v.update(bytes=nbytes[k], gb_s=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4),
                  launches_per_step=per_step[k],
                  share_of_step=round(v["us_graph"] * per_step[k] / (step_ms * 1e3), 4), kernel=KERNEL_NAMES[k])
+    return out
+
+
+def roofline_timing(ctx, gf, desc, prompt, iters: int):
+    """The roofline line's kernel (ffn_in) on a fixed state: the prompt
+    ingested by one batched prefill (which launches no k_gemv_row), then
+    `iters` eager launches back to back over the 24 layers' weights, paced by
+    the GPU, between one pair of HIP events.  The kernel's time depends on
+    its input (the exact RMSNorm sum takes more rounds on some rows), so the
+    bench line and `bench.py --only roofline` (the profiled command) time it
+    on the same state."""
+    ctx.prefill(prompt, 0, want_normx=False)
+    us = ctx.time_layer_kernel(ROOFLINE_KERNEL, iters) * 1e3
+    nb = kernel_bytes(gf, desc, PROMPT_LEN + 1)[ROOFLINE_KERNEL]
+    return us, nb
+
+
+def producer_consumer_wait(ctx, n_launch: int = 100, reps: int = 5):
+    """The cost of a producer -> consumer dependency inside one launch
+    against a kernel boundary (c2h_time_producer_consumer): for the
+    producer/consumer workgroup counts of the decode layer's boundaries
+    (qkv 129 -> attention, attention 14 -> attn_out, ffn_out 150 -> the
+    next qkv, ffn_in 232 -> ffn_out), without and with 400 dependent float
+    steps of producer work, under both wait protocols (per-XCD counters;
+    outputs tagged with the launch number), µs per fused launch and per
+    split launch pair; plus the launch floor at those grids."""
+    out = {"launch_floor_us": {g: round(ctx.launch_floor(240, g, 5), 3) for g in (57, 185, 279, 382)}}
+    for proto, name in ((0, "counters"), (1, "tagged")):
+        for work in (0, 400):
+            for p, c in ((14, 43), (129, 56), (150, 129), (232, 150)):
+                f, sp = ctx.time_producer_consumer(p, c, work, n_launch, reps, proto)
+                out[f"{name}_P{p}_C{c}_work{work}"] = {"fused_us": round(f, 3), "split_pair_us": round(sp, 3),
+                                                       "saving_us": round(sp - f, 3)}
     return out
 
 
@@ -410,7 +446,7 @@ def main():
                     help="with --only kernels: greedy steps after the prompt up to this position, so attention "
                          "covers pos+1 positions (default: the decode line's last position, prompt + warmup + steps)")
     ap.add_argument("--only", choices=["prefill", "long", "float-dots", "real-formats", "vocab", "microbench",
-                                       "kernels", "qwen3"],
+                                       "kernels", "qwen3", "roofline", "wait"],
                     default=None,
                     help="run just the prefill reps or just the long-context decode (profiler runs); "
                          "prints their JSON object, not the bench line")
@@ -452,10 +488,12 @@ def main():
         os.rmdir(rdir)
         cleanup()
         return
-    if args.only in ("float-dots", "microbench"):
+    if args.only in ("float-dots", "microbench", "wait"):
         ctx = H.Ctx(None)
         if args.only == "float-dots":
             print(json.dumps({"float_x_dots": float_x_dots(ctx)}))
+        elif args.only == "wait":
+            print(json.dumps({"producer_consumer_wait": producer_consumer_wait(ctx)}))
         else:
             print(json.dumps({"layer_microbench": layer_microbench(ctx)}))
         ctx.close()
@@ -484,13 +522,23 @@ def main():
         for p in range(PROMPT_LEN, kpos):
             ctx.step(p, PENALTY, im_end, eos)
         ctx.sync()
-        out = {k: [round(ctx.time_layer_kernel(k, args.kernel_iters, per_launch=True) * 1e3, 3)]
-                  + [round(ctx.time_layer_kernel(k, args.kernel_iters, captured=g) * 1e3, 3) for g in (False, True)]
+        out = {k: [round(ctx.time_layer_kernel(k, args.kernel_iters, captured=g) * 1e3, 3) for g in (False, True)]
                for k in ctx.KERNELS}
         out["attended_positions"] = ctx.seq_len + 1
         if args.copy_calib_mib:
             copy_calibration(ctx, args.copy_calib_mib)
-        print(json.dumps({"decode_kernels_us_per_launch_b2b_graph": out}))
+        print(json.dumps({"decode_kernels_us_eager_graph": out}))
+        ctx.close()
+        cleanup()
+        return
+    if args.only == "roofline":  # the roofline line's timing alone (profiler runs)
+        us, nb = roofline_timing(ctx, gf, desc, prompt, args.kernel_iters)
+        if args.copy_calib_mib:
+            copy_calibration(ctx, args.copy_calib_mib)
+        print(json.dumps({"roofline_kernel": f"{ROOFLINE_KERNEL}: {KERNEL_NAMES[ROOFLINE_KERNEL]}",
+                          "launches_timed": args.kernel_iters, "us_per_launch": round(us, 3), "bytes_per_launch": nb,
+                          "achieved_gbs": round(nb / (us * 1e-6) / 1e9, 1),
+                          "frac": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}))
         ctx.close()
         cleanup()
         return
@@ -506,6 +554,12 @@ def main():
         ctx.close()
         cleanup()
         return
+
+    # first on the fresh context: the roofline kernel on the state bench.py
+    # --only roofline reproduces (model uploaded, the prompt ingested by a
+    # batched prefill); its time depends on the caches' contents, which the
+    # later work changes
+    roof_us, roof_bytes = roofline_timing(ctx, gf, desc, prompt, args.kernel_iters)
 
     ctx.set_token_ids(0, prompt)
     for p, t in enumerate(prompt):
@@ -534,9 +588,6 @@ def main():
     kern = decode_kernels(ctx, gf, desc, vocab_ms, ms_per_step, pos + 1, args.kernel_iters)
     step_bytes = sum(v["bytes"] * v["launches_per_step"] for k, v in kern.items() if k != "attn")
     step_bytes += desc.n_layers * kernel_bytes(gf, desc, t_avg)["attn"]
-    dom = ROOFLINE_KERNEL
-    dk = kern[dom]
-    achieved = dk["bytes"] / (dk["us"] * 1e-6) / 1e9
 
     pipelined_ms = ctx.time_steps(pos, args.pipelined_iters, PENALTY, im_end, eos)
     # In-step timing: a forward pass between launches streams the layer
@@ -578,6 +629,9 @@ def main():
     fdots = None if args.no_float_dots else float_x_dots(ctx)
     micro = None if args.no_microbench else layer_microbench(ctx)
 
+    achieved = roof_bytes / (roof_us * 1e-6) / 1e9
+    dk = kern[ROOFLINE_KERNEL]
+
     base = None
     if not args.no_cpu_baseline:
         base = cpu_baseline(gf, prompt, args.steps, im_end, eos)
@@ -601,12 +655,13 @@ def main():
                                f"repetition penalty {PENALTY}",
                    "batch": 1, "prompt_len": PROMPT_LEN, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(dom),
-                     "kernel": f"{dom}: {dk['kernel']} (the layer kernel with the most bytes; "
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(ROOFLINE_KERNEL),
+                     "kernel": f"{ROOFLINE_KERNEL}: {dk['kernel']} (the layer kernel with the most bytes; "
                                f"{dk['share_of_step']:.0%} of the step)",
-                     "bytes_per_launch": dk["bytes"], "us_per_launch": dk["us"],
-                     "timing": f"{args.kernel_iters} eager launches over the 24 layers' weights, each between its own "
-                               "pair of HIP events on the context stream (per-dispatch time, as a kernel trace)"},
+                     "bytes_per_launch": roof_bytes, "us_per_launch": round(roof_us, 3),
+                     "timing": f"{args.kernel_iters} eager launches back to back over the 24 layers' weights, paced "
+                               "by the GPU, one pair of HIP events on the context stream, on a fresh context after a "
+                               "batched prefill of the prompt (the state `bench.py --only roofline` reproduces)"},
         "cpu_baseline": base,
         "extra": {"step": {"bytes": int(step_bytes), "gb_s": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
                            "hbm_frac": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

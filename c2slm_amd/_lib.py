@@ -87,6 +87,8 @@ def lib():
             "c2h_time_vocab": (C.c_int, [VP, I32, I32, I32, C.POINTER(C.c_float)]),
             "c2h_copy_bench": (C.c_int, [VP, C.c_int64, I32, C.POINTER(C.c_float)]),
             "c2h_launch_floor": (C.c_int, [VP, I32, I32, I32, C.POINTER(C.c_float)]),
+            "c2h_time_producer_consumer": (C.c_int, [VP, I32, I32, I32, I32, I32, I32, C.POINTER(C.c_float),
+                                                     C.POINTER(C.c_float)]),
             "c2h_check_rms_scale": (C.c_int, [VP, C.c_uint32, C.c_uint64, C.POINTER(C.c_uint64),
                                               C.POINTER(C.c_uint32)]),
             "c2h_time_steps": (C.c_int, [VP, I32, I32, C.c_float, I32, I32, C.POINTER(C.c_float)]),
@@ -235,6 +237,15 @@ class Ctx:
         self._chk(lib().c2h_launch_floor(self.h, n, grid, reps, C.byref(us)))
         return us.value
 
+    def time_producer_consumer(self, n_prod: int, n_cons: int, work: int = 0, n_launch: int = 100,
+                               reps: int = 5, proto: int = 0) -> tuple[float, float]:
+        """(µs per fused producer->consumer launch, µs per split launch pair)
+        (c2h_time_producer_consumer; proto 0 counters, 1 tagged outputs)."""
+        f, sp = C.c_float(), C.c_float()
+        self._chk(lib().c2h_time_producer_consumer(self.h, n_prod, n_cons, work, n_launch, reps, proto, C.byref(f),
+                                                   C.byref(sp)))
+        return f.value, sp.value
+
     def check_rms_scale(self, lo: int, hi: int) -> tuple[int, int]:
         """(mismatches, lowest mismatching bit pattern) of the kernels' RMSNorm
         scale against the IEEE sqrt and division over patterns [lo, hi)."""
@@ -249,13 +260,11 @@ class Ctx:
 
     KERNELS = ("qkv", "attn", "attn_out", "ffn_in", "ffn_out", "final_norm")  # C2H_KERNEL_*
 
-    def time_layer_kernel(self, kernel: str, iters: int, captured: bool = False, per_launch: bool = False) -> float:
+    def time_layer_kernel(self, kernel: str, iters: int, captured: bool = False) -> float:
         """ms per launch of one decoder-layer kernel (c2h_time_layer_kernel):
-        eager launches between one pair of events, one captured graph, or
-        (per_launch) eager launches each between its own pair of events."""
+        eager launches back to back (paced by the GPU), or one captured graph."""
         ms = C.c_float()
-        mode = 2 if per_launch else int(captured)
-        self._chk(lib().c2h_time_layer_kernel(self.h, self.KERNELS.index(kernel), iters, mode, C.byref(ms)))
+        self._chk(lib().c2h_time_layer_kernel(self.h, self.KERNELS.index(kernel), iters, int(captured), C.byref(ms)))
         return ms.value
 
     def time_gemv(self, ggml_type: int, w: np.ndarray, xq: np.ndarray, rows: int, cols: int, iters: int,

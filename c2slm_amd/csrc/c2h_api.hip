@@ -2039,6 +2039,106 @@ int c2h_launch_floor(c2h_ctx* c, int32_t n, int32_t grid, int32_t reps, float* u
   return C2H_OK;
 }
 
+int c2h_time_producer_consumer(c2h_ctx* c, int32_t n_prod, int32_t n_cons, int32_t work, int32_t n_launch,
+                               int32_t reps, int32_t proto, float* us_fused, float* us_split) {
+  if (!c || !us_fused || !us_split || n_prod <= 0 || n_prod > 4096 || n_cons <= 0 || n_cons > 4096 || work < 0 ||
+      work > 100000 || n_launch <= 0 || n_launch > 256 || reps <= 0 || proto < 0 || proto > 1)
+    return C2H_ERR_INVALID;
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  constexpr int kData = 896;  // k_pc_bench polls up to 8 x 256 outputs per thread set
+  unsigned* counters = nullptr;
+  uint64_t* data_ll = nullptr;
+  float *data = nullptr, *out = nullptr;
+  uint4* weights = nullptr;
+  int* err = nullptr;
+  hipGraph_t g[2] = {nullptr, nullptr};
+  hipGraphExec_t ge[2] = {nullptr, nullptr};
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  float best[2] = {0.0f, 0.0f};
+  int herr[2] = {0, 0};
+  const size_t wbytes = (size_t)n_launch * n_cons * 4 * 256 * sizeof(uint4);
+  hipError_t e = hipMalloc(&counters, 8 * 64 * sizeof(unsigned));
+  if (e == hipSuccess) e = hipMalloc(&data, kData * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&out, (size_t)n_cons * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&weights, wbytes);
+  if (e == hipSuccess) e = hipMalloc(&err, 2 * sizeof(int));
+  if (e == hipSuccess) e = hipMalloc(&data_ll, kData * sizeof(uint64_t));
+  if (e == hipSuccess) e = hipMemsetAsync(weights, 0x5a, wbytes, c->stream);
+  if (e == hipSuccess) e = hipMemsetAsync(err, 0, 2 * sizeof(int), c->stream);
+  if (e == hipSuccess) e = hipEventCreate(&e0);
+  if (e == hipSuccess) e = hipEventCreate(&e1);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  PcBenchParams P;
+  memset(&P, 0, sizeof(P));
+  P.counters = counters;
+  P.data = data;
+  P.weights = weights;
+  P.out = out;
+  P.err = err;
+  P.n_prod = n_prod;
+  P.n_cons = n_cons;
+  P.spin_limit = 1 << 20;  // polls of >= ~0.5 us each: every wait ends within about a second
+  P.data_floats = kData;
+  P.work = work;
+  P.proto = proto;
+  P.data_ll = data_ll;
+  // graph 0: the counters (and the tagged outputs' epochs) cleared by a
+  // kernel, then n_launch fused launches
+  // (epoch i+1: the counters' sum a launch's consumers wait for); graph 1:
+  // the same work as a producer launch and a consumer launch per step
+  for (int which = 0; which < 2 && e == hipSuccess; ++which) {
+    e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) break;
+    if (which == 0) {
+      hipLaunchKernelGGL(k_fill_u32, dim3(2), dim3(256), 0, c->stream, counters, 8 * 64, 0u);
+      hipLaunchKernelGGL(k_fill_u32, dim3(8), dim3(256), 0, c->stream, reinterpret_cast<unsigned*>(data_ll),
+                         2 * kData, 0u);
+    }
+    for (int i = 0; i < n_launch; ++i) {
+      P.epoch = i + 1;
+      P.w_index = i;
+      if (which == 0) {
+        P.mode = 0;
+        hipLaunchKernelGGL(k_pc_bench, dim3(n_prod + n_cons), dim3(256), 0, c->stream, P);
+      } else {
+        P.mode = 1;
+        hipLaunchKernelGGL(k_pc_bench, dim3(n_prod), dim3(256), 0, c->stream, P);
+        P.mode = 2;
+        hipLaunchKernelGGL(k_pc_bench, dim3(n_cons), dim3(256), 0, c->stream, P);
+      }
+    }
+    e = hipStreamEndCapture(c->stream, &g[which]);
+    if (e == hipSuccess) e = hipGraphInstantiate(&ge[which], g[which], nullptr, nullptr, 0);
+  }
+  for (int r = 0; e == hipSuccess && r < reps + 1; ++r) {  // one untimed replay of each first
+    for (int which = 0; which < 2 && e == hipSuccess; ++which) {
+      float ms = 0.0f;
+      e = hipEventRecord(e0, c->stream);
+      if (e == hipSuccess) e = hipGraphLaunch(ge[which], c->stream);
+      if (e == hipSuccess) e = hipEventRecord(e1, c->stream);
+      if (e == hipSuccess) e = hipEventSynchronize(e1);
+      if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+      if (e == hipSuccess && r >= 1 && (r == 1 || ms < best[which])) best[which] = ms;
+    }
+  }
+  if (e == hipSuccess) e = hipMemcpy(herr, err, sizeof(herr), hipMemcpyDeviceToHost);
+  for (int i = 0; i < 2; ++i) {
+    if (ge[i]) (void)hipGraphExecDestroy(ge[i]);
+    if (g[i]) (void)hipGraphDestroy(g[i]);
+  }
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  for (void* p : {(void*)counters, (void*)data, (void*)out, (void*)weights, (void*)err, (void*)data_ll})
+    if (p) (void)hipFree(p);
+  if (e != hipSuccess) return fail(c, C2H_ERR_HIP, "producer/consumer timing: %s", hipGetErrorString(e));
+  if (herr[0]) return fail(c, C2H_ERR_HIP, "producer/consumer timing: a consumer's wait ran out");
+  if (herr[1]) return fail(c, C2H_ERR_HIP, "producer/consumer timing: %d outputs read stale", herr[1]);
+  *us_fused = best[0] * 1000.0f / n_launch;
+  *us_split = best[1] * 1000.0f / n_launch;
+  return C2H_OK;
+}
+
 int c2h_time_vocab(c2h_ctx* c, int32_t iters, int32_t pos, int32_t in_step, float* ms) {
   if (!c || !ms || iters <= 0 || iters > 4096) return C2H_ERR_INVALID;
   HIPCHK(c, hipSetDevice(c->device));
@@ -2272,39 +2372,21 @@ int c2h_time_layer_kernel(c2h_ctx* c, int32_t kernel, int32_t iters, int32_t cap
   float t = 0.0f;
   hipGraph_t g = nullptr;
   hipGraphExec_t ge = nullptr;
-  if (!rc && captured == 2) {
-    // one pair of events around each eager launch: the sum of the pairs'
-    // times, the per-dispatch duration a kernel trace of the same launches
-    // records (no overlap of a launch's set-up with the previous kernel)
-    for (int i = 0; i < D.n_layers; ++i) one(i);  // warm-up: every layer once
-    std::vector<hipEvent_t> ev(2 * (size_t)iters, nullptr);
-    hipError_t e = hipSuccess;
-    for (auto& x : ev)
-      if (e == hipSuccess) e = hipEventCreate(&x);
-    for (int i = 0; e == hipSuccess && i < iters; ++i) {
-      e = hipEventRecord(ev[2 * i], c->stream);
-      one(i);
-      if (e == hipSuccess) e = hipEventRecord(ev[2 * i + 1], c->stream);
-    }
-    if (e == hipSuccess) e = hipGetLastError();
-    if (e == hipSuccess) e = hipEventSynchronize(ev.back());
-    double total = 0.0;
-    for (int i = 0; e == hipSuccess && i < iters; ++i) {
-      float ms1 = 0.0f;
-      e = hipEventElapsedTime(&ms1, ev[2 * i], ev[2 * i + 1]);
-      total += ms1;
-    }
-    for (auto& x : ev)
-      if (x) (void)hipEventDestroy(x);
-    if (e != hipSuccess) rc = fail(c, C2H_ERR_HIP, "kernel timing failed: %s", hipGetErrorString(e));
-    t = (float)total;
-  } else if (!rc) {
+  if (!rc) {
+    // eager: the GPU first waits 60 us per launch to come (several times
+    // the host's enqueue time of a launch, also under a kernel-trace
+    // profiler), so the warm-up and the timed launches run back to back,
+    // paced by the GPU rather than by the host's enqueue rate
+    const bool eager = !(captured && c->use_graphs);
+    if (eager)
+      hipLaunchKernelGGL(k_delay, dim3(1), dim3(64), 0, c->stream,
+                         std::min<long long>(C2H_DELAY_MAX_TICKS, 6000ll * (iters + D.n_layers)));
     for (int i = 0; i < D.n_layers; ++i) one(i);  // warm-up: every layer once
     // captured: the timed launches replay as one graph (as the decode step
     // does), so the host's launch rate does not pace them; eager when the
     // context runs without graphs (C2H_NO_GRAPH=1)
     hipError_t e = hipSuccess;
-    if (captured && c->use_graphs) {
+    if (!eager) {
       e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
       if (e == hipSuccess) {
         for (int i = 0; i < iters; ++i) one(i);

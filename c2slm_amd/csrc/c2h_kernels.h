@@ -461,6 +461,39 @@ __host__ __device__ inline int dot_rows_lds_bytes(int type, int cols) {
 __global__ void k_argmax_final(const float* pv, const int* pi, int n, C2hState* state);
 __global__ void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16);
 __global__ void k_empty(const int* __restrict__ flag, int* __restrict__ out);
+// One wave that returns after `ticks` of the 100 MHz real-time counter
+// (bounded: the caller passes at most C2H_DELAY_MAX_TICKS); a timing call
+// puts it ahead of eager launches so that they run paced by the GPU, not by
+// the host's enqueue rate.
+constexpr long long C2H_DELAY_MAX_TICKS = 1000000;  // 10 ms
+__global__ void k_delay(long long ticks);
+// Producer -> consumer wait in one launch (measurement of the cost of
+// replacing a kernel boundary by a counter wait).  Workgroups below n_prod
+// (mode 0) are producers: a dependent chain of `work` steps, then their
+// share of data_floats outputs, stored with agent-scope stores; once those
+// are complete, one agent-scope atomic add per workgroup on counter
+// blockIdx % 8.  The others are consumers: they load a 16 KB weight slice,
+// then poll the counters (relaxed agent-scope loads, s_sleep between polls)
+// until their sum reaches `target`, read every output with agent-scope loads
+// and check it.  proto 1 drops the counters: every output is one 8-byte
+// agent-scope store of {value, epoch}, and a consumer polls the outputs it
+// reads until each carries the launch's epoch.
+// mode 1: producers only (no counter); mode 2: consumers only
+// (no wait): the same work split over two launches.  Every wait is bounded
+// by spin_limit polls; a consumer that runs out sets err[0] = 1 and exits,
+// a wrong output value adds to err[1].
+struct PcBenchParams {
+  unsigned* counters;     // 8 counters, 64 dwords apart
+  float* data;            // [data_floats]
+  const uint4* weights;   // consumer prefetch: 1,024 uint4 per (launch, consumer)
+  float* out;             // one value per consumer workgroup
+  int* err;               // [2]
+  uint64_t* data_ll;      // proto 1: [data_floats] of {value bits, epoch}
+  int n_prod, n_cons, mode, epoch, spin_limit, data_floats, work, w_index;
+  int proto;              // 0: counters; 1: each output carries its epoch (no counter)
+};
+__global__ void k_pc_bench(PcBenchParams P);
+__global__ void k_fill_u32(unsigned* p, int n, unsigned v);
 __global__ void k_check_rms_scale(uint32_t lo, uint32_t n, unsigned long long* bad, uint32_t* first);
 
 }  // namespace c2h

@@ -3329,6 +3329,124 @@ __global__ void __launch_bounds__(256) k_empty(const int* __restrict__ flag, int
   if (threadIdx.x == 0 && blockIdx.x == 0 && flag[0] == 0x5eed) out[0] = 1;
 }
 
+__global__ void __launch_bounds__(64) k_delay(long long ticks) {
+  const long long t0 = (long long)__builtin_amdgcn_s_memrealtime();
+  const long long n = min(max(ticks, 0ll), C2H_DELAY_MAX_TICKS);
+  while ((long long)__builtin_amdgcn_s_memrealtime() - t0 < n) __builtin_amdgcn_s_sleep(8);
+}
+
+__global__ void __launch_bounds__(256) k_fill_u32(unsigned* p, int n, unsigned v) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = v;
+}
+
+__global__ void __launch_bounds__(256) k_pc_bench(PcBenchParams P) {
+  const int bid = blockIdx.x, tid = threadIdx.x;
+  const bool producer = (P.mode == 1) || (P.mode == 0 && bid < P.n_prod);
+  const float base = (float)(P.epoch * 4096);
+  if (producer) {
+    float v = (float)tid;
+    for (int i = 0; i < P.work; ++i) v = v * 1.0000001f + 1.0f;  // a dependent chain
+    const int per = (P.data_floats + P.n_prod - 1) / P.n_prod;
+    for (int i = tid; i < per; i += 256) {
+      const int idx = bid * per + i;
+      const float val = base + (float)idx + (v < 0.0f ? 1.0f : 0.0f);
+      if (idx < P.data_floats) {
+        if (P.mode == 0 && P.proto == 1)  // the split form passes plain floats through the boundary
+          __hip_atomic_store(&P.data_ll[idx], ((uint64_t)(uint32_t)P.epoch << 32) | __float_as_uint(val),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          __hip_atomic_store(&P.data[idx], val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    if (P.mode == 0 && P.proto == 0) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's outputs are complete
+      __syncthreads();
+      if (tid == 0) __hip_atomic_fetch_add(&P.counters[(bid & 7) * 64], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
+  const int cb = (P.mode == 0) ? bid - P.n_prod : bid;
+  uint4 w[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) w[k] = P.weights[(((size_t)P.w_index * P.n_cons + cb) * 4 + k) * 256 + tid];
+  __shared__ int ok;
+  __shared__ float red[4];
+  float acc = 0.0f;
+  int bad = 0;
+  if (P.mode == 0 && P.proto == 1) {
+    // poll this thread's outputs until each carries the epoch
+    constexpr int kMaxPer = 8;  // data_floats <= 8 * 256
+    uint64_t got[kMaxPer];
+    int spin = 0;
+    bool ready = false;
+    while (!ready && spin < P.spin_limit) {
+      ready = true;
+#pragma unroll
+      for (int k = 0; k < kMaxPer; ++k) {
+        const int i = tid + 256 * k;
+        if (i < P.data_floats) {
+          got[k] = __hip_atomic_load(&P.data_ll[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ready = ready && (uint32_t)(got[k] >> 32) == (uint32_t)P.epoch;
+        }
+      }
+      if (!ready) {
+        ++spin;
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    // a lane whose wait ran out reports it and carries on to the end (the
+    // workgroup's barrier below is reached by every wave)
+    if (!ready) __hip_atomic_store(&P.err[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k) {
+      const int i = tid + 256 * k;
+      if (i < P.data_floats) {
+        const float g = __uint_as_float((uint32_t)got[k]);
+        bad += (g != base + (float)i) ? 1 : 0;
+        acc += g;
+      }
+    }
+  } else if (P.mode == 0) {
+    if (tid < 64) {
+      const unsigned* cp = &P.counters[(tid & 7) * 64];
+      const unsigned target = (unsigned)(P.epoch * P.n_prod);
+      bool done = false;
+      for (int spin = 0; spin < P.spin_limit; ++spin) {
+        unsigned c = __hip_atomic_load(cp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid >= 8) c = 0u;
+        c += __shfl_xor(c, 1);
+        c += __shfl_xor(c, 2);
+        c += __shfl_xor(c, 4);
+        c = __shfl(c, 0);
+        if (c >= target) {
+          done = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (tid == 0) ok = done ? 1 : 0;
+    }
+    __syncthreads();
+    if (!ok) {
+      if (tid == 0) __hip_atomic_store(&P.err[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+  }
+  if (!(P.mode == 0 && P.proto == 1)) {
+    for (int i = tid; i < P.data_floats; i += 256) {
+      const float g = __hip_atomic_load(&P.data[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      bad += (g != base + (float)i) ? 1 : 0;
+      acc += g;
+    }
+  }
+  if (bad) atomicAdd(&P.err[1], bad);
+  acc += (float)((w[0].x ^ w[1].y ^ w[2].z ^ w[3].w) & 1u);
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+  if ((tid & 63) == 0) red[tid >> 6] = acc;
+  __syncthreads();
+  if (tid == 0) P.out[cb] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
 // Plain 16-byte copy (grid-stride), the calibration load for the memory
 // traffic counters: it reads and writes exactly n16*16 bytes.
 __global__ void __launch_bounds__(256) k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16) {

@@ -287,6 +287,21 @@ int c2h_copy_bench(c2h_ctx* ctx, int64_t bytes, int32_t reps, float* ms_per_copy
  * floor a chain of decode kernels pays per launch. */
 int c2h_launch_floor(c2h_ctx* ctx, int32_t n, int32_t grid, int32_t reps, float* us_per_kernel);
 
+/* Measurement aid with no counterpart in the reference: the cost of a
+ * producer -> consumer dependency inside one launch against a kernel
+ * boundary.  Fused: `n_launch` dependent launches of n_prod + n_cons
+ * workgroups (256 threads); the producers run `work` dependent float steps,
+ * store 896 floats between them and signal per-XCD counters; the consumers
+ * prefetch 16 KB of weights each, wait on the counters (bounded), then read
+ * and check the 896 floats.  Split: the same work as a producer launch then
+ * a consumer launch, n_launch times.  Best of `reps` graph replays; µs per
+ * fused launch and per split pair.  proto 0 signals through the counters;
+ * proto 1 stores each float with its launch number in one 8-byte store and
+ * the consumers poll the floats themselves (no counter).  C2H_ERR_HIP if a
+ * wait ran out or a consumer read a stale value. */
+int c2h_time_producer_consumer(c2h_ctx* ctx, int32_t n_prod, int32_t n_cons, int32_t work, int32_t n_launch,
+                               int32_t reps, int32_t proto, float* us_fused, float* us_split);
+
 /* Self-check with no counterpart in the reference: the RMSNorm scale
  * f32(1/sqrt(f64(v))) as the kernels compute it (a reciprocal square root
  * estimate and one Newton step for normal positive v) against the IEEE
@@ -306,10 +321,11 @@ int c2h_check_rms_scale(c2h_ctx* ctx, uint32_t lo, uint64_t hi, uint64_t* mismat
 
 /* Measurement aid with no counterpart in the reference: average device time
  * (ms) of one decoder-layer kernel, `iters` launches back to back on the
- * context stream between one pair of HIP events (captured == 1: as one
+ * context stream between one pair of HIP events (captured != 0: as one
  * captured graph, replayed once untimed first, unless the context runs
- * without graphs (C2H_NO_GRAPH=1); 0: eager launches; 2: eager launches,
- * each between its own pair of events, the pairs' times summed), layer
+ * without graphs (C2H_NO_GRAPH=1); 0: eager launches, behind a short
+ * bounded wait on the GPU so that the host has enqueued them all before the
+ * first runs), layer
  * i % n_layers on launch i (so each launch reads another layer's weights,
  * as inside a step), after one untimed round over the layers.  The q|k|v kernel runs the
  * later layers' prologue (RMSNorm of X) on every layer.  Inputs are the

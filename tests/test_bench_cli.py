@@ -44,3 +44,15 @@ def test_kernel_bytes_match_the_algorithmic_table():
     assert b["ffn_in"] == 4_229_120 and b["ffn_out"] == 3_601_664
     assert b["vocab"] == bench.VOCAB_BYTES
     assert b["attn"] - b0["attn"] == 1_024 * 100
+
+
+def test_roofline_kernel_is_fixed_and_its_traffic_is_recorded():
+    """The roofline line's kernel does not depend on a run's timings, and
+    the traffic it reports comes from the roofline command's own counter
+    passes, within 10 % of its algorithmic bytes."""
+    sys.path.insert(0, ROOT)
+    import bench
+    assert bench.ROOFLINE_KERNEL == "ffn_in"
+    t = bench.profiled_traffic("ffn_in")
+    assert isinstance(t, int)
+    assert 1.0 <= t / 4_229_120 < 1.1
