@@ -27,6 +27,7 @@ constexpr int PF_ATT_SUB = 16;  // batch tokens per long-context attention launc
 struct Tensor {
   uint8_t* q = nullptr;
   uint16_t* d = nullptr;
+  uint4* pf6 = nullptr;  // Q6_K: the split copy batched prefill reads (built at its first use)
   int type = -1;
   int64_t rows = 0, cols = 0;
   bool present() const { return q != nullptr; }
@@ -97,6 +98,8 @@ struct c2h_ctx {
     float* xn = nullptr;  // normalised rows as f32 (Q5_0 / Q8_0 projections)
     int8_t* q8 = nullptr;
     float* q8d = nullptr;
+    float* q8dT = nullptr;  // the Q8_K scales block-major [nbs][PF_MAX]
+    int8_t* q8T = nullptr;  // the Q8_K quants chunk-major [nbs * 8][PF_MAX][32]
     int32_t* q8bs = nullptr;
     int32_t* tok = nullptr;
     int nbs = 0;
@@ -157,6 +160,13 @@ int dalloc(c2h_ctx* c, T** p, size_t bytes) {
   c->allocs.push_back(ptr);
   *p = reinterpret_cast<T*>(ptr);
   return C2H_OK;
+}
+
+// Frees one allocation dalloc made (and forgets it).
+void dfree(c2h_ctx* c, void* p) {
+  auto it = std::find(c->allocs.begin(), c->allocs.end(), p);
+  if (it != c->allocs.end()) c->allocs.erase(it);
+  (void)hipFree(p);
 }
 
 int nb_k(int64_t cols) { return (int)(cols / 256); }
@@ -264,6 +274,11 @@ int upload_quant(c2h_ctx* c, Tensor* t, int type, int64_t rows, int64_t cols, co
   if (db) {
     if ((rc = dalloc(c, &d, db))) return rc;
     HIPCHK(c, stream_copy(c->stream, d, dh.data(), db, hipMemcpyHostToDevice));
+  }
+  if (t->pf6) {  // the split prefill copy of the previous contents
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    dfree(c, t->pf6);
+    t->pf6 = nullptr;
   }
   t->q = q;
   t->d = d;
@@ -1194,6 +1209,21 @@ int c2h_forward(c2h_ctx* c, int32_t token, int32_t pos, float* normx_out) {
 
 namespace {
 
+// The split copy (k_q6_pf_pack) of every Q6_K layer projection, built on
+// the stream at the first batched prefill after its upload.
+int pf_q6_ready(c2h_ctx* c) {
+  for (Layer& L : c->layers)
+    for (Tensor* t : {&L.wq, &L.wk, &L.wv, &L.wo, &L.wg, &L.wu, &L.wd}) {
+      if (t->type != C2H_Q6_K || t->pf6) continue;
+      const int tiles = (int)((t->rows + 31) / 32), nb = nb_k(t->cols);
+      int rc = dalloc(c, &t->pf6, (size_t)tiles * nb * PF_Q6_TILE_BYTES);
+      if (rc) return rc;
+      hipLaunchKernelGGL(k_q6_pf_pack, dim3(tiles, nb), dim3(64), 0, c->stream, t->ref(), (int)t->rows, nb, t->pf6);
+      HIPCHK(c, hipGetLastError());
+    }
+  return C2H_OK;
+}
+
 int pf_alloc(c2h_ctx* c) {
   if (c->pf.ready) return C2H_OK;
   const c2h_model_desc& D = c->desc;
@@ -1206,6 +1236,7 @@ int pf_alloc(c2h_ctx* c) {
       (rc = dalloc(c, &p.g, M * F * 4)) || (rc = dalloc(c, &p.u, M * F * 4)) || (rc = dalloc(c, &p.h, M * F * 4)) ||
       (rc = dalloc(c, &p.xn, M * E * 4)) ||
       (rc = dalloc(c, &p.q8, M * p.nbs * QK_K)) || (rc = dalloc(c, &p.q8d, M * p.nbs * 4)) ||
+      (rc = dalloc(c, &p.q8dT, M * p.nbs * 4)) || (rc = dalloc(c, &p.q8T, M * p.nbs * QK_K)) ||
       (rc = dalloc(c, &p.q8bs, M * p.nbs * 16 * 4)) || (rc = dalloc(c, &p.tok, M * 4)))
     return rc;
   p.ready = true;
@@ -1215,7 +1246,7 @@ int pf_alloc(c2h_ctx* c) {
 typedef void (*PFGemmKernel)(PFGemmParams);
 PFGemmKernel pf_gemm_kernel(int type, int mode) {
   if (type == C2H_Q4_K) return mode == MODE_RESID ? k_pf_gemm<T_Q4_K, MODE_RESID> : k_pf_gemm<T_Q4_K, MODE_BIAS>;
-  return mode == MODE_RESID ? k_pf_gemm<T_Q6_K, MODE_RESID> : k_pf_gemm<T_Q6_K, MODE_BIAS>;
+  return mode == MODE_RESID ? k_pf_gemm_q6<MODE_RESID> : k_pf_gemm_q6<MODE_BIAS>;
 }
 
 // y[t][r] (=|+=) W * x[t] for the given matrices: Q4_K / Q6_K on the
@@ -1231,10 +1262,12 @@ void pf_gemm(c2h_ctx* c, int m, int m_pad, int nb, int mode, std::initializer_li
   for (int type : {(int)C2H_Q4_K, (int)C2H_Q6_K}) {
     PFGemmParams P;
     memset(&P, 0, sizeof(P));
-    P.in = PFQ8{c->pf.q8, c->pf.q8d, c->pf.q8bs, c->pf.nbs};
+    P.in = PFQ8{c->pf.q8, c->pf.q8d, c->pf.q8bs, c->pf.nbs, c->pf.q8dT, c->pf.q8T};
     P.nb = nb;
     P.m = m;
     int tiles = 0;
+    // Q6_K: 32-row tiles of one wave (k_pf_gemm_q6); Q4_K: PF_TILE rows
+    const int rows_per_tile = (type == C2H_Q6_K) ? 32 : PF_TILE;
     for (size_t i = 0; i < W.size(); ++i) {
       if (W[i]->type != type) continue;
       PFJob& J = P.jobs[P.n_jobs++];
@@ -1242,14 +1275,22 @@ void pf_gemm(c2h_ctx* c, int m, int m_pad, int nb, int mode, std::initializer_li
       J.type = type;
       J.rows = (int)W[i]->rows;
       J.tile_begin = tiles;
-      tiles += (J.rows + PF_TILE - 1) / PF_TILE;
+      tiles += (J.rows + rows_per_tile - 1) / rows_per_tile;
+      if (type == C2H_Q6_K) J.w6 = W[i]->pf6;  // built by pf_q6_ready before the first pass
       J.mode = mode;
       J.y = Y[i];
       J.ldy = L[i];
       J.bias = B[i];
     }
     if (P.n_jobs == 0) continue;
-    hipLaunchKernelGGL(pf_gemm_kernel(type, mode), dim3(tiles, m_pad / PF_TILE), dim3(256), 0, c->stream, P);
+    P.m_pad = m_pad;
+    P.n_row_tiles = tiles;
+    if (type == C2H_Q6_K) {
+      const int per_xcd = (tiles * (m_pad / 32) + 7) / 8;
+      hipLaunchKernelGGL(pf_gemm_kernel(type, mode), dim3(8 * per_xcd), dim3(64), 0, c->stream, P);
+    } else {
+      hipLaunchKernelGGL(pf_gemm_kernel(type, mode), dim3(tiles, m_pad / PF_TILE), dim3(256), 0, c->stream, P);
+    }
   }
   PFGemmFParams F;
   memset(&F, 0, sizeof(F));
@@ -1310,7 +1351,7 @@ int pf_pass(c2h_ctx* c, const int32_t* tokens, int m, int pos0) {
   s.nx_in = c->nx_cur;
   s.nx_out = c->nx_cur ^ 1;
   if ((rc = push_state(c, s))) return rc;
-  const PFQ8 q8{p.q8, p.q8d, p.q8bs, p.nbs};
+  const PFQ8 q8{p.q8, p.q8d, p.q8bs, p.nbs, p.q8dT, p.q8T};
   const size_t norm_lds = (size_t)chain_lds_floats(E) * 4;
   for (int l = 0; l < D.n_layers; ++l) {
     Layer& L = c->layers[l];
@@ -1449,7 +1490,7 @@ int c2h_prefill(c2h_ctx* c, const int32_t* tokens, int32_t n, int32_t pos0, floa
     }
     HIPCHK(c, hipStreamSynchronize(c->stream));
   } else {
-    if ((rc = pf_alloc(c))) return rc;
+    if ((rc = pf_alloc(c)) || (rc = pf_q6_ready(c))) return rc;
     HIPCHK(c, hipStreamSynchronize(c->stream));
     c->ring_next = 0;
     for (int done = 0; done < n;) {

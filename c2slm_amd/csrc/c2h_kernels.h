@@ -278,7 +278,12 @@ struct PFQ8 {
   int8_t* q;
   float* d;
   int32_t* bs;
-  int nbs;  // block stride per token
+  int nbs;    // block stride per token
+  float* dT;  // the scales again, block-major: block b, token t at dT[b*PF_MAX + t]
+  // the quants again, by 32-element chunk: chunk k = 8b + c (elements
+  // 32c .. 32c+32 of block b), token t at qT[(k*PF_MAX + t)*32]: 32 tokens'
+  // chunk is 1 KB contiguous (the A operand of one k_pf_gemm_q6 MFMA)
+  int8_t* qT;
 };
 
 // Per token: [embed tokens[t] into X[t]] RMSNorm(X[t]) * w -> Q8_K.
@@ -307,6 +312,7 @@ struct PFQuantParams {
 
 struct PFJob {
   WeightRef w, w2;
+  const uint4* w6;  // Q6_K: the split copy k_q6_pf_pack builds (k_pf_gemm_q6)
   int type, type2;
   int rows;
   int tile_begin;  // first row tile (blockIdx.x) of this job
@@ -320,6 +326,8 @@ struct PFGemmParams {
   PFQ8 in;
   int nb;  // super-blocks per row
   int m;   // valid tokens
+  int m_pad;
+  int n_row_tiles;  // row tiles of all jobs (k_pf_gemm_q6)
   int n_jobs;
   PFJob jobs[3];
 };
@@ -408,6 +416,24 @@ template <int NB>
 __global__ void k_pf_quant(PFQuantParams P);
 template <int TYPE, int MODE>
 __global__ void k_pf_gemm(PFGemmParams P);
+// Q6_K jobs of a prefill: the reference's integer super-block sum
+// isum = sum over sub-blocks of sc * sum(q8 * (q6 - 32)) is, element by
+// element, sum(q8 * B) with B = (q6 - 32) * sc in [-4064, 4096], which
+// splits exactly into int8 parts hi = B >> 6 (in [-64, 64]) and lo = B & 63:
+// isum = 64 * sum(q8 * hi) + sum(q8 * lo), two int8 GEMMs over the 256
+// elements.  k_q6_pf_pack writes that split copy of a Q6_K matrix (rows
+// padded to 32): per (32-row tile, super-block, 32-element chunk c, part
+// hi | lo) 1 KB, lane l's 16 bytes = row l % 32, elements
+// 32c + 16 * (l / 32) .. +16 -- one v_mfma_i32_32x32x32_i8 B operand.
+// Grid (row tiles, super-blocks), 64 threads.
+constexpr size_t PF_Q6_TILE_BYTES = 32 * 512;  // one 32-row tile of one super-block
+__global__ void k_q6_pf_pack(WeightRef w, int rows, int nb, uint4* out);
+// One wave per 32 tokens x 32 rows; a 1-D grid of 8 * ceil(n_row_tiles *
+// m_pad / 32 / 8) workgroups of 64 threads (tile_begin and n_row_tiles in
+// 32-row tiles).
+template <int MODE>
+__global__ void k_pf_gemm_q6(PFGemmParams P);
+
 template <int MODE>
 __global__ void k_pf_gemm_f(PFGemmFParams P);
 __global__ void k_pf_rope_store(PFRopeParams P);

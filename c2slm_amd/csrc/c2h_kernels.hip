@@ -2421,9 +2421,13 @@ __device__ __forceinline__ void store_q8_row(const Q8KRow<NB>& s, const PFQ8& o,
   for (int i = tid; i < NB * 64; i += 256) {
     const int b = i >> 6, w = i & 63;
     reinterpret_cast<uint32_t*>(o.q + ((size_t)t * o.nbs + b) * QK_K)[w] = s.q[b][w];
+    reinterpret_cast<uint32_t*>(o.qT + (((size_t)b * 8 + (w >> 3)) * PF_MAX + t) * 32)[w & 7] = s.q[b][w];
   }
   for (int i = tid; i < NB * 16; i += 256) o.bs[((size_t)t * o.nbs + (i >> 4)) * 16 + (i & 15)] = s.bs[i >> 4][i & 15];
-  if (tid < NB) o.d[(size_t)t * o.nbs + tid] = s.d[tid];
+  if (tid < NB) {
+    o.d[(size_t)t * o.nbs + tid] = s.d[tid];
+    o.dT[(size_t)tid * PF_MAX + t] = s.d[tid];
+  }
 }
 
 // Token blockIdx.x (rows past m repeat token m-1; their results are dropped).
@@ -2828,6 +2832,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
 }
 
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
 
 // One super-block of one weight row as the MFMA A operand needs it: lane
 // (r = lane%16, k-group lk = lane/16) holds 8 consecutive quants of every
@@ -2853,16 +2858,6 @@ __device__ __forceinline__ PFA pf_load_a(const WeightRef& W, int nb, int row, in
 #pragma unroll
     for (int p = 4; p < 16; ++p) A.a[p] = A.a[0];
     A.d6 = 0;
-  } else {
-    const uint8_t* base = W.q + blk * BS_Q6K_PACKED;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const int n = c >> 2, k = c & 3;
-      A.a[c] = *reinterpret_cast<const u32x2_t*>(base + 64 * n + 32 * (k & 1) + 8 * lk);
-      A.a[8 + c] = *reinterpret_cast<const u32x2_t*>(base + 128 + 32 * n + 8 * lk);
-    }
-    A.hdr = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(base + 192));
-    A.d6 = W.d[blk];
   }
   return A;
 }
@@ -2887,27 +2882,20 @@ __device__ __forceinline__ void pf_row_params(const PFA& A, int32_t* rp) {
       rp[2 + 4 + j] = (s(j + 8) & 15) | ((s(j) >> 6) << 4);
       rp[10 + 4 + j] = (s(j + 8) >> 4) | ((s(j + 4) >> 6) << 4);
     }
-  } else {
-    rp[0] = __float_as_int(fp16_simd_nb(A.d6));
-    const uint4 h = make_uint4(A.hdr.x, A.hdr.y, A.hdr.z, A.hdr.w);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) rp[1 + j] = (int)(int8_t)byte_of(h, j);
   }
 }
 
-// tokens x rows GEMM of one prefill projection: workgroup tile = 64 rows x
-// 64 tokens; wave w owns rows [16w, 16w+16) against all 64 tokens (four
-// 16x16 MFMA tiles).  Per super-block the token tile's Q8_K block is staged
-// in LDS and the next block's weights are loaded while this one runs.
-//   Q4_K: per pair p two v_mfma_i32_16x16x32_i8 (low nibbles x q8[64p..+32),
-//   high nibbles x q8[64p+32..+32)) give s_lo, s_hi; the lane then adds the
-//   pair term of c2_tensor_dot_q4_k_q8_k_gen.go:85 for its 4 rows x 1 token.
-//   Q6_K: per 32-element quarter c two MFMAs (q8 masked to each 16-element
-//   half) give the sub-block sums; isum += (s - 32*bsum)*sc (exact int), and
-//   per super-block acc += f32(isum)*(d*q8d)
-//   (c2_tensor_gemv2_q6_k_q8_k_gen.go:168-209).
+// tokens x rows GEMM of one Q4_K prefill projection: workgroup tile = 64
+// rows x 64 tokens; wave w owns rows [16w, 16w+16) against all 64 tokens
+// (four 16x16 MFMA tiles).  Per super-block the token tile's Q8_K block is
+// staged in LDS and the next block's weights are loaded while this one
+// runs.  Per pair p two v_mfma_i32_16x16x32_i8 (low nibbles x
+// q8[64p..+32), high nibbles x q8[64p+32..+32)) give s_lo, s_hi; the lane
+// then adds the pair term of c2_tensor_dot_q4_k_q8_k_gen.go:85 for its 4
+// rows x 1 token.  (Q6_K projections run k_pf_gemm_q6.)
 template <int TYPE, int MODE>
 __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
+  static_assert(TYPE == T_Q4_K, "Q6_K prefill projections run k_pf_gemm_q6");
   __shared__ __align__(16) uint32_t sq[PF_TILE][68];  // Q8_K quants of the token tile (4-dword pad per row)
   __shared__ float sd[PF_TILE];
   __shared__ int32_t sbs[PF_TILE][17];
@@ -2959,7 +2947,7 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
     if (lk == 0) pf_row_params<TYPE>(cur, rp[wave][lr]);
     __syncthreads();
 
-    if (TYPE == T_Q4_K) {
+    {
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
         const u32x2_t qs = cur.a[p];
@@ -2989,42 +2977,6 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
           }
         }
       }
-    } else {
-      int32_t isum[4][4];
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) isum[tt][v] = 0;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const int k = c & 3;
-        const u32x2_t ql = cur.a[c], qh = cur.a[8 + c];
-        const u32x2_t lo = (k < 2) ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
-        const long a = as_long(lo | (((qh >> (2 * k)) & 0x03030303u) << 4));
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-          const int t = tt * 16 + lr;
-          const long bq = as_long(*reinterpret_cast<const u32x2_t*>(&sq[t][8 * c + 2 * lk]));
-          const long b0 = (lk < 2) ? bq : 0l;  // sub-block 2c: elements 0..15 of the chunk
-          const long b1 = (lk < 2) ? 0l : bq;  // sub-block 2c+1: elements 16..31
-          const i32x4_t zero = {0, 0, 0, 0};
-          const i32x4_t s0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b0, zero, 0, 0, 0);
-          const i32x4_t s1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, zero, 0, 0, 0);
-          const int32_t bs0 = sbs[t][2 * c], bs1 = sbs[t][2 * c + 1];
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int32_t* r = rp[wave][4 * lk + v];
-            isum[tt][v] += (s0[v] - 32 * bs0) * r[1 + 2 * c] + (s1[v] - 32 * bs1) * r[2 + 2 * c];
-          }
-        }
-      }
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        const float q8d = sd[tt * 16 + lr];
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-          acc[tt][v] = acc[tt][v] + (float)isum[tt][v] * (__int_as_float(rp[wave][4 * lk + v][0]) * q8d);
-      }
     }
     cur = nxt;
   }
@@ -3046,6 +2998,156 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
     }
   }
 }
+
+// The split copy of a Q6_K matrix for k_pf_gemm_q6 (layout with the
+// declaration).  Element e of a super-block (c2_tensor_gemv2_q6_k_q8_k_gen.go
+// :112-140): half n = e / 128, quarter k = (e % 128) / 32, l = e % 32;
+// q6 = (ql[64n + 32(k & 1) + l] >> 4 * (k >= 2)) & 15 | ((qh[32n + l] >> 2k) & 3) << 4,
+// sub-block e / 16 with its int8 scale.  Rows past `rows` are zero.
+__global__ void __launch_bounds__(64) k_q6_pf_pack(WeightRef w, int rows, int nb, uint4* out) {
+  const int lane = threadIdx.x, l32 = lane & 31, kg = lane >> 5;
+  const int tile = blockIdx.x, b = blockIdx.y;
+  const int row = tile * 32 + l32;
+  const bool valid = row < rows;
+  const uint8_t* blk = w.q + ((size_t)min(row, rows - 1) * nb + b) * BS_Q6K_PACKED;
+  for (int c = 0; c < 8; ++c) {
+    uint32_t hi[4] = {0u, 0u, 0u, 0u}, lo[4] = {0u, 0u, 0u, 0u};
+    for (int j = 0; j < 16; ++j) {
+      const int e = 32 * c + 16 * kg + j;
+      const int n = e >> 7, k = (e >> 5) & 3, l = e & 31;
+      const int q6 = ((blk[64 * n + 32 * (k & 1) + l] >> (4 * (k >> 1))) & 15) | (((blk[128 + 32 * n + l] >> (2 * k)) & 3) << 4);
+      const int sc = (int)(int8_t)blk[192 + (e >> 4)];
+      const int v = valid ? (q6 - 32) * sc : 0;
+      hi[j >> 2] |= (uint32_t)(uint8_t)(int8_t)(v >> 6) << (8 * (j & 3));
+      lo[j >> 2] |= (uint32_t)(v & 63) << (8 * (j & 3));
+    }
+    uint4* dst = out + (((size_t)tile * nb + b) * 8 + c) * 2 * 64 + lane;
+    dst[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    dst[64] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+  }
+}
+
+// Q6_K projection of a token batch (c2_tensor_gemv2_q6_k_q8_k_gen.go:168-209
+// per (row, token)), one wave per 32 tokens x 32 rows.  Per super-block b:
+// eight 32-element chunks, each two v_mfma_i32_32x32x32_i8 on the split
+// copy (A = the 32 tokens' Q8_K quants from the chunk-major copy, lane l:
+// token l % 32, elements 32c + 16 * (l / 32) .. +16; B = hi or lo of the 32
+// rows), accumulated in the MFMA; then isum = 64 * D_hi + D_lo, exactly the
+// reference's integer, and acc += f32(isum) * (d * q8d) in super-block
+// order.  Lane l holds row l % 32 and tokens 8 * (i / 4) + 4 * (l / 32) +
+// i % 4 (i = 0..15).  The next super-block's operands are in flight while
+// one runs; no LDS, no barrier.  (Measured against this form, all slower:
+// one workgroup of four waves per tile, each wave a quarter of the
+// super-blocks and the terms of three of them folded in order through LDS,
+// 36.9 against 29.5 us for the 512-token ffn_down; four accumulation chains
+// instead of two, 31.1 against 28.3 us.)
+template <int MODE>
+__global__ void __launch_bounds__(64) k_pf_gemm_q6(PFGemmParams P) {
+  // Workgroup L runs on XCD L % 8 (the dispatcher's round robin).  The
+  // (row tile, token tile) pairs, row-tile major, are dealt to the XCDs in
+  // contiguous runs of per_xcd = ceil(pairs / 8), so the token tiles of a
+  // row tile share one L2 for its weights (each weight byte comes into about
+  // one L2 instead of eight); workgroups past the pairs exit.
+  const int n_tt = P.m_pad / 32;
+  const int pairs = P.n_row_tiles * n_tt, per_xcd = (pairs + 7) >> 3;
+  const int q = ((int)blockIdx.x & 7) * per_xcd + ((int)blockIdx.x >> 3);
+  if (q >= pairs) return;
+  const int rtile = q / n_tt;
+  int ji = 0;
+#pragma unroll
+  for (int j = 1; j < 3; ++j)
+    if (j < P.n_jobs && rtile >= P.jobs[j].tile_begin) ji = j;
+  const PFJob& J = P.jobs[ji];
+  const int lane = threadIdx.x, l32 = lane & 31, kg = lane >> 5;
+  const int tile = rtile - J.tile_begin;
+  const int row0 = tile * 32;
+  const int t0 = (q - rtile * n_tt) * 32;
+  const int wrow = min(row0 + l32, J.rows - 1);
+  const int nb = P.nb;
+  const int8_t* qa = P.in.qT + (size_t)(t0 + l32) * 32 + 16 * kg;  // + chunk * PF_MAX * 32
+  const uint4* wb = J.w6 + (size_t)tile * nb * (PF_Q6_TILE_BYTES / 16) + lane;
+
+  float acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+
+  // one super-block's MFMA operands and the row's d (the tokens' scales,
+  // used after the MFMAs, load when the super-block runs)
+  struct Ops {
+    i32x4_t a[8], bh[8], bl[8];
+    uint32_t d16;
+  };
+  auto load_ops = [&](int b, Ops& o) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      o.a[c] = *reinterpret_cast<const i32x4_t*>(qa + ((size_t)b * 8 + c) * PF_MAX * 32);
+      o.bh[c] = __builtin_bit_cast(i32x4_t, wb[((size_t)b * 16 + 2 * c) * 64]);
+      o.bl[c] = __builtin_bit_cast(i32x4_t, wb[((size_t)b * 16 + 2 * c + 1) * 64]);
+    }
+    o.d16 = J.w.d[(size_t)wrow * nb + b];
+  };
+  // the 16 tokens' scales of super-block b (vector loads retire in order:
+  // issued before the next super-block's operands, they do not wait for them)
+  auto load_q8d = [&](int b, float4 (&q8d)[4]) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      q8d[g] = *reinterpret_cast<const float4*>(P.in.dT + (size_t)b * PF_MAX + t0 + 8 * g + 4 * kg);
+  };
+  auto run = [&](const Ops& cur, const float4 (&q8d)[4]) {
+    i32x16_t dh = {}, dl = {};
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      dh = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[c], cur.bh[c], dh, 0, 0, 0);
+      dl = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[c], cur.bl[c], dl, 0, 0, 0);
+    }
+    const float dW = fp16_simd_nb(cur.d16);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float4& qd = q8d[i >> 2];
+      const float qs = (i & 3) == 0 ? qd.x : (i & 3) == 1 ? qd.y : (i & 3) == 2 ? qd.z : qd.w;
+      acc[i] = acc[i] + (float)(dh[i] * 64 + dl[i]) * (dW * qs);
+    }
+  };
+  // two operand sets in turn: the loads of the next super-block go out
+  // (pinned ahead of the MFMAs) before each one runs; whole trips of two
+  // unconditional steps, the odd last super-block peeled (a load on one
+  // side of a branch would make the waits drain)
+  Ops o0, o1;
+  load_ops(0, o0);
+  int b = 0;
+  float4 qd[4];
+  for (; b + 1 < nb; b += 2) {
+    load_q8d(b, qd);
+    load_ops(b + 1, o1);
+    issue_fence();
+    run(o0, qd);
+    load_q8d(b + 1, qd);
+    load_ops(min(b + 2, nb - 1), o0);
+    issue_fence();
+    run(o1, qd);
+  }
+  if (b < nb) {
+    load_q8d(b, qd);
+    run(o0, qd);
+  }
+
+  const int r = row0 + l32;
+  if (r < J.rows) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int t = t0 + 8 * (i >> 2) + 4 * kg + (i & 3);
+      if (t < P.m) {
+        float* y = J.y + (size_t)t * J.ldy + r;
+        if (MODE == MODE_RESID)
+          *y = *y + acc[i];
+        else
+          *y = J.bias ? acc[i] + J.bias[r] : acc[i];
+      }
+    }
+  }
+}
+template __global__ void k_pf_gemm_q6<MODE_BIAS>(PFGemmParams);
+template __global__ void k_pf_gemm_q6<MODE_RESID>(PFGemmParams);
 
 // h = SwiGLU(gate, up) elementwise (c2_tensor_swiglu_gen.go; the tail of
 // n % 8 elements per row takes the scalar f64 path).
@@ -3069,8 +3171,6 @@ template __global__ void k_pf_quant<12>(PFQuantParams);
 template __global__ void k_pf_quant<19>(PFQuantParams);
 template __global__ void k_pf_gemm<T_Q4_K, MODE_BIAS>(PFGemmParams);
 template __global__ void k_pf_gemm<T_Q4_K, MODE_RESID>(PFGemmParams);
-template __global__ void k_pf_gemm<T_Q6_K, MODE_BIAS>(PFGemmParams);
-template __global__ void k_pf_gemm<T_Q6_K, MODE_RESID>(PFGemmParams);
 
 // ------------------------------------------------------------------ vocab
 
