@@ -355,6 +355,9 @@ GemvKernel gemv_row_kernel(int nb, int pro, int mode) {
       case 19: return k_gemv_row<19, PRO_QUANT, MODE_RESID>;
       case 8: return k_gemv_row<8, PRO_QUANT, MODE_RESID>;
       case 24: return k_gemv_row<24, PRO_QUANT, MODE_RESID>;
+      case 6: return k_gemv_row<6, PRO_QUANT, MODE_RESID>;
+      case 35: return k_gemv_row<35, PRO_QUANT, MODE_RESID>;
+      case 43: return k_gemv_row<43, PRO_QUANT, MODE_RESID>;
       default: return nullptr;
     }
   }
@@ -363,6 +366,7 @@ GemvKernel gemv_row_kernel(int nb, int pro, int mode) {
       case 3: return k_gemv_row<3, PRO_NORM, MODE_SWIGLU>;
       case 4: return k_gemv_row<4, PRO_NORM, MODE_SWIGLU>;
       case 8: return k_gemv_row<8, PRO_NORM, MODE_SWIGLU>;
+      case 6: return k_gemv_row<6, PRO_NORM, MODE_SWIGLU>;
       default: return nullptr;
     }
   }
@@ -375,6 +379,11 @@ GemvKernel gemv_row_kernel(int nb, int pro, int mode) {
     if (pro == PRO_NORM) return k_gemv_row<4, PRO_NORM, MODE_BIAS>;
     if (pro == PRO_EMBED_NORM) return k_gemv_row<4, PRO_EMBED_NORM, MODE_BIAS>;
     if (pro == PRO_ARGMAX_EMBED_NORM) return k_gemv_row<4, PRO_ARGMAX_EMBED_NORM, MODE_BIAS>;
+  }
+  if (mode == MODE_BIAS && nb == 6) {
+    if (pro == PRO_NORM) return k_gemv_row<6, PRO_NORM, MODE_BIAS>;
+    if (pro == PRO_EMBED_NORM) return k_gemv_row<6, PRO_EMBED_NORM, MODE_BIAS>;
+    if (pro == PRO_ARGMAX_EMBED_NORM) return k_gemv_row<6, PRO_ARGMAX_EMBED_NORM, MODE_BIAS>;
   }
   if (mode == MODE_BIAS && nb == 8) {
     if (pro == PRO_NORM) return k_gemv_row<8, PRO_NORM, MODE_BIAS>;
@@ -454,6 +463,7 @@ VocabKernel vocab_kernel(int nb8) {
     case 30: return k_vocab<30>;
     case 31: return k_vocab<31>;
     case 32: return k_vocab<32>;
+    case 48: return k_vocab<48>;
     case 64: return k_vocab<64>;
     default: return nullptr;
   }
@@ -470,7 +480,7 @@ size_t vocab_lds(int64_t cols) { return (size_t)nq_of((int)cols) * 4 * 32 * size
 int vocab_grid(c2h_ctx* c, int64_t rows, int64_t cols, int* grid) {
   VocabKernel k = vocab_kernel(nb8_of(cols));
   if (!k)
-    return fail(c, C2H_ERR_UNSUPPORTED, "Q8_0 vocab rows of %lld columns (this build: %d..%d and 2048)",
+    return fail(c, C2H_ERR_UNSUPPORTED, "Q8_0 vocab rows of %lld columns (this build: %d..%d, 1536 and 2048)",
                 (long long)cols, 32 * VOCAB_MIN_NB8, 32 * VOCAB_MAX_NB8);
   int per_cu = 0, n_cu = 0;
   HIPCHK(c, hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, 256, vocab_lds(cols)));
@@ -1000,8 +1010,8 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
       !gemv_row_kernel(nb_k(D.n_embd), PRO_NORM, MODE_SWIGLU) ||
       !gemv_row_kernel(nb_k(D.n_ff), PRO_QUANT, MODE_RESID))
     return bail(fail(c, C2H_ERR_UNSUPPORTED,
-                     "no kernel instance for n_embd %d / n_ff %d (built: n_embd/256 in {3,4,8}, n_ff/256 in "
-                     "{3,4,12,19,24})",
+                     "no kernel instance for n_embd %d / n_ff %d (built: n_embd/256 in {3,4,6,8}, n_ff/256 in "
+                     "{3,4,6,8,12,19,24,35,43})",
                      D.n_embd, D.n_ff));
   c->desc = D;
   c->has_model = true;

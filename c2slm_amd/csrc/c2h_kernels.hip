@@ -1101,8 +1101,15 @@ C2H_GEMV_ROW(3, PRO_QUANT, MODE_RESID)
 C2H_GEMV_ROW(4, PRO_QUANT, MODE_RESID)
 C2H_GEMV_ROW(12, PRO_QUANT, MODE_RESID)
 C2H_GEMV_ROW(19, PRO_QUANT, MODE_RESID)
-C2H_GEMV_ROW(8, PRO_QUANT, MODE_RESID)   // Qwen3-1.7B: attn_out (2048 columns)
+C2H_GEMV_ROW(8, PRO_QUANT, MODE_RESID)   // Qwen3-1.7B, Qwen2.5-3B: attn_out (2048 columns)
 C2H_GEMV_ROW(24, PRO_QUANT, MODE_RESID)  // Qwen3-1.7B: ffn_down (6144 columns)
+C2H_GEMV_ROW(6, PRO_QUANT, MODE_RESID)   // Qwen2.5-1.5B: attn_out (1536 columns)
+C2H_GEMV_ROW(35, PRO_QUANT, MODE_RESID)  // Qwen2.5-1.5B: ffn_down (8960 columns)
+C2H_GEMV_ROW(43, PRO_QUANT, MODE_RESID)  // Qwen2.5-3B: ffn_down (11008 columns)
+C2H_GEMV_ROW(6, PRO_NORM, MODE_SWIGLU)
+C2H_GEMV_ROW(6, PRO_NORM, MODE_BIAS)
+C2H_GEMV_ROW(6, PRO_EMBED_NORM, MODE_BIAS)
+C2H_GEMV_ROW(6, PRO_ARGMAX_EMBED_NORM, MODE_BIAS)
 C2H_GEMV_ROW(3, PRO_NORM, MODE_SWIGLU)
 C2H_GEMV_ROW(4, PRO_NORM, MODE_SWIGLU)
 C2H_GEMV_ROW(8, PRO_NORM, MODE_SWIGLU)
@@ -3371,6 +3378,7 @@ C2H_VOCAB(28)
 C2H_VOCAB(29)
 C2H_VOCAB(30)
 C2H_VOCAB(31)
+C2H_VOCAB(48)  // n_embd 1536 (Qwen2.5-1.5B)
 C2H_VOCAB(32)
 C2H_VOCAB(64)  // Qwen3-1.7B: 2048 columns
 #undef C2H_VOCAB

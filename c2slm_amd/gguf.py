@@ -319,6 +319,13 @@ QWEN05B = ModelShape()
 # Q4_K_M mix of the other shapes.
 QWEN3_1_7B = ModelShape(n_layers=28, n_embd=2048, n_heads=16, n_kv_heads=8, n_ff=6144, arch="qwen3")
 
+# Qwen2.5-1.5B and Qwen2.5-3B dimensions (hidden 1536 / 2048, 12 / 16 query
+# heads and 2 KV heads of 128, FFN 8960 / 11008, q/k/v biases, tied
+# embedding), read by LoadModel's qwen2.* keys like the 0.5B
+# (engine/model.go:64-145; head_dim = n_embd / n_heads), in the Q4_K_M mix.
+QWEN25_1_5B = ModelShape(n_layers=28, n_embd=1536, n_heads=12, n_kv_heads=2, n_ff=8960)
+QWEN25_3B = ModelShape(n_layers=36, n_embd=2048, n_heads=16, n_kv_heads=2, n_ff=11008)
+
 # The published Qwen2.5-0.5B-Instruct Q4_K_M file's format mix: 896-column
 # matrices cannot hold K-quant super-blocks whole, so q/k/o/gate/up are Q5_0
 # and attn_v is Q8_0; ffn_down (4864 columns) stays a K-quant

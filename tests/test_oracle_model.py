@@ -55,6 +55,9 @@ SHAPES = {
     # Qwen3: head_dim 128, per-head QK-norm before RoPE, no biases
     "qwen3_hd128": G.ModelShape(n_layers=2, n_embd=512, n_heads=4, n_kv_heads=2, n_ff=768, n_vocab=V,
                                 arch="qwen3"),
+    # Qwen2.5-1.5B / 3B layout: head_dim 128 with q/k/v biases and no
+    # QK-norm, 6 query heads per KV head (smaller widths, same structure)
+    "qwen25_hd128": G.ModelShape(n_layers=2, n_embd=768, n_heads=6, n_kv_heads=1, n_ff=1024, n_vocab=V),
 }
 CASES = sorted(SHAPES) + ["bench_draw"]
 
