@@ -14,7 +14,8 @@ roofline of ffn_in, the layer kernel that moves the most bytes (RMSNorm +
 Q8_K + gate/up Q4_K GEMV + SwiGLU; eager launches back to back over the 24
 layers' weights, paced by the GPU, between one pair of HIP events: the
 per-dispatch time a kernel trace of `bench.py --only roofline` records);
-and the CPU baseline (the oracle on this host's cores, same workload).
+and the CPU baseline (the reference's CPU path restated in C with its AVX2
+kernels, on this host's cores, same workload; the scalar port beside it).
 `extra` adds, outside the timed region: every decode kernel's time, bytes
 and GB/s and the step's bytes and GB/s; the vocab kernel from HBM; the
 operator microbench of the layer shapes (Q4_K/Q6_K x Q8_K GEMV and the Q8_K
@@ -77,16 +78,19 @@ def cpu_threads() -> int:
 
 
 def cpu_baseline(gf, prompt, steps, im_end, eos, runs: int = 5, single_steps: int = 16):
-    """The oracle (plain-C restatement of the reference's CPU path; scalar
-    integer dots, not the reference's VPMADDUBSW/VPMADDWD kernels) on this
-    host: after an untimed prompt ingest, `steps` greedy steps timed, the
-    median of `runs` runs with the reference's pool size, plus one run of
-    `single_steps` steps on one thread."""
+    """The reference's CPU path on this host, as its C restatement with the
+    reference's AVX2 kernels (oracle/c2slm_avx2.c: VPMADDUBSW / VPMADDWD
+    Q4_K and Q6_K dots, the 8-lane float Q8_0 dot; the rest of the oracle's
+    C), the reference's pool size (nw = min(32, cores granted) workers, rows
+    split per worker, inline below 256 rows): after an untimed prompt ingest,
+    `steps` greedy steps timed, the median of `runs` runs; beside it the
+    scalar port (the oracle's scalar integer dots) on the same pool, and the
+    AVX2 path on one thread for `single_steps` steps."""
     from oracle import oracle as O
     threads = cpu_threads()
 
-    def rate(nt, n):
-        orc = O.OracleEngine(gf, max_ctx=512, n_threads=nt)
+    def rate(nt, n, avx2):
+        orc = O.OracleEngine(gf, max_ctx=512, n_threads=nt, avx2_dots=avx2)
         orc.ingest_from(0, prompt)
         t0 = time.perf_counter()
         toks = orc.generate(n, -1, -1, PENALTY)  # run exactly n steps
@@ -94,13 +98,16 @@ def cpu_baseline(gf, prompt, steps, im_end, eos, runs: int = 5, single_steps: in
         orc.close()
         return len(toks) / dt, dt
 
-    rs = [rate(threads, steps) for _ in range(runs)]
+    rs = [rate(threads, steps, True) for _ in range(runs)]
     med = float(np.median([r for r, _ in rs]))
-    one, one_dt = rate(1, single_steps)
+    scalar, scalar_dt = rate(threads, steps, False)
+    one, one_dt = rate(1, single_steps, True)
     return {"value": round(med, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"oracle/c2slm_oracle.c, plain C with scalar integer dots (OpenMP, {threads} threads = "
-                      f"min(32, cores granted)): {PROMPT_LEN}-token prompt ingest untimed, then {steps} greedy "
-                      f"steps timed, median of {runs} runs ({sum(d for _, d in rs):.1f} s)",
+            "implementation": "C restatement of the reference's AVX2 path (oracle/c2slm_avx2.c + oracle/c2slm_oracle.c)",
+            "sample": f"{PROMPT_LEN}-token prompt ingest untimed, then {steps} greedy steps timed, median of {runs} "
+                      f"runs ({sum(d for _, d in rs):.1f} s), {threads} OpenMP threads = min(32, cores granted)",
+            "scalar_port_tok_s": round(scalar, 3),
+            "scalar_port_sample": f"the same workload with the oracle's scalar integer dots, one run ({scalar_dt:.1f} s)",
             "single_thread_tok_s": round(one, 3), "single_thread_sample": f"{single_steps} steps ({one_dt:.1f} s)",
             "nproc": os.cpu_count(), "cpu_model": cpu_model(), "runs_tok_s": [round(r, 3) for r, _ in rs]}
 

@@ -644,7 +644,16 @@ typedef struct {
   const float* output_norm;
   const orc_layer* layers;
   int32_t n_threads;
+  /* 1: the GEMVs run the reference's AVX2 kernels as restated in
+   * c2slm_avx2.c (the CPU baseline); 0: the scalar restatement.  The results
+   * are identical. */
+  int32_t simd_avx2;
 } orc_model;
+
+float orc_avx2_dot_q4k_q8k(const uint8_t* w, const uint8_t* q8k, int cols);
+float orc_avx2_dot_q6k_q8k(const uint8_t* w, const uint8_t* q8k, int cols);
+int32_t orc_avx2_q6k_block_isum(const uint8_t* wb, const uint8_t* qb);
+float orc_avx2_dot_q8_0(const uint8_t* w, const float* x, int cols);
 
 typedef struct {
   orc_model m;
@@ -721,23 +730,29 @@ static void dispatch_gemv(orc_state* s, float* y, const uint8_t* w, int type, co
   }
   int nw = (rows < 256) ? 1 : n_workers(s);
   const uint8_t* q8k = s->q8k;
+  const int avx2 = s->m.simd_avx2;
+  float (*dot_q8k)(const uint8_t*, const uint8_t*, int);
   long rb;
   switch (type) {
     case T_Q4_K:
       rb = (long)(cols / QK_K) * BS_Q4K;
+      dot_q8k = avx2 ? orc_avx2_dot_q4k_q8k : orc_dot_q4k_q8k;
 #pragma omp parallel for num_threads(nw) schedule(static)
-      for (int r = 0; r < rows; ++r) y[r] = orc_dot_q4k_q8k(w + r * rb, q8k, cols);
+      for (int r = 0; r < rows; ++r) y[r] = dot_q8k(w + r * rb, q8k, cols);
       break;
     case T_Q6_K:
       rb = (long)(cols / QK_K) * BS_Q6K;
+      dot_q8k = avx2 ? orc_avx2_dot_q6k_q8k : orc_dot_q6k_q8k;
 #pragma omp parallel for num_threads(nw) schedule(static)
-      for (int r = 0; r < rows; ++r) y[r] = orc_dot_q6k_q8k(w + r * rb, q8k, cols);
+      for (int r = 0; r < rows; ++r) y[r] = dot_q8k(w + r * rb, q8k, cols);
       break;
-    case T_Q8_0:
+    case T_Q8_0: {
+      float (*dot_x)(const uint8_t*, const float*, int) = avx2 ? orc_avx2_dot_q8_0 : orc_dot_q8_0;
       rb = (long)(cols / QK8_0) * BS_Q8_0;
 #pragma omp parallel for num_threads(nw) schedule(static)
-      for (int r = 0; r < rows; ++r) y[r] = orc_dot_q8_0(w + r * rb, x, cols);
+      for (int r = 0; r < rows; ++r) y[r] = dot_x(w + r * rb, x, cols);
       break;
+    }
     case T_Q5_0:
       rb = (long)(cols / QK5_0) * BS_Q5_0;
 #pragma omp parallel for num_threads(nw) schedule(static)

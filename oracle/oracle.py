@@ -32,7 +32,7 @@ class OrcModel(C.Structure):
                                          "n_vocab", "max_ctx")] + \
                [("eps", C.c_float), ("theta", C.c_float), ("token_embd", U8P), ("embd_type", C.c_int32),
                 ("output", U8P), ("output_type", C.c_int32), ("output_norm", F32P),
-                ("layers", C.POINTER(OrcLayer)), ("n_threads", C.c_int32)]
+                ("layers", C.POINTER(OrcLayer)), ("n_threads", C.c_int32), ("simd_avx2", C.c_int32)]
 
 
 def build():
@@ -60,6 +60,10 @@ def lib(path: str | None = None):
             "orc_dot_q4k_q8k": (C.c_float, [U8P, U8P, C.c_int]),
             "orc_dot_q6k_q8k": (C.c_float, [U8P, U8P, C.c_int]),
             "orc_dot_q8_0": (C.c_float, [U8P, F32P, C.c_int]),
+            "orc_avx2_dot_q4k_q8k": (C.c_float, [U8P, U8P, C.c_int]),
+            "orc_avx2_dot_q6k_q8k": (C.c_float, [U8P, U8P, C.c_int]),
+            "orc_avx2_q6k_block_isum": (C.c_int32, [U8P, U8P]),
+            "orc_avx2_dot_q8_0": (C.c_float, [U8P, F32P, C.c_int]),
             "orc_dot_q5_0": (C.c_float, [U8P, F32P, C.c_int]),
             "orc_dot_q4k_f32": (C.c_float, [U8P, F32P, C.c_int]),
             "orc_dot_q6k_f32": (C.c_float, [U8P, F32P, C.c_int]),
@@ -154,7 +158,11 @@ class OracleEngine:
     """The reference's Engine state (model + KV cache + arena) over a GGUF file,
     computed by the oracle on the host CPU."""
 
-    def __init__(self, gf, max_ctx: int = 1024, n_threads: int = 1, lib_path: str | None = None):
+    def __init__(self, gf, max_ctx: int = 1024, n_threads: int = 1, lib_path: str | None = None,
+                 avx2_dots: bool = False):
+        """avx2_dots: the GEMVs run the reference's AVX2 kernels as restated
+        in oracle/c2slm_avx2.c (the CPU baseline) instead of the scalar
+        restatement; the results are identical."""
         from c2slm_amd import gguf as G
         self._L = lib(lib_path)
         self.gf = gf
@@ -215,6 +223,7 @@ class OracleEngine:
         m.output_norm = fp(tm["output_norm.weight"])
         m.layers = layers
         m.n_threads = n_threads
+        m.simd_avx2 = 1 if avx2_dots else 0
         self.model = m
         self.n_embd, self.n_vocab, self.max_ctx = E, V, max_ctx
         self.n_layers, self.n_kv_heads, self.head_dim = L, KVH, E // H

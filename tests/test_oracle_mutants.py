@@ -15,6 +15,7 @@ from tests import test_oracle_model as T
 from tests.qwen2_f64 import Qwen2F64, write_pin_model
 
 SRC = os.path.join(os.path.dirname(O.__file__), "c2slm_oracle.c")
+AVX2_SRC = os.path.join(os.path.dirname(O.__file__), "c2slm_avx2.c")  # linked unchanged
 CFLAGS = ["-O1", "-fPIC", "-std=c11", "-ffp-contract=off", "-fno-fast-math", "-mavx2", "-mfma", "-fopenmp",
           "-shared"]
 
@@ -58,7 +59,7 @@ def build_variant(tmp, name, old, new):
     d.mkdir()
     (d / "o.c").write_text(text)
     so = str(d / "liboracle_variant.so")
-    subprocess.run(["gcc", *CFLAGS, "-o", so, str(d / "o.c"), "-lm"], check=True)
+    subprocess.run(["gcc", *CFLAGS, "-o", so, str(d / "o.c"), AVX2_SRC, "-lm"], check=True)
     return so
 
 

@@ -17,6 +17,7 @@ from oracle import oracle as O
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 SRC = os.path.join(os.path.dirname(O.__file__), "c2slm_oracle.c")
+AVX2_SRC = os.path.join(os.path.dirname(O.__file__), "c2slm_avx2.c")  # the CPU baseline's kernels, linked too
 CFLAGS = ["-O1", "-g", "-fPIC", "-std=c11", "-ffp-contract=off", "-fno-fast-math", "-mavx2", "-mfma", "-fopenmp",
           "-fsanitize=address,undefined", "-fno-omit-frame-pointer", "-fno-sanitize-recover=undefined", "-shared"]
 
@@ -32,7 +33,7 @@ def build(tmp, text: str) -> str:
     src = tmp / "o.c"
     src.write_text(text)
     so = str(tmp / "liboracle_san.so")
-    subprocess.run(["gcc", *CFLAGS, "-o", so, str(src), "-lm"], check=True)
+    subprocess.run(["gcc", *CFLAGS, "-o", so, str(src), AVX2_SRC, "-lm"], check=True)
     return so
 
 
