@@ -596,7 +596,18 @@ def main():
     step_bytes = sum(v["bytes"] * v["launches_per_step"] for k, v in kern.items() if k != "attn")
     step_bytes += desc.n_layers * kernel_bytes(gf, desc, t_avg)["attn"]
 
-    pipelined_ms = ctx.time_steps(pos, args.pipelined_iters, PENALTY, im_end, eos)
+    # device-fed steps at the host loop's positions, from the same state: the
+    # prompt forwarded again and the same warm-up steps on the host, then
+    # c2h_time_steps over the timed loop's positions
+    ctx.set_token_ids(0, prompt)
+    for p, t in enumerate(prompt):
+        ctx.forward(int(t), p, want_normx=False)
+    for p in range(PROMPT_LEN, PROMPT_LEN + args.warmup):
+        ctx.step(p, PENALTY, im_end, eos)
+    ctx.sync()
+    pipelined_ms = ctx.time_steps(PROMPT_LEN + args.warmup, args.steps, PENALTY, im_end, eos)
+    # and past them (positions pos .. pos + pipelined_iters - 1)
+    pipelined_next_ms = ctx.time_steps(pos, args.pipelined_iters, PENALTY, im_end, eos)
     # In-step timing: a forward pass between launches streams the layer
     # weights, so the vocab rows come from HBM as they do inside a step.
     # Roofline timing: launches back to back alternating between the matrix
@@ -684,6 +695,9 @@ def main():
                   "launch_floor_us_by_grid": floor_by_grid,
                   "pipelined_ms_per_step": round(pipelined_ms, 4),
                   "pipelined_tok_s": round(1000.0 / pipelined_ms, 1),
+                  "pipelined_positions": [PROMPT_LEN + args.warmup, pos - 1],
+                  "pipelined_next_tok_s": round(1000.0 / pipelined_next_ms, 1),
+                  "pipelined_next_positions": [pos, pos + args.pipelined_iters - 1],
                   "prefill_512": prefill,
                   "long_context_decode": longctx,
                   "real_formats": realf,
