@@ -192,10 +192,10 @@ __host__ __device__ inline int attn_tier(int T) {
 constexpr int ATT_SPLIT_T = 1024;  // default split length (positions attended)
 constexpr int ATT_SB = 256;        // positions per k_attn_scores workgroup
 constexpr int ATT_AV_CH = 256;     // positions per k_attn_av LDS chunk
-constexpr int ATT_AV_THREADS = 512;  // k_attn_av: two chain waves, six staging waves
-constexpr int ATT_AV_DSL = 16;       // k_attn_av: dims of a head per workgroup
+constexpr int ATT_AV_THREADS = 256;  // k_attn_av: one chain wave, three staging waves
+constexpr int ATT_AV_DSL = 8;        // k_attn_av: dims of a head per workgroup
 constexpr int ATT_AV_SLICES = 64 / ATT_AV_DSL;
-constexpr int ATT_AV_ITEMS = 4;      // 16-byte staging items per staging lane and chunk
+constexpr int ATT_AV_ITEMS = 6;      // 16-byte staging items per staging lane and chunk
 constexpr int ATT_MAX_QPKV = 8;    // query heads per KV head the long form handles
 constexpr int ATT_LONG_MAX_CTX = 36864;  // exps of one head in LDS (k_attn_softmax)
 // grid (n_heads, tokens) for k_attn_core / k_attn_softmax / k_attn_av and
@@ -265,7 +265,10 @@ __host__ __device__ inline int attn_lds_floats(int max_ctx) { return attn_kv_lds
 // Dynamic LDS of k_attn_softmax (exps of up to max_ctx positions) and of
 // k_attn_av (two chunks of V quads and probabilities), in floats.
 __host__ __device__ inline int attn_softmax_lds_floats(int max_ctx) { return (max_ctx + 3) & ~3; }
-constexpr int ATT_AV_LDS_FLOATS = 2 * ATT_AV_CH * ATT_AV_DSL + 2 * ATT_MAX_QPKV * ATT_AV_CH;
+// probability rows of k_attn_av padded by 4 floats: the query heads' rows
+// start in different LDS banks
+constexpr int ATT_AV_PLD = ATT_AV_CH + 4;
+constexpr int ATT_AV_LDS_FLOATS = 2 * ATT_AV_CH * ATT_AV_DSL + 2 * ATT_MAX_QPKV * ATT_AV_PLD;
 
 // ---- batched prefill (a prompt of up to PF_MAX tokens per pass)
 

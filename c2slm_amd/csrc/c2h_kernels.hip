@@ -2296,13 +2296,20 @@ __global__ void __launch_bounds__(1024) k_attn_softmax(AttnCoreParams P) {
 // 0 chains through the current one.
 // The AV chains of long contexts (c2_tensor_attn_gen.go:85-117: per query
 // head and dim, out[d] = fma(p, V[p][d], out[d]) for p = 0..pos in order).
-// A workgroup takes one KV head and a 16-dim slice of it for all the KV
-// head's query heads: two chain waves, lane = (query head j, dim), and six
-// staging waves that bring each 256-position chunk of the V slice (16 KB)
+// A workgroup takes one KV head and an 8-dim slice of it for all the KV
+// head's query heads: one chain wave, lane = (query head j, dim), and three
+// staging waves that bring each 256-position chunk of the V slice (8 KB)
 // and the heads' probabilities into LDS, three chunks of loads in flight.
-// Slicing the dims keeps the V stream per CU at a quarter of a head's rows,
-// so the staging stays ahead of the chains; the V slice is read once for
-// all query heads of the group.
+// The chain wave reads a 16-byte V quad and a 16-byte probability quad per
+// lane and four positions: with one chain wave per CU those reads take
+// about four clocks per position of the CU's LDS bandwidth, under the
+// six-clock dependent FMA (two chain waves of 16-dim slices per CU needed
+// about eight and ran at ~12); the V slice is read once for all query
+// heads of the group.  Measured at 32,768 positions: 146 us per layer
+// (10.7 clocks per position at 2.4 GHz; the chain loop alone, one wave on
+// LDS-resident data, runs at 7.6).  Not faster: 1,024-position chunks with
+// seven staging waves (151 us), the chain wave at a raised issue priority
+// (148 us); the probability rows' padding did not change it.
 struct AvStage {
   f32x4_t r[ATT_AV_ITEMS];
 };
@@ -2313,11 +2320,11 @@ __global__ void __launch_bounds__(ATT_AV_THREADS) k_attn_av(AttnCoreParams P) {
   constexpr int NQ = ATT_AV_CH / 4;                    // quads per chunk
   constexpr int NV = NQ * DS;                          // V items (16 B) per chunk
   constexpr int NP = ATT_MAX_QPKV * (ATT_AV_CH / 4);   // probability items per chunk
-  constexpr int NS = ATT_AV_THREADS - 128;             // staging lanes
+  constexpr int NS = ATT_AV_THREADS - 64;              // staging lanes
   static_assert(ATT_AV_ITEMS * NS >= NV + NP, "staging covers a chunk");
   extern __shared__ __align__(16) unsigned char smem[];
   f32x4_t* vb = reinterpret_cast<f32x4_t*>(smem);      // [2][NQ][DS]: quad q of dim dd
-  float* pb = reinterpret_cast<float*>(vb + 2 * NV);   // [2][ATT_MAX_QPKV][ATT_AV_CH]
+  float* pb = reinterpret_cast<float*>(vb + 2 * NV);   // [2][ATT_MAX_QPKV][ATT_AV_PLD]
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int qpkv = P.n_heads / P.n_kv_heads;
@@ -2332,7 +2339,7 @@ __global__ void __launch_bounds__(ATT_AV_THREADS) k_attn_av(AttnCoreParams P) {
   const int nch = (T + ATT_AV_CH - 1) / ATT_AV_CH;
   const int qlast = pos >> 2;
   const int plast4 = (T - 1) & ~3;  // a float4 starting there stays inside the row
-  const int sidx = tid - 128;       // staging lane
+  const int sidx = tid - 64;        // staging lane
   // item it of a chunk: V (quad it/DS, dim it%DS) for it < NV, then the
   // probabilities of head (it-NV)/(ATT_AV_CH/4), float4 (it-NV)%(ATT_AV_CH/4)
   auto load_set = [&](AvStage& st, int c) {
@@ -2356,14 +2363,16 @@ __global__ void __launch_bounds__(ATT_AV_THREADS) k_attn_av(AttnCoreParams P) {
       const int it = sidx + NS * k;
       if (it < NV)
         vb[(c & 1) * NV + it] = st.r[k];
-      else if (it < NV + NP)
-        reinterpret_cast<f32x4_t*>(pb + (c & 1) * ATT_MAX_QPKV * ATT_AV_CH)[it - NV] = st.r[k];
+      else if (it < NV + NP) {
+        const int e = it - NV, j = e / (ATT_AV_CH / 4), f = e % (ATT_AV_CH / 4);
+        *reinterpret_cast<f32x4_t*>(pb + ((c & 1) * ATT_MAX_QPKV + j) * ATT_AV_PLD + 4 * f) = st.r[k];
+      }
     }
   };
-  // Waves 0-1 chain; waves 2.. stage.  The two roles run separate loops with
+  // Wave 0 chains; waves 1.. stage.  The two roles run separate loops with
   // the same number of barriers (one per chunk, plus the first), and the
   // staging loop issues its loads unconditionally (chunk indices clamped).
-  if (wave >= 2) {
+  if (wave >= 1) {
     AvStage a, b, d;
     load_set(a, 0);
     load_set(b, min(1, nch - 1));
@@ -2401,7 +2410,7 @@ __global__ void __launch_bounds__(ATT_AV_THREADS) k_attn_av(AttnCoreParams P) {
     __syncthreads();
     for (int c = 0; c < nch; ++c) {
       const int np = min(ATT_AV_CH, T - c * ATT_AV_CH);
-      acc = av_chain_q3<DS>(pb + ((c & 1) * ATT_MAX_QPKV + jc) * ATT_AV_CH, vb + (c & 1) * NV, np, dd, acc);
+      acc = av_chain_q3<DS>(pb + ((c & 1) * ATT_MAX_QPKV + jc) * ATT_AV_PLD, vb + (c & 1) * NV, np, dd, acc);
       __syncthreads();
     }
     if (j < qpkv) P.out[(size_t)ti * P.out_ld + (size_t)(g * qpkv + j) * HD + sl * DS + dd] = acc;
