@@ -1413,10 +1413,10 @@ int pf_pass(c2h_ctx* c, const int32_t* tokens, int m, int pos0) {
       A.out_ld = E;
       A.store_kv = 0;
       if (pos0 + m <= c->att_split && pos0 + m <= c->pfa_max_pos) {
-        // blocks of 16 query tokens per head, K/V chunks shared by the block
+        // blocks of PFA_TB query tokens per head, longest first, K/V chunks shared by the block
         A.n_tok = m;
         A.sc_ld = pfa_sc_ld(pos0 + m - 1);
-        hipLaunchKernelGGL(k_pf_attn, dim3(D.n_heads, (m + PFA_TB - 1) / PFA_TB), dim3(256),
+        hipLaunchKernelGGL(k_pf_attn, dim3(D.n_heads * ((m + PFA_TB - 1) / PFA_TB)), dim3(256),
                            (size_t)pfa_lds_floats(pos0 + m - 1) * 4, c->stream, A);
       } else if (pos0 + m <= c->att_split) {
         const size_t lds = (size_t)attn_lds_floats(pos0 + m) * 4;

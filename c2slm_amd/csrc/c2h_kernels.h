@@ -242,7 +242,8 @@ constexpr int ATT_XCDS = 8;
 // Causal attention of a prefill pass (k_pf_attn): one workgroup per query
 // head and block of PFA_TB query tokens, K and V staged through LDS in
 // chunks of PFA_CH positions shared by the block's tokens.
-constexpr int PFA_TB = 16;
+constexpr int PFA_TB = 8;
+constexpr int PFA_WAVES_PER_EU = 3;  // occupancy the register budget is sized for (three workgroups per CU)
 constexpr int PFA_CH = 128;
 constexpr int PFA_KPAD = 68;  // floats per staged K row (64 + 4: conflict-free row reads)
 // Row stride (floats) of the block's scores for positions up to pmax.

@@ -2645,6 +2645,48 @@ __global__ void __launch_bounds__(64) k_pf_rope_store(PFRopeParams P) {
   P.kv[(((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * head_stride + vq_index(pos, d)] = vr[d];
 }
 
+// fma(src of lane K of this lane's row of 16 lanes, v, acc) in one
+// instruction: v_fmac_f32 with the DPP operand row_newbcast:K (gfx90a and
+// later), where a broadcast LDS read and an FMA would be two.  Callers keep
+// every lane of the wave active (a disabled source lane reads as 0) and
+// take src straight from an LDS read (a VALU write of src in the two
+// instructions before would need wait states).  Volatile: never moved into
+// a branch.
+template <int K>
+__device__ __forceinline__ float fmac_row_bcast(float acc, float src, float v) {
+  asm volatile("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(src), "v"(v), "n"(K));
+  return acc;
+}
+
+// attn_score with the query broadcast from registers: lane k of each row of
+// 16 holds q[4k .. 4k+3] in qr, every lane its own K row in kk4.  The same
+// two-accumulator FMA order, sum tree and scale.
+__device__ __forceinline__ float attn_score_bc(const f32x4_t& qr, const float4 (&kk4)[16], float scale) {
+  float a0[8], a1[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l) {
+    a0[l] = 0.0f;
+    a1[l] = 0.0f;
+  }
+  static_for<4>([&](auto dd) {
+    constexpr int d = 16 * (int)dd;
+    const float kk[16] = {kk4[d / 4].x,     kk4[d / 4].y,     kk4[d / 4].z,     kk4[d / 4].w,
+                          kk4[d / 4 + 1].x, kk4[d / 4 + 1].y, kk4[d / 4 + 1].z, kk4[d / 4 + 1].w,
+                          kk4[d / 4 + 2].x, kk4[d / 4 + 2].y, kk4[d / 4 + 2].z, kk4[d / 4 + 2].w,
+                          kk4[d / 4 + 3].x, kk4[d / 4 + 3].y, kk4[d / 4 + 3].z, kk4[d / 4 + 3].w};
+    static_for<8>([&](auto l) {
+      constexpr int i0 = d + (int)l, i1 = d + 8 + (int)l;
+      a0[l] = fmac_row_bcast<i0 / 4>(a0[l], qr[i0 % 4], kk[l]);
+      a1[l] = fmac_row_bcast<i1 / 4>(a1[l], qr[i1 % 4], kk[8 + l]);
+    });
+  });
+  float v[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l) v[l] = a0[l] + a1[l];
+  const float sco = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+  return sco * scale;
+}
+
 // Causal attention of a prefill pass: workgroup (query head h, block of
 // PFA_TB query tokens), token i at position pos0 + i attending positions
 // 0..pos0+i, all of whose K/V rows are in the cache.  Per (token, head) the
@@ -2658,31 +2700,44 @@ __global__ void __launch_bounds__(64) k_pf_rope_store(PFRopeParams P) {
 //     (c2_tensor_attn_gen.go:85-117).
 // Sharing: the K rows of a PFA_CH-position chunk are read from the cache
 // once per block (coalesced, into LDS rows padded to PFA_KPAD floats) and
-// serve the block's 16 tokens; likewise the V quads.  Thread roles:
-//   scores     position c0 + (t % 128) of the chunk, tokens 8*(t/128)..+7;
-//   sums       lanes 0..15 of wave 0, one token each: the sequential sum is
-//              one dependent chain per token, so the 16 chains run side by
-//              side (lanes past a token's last position add +0, exactly);
-//   AV         dim t % 64 of tokens 4*(t/64)..+3: four independent chains.
-// (LDS limits a CU to two of these workgroups: two waves per SIMD, the VGPR budget of that occupancy)
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) k_pf_attn(AttnCoreParams P) {
+// serve the block's tokens; likewise the V quads.  Thread roles (TB =
+// PFA_TB):
+//   scores     position c0 + (t % 128) of the chunk, tokens (TB/2)*(t/128)
+//              .. +TB/2, the query broadcast from registers (every lane
+//              computes, lanes past the token's last position drop theirs);
+//   sums       wave w the tokens w, w+4, ..: each the exact sequential sum
+//              spread over the wave's 64 lanes (seq_sum_wave / _n);
+//   AV         dim t % 64 of tokens (TB/4)*(t/64) .. +TB/4: independent
+//              chains, the probabilities of 64 positions at a time
+//              broadcast from registers.
+// Block order: a block's work grows with its last position, so the grid is
+// one-dimensional and runs the blocks from the last (longest) to the first;
+// the dispatcher hands each freed slot the next block, which evens out the
+// CUs' loads (the longest block sets the kernel's length).
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PFA_WAVES_PER_EU, PFA_WAVES_PER_EU))) k_pf_attn(AttnCoreParams P) {
   constexpr int HD = 64;
+  constexpr int TB = PFA_TB;
+  constexpr int TPT = TB / 2;                 // score tokens per thread
+  constexpr int TPW = TB / 4;                 // AV tokens per wave
+  static_assert(TB % 4 == 0 && TB <= 16, "roles assume 4..16 tokens per block");
   constexpr int KP = PFA_KPAD;
   constexpr int KL = PFA_CH * 16 / 256;       // 16-byte K loads per thread and chunk
   constexpr int VL = PFA_CH / 4 * 64 / 256;   // V quads per thread and chunk
   extern __shared__ __align__(16) unsigned char smem[];
   float* kbuf = reinterpret_cast<float*>(smem);        // [PFA_CH][KP]   (scores phase)
   f32x4_t* vbuf = reinterpret_cast<f32x4_t*>(smem);    // [PFA_CH/4][64] (AV phase)
-  float* q_s = kbuf + PFA_CH * KP;                     // [PFA_TB][64]
-  float* sc = q_s + PFA_TB * HD;                       // [PFA_TB][P.sc_ld]
-  __shared__ float red_m[4][8];
-  __shared__ float mx_s[PFA_TB], inv_s[PFA_TB];
+  float* q_s = kbuf + PFA_CH * KP;                     // [TB][64]
+  float* sc = q_s + TB * HD;                           // [TB][P.sc_ld]
+  __shared__ float red_m[4][TPT];
+  __shared__ float mx_s[TB], inv_s[TB];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int h = (int)blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the AV loops run with every lane on
+  const int nblk = (int)gridDim.x / P.n_heads;
+  const int h = (int)blockIdx.x % P.n_heads;
   const int g = h / (P.n_heads / P.n_kv_heads);
-  const int t0 = (int)blockIdx.y * PFA_TB;
-  const int nt = min(PFA_TB, P.n_tok - t0);  // tokens of this block
+  const int t0 = (nblk - 1 - (int)blockIdx.x / P.n_heads) * TB;
+  const int nt = min(TB, P.n_tok - t0);      // tokens of this block
   const int ld = P.sc_ld;
   const int pos0 = P.state->pos;
   const int pmax = pos0 + t0 + nt - 1;       // last position the block attends
@@ -2705,7 +2760,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
     const int i = tid + 256 * k;
     kn[k] = reinterpret_cast<const f32x4_t*>(kcache + (size_t)min(i >> 4, pmax) * HD)[i & 15];
   });
-  reinterpret_cast<float4*>(q_s)[tid] = qv;
+  if (tid < TB * 16) reinterpret_cast<float4*>(q_s)[tid] = qv;
   __syncthreads();
   {  // RoPE (pairs i, i+32) at each token's position
     const int tk = tid >> 4;
@@ -2725,9 +2780,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
 
   // ---- scores, chunk by chunk of K rows; the next chunk loads meanwhile
   const int th = tid >> 7, pl = tid & 127;
-  float lmax[8];
+  __syncthreads();  // q is turned
+  f32x4_t qr[TPT];  // lane k of each row: q[4k .. 4k+3] of token th*TPT + j
+  static_for<TPT>([&](auto j) { qr[j] = reinterpret_cast<const f32x4_t*>(q_s + (th * TPT + (int)j) * HD)[lane & 15]; });
+  float lmax[TPT];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) lmax[j] = -__builtin_inff();
+  for (int j = 0; j < TPT; ++j) lmax[j] = -__builtin_inff();
   for (int c0 = 0; c0 <= pmax; c0 += PFA_CH) {
     __syncthreads();  // the previous chunk's rows are read (and, first time, q is turned)
     static_for<KL>([&](auto k) {
@@ -2740,30 +2798,27 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
     });
     __syncthreads();
     const int p = c0 + pl;
-    if (p <= pmax) {
-      float4 kk4[16];
+    float4 kk4[16];  // rows past pmax repeat row pmax: finite, computed, dropped
 #pragma unroll
-      for (int i = 0; i < 16; ++i) kk4[i] = reinterpret_cast<const float4*>(kbuf + pl * KP)[i];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int tk = th * 8 + j;
-        if (tk < nt && p <= pos0 + t0 + tk) {
-          const float sco = attn_score(q_s + tk * HD, kk4, P.scale);
-          sc[tk * ld + p] = sco;
-          lmax[j] = (sco > lmax[j]) ? sco : lmax[j];
-        }
+    for (int i = 0; i < 16; ++i) kk4[i] = reinterpret_cast<const float4*>(kbuf + pl * KP)[i];
+    static_for<TPT>([&](auto j) {
+      const int tk = th * TPT + (int)j;
+      const float sco = attn_score_bc(qr[j], kk4, P.scale);
+      if (tk < nt && p <= pos0 + t0 + tk) {
+        sc[tk * ld + p] = sco;
+        lmax[j] = (sco > lmax[j]) ? sco : lmax[j];
       }
-    }
+    });
   }
-  // ---- max per token: waves 2th, 2th+1 hold tokens 8th..8th+7
+  // ---- max per token: waves 2th, 2th+1 hold tokens TPT*th .. +TPT
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < TPT; ++j) {
     const float m = wave_max_dpp(lmax[j]);
     if (lane == 0) red_m[wave][j] = m;
   }
   __syncthreads();
   if (tid < nt) {
-    const int w0 = 2 * (tid >> 3), j = tid & 7;
+    const int w0 = 2 * (tid / TPT), j = tid % TPT;
     float m = fmax_gt(red_m[w0][j], red_m[w0 + 1][j]);
     const float s0 = sc[tid * ld];
     if (s0 != s0) m = s0;
@@ -2781,11 +2836,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
     vn[k] = vcache[(size_t)min(i >> 6, pmax >> 2) * 64 + (i & 63)];
   });
   __syncthreads();
-  // ---- sequential sums: lane tk of wave 0 runs token tk's chain (reads 16 ahead)
-  if (tid < 64) {
-    const int tk = min(lane, nt - 1);
-    const float s = chunk_chain(sc + tk * ld, 0, pos0 + t0 + tk + 1, 0.0f);
-    if (lane < nt) inv_s[lane] = 1.0f / s;
+  // ---- sequential sums: wave w the tokens w, w+4, .. over its 64 lanes
+  for (int tk = wave; tk < nt; tk += 4) {
+    const int n = pos0 + t0 + tk + 1;
+    const float s = (n <= 64 * SPEC_C) ? seq_sum_wave(sc + tk * ld, n) : seq_sum_wave_n(sc + tk * ld, n);
+    if (lane == 0) inv_s[tk] = 1.0f / s;
   }
   __syncthreads();
   for (int tk = 0; tk < nt; ++tk) {
@@ -2793,12 +2848,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
     for (int p = tid; p <= pos0 + t0 + tk; p += 256) sc[tk * ld + p] = sc[tk * ld + p] * iv;
   }
 
-  // ---- AV: four chains per thread (dim lane, tokens 4*wave..+3), V quads by chunk
-  const float4* sc4[4];
+  // ---- AV: TPW chains per thread (dim lane, tokens TPW*wave .. +TPW), V quads by chunk
+  const float4* sc4[TPW];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) sc4[j] = reinterpret_cast<const float4*>(sc + min(wave * 4 + j, PFA_TB - 1) * ld);
-  const int last0 = pos0 + t0 + wave * 4;  // every token of the wave attends [0, last0]
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int j = 0; j < TPW; ++j) sc4[j] = reinterpret_cast<const float4*>(sc + min(wave * TPW + j, TB - 1) * ld);
+  const int last0 = pos0 + t0 + wave * TPW;  // every token of the wave attends [0, last0]
+  float acc[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) acc[j] = 0.0f;
   for (int c0 = 0; c0 <= pmax; c0 += PFA_CH) {
     __syncthreads();  // K rows (first time) / the previous V chunk are read
     static_for<VL>([&](auto k) { vbuf[tid + 256 * k] = vn[k]; });
@@ -2808,27 +2865,44 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
     });
     __syncthreads();
     const int nq = min(PFA_CH, pmax + 1 - c0 + 3) >> 2;               // quads of the chunk up to pmax
-    const int nfull = max(min((last0 + 1 - c0) >> 2, nq), 0);          // quads all four tokens use whole
+    const int nfull = max(min((last0 + 1 - c0) >> 2, nq), 0);          // quads all the wave's tokens use whole
     int qd = 0;
+    for (; qd + 16 <= nfull; qd += 16) {  // 64 positions: p of c0 + 4(qd+k) + c is component c of lane k
+      f32x4_t pq[TPW];
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) pq[j] = reinterpret_cast<const f32x4_t*>(sc4[j])[(c0 >> 2) + qd + (lane & 15)];
+      static_for<2>([&](auto hf) {  // two halves of eight quads
+        f32x4_t v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = vbuf[(qd + 8 * (int)hf + k) * 64 + lane];
+        static_for<8>([&](auto k) {
+          static_for<4>([&](auto c) {
+#pragma unroll
+            for (int j = 0; j < TPW; ++j)
+              acc[j] = fmac_row_bcast<8 * (int)hf + (int)k>(acc[j], pq[j][(int)c], v[k][(int)c]);
+          });
+        });
+      });
+    }
     for (; qd + 4 <= nfull; qd += 4) {  // sixteen positions: every read issued before the FMAs
       f32x4_t v[4];
-      float4 pr[4][4];
+      float4 pr[TPW][4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         v[k] = vbuf[(qd + k) * 64 + lane];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) pr[j][k] = sc4[j][(c0 >> 2) + qd + k];
+        for (int j = 0; j < TPW; ++j) pr[j][k] = sc4[j][(c0 >> 2) + qd + k];
       }
 #pragma unroll
       for (int k = 0; k < 4; ++k)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[j] = fma4(acc[j], pr[j][k], v[k]);
+        for (int j = 0; j < TPW; ++j) acc[j] = fma4(acc[j], pr[j][k], v[k]);
     }
     for (; qd < nq; ++qd) {  // the rest, position by position against each token's last
       const f32x4_t v = vbuf[qd * 64 + lane];
       const int p = c0 + 4 * qd;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < TPW; ++j) {
         const int last = last0 + j;
         if (p <= last) {
           const float4 pr = sc4[j][p >> 2];
@@ -2841,8 +2915,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
     }
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int tk = wave * 4 + j;
+  for (int j = 0; j < TPW; ++j) {
+    const int tk = wave * TPW + j;
     if (tk < nt) P.out[(size_t)(t0 + tk) * P.out_ld + h * HD + lane] = acc[j];
   }
 }
