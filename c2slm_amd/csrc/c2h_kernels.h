@@ -264,12 +264,12 @@ __host__ __device__ constexpr int attn_kv_lds_floats() {
 }
 __host__ __device__ inline int attn_lds_floats(int max_ctx) { return attn_kv_lds_floats() + chain_lds_floats(max_ctx); }
 // Dynamic LDS of k_attn_softmax (exps of up to max_ctx positions) and of
-// k_attn_av (two chunks of V quads and probabilities), in floats.
+// k_attn_av (three chunks of V quads and probabilities), in floats.
 __host__ __device__ inline int attn_softmax_lds_floats(int max_ctx) { return (max_ctx + 3) & ~3; }
 // probability rows of k_attn_av padded by 4 floats: the query heads' rows
-// start in different LDS banks
+// start in different LDS banks; three buffers of V quads and probabilities
 constexpr int ATT_AV_PLD = ATT_AV_CH + 4;
-constexpr int ATT_AV_LDS_FLOATS = 2 * ATT_AV_CH * ATT_AV_DSL + 2 * ATT_MAX_QPKV * ATT_AV_PLD;
+constexpr int ATT_AV_LDS_FLOATS = 3 * (ATT_AV_CH * ATT_AV_DSL + ATT_MAX_QPKV * ATT_AV_PLD);
 
 // ---- batched prefill (a prompt of up to PF_MAX tokens per pass)
 

@@ -2290,28 +2290,32 @@ __global__ void __launch_bounds__(1024) k_attn_softmax(AttnCoreParams P) {
   for (int p = tid; p < T; p += 1024) s[p] = e[p] * inv;
 }
 
-// Staging of k_attn_av: chunk j of V quads and probabilities travels
-// global -> registers of set j % 3 -> LDS buffer j & 1 (a plain copy: the
-// cache is quad-major), so three chunks (~190 KB) are in flight while wave
-// 0 chains through the current one.
 // The AV chains of long contexts (c2_tensor_attn_gen.go:85-117: per query
 // head and dim, out[d] = fma(p, V[p][d], out[d]) for p = 0..pos in order).
 // A workgroup takes one KV head and an 8-dim slice of it for all the KV
 // head's query heads: one chain wave, lane = (query head j, dim), and three
 // staging waves that bring each 256-position chunk of the V slice (8 KB)
-// and the heads' probabilities into LDS, three chunks of loads in flight.
-// The chain wave reads a 16-byte V quad and a 16-byte probability quad per
-// lane and four positions: with one chain wave per CU those reads take
-// about four clocks per position of the CU's LDS bandwidth, under the
-// six-clock dependent FMA (two chain waves of 16-dim slices per CU needed
-// about eight and ran at ~12); the V slice is read once for all query
-// heads of the group.  Measured at 32,768 positions: 146 us per layer
-// (10.7 clocks per position at 2.4 GHz; the chain loop alone, one wave on
-// LDS-resident data, runs at 7.6).  Not faster: 1,024-position chunks with
-// seven staging waves (151 us), the chain wave at a raised issue priority
-// (148 us); the probability rows' padding did not change it.
+// and the heads' probabilities (rows padded by 4 floats) into LDS.
+// The chain runs one dependent FMA per position and lane, so its speed is
+// the wave's instruction count per position: one FMA, a quarter of a V
+// quad read and a quarter of a probability quad read.  Everything else is
+// kept out of its loop:
+//   - the role split is wave-uniform (a scalar branch), so the chain's code
+//     carries none of the staging loads' memory-counter waits;
+//   - a whole chunk is unrolled with every LDS address an immediate offset
+//     from two base registers, the reads two batches of 16 positions ahead;
+//   - three LDS buffers: chunk c+1 is in LDS before the chain starts chunk
+//     c, so the read-ahead runs across the chunk boundary and the barrier
+//     after each chunk finds the staging waves waiting.
+// Staging: chunk k travels global -> register set k % 3 -> LDS buffer
+// k % 3, three chunks of loads in flight; between the barriers after
+// chunks c-1 and c the staging waves store chunk c+2, whose buffer held
+// chunk c-1.
 struct AvStage {
   f32x4_t r[ATT_AV_ITEMS];
+};
+struct AvBatch {
+  f32x4_t v[4], p[4];
 };
 
 __global__ void __launch_bounds__(ATT_AV_THREADS) k_attn_av(AttnCoreParams P) {
@@ -2321,12 +2325,15 @@ __global__ void __launch_bounds__(ATT_AV_THREADS) k_attn_av(AttnCoreParams P) {
   constexpr int NV = NQ * DS;                          // V items (16 B) per chunk
   constexpr int NP = ATT_MAX_QPKV * (ATT_AV_CH / 4);   // probability items per chunk
   constexpr int NS = ATT_AV_THREADS - 64;              // staging lanes
+  constexpr int PQ = ATT_AV_PLD / 4;                   // 16-byte items per probability row
+  constexpr int BUF = NV + ATT_MAX_QPKV * PQ;          // 16-byte items per LDS buffer
+  constexpr int NB = ATT_AV_CH / 16;                   // batches of 16 positions per chunk
   static_assert(ATT_AV_ITEMS * NS >= NV + NP, "staging covers a chunk");
+  static_assert(ATT_AV_PLD % 4 == 0, "probability rows stay 16-byte aligned");
   extern __shared__ __align__(16) unsigned char smem[];
-  f32x4_t* vb = reinterpret_cast<f32x4_t*>(smem);      // [2][NQ][DS]: quad q of dim dd
-  float* pb = reinterpret_cast<float*>(vb + 2 * NV);   // [2][ATT_MAX_QPKV][ATT_AV_PLD]
+  f32x4_t* lds = reinterpret_cast<f32x4_t*>(smem);    // [3][BUF]: V quads [NQ][DS], then [ATT_MAX_QPKV][PQ]
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qpkv = P.n_heads / P.n_kv_heads;
   const int g = (int)blockIdx.x / ATT_AV_SLICES, sl = (int)blockIdx.x % ATT_AV_SLICES;
   const int i = blockIdx.y;
@@ -2337,69 +2344,72 @@ __global__ void __launch_bounds__(ATT_AV_THREADS) k_attn_av(AttnCoreParams P) {
       P.kv + (((size_t)P.n_layers + P.layer) * P.n_kv_heads + g) * (size_t)kv_slot(P.max_ctx) * HD);
   const float* s0 = P.sc + ((size_t)i * P.n_heads + (size_t)g * qpkv) * P.sc_ld;  // head j at + j*sc_ld
   const int nch = (T + ATT_AV_CH - 1) / ATT_AV_CH;
-  const int qlast = pos >> 2;
-  const int plast4 = (T - 1) & ~3;  // a float4 starting there stays inside the row
-  const int sidx = tid - 64;        // staging lane
-  // item it of a chunk: V (quad it/DS, dim it%DS) for it < NV, then the
-  // probabilities of head (it-NV)/(ATT_AV_CH/4), float4 (it-NV)%(ATT_AV_CH/4)
-  auto load_set = [&](AvStage& st, int c) {
-#pragma unroll
-    for (int k = 0; k < ATT_AV_ITEMS; ++k) {
-      const int it = sidx + NS * k;
-      if (it < NV) {
-        const int q = min(c * NQ + it / DS, qlast);
-        st.r[k] = vcache[(size_t)q * HD + sl * DS + (it % DS)];
-      } else {
-        const int e = min(it - NV, NP - 1);
-        const int j = min(e / (ATT_AV_CH / 4), qpkv - 1);
-        st.r[k] = *reinterpret_cast<const f32x4_t*>(s0 + (size_t)j * P.sc_ld +
-                                                     min(c * ATT_AV_CH + 4 * (e % (ATT_AV_CH / 4)), plast4));
-      }
-    }
-  };
-  auto store_set = [&](const AvStage& st, int c) {
-#pragma unroll
-    for (int k = 0; k < ATT_AV_ITEMS; ++k) {
-      const int it = sidx + NS * k;
-      if (it < NV)
-        vb[(c & 1) * NV + it] = st.r[k];
-      else if (it < NV + NP) {
-        const int e = it - NV, j = e / (ATT_AV_CH / 4), f = e % (ATT_AV_CH / 4);
-        *reinterpret_cast<f32x4_t*>(pb + ((c & 1) * ATT_MAX_QPKV + j) * ATT_AV_PLD + 4 * f) = st.r[k];
-      }
-    }
-  };
-  // Wave 0 chains; waves 1.. stage.  The two roles run separate loops with
-  // the same number of barriers (one per chunk, plus the first), and the
-  // staging loop issues its loads unconditionally (chunk indices clamped).
+  const int nfull = T / ATT_AV_CH;  // whole chunks; the last, if partial, runs the general loop
   if (wave >= 1) {
+    const int qlast = pos >> 2;
+    const int plast4 = (T - 1) & ~3;  // a float4 starting there stays inside the row
+    const int sidx = tid - 64;        // staging lane
+    // item it of a chunk: V (quad it/DS, dim it%DS) for it < NV, then the
+    // probabilities of head (it-NV)/(ATT_AV_CH/4), float4 (it-NV)%(ATT_AV_CH/4)
+    auto load_set = [&](AvStage& st, int c) {
+#pragma unroll
+      for (int k = 0; k < ATT_AV_ITEMS; ++k) {
+        const int it = sidx + NS * k;
+        if (it < NV) {
+          const int q = min(c * NQ + it / DS, qlast);
+          st.r[k] = vcache[(size_t)q * HD + sl * DS + (it % DS)];
+        } else {
+          const int e = min(it - NV, NP - 1);
+          const int j = min(e / (ATT_AV_CH / 4), qpkv - 1);
+          st.r[k] = *reinterpret_cast<const f32x4_t*>(s0 + (size_t)j * P.sc_ld +
+                                                       min(c * ATT_AV_CH + 4 * (e % (ATT_AV_CH / 4)), plast4));
+        }
+      }
+    };
+    auto store_set = [&](const AvStage& st, int buf) {
+      f32x4_t* b = lds + buf * BUF;
+#pragma unroll
+      for (int k = 0; k < ATT_AV_ITEMS; ++k) {
+        const int it = sidx + NS * k;
+        if (it < NV)
+          b[it] = st.r[k];
+        else if (it < NV + NP) {
+          const int e = it - NV;
+          b[NV + (e / (ATT_AV_CH / 4)) * PQ + e % (ATT_AV_CH / 4)] = st.r[k];
+        }
+      }
+    };
+    // every load's chunk index is clamped to the last chunk, so the loop
+    // issues them unconditionally and its trips have a fixed shape
     AvStage a, b, d;
     load_set(a, 0);
     load_set(b, min(1, nch - 1));
     load_set(d, min(2, nch - 1));
     store_set(a, 0);
     load_set(a, min(3, nch - 1));
-    __syncthreads();
-    // iteration c: chunk c+1 from its set to LDS buffer (c+1)&1 (the chains
-    // read buffer c&1), then that set reloads chunk c+4
+    store_set(b, 1);
+    load_set(b, min(4, nch - 1));
+    __syncthreads();  // chunks 0 and 1 are in buffers 0 and 1
+    // iteration c (before the barrier after chunk c): chunk c+2 from set
+    // (c+2)%3 to buffer (c+2)%3, the set then loads chunk c+5
     int c = 0;
-    for (; c + 3 <= nch; c += 3) {
-      store_set(b, c + 1);
-      load_set(b, min(c + 4, nch - 1));
-      __syncthreads();
-      store_set(d, c + 2);
+    for (; c + 3 <= nfull; c += 3) {
+      store_set(d, 2);
       load_set(d, min(c + 5, nch - 1));
       __syncthreads();
-      store_set(a, c + 3);
+      store_set(a, 0);
       load_set(a, min(c + 6, nch - 1));
       __syncthreads();
-    }
-    if (c < nch) {
-      store_set(b, c + 1);
+      store_set(b, 1);
+      load_set(b, min(c + 7, nch - 1));
       __syncthreads();
     }
-    if (c + 1 < nch) {
-      store_set(d, c + 2);
+    if (c < nfull) {
+      store_set(d, 2);
+      __syncthreads();
+    }
+    if (c + 1 < nfull) {
+      store_set(a, 0);
       __syncthreads();
     }
   } else {
@@ -2407,11 +2417,58 @@ __global__ void __launch_bounds__(ATT_AV_THREADS) k_attn_av(AttnCoreParams P) {
     const int j = cl / DS, dd = cl % DS;
     const int jc = min(j, qpkv - 1);
     float acc = 0.0f;
+    // batch b of the chunk in buffer buf: V quads 4b..4b+3 of dim dd and the
+    // probability quads 4b..4b+3 of head jc, at immediate offsets
+    auto ldb = [&](AvBatch& r, const f32x4_t* base, int b) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        r.v[k] = base[(4 * b + k) * DS];
+        r.p[k] = base[NV + jc * PQ - dd + 4 * b + k];
+      }
+    };
+    auto fmab = [&](const AvBatch& r) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc = __builtin_fmaf(r.p[k].x, r.v[k].x, acc);
+        acc = __builtin_fmaf(r.p[k].y, r.v[k].y, acc);
+        acc = __builtin_fmaf(r.p[k].z, r.v[k].z, acc);
+        acc = __builtin_fmaf(r.p[k].w, r.v[k].w, acc);
+      }
+    };
     __syncthreads();
-    for (int c = 0; c < nch; ++c) {
-      const int np = min(ATT_AV_CH, T - c * ATT_AV_CH);
-      acc = av_chain_q3<DS>(pb + ((c & 1) * ATT_MAX_QPKV + jc) * ATT_AV_PLD, vb + (c & 1) * NV, np, dd, acc);
-      __syncthreads();
+    // batch b of a chunk in phase ph lives in register set (b + ph) % 3; a
+    // chunk of NB = 16 batches leaves the next chunk's first two batches in
+    // the sets of phase ph + 1, so three chunks in a row return to phase 0
+    static_assert(NB % 3 == 1, "register sets rotate by one per chunk");
+    AvBatch R[3];
+    ldb(R[0], lds + dd, 0);
+    ldb(R[1], lds + dd, 1);
+    int c = 0;
+    while (c < nfull) {
+      static_for<3>([&](auto phc) {
+        constexpr int ph = (int)phc;
+        if (c < nfull) {
+          const f32x4_t* cur = lds + ph * BUF + dd;             // chunk c, c % 3 == ph
+          const f32x4_t* nxt = lds + ((ph + 1) % 3) * BUF + dd;  // chunk c+1, in LDS since the last barrier
+          static_for<NB>([&](auto bb) {
+            constexpr int b = (int)bb;
+            if constexpr (b + 2 < NB)
+              ldb(R[(b + 2 + ph) % 3], cur, b + 2);
+            else
+              ldb(R[(b + 2 + ph) % 3], nxt, b + 2 - NB);
+            __builtin_amdgcn_sched_barrier(0);
+            fmab(R[(b + ph) % 3]);
+            __builtin_amdgcn_sched_barrier(0);
+          });
+          __syncthreads();
+          ++c;
+        }
+      });
+    }
+    if (nfull < nch) {  // the partial last chunk, in buffer nfull % 3
+      const int np = T - nfull * ATT_AV_CH;
+      const f32x4_t* lb = lds + (nfull % 3) * BUF;
+      acc = av_chain_q3<DS>(reinterpret_cast<const float*>(lb + NV + jc * PQ), lb, np, dd, acc);
     }
     if (j < qpkv) P.out[(size_t)ti * P.out_ld + (size_t)(g * qpkv + j) * HD + sl * DS + dd] = acc;
   }
