@@ -3012,23 +3012,20 @@ __device__ __forceinline__ PFA pf_load_a(const WeightRef& W, int nb, int row, in
 __device__ __forceinline__ long as_long(u32x2_t v) { return (long)((uint64_t)v.x | ((uint64_t)v.y << 32)); }
 
 // Row parameters a row's lanes publish for the lanes that fold its outputs:
-// Q4_K d, dmin, sc[8], m[8] (c2_tensor_dot_q4_k_q8_k_gen.go:38-61);
-// Q6_K d, sc[16] (int8).
+// Q4_K d, dmin, sc[8], m[8] (c2_tensor_dot_q4_k_q8_k_gen.go:38-61), the
+// 6-bit scales and mins already as floats (exact).
 constexpr int PF_RP = 20;
-template <int TYPE>
-__device__ __forceinline__ void pf_row_params(const PFA& A, int32_t* rp) {
-  if (TYPE == T_Q4_K) {
-    rp[0] = __float_as_int(fp16_simd_nb(A.hdr.x & 0xffffu));
-    rp[1] = __float_as_int(fp16_simd_nb(A.hdr.x >> 16));
-    const uint4 h = make_uint4(A.hdr.x, A.hdr.y, A.hdr.z, A.hdr.w);
-    auto s = [&](int i) { return (int)byte_of(h, 4 + i); };
+__device__ __forceinline__ void pf_row_params_q4k(const PFA& A, float* rp) {
+  rp[0] = fp16_simd_nb(A.hdr.x & 0xffffu);
+  rp[1] = fp16_simd_nb(A.hdr.x >> 16);
+  const uint4 h = make_uint4(A.hdr.x, A.hdr.y, A.hdr.z, A.hdr.w);
+  auto s = [&](int i) { return (int)byte_of(h, 4 + i); };
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      rp[2 + j] = s(j) & 63;
-      rp[10 + j] = s(j + 4) & 63;
-      rp[2 + 4 + j] = (s(j + 8) & 15) | ((s(j) >> 6) << 4);
-      rp[10 + 4 + j] = (s(j + 8) >> 4) | ((s(j + 4) >> 6) << 4);
-    }
+  for (int j = 0; j < 4; ++j) {
+    rp[2 + j] = (float)(s(j) & 63);
+    rp[10 + j] = (float)(s(j + 4) & 63);
+    rp[2 + 4 + j] = (float)((s(j + 8) & 15) | ((s(j) >> 6) << 4));
+    rp[10 + 4 + j] = (float)((s(j + 8) >> 4) | ((s(j + 4) >> 6) << 4));
   }
 }
 
@@ -3045,8 +3042,8 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
   static_assert(TYPE == T_Q4_K, "Q6_K prefill projections run k_pf_gemm_q6");
   __shared__ __align__(16) uint32_t sq[PF_TILE][68];  // Q8_K quants of the token tile (4-dword pad per row)
   __shared__ float sd[PF_TILE];
-  __shared__ int32_t sbs[PF_TILE][17];
-  __shared__ int32_t rp[4][16][PF_RP];
+  __shared__ __align__(8) float sbp[PF_TILE][8];     // f32(bsum[2i] + bsum[2i+1]) per token, i = 0..7
+  __shared__ float rp[4][16][PF_RP];
 
   int ji = 0;
 #pragma unroll
@@ -3059,6 +3056,33 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
   const int lr = lane & 15, lk = lane >> 4;
   const int arow = min(row0 + 16 * wave + lr, J.rows - 1);  // the A-operand row of this lane
   const int nb = P.nb;
+  const int nbs = P.in.nbs;
+
+  // Every per-block load is a buffer load whose block-dependent part is a
+  // scalar offset: the per-lane offsets are computed once.
+  const __amdgpu_buffer_rsrc_t qrs =
+      __builtin_amdgcn_make_buffer_rsrc(P.in.q + (size_t)t0 * nbs * QK_K, 0, PF_TILE * nbs * QK_K, 0x00020000);
+  const __amdgpu_buffer_rsrc_t brs =
+      __builtin_amdgcn_make_buffer_rsrc(P.in.bs + (size_t)t0 * nbs * 16, 0, PF_TILE * nbs * 64, 0x00020000);
+  const __amdgpu_buffer_rsrc_t drs =
+      __builtin_amdgcn_make_buffer_rsrc(P.in.d + (size_t)t0 * nbs, 0, PF_TILE * nbs * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t ars =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(J.w.q), 0, J.rows * nb * BS_Q4K, 0x00020000);
+  const int tq = tid >> 4, w4 = tid & 15;  // token tq + 16i, 16-byte piece w4 of its block
+  const int qoff = (tq * nbs) * QK_K + w4 * 16, qstep = 16 * nbs * QK_K;
+  const int boff = (tq * nbs * 16 + w4) * 4, bstep = 16 * nbs * 64;
+  const int doff = lane * nbs * 4;
+  const int aoff = arow * nb * BS_Q4K;
+  auto load_a = [&](PFA& A, int b) {
+    const int so = b * BS_Q4K;
+    A.hdr = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ars, aoff, so, 0));
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+      A.a[p] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(ars, aoff + 16 + 32 * p + 8 * lk, so, 0));
+#pragma unroll
+    for (int p = 4; p < 16; ++p) A.a[p] = A.a[0];
+    A.d6 = 0;
+  };
 
   float acc[4][4];
 #pragma unroll
@@ -3066,32 +3090,30 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc[tt][v] = 0.0f;
 
-  PFA cur = pf_load_a<TYPE>(J.w, nb, arow, 0, lk);
+  PFA cur;
+  load_a(cur, 0);
   for (int b = 0; b < nb; ++b) {
     // the token tile's block b: 16 dwords of quants, the scale and 4 bsums per thread
     u32x4_t qv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int f = tid + 256 * i, t = f >> 4, w4 = f & 15;
-      qv[i] = reinterpret_cast<const u32x4_t*>(P.in.q + ((size_t)(t0 + t) * P.in.nbs + b) * QK_K)[w4];
-    }
-    const float dv = P.in.d[(size_t)(t0 + (tid & 63)) * P.in.nbs + b];
     int32_t bsv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int f = tid + 256 * i;
-      bsv[i] = P.in.bs[((size_t)(t0 + (f >> 4)) * P.in.nbs + b) * 16 + (f & 15)];
+      qv[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(qrs, qoff + i * qstep, b * QK_K, 0));
+      bsv[i] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(brs, boff + i * bstep, b * 64, 0);
     }
-    const PFA nxt = pf_load_a<TYPE>(J.w, nb, arow, min(b + 1, nb - 1), lk);
+    const float dv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(drs, doff, b * 4, 0));
+    PFA nxt;
+    load_a(nxt, min(b + 1, nb - 1));
     __syncthreads();  // the previous block is consumed
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int f = tid + 256 * i, t = f >> 4, w4 = f & 15;
-      *reinterpret_cast<u32x4_t*>(&sq[t][4 * w4]) = qv[i];
-      sbs[t][f & 15] = bsv[i];
+      *reinterpret_cast<u32x4_t*>(&sq[tq + 16 * i][4 * w4]) = qv[i];
+      // bsums j, j^1 sit in lanes l, l^1: the even lane stores their pair sum
+      const int other = __builtin_amdgcn_mov_dpp(bsv[i], 0xb1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+      if ((w4 & 1) == 0) sbp[tq + 16 * i][w4 >> 1] = (float)(bsv[i] + other);
     }
     if (tid < PF_TILE) sd[tid] = dv;
-    if (lk == 0) pf_row_params<TYPE>(cur, rp[wave][lr]);
+    if (lk == 0) pf_row_params_q4k(cur, rp[wave][lr]);
     __syncthreads();
 
     {
@@ -3109,15 +3131,14 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
           const i32x4_t slo = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, b_lo, zero, 0, 0, 0);
           const i32x4_t shi = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, b_hi, zero, 0, 0, 0);
           const float q8d = sd[t];
-          const float bA = (float)(sbs[t][4 * p] + sbs[t][4 * p + 1]);
-          const float bB = (float)(sbs[t][4 * p + 2] + sbs[t][4 * p + 3]);
+          const float bA = sbp[t][2 * p], bB = sbp[t][2 * p + 1];
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            const int32_t* r = rp[wave][4 * lk + v];
-            const float dW = __int_as_float(r[0]) * q8d;
-            const float mW = __int_as_float(r[1]) * q8d;
-            const float sc0 = (float)r[2 + 2 * p], sc1 = (float)r[3 + 2 * p];
-            const float m0 = (float)r[10 + 2 * p], m1 = (float)r[11 + 2 * p];
+            const float* r = rp[wave][4 * lk + v];
+            const float dW = r[0] * q8d;
+            const float mW = r[1] * q8d;
+            const float sc0 = r[2 + 2 * p], sc1 = r[3 + 2 * p];
+            const float m0 = r[10 + 2 * p], m1 = r[11 + 2 * p];
             const float term = (((float)slo[v] * (dW * sc0)) - (bA * (mW * m0))) +
                                (((float)shi[v] * (dW * sc1)) - (bB * (mW * m1)));
             acc[tt][v] = acc[tt][v] + term;
