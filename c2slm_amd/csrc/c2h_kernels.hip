@@ -2981,33 +2981,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PFA_WA
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x16_t __attribute__((ext_vector_type(16)));
 
-// One super-block of one weight row as the MFMA A operand needs it: lane
-// (r = lane%16, k-group lk = lane/16) holds 8 consecutive quants of every
-// 32-element chunk: Q4_K qs[32p + 8lk .. +8) (low nibbles: chunk 2p, high:
-// 2p+1); Q6_K ql/qh bytes of quarter (n, k).  Plus the row's scale header.
+// One Q4_K super-block of one weight row as the MFMA A operand needs it:
+// lane (r = lane%16, k-group lk = lane/16) holds qs[32p + 8lk .. +8) of
+// every pair p (low nibbles: chunk 2p, high: 2p+1), plus the row's header.
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
 struct PFA {
-  u32x2_t a[16];  // Q4_K: a[p] = qs bytes of pair p; Q6_K: a[c] = ql, a[8 + c] = qh of chunk c = 4n + k
-  u32x4_t hdr;    // Q4_K: d | dmin | scales[12]; Q6_K: scales[16]
-  uint32_t d6;    // Q6_K fp16 d
+  u32x2_t a[4];  // a[p] = qs bytes of pair p
+  u32x4_t hdr;   // d | dmin | scales[12]
 };
-
-template <int TYPE>
-__device__ __forceinline__ PFA pf_load_a(const WeightRef& W, int nb, int row, int b, int lk) {
-  PFA A;
-  const size_t blk = (size_t)row * nb + b;
-  if (TYPE == T_Q4_K) {
-    const uint8_t* base = W.q + blk * BS_Q4K;
-    A.hdr = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(base));
-#pragma unroll
-    for (int p = 0; p < 4; ++p) A.a[p] = *reinterpret_cast<const u32x2_t*>(base + 16 + 32 * p + 8 * lk);
-#pragma unroll
-    for (int p = 4; p < 16; ++p) A.a[p] = A.a[0];
-    A.d6 = 0;
-  }
-  return A;
-}
 
 __device__ __forceinline__ long as_long(u32x2_t v) { return (long)((uint64_t)v.x | ((uint64_t)v.y << 32)); }
 
@@ -3079,9 +3061,6 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
 #pragma unroll
     for (int p = 0; p < 4; ++p)
       A.a[p] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(ars, aoff + 16 + 32 * p + 8 * lk, so, 0));
-#pragma unroll
-    for (int p = 4; p < 16; ++p) A.a[p] = A.a[0];
-    A.d6 = 0;
   };
 
   float acc[4][4];
