@@ -1254,10 +1254,17 @@ int pf_alloc(c2h_ctx* c) {
 }
 
 typedef void (*PFGemmKernel)(PFGemmParams);
-PFGemmKernel pf_gemm_kernel(int type, int mode) {
-  if (type == C2H_Q4_K) return mode == MODE_RESID ? k_pf_gemm<T_Q4_K, MODE_RESID> : k_pf_gemm<T_Q4_K, MODE_BIAS>;
+PFGemmKernel pf_gemm_kernel(int type, int mode, bool small_tile = false) {
+  if (type == C2H_Q4_K) {
+    if (small_tile)
+      return mode == MODE_RESID ? k_pf_gemm<T_Q4_K, MODE_RESID, 1> : k_pf_gemm<T_Q4_K, MODE_BIAS, 1>;
+    return mode == MODE_RESID ? k_pf_gemm<T_Q4_K, MODE_RESID, 4> : k_pf_gemm<T_Q4_K, MODE_BIAS, 4>;
+  }
   return mode == MODE_RESID ? k_pf_gemm_q6<MODE_RESID> : k_pf_gemm_q6<MODE_BIAS>;
 }
+// A Q4_K launch whose 64 x 64 tiles would leave CUs idle runs 64-row x
+// 16-token workgroups instead (four times as many).
+constexpr int PF_SMALL_TILE_WG = 512;
 
 // y[t][r] (=|+=) W * x[t] for the given matrices: Q4_K / Q6_K on the
 // Q8_K rows (one MFMA launch per type), Q5_0 / Q8_0 on the f32 rows xf
@@ -1299,7 +1306,9 @@ void pf_gemm(c2h_ctx* c, int m, int m_pad, int nb, int mode, std::initializer_li
       const int per_xcd = (tiles * (m_pad / 32) + 7) / 8;
       hipLaunchKernelGGL(pf_gemm_kernel(type, mode), dim3(8 * per_xcd), dim3(64), 0, c->stream, P);
     } else {
-      hipLaunchKernelGGL(pf_gemm_kernel(type, mode), dim3(tiles, m_pad / PF_TILE), dim3(256), 0, c->stream, P);
+      const bool small = tiles * (m_pad / PF_TILE) < PF_SMALL_TILE_WG;
+      hipLaunchKernelGGL(pf_gemm_kernel(type, mode, small), dim3(tiles, m_pad / (small ? 16 : PF_TILE)), dim3(256), 0,
+                         c->stream, P);
     }
   }
   PFGemmFParams F;

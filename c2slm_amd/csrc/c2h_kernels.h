@@ -418,7 +418,7 @@ template <int NB>
 __global__ void k_pf_norm_quant(PFNormParams P);
 template <int NB>
 __global__ void k_pf_quant(PFQuantParams P);
-template <int TYPE, int MODE>
+template <int TYPE, int MODE, int TT>  // TT: 16-token sub-tiles per wave (64 or 16 tokens per workgroup)
 __global__ void k_pf_gemm(PFGemmParams P);
 // Q6_K jobs of a prefill: the reference's integer super-block sum
 // isum = sum over sub-blocks of sc * sum(q8 * (q6 - 32)) is, element by

@@ -3019,12 +3019,14 @@ __device__ __forceinline__ void pf_row_params_q4k(const PFA& A, float* rp) {
 // q8[64p..+32), high nibbles x q8[64p+32..+32)) give s_lo, s_hi; the lane
 // then adds the pair term of c2_tensor_dot_q4_k_q8_k_gen.go:85 for its 4
 // rows x 1 token.  (Q6_K projections run k_pf_gemm_q6.)
-template <int TYPE, int MODE>
+template <int TYPE, int MODE, int TT>
 __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
   static_assert(TYPE == T_Q4_K, "Q6_K prefill projections run k_pf_gemm_q6");
-  __shared__ __align__(16) uint32_t sq[PF_TILE][68];  // Q8_K quants of the token tile (4-dword pad per row)
-  __shared__ float sd[PF_TILE];
-  __shared__ __align__(8) float sbp[PF_TILE][8];     // f32(bsum[2i] + bsum[2i+1]) per token, i = 0..7
+  static_assert(TT == 1 || TT == 4, "16 or 64 tokens per workgroup");
+  constexpr int TOK = 16 * TT;  // tokens of the workgroup's tile
+  __shared__ __align__(16) uint32_t sq[TOK][68];  // Q8_K quants of the token tile (4-dword pad per row)
+  __shared__ float sd[TOK];
+  __shared__ __align__(8) float sbp[TOK][8];     // f32(bsum[2i] + bsum[2i+1]) per token, i = 0..7
   __shared__ float rp[4][16][PF_RP];
 
   int ji = 0;
@@ -3033,7 +3035,7 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
     if (j < P.n_jobs && (int)blockIdx.x >= P.jobs[j].tile_begin) ji = j;
   const PFJob& J = P.jobs[ji];
   const int row0 = ((int)blockIdx.x - J.tile_begin) * PF_TILE;
-  const int t0 = (int)blockIdx.y * PF_TILE;
+  const int t0 = (int)blockIdx.y * TOK;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lr = lane & 15, lk = lane >> 4;
   const int arow = min(row0 + 16 * wave + lr, J.rows - 1);  // the A-operand row of this lane
@@ -3043,17 +3045,17 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
   // Every per-block load is a buffer load whose block-dependent part is a
   // scalar offset: the per-lane offsets are computed once.
   const __amdgpu_buffer_rsrc_t qrs =
-      __builtin_amdgcn_make_buffer_rsrc(P.in.q + (size_t)t0 * nbs * QK_K, 0, PF_TILE * nbs * QK_K, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(P.in.q + (size_t)t0 * nbs * QK_K, 0, TOK * nbs * QK_K, 0x00020000);
   const __amdgpu_buffer_rsrc_t brs =
-      __builtin_amdgcn_make_buffer_rsrc(P.in.bs + (size_t)t0 * nbs * 16, 0, PF_TILE * nbs * 64, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(P.in.bs + (size_t)t0 * nbs * 16, 0, TOK * nbs * 64, 0x00020000);
   const __amdgpu_buffer_rsrc_t drs =
-      __builtin_amdgcn_make_buffer_rsrc(P.in.d + (size_t)t0 * nbs, 0, PF_TILE * nbs * 4, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(P.in.d + (size_t)t0 * nbs, 0, TOK * nbs * 4, 0x00020000);
   const __amdgpu_buffer_rsrc_t ars =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(J.w.q), 0, J.rows * nb * BS_Q4K, 0x00020000);
   const int tq = tid >> 4, w4 = tid & 15;  // token tq + 16i, 16-byte piece w4 of its block
   const int qoff = (tq * nbs) * QK_K + w4 * 16, qstep = 16 * nbs * QK_K;
   const int boff = (tq * nbs * 16 + w4) * 4, bstep = 16 * nbs * 64;
-  const int doff = lane * nbs * 4;
+  const int doff = (lane & (TOK - 1)) * nbs * 4;
   const int aoff = arow * nb * BS_Q4K;
   auto load_a = [&](PFA& A, int b) {
     const int so = b * BS_Q4K;
@@ -3063,9 +3065,9 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
       A.a[p] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(ars, aoff + 16 + 32 * p + 8 * lk, so, 0));
   };
 
-  float acc[4][4];
+  float acc[TT][4];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
+  for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc[tt][v] = 0.0f;
 
@@ -3073,10 +3075,10 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
   load_a(cur, 0);
   for (int b = 0; b < nb; ++b) {
     // the token tile's block b: 16 dwords of quants, the scale and 4 bsums per thread
-    u32x4_t qv[4];
-    int32_t bsv[4];
+    u32x4_t qv[TT];
+    int32_t bsv[TT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < TT; ++i) {
       qv[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(qrs, qoff + i * qstep, b * QK_K, 0));
       bsv[i] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(brs, boff + i * bstep, b * 64, 0);
     }
@@ -3085,13 +3087,13 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
     load_a(nxt, min(b + 1, nb - 1));
     __syncthreads();  // the previous block is consumed
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < TT; ++i) {
       *reinterpret_cast<u32x4_t*>(&sq[tq + 16 * i][4 * w4]) = qv[i];
       // bsums j, j^1 sit in lanes l, l^1: the even lane stores their pair sum
       const int other = __builtin_amdgcn_mov_dpp(bsv[i], 0xb1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
       if ((w4 & 1) == 0) sbp[tq + 16 * i][w4 >> 1] = (float)(bsv[i] + other);
     }
-    if (tid < PF_TILE) sd[tid] = dv;
+    if (tid < TOK) sd[tid] = dv;
     if (lk == 0) pf_row_params_q4k(cur, rp[wave][lr]);
     __syncthreads();
 
@@ -3102,7 +3104,7 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
         const long a_lo = as_long(qs & 0x0f0f0f0fu);
         const long a_hi = as_long((qs >> 4) & 0x0f0f0f0fu);
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
+        for (int tt = 0; tt < TT; ++tt) {
           const int t = tt * 16 + lr;
           const long b_lo = as_long(*reinterpret_cast<const u32x2_t*>(&sq[t][16 * p + 2 * lk]));
           const long b_hi = as_long(*reinterpret_cast<const u32x2_t*>(&sq[t][16 * p + 8 + 2 * lk]));
@@ -3130,7 +3132,7 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PFGemmParams P) {
 
   // ---- epilogue: lane holds rows 16w + 4lk + v, tokens 16tt + lr
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
+  for (int tt = 0; tt < TT; ++tt) {
     const int t = t0 + tt * 16 + lr;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -3316,8 +3318,10 @@ C2H_PF(4)
 #undef C2H_PF
 template __global__ void k_pf_quant<12>(PFQuantParams);
 template __global__ void k_pf_quant<19>(PFQuantParams);
-template __global__ void k_pf_gemm<T_Q4_K, MODE_BIAS>(PFGemmParams);
-template __global__ void k_pf_gemm<T_Q4_K, MODE_RESID>(PFGemmParams);
+template __global__ void k_pf_gemm<T_Q4_K, MODE_BIAS, 4>(PFGemmParams);
+template __global__ void k_pf_gemm<T_Q4_K, MODE_RESID, 4>(PFGemmParams);
+template __global__ void k_pf_gemm<T_Q4_K, MODE_BIAS, 1>(PFGemmParams);
+template __global__ void k_pf_gemm<T_Q4_K, MODE_RESID, 1>(PFGemmParams);
 
 // ------------------------------------------------------------------ vocab
 
