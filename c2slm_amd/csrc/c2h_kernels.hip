@@ -2279,7 +2279,16 @@ __global__ void __launch_bounds__(1024) k_attn_softmax(AttnCoreParams P) {
   for (int w = 1; w < 16; ++w) mx = fmax_gt(mx, red[w]);
   const float s0 = s[0];
   if (s0 != s0) mx = s0;
-  for (int p = tid; p < T; p += 1024) e[p] = (float)exp((double)(s[p] - mx));
+  // the scores come from global memory: eight loads per thread in flight
+  // before their exps (a load-then-exp loop waits out the latency each time)
+  for (int p0 = tid; p0 < T; p0 += 8 * 1024) {
+    float sv[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) sv[k] = s[min(p0 + 1024 * k, T - 1)];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (p0 + 1024 * k < T) e[p0 + 1024 * k] = (float)exp((double)(sv[k] - mx));
+  }
   __syncthreads();
   if (tid < 64) {
     const float ssum = seq_sum_wave_n(e, T);
