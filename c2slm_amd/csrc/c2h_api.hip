@@ -1079,7 +1079,8 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
         if (hipFuncSetAttribute((const void*)attn_core_kernel(form), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)c->attn_lds) != hipSuccess)
           return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
-      const void* pff[] = {(const void*)k_pf_gemm_f<MODE_BIAS>, (const void*)k_pf_gemm_f<MODE_RESID>};
+      const void* pff[] = {(const void*)k_pf_gemm_f<MODE_BIAS>, (const void*)k_pf_gemm_f<MODE_RESID>,
+                           (const void*)k_pf_gemm_q50<MODE_BIAS>, (const void*)k_pf_gemm_q50<MODE_RESID>};
       for (const void* k : pff)
         if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, PF_F_LDS_MAX) != hipSuccess)
           return bail(fail(c, C2H_ERR_HIP, "prefill GEMM LDS attribute"));
@@ -1311,33 +1312,43 @@ void pf_gemm(c2h_ctx* c, int m, int m_pad, int nb, int mode, std::initializer_li
                          c->stream, P);
     }
   }
-  PFGemmFParams F;
-  memset(&F, 0, sizeof(F));
-  F.x = xf;
-  F.ldx = ldxf;
-  F.n_x = n_x;
-  F.m = m;
-  int tiles = 0;
+  // float-input jobs: Q5_0 rows of up to PF_Q50_MAXB blocks in one
+  // k_pf_gemm_q50 launch, the others (Q8_0, wider Q5_0) in one k_pf_gemm_f
   const int nb8 = n_x / 32;
-  for (size_t i = 0; i < W.size(); ++i) {
-    if (!float_input(W[i]->type)) continue;
-    PFJob& J = F.jobs[F.n_jobs++];
-    J.w = W[i]->ref();
-    J.type = W[i]->type;
-    J.rows = (int)W[i]->rows;
-    J.tile_begin = tiles;
-    const int R = (J.type == C2H_Q5_0) ? std::max(1, 256 / nb8) : 32;
-    tiles += (J.rows + R - 1) / R;
-    J.mode = mode;
-    J.y = Y[i];
-    J.ldy = L[i];
-    J.bias = B[i];
-  }
-  if (F.n_jobs) {
-    // one launch for all float-input jobs: the Q8_0 v rows overlap the Q5_0 q/k rows
-    const size_t lds = (size_t)pf_gemm_f_lds_bytes(n_x);
-    auto k = (mode == MODE_RESID) ? k_pf_gemm_f<MODE_RESID> : k_pf_gemm_f<MODE_BIAS>;
-    hipLaunchKernelGGL(k, dim3(tiles, (m + PF_FT - 1) / PF_FT), dim3(256), lds, c->stream, F);
+  for (int batched = 1; batched >= 0; --batched) {
+    PFGemmFParams F;
+    memset(&F, 0, sizeof(F));
+    F.x = xf;
+    F.ldx = ldxf;
+    F.n_x = n_x;
+    F.m = m;
+    int tiles = 0;
+    for (size_t i = 0; i < W.size(); ++i) {
+      if (!float_input(W[i]->type)) continue;
+      const bool q50b = W[i]->type == C2H_Q5_0 && nb8 <= PF_Q50_MAXB;
+      if (q50b != (batched == 1)) continue;
+      PFJob& J = F.jobs[F.n_jobs++];
+      J.w = W[i]->ref();
+      J.type = W[i]->type;
+      J.rows = (int)W[i]->rows;
+      J.tile_begin = tiles;
+      const int R = (J.type == C2H_Q5_0) ? std::max(1, 256 / nb8) : 32;
+      tiles += (J.rows + R - 1) / R;
+      J.mode = mode;
+      J.y = Y[i];
+      J.ldy = L[i];
+      J.bias = B[i];
+    }
+    if (F.n_jobs == 0) continue;
+    if (batched) {
+      auto k = (mode == MODE_RESID) ? k_pf_gemm_q50<MODE_RESID> : k_pf_gemm_q50<MODE_BIAS>;
+      hipLaunchKernelGGL(k, dim3(tiles, (m + PF_FT - 1) / PF_FT), dim3(256), (size_t)pf_gemm_q50_lds_bytes(n_x),
+                         c->stream, F);
+    } else {
+      auto k = (mode == MODE_RESID) ? k_pf_gemm_f<MODE_RESID> : k_pf_gemm_f<MODE_BIAS>;
+      hipLaunchKernelGGL(k, dim3(tiles, (m + PF_FT - 1) / PF_FT), dim3(256), (size_t)pf_gemm_f_lds_bytes(n_x),
+                         c->stream, F);
+    }
   }
 }
 

@@ -340,7 +340,7 @@ struct PFGemmParams {
 // tiles of the jobs, ceil(m / PF_FT)); tile_begin counts row tiles of
 // max(1, 256/(n_x/32)) rows (Q5_0) or 32 rows (Q8_0).
 constexpr int PF_FT = 16;  // tokens per k_pf_gemm_f workgroup
-constexpr int PF_Q50_MAXB = 32;  // Q5_0 blocks per row of k_pf_gemm_f's batched-token form
+constexpr int PF_Q50_MAXB = 32;  // Q5_0 blocks per row of k_pf_gemm_q50 (wider rows run k_pf_gemm_f)
 struct PFGemmFParams {
   const float* x;
   int ldx;
@@ -388,15 +388,16 @@ __global__ void k_gemv_row(const float* xp, int n_xp, GemvParams P);  // xp, n_x
 template <int PRO, int MODE>
 __global__ void k_gemv_f(GemvParams P);
 constexpr int GF_XPAD = 36;  // floats per 32-element block of x in LDS (Q5_0 reads, bank spread)
-// Dynamic LDS of k_pf_gemm_f, bytes: x of one token in both layouts, or
-// (Q5_0 rows up to PF_Q50_MAXB blocks) x of PF_FT tokens and their terms.
+// Dynamic LDS of k_pf_gemm_f, bytes: x of one token in both layouts.
 __host__ __device__ inline int pf_gemm_f_lds_bytes(int n_x) {
   const int nb8 = n_x / 32;
-  const int one = (nb8 * GF_XPAD + nb8 * 32) * 4;
-  const int batch = (PF_FT * nb8 * GF_XPAD + PF_FT * 256) * 4;
-  return (nb8 <= PF_Q50_MAXB && batch > one) ? batch : one;
+  return (nb8 * GF_XPAD + nb8 * 32) * 4;
 }
-constexpr int PF_F_LDS_MAX = (PF_FT * PF_Q50_MAXB * GF_XPAD + PF_FT * 256) * 4;
+// Dynamic LDS of k_pf_gemm_q50, bytes: x of half the tokens, the terms.
+__host__ __device__ inline int pf_gemm_q50_lds_bytes(int n_x) {
+  return ((PF_FT / 2) * (n_x / 32) * GF_XPAD + PF_FT * 256) * 4;
+}
+constexpr int PF_F_LDS_MAX = ((PF_FT / 2) * PF_Q50_MAXB * GF_XPAD + PF_FT * 256) * 4;
 // Dynamic LDS of k_gemv_f, in floats: x padded per block | x permuted | norm chain.
 __host__ __device__ inline int gemv_f_lds_floats(int n_x) {
   return (n_x / 32) * GF_XPAD + (n_x / 32) * 32 + chain_lds_floats(n_x);
@@ -440,6 +441,8 @@ __global__ void k_pf_gemm_q6(PFGemmParams P);
 
 template <int MODE>
 __global__ void k_pf_gemm_f(PFGemmFParams P);
+template <int MODE>
+__global__ void k_pf_gemm_q50(PFGemmFParams P);
 __global__ void k_pf_rope_store(PFRopeParams P);
 __global__ void k_pf_swiglu(const float* gate, const float* up, float* h, int n, int m);
 template <int NB8>

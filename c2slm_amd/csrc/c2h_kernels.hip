@@ -2554,7 +2554,8 @@ __global__ void __launch_bounds__(256) k_pf_quant(PFQuantParams P) {
 
 // Q5_0 / Q8_0 projections of a token batch on f32 rows (the decode
 // kernel's per-row arithmetic, k_gemv_f): a workgroup keeps its rows'
-// weights in registers and runs PF_FT tokens one after the other.
+// weights in registers and runs PF_FT tokens one after the other.  (Q5_0
+// rows of up to PF_Q50_MAXB blocks run k_pf_gemm_q50.)
 template <int MODE>
 __global__ void __launch_bounds__(256) k_pf_gemm_f(PFGemmFParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -2585,76 +2586,6 @@ __global__ void __launch_bounds__(256) k_pf_gemm_f(PFGemmFParams P) {
   else
     w8 = load_q80(J.w, nb8, row_c, lane8);
   const int t0 = blockIdx.y * PF_FT;
-  if (q50 && nb8 <= PF_Q50_MAXB) {
-    // Q5_0 rows of up to 1,024 columns: the thread's block decoded once to
-    // floats, x of all the workgroup's tokens staged together, every
-    // (token, block) term into LDS, then one thread per (token, row) folds
-    // the row's terms in block order -- two barriers for the 16 tokens.
-    float* xs = reinterpret_cast<float*>(smem);  // [PF_FT][nb8][GF_XPAD]
-    float* tm = xs + PF_FT * nb8 * GF_XPAD;      // [PF_FT][256]
-    const int nt = min(PF_FT, P.m - t0);
-    float qf[32];
-    {
-      const uint32_t qw[4] = {w5.qs.x, w5.qs.y, w5.qs.z, w5.qs.w};
-      const uint32_t qh = w5.hd.x;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const uint32_t byte = (qw[e >> 2] >> (8 * (e & 3))) & 0xffu;
-        qf[e] = (float)((int)((byte & 15u) | (((qh >> e) & 1u) << 4)) - 16);
-        qf[e + 16] = (float)((int)((byte >> 4) | (((qh >> (e + 16)) & 1u) << 4)) - 16);
-      }
-    }
-    const float dq = fp16_tensor(w5.hd.y & 0xffffu);
-    for (int e = tid; e < nt * nb8 * 32; e += 256) {
-      const int tt = e / (nb8 * 32), r = e - tt * (nb8 * 32);
-      xs[(tt * nb8 + (r >> 5)) * GF_XPAD + (r & 31)] = P.x[(size_t)(t0 + tt) * P.ldx + r];
-    }
-    __syncthreads();
-    if (active) {
-      for (int tt = 0; tt < nt; ++tt) {
-        const float4* xb = reinterpret_cast<const float4*>(xs + (tt * nb8 + b5) * GF_XPAD);
-        float xv[32];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const float4 v = xb[k];
-          xv[4 * k] = v.x;
-          xv[4 * k + 1] = v.y;
-          xv[4 * k + 2] = v.z;
-          xv[4 * k + 3] = v.w;
-        }
-        float sum = 0.0f;  // q50_term's order
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          sum = sum + qf[e] * xv[e];
-          sum = sum + qf[e + 16] * xv[e + 16];
-        }
-        tm[tt * 256 + r5 * nb8 + b5] = dq * sum;
-      }
-    }
-    __syncthreads();
-    if (tid < nt * R) {
-      const int tt = tid / R, r = tid - (tid / R) * R;
-      if (row0 + r < J.rows) {
-        const float* tr = tm + tt * 256 + r * nb8;
-        float acc = 0.0f;
-#pragma unroll
-        for (int h = 0; h < PF_Q50_MAXB; h += 16) {  // sixteen terms per LDS round trip
-          float tv[16];
-#pragma unroll
-          for (int b = 0; b < 16; ++b) tv[b] = tr[min(h + b, nb8 - 1)];
-#pragma unroll
-          for (int b = 0; b < 16; ++b)
-            if (h + b < nb8) acc = acc + tv[b];
-        }
-        float* y = J.y + (size_t)(t0 + tt) * J.ldy + row0 + r;
-        if (MODE == MODE_RESID)
-          *y = *y + acc;
-        else
-          *y = J.bias ? acc + J.bias[row0 + r] : acc;
-      }
-    }
-    return;
-  }
   const float bias = (MODE == MODE_BIAS && J.bias) ? J.bias[orow] : 0.0f;
   for (int tt = 0; tt < PF_FT; ++tt) {
     const int t = t0 + tt;
@@ -2690,6 +2621,122 @@ __global__ void __launch_bounds__(256) k_pf_gemm_f(PFGemmFParams P) {
 }
 template __global__ void k_pf_gemm_f<MODE_BIAS>(PFGemmFParams);
 template __global__ void k_pf_gemm_f<MODE_RESID>(PFGemmFParams);
+
+// Q5_0 projections of a token batch on f32 rows of up to PF_Q50_MAXB blocks
+// (1,024 columns), each (row, token) in the reference's order
+// (c2_tensor_dot_q5_0: per block sum = ((0 + q0 x0) + q16 x16) + q1 x1 ...
+// as mul-then-add, term = d * sum; the row's terms added in block order).
+// Thread (row r5, block b5) of a workgroup of R = 256 / nb rows decodes its
+// block's 32 quants once into floats.  The workgroup's PF_FT tokens go
+// through in two halves: a half's x is staged in LDS, then each thread
+// runs four tokens' block sums at a time as four interleaved chains and
+// stores the terms; at the end one thread per (token, row) folds the row's
+// terms in block order.  48 KB of LDS and <= 168 registers: three
+// workgroups per CU.
+template <int MODE>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) k_pf_gemm_q50(PFGemmFParams P) {
+  constexpr int TH = PF_FT / 2;  // tokens staged at a time
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nb8 = P.n_x / 32;
+  float* xs = reinterpret_cast<float*>(smem);  // [TH][nb8][GF_XPAD]
+  float* tm = xs + TH * nb8 * GF_XPAD;         // [PF_FT][256]
+  int ji = 0;
+#pragma unroll
+  for (int j = 1; j < 3; ++j)
+    if (j < P.n_jobs && (int)blockIdx.x >= P.jobs[j].tile_begin) ji = j;
+  const PFJob& J = P.jobs[ji];
+  const int tid = threadIdx.x;
+  const int R = max(1, 256 / nb8);
+  const int row0 = ((int)blockIdx.x - J.tile_begin) * R;
+  const int b5 = tid / R, r5 = tid - (tid / R) * R;
+  const bool active = b5 < nb8 && row0 + r5 < J.rows;
+  const int bc = min(b5, nb8 - 1);
+  const Q50Item w5 = load_q50(J.w, nb8, min(row0 + r5, J.rows - 1), bc);
+  const int t0 = blockIdx.y * PF_FT;
+  const int nt = min(PF_FT, P.m - t0);
+  float qf[32];
+  {
+    const uint32_t qw[4] = {w5.qs.x, w5.qs.y, w5.qs.z, w5.qs.w};
+    const uint32_t qh = w5.hd.x;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t byte = (qw[e >> 2] >> (8 * (e & 3))) & 0xffu;
+      qf[e] = (float)((int)((byte & 15u) | (((qh >> e) & 1u) << 4)) - 16);
+      qf[e + 16] = (float)((int)((byte >> 4) | (((qh >> (e + 16)) & 1u) << 4)) - 16);
+    }
+  }
+  const float dq = fp16_tensor(w5.hd.y & 0xffffu);
+  for (int hf = 0; hf < 2; ++hf) {
+    if (hf) __syncthreads();  // the first half's x is read
+    if (tid < nb8 * 8) {      // stage x of tokens t0 + hf*TH .. +TH (zeros past the batch)
+      const int b = tid >> 3, kk = (tid & 7) * 4;
+      float4 v[TH];
+#pragma unroll
+      for (int tt = 0; tt < TH; ++tt) {
+        const int t = hf * TH + tt;
+        v[tt] = (t < nt) ? reinterpret_cast<const float4*>(P.x + (size_t)(t0 + t) * P.ldx)[tid]
+                         : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+#pragma unroll
+      for (int tt = 0; tt < TH; ++tt) *reinterpret_cast<float4*>(xs + (tt * nb8 + b) * GF_XPAD + kk) = v[tt];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < TH; g += 4) {
+      float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {  // elements 4e4..+3 and 16+4e4..+3 of the block
+        float4 lo[4], hi[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float4* xb = reinterpret_cast<const float4*>(xs + ((g + j) * nb8 + bc) * GF_XPAD);
+          lo[j] = xb[e4];
+          hi[j] = xb[4 + e4];
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int e = 4 * e4 + c;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float xl = c == 0 ? lo[j].x : c == 1 ? lo[j].y : c == 2 ? lo[j].z : lo[j].w;
+            const float xh = c == 0 ? hi[j].x : c == 1 ? hi[j].y : c == 2 ? hi[j].z : hi[j].w;
+            sum[j] = sum[j] + qf[e] * xl;
+            sum[j] = sum[j] + qf[e + 16] * xh;
+          }
+        }
+      }
+      if (active) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) tm[(hf * TH + g + j) * 256 + r5 * nb8 + b5] = dq * sum[j];
+      }
+      __builtin_amdgcn_sched_barrier(0);  // one group's x in registers at a time
+    }
+  }
+  __syncthreads();
+  if (tid < nt * R) {
+    const int tt = tid / R, r = tid - (tid / R) * R;
+    if (row0 + r < J.rows) {
+      const float* tr = tm + tt * 256 + r * nb8;
+      float acc = 0.0f;
+#pragma unroll
+      for (int h = 0; h < PF_Q50_MAXB; h += 16) {  // sixteen terms per LDS round trip
+        float tv[16];
+#pragma unroll
+        for (int b = 0; b < 16; ++b) tv[b] = tr[min(h + b, nb8 - 1)];
+#pragma unroll
+        for (int b = 0; b < 16; ++b)
+          if (h + b < nb8) acc = acc + tv[b];
+      }
+      float* y = J.y + (size_t)(t0 + tt) * J.ldy + row0 + r;
+      if (MODE == MODE_RESID)
+        *y = *y + acc;
+      else
+        *y = J.bias ? acc + J.bias[row0 + r] : acc;
+    }
+  }
+}
+template __global__ void k_pf_gemm_q50<MODE_BIAS>(PFGemmFParams);
+template __global__ void k_pf_gemm_q50<MODE_RESID>(PFGemmFParams);
 
 // RoPE of token t's k (tensor/ops.go:262-286, same expressions as the
 // attention kernel) and the K/V store at pos0 + t (engine/kvcache.go:143-157).

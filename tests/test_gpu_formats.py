@@ -78,8 +78,9 @@ def test_real_formats_greedy_stream(real_tiny):
 
 
 def test_real_formats_batched_prefill(real_tiny):
-    # Q5_0 / Q8_0 projections of a token batch (k_pf_gemm_f) with the
-    # K-quant ffn_down on MFMA: KV and normX equal sequential ingest
+    # Q5_0 / Q8_0 projections of a token batch (k_pf_gemm_q50, k_pf_gemm_f;
+    # 37 and 21 tokens: partial 16-token tiles) with the K-quant ffn_down on
+    # MFMA: KV and normX equal sequential ingest
     gf, ctx, orc, _, _ = open_pair(real_tiny, 256)
     rng = np.random.default_rng(81)
     a = rng.integers(0, 4093, 37).astype(np.int32)
