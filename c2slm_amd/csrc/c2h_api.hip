@@ -1345,8 +1345,12 @@ void pf_gemm(c2h_ctx* c, int m, int m_pad, int nb, int mode, std::initializer_li
       hipLaunchKernelGGL(k, dim3(tiles, (m + PF_FT - 1) / PF_FT), dim3(256), (size_t)pf_gemm_q50_lds_bytes(n_x),
                          c->stream, F);
     } else {
+      // tokens one after another per workgroup: fewer of them when the rows
+      // alone would leave CUs idle (the 128 rows of attn_v)
+      F.ft = PF_FT;
+      while (F.ft > 1 && tiles * ((m + F.ft - 1) / F.ft) < 512) F.ft /= 2;
       auto k = (mode == MODE_RESID) ? k_pf_gemm_f<MODE_RESID> : k_pf_gemm_f<MODE_BIAS>;
-      hipLaunchKernelGGL(k, dim3(tiles, (m + PF_FT - 1) / PF_FT), dim3(256), (size_t)pf_gemm_f_lds_bytes(n_x),
+      hipLaunchKernelGGL(k, dim3(tiles, (m + F.ft - 1) / F.ft), dim3(256), (size_t)pf_gemm_f_lds_bytes(n_x),
                          c->stream, F);
     }
   }

@@ -346,6 +346,7 @@ struct PFGemmFParams {
   int ldx;
   int n_x;
   int m;
+  int ft;  // k_pf_gemm_f: tokens per workgroup (<= PF_FT)
   int n_jobs;
   PFJob jobs[3];
 };

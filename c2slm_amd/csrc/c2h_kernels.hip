@@ -2554,7 +2554,7 @@ __global__ void __launch_bounds__(256) k_pf_quant(PFQuantParams P) {
 
 // Q5_0 / Q8_0 projections of a token batch on f32 rows (the decode
 // kernel's per-row arithmetic, k_gemv_f): a workgroup keeps its rows'
-// weights in registers and runs PF_FT tokens one after the other.  (Q5_0
+// weights in registers and runs P.ft tokens one after the other.  (Q5_0
 // rows of up to PF_Q50_MAXB blocks run k_pf_gemm_q50.)
 template <int MODE>
 __global__ void __launch_bounds__(256) k_pf_gemm_f(PFGemmFParams P) {
@@ -2585,9 +2585,9 @@ __global__ void __launch_bounds__(256) k_pf_gemm_f(PFGemmFParams P) {
     w5 = load_q50(J.w, nb8, row_c, min(b5, nb8 - 1));
   else
     w8 = load_q80(J.w, nb8, row_c, lane8);
-  const int t0 = blockIdx.y * PF_FT;
+  const int t0 = blockIdx.y * P.ft;
   const float bias = (MODE == MODE_BIAS && J.bias) ? J.bias[orow] : 0.0f;
-  for (int tt = 0; tt < PF_FT; ++tt) {
+  for (int tt = 0; tt < P.ft; ++tt) {
     const int t = t0 + tt;
     if (t >= P.m) break;  // uniform
     __syncthreads();      // the previous token's LDS reads are done
