@@ -453,7 +453,7 @@ def main():
                     help="with --only kernels: greedy steps after the prompt up to this position, so attention "
                          "covers pos+1 positions (default: the decode line's last position, prompt + warmup + steps)")
     ap.add_argument("--only", choices=["prefill", "long", "float-dots", "real-formats", "vocab", "microbench",
-                                       "kernels", "qwen3", "roofline", "wait"],
+                                       "kernels", "qwen3", "roofline", "wait", "steps"],
                     default=None,
                     help="run just the prefill reps or just the long-context decode (profiler runs); "
                          "prints their JSON object, not the bench line")
@@ -546,6 +546,17 @@ def main():
                           "launches_timed": args.kernel_iters, "us_per_launch": round(us, 3), "bytes_per_launch": nb,
                           "achieved_gbs": round(nb / (us * 1e-6) / 1e9, 1),
                           "frac": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}))
+        ctx.close()
+        cleanup()
+        return
+    if args.only == "steps":  # the decode workload's steps fed on the device: graph replays only (profiler runs)
+        ctx.set_token_ids(0, prompt)
+        for p, t in enumerate(prompt):
+            ctx.forward(int(t), p, want_normx=False)
+        n = args.warmup + args.steps
+        ms = ctx.time_steps(PROMPT_LEN, n, PENALTY, im_end, eos)
+        print(json.dumps({"device_fed_steps": {"positions": [PROMPT_LEN, PROMPT_LEN + n - 1],
+                                               "ms_per_step": round(ms, 4), "tok_s": round(1000.0 / ms, 1)}}))
         ctx.close()
         cleanup()
         return
