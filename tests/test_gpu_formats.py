@@ -99,6 +99,25 @@ def test_real_formats_batched_prefill(real_tiny):
     orc.close()
 
 
+def test_real_formats_prefill_300_tokens(real_tiny):
+    # 300 tokens from position 0: nineteen 16-token tiles of k_pf_gemm_q50
+    # (the last partial, 12 tokens: both staged halves hold padding), attn_v
+    # through k_pf_gemm_f at 4 tokens per workgroup, and the 8-token blocks
+    # of k_pf_attn up to 300 positions
+    gf, ctx, orc, _, _ = open_pair(real_tiny, 512)
+    toks = np.random.default_rng(83).integers(0, 4093, 300).astype(np.int32)
+    got = ctx.prefill(toks, 0)
+    want = orc.ingest_from(0, toks)
+    assert np.array_equal(bits(got), bits(want))
+    kv = orc.kv()
+    for which in (0, 1):
+        for layer in (0, 1):
+            for h in (0, 1):
+                assert np.array_equal(bits(ctx.kv(which, layer, h, 300)), bits(kv[which, layer, h, :300]))
+    ctx.close()
+    orc.close()
+
+
 def test_full_model_real_formats_64_steps(tmp_path_factory):
     p = str(tmp_path_factory.mktemp("models") / "qwen05b_real.gguf")
     G.write_synthetic_model(p, G.QWEN05B_REAL_FORMATS, seed=20261202)
