@@ -1059,6 +1059,9 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   // positions (staged V | all scores in LDS, within the 160 KB of a gfx950
   // workgroup, 8 KB kept for static shared data), the long-context kernels
   // beyond.  C2H_ATT_SPLIT overrides the split length (measurement aid).
+  for (const void* k : {(const void*)k_pf_gemm_q6<MODE_BIAS, 2>, (const void*)k_pf_gemm_q6<MODE_RESID, 2>})
+    if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, PF_Q6_LDS_MAX) != hipSuccess)
+      return bail(fail(c, C2H_ERR_HIP, "prefill Q6_K GEMM LDS attribute"));
   if (D.head_dim == 128) {  // k_attn_h128 at every T: the scores of max_ctx positions in LDS
     c->attn_lds = (size_t)attn_h128_lds_floats(D.max_ctx) * 4;
     if (c->attn_lds > 152u * 1024)
@@ -1254,14 +1257,19 @@ int pf_alloc(c2h_ctx* c) {
   return C2H_OK;
 }
 
+// Waves per Q6_K tile: two, each half of the super-blocks, while the
+// second wave's terms fit PF_Q6_LDS_MAX (rows of up to 65 super-blocks,
+// which covers n_ff up to the 16384 c2h_create accepts); one beyond.
+int pf_q6_split(int nb) { return pf_q6_lds_bytes(nb, 2) <= PF_Q6_LDS_MAX ? 2 : 1; }
 typedef void (*PFGemmKernel)(PFGemmParams);
-PFGemmKernel pf_gemm_kernel(int type, int mode, bool small_tile = false) {
+PFGemmKernel pf_gemm_kernel(int type, int mode, bool small_tile = false, int q6_split = 1) {
   if (type == C2H_Q4_K) {
     if (small_tile)
       return mode == MODE_RESID ? k_pf_gemm<T_Q4_K, MODE_RESID, 1> : k_pf_gemm<T_Q4_K, MODE_BIAS, 1>;
     return mode == MODE_RESID ? k_pf_gemm<T_Q4_K, MODE_RESID, 4> : k_pf_gemm<T_Q4_K, MODE_BIAS, 4>;
   }
-  return mode == MODE_RESID ? k_pf_gemm_q6<MODE_RESID> : k_pf_gemm_q6<MODE_BIAS>;
+  if (q6_split == 2) return mode == MODE_RESID ? k_pf_gemm_q6<MODE_RESID, 2> : k_pf_gemm_q6<MODE_BIAS, 2>;
+  return mode == MODE_RESID ? k_pf_gemm_q6<MODE_RESID, 1> : k_pf_gemm_q6<MODE_BIAS, 1>;
 }
 // A Q4_K launch whose 64 x 64 tiles would leave CUs idle runs 64-row x
 // 16-token workgroups instead (four times as many).
@@ -1305,7 +1313,9 @@ void pf_gemm(c2h_ctx* c, int m, int m_pad, int nb, int mode, std::initializer_li
     P.n_row_tiles = tiles;
     if (type == C2H_Q6_K) {
       const int per_xcd = (tiles * (m_pad / 32) + 7) / 8;
-      hipLaunchKernelGGL(pf_gemm_kernel(type, mode), dim3(8 * per_xcd), dim3(64), 0, c->stream, P);
+      const int ns = pf_q6_split(nb);
+      hipLaunchKernelGGL(pf_gemm_kernel(type, mode, false, ns), dim3(8 * per_xcd), dim3(64 * ns),
+                         (size_t)pf_q6_lds_bytes(nb, ns), c->stream, P);
     } else {
       const bool small = tiles * (m_pad / PF_TILE) < PF_SMALL_TILE_WG;
       hipLaunchKernelGGL(pf_gemm_kernel(type, mode, small), dim3(tiles, m_pad / (small ? 16 : PF_TILE)), dim3(256), 0,

@@ -434,11 +434,17 @@ __global__ void k_pf_gemm(PFGemmParams P);
 // Grid (row tiles, super-blocks), 64 threads.
 constexpr size_t PF_Q6_TILE_BYTES = 32 * 512;  // one 32-row tile of one super-block
 __global__ void k_q6_pf_pack(WeightRef w, int rows, int nb, uint4* out);
-// One wave per 32 tokens x 32 rows; a 1-D grid of 8 * ceil(n_row_tiles *
-// m_pad / 32 / 8) workgroups of 64 threads (tile_begin and n_row_tiles in
-// 32-row tiles).
-template <int MODE>
+// NS waves per 32 tokens x 32 rows (the super-blocks split between them);
+// a 1-D grid of 8 * ceil(n_row_tiles * m_pad / 32 / 8) workgroups of 64 NS
+// threads (tile_begin and n_row_tiles in 32-row tiles); dynamic LDS of
+// pf_q6_lds_bytes(nb, NS).
+template <int MODE, int NS>
 __global__ void k_pf_gemm_q6(PFGemmParams P);
+__host__ __device__ inline int pf_q6_lds_bytes(int nb, int ns) {
+  const int per = (nb + ns - 1) / ns;
+  return ns > 1 ? (nb - per) * 16 * 64 * 4 : 0;
+}
+constexpr int PF_Q6_LDS_MAX = 128 * 1024;
 
 template <int MODE>
 __global__ void k_pf_gemm_f(PFGemmFParams P);

@@ -3241,13 +3241,21 @@ __global__ void __launch_bounds__(64) k_q6_pf_pack(WeightRef w, int rows, int nb
 // reference's integer, and acc += f32(isum) * (d * q8d) in super-block
 // order.  Lane l holds row l % 32 and tokens 8 * (i / 4) + 4 * (l / 32) +
 // i % 4 (i = 0..15).  The next super-block's operands are in flight while
-// one runs; no LDS, no barrier.  (Measured against this form, all slower:
-// one workgroup of four waves per tile, each wave a quarter of the
-// super-blocks and the terms of three of them folded in order through LDS,
-// 36.9 against 29.5 us for the 512-token ffn_down; four accumulation chains
-// instead of two, 31.1 against 28.3 us.)
-template <int MODE>
-__global__ void __launch_bounds__(64) k_pf_gemm_q6(PFGemmParams P) {
+// one runs.  NS = 2 splits the super-blocks between two waves of one
+// workgroup: wave 1 leaves its per-block terms in LDS and wave 0, after
+// its own half, adds them in super-block order, so the sum is the NS = 1
+// sum bit for bit (512-token prefill 3.73 -> 3.66 ms; three and four waves
+// per tile measured slower, 3.76 and 3.87 ms; four accumulation chains
+// instead of two, 31.1 against 28.3 us for the 512-token ffn_down).
+// NS = 1: no LDS, no barrier.
+template <int MODE, int NS>
+__global__ void __launch_bounds__(64 * NS) k_pf_gemm_q6(PFGemmParams P) {
+  // NS waves per tile: wave w runs super-blocks [w per, (w+1) per); wave 0
+  // accumulates its own, the others leave their per-block terms in LDS,
+  // and wave 0 adds them in super-block order
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* tl = reinterpret_cast<float*>(smem);  // [nb - per][16][64]
+
   // Workgroup L runs on XCD L % 8 (the dispatcher's round robin).  The
   // (row tile, token tile) pairs, row-tile major, are dealt to the XCDs in
   // contiguous runs of per_xcd = ceil(pairs / 8), so the token tiles of a
@@ -3263,7 +3271,8 @@ __global__ void __launch_bounds__(64) k_pf_gemm_q6(PFGemmParams P) {
   for (int j = 1; j < 3; ++j)
     if (j < P.n_jobs && rtile >= P.jobs[j].tile_begin) ji = j;
   const PFJob& J = P.jobs[ji];
-  const int lane = threadIdx.x, l32 = lane & 31, kg = lane >> 5;
+  const int lane = threadIdx.x & 63, l32 = lane & 31, kg = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int tile = rtile - J.tile_begin;
   const int row0 = tile * 32;
   const int t0 = (q - rtile * n_tt) * 32;
@@ -3298,7 +3307,9 @@ __global__ void __launch_bounds__(64) k_pf_gemm_q6(PFGemmParams P) {
     for (int g = 0; g < 4; ++g)
       q8d[g] = *reinterpret_cast<const float4*>(P.in.dT + (size_t)b * PF_MAX + t0 + 8 * g + 4 * kg);
   };
-  auto run = [&](const Ops& cur, const float4 (&q8d)[4]) {
+  const int per = (nb + NS - 1) / NS;
+  const int bb0 = min(w * per, nb), bb1 = min(bb0 + per, nb);
+  auto run = [&](const Ops& cur, const float4 (&q8d)[4], int b) {
     i32x16_t dh = {}, dl = {};
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
@@ -3310,7 +3321,11 @@ __global__ void __launch_bounds__(64) k_pf_gemm_q6(PFGemmParams P) {
     for (int i = 0; i < 16; ++i) {
       const float4& qd = q8d[i >> 2];
       const float qs = (i & 3) == 0 ? qd.x : (i & 3) == 1 ? qd.y : (i & 3) == 2 ? qd.z : qd.w;
-      acc[i] = acc[i] + (float)(dh[i] * 64 + dl[i]) * (dW * qs);
+      const float term = (float)(dh[i] * 64 + dl[i]) * (dW * qs);
+      if (NS == 1 || w == 0)
+        acc[i] = acc[i] + term;
+      else
+        tl[((b - per) * 16 + i) * 64 + lane] = term;
     }
   };
   // two operand sets in turn: the loads of the next super-block go out
@@ -3318,22 +3333,31 @@ __global__ void __launch_bounds__(64) k_pf_gemm_q6(PFGemmParams P) {
   // unconditional steps, the odd last super-block peeled (a load on one
   // side of a branch would make the waits drain)
   Ops o0, o1;
-  load_ops(0, o0);
-  int b = 0;
-  float4 qd[4];
-  for (; b + 1 < nb; b += 2) {
-    load_q8d(b, qd);
-    load_ops(b + 1, o1);
-    issue_fence();
-    run(o0, qd);
-    load_q8d(b + 1, qd);
-    load_ops(min(b + 2, nb - 1), o0);
-    issue_fence();
-    run(o1, qd);
+  if (bb0 < bb1) {
+    load_ops(bb0, o0);
+    int b = bb0;
+    float4 qd[4];
+    for (; b + 1 < bb1; b += 2) {
+      load_q8d(b, qd);
+      load_ops(b + 1, o1);
+      issue_fence();
+      run(o0, qd, b);
+      load_q8d(b + 1, qd);
+      load_ops(min(b + 2, bb1 - 1), o0);
+      issue_fence();
+      run(o1, qd, b + 1);
+    }
+    if (b < bb1) {
+      load_q8d(b, qd);
+      run(o0, qd, b);
+    }
   }
-  if (b < nb) {
-    load_q8d(b, qd);
-    run(o0, qd);
+  if constexpr (NS > 1) {
+    __syncthreads();
+    if (w != 0) return;
+    for (int b = per; b < nb; ++b)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] = acc[i] + tl[((b - per) * 16 + i) * 64 + lane];
   }
 
   const int r = row0 + l32;
@@ -3351,8 +3375,10 @@ __global__ void __launch_bounds__(64) k_pf_gemm_q6(PFGemmParams P) {
     }
   }
 }
-template __global__ void k_pf_gemm_q6<MODE_BIAS>(PFGemmParams);
-template __global__ void k_pf_gemm_q6<MODE_RESID>(PFGemmParams);
+template __global__ void k_pf_gemm_q6<MODE_BIAS, 1>(PFGemmParams);
+template __global__ void k_pf_gemm_q6<MODE_RESID, 1>(PFGemmParams);
+template __global__ void k_pf_gemm_q6<MODE_BIAS, 2>(PFGemmParams);
+template __global__ void k_pf_gemm_q6<MODE_RESID, 2>(PFGemmParams);
 
 // h = SwiGLU(gate, up) elementwise (c2_tensor_swiglu_gen.go; the tail of
 // n % 8 elements per row takes the scalar f64 path).
