@@ -55,6 +55,10 @@ struct c2h_ctx {
   float* output_norm = nullptr;
 
   float *X = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *h = nullptr;
+  uint64_t* attn_tag = nullptr;  // the attention output as {value, tag} words (k_attn_oproj)
+  uint64_t* qkv_tag = nullptr;   // q|k|v as {value, tag} words (k_attn_block)
+  bool fuse_oproj = true;        // attention and o-projection in one launch where an instance exists
+  bool fuse_qkv = true;          // and qkv with them (layers past 0)
   float* normx[2] = {nullptr, nullptr};
   int nx_cur = 0, nx_prev = 0;
   float* kv = nullptr;
@@ -67,7 +71,7 @@ struct c2h_ctx {
   float* logits = nullptr;
   C2hState* state_dev = nullptr;
   C2hState* state_ring = nullptr;  // pinned
-  int32_t* tok_host = nullptr;     // pinned: {token, seq} written by a step's layer 0
+  int32_t* tok_host = nullptr;     // pinned: {token, seq} written by a step's layer 0; [2] the wait flag
   unsigned step_seq = 0;           // last step number handed to the device
   // the state a completed step graph leaves on the device (its final norm
   // advances pos, seq and the normX buffers); valid until the next push
@@ -417,14 +421,19 @@ void launch_gemv_f(c2h_ctx* c, GemvParams& P) {
 
 // A row-kernel launch over all its jobs (same width and mode); the norm
 // prologues need the x*x chain buffer.
-void launch_gemv_row(c2h_ctx* c, GemvParams& P) {
-  const int nt = row_threads(P.jobs[0].nb, P.prologue, P.jobs[0].mode);
+// rows per workgroup and workgroups of each job of a k_gemv_row launch
+void prep_gemv_row(GemvParams& P) {
   const int ni = row_item_threads(P.jobs[0].nb, P.prologue, P.jobs[0].mode);
-  for (int j = 0; j < P.n_jobs; ++j) {  // rows per workgroup at this width
+  for (int j = 0; j < P.n_jobs; ++j) {
     GemvJob& J = P.jobs[j];
     J.rpw = ni / (4 * J.nb);
     J.n_wg = (J.rows + J.rpw - 1) / J.rpw;
   }
+}
+
+void launch_gemv_row(c2h_ctx* c, GemvParams& P) {
+  const int nt = row_threads(P.jobs[0].nb, P.prologue, P.jobs[0].mode);
+  prep_gemv_row(P);
   const GemvJob& J = P.jobs[0];
   GemvKernel k = gemv_row_kernel(J.nb, P.prologue, J.mode);
   size_t lds = (P.prologue != PRO_QUANT) ? (size_t)P.n_x_lds * sizeof(float) : 0;
@@ -715,6 +724,126 @@ void enqueue_attn(c2h_ctx* c, int l, int form) {
   }
 }
 
+// The k_attn_block instance of a decode tier (nullptr past the tiers).
+decltype(&k_attn_block<ATT_TIER_32, 3>) attn_block_kernel(int form) {
+  switch (form) {
+    case ATT_FORM_32: return k_attn_block<ATT_TIER_32, 3>;
+    case ATT_FORM_64: return k_attn_block<ATT_TIER_64, 3>;
+    case ATT_FORM_96: return k_attn_block<ATT_TIER_96, 3>;
+    case ATT_FORM_128: return k_attn_block<ATT_TIER_128, 3>;
+    case ATT_FORM_256: return k_attn_block<ATT_TIER_256, 3>;
+    default: return nullptr;
+  }
+}
+
+// The k_attn_oproj instance of a core form.
+decltype(&k_attn_oproj<ATT_TIER_ANY, 3>) attn_oproj_kernel(int form) {
+  switch (form) {
+    case ATT_FORM_32: return k_attn_oproj<ATT_TIER_32, 3>;
+    case ATT_FORM_64: return k_attn_oproj<ATT_TIER_64, 3>;
+    case ATT_FORM_96: return k_attn_oproj<ATT_TIER_96, 3>;
+    case ATT_FORM_128: return k_attn_oproj<ATT_TIER_128, 3>;
+    case ATT_FORM_256: return k_attn_oproj<ATT_TIER_256, 3>;
+    default: return k_attn_oproj<ATT_TIER_ANY, 3>;
+  }
+}
+
+// Whether layer l's attention and o-projection run as one launch
+// (k_attn_oproj): the head_dim 64 decode forms over the XCD-grouped grid,
+// and a K-quant o-projection of 3 super-blocks per row (the instances built).
+bool fuse_attn_oproj(const c2h_ctx* c, int l, int form) {
+  const c2h_model_desc& D = c->desc;
+  return c->fuse_oproj && D.head_dim == 64 && form < ATT_FORM_LONG && D.n_kv_heads <= ATT_XCDS &&
+         !float_input(c->layers[l].wo.type) && nb_k(D.n_embd) == 3;
+}
+
+// Whether layer l runs qkv in that launch too (k_attn_block): past layer 0
+// (whose qkv embeds the token), at the decode tiers, with K-quant q|k|v.
+bool fuse_attn_block(const c2h_ctx* c, int l, int form) {
+  const Layer& L = c->layers[l];
+  return l > 0 && c->fuse_qkv && fuse_attn_oproj(c, l, form) && attn_block_kernel(form) != nullptr &&
+         !float_input(L.wq.type) &&
+         !float_input(L.wk.type) && !float_input(L.wv.type);
+}
+
+// The attention part of the fused launches: k_attn_core's XCD-grouped grid,
+// output also tagged
+AttnCoreParams fused_attn_params(c2h_ctx* c, int l) {
+  const c2h_model_desc& D = c->desc;
+  AttnCoreParams A = attn_params(c, l);
+  A.q = c->q;
+  A.k = c->k;
+  A.v = c->v;
+  A.out = c->attn;
+  A.store_kv = 1;
+  A.xcd_map = 1;
+  A.out_tag = c->attn_tag;
+  A.n_attn_wg = ATT_XCDS * (D.n_heads / D.n_kv_heads);
+  A.wait_err = c->tok_host + 2;
+  return A;
+}
+
+// The o-projection part: X += Wo * x(attn), x read tagged
+GemvParams fused_oproj_params(c2h_ctx* c, int l) {
+  const c2h_model_desc& D = c->desc;
+  GemvParams P = base_params(c);
+  add_job(P, c->layers[l].wo, nullptr, MODE_RESID, c->X, nullptr, nullptr);
+  P.prologue = PRO_QUANT;
+  P.x = c->attn;
+  P.x_out = c->X;
+  P.n_x = D.n_embd;
+  P.n_x_lds = chain_lds_floats(D.n_embd);
+  P.nb_in = nb_k(D.n_embd);
+  P.x_tag = c->attn_tag;
+  P.wait_err = c->tok_host + 2;
+  prep_gemv_row(P);
+  return P;
+}
+
+// attention + attn_out in one launch: the attention workgroups first, then
+// the o-projection's, which wait for the tagged output
+void enqueue_attn_oproj(c2h_ctx* c, int l, int form) {
+  const c2h_model_desc& D = c->desc;
+  const AttnCoreParams A = fused_attn_params(c, l);
+  const GemvParams P = fused_oproj_params(c, l);
+  hipLaunchKernelGGL(attn_oproj_kernel(form), dim3(A.n_attn_wg + P.jobs[0].n_wg), dim3(256), c->attn_lds, c->stream,
+                     A.state, A.kv, A.q, A.k, A.v, attn_dims(A, D.n_heads / D.n_kv_heads), A.max_ctx, A, P);
+}
+
+// qkv + attention + attn_out in one launch (layers past 0): q|k|v = W *
+// x(RMSNorm(X)) + bias on 3 W workgroups (job-major, W the widest job's
+// count), stored tagged as well, then the two parts of k_attn_oproj, the
+// attention's reading q|k|v tagged
+void enqueue_attn_block(c2h_ctx* c, int l, int form) {
+  const c2h_model_desc& D = c->desc;
+  Layer& L = c->layers[l];
+  const int E = D.n_embd, KVd = D.n_kv_heads * D.head_dim;
+  GemvParams Q = base_params(c);
+  add_job(Q, L.wq, nullptr, MODE_BIAS, c->q, L.bq, nullptr);
+  add_job(Q, L.wk, nullptr, MODE_BIAS, c->k, L.bk, nullptr);
+  add_job(Q, L.wv, nullptr, MODE_BIAS, c->v, L.bv, nullptr);
+  Q.jobs[0].spare = 0;
+  Q.jobs[1].spare = E;
+  Q.jobs[2].spare = E + KVd;
+  Q.prologue = PRO_NORM;
+  Q.x = c->X;
+  Q.x_out = c->X;
+  Q.n_x = E;
+  Q.n_x_lds = chain_lds_floats(E);
+  Q.norm_w = L.attn_norm;
+  Q.nb_in = nb_k(E);
+  Q.y_tag = c->qkv_tag;
+  prep_gemv_row(Q);
+  int w = 1;
+  for (int j = 0; j < Q.n_jobs; ++j) w = std::max(w, Q.jobs[j].n_wg);
+  const AttnCoreParams A = fused_attn_params(c, l);
+  const GemvParams P = fused_oproj_params(c, l);
+  const size_t lds = std::max(c->attn_lds, (size_t)Q.n_x_lds * sizeof(float));
+  hipLaunchKernelGGL(attn_block_kernel(form), dim3(3 * w + A.n_attn_wg + P.jobs[0].n_wg), dim3(256), lds, c->stream,
+                     A.state, A.kv, (const float*)c->X, E | (w << 16), (const uint64_t*)c->qkv_tag,
+                     attn_dims(A, D.n_heads / D.n_kv_heads), A.max_ctx, A, Q, P);
+}
+
 // attn_out: X += Wo * x(attn)
 void enqueue_attn_out(c2h_ctx* c, int l) {
   launch_group(c, {{&c->layers[l].wo, nullptr, c->X, nullptr}}, PRO_QUANT, MODE_RESID, c->attn, c->desc.n_embd,
@@ -764,9 +893,17 @@ void enqueue_final_norm(c2h_ctx* c, int advance = 0) {
 // form selects the attention kernels.
 void enqueue_layers(c2h_ctx* c, bool from_argmax, int form) {
   for (int l = 0; l < c->desc.n_layers; ++l) {
-    enqueue_qkv(c, l, (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM);
-    enqueue_attn(c, l, form);
-    enqueue_attn_out(c, l);
+    if (fuse_attn_block(c, l, form)) {
+      enqueue_attn_block(c, l, form);
+    } else {
+      enqueue_qkv(c, l, (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM);
+      if (fuse_attn_oproj(c, l, form)) {
+        enqueue_attn_oproj(c, l, form);
+      } else {
+        enqueue_attn(c, l, form);
+        enqueue_attn_out(c, l);
+      }
+    }
     enqueue_ffn_in(c, l);
     enqueue_ffn_out(c, l);
   }
@@ -861,8 +998,17 @@ int push_state(c2h_ctx* c, const C2hState& s) {
     memcpy(t.rope, &c->rope_cos_h[(size_t)rp * 32], 32 * 4);
     memcpy(t.rope + 32, &c->rope_sin_h[(size_t)rp * 32], 32 * 4);
   }
-  HIPCHK(c, hipMemcpyAsync(c->state_dev, &c->state_ring[slot], sizeof(C2hState), hipMemcpyHostToDevice, c->stream));
+  // (the epoch, the last field, stays the device's)
+  HIPCHK(c, hipMemcpyAsync(c->state_dev, &c->state_ring[slot], kStatePushBytes, hipMemcpyHostToDevice, c->stream));
   return C2H_OK;
+}
+
+// A handover wait inside a launch (k_attn_oproj) that ran out sets the
+// pinned flag; the next entry point that checks reports it, once.
+int check_wait_flag(c2h_ctx* c) {
+  if (!c->tok_host || __atomic_load_n(&c->tok_host[2], __ATOMIC_ACQUIRE) == 0) return C2H_OK;
+  __atomic_store_n(&c->tok_host[2], 0, __ATOMIC_RELEASE);
+  return fail(c, C2H_ERR_HIP, "a wait for the attention output inside a launch ran out");
 }
 
 // Decode at `pos` attends to pos+1 positions.
@@ -974,15 +1120,22 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   }
   const char* ng = getenv("C2H_NO_GRAPH");
   c->use_graphs = !(ng && ng[0] == '1');
+  // measurement aid: C2H_NO_FUSE=1 separate launches, =qkv qkv on its own
+  const char* nf = getenv("C2H_NO_FUSE");
+  c->fuse_oproj = !(nf && nf[0] == '1');
+  c->fuse_qkv = c->fuse_oproj && !(nf && strcmp(nf, "qkv") == 0);
   void* pinned = nullptr;
   if (hipHostMalloc(&pinned, sizeof(C2hState) * kStateRing + 64, hipHostMallocDefault) != hipSuccess) return bail(C2H_ERR_HIP);
   c->state_ring = reinterpret_cast<C2hState*>(pinned);
   c->tok_host = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(pinned) + sizeof(C2hState) * kStateRing);
   c->tok_host[0] = 0;
   c->tok_host[1] = -1;
+  c->tok_host[2] = 0;
   int rc;
   if ((rc = noalloc_setup(c))) return bail(rc);
   if ((rc = dalloc(c, &c->state_dev, sizeof(C2hState)))) return bail(rc);
+  // the epoch (which no state push writes) starts at 0
+  if (hipMemsetAsync(c->state_dev, 0, sizeof(C2hState), c->stream) != hipSuccess) return bail(C2H_ERR_HIP);
   if (!desc) {
     C2hState s0;
     memset(&s0, 0, sizeof(s0));
@@ -1019,8 +1172,13 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   const int E = D.n_embd, KV = D.n_kv_heads * D.head_dim, F = D.n_ff;
   if ((rc = dalloc(c, &c->X, E * 4)) || (rc = dalloc(c, &c->q, E * 4)) || (rc = dalloc(c, &c->k, KV * 4)) ||
       (rc = dalloc(c, &c->v, KV * 4)) || (rc = dalloc(c, &c->attn, E * 4)) || (rc = dalloc(c, &c->h, F * 4)) ||
-      (rc = dalloc(c, &c->normx[0], E * 4)) || (rc = dalloc(c, &c->normx[1], E * 4)))
+      (rc = dalloc(c, &c->normx[0], E * 4)) || (rc = dalloc(c, &c->normx[1], E * 4)) ||
+      (rc = dalloc(c, &c->attn_tag, (size_t)E * 8)) || (rc = dalloc(c, &c->qkv_tag, (size_t)(E + 2 * KV) * 8)))
     return bail(rc);
+  // tag 0xffffffff: no launch's (its layer field would be 255)
+  if (hipMemsetAsync(c->attn_tag, 0xff, (size_t)E * 8, c->stream) != hipSuccess ||
+      hipMemsetAsync(c->qkv_tag, 0xff, (size_t)(E + 2 * KV) * 8, c->stream) != hipSuccess)
+    return bail(C2H_ERR_HIP);
   size_t kv_bytes = (size_t)2 * D.n_layers * D.n_kv_heads * kv_slot(D.max_ctx) * D.head_dim * 4;
   if ((rc = dalloc(c, &c->kv, kv_bytes))) return bail(rc);
   if ((rc = dalloc(c, &c->token_ids, (size_t)D.max_ctx * 4))) return bail(rc);
@@ -1080,7 +1238,12 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
     {
       for (int form = 0; form <= ATT_FORM_CORE; ++form)
         if (hipFuncSetAttribute((const void*)attn_core_kernel(form), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)c->attn_lds) != hipSuccess)
+                                (int)c->attn_lds) != hipSuccess ||
+            hipFuncSetAttribute((const void*)attn_oproj_kernel(form), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)c->attn_lds) != hipSuccess ||
+            (attn_block_kernel(form) &&
+             hipFuncSetAttribute((const void*)attn_block_kernel(form), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)std::max(c->attn_lds, (size_t)chain_lds_floats(D.n_embd) * 4)) != hipSuccess))
           return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
       const void* pff[] = {(const void*)k_pf_gemm_f<MODE_BIAS>, (const void*)k_pf_gemm_f<MODE_RESID>,
                            (const void*)k_pf_gemm_q50<MODE_BIAS>, (const void*)k_pf_gemm_q50<MODE_RESID>};
@@ -1217,6 +1380,7 @@ int c2h_forward(c2h_ctx* c, int32_t token, int32_t pos, float* normx_out) {
     HIPCHK(c, hipMemcpyAsync(normx_out, c->normx[c->nx_cur], (size_t)c->desc.n_embd * 4, hipMemcpyDeviceToHost,
                              c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
+    return check_wait_flag(c);
   }
   return C2H_OK;
 }
@@ -1576,6 +1740,7 @@ int c2h_step(c2h_ctx* c, int32_t pos, float penalty, int32_t im_end, int32_t eos
   int rc = build_graphs(c);
   if (rc) return rc;
   if (pos < 0 || pos >= c->desc.max_ctx) return fail(c, C2H_ERR_RANGE, "pos %d outside [0, %d)", pos, c->desc.max_ctx);
+  if ((rc = check_wait_flag(c))) return rc;  // a previous forward's
   C2hState s;
   memset(&s, 0, sizeof(s));
   s.pos = pos;
@@ -1934,7 +2099,7 @@ int c2h_sync(c2h_ctx* c) {
   if (!c) return C2H_ERR_INVALID;
   HIPCHK(c, hipSetDevice(c->device));
   HIPCHK(c, hipStreamSynchronize(c->stream));
-  return C2H_OK;
+  return check_wait_flag(c);
 }
 
 int c2h_quantize_q8k(c2h_ctx* c, const float* x, int32_t cols, void* q8k_out) {

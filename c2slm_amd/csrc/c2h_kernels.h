@@ -19,7 +19,13 @@ struct C2hState {
   // head_dim 64: the RoPE row of pos (cos at [0, 32), sin at [32, 64)), so
   // that decode attention reads it with pos instead of after it
   float rope[64];
+  // forward count: the final RMSNorm of every forward advances it, and the
+  // tags of a launch's handover (k_attn_oproj) are epoch * 256 + layer.
+  // Last field: the host's state copies stop before it (kStatePushBytes),
+  // so it only ever moves forward.
+  uint32_t epoch;
 };
+constexpr size_t kStatePushBytes = offsetof(C2hState, epoch);
 
 // Q8_K row as the GEMVs keep it in LDS: quants packed four per dword, the
 // f32 scale and the sixteen 16-element sums widened to int32.
@@ -78,7 +84,7 @@ struct GemvJob {
   int rpw;       // rows per workgroup = floor(256 / (4*nb))
   int n_wg;      // workgroups of this job (grid row blockIdx.y = job)
   int mode;
-  int spare;     // (unused: named so that the fields load as one scalar batch)
+  int spare;     // k_attn_block: the job's offset in y_tag (else unused; named so the fields load as one batch)
   float* y;
   const float* bias;
   int32_t* isums;  // optional integer sums (Q4_K: 8 per row-block; Q6_K: 1)
@@ -127,6 +133,11 @@ struct GemvParams {
   // prologue into host-pinned memory (system scope) so that the host has
   // the token while the rest of the step runs (nullptr: none)
   int32_t* tok_out;
+  // k_attn_oproj's o-projection half: its input as {value, tag} words, and
+  // the flag a wait that runs out sets (host-pinned)
+  const uint64_t* x_tag;
+  int* wait_err;
+  uint64_t* y_tag;  // k_attn_block's q|k|v half: its outputs again as {value, tag} words (job offset in spare)
   int n_jobs;
   GemvJob jobs[MAX_JOBS];
 };
@@ -141,7 +152,7 @@ struct NormParams {
   float eps;
   int n;
   int n_lds;    // chain_lds_floats(n)
-  int out_sel;  // 1: write out_buf[state->nx_out]
+  int out_sel;  // 1: write out_buf[state->nx_out] (the forward's last launch: advances state->epoch)
   float* out;
   float* out_buf[2];
   C2hState* state;
@@ -209,6 +220,9 @@ struct AttnCoreParams {
   const float* k_norm;
   float eps;
   float* out;      // attention output [tokens][out_ld]
+  uint64_t* out_tag;  // k_attn_oproj: the output again as {value, tag} words
+  int n_attn_wg;      // k_attn_oproj: workgroups of the attention half
+  int* wait_err;      // k_attn_block: the flag a wait for q|k|v that runs out sets
   int q_ld, kv_ld, out_ld;
   int store_kv;    // 1: K/V of pos come from k/v and are stored by this launch
   float* kv;
@@ -407,6 +421,17 @@ __global__ void k_rmsnorm(NormParams P);
 template <int TIER>
 __global__ void k_attn_core(C2hState* st, float* kv, const float* qg, const float* kg, const float* vg, int dims,
                             int max_ctx, AttnCoreParams P);  // (P.state, P.kv, P.q, P.k, P.v, attn_dims, P.max_ctx)
+// k_attn_core's XCD-grouped grid (P.n_attn_wg workgroups) followed by the
+// o-projection's k_gemv_row<NB, PRO_QUANT, MODE_RESID> workgroups of G,
+// 256 threads each, one launch; G.x_tag = P.out_tag
+// qkv (3 W workgroups, W = xw >> 16), then k_attn_oproj's two parts, one
+// launch; Gq.y_tag = qkv_tag, Go.x_tag = P.out_tag
+template <int TIER, int NB>
+__global__ void k_attn_block(C2hState* st, float* kv, const float* xp, int xw, const uint64_t* qkv_tag, int dims,
+                             int max_ctx, AttnCoreParams P, GemvParams Gq, GemvParams Go);
+template <int TIER, int NB>
+__global__ void k_attn_oproj(C2hState* st, float* kv, const float* qg, const float* kg, const float* vg, int dims,
+                             int max_ctx, AttnCoreParams P, GemvParams G);
 // layer | n_layers << 8 | n_kv_heads << 16 | xcd_map << 23 | query heads per KV head << 24
 inline int attn_dims(const AttnCoreParams& A, int qpkv) {
   return A.layer | (A.n_layers << 8) | (A.n_kv_heads << 16) | ((A.xcd_map ? 1 : 0) << 23) | (qpkv << 24);

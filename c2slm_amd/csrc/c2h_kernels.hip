@@ -910,6 +910,42 @@ __device__ __forceinline__ float4 embed4(const WeightRef& emb, int n_vocab, int 
 
 // ------------------------------------------------------ GEMV (row kernel)
 
+// Four consecutive 8-byte {value, tag} words, polled until each carries
+// `tag` (agent-scope loads: the producers' stores of the same launch are
+// seen past the XCDs' L2s), then their values.  At most TAG_WAIT_POLLS
+// rounds: a lane that runs out sets *err (system scope, read by the host)
+// and returns what it last read.
+constexpr int TAG_WAIT_POLLS = 1 << 20;
+__device__ __forceinline__ float4 poll_tagged4(const uint64_t* src, uint32_t tag, int* err) {
+  uint64_t v0, v1, v2, v3;
+  bool ready = false;
+  for (int spin = 0; spin < TAG_WAIT_POLLS; ++spin) {
+    v0 = __hip_atomic_load(src + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    v1 = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    v2 = __hip_atomic_load(src + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    v3 = __hip_atomic_load(src + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ready = (uint32_t)(v0 >> 32) == tag && (uint32_t)(v1 >> 32) == tag && (uint32_t)(v2 >> 32) == tag &&
+            (uint32_t)(v3 >> 32) == tag;
+    if (ready) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (!ready) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  return make_float4(__uint_as_float((uint32_t)v0), __uint_as_float((uint32_t)v1), __uint_as_float((uint32_t)v2),
+                     __uint_as_float((uint32_t)v3));
+}
+__device__ __forceinline__ float poll_tagged1(const uint64_t* src, uint32_t tag, int* err) {
+  uint64_t v = 0;
+  bool ready = false;
+  for (int spin = 0; spin < TAG_WAIT_POLLS; ++spin) {
+    v = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ready = (uint32_t)(v >> 32) == tag;
+    if (ready) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (!ready) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  return __uint_as_float((uint32_t)v);
+}
+
 // A GEMV launch covers its jobs as grid rows: job blockIdx.y, workgroup
 // blockIdx.x of it.  The job's fields go through an empty asm together with
 // the launch's x, so they load in one scalar batch instead of a chain of
@@ -955,8 +991,20 @@ __device__ __forceinline__ void publish_token(const GemvParams& P, int tok) {
 // (t%(4*RPW))/4, quarter t%4, so the lanes of a 16-lane LDS access group
 // read the same block of the Q8_K row (broadcast, no bank conflicts).  The
 // fold runs per row in the reference's order.
-template <int NB, int PRO, int MODE>
-__global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(const float* __restrict__ xp, int n_xp, GemvParams P) {
+//
+// TAGX (PRO_QUANT only): x is the output of producers in the same launch,
+// 8-byte {value, tag} words at P.x_tag; each lane polls its four values
+// (agent-scope loads, s_sleep between rounds) until all carry `tag`, after
+// the weights, the job fields and the residual have been issued.  The wait
+// is bounded: a lane that runs out sets *P.wait_err (system scope) and goes
+// on with what it read.
+// TAGY (MODE_BIAS only): each output y[r] is also stored as a {value, tag}
+// word at P.y_tag[J.spare + r] for consumers in the same launch.
+template <int NB, int PRO, int MODE, bool TAGX, bool TAGY = false>
+__device__ __forceinline__ void gemv_row_body(const int bx, const int by, const float* __restrict__ xp, int n_xp,
+                                              const GemvParams& P, const uint32_t tag) {
+  static_assert(!TAGX || PRO == PRO_QUANT, "tagged input feeds the quantising prologue");
+  static_assert(!TAGY || MODE == MODE_BIAS, "tagged output from the bias epilogue");
   constexpr int NT = row_threads(NB, PRO, MODE);
   constexpr int NI = row_item_threads(NB, PRO, MODE);  // threads per matrix's items
   constexpr int NW = NT / 64;
@@ -977,7 +1025,7 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(const f
 
   // the job's fields: their scalar loads are issued first and waited for
   // after the input row's loads are out
-  GemvJob J = P.jobs[blockIdx.y];
+  GemvJob J = P.jobs[by];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   // ---- the input row's loads first: they need only xp and n_xp
@@ -995,13 +1043,13 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(const f
       for (int k = 0; k < SPEC_C / 4; ++k) xs[k] = x4[min(4 * lane + k, last4)];
     }
     xa[0] = load4(xp, n_xp);
-  } else if (!NORM) {
+  } else if (!NORM && !TAGX) {
 #pragma unroll
     for (int i = 0; i < BPW; ++i) xa[i] = reinterpret_cast<const float4*>(xp + min(wave + NW * i, NB - 1) * QK_K)[lane];
   }
   issue_fence();
   pin_job_rows(J, P);
-  if ((int)blockIdx.x >= J.n_wg) return;  // uniform: the launch's widest job sets the grid
+  if (bx >= J.n_wg) return;  // uniform: the launch's widest job sets the grid
   const int it = SPLIT ? (tid & (NI - 1)) : tid;  // item index within its matrix
   // 0: gate (w), 1: up (w2); wave-uniform, and scalar so that the type
   // tests on it branch on SCC, not per lane
@@ -1009,7 +1057,7 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(const f
   const int b = it / (4 * RPW);
   const int r_local = (it - b * 4 * RPW) >> 2;
   const int u = it & 3;
-  const int row0 = (int)blockIdx.x * RPW;
+  const int row0 = bx * RPW;
   const int row = row0 + r_local;
   const bool active = (b < NB) && (row < J.rows);
   const int row_c = min(row, J.rows - 1);
@@ -1034,10 +1082,14 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(const f
   // an absent bias reads x instead (a valid address) and is not added
   if (MODE == MODE_BIAS) yres = (J.bias ? J.bias : xp)[J.bias ? out_row : 0];
   issue_fence();
+  if constexpr (TAGX) {
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) xa[i] = poll_tagged4(P.x_tag + min(wave + NW * i, NB - 1) * QK_K + 4 * lane, tag, P.wait_err);
+  }
 
   // ---- prologue: the Q8_K input row in LDS
   if (NORM) {
-    if (PRO != PRO_NORM && blockIdx.x == 0 && blockIdx.y == 0) {  // layer 0 publishes the embedded token
+    if (PRO != PRO_NORM && bx == 0 && by == 0) {  // layer 0 publishes the embedded token
       if (4 * tid < n_xp) reinterpret_cast<float4*>(P.x_out)[tid] = xa[0];
       if (tid == 0) {
         const int pos = P.state->pos;
@@ -1087,12 +1139,21 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(const f
         const int n8 = J.rows - (J.rows % 8);
         J.y[r] = (r < n8) ? swiglu_poly(acc, up) : swiglu_tail(acc, up);
       } else if (MODE == MODE_BIAS) {
-        J.y[r] = J.bias ? acc + yres : acc;
+        const float yv = J.bias ? acc + yres : acc;
+        J.y[r] = yv;
+        if constexpr (TAGY)
+          __hip_atomic_store(&P.y_tag[J.spare + r], ((uint64_t)tag << 32) | __float_as_uint(yv), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
       } else {
         J.y[r] = yres + acc;
       }
     }
   }
+}
+
+template <int NB, int PRO, int MODE>
+__global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(const float* __restrict__ xp, int n_xp, GemvParams P) {
+  gemv_row_body<NB, PRO, MODE, false>((int)blockIdx.x, (int)blockIdx.y, xp, n_xp, P, 0u);
 }
 
 #define C2H_GEMV_ROW(NB_, PRO_, MODE_) \
@@ -1454,6 +1515,7 @@ __global__ void __launch_bounds__(512) k_rmsnorm(NormParams P) {
   const float inv = rms_inv4(x, P.n, P.eps, sq, &inv_slot);
   float* out = P.out_sel ? P.out_buf[nx_out] : P.out;
   if (4 * (int)threadIdx.x < P.n) reinterpret_cast<float4*>(out)[threadIdx.x] = norm4(x, inv, w);
+  if (P.out_sel && threadIdx.x == 0) P.state->epoch = P.state->epoch + 1u;  // no other launch of the forward runs
   if (P.advance) {
     __syncthreads();  // every thread has read the state
     C2hState* st = P.state;
@@ -1687,10 +1749,20 @@ struct VStage {
   f32x4_t r[PER];
 };
 
-template <int TIER>
-__global__ void __launch_bounds__(256)
-    k_attn_core(C2hState* __restrict__ st, float* __restrict__ kv, const float* __restrict__ qg,
-                const float* __restrict__ kg, const float* __restrict__ vg, int dims, int max_ctx, AttnCoreParams P) {
+// The body of k_attn_core for workgroup (bx, by, bz) of its grid.  TAG:
+// the output is also stored as 8-byte {value, tag} words in P.out_tag for
+// the consumers of the same launch (k_attn_oproj), tag = the state's epoch
+// * 256 + layer.  TAGIN (with TAG): q|k|v come from producers of the same
+// launch as {value, tag} words at in_tag (q of head h at h*64, k of group g
+// at (n_heads + g)*64, v at (n_heads + n_kv + g)*64), polled after the K/V
+// rows and the position have been issued.
+template <int TIER, bool TAG, bool TAGIN = false>
+__device__ __forceinline__ void attn_core_body(const int bx, const int by, const int bz, C2hState* __restrict__ st,
+                                               float* __restrict__ kv, const float* __restrict__ qg,
+                                               const float* __restrict__ kg, const float* __restrict__ vg, int dims,
+                                               int max_ctx, const AttnCoreParams& P,
+                                               const uint64_t* __restrict__ in_tag = nullptr) {
+  static_assert(!TAGIN || (TAG && TIER != ATT_TIER_ANY), "tagged input: the decode tiers of the fused launch");
   constexpr int HD = 64;
   constexpr bool ANY = (TIER == ATT_TIER_ANY);
   static_assert(ANY || (TIER % 32 == 0 && TIER <= ATT_KPF), "a tier reads whole batches of K and V rows");
@@ -1714,22 +1786,25 @@ __global__ void __launch_bounds__(256)
   const int qpkv = (dims >> 24) & 0xff;
   // grid (query heads per KV head, KV heads, query tokens of the batch), or
   // the XCD-grouped order of xcd_map (at most ATT_XCDS KV heads)
-  int g = (int)blockIdx.y, hx = (int)blockIdx.x;
+  int g = by, hx = bx;
   if ((dims >> 23) & 1) {
-    g = (int)blockIdx.x % ATT_XCDS;
-    hx = (int)blockIdx.x / ATT_XCDS;
+    g = bx % ATT_XCDS;
+    hx = bx / ATT_XCDS;
     if (g >= n_kv) return;  // uniform: a spare workgroup of the grid
   }
   const int h = g * qpkv + hx;
   // query token of the batch (the tiers serve decode: one token, row 0)
-  const int ti = ANY ? P.tok0 + (int)blockIdx.z : 0;
+  const int ti = ANY ? P.tok0 + bz : 0;
   // this head's q and the group's k, v: thread t < 192 holds element t%64
   // of q_h (t < 64), k_g, v_g.  Issued before the position is read.
   const int bm = min(tid >> 6, 2);
-  const float* qsrc = qg + (ANY ? (size_t)ti * P.q_ld : 0) + h * HD;
-  const float* ksrc = kg + (ANY ? (size_t)ti * P.kv_ld : 0) + g * HD;
-  const float* vsrc = vg + (ANY ? (size_t)ti * P.kv_ld : 0) + g * HD;
-  const float own = ((bm == 0) ? qsrc : ((bm == 1) ? ksrc : vsrc))[tid & 63];
+  float own = 0.0f;
+  if constexpr (!TAGIN) {
+    const float* qsrc = qg + (ANY ? (size_t)ti * P.q_ld : 0) + h * HD;
+    const float* ksrc = kg + (ANY ? (size_t)ti * P.kv_ld : 0) + g * HD;
+    const float* vsrc = vg + (ANY ? (size_t)ti * P.kv_ld : 0) + g * HD;
+    own = ((bm == 0) ? qsrc : ((bm == 1) ? ksrc : vsrc))[tid & 63];
+  }
   // the position, and for a tier its RoPE row from the state: issued now,
   // first used (waited for) after a tier's K/V loads are issued
   // a vector load (a VGPR offset): as a scalar load its wait would also
@@ -1737,6 +1812,9 @@ __global__ void __launch_bounds__(256)
   int zero_v = 0;
   asm volatile("" : "+v"(zero_v));
   int pos_state = (&st->pos)[zero_v];
+  // (the handover tag: used, so waited for, only after the K/V rows are issued)
+  int epoch_state = 0;
+  if constexpr (TAG) epoch_state = (&st->epoch)[zero_v];
   float rcos = 0.0f, rsin = 0.0f;
   if constexpr (!ANY) {
     rcos = st->rope[tid & 31];
@@ -1799,6 +1877,12 @@ __global__ void __launch_bounds__(256)
     issue_fence();
   }
 
+  if constexpr (TAGIN) {
+    const int n_h = qpkv * n_kv;
+    const int slot = (bm == 0) ? h : ((bm == 1) ? n_h + g : n_h + n_kv + g);
+    const uint32_t tag = (uint32_t)__builtin_amdgcn_readfirstlane(epoch_state) * 256u + (uint32_t)layer;
+    own = poll_tagged1(in_tag + slot * HD + (tid & 63), tag, P.wait_err);
+  }
   // every thread stores (threads 192.. repeat v_g): a store under a branch
   // would let the compiler sink the load of own into it, behind the K/V loads
   qkv_s[bm][tid & 63] = own;
@@ -1985,7 +2069,20 @@ __global__ void __launch_bounds__(256)
   if (tid < HD) {
     acc = __builtin_fmaf(sc[pos], v_s[d], acc);
     P.out[(size_t)ti * P.out_ld + h * HD + d] = acc;
+    if constexpr (TAG) {
+      const uint32_t tag = (uint32_t)__builtin_amdgcn_readfirstlane(epoch_state) * 256u + (uint32_t)layer;
+      __hip_atomic_store(&P.out_tag[h * HD + d], ((uint64_t)tag << 32) | __float_as_uint(acc), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
+}
+
+template <int TIER>
+__global__ void __launch_bounds__(256)
+    k_attn_core(C2hState* __restrict__ st, float* __restrict__ kv, const float* __restrict__ qg,
+                const float* __restrict__ kg, const float* __restrict__ vg, int dims, int max_ctx, AttnCoreParams P) {
+  attn_core_body<TIER, false>((int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, st, kv, qg, kg, vg, dims, max_ctx,
+                              P);
 }
 template __global__ void k_attn_core<ATT_TIER_32>(C2hState*, float*, const float*, const float*, const float*, int, int,
                                                    AttnCoreParams);
@@ -1999,6 +2096,78 @@ template __global__ void k_attn_core<ATT_TIER_256>(C2hState*, float*, const floa
                                                    AttnCoreParams);
 template __global__ void k_attn_core<ATT_TIER_ANY>(C2hState*, float*, const float*, const float*, const float*, int, int,
                                                    AttnCoreParams);
+
+// Attention and the o-projection of one layer in one launch
+// (engine/forward.go:94-118): workgroups [0, P.n_attn_wg) run k_attn_core's
+// XCD-grouped grid and store the output tagged as well; the workgroups past
+// them (dispatched after them) run k_gemv_row<NB, PRO_QUANT, MODE_RESID>'s
+// workgroups of the o-projection, whose weight, job and residual loads are
+// issued before they wait for the tagged output.  The handover replaces a
+// kernel boundary; the arithmetic of both halves is unchanged.
+template <int TIER, int NB>
+__global__ void __launch_bounds__(256)
+    k_attn_oproj(C2hState* __restrict__ st, float* __restrict__ kv, const float* __restrict__ qg,
+                 const float* __restrict__ kg, const float* __restrict__ vg, int dims, int max_ctx, AttnCoreParams P,
+                 GemvParams G) {
+  static_assert(row_threads(NB, PRO_QUANT, MODE_RESID) == 256, "both halves run 256-thread workgroups");
+  const int n_attn = P.n_attn_wg;
+  if ((int)blockIdx.x < n_attn) {
+    attn_core_body<TIER, true>((int)blockIdx.x, 0, 0, st, kv, qg, kg, vg, dims, max_ctx, P);
+    return;
+  }
+  const uint32_t tag = (uint32_t)st->epoch * 256u + (uint32_t)(dims & 0xff);
+  gemv_row_body<NB, PRO_QUANT, MODE_RESID, true>((int)blockIdx.x - n_attn, 0, nullptr, 0, G, tag);
+}
+// qkv, attention and the o-projection of one layer past layer 0 in one
+// launch (engine/forward.go:65-118): workgroups [0, 3 W) run
+// k_gemv_row<NB, PRO_NORM, MODE_BIAS>'s (job b / W, workgroup b % W, W = the
+// widest of the q/k/v jobs' workgroup counts, xw >> 16) and store q|k|v
+// tagged as well (Gq.y_tag = qkv_tag); the next P.n_attn_wg run
+// k_attn_core's XCD-grouped grid on them (polled after the K/V rows are
+// issued); the rest run the o-projection of Go on the tagged attention
+// output.  x, its length (xw & 0xffff) and the tagged q|k|v arrive as
+// preloaded kernel arguments with the state and the KV cache.
+template <int TIER, int NB>
+__global__ void __launch_bounds__(256)
+    k_attn_block(C2hState* __restrict__ st, float* __restrict__ kv, const float* __restrict__ xp, int xw,
+                 const uint64_t* __restrict__ qkv_tag, int dims, int max_ctx, AttnCoreParams P, GemvParams Gq,
+                 GemvParams Go) {
+  static_assert(row_threads(NB, PRO_NORM, MODE_BIAS) == 256 && row_threads(NB, PRO_QUANT, MODE_RESID) == 256,
+                "every part runs 256-thread workgroups");
+  const int b = (int)blockIdx.x;
+  const int w = xw >> 16, nq = 3 * w;
+  if (b < nq) {
+    const int by = b / w;
+    const uint32_t tag = (uint32_t)st->epoch * 256u + (uint32_t)(dims & 0xff);
+    gemv_row_body<NB, PRO_NORM, MODE_BIAS, false, true>(b - by * w, by, xp, xw & 0xffff, Gq, tag);
+    return;
+  }
+  const int n_attn = P.n_attn_wg;
+  if (b < nq + n_attn) {
+    attn_core_body<TIER, true, true>(b - nq, 0, 0, st, kv, nullptr, nullptr, nullptr, dims, max_ctx, P, qkv_tag);
+    return;
+  }
+  const uint32_t tag = (uint32_t)st->epoch * 256u + (uint32_t)(dims & 0xff);
+  gemv_row_body<NB, PRO_QUANT, MODE_RESID, true>(b - nq - n_attn, 0, nullptr, 0, Go, tag);
+}
+#define C2H_ATTN_BLOCK(TIER_, NB_)                                                                                 \
+  template __global__ void k_attn_block<TIER_, NB_>(C2hState*, float*, const float*, int, const uint64_t*, int, int, \
+                                                    AttnCoreParams, GemvParams, GemvParams);
+C2H_ATTN_BLOCK(ATT_TIER_32, 3)
+C2H_ATTN_BLOCK(ATT_TIER_64, 3)
+C2H_ATTN_BLOCK(ATT_TIER_96, 3)
+C2H_ATTN_BLOCK(ATT_TIER_128, 3)
+C2H_ATTN_BLOCK(ATT_TIER_256, 3)
+
+#define C2H_ATTN_OPROJ(TIER_, NB_)                                                                                  \
+  template __global__ void k_attn_oproj<TIER_, NB_>(C2hState*, float*, const float*, const float*, const float*, int, \
+                                                    int, AttnCoreParams, GemvParams);
+C2H_ATTN_OPROJ(ATT_TIER_32, 3)
+C2H_ATTN_OPROJ(ATT_TIER_64, 3)
+C2H_ATTN_OPROJ(ATT_TIER_96, 3)
+C2H_ATTN_OPROJ(ATT_TIER_128, 3)
+C2H_ATTN_OPROJ(ATT_TIER_256, 3)
+C2H_ATTN_OPROJ(ATT_TIER_ANY, 3)
 
 // ------------------------------------------------ attention, head_dim 128
 
