@@ -724,7 +724,7 @@ void enqueue_attn(c2h_ctx* c, int l, int form) {
   }
 }
 
-// The k_attn_block instance of a decode tier (nullptr past the tiers).
+// The k_attn_block instance of a core form.
 decltype(&k_attn_block<ATT_TIER_32, 3>) attn_block_kernel(int form) {
   switch (form) {
     case ATT_FORM_32: return k_attn_block<ATT_TIER_32, 3>;
@@ -732,7 +732,7 @@ decltype(&k_attn_block<ATT_TIER_32, 3>) attn_block_kernel(int form) {
     case ATT_FORM_96: return k_attn_block<ATT_TIER_96, 3>;
     case ATT_FORM_128: return k_attn_block<ATT_TIER_128, 3>;
     case ATT_FORM_256: return k_attn_block<ATT_TIER_256, 3>;
-    default: return nullptr;
+    default: return k_attn_block<ATT_TIER_ANY, 3>;
   }
 }
 
@@ -758,11 +758,10 @@ bool fuse_attn_oproj(const c2h_ctx* c, int l, int form) {
 }
 
 // Whether layer l runs qkv in that launch too (k_attn_block): past layer 0
-// (whose qkv embeds the token), at the decode tiers, with K-quant q|k|v.
+// (whose qkv embeds the token), with K-quant q|k|v.
 bool fuse_attn_block(const c2h_ctx* c, int l, int form) {
   const Layer& L = c->layers[l];
-  return l > 0 && c->fuse_qkv && fuse_attn_oproj(c, l, form) && attn_block_kernel(form) != nullptr &&
-         !float_input(L.wq.type) &&
+  return l > 0 && c->fuse_qkv && fuse_attn_oproj(c, l, form) && !float_input(L.wq.type) &&
          !float_input(L.wk.type) && !float_input(L.wv.type);
 }
 
@@ -1241,9 +1240,8 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
                                 (int)c->attn_lds) != hipSuccess ||
             hipFuncSetAttribute((const void*)attn_oproj_kernel(form), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)c->attn_lds) != hipSuccess ||
-            (attn_block_kernel(form) &&
-             hipFuncSetAttribute((const void*)attn_block_kernel(form), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 (int)std::max(c->attn_lds, (size_t)chain_lds_floats(D.n_embd) * 4)) != hipSuccess))
+            hipFuncSetAttribute((const void*)attn_block_kernel(form), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)std::max(c->attn_lds, (size_t)chain_lds_floats(D.n_embd) * 4)) != hipSuccess)
           return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
       const void* pff[] = {(const void*)k_pf_gemm_f<MODE_BIAS>, (const void*)k_pf_gemm_f<MODE_RESID>,
                            (const void*)k_pf_gemm_q50<MODE_BIAS>, (const void*)k_pf_gemm_q50<MODE_RESID>};

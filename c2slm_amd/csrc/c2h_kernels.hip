@@ -1762,7 +1762,7 @@ __device__ __forceinline__ void attn_core_body(const int bx, const int by, const
                                                const float* __restrict__ kg, const float* __restrict__ vg, int dims,
                                                int max_ctx, const AttnCoreParams& P,
                                                const uint64_t* __restrict__ in_tag = nullptr) {
-  static_assert(!TAGIN || (TAG && TIER != ATT_TIER_ANY), "tagged input: the decode tiers of the fused launch");
+  static_assert(!TAGIN || TAG, "tagged input: the fused launch's attention also tags its output");
   constexpr int HD = 64;
   constexpr bool ANY = (TIER == ATT_TIER_ANY);
   static_assert(ANY || (TIER % 32 == 0 && TIER <= ATT_KPF), "a tier reads whole batches of K and V rows");
@@ -2158,6 +2158,7 @@ C2H_ATTN_BLOCK(ATT_TIER_64, 3)
 C2H_ATTN_BLOCK(ATT_TIER_96, 3)
 C2H_ATTN_BLOCK(ATT_TIER_128, 3)
 C2H_ATTN_BLOCK(ATT_TIER_256, 3)
+C2H_ATTN_BLOCK(ATT_TIER_ANY, 3)
 
 #define C2H_ATTN_OPROJ(TIER_, NB_)                                                                                  \
   template __global__ void k_attn_oproj<TIER_, NB_>(C2hState*, float*, const float*, const float*, const float*, int, \
