@@ -156,7 +156,7 @@ def kernel_bytes(gf, desc, T: float) -> dict:
     dn = avg(lambda i: w(f"blk.{i}.ffn_down.weight"))
     out = tm.get("output.weight", tm["token_embd.weight"])
     vocab_w = G.row_bytes(out.ggml_type, int(out.dims[0])) * int(out.dims[1])
-    return {
+    b = {
         "qkv": int(q + 4 * (E + E + 2 * (E + 2 * KVd))),          # + x, norm w, bias, q|k|v out
         "attn": int(4 * 2 * KVd * T + 4 * (2 * (E + 2 * KVd) + E)),  # K,V rows + q|k|v in, K/V store, out
         "attn_out": int(o + 4 * (E + 2 * E)),                      # + attn in, X read and written
@@ -165,6 +165,29 @@ def kernel_bytes(gf, desc, T: float) -> dict:
         "final_norm": int(4 * 3 * E),
         "vocab": int(vocab_w + 4 * E + 4 * 64 + 4),                # + normX, window ids, chosen id
     }
+    # the fused launches: the sum of their parts (the handed-over q|k|v and
+    # attention output counted once written, once read, as between kernels)
+    b["attn_block"] = b["qkv"] + b["attn"] + b["attn_out"]
+    b["attn_oproj"] = b["attn"] + b["attn_out"]
+    return b
+
+
+def step_launches(n_layers: int) -> dict:
+    """Launches of each decode kernel per step.  The Qwen2.5-0.5B shape has
+    the fused attention launches (k_attn_block on layers past 0, qkv then
+    k_attn_oproj on layer 0) unless C2H_NO_FUSE selects the separate forms
+    (=1: every kernel on its own; =qkv: qkv on its own, attention and the
+    o-projection fused)."""
+    nf = os.environ.get("C2H_NO_FUSE", "")
+    L = n_layers
+    n = dict(qkv=L, attn=0, attn_out=0, attn_block=0, attn_oproj=0, ffn_in=L, ffn_out=L, final_norm=1, vocab=1)
+    if nf == "1":
+        n.update(attn=L, attn_out=L)
+    elif nf == "qkv":
+        n.update(attn_oproj=L)
+    else:
+        n.update(qkv=1, attn_oproj=1, attn_block=L - 1)
+    return n
 
 
 # The roofline line's kernel: the decode layer kernel with the most bytes per
@@ -175,7 +198,7 @@ ROOFLINE_KERNEL = "ffn_in"
 KERNEL_NAMES = {"qkv": "k_gemv_row<3, PRO_NORM, MODE_BIAS>", "attn": "k_attn_core",
                 "attn_out": "k_gemv_row<3, PRO_QUANT, MODE_RESID>", "ffn_in": "k_gemv_row<3, PRO_NORM, MODE_SWIGLU>",
                 "ffn_out": "k_gemv_row<19, PRO_QUANT, MODE_RESID>", "final_norm": "k_rmsnorm",
-                "vocab": "k_vocab<28>"}
+                "vocab": "k_vocab<28>", "attn_block": "k_attn_block<TIER, 3>", "attn_oproj": "k_attn_oproj<TIER, 3>"}
 
 
 def decode_kernels(ctx, gf, desc, vocab_ms, step_ms, T, iters: int = 96):
@@ -186,14 +209,18 @@ def decode_kernels(ctx, gf, desc, vocab_ms, step_ms, T, iters: int = 96):
     the same launches records per-dispatch durations within a few per cent
     of it), `us_graph` the same launches captured in one graph (the figure a
     step's replay sees); its algorithmic bytes and GB/s at `us`, and its
-    share of the step at `us_graph`."""
+    share of the step at `us_graph`.  The separate attention kernels are
+    timed too where the step runs them fused (launches_per_step 0)."""
+    from c2slm_amd import _lib as H
     nbytes = kernel_bytes(gf, desc, T)
-    per_step = {k: desc.n_layers for k in ("qkv", "attn", "attn_out", "ffn_in", "ffn_out")}
-    per_step.update(final_norm=1, vocab=1)
+    per_step = step_launches(desc.n_layers)
     out = {}
     for k in ctx.KERNELS:
-        us = ctx.time_layer_kernel(k, iters) * 1e3
-        usg = ctx.time_layer_kernel(k, iters, captured=True) * 1e3
+        try:
+            us = ctx.time_layer_kernel(k, iters) * 1e3
+            usg = ctx.time_layer_kernel(k, iters, captured=True) * 1e3
+        except H.C2hError:  # a fused launch this model or C2H_NO_FUSE does not run
+            continue
         out[k] = {"us": round(us, 3), "us_graph": round(usg, 3)}
     out["vocab"] = {"us": round(vocab_ms * 1e3, 3), "us_graph": round(vocab_ms * 1e3, 3)}
     for k, v in out.items():
@@ -529,8 +556,13 @@ def main():
         for p in range(PROMPT_LEN, kpos):
             ctx.step(p, PENALTY, im_end, eos)
         ctx.sync()
-        out = {k: [round(ctx.time_layer_kernel(k, args.kernel_iters, captured=g) * 1e3, 3) for g in (False, True)]
-               for k in ctx.KERNELS}
+        out = {}
+        for k in ctx.KERNELS:
+            try:
+                out[k] = [round(ctx.time_layer_kernel(k, args.kernel_iters, captured=g) * 1e3, 3)
+                          for g in (False, True)]
+            except H.C2hError:  # a fused launch this run does not have
+                pass
         out["attended_positions"] = ctx.seq_len + 1
         if args.copy_calib_mib:
             copy_calibration(ctx, args.copy_calib_mib)
@@ -604,8 +636,10 @@ def main():
     vocab_ms = ctx.time_vocab(args.vocab_iters, pos, in_step=2)
     # every decode kernel, at the next position (attending pos + 1)
     kern = decode_kernels(ctx, gf, desc, vocab_ms, ms_per_step, pos + 1, args.kernel_iters)
-    step_bytes = sum(v["bytes"] * v["launches_per_step"] for k, v in kern.items() if k != "attn")
-    step_bytes += desc.n_layers * kernel_bytes(gf, desc, t_avg)["attn"]
+    # a step's algorithmic bytes, however its kernels are grouped into launches
+    kb = kernel_bytes(gf, desc, t_avg)
+    step_bytes = (desc.n_layers * sum(kb[k] for k in ("qkv", "attn", "attn_out", "ffn_in", "ffn_out"))
+                  + kb["final_norm"] + kb["vocab"])
 
     # device-fed steps at the host loop's positions, from the same state: the
     # prompt forwarded again and the same warm-up steps on the host, then

@@ -258,7 +258,8 @@ class Ctx:
         self._chk(lib().c2h_time_steps(self.h, pos, iters, penalty, im_end, eos, C.byref(ms)))
         return ms.value
 
-    KERNELS = ("qkv", "attn", "attn_out", "ffn_in", "ffn_out", "final_norm")  # C2H_KERNEL_*
+    KERNELS = ("qkv", "attn", "attn_out", "ffn_in", "ffn_out", "final_norm", "attn_block",
+               "attn_oproj")  # C2H_KERNEL_*
 
     def time_layer_kernel(self, kernel: str, iters: int, captured: bool = False) -> float:
         """ms per launch of one decoder-layer kernel (c2h_time_layer_kernel):

@@ -2573,7 +2573,7 @@ int c2h_time_steps(c2h_ctx* c, int32_t pos, int32_t iters, float penalty, int32_
 
 
 int c2h_time_layer_kernel(c2h_ctx* c, int32_t kernel, int32_t iters, int32_t captured, float* ms) {
-  if (!c || !ms || iters <= 0 || iters > 100000 || kernel < 0 || kernel > C2H_KERNEL_FINAL_NORM) return C2H_ERR_INVALID;
+  if (!c || !ms || iters <= 0 || iters > 100000 || kernel < 0 || kernel > C2H_KERNEL_ATTN_OPROJ) return C2H_ERR_INVALID;
   HIPCHK(c, hipSetDevice(c->device));
   int rc = build_graphs(c);
   if (rc) return rc;
@@ -2595,6 +2595,10 @@ int c2h_time_layer_kernel(c2h_ctx* c, int32_t kernel, int32_t iters, int32_t cap
   s.nx_out = c->nx_cur ^ 1;
   if ((rc = push_state(c, s))) return rc;
   const int form = attn_form(c, pos + 1);
+  // the fused launches exist where layer 1's would run (the timing runs them on every layer)
+  if ((kernel == C2H_KERNEL_ATTN_BLOCK || kernel == C2H_KERNEL_ATTN_OPROJ) &&
+      !(D.n_layers > 1 && fuse_attn_block(c, 1, form)))
+    return fail(c, C2H_ERR_UNSUPPORTED, "no fused attention launch for this model or position");
   // the residual kernels update X and the final norm writes normX[nx_out]:
   // both are restored afterwards
   float* saved = nullptr;
@@ -2609,6 +2613,8 @@ int c2h_time_layer_kernel(c2h_ctx* c, int32_t kernel, int32_t iters, int32_t cap
       case C2H_KERNEL_ATTN_OUT: enqueue_attn_out(c, l); break;
       case C2H_KERNEL_FFN_IN: enqueue_ffn_in(c, l); break;
       case C2H_KERNEL_FFN_OUT: enqueue_ffn_out(c, l); break;
+      case C2H_KERNEL_ATTN_BLOCK: enqueue_attn_block(c, l, form); break;
+      case C2H_KERNEL_ATTN_OPROJ: enqueue_attn_oproj(c, l, form); break;
       default: enqueue_final_norm(c); break;
     }
   };

@@ -318,6 +318,11 @@ int c2h_check_rms_scale(c2h_ctx* ctx, uint32_t lo, uint64_t hi, uint64_t* mismat
 #define C2H_KERNEL_FFN_IN 3     /* RMSNorm + Q8_K + gate|up GEMV + SwiGLU */
 #define C2H_KERNEL_FFN_OUT 4    /* Q8_K(h) + down GEMV + residual */
 #define C2H_KERNEL_FINAL_NORM 5 /* the final RMSNorm */
+/* The launches a decode step runs where the model has their instances
+ * (head_dim 64, K-quant projections, rows of 3 super-blocks; C2H_ERR_UNSUPPORTED
+ * otherwise): */
+#define C2H_KERNEL_ATTN_BLOCK 6 /* QKV + ATTN + ATTN_OUT in one launch (layers past 0) */
+#define C2H_KERNEL_ATTN_OPROJ 7 /* ATTN + ATTN_OUT in one launch (layer 0) */
 
 /* Measurement aid with no counterpart in the reference: average device time
  * (ms) of one decoder-layer kernel, `iters` launches back to back on the
