@@ -413,13 +413,15 @@ def real_formats(tmpdir, im_end, eos, steps: int = 64):
             "prefill_512_ms": pf["ms"], "prefill_512_tok_s": pf["tok_s"]}
 
 
-def qwen3_decode(tmpdir, im_end, eos, steps: int = 64):
+def qwen3_decode(tmpdir, im_end, eos, steps: int = 64, device_fed_only: bool = False):
     """The Qwen3-1.7B shape (28 layers, hidden 2048, 16/8 heads of 128, FFN
     6144, per-head QK-norm, tied Q8_0 embedding; Q4_K / Q6_K projections),
     random-init: a 32-token prompt (one forward per token at head_dim 128),
     then greedy steps timed on the host around synchronous c2h_step calls,
     as the main line, and device-fed (c2h_time_steps); algorithmic bytes of
-    a step at the mean attended position."""
+    a step at the mean attended position.  device_fed_only: the warm-up and
+    timed steps fed on the device only (graph replays without c2h_step, the
+    form a rocprofv3 kernel trace runs through)."""
     from c2slm_amd import _lib as H
     from c2slm_amd import gguf as G
     path = os.path.join(tmpdir, "qwen3_1_7b_synth.gguf")
@@ -432,6 +434,13 @@ def qwen3_decode(tmpdir, im_end, eos, steps: int = 64):
     ctx.set_token_ids(0, prompt)
     ctx.prefill(prompt, 0, want_normx=False)
     pos = PROMPT_LEN
+    if device_fed_only:
+        fed_ms = ctx.time_steps(pos, 8 + steps, PENALTY, im_end, eos)
+        ctx.close()
+        del gf
+        os.remove(path)
+        return {"shape": "Qwen3-1.7B", "positions": [pos, pos + 8 + steps - 1],
+                "device_fed_ms_per_step": round(fed_ms, 4), "device_fed_tok_s": round(1000.0 / fed_ms, 1)}
     for _ in range(8):
         ctx.step(pos, PENALTY, im_end, eos)
         pos += 1
@@ -480,7 +489,7 @@ def main():
                     help="with --only kernels: greedy steps after the prompt up to this position, so attention "
                          "covers pos+1 positions (default: the decode line's last position, prompt + warmup + steps)")
     ap.add_argument("--only", choices=["prefill", "long", "float-dots", "real-formats", "vocab", "microbench",
-                                       "kernels", "qwen3", "roofline", "wait", "steps"],
+                                       "kernels", "qwen3", "qwen3-steps", "roofline", "wait", "steps"],
                     default=None,
                     help="run just the prefill reps or just the long-context decode (profiler runs); "
                          "prints their JSON object, not the bench line")
@@ -516,9 +525,10 @@ def main():
         os.rmdir(rdir)
         cleanup()
         return
-    if args.only == "qwen3":
+    if args.only in ("qwen3", "qwen3-steps"):
         rdir = tempfile.mkdtemp(prefix="c2slm_bench_")
-        print(json.dumps({"qwen3_1_7b_decode": qwen3_decode(rdir, im_end, eos)}))
+        print(json.dumps({"qwen3_1_7b_decode": qwen3_decode(rdir, im_end, eos,
+                                                            device_fed_only=args.only == "qwen3-steps")}))
         os.rmdir(rdir)
         cleanup()
         return

@@ -397,15 +397,15 @@ __device__ __forceinline__ void pad_chain(float* a, int n) {
   if (threadIdx.x < 16 && p < ((n + 15) & ~15)) a[p] = -0.0f;
 }
 
-// n <= 1024 values, lane l holding [16l, 16l+16) in v (+0 past n: +0 adds
+// n <= 64 C values, lane l holding [C l, C l + C) in v (+0 past n: +0 adds
 // are exact no-ops, the sums being >= +0 or NaN).  tail(c, E): the rest of
 // the chain in order from chunk c, E the exact start of chunk c (after
 // SPEC_ROUNDS rounds without a verified total).
-template <class Tail>
-__device__ __forceinline__ float seq_sum_v(const float (&v)[SPEC_C], int n, Tail tail) {
+template <int C, class Tail>
+__device__ __forceinline__ float seq_sum_v(const float (&v)[C], int n, Tail tail) {
   float cs = 0.0f;
 #pragma unroll
-  for (int k = 0; k < SPEC_C; ++k) cs = cs + v[k];
+  for (int k = 0; k < C; ++k) cs = cs + v[k];
   float S = pin_full_wave(wave_shift_up(wave_incl_scan(cs)));
   float total;
   if (n <= WIN_MIN_N) {  // a few chunks: plain rounds are shorter
@@ -413,7 +413,7 @@ __device__ __forceinline__ float seq_sum_v(const float (&v)[SPEC_C], int n, Tail
     for (int round = 0; round < SPEC_ROUNDS; ++round) {
       float R = S;
 #pragma unroll
-      for (int k = 0; k < SPEC_C; ++k) R = R + v[k];
+      for (int k = 0; k < C; ++k) R = R + v[k];
       if (spec_round(S, R, m, total)) return total;
     }
     return tail(m + 1, lane_value(S, m + 1));
@@ -424,7 +424,7 @@ __device__ __forceinline__ float seq_sum_v(const float (&v)[SPEC_C], int n, Tail
     int m = -1;
     float R = S;
 #pragma unroll
-    for (int k = 0; k < SPEC_C; ++k) R = R + v[k];
+    for (int k = 0; k < C; ++k) R = R + v[k];
     if (spec_round(S, R, m, total)) return total;
   }
   int f = 0;
@@ -433,7 +433,7 @@ __device__ __forceinline__ float seq_sum_v(const float (&v)[SPEC_C], int n, Tail
     const float u = __int_as_float(__float_as_int(S) + 1) - S;  // S >= +0: the ulp above S
     float Rm = S - u, R0 = S, Rp = S + u;
 #pragma unroll
-    for (int k = 0; k < SPEC_C; ++k) {
+    for (int k = 0; k < C; ++k) {
       Rm = Rm + v[k];
       R0 = R0 + v[k];
       Rp = Rp + v[k];
@@ -443,13 +443,14 @@ __device__ __forceinline__ float seq_sum_v(const float (&v)[SPEC_C], int n, Tail
   return tail(f, E);
 }
 
-// The same over values in LDS: a readable up to round_up(n, 16).
+// The same over values in LDS, n <= 64 C: a readable up to round_up(n, C).
+template <int C = SPEC_C>
 __device__ __forceinline__ float seq_sum_wave(const float* a, int n) {
-  const int base = (threadIdx.x & 63) * SPEC_C;
-  float v[SPEC_C];
-  const float4* a4 = reinterpret_cast<const float4*>(a + min(base, (n - 1) & ~(SPEC_C - 1)));
+  const int base = (threadIdx.x & 63) * C;
+  float v[C];
+  const float4* a4 = reinterpret_cast<const float4*>(a + min(base, (n - 1) & ~(C - 1)));
 #pragma unroll
-  for (int k = 0; k < SPEC_C / 4; ++k) {
+  for (int k = 0; k < C / 4; ++k) {
     const float4 t = a4[k];
     v[4 * k + 0] = t.x;
     v[4 * k + 1] = t.y;
@@ -457,9 +458,9 @@ __device__ __forceinline__ float seq_sum_wave(const float* a, int n) {
     v[4 * k + 3] = t.w;
   }
 #pragma unroll
-  for (int k = 0; k < SPEC_C; ++k) v[k] = (base + k < n) ? v[k] : 0.0f;
+  for (int k = 0; k < C; ++k) v[k] = (base + k < n) ? v[k] : 0.0f;
   // the rest in order from the last exact start, reads issued 16 ahead
-  return seq_sum_v(v, n, [&](int c, float E) { return chunk_chain(a, c * SPEC_C, n, E); });
+  return seq_sum_v<C>(v, n, [&](int c, float E) { return chunk_chain(a, c * C, n, E); });
 }
 
 // The same exact sequential sum for any n >= 1 (softmax over long contexts):
@@ -522,7 +523,8 @@ __device__ __forceinline__ float rms_inv4(const float4& x, int n, float eps, flo
   if (4 * tid < n) reinterpret_cast<float4*>(sq)[tid] = make_float4(x.x * x.x, x.y * x.y, x.z * x.z, x.w * x.w);
   __syncthreads();
   if (tid < 64) {
-    const float s = (n <= 64 * SPEC_C) ? seq_sum_wave(sq, n) : seq_sum_wave_n(sq, n);
+    // up to 1024 values 16 per lane, up to 2048 (the widest row) 32 per lane
+    const float s = (n <= 64 * SPEC_C) ? seq_sum_wave(sq, n) : seq_sum_wave<2 * SPEC_C>(sq, n);
     if (tid == 0) *inv_slot = rms_scale(s / (float)n + eps);
   }
   __syncthreads();

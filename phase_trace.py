@@ -2,8 +2,10 @@
 
 `build` writes an instrumented copy of the kernel sources into
 _build/phase/ at the repository root, with `s_memtime` stamps at the phase
-boundaries of k_gemv_row (qkv, attn_out, ffn_in, ffn_out) and the tiers of
-k_attn_core, and links it as _build/phase/libc2h_phase.so (same C ABI plus
+boundaries of k_gemv_row's body (qkv, attn_out, ffn_in, ffn_out) and of
+k_attn_core's tiers, in the separate kernels and in the fused launches
+(k_attn_block, k_attn_oproj: their parts stamp as the kernels they run; set
+C2H_NO_FUSE=1 for the separate launches' figures), and links it as _build/phase/libc2h_phase.so (same C ABI plus
 c2h_phase_read).  Nothing is written into the c2slm_amd package.  Lane 0 of every wave writes its stamp per phase into LDS;
 at the kernel's end the first and the last workgroup of each launch copy
 their stamps into a device array, which every later launch of the same
@@ -20,6 +22,7 @@ tier's stamps wave by wave instead.
     python phase_trace.py build      # CPU: hipcc cross-compiles
     python phase_trace.py run        # GPU
     python phase_trace.py run 512    # GPU, long-context attention
+    python phase_trace.py run 48 qwen3   # GPU, the Qwen3-1.7B shape's GEMVs
 """
 from __future__ import annotations
 
@@ -58,13 +61,13 @@ __device__ __forceinline__ int phase_kind() {
     for (int k_ = 0; k_ < 16; ++k_) ph_s_[threadIdx.x >> 6][k_] = 0
 #define PH_G(k) do { if ((threadIdx.x & 63) == 0) ph_s_[threadIdx.x >> 6][k] = __builtin_amdgcn_s_memtime(); } while (0)
 #define PH_G_END do { const int kd_ = phase_kind<NB, PRO, MODE>(); \
-  if (kd_ >= 0 && (threadIdx.x & 63) == 0 && blockIdx.y == 0 && (blockIdx.x == 0 || blockIdx.x == gridDim.x - 1)) \
+  if (kd_ >= 0 && (threadIdx.x & 63) == 0 && by == 0 && (bx == 0 || bx == J.n_wg - 1)) \
     for (int k_ = 0; k_ < 16; ++k_) \
-      g_phase[kd_][blockIdx.x == 0 ? 0 : 1][threadIdx.x >> 6][k_] = ph_s_[threadIdx.x >> 6][k_]; } while (0)
+      g_phase[kd_][bx == 0 ? 0 : 1][threadIdx.x >> 6][k_] = ph_s_[threadIdx.x >> 6][k_]; } while (0)
 #define PH_AT(k, t) do { if ((threadIdx.x & 63) == 0) ph_s_[threadIdx.x >> 6][k] = (t); } while (0)
 #define PH_A_END do { const bool f_ = h == 0; \
   const bool l_ = h == P.n_heads - 1; \
-  if ((threadIdx.x & 63) == 0 && blockIdx.z == 0 && (f_ || l_)) \
+  if ((threadIdx.x & 63) == 0 && bz == 0 && (f_ || l_)) \
     for (int k_ = 0; k_ < 16; ++k_) \
       g_phase[TIER == ATT_TIER_ANY ? 5 : 4][f_ ? 0 : 1][threadIdx.x >> 6][k_] = ph_s_[threadIdx.x >> 6][k_]; } while (0)
 #define PH_A(k) PH_AT(k, __builtin_amdgcn_s_memtime())
@@ -86,18 +89,22 @@ def _patch(text: str, start: str, end: str, edits) -> str:
 
 def instrument(kernels: str) -> str:
     s = kernels.replace("namespace c2h {\n", _STAMPS, 1)
-    s = _patch(s, "__global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(const float* __restrict__ xp, int n_xp,",
-               "#define C2H_GEMV_ROW(NB_, PRO_, MODE_)", [
+    # the bodies shared by the separate kernels and the fused launches
+    s = _patch(s, "__device__ __forceinline__ void gemv_row_body(",
+               "template <int NB, int PRO, int MODE>\n__global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(", [
                    ("  constexpr int NT = row_threads(NB, PRO, MODE);\n",
                     "  PH_DECL;\n  constexpr int NT = row_threads(NB, PRO, MODE);\n"),
                    ("  const int tid = threadIdx.x;\n  const int wave = tid >> 6, lane = tid & 63;\n  // ---- the input",
                     "  PH_G(0);\n  const int tid = threadIdx.x;\n  const int wave = tid >> 6, lane = tid & 63;\n"
                     "  // ---- the input"),
-                   ("  if ((int)blockIdx.x >= J.n_wg) return;  // uniform: the launch's widest job sets the grid\n",
-                    "  if ((int)blockIdx.x >= J.n_wg) return;  // uniform: the launch's widest job sets the grid\n"
+                   ("  if (bx >= J.n_wg) return;  // uniform: the launch's widest job sets the grid\n",
+                    "  if (bx >= J.n_wg) return;  // uniform: the launch's widest job sets the grid\n"
                     "  PH_G(1);\n"),
-                   ("  issue_fence();\n\n  // ---- prologue", "  issue_fence();\n  PH_G(2);\n"
-                    "  asm volatile(\"\" ::\"v\"(xa[0].x));\n  PH_G(3);\n\n  // ---- prologue"),
+                   ("  if (MODE == MODE_BIAS) yres = (J.bias ? J.bias : xp)[J.bias ? out_row : 0];\n  issue_fence();\n",
+                    "  if (MODE == MODE_BIAS) yres = (J.bias ? J.bias : xp)[J.bias ? out_row : 0];\n  issue_fence();\n"
+                    "  PH_G(2);\n"),
+                   ("\n\n  // ---- prologue: the Q8_K input row in LDS", "\n  asm volatile(\"\" ::\"v\"(xa[0].x));\n  PH_G(3);\n"
+                    "\n  // ---- prologue: the Q8_K input row in LDS"),
                    ("    float inv = 0.0f;  //", "    PH_G(9);\n    float inv = 0.0f;  //"),
                    ("    const float4 xn[1] = {norm4(", "    PH_G(4);\n    const float4 xn[1] = {norm4("),
                    ("  // ---- items\n", "  PH_G(5);\n  asm volatile(\"\" ::\"v\"(w1.a.x), \"v\"(w1.c.w));\n"
@@ -105,8 +112,8 @@ def instrument(kernels: str) -> str:
                    ("  // ---- per-row fold in the reference's order, then the epilogue\n",
                     "  PH_G(7);\n  // ---- per-row fold in the reference's order, then the epilogue\n"),
                ]).replace("PH_END;", "PH_G(8);\n  PH_G_END;", 1)
-    s = _patch(s, "template <int TIER>\n__global__ void __launch_bounds__(256)\n    k_attn_core(C2hState* __restrict__ st,",
-               "template __global__ void k_attn_core<ATT_TIER_32>(", [
+    s = _patch(s, "__device__ __forceinline__ void attn_core_body(",
+               "template <int TIER>\n__global__ void __launch_bounds__(256)\n    k_attn_core(C2hState* __restrict__ st,", [
                    ("  const int tid = threadIdx.x;\n  const int layer = dims & 0xff",
                     "  PH_DECL;\n  const long long ph_entry_ = __builtin_amdgcn_s_memtime();\n"
                     "  const int tid = threadIdx.x;\n  const int layer = dims & 0xff"),
@@ -182,7 +189,7 @@ def build() -> str:
     return OUT_LIB
 
 
-def run(last: int = 48, path: str = "/tmp/c2h_phase_q05.gguf") -> None:
+def run(last: int = 48, model: str = "qwen2.5-0.5b") -> None:
     """Prefill last-16 tokens, take 16 greedy steps, print the stamps of the last launches.
 
     At last <= 256 the table covers every kernel (first and last workgroup, latest wave); above
@@ -190,8 +197,8 @@ def run(last: int = 48, path: str = "/tmp/c2h_phase_q05.gguf") -> None:
     """
     if os.environ.get("C2H_LIB") != OUT_LIB:  # the library path is fixed when _lib loads
         env = dict(os.environ, C2H_LIB=OUT_LIB)
-        sys.exit(subprocess.run([sys.executable, "-u", os.path.join(ROOT, "phase_trace.py"), "run", str(last)], env=env,
-                                cwd=ROOT).returncode)
+        sys.exit(subprocess.run([sys.executable, "-u", os.path.join(ROOT, "phase_trace.py"), "run", str(last), model],
+                                env=env, cwd=ROOT).returncode)
     if not 17 <= last <= 1024:
         raise ValueError("last must lie in 17..1024")
     import ctypes as C
@@ -200,8 +207,10 @@ def run(last: int = 48, path: str = "/tmp/c2h_phase_q05.gguf") -> None:
 
     from c2slm_amd import _lib as H
     from c2slm_amd import gguf as G
+    shape = {"qwen2.5-0.5b": G.QWEN05B, "qwen3": G.QWEN3_1_7B}[model]
+    path = f"/tmp/c2h_phase_{model}.gguf"
     if not os.path.exists(path):
-        G.write_synthetic_model(path, G.QWEN05B, seed=20261201)
+        G.write_synthetic_model(path, shape, seed=20261201)
     gf = G.GGUFFile(path)
     ctx = H.Ctx(H.desc_from_gguf(gf, max_ctx=1024))
     H.load_gguf_into(ctx, gf)
@@ -228,8 +237,8 @@ def run(last: int = 48, path: str = "/tmp/c2h_phase_q05.gguf") -> None:
                     f"{int(a[5, wg, w, i] - t0) if a[5, wg, w, i] else -1:8d}" for i in range(len(ATTN_PHASES))))
         ctx.close()
         return
-    print(f"last launch of each kernel (layer 23 of the 16th step, T = {last}); shader clocks from wave 0's"
-          " entry, latest wave")
+    print(f"{model}: last launch of each kernel (last layer of the 16th step, T = {last}); shader clocks from"
+          " wave 0's entry, latest wave (attention: head_dim 64 only)")
     for k, name in enumerate(GEMV_KINDS + ["attn"]):
         cols = ATTN_PHASES if name == "attn" else GEMV_PHASES
         print(f"{name:9s} {'wg':5s} " + " ".join(f"{p:>10s}" for p in cols))
@@ -244,10 +253,11 @@ def run(last: int = 48, path: str = "/tmp/c2h_phase_q05.gguf") -> None:
 
 
 if __name__ == "__main__":
-    if len(sys.argv) not in (2, 3) or sys.argv[1] not in ("build", "run") or (
-            len(sys.argv) == 3 and (sys.argv[1] != "run" or not sys.argv[2].isdigit())):
-        sys.exit("usage: python phase_trace.py build | run [positions]")
+    if len(sys.argv) not in (2, 3, 4) or sys.argv[1] not in ("build", "run") or (
+            len(sys.argv) >= 3 and (sys.argv[1] != "run" or not sys.argv[2].isdigit())) or (
+            len(sys.argv) == 4 and sys.argv[3] not in ("qwen2.5-0.5b", "qwen3")):
+        sys.exit("usage: python phase_trace.py build | run [positions [qwen2.5-0.5b | qwen3]]")
     if sys.argv[1] == "build":
         print(build())
     else:
-        run(int(sys.argv[2]) if len(sys.argv) == 3 else 48)
+        run(int(sys.argv[2]) if len(sys.argv) >= 3 else 48, sys.argv[3] if len(sys.argv) == 4 else "qwen2.5-0.5b")
