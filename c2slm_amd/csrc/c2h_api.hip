@@ -59,6 +59,7 @@ struct c2h_ctx {
   uint64_t* qkv_tag = nullptr;   // q|k|v as {value, tag} words (k_attn_block)
   bool fuse_oproj = true;        // attention and o-projection in one launch where an instance exists
   bool fuse_qkv = true;          // and qkv with them (layers past 0)
+  bool h128_staged = false;      // head_dim 128: k_attn_h128<H128_VCH> (V through LDS) fits beside the scores
   float* normx[2] = {nullptr, nullptr};
   int nx_cur = 0, nx_prev = 0;
   float* kv = nullptr;
@@ -712,8 +713,11 @@ void enqueue_attn(c2h_ctx* c, int l, int form) {
   A.out = c->attn;
   A.store_kv = 1;
   const dim3 grid(D.n_heads / D.n_kv_heads, D.n_kv_heads);
-  if (D.head_dim == 128)
-    hipLaunchKernelGGL(k_attn_h128, grid, dim3(256), c->attn_lds, c->stream, A);
+  if (D.head_dim == 128) {
+    A.sc_ld = attn_h128_lds_floats(D.max_ctx);  // the V chunks follow the scores
+    hipLaunchKernelGGL(c->h128_staged ? k_attn_h128<H128_VCH> : k_attn_h128<0>, grid, dim3(256), c->attn_lds,
+                       c->stream, A);
+  }
   else if (form == ATT_FORM_LONG)
     enqueue_attn_long(c, A, 1);
   else {
@@ -1223,8 +1227,11 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
     c->attn_lds = (size_t)attn_h128_lds_floats(D.max_ctx) * 4;
     if (c->attn_lds > 152u * 1024)
       return bail(fail(c, C2H_ERR_UNSUPPORTED, "head_dim 128 runs up to %d positions", 152 * 256 - 64));
-    if (hipFuncSetAttribute((const void*)k_attn_h128, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)c->attn_lds) != hipSuccess)
+    // V staged through LDS where its two chunks fit beside the scores
+    c->h128_staged = c->attn_lds + (size_t)attn_h128_v_lds_floats() * 4 <= 152u * 1024;
+    if (c->h128_staged) c->attn_lds += (size_t)attn_h128_v_lds_floats() * 4;
+    if (hipFuncSetAttribute(c->h128_staged ? (const void*)k_attn_h128<H128_VCH> : (const void*)k_attn_h128<0>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->attn_lds) != hipSuccess)
       return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
     c->att_split = D.max_ctx;
   } else {

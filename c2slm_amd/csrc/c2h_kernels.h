@@ -267,8 +267,11 @@ __host__ __device__ inline int pfa_sc_ld(int pmax) { return ((pmax + 1 + 63) & ~
 __host__ __device__ inline int pfa_lds_floats(int pmax) { return PFA_CH * PFA_KPAD + PFA_TB * 64 + PFA_TB * pfa_sc_ld(pmax); }
 
 // Dynamic LDS of k_attn_h128 (head_dim 128), in floats: the scores of every
-// position up to max_ctx.
+// position up to max_ctx, then (k_attn_h128<H128_VCH>) two chunks of
+// H128_VCH positions of V.
+constexpr int H128_VCH = 32;
 __host__ __device__ inline int attn_h128_lds_floats(int max_ctx) { return chain_lds_floats(max_ctx); }
+__host__ __device__ inline int attn_h128_v_lds_floats() { return 2 * H128_VCH * 128; }
 
 // Dynamic LDS of k_attn_core, in floats: the staged K rows of the scores
 // (ATT_KPF padded rows), which the two staged V chunks of the AV chains
@@ -439,6 +442,7 @@ inline int attn_dims(const AttnCoreParams& A, int qpkv) {
 __global__ void k_attn_scores(AttnCoreParams P);
 __global__ void k_attn_softmax(AttnCoreParams P);
 __global__ void k_attn_av(AttnCoreParams P);
+template <int VCH>
 __global__ void k_attn_h128(AttnCoreParams P);
 __global__ void k_pf_attn(AttnCoreParams P);
 template <int NB>

@@ -251,6 +251,7 @@ constexpr int SPEC_C = 16;
 constexpr int SPEC_ROUNDS = 10;
 constexpr int WIN_MIN_N = 256;
 constexpr int SUM_DIRECT_N = 64;
+constexpr int H128_SUM_DIRECT_N = 128;
 
 // One round: R is this lane's chunk run from its start S.  Returns true with
 // the total once every start is verified; else advances S (and m, the last
@@ -2174,39 +2175,6 @@ C2H_ATTN_OPROJ(ATT_TIER_ANY, 3)
 
 // ------------------------------------------------ attention, head_dim 128
 
-// Score of one position for head_dim 128 (internal/simd/c2_tensor_attn_gen.go:
-// 18-50 with hd = 128): two 8-lane FMA accumulators over d = 0,16,..,112
-// (lanes l and 8+l), then ((l0+l1)+(l2+l3))+((l4+l5)+(l6+l7)) of acc0+acc1,
-// times scale.  kr: the K row (cache or LDS), read as 32 float4.
-__device__ __forceinline__ float attn_score_h128(const float* q_s, const float* kr, float scale) {
-  const float4* k4 = reinterpret_cast<const float4*>(kr);
-  float4 kk[32];
-#pragma unroll
-  for (int i = 0; i < 32; ++i) kk[i] = k4[i];
-  float a0[8], a1[8];
-#pragma unroll
-  for (int l = 0; l < 8; ++l) {
-    a0[l] = 0.0f;
-    a1[l] = 0.0f;
-  }
-#pragma unroll
-  for (int d = 0; d < 128; d += 16) {
-    const float4 c0 = kk[d / 4], c1 = kk[d / 4 + 1], c2 = kk[d / 4 + 2], c3 = kk[d / 4 + 3];
-    const float k16[16] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w,
-                           c2.x, c2.y, c2.z, c2.w, c3.x, c3.y, c3.z, c3.w};
-#pragma unroll
-    for (int l = 0; l < 8; ++l) {
-      a0[l] = __builtin_fmaf(q_s[d + l], k16[l], a0[l]);
-      a1[l] = __builtin_fmaf(q_s[d + 8 + l], k16[8 + l], a1[l]);
-    }
-  }
-  float v[8];
-#pragma unroll
-  for (int l = 0; l < 8; ++l) v[l] = a0[l] + a1[l];
-  const float sco = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-  return sco * scale;
-}
-
 // Attention of one query head per workgroup for head_dim 128 (Qwen3;
 // engine/forward.go:66-106 from the q|k|v rows on, for that head):
 //   per-head QK-RMSNorm of q_h and k_g when the layer has the weights
@@ -2214,15 +2182,27 @@ __device__ __forceinline__ float attn_score_h128(const float* q_s, const float* 
 //     values: exact sequential sum of x*x, one wave per vector);
 //   RoPE (tensor/ops.go:262-286, pairs (i, i+64));
 //   KV store (engine/kvcache.go:143-157) by the group's first head;
-//   scores in the two-accumulator FMA order (attn_score_h128), softmax with
-//     f64 exp and an exact sequential f32 sum (tensor/ops.go:317-339);
+//   scores in the reference's order (internal/simd/c2_tensor_attn_gen.go:
+//     18-50 with hd = 128): two 8-lane FMA accumulators a0[l], a1[l] over
+//     d = 0,16,..,112 (elements d + l and d + 8 + l), then
+//     ((v0+v1)+(v2+v3))+((v4+v5)+(v6+v7)) of v_l = a0[l] + a1[l], times
+//     scale; softmax with f64 exp and an exact sequential f32 sum
+//     (tensor/ops.go:317-339);
 //   per output dimension one FMA chain over the positions
-//     (c2_tensor_attn_gen.go:85-117, the hd % 64 == 0 path), V read from
-//     the quad-major cache, four positions per 16-byte load; position pos
-//     uses this launch's v.
-// The scores of every position sit in LDS (attn_h128_lds_floats(max_ctx)).
+//     (c2_tensor_attn_gen.go:85-117, the hd % 64 == 0 path), four positions
+//     per 16-byte V quad; position pos uses this launch's v.
+// VCH = 0: the chains (waves 0-1, one lane per dimension) read V from the
+//   quad-major cache, three batches of sixteen positions in flight.
+// VCH > 0: waves 2-3 stage V in chunks of VCH positions through two LDS
+//   buffers (coalesced: a wave's load is one 1 KB quad row), three chunks in
+//   flight in registers, the first ones issued while wave 0 sums the
+//   exponentials; the chains read each chunk from LDS, one barrier per chunk.
+// The scores of every position sit in LDS (P.sc_ld floats,
+// attn_h128_lds_floats(max_ctx)), the V buffers (VCH > 0) after them.
 // Grid (query heads per KV head, KV heads, query tokens); 256 threads.
+template <int VCH>
 __global__ void __launch_bounds__(256) k_attn_h128(AttnCoreParams P) {
+  constexpr int VQ = VCH / 4 > 0 ? VCH / 4 : 1;  // V quads per chunk
   constexpr int HD = 128;
   extern __shared__ __align__(16) unsigned char smem[];
   float* sc = reinterpret_cast<float*>(smem);
@@ -2301,13 +2281,61 @@ __global__ void __launch_bounds__(256) k_attn_h128(AttnCoreParams P) {
   }
   if (T > P.max_ctx) return;  // rejected on the host; kept as a guard
 
-  // ---- scores; position pos uses this launch's k
+  // ---- scores; position pos uses this launch's k.  Sixteen lanes per
+  // position (group gi = tid / 16 takes positions gi, gi + 16, ...): lane j
+  // runs one accumulator over the elements 16 s + j (s = 0..7), a0[j] for
+  // j < 8 and a1[j - 8] for j >= 8, and the group then adds in the
+  // reference's tree: v_l = lane l + lane l+8, then pairs, quads, halves
+  // (each add commutes, so both lanes of a pair compute the same value).  A
+  // group reads 64 contiguous bytes of its row per load; the loads of four
+  // rounds of sixteen positions are in flight while the previous four run.
   float lmax = -__builtin_inff();
-  for (int p = tid; p < T; p += 256) {
-    const float* kr = (p == pos) ? k_s : kcache + (size_t)p * HD;
-    const float sco = attn_score_h128(q_s, kr, P.scale);
-    sc[p] = sco;
-    lmax = (sco > lmax) ? sco : lmax;
+  {
+    const int j = tid & 15, gi = tid >> 4;
+    float qv[8], kp[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      qv[s] = q_s[16 * s + j];
+      kp[s] = k_s[16 * s + j];
+    }
+    const int kmax = max(pos - 1, 0);  // cached rows [0, pos)
+    const int nr = (T + 15) >> 4;      // rounds of sixteen positions
+    constexpr int RB = 4;
+    float ka[RB][8], kb[RB][8];
+    auto load_rounds = [&](float(&k)[RB][8], int r0) {
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const float* kr = kcache + (size_t)min((r0 + r) * 16 + gi, kmax) * HD + j;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) k[r][s] = kr[16 * s];
+      }
+    };
+    auto score_rounds = [&](const float(&k)[RB][8], int r0) {
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        if (r0 + r >= nr) break;  // uniform
+        const int p = (r0 + r) * 16 + gi;
+        float a = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) a = __builtin_fmaf(qv[s], (p == pos) ? kp[s] : k[r][s], a);
+        a = a + __shfl_xor(a, 8, 16);
+        a = a + __shfl_xor(a, 1, 16);
+        a = a + __shfl_xor(a, 2, 16);
+        a = a + __shfl_xor(a, 4, 16);
+        if (j == 0 && p < T) {
+          const float sco = a * P.scale;
+          sc[p] = sco;
+          lmax = (sco > lmax) ? sco : lmax;
+        }
+      }
+    };
+    load_rounds(ka, 0);
+    for (int r0 = 0; r0 < nr; r0 += 2 * RB) {
+      load_rounds(kb, r0 + RB);
+      score_rounds(ka, r0);
+      load_rounds(ka, r0 + 2 * RB);
+      score_rounds(kb, r0 + RB);
+    }
   }
   // ---- softmax: max (x[0] first, strict '>': the max of the non-NaN
   // scores, or NaN when score[0] is NaN), f32(exp(f64(x - max))), the exact
@@ -2318,10 +2346,31 @@ __global__ void __launch_bounds__(256) k_attn_h128(AttnCoreParams P) {
   float mx = fmax_gt(fmax_gt(fmax_gt(red_m[0], red_m[1]), red_m[2]), red_m[3]);
   if (sc[0] != sc[0]) mx = sc[0];
   for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));
+  if (T <= H128_SUM_DIRECT_N) pad_chain(sc, T);
   __syncthreads();
+  // VCH > 0: the staging waves' V (chunk c: quads [c VQ, c VQ + VQ) of the
+  // stored positions [0, pos); quads past them read zeros)
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nch = VCH > 0 ? (pos + VCH - 1) / VCH : 0;
+  const int st = tid - 128;  // staging thread: dimension st of each quad
+  const __amdgpu_buffer_rsrc_t vrs = cache_rsrc(vcache, ((max(pos, 0) + 3) >> 2) * HD * 16);
+  f32x4_t s0[VQ], s1[VQ], s2[VQ];
+  auto load_set = [&](f32x4_t(&r)[VQ], int c) {
+#pragma unroll
+    for (int k = 0; k < VQ; ++k) r[k] = cache_ld4(vrs, ((c * VQ + k) * HD + st) * 16);
+  };
   if (tid < 64) {
-    const float ssum = (T <= 64 * SPEC_C) ? seq_sum_wave(sc, T) : seq_sum_wave_n(sc, T);
+    // one lane's chain up to H128_SUM_DIRECT_N values (shorter than the
+    // speculative rounds there), then the rounds
+    const float ssum = (T <= H128_SUM_DIRECT_N) ? chain_sum(sc, T)
+                       : (T <= 64 * SPEC_C)     ? seq_sum_wave(sc, T)
+                       : (T <= 128 * SPEC_C)    ? seq_sum_wave<2 * SPEC_C>(sc, T)
+                                                : seq_sum_wave_n(sc, T);
     if (tid == 0) inv_s[2] = 1.0f / ssum;
+  } else if (VCH > 0 && wv >= 2 && nch > 0) {  // issued while wave 0 sums
+    load_set(s0, 0);
+    load_set(s1, min(1, nch - 1));
+    load_set(s2, min(2, nch - 1));
   }
   __syncthreads();
   const float inv = inv_s[2];
@@ -2329,13 +2378,56 @@ __global__ void __launch_bounds__(256) k_attn_h128(AttnCoreParams P) {
   __syncthreads();
 
   // ---- AV: out[d] = fma chain over p of (prob[p], V[p][d])
-  if (tid < HD) {
-    float acc = 0.0f;
-    if (pos > 0) acc = av_chain_q3<HD>(sc, reinterpret_cast<const f32x4_t*>(vcache), pos, tid, acc);
-    acc = __builtin_fmaf(sc[pos], v_s[tid], acc);
-    P.out[(size_t)ti * P.out_ld + h * HD + tid] = acc;
+  if constexpr (VCH == 0) {
+    if (tid < HD) {
+      float acc = 0.0f;
+      if (pos > 0) acc = av_chain_q3<HD>(sc, reinterpret_cast<const f32x4_t*>(vcache), pos, tid, acc);
+      acc = __builtin_fmaf(sc[pos], v_s[tid], acc);
+      P.out[(size_t)ti * P.out_ld + h * HD + tid] = acc;
+    }
+  } else {
+    f32x4_t* vbuf = reinterpret_cast<f32x4_t*>(sc + P.sc_ld);  // [2][VQ][HD]
+    // chunk c is stored into buffer c & 1 before barrier c and read after
+    // it; the store of chunk c + 2 follows barrier c + 1, which the chains
+    // pass once chunk c is done
+    if (wv >= 2) {
+      auto store_set = [&](const f32x4_t(&r)[VQ], int c) {
+#pragma unroll
+        for (int k = 0; k < VQ; ++k) vbuf[((c & 1) * VQ + k) * HD + st] = r[k];
+      };
+      int c = 0;
+      for (; c + 3 <= nch; c += 3) {
+        store_set(s0, c);
+        load_set(s0, min(c + 3, nch - 1));
+        __syncthreads();
+        store_set(s1, c + 1);
+        load_set(s1, min(c + 4, nch - 1));
+        __syncthreads();
+        store_set(s2, c + 2);
+        load_set(s2, min(c + 5, nch - 1));
+        __syncthreads();
+      }
+      if (c < nch) {
+        store_set(s0, c);
+        __syncthreads();
+      }
+      if (c + 1 < nch) {
+        store_set(s1, c + 1);
+        __syncthreads();
+      }
+    } else {
+      float acc = 0.0f;
+      for (int c = 0; c < nch; ++c) {
+        __syncthreads();
+        acc = av_chain_q3<HD>(sc + c * VCH, vbuf + (c & 1) * VQ * HD, min(VCH, pos - c * VCH), tid, acc);
+      }
+      acc = __builtin_fmaf(sc[pos], v_s[tid], acc);
+      P.out[(size_t)ti * P.out_ld + h * HD + tid] = acc;
+    }
   }
 }
+template __global__ void k_attn_h128<0>(AttnCoreParams);
+template __global__ void k_attn_h128<H128_VCH>(AttnCoreParams);
 
 
 // ------------------------------------------- attention, long contexts

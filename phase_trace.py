@@ -71,6 +71,12 @@ __device__ __forceinline__ int phase_kind() {
     for (int k_ = 0; k_ < 16; ++k_) \
       g_phase[TIER == ATT_TIER_ANY ? 5 : 4][f_ ? 0 : 1][threadIdx.x >> 6][k_] = ph_s_[threadIdx.x >> 6][k_]; } while (0)
 #define PH_A(k) PH_AT(k, __builtin_amdgcn_s_memtime())
+// k_attn_h128 (no k_attn_core runs at head_dim 128): its stamps take the attention slot
+#define PH_H_END do { const bool f_ = h == 0; \
+  const bool l_ = h == (int)(gridDim.x * gridDim.y) - 1; \
+  if ((threadIdx.x & 63) == 0 && blockIdx.z == 0 && (f_ || l_)) \
+    for (int k_ = 0; k_ < 16; ++k_) \
+      g_phase[4][f_ ? 0 : 1][threadIdx.x >> 6][k_] = ph_s_[threadIdx.x >> 6][k_]; } while (0)
 """
 
 
@@ -142,6 +148,26 @@ def instrument(kernels: str) -> str:
                    ("  if (tid < HD) {\n    acc = __builtin_fmaf(sc[pos], v_s[d], acc);\n",
                     "  PH_A(7);\n  if (tid < HD) {\n    acc = __builtin_fmaf(sc[pos], v_s[d], acc);\n"),
                ]).replace("PH_END;", "PH_A(8);\n  PH_A_END;", 1)
+    # head_dim 128: entry, args, issued, pos, qkv (q|k|v in LDS), rope (QK-norm and RoPE done), scores, max,
+    # exp, sum, softmax (normalised), av, end
+    s = _patch(s, "template <int VCH>\n__global__ void __launch_bounds__(256) k_attn_h128(AttnCoreParams P) {",
+               "template __global__ void k_attn_h128<0>(AttnCoreParams);", [
+                   ("  extern __shared__ __align__(16) unsigned char smem[];\n  float* sc = reinterpret_cast<float*>(smem);\n",
+                    "  extern __shared__ __align__(16) unsigned char smem[];\n  float* sc = reinterpret_cast<float*>(smem);\n"
+                    "  PH_DECL;\n  const long long ph_entry_ = __builtin_amdgcn_s_memtime();\n"),
+                   ('"s"(P.scale), "s"(P.state), "s"(P.tok0), "s"(gridDim.x));\n',
+                    '"s"(P.scale), "s"(P.state), "s"(P.tok0), "s"(gridDim.x));\n  PH_AT(0, ph_entry_);\n  PH_A(1);\n'),
+                   ("  const int T = pos + 1;\n", "  asm volatile(\"\" ::\"s\"(pos));\n  PH_A(9);\n  const int T = pos + 1;\n"),
+                   ("  qkv_s[role][e] = own;\n", "  PH_A(2);\n  qkv_s[role][e] = own;\n"),
+                   ("  // ---- RoPE: threads 0..63", "  PH_A(3);\n  // ---- RoPE: threads 0..63"),
+                   ("  if (P.store_kv && blockIdx.x == 0 && tid < HD", "  PH_A(4);\n  if (P.store_kv && blockIdx.x == 0 && tid < HD"),
+                   ("  // ---- softmax: max (x[0] first", "  PH_A(5);\n  // ---- softmax: max (x[0] first"),
+                   ("  if (sc[0] != sc[0]) mx = sc[0];\n  for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));\n  if (T <= H128_SUM_DIRECT_N) pad_chain(sc, T);\n  __syncthreads();\n",
+                    "  if (sc[0] != sc[0]) mx = sc[0];\n  PH_A(12);\n  for (int p = tid; p < T; p += 256) sc[p] = (float)exp((double)(sc[p] - mx));\n  if (T <= H128_SUM_DIRECT_N) pad_chain(sc, T);\n  __syncthreads();\n  PH_A(13);\n"),
+                   ("  const float inv = inv_s[2];\n", "  PH_A(14);\n  const float inv = inv_s[2];\n"),
+                   ("  // ---- AV: out[d] = fma chain over p of (prob[p], V[p][d])\n",
+                    "  PH_A(6);\n  // ---- AV: out[d] = fma chain over p of (prob[p], V[p][d])\n"),
+               ]).replace("PH_END;", "PH_A(8);\n  PH_H_END;", 1)
     return s
 
 
@@ -226,7 +252,7 @@ def run(last: int = 48, model: str = "qwen2.5-0.5b") -> None:
     if fn(buf) != 0:
         raise RuntimeError("c2h_phase_read failed")
     a = np.array(buf, dtype=np.int64).reshape(6, 2, N_WAVES, N_SLOTS)
-    if last > 256:
+    if last > 256 and model != "qwen3":
         print(f"attention, any-length tier, layer 23 of the 16th step, T = {last}; shader clocks from wave 0's"
               " entry, per wave")
         print(f"{'wg':5s} {'wave':4s} " + " ".join(f"{p:>8s}" for p in ATTN_PHASES))
