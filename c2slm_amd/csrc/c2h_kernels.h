@@ -270,6 +270,7 @@ __host__ __device__ inline int pfa_lds_floats(int pmax) { return PFA_CH * PFA_KP
 // position up to max_ctx, then (k_attn_h128<H128_VCH>) two chunks of
 // H128_VCH positions of V.
 constexpr int H128_VCH = 32;
+constexpr int H128_VSETS = 6;  // V chunks of k_attn_h128 in flight
 __host__ __device__ inline int attn_h128_lds_floats(int max_ctx) { return chain_lds_floats(max_ctx); }
 __host__ __device__ inline int attn_h128_v_lds_floats() { return 2 * H128_VCH * 128; }
 

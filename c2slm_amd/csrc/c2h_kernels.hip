@@ -2194,9 +2194,10 @@ C2H_ATTN_OPROJ(ATT_TIER_ANY, 3)
 // VCH = 0: the chains (waves 0-1, one lane per dimension) read V from the
 //   quad-major cache, three batches of sixteen positions in flight.
 // VCH > 0: waves 2-3 stage V in chunks of VCH positions through two LDS
-//   buffers (coalesced: a wave's load is one 1 KB quad row), three chunks in
-//   flight in registers, the first ones issued while wave 0 sums the
-//   exponentials; the chains read each chunk from LDS, one barrier per chunk.
+//   buffers (coalesced: a wave's load is one 1 KB quad row), H128_VSETS
+//   chunks in flight in registers (one workgroup per CU: registers are not
+//   what limits), the first ones issued while wave 0 sums the exponentials;
+//   the chains read each chunk from LDS, one barrier per chunk.
 // The scores of every position sit in LDS (P.sc_ld floats,
 // attn_h128_lds_floats(max_ctx)), the V buffers (VCH > 0) after them.
 // Grid (query heads per KV head, KV heads, query tokens); 256 threads.
@@ -2354,7 +2355,8 @@ __global__ void __launch_bounds__(256) k_attn_h128(AttnCoreParams P) {
   const int nch = VCH > 0 ? (pos + VCH - 1) / VCH : 0;
   const int st = tid - 128;  // staging thread: dimension st of each quad
   const __amdgpu_buffer_rsrc_t vrs = cache_rsrc(vcache, ((max(pos, 0) + 3) >> 2) * HD * 16);
-  f32x4_t s0[VQ], s1[VQ], s2[VQ];
+  constexpr int NSET = H128_VSETS;  // V chunks in flight in the staging waves' registers
+  f32x4_t vset[NSET][VQ];
   auto load_set = [&](f32x4_t(&r)[VQ], int c) {
 #pragma unroll
     for (int k = 0; k < VQ; ++k) r[k] = cache_ld4(vrs, ((c * VQ + k) * HD + st) * 16);
@@ -2368,9 +2370,8 @@ __global__ void __launch_bounds__(256) k_attn_h128(AttnCoreParams P) {
                                                 : seq_sum_wave_n(sc, T);
     if (tid == 0) inv_s[2] = 1.0f / ssum;
   } else if (VCH > 0 && wv >= 2 && nch > 0) {  // issued while wave 0 sums
-    load_set(s0, 0);
-    load_set(s1, min(1, nch - 1));
-    load_set(s2, min(2, nch - 1));
+#pragma unroll
+    for (int k = 0; k < NSET; ++k) load_set(vset[k], min(k, nch - 1));
   }
   __syncthreads();
   const float inv = inv_s[2];
@@ -2396,24 +2397,20 @@ __global__ void __launch_bounds__(256) k_attn_h128(AttnCoreParams P) {
         for (int k = 0; k < VQ; ++k) vbuf[((c & 1) * VQ + k) * HD + st] = r[k];
       };
       int c = 0;
-      for (; c + 3 <= nch; c += 3) {
-        store_set(s0, c);
-        load_set(s0, min(c + 3, nch - 1));
-        __syncthreads();
-        store_set(s1, c + 1);
-        load_set(s1, min(c + 4, nch - 1));
-        __syncthreads();
-        store_set(s2, c + 2);
-        load_set(s2, min(c + 5, nch - 1));
-        __syncthreads();
+      for (; c + NSET <= nch; c += NSET) {
+#pragma unroll
+        for (int k = 0; k < NSET; ++k) {
+          store_set(vset[k], c + k);
+          load_set(vset[k], min(c + k + NSET, nch - 1));
+          __syncthreads();
+        }
       }
-      if (c < nch) {
-        store_set(s0, c);
-        __syncthreads();
-      }
-      if (c + 1 < nch) {
-        store_set(s1, c + 1);
-        __syncthreads();
+#pragma unroll
+      for (int k = 0; k < NSET - 1; ++k) {
+        if (c + k < nch) {  // uniform
+          store_set(vset[k], c + k);
+          __syncthreads();
+        }
       }
     } else {
       float acc = 0.0f;
