@@ -2286,8 +2286,8 @@ __global__ void __launch_bounds__(256) k_attn_h128(AttnCoreParams P) {
   // position (group gi = tid / 16 takes positions gi, gi + 16, ...): lane j
   // runs one accumulator over the elements 16 s + j (s = 0..7), a0[j] for
   // j < 8 and a1[j - 8] for j >= 8, and the group then adds in the
-  // reference's tree: v_l = lane l + lane l+8, then pairs, quads, halves
-  // (each add commutes, so both lanes of a pair compute the same value).  A
+  // reference's tree in lane 0: v_l = lane l + lane l+8, then pairs,
+  // quads, halves (each add commutes).  A
   // group reads 64 contiguous bytes of its row per load; the loads of four
   // rounds of sixteen positions are in flight while the previous four run.
   float lmax = -__builtin_inff();
@@ -2319,10 +2319,12 @@ __global__ void __launch_bounds__(256) k_attn_h128(AttnCoreParams P) {
         float a = 0.0f;
 #pragma unroll
         for (int s = 0; s < 8; ++s) a = __builtin_fmaf(qv[s], (p == pos) ? kp[s] : k[r][s], a);
-        a = a + __shfl_xor(a, 8, 16);
-        a = a + __shfl_xor(a, 1, 16);
-        a = a + __shfl_xor(a, 2, 16);
-        a = a + __shfl_xor(a, 4, 16);
+        // lane 0 of the group ends with ((v0+v1)+(v2+v3))+((v4+v5)+(v6+v7)),
+        // row-local DPP adds (the whole wave runs them)
+        a = a + dpp_or0<0x128>(a);  // row_ror:8: lane l += lane l+8 (v_l, l < 8)
+        a = a + dpp_or0<0xb1>(a);   // quad_perm [1,0,3,2]: pairs
+        a = a + dpp_or0<0x4e>(a);   // quad_perm [2,3,0,1]: quads
+        a = a + dpp_or0<0x104>(a);  // row_shl:4: lane 0 += lane 4
         if (j == 0 && p < T) {
           const float sco = a * P.scale;
           sc[p] = sco;
