@@ -420,8 +420,6 @@ void launch_gemv_f(c2h_ctx* c, GemvParams& P) {
   hipLaunchKernelGGL(k, job_grid(P), dim3(256), lds, c->stream, P);
 }
 
-// A row-kernel launch over all its jobs (same width and mode); the norm
-// prologues need the x*x chain buffer.
 // rows per workgroup and workgroups of each job of a k_gemv_row launch
 void prep_gemv_row(GemvParams& P) {
   const int ni = row_item_threads(P.jobs[0].nb, P.prologue, P.jobs[0].mode);
@@ -432,6 +430,8 @@ void prep_gemv_row(GemvParams& P) {
   }
 }
 
+// A row-kernel launch over all its jobs (same width and mode); the norm
+// prologues need the x*x chain buffer.
 void launch_gemv_row(c2h_ctx* c, GemvParams& P) {
   const int nt = row_threads(P.jobs[0].nb, P.prologue, P.jobs[0].mode);
   prep_gemv_row(P);
@@ -740,6 +740,18 @@ decltype(&k_attn_block<ATT_TIER_32, 3>) attn_block_kernel(int form) {
   }
 }
 
+// The k_attn_block_f instance of a core form.
+decltype(&k_attn_block_f<ATT_TIER_32>) attn_block_f_kernel(int form) {
+  switch (form) {
+    case ATT_FORM_32: return k_attn_block_f<ATT_TIER_32>;
+    case ATT_FORM_64: return k_attn_block_f<ATT_TIER_64>;
+    case ATT_FORM_96: return k_attn_block_f<ATT_TIER_96>;
+    case ATT_FORM_128: return k_attn_block_f<ATT_TIER_128>;
+    case ATT_FORM_256: return k_attn_block_f<ATT_TIER_256>;
+    default: return k_attn_block_f<ATT_TIER_ANY>;
+  }
+}
+
 // The k_attn_oproj instance of a core form.
 decltype(&k_attn_oproj<ATT_TIER_ANY, 3>) attn_oproj_kernel(int form) {
   switch (form) {
@@ -801,6 +813,55 @@ GemvParams fused_oproj_params(c2h_ctx* c, int l) {
   P.wait_err = c->tok_host + 2;
   prep_gemv_row(P);
   return P;
+}
+
+// Whether layer l runs qkv, attention and attn_out as one launch of the
+// float-input GEMV (k_attn_block_f): past layer 0, the head_dim 64 decode
+// forms over the XCD-grouped grid, Q5_0 / Q8_0 q, k, v and o.
+bool fuse_attn_block_f(const c2h_ctx* c, int l, int form) {
+  const c2h_model_desc& D = c->desc;
+  const Layer& L = c->layers[l];
+  return l > 0 && c->fuse_qkv && D.head_dim == 64 && form < ATT_FORM_LONG && D.n_kv_heads <= ATT_XCDS &&
+         float_input(L.wq.type) && float_input(L.wk.type) && float_input(L.wv.type) && float_input(L.wo.type);
+}
+
+// qkv + attention + attn_out in one launch, the GEMV parts k_gemv_f's
+void enqueue_attn_block_f(c2h_ctx* c, int l, int form) {
+  const c2h_model_desc& D = c->desc;
+  Layer& L = c->layers[l];
+  const int E = D.n_embd, KVd = D.n_kv_heads * D.head_dim;
+  GemvParams Q = base_params(c);
+  add_job(Q, L.wq, nullptr, MODE_BIAS, c->q, L.bq, nullptr);
+  add_job(Q, L.wk, nullptr, MODE_BIAS, c->k, L.bk, nullptr);
+  add_job(Q, L.wv, nullptr, MODE_BIAS, c->v, L.bv, nullptr);
+  Q.jobs[0].spare = 0;
+  Q.jobs[1].spare = E;
+  Q.jobs[2].spare = E + KVd;
+  Q.prologue = PRO_NORM;
+  Q.x = c->X;
+  Q.x_out = c->X;
+  Q.n_x = E;
+  Q.n_x_lds = chain_lds_floats(E);
+  Q.norm_w = L.attn_norm;
+  Q.nb_in = nb8_of(E);
+  Q.y_tag = c->qkv_tag;
+  int w = 1;
+  for (int j = 0; j < Q.n_jobs; ++j) w = std::max(w, Q.jobs[j].n_wg);
+  const AttnCoreParams A = fused_attn_params(c, l);
+  GemvParams P = base_params(c);
+  add_job(P, L.wo, nullptr, MODE_RESID, c->X, nullptr, nullptr);
+  P.prologue = PRO_QUANT;
+  P.x = c->attn;
+  P.x_out = c->X;
+  P.n_x = E;
+  P.n_x_lds = chain_lds_floats(E);
+  P.nb_in = nb8_of(E);
+  P.x_tag = c->attn_tag;
+  P.wait_err = c->tok_host + 2;
+  const size_t lds = std::max(c->attn_lds, (size_t)gemv_f_lds_floats(E) * sizeof(float));
+  hipLaunchKernelGGL(attn_block_f_kernel(form), dim3(3 * w + A.n_attn_wg + P.jobs[0].n_wg), dim3(256), lds,
+                     c->stream, A.state, A.kv, (const float*)c->X, w << 16, (const uint64_t*)c->qkv_tag,
+                     attn_dims(A, D.n_heads / D.n_kv_heads), A.max_ctx, A, Q, P);
 }
 
 // attention + attn_out in one launch: the attention workgroups first, then
@@ -898,6 +959,8 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax, int form) {
   for (int l = 0; l < c->desc.n_layers; ++l) {
     if (fuse_attn_block(c, l, form)) {
       enqueue_attn_block(c, l, form);
+    } else if (fuse_attn_block_f(c, l, form)) {
+      enqueue_attn_block_f(c, l, form);
     } else {
       enqueue_qkv(c, l, (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM);
       if (fuse_attn_oproj(c, l, form)) {
@@ -1248,7 +1311,9 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
             hipFuncSetAttribute((const void*)attn_oproj_kernel(form), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)c->attn_lds) != hipSuccess ||
             hipFuncSetAttribute((const void*)attn_block_kernel(form), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)std::max(c->attn_lds, (size_t)chain_lds_floats(D.n_embd) * 4)) != hipSuccess)
+                                (int)std::max(c->attn_lds, (size_t)chain_lds_floats(D.n_embd) * 4)) != hipSuccess ||
+            hipFuncSetAttribute((const void*)attn_block_f_kernel(form), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)std::max(c->attn_lds, (size_t)gemv_f_lds_floats(D.n_embd) * 4)) != hipSuccess)
           return bail(fail(c, C2H_ERR_HIP, "attention LDS attribute"));
       const void* pff[] = {(const void*)k_pf_gemm_f<MODE_BIAS>, (const void*)k_pf_gemm_f<MODE_RESID>,
                            (const void*)k_pf_gemm_q50<MODE_BIAS>, (const void*)k_pf_gemm_q50<MODE_RESID>};

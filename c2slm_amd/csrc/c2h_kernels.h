@@ -433,6 +433,10 @@ __global__ void k_attn_core(C2hState* st, float* kv, const float* qg, const floa
 template <int TIER, int NB>
 __global__ void k_attn_block(C2hState* st, float* kv, const float* xp, int xw, const uint64_t* qkv_tag, int dims,
                              int max_ctx, AttnCoreParams P, GemvParams Gq, GemvParams Go);
+// k_attn_block with k_gemv_f's float-input q|k|v and o-projection parts
+template <int TIER>
+__global__ void k_attn_block_f(C2hState* st, float* kv, const float* xp, int xw, const uint64_t* qkv_tag, int dims,
+                               int max_ctx, AttnCoreParams P, GemvParams Gq, GemvParams Go);
 template <int TIER, int NB>
 __global__ void k_attn_oproj(C2hState* st, float* kv, const float* qg, const float* kg, const float* vg, int dims,
                              int max_ctx, AttnCoreParams P, GemvParams G);

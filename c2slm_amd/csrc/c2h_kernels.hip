@@ -956,8 +956,8 @@ __device__ __forceinline__ float poll_tagged1(const uint64_t* src, uint32_t tag,
 // keeps them in SGPRs rather than re-read in the epilogue; the pointers only
 // go in (a pointer out of an asm loses its global address space, and its
 // loads would turn into flat loads with whole-queue waits).
-__device__ __forceinline__ GemvJob launch_job(const GemvParams& P) {
-  GemvJob J = P.jobs[blockIdx.y];
+__device__ __forceinline__ GemvJob launch_job(const GemvParams& P, int by) {
+  GemvJob J = P.jobs[by];
   asm volatile(""
                : "+s"(J.type), "+s"(J.type2), "+s"(J.rows), "+s"(J.nb), "+s"(J.rpw), "+s"(J.n_wg), "+s"(J.mode)
                : "s"(J.spare), "s"(J.w.q), "s"(J.w.d), "s"(J.w2.q), "s"(J.w2.d), "s"(J.y), "s"(J.bias), "s"(J.isums),
@@ -1205,7 +1205,7 @@ __global__ void __launch_bounds__(256) k_gemv_q8k(GemvParams P) {
   float* terms = reinterpret_cast<float*>(smem + sizeof(Q8KLds));  // [256]
   float* dq = terms + 256;                                          // [256]
   const int tid = threadIdx.x;
-  const GemvJob J = launch_job(P);
+  const GemvJob J = launch_job(P, (int)blockIdx.y);
   if ((int)blockIdx.x >= J.n_wg) return;
   const int nb = J.nb;
   const int ipr = 4 * nb;
@@ -1352,8 +1352,16 @@ __device__ __forceinline__ float q80_row_sum(float acc) {
   return tot;
 }
 
-template <int PRO, int MODE>
-__global__ void __launch_bounds__(256) k_gemv_f(GemvParams P) {
+// The body of k_gemv_f for workgroup bx of job by.  TAGX (PRO_QUANT): x is
+// the output of producers in the same launch, {value, tag} words at
+// P.x_tag, polled (every element this thread stages, bounded as
+// poll_tagged4) after the weights and the residual are issued.  TAGY
+// (MODE_BIAS): each output y[r] is also stored as a {value, tag} word at
+// P.y_tag[J.spare + r].
+template <int PRO, int MODE, bool TAGX = false, bool TAGY = false>
+__device__ __forceinline__ void gemv_f_body(const int bx, const int by, const GemvParams& P, const uint32_t tag) {
+  static_assert(!TAGX || PRO == PRO_QUANT, "tagged input feeds the plain prologue");
+  static_assert(!TAGY || MODE == MODE_BIAS, "tagged output from the bias epilogue");
   constexpr bool PAIRED = (MODE == MODE_SWIGLU);
   constexpr bool NORM = (PRO == PRO_NORM || PRO == PRO_EMBED_NORM || PRO == PRO_ARGMAX_EMBED_NORM);
   extern __shared__ __align__(16) unsigned char smem[];
@@ -1365,12 +1373,12 @@ __global__ void __launch_bounds__(256) k_gemv_f(GemvParams P) {
   __shared__ float inv_slot;
   __shared__ ArgCand ared[4];
 
-  const GemvJob J = launch_job(P);
-  if ((int)blockIdx.x >= J.n_wg) return;
+  const GemvJob J = launch_job(P, by);
+  if (bx >= J.n_wg) return;
   const int tid = threadIdx.x;
   const bool q50 = (J.type == T_Q5_0);
   const int R = J.rpw;
-  const int row0 = (int)blockIdx.x * R;
+  const int row0 = bx * R;
   // Q5_0: thread = (block b, row r) block-major; Q8_0: row tid/8, lane tid%8
   const int b5 = tid / R, r5 = tid - (tid / R) * R;
   const int r_local = q50 ? r5 : (tid >> 3);
@@ -1412,7 +1420,7 @@ __global__ void __launch_bounds__(256) k_gemv_f(GemvParams P) {
     xp[(b * 8 + (kk & 7)) * 4 + (kk >> 3)] = v;
   };
   if (NORM) {
-    if (PRO != PRO_NORM && blockIdx.x == 0 && blockIdx.y == 0) {  // layer 0 publishes the embedded token
+    if (PRO != PRO_NORM && bx == 0 && by == 0) {  // layer 0 publishes the embedded token
       if (4 * tid < P.n_x) reinterpret_cast<float4*>(P.x_out)[tid] = xa;
       if (tid == 0) {
         const int pos = P.state->pos;
@@ -1429,6 +1437,25 @@ __global__ void __launch_bounds__(256) k_gemv_f(GemvParams P) {
       put(4 * tid + 2, xn.z);
       put(4 * tid + 3, xn.w);
     }
+  } else if constexpr (TAGX) {
+    // up to 4 elements per thread (n_x <= 1024), polled together
+    uint64_t v[4];
+    bool ready = false;
+    for (int spin = 0; spin < TAG_WAIT_POLLS && !ready; ++spin) {
+      ready = true;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int e = tid + 256 * k;
+        v[k] = (e < nb8 * 32) ? __hip_atomic_load(&P.x_tag[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                              : ((uint64_t)tag << 32);
+        ready = ready && (uint32_t)(v[k] >> 32) == tag;
+      }
+      if (!ready) __builtin_amdgcn_s_sleep(1);
+    }
+    if (!ready) __hip_atomic_store(P.wait_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (tid + 256 * k < nb8 * 32) put(tid + 256 * k, __uint_as_float((uint32_t)v[k]));
   } else {
     for (int e = tid; e < nb8 * 32; e += 256) put(e, P.x[e]);
   }
@@ -1470,7 +1497,11 @@ __global__ void __launch_bounds__(256) k_gemv_f(GemvParams P) {
         const int n8 = J.rows - (J.rows % 8);
         J.y[r] = (r < n8) ? swiglu_poly(acc, acc2) : swiglu_tail(acc, acc2);
       } else if (MODE == MODE_BIAS) {
-        J.y[r] = J.bias ? acc + yres : acc;
+        const float yv = J.bias ? acc + yres : acc;
+        J.y[r] = yv;
+        if constexpr (TAGY)
+          __hip_atomic_store(&P.y_tag[J.spare + r], ((uint64_t)tag << 32) | __float_as_uint(yv), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
       } else if (MODE == MODE_RESID) {
         J.y[r] = yres + acc;
       } else {
@@ -1478,6 +1509,11 @@ __global__ void __launch_bounds__(256) k_gemv_f(GemvParams P) {
       }
     }
   }
+}
+
+template <int PRO, int MODE>
+__global__ void __launch_bounds__(256) k_gemv_f(GemvParams P) {
+  gemv_f_body<PRO, MODE>((int)blockIdx.x, (int)blockIdx.y, P, 0u);
 }
 
 #define C2H_GEMV_F(PRO_, MODE_) template __global__ void k_gemv_f<PRO_, MODE_>(GemvParams);
@@ -2162,6 +2198,44 @@ C2H_ATTN_BLOCK(ATT_TIER_96, 3)
 C2H_ATTN_BLOCK(ATT_TIER_128, 3)
 C2H_ATTN_BLOCK(ATT_TIER_256, 3)
 C2H_ATTN_BLOCK(ATT_TIER_ANY, 3)
+
+// The same launch for float-input projections (Q5_0 / Q8_0, the published
+// file's q/k/v/o): k_gemv_f<PRO_NORM, MODE_BIAS>'s workgroups for q|k|v
+// (job b / W), the attention, then k_gemv_f<PRO_QUANT, MODE_RESID>'s for
+// the o-projection on the tagged attention output.  xp and the low half of
+// xw are unused (the float GEMV reads x through Gq.x).
+template <int TIER>
+__global__ void __launch_bounds__(256)
+    k_attn_block_f(C2hState* __restrict__ st, float* __restrict__ kv, const float* __restrict__ xp, int xw,
+                   const uint64_t* __restrict__ qkv_tag, int dims, int max_ctx, AttnCoreParams P, GemvParams Gq,
+                   GemvParams Go) {
+  const int b = (int)blockIdx.x;
+  const int w = xw >> 16, nq = 3 * w;
+  const uint32_t tag = (uint32_t)st->epoch * 256u + (uint32_t)(dims & 0xff);
+  if (b < nq) {
+    const int by = b / w;
+    gemv_f_body<PRO_NORM, MODE_BIAS, false, true>(b - by * w, by, Gq, tag);
+    return;
+  }
+  const int n_attn = P.n_attn_wg;
+  if (b < nq + n_attn) {
+    attn_core_body<TIER, true, true>(b - nq, 0, 0, st, kv, nullptr, nullptr, nullptr, dims, max_ctx, P, qkv_tag);
+    return;
+  }
+  gemv_f_body<PRO_QUANT, MODE_RESID, true>(b - nq - n_attn, 0, Go, tag);
+}
+template __global__ void k_attn_block_f<ATT_TIER_32>(C2hState*, float*, const float*, int, const uint64_t*, int, int,
+                                                     AttnCoreParams, GemvParams, GemvParams);
+template __global__ void k_attn_block_f<ATT_TIER_64>(C2hState*, float*, const float*, int, const uint64_t*, int, int,
+                                                     AttnCoreParams, GemvParams, GemvParams);
+template __global__ void k_attn_block_f<ATT_TIER_96>(C2hState*, float*, const float*, int, const uint64_t*, int, int,
+                                                     AttnCoreParams, GemvParams, GemvParams);
+template __global__ void k_attn_block_f<ATT_TIER_128>(C2hState*, float*, const float*, int, const uint64_t*, int, int,
+                                                      AttnCoreParams, GemvParams, GemvParams);
+template __global__ void k_attn_block_f<ATT_TIER_256>(C2hState*, float*, const float*, int, const uint64_t*, int, int,
+                                                      AttnCoreParams, GemvParams, GemvParams);
+template __global__ void k_attn_block_f<ATT_TIER_ANY>(C2hState*, float*, const float*, int, const uint64_t*, int, int,
+                                                      AttnCoreParams, GemvParams, GemvParams);
 
 #define C2H_ATTN_OPROJ(TIER_, NB_)                                                                                  \
   template __global__ void k_attn_oproj<TIER_, NB_>(C2hState*, float*, const float*, const float*, const float*, int, \
