@@ -1391,7 +1391,15 @@ __device__ __forceinline__ void gemv_f_body(const int bx, const int by, const Ge
   // ---- loads
   float4 xa = make_float4(0.0f, 0.0f, 0.0f, 0.0f), nw = xa;
   int tok = 0;
+  // PRO_NORM (n_x <= 1024 here): every wave sums x*x itself from its own
+  // loads, lane l from x[16l, 16l+16), as k_gemv_row's norm waves do (no LDS
+  // round trip, no barrier)
+  float4 xs[SPEC_C / 4];
   if (PRO == PRO_NORM) {
+    const float4* x4 = reinterpret_cast<const float4*>(P.x);
+    const int last4 = (P.n_x >> 2) - 1;
+#pragma unroll
+    for (int k = 0; k < SPEC_C / 4; ++k) xs[k] = x4[min(4 * (tid & 63) + k, last4)];
     xa = load4(P.x, P.n_x);
   } else if (NORM) {
     tok = (PRO == PRO_ARGMAX_EMBED_NORM) ? reduce_argmax_partials<256>(P.part_v, P.part_i, P.n_part, ared)
@@ -1429,7 +1437,7 @@ __device__ __forceinline__ void gemv_f_body(const int bx, const int by, const Ge
         publish_token(P, tok);
       }
     }
-    const float inv = rms_inv4(xa, P.n_x, P.eps, sq, &inv_slot);
+    const float inv = (PRO == PRO_NORM) ? rms_inv_regs(xs, P.n_x, P.eps) : rms_inv4(xa, P.n_x, P.eps, sq, &inv_slot);
     const float4 xn = norm4(xa, inv, nw);
     if (4 * tid < P.n_x) {
       put(4 * tid, xn.x);
@@ -1469,7 +1477,24 @@ __device__ __forceinline__ void gemv_f_body(const int bx, const int by, const Ge
       if (PAIRED) terms[PAIRED ? 1 : 0][r5 * nb8 + b5] = q50_term(w5b, xq + b5 * GF_XPAD);
     }
     __syncthreads();
-    if (tid < R) {
+    if (tid < R && nb8 <= 32) {
+      // the row's terms read in one batch, then added in block order (blocks
+      // past nb8 are skipped, not added as zeros)
+      float ta[32], tb[PAIRED ? 32 : 1];
+      // (unconditional reads at clamped indices: issued together, one wait)
+#pragma unroll
+      for (int b = 0; b < 32; ++b) {
+        ta[b] = terms[0][tid * nb8 + min(b, nb8 - 1)];
+        if (PAIRED) tb[PAIRED ? b : 0] = terms[PAIRED ? 1 : 0][tid * nb8 + min(b, nb8 - 1)];
+      }
+#pragma unroll
+      for (int b = 0; b < 32; ++b) {
+        if (b < nb8) {  // uniform
+          acc = acc + ta[b];
+          if (PAIRED) acc2 = acc2 + tb[PAIRED ? b : 0];
+        }
+      }
+    } else if (tid < R) {  // wider rows (a Q5_0 ffn_down): one row per workgroup
       for (int b = 0; b < nb8; ++b) acc = acc + terms[0][tid * nb8 + b];
       if (PAIRED)
         for (int b = 0; b < nb8; ++b) acc2 = acc2 + terms[PAIRED ? 1 : 0][tid * nb8 + b];

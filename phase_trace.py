@@ -23,6 +23,8 @@ tier's stamps wave by wave instead.
     python phase_trace.py run        # GPU
     python phase_trace.py run 512    # GPU, long-context attention
     python phase_trace.py run 48 qwen3   # GPU, the Qwen3-1.7B shape's GEMVs
+    python phase_trace.py run 48 real-formats   # GPU, the published format mix (k_gemv_f stamps:
+                                                # x = staged in LDS, items = block terms in LDS)
 """
 from __future__ import annotations
 
@@ -61,6 +63,18 @@ __device__ __forceinline__ int phase_kind() {
     for (int k_ = 0; k_ < 16; ++k_) ph_s_[threadIdx.x >> 6][k_] = 0
 #define PH_G(k) do { if ((threadIdx.x & 63) == 0) ph_s_[threadIdx.x >> 6][k] = __builtin_amdgcn_s_memtime(); } while (0)
 #define PH_G_END do { const int kd_ = phase_kind<NB, PRO, MODE>(); \
+  if (kd_ >= 0 && (threadIdx.x & 63) == 0 && by == 0 && (bx == 0 || bx == J.n_wg - 1)) \
+    for (int k_ = 0; k_ < 16; ++k_) \
+      g_phase[kd_][bx == 0 ? 0 : 1][threadIdx.x >> 6][k_] = ph_s_[threadIdx.x >> 6][k_]; } while (0)
+// k_gemv_f's body (float-input projections) stamps into the same slots
+template <int PRO, int MODE>
+__device__ __forceinline__ int phase_kind_f() {
+  return (PRO == PRO_NORM && MODE == MODE_BIAS)       ? 0
+         : (PRO == PRO_QUANT && MODE == MODE_RESID)   ? 1
+         : (PRO == PRO_NORM && MODE == MODE_SWIGLU)   ? 2
+                                                      : -1;
+}
+#define PH_F_END do { const int kd_ = phase_kind_f<PRO, MODE>(); \
   if (kd_ >= 0 && (threadIdx.x & 63) == 0 && by == 0 && (bx == 0 || bx == J.n_wg - 1)) \
     for (int k_ = 0; k_ < 16; ++k_) \
       g_phase[kd_][bx == 0 ? 0 : 1][threadIdx.x >> 6][k_] = ph_s_[threadIdx.x >> 6][k_]; } while (0)
@@ -148,6 +162,19 @@ def instrument(kernels: str) -> str:
                    ("  if (tid < HD) {\n    acc = __builtin_fmaf(sc[pos], v_s[d], acc);\n",
                     "  PH_A(7);\n  if (tid < HD) {\n    acc = __builtin_fmaf(sc[pos], v_s[d], acc);\n"),
                ]).replace("PH_END;", "PH_A(8);\n  PH_A_END;", 1)
+    # float-input projections (k_gemv_f): entry, args, issued, norm_start, norm_end, x (staged in LDS),
+    # items (the block terms in LDS), end
+    s = _patch(s, "__device__ __forceinline__ void gemv_f_body(",
+               "template <int PRO, int MODE>\n__global__ void __launch_bounds__(256) k_gemv_f(GemvParams P) {", [
+                   ("  constexpr bool PAIRED = (MODE == MODE_SWIGLU);\n",
+                    "  constexpr bool PAIRED = (MODE == MODE_SWIGLU);\n  PH_DECL;\n  PH_G(0);\n"),
+                   ("  if (bx >= J.n_wg) return;\n", "  if (bx >= J.n_wg) return;\n  PH_G(1);\n"),
+                   ("  issue_fence();\n\n  // ---- prologue: x (normalised", "  issue_fence();\n  PH_G(2);\n\n  // ---- prologue: x (normalised"),
+                   ("    const float inv = (PRO == PRO_NORM) ? rms_inv_regs(xs, P.n_x, P.eps) : rms_inv4(xa, P.n_x, P.eps, sq, &inv_slot);\n",
+                    "    PH_G(9);\n    const float inv = (PRO == PRO_NORM) ? rms_inv_regs(xs, P.n_x, P.eps) : rms_inv4(xa, P.n_x, P.eps, sq, &inv_slot);\n    PH_G(4);\n"),
+                   ("  __syncthreads();\n\n  // ---- items and the per-row fold", "  __syncthreads();\n  PH_G(3);\n\n  // ---- items and the per-row fold"),
+                   ("    __syncthreads();\n    if (tid < R && nb8 <= 32) {", "    __syncthreads();\n    PH_G(7);\n    if (tid < R && nb8 <= 32) {"),
+               ]).replace("PH_END;", "PH_G(8);\n  PH_F_END;", 1)
     # head_dim 128: entry, args, issued, pos, qkv (q|k|v in LDS), rope (QK-norm and RoPE done), scores, max,
     # exp, sum, softmax (normalised), av, end
     s = _patch(s, "template <int VCH>\n__global__ void __launch_bounds__(256) k_attn_h128(AttnCoreParams P) {",
@@ -233,7 +260,7 @@ def run(last: int = 48, model: str = "qwen2.5-0.5b") -> None:
 
     from c2slm_amd import _lib as H
     from c2slm_amd import gguf as G
-    shape = {"qwen2.5-0.5b": G.QWEN05B, "qwen3": G.QWEN3_1_7B}[model]
+    shape = {"qwen2.5-0.5b": G.QWEN05B, "qwen3": G.QWEN3_1_7B, "real-formats": G.QWEN05B_REAL_FORMATS}[model]
     path = f"/tmp/c2h_phase_{model}.gguf"
     if not os.path.exists(path):
         G.write_synthetic_model(path, shape, seed=20261201)
@@ -281,8 +308,8 @@ def run(last: int = 48, model: str = "qwen2.5-0.5b") -> None:
 if __name__ == "__main__":
     if len(sys.argv) not in (2, 3, 4) or sys.argv[1] not in ("build", "run") or (
             len(sys.argv) >= 3 and (sys.argv[1] != "run" or not sys.argv[2].isdigit())) or (
-            len(sys.argv) == 4 and sys.argv[3] not in ("qwen2.5-0.5b", "qwen3")):
-        sys.exit("usage: python phase_trace.py build | run [positions [qwen2.5-0.5b | qwen3]]")
+            len(sys.argv) == 4 and sys.argv[3] not in ("qwen2.5-0.5b", "qwen3", "real-formats")):
+        sys.exit("usage: python phase_trace.py build | run [positions [qwen2.5-0.5b | qwen3 | real-formats]]")
     if sys.argv[1] == "build":
         print(build())
     else:
