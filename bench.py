@@ -10,8 +10,9 @@ steps are timed.  A step is the reference's generate-loop body
 then Forward(best, pos); only the chosen id crosses to the host each step.
 
 Prints one JSON line: value = K / wall time of the K steps on one GPU; the
-roofline of ffn_in, the layer kernel that moves the most bytes (RMSNorm +
-Q8_K + gate/up Q4_K GEMV + SwiGLU; eager launches back to back over the 24
+roofline of the FFN launch, the decode launch that moves the most bytes
+(k_ffn_block: RMSNorm + Q8_K + gate/up Q4_K GEMV + SwiGLU, then the Q6_K
+down projection and the residual; eager launches back to back over the 24
 layers' weights, paced by the GPU, between one pair of HIP events: the
 per-dispatch time a kernel trace of `bench.py --only roofline` records);
 and the CPU baseline (the reference's CPU path restated in C with its AVX2
@@ -165,40 +166,49 @@ def kernel_bytes(gf, desc, T: float) -> dict:
         "final_norm": int(4 * 3 * E),
         "vocab": int(vocab_w + 4 * E + 4 * 64 + 4),                # + normX, window ids, chosen id
     }
-    # the fused launches: the sum of their parts (the handed-over q|k|v and
-    # attention output counted once written, once read, as between kernels)
+    # the fused launches: the sum of their parts (the handed-over q|k|v,
+    # attention output and h counted once written, once read, as between
+    # kernels; the FFN's residual add, which the next k_attn_block does from
+    # the down projection's 19 terms per row, counted with the FFN)
     b["attn_block"] = b["qkv"] + b["attn"] + b["attn_out"]
     b["attn_oproj"] = b["attn"] + b["attn_out"]
+    b["ffn_block"] = b["ffn_in"] + b["ffn_out"]
     return b
 
 
 def step_launches(n_layers: int) -> dict:
     """Launches of each decode kernel per step.  The Qwen2.5-0.5B shape has
     the fused attention launches (k_attn_block on layers past 0, qkv then
-    k_attn_oproj on layer 0) unless C2H_NO_FUSE selects the separate forms
-    (=1: every kernel on its own; =qkv: qkv on its own, attention and the
-    o-projection fused)."""
+    k_attn_oproj on layer 0) and, on every layer but the last, the FFN as
+    one launch (k_ffn_block) whose residual add the next k_attn_block does,
+    unless C2H_NO_FUSE selects the separate forms (=1: every kernel on its
+    own; =qkv: qkv on its own, attention and the o-projection fused, the
+    FFN's two launches apart; =ffn: the FFN's two launches apart)."""
     nf = os.environ.get("C2H_NO_FUSE", "")
     L = n_layers
-    n = dict(qkv=L, attn=0, attn_out=0, attn_block=0, attn_oproj=0, ffn_in=L, ffn_out=L, final_norm=1, vocab=1)
+    n = dict(qkv=1, attn=0, attn_out=0, attn_block=L - 1, attn_oproj=1, ffn_in=1, ffn_out=1, ffn_block=L - 1,
+             final_norm=1, vocab=1)
+    if nf in ("1", "qkv", "ffn"):
+        n.update(ffn_in=L, ffn_out=L, ffn_block=0)
     if nf == "1":
-        n.update(attn=L, attn_out=L)
+        n.update(qkv=L, attn=L, attn_out=L, attn_block=0, attn_oproj=0)
     elif nf == "qkv":
-        n.update(attn_oproj=L)
-    else:
-        n.update(qkv=1, attn_oproj=1, attn_block=L - 1)
+        n.update(qkv=L, attn_oproj=L, attn_block=0)
     return n
 
 
-# The roofline line's kernel: the decode layer kernel with the most bytes per
-# launch (two 4864 x 896 Q4_K matrices), fixed so the line does not depend on
-# which kernel a run's timings make the largest.
-ROOFLINE_KERNEL = "ffn_in"
+# The roofline line's kernel: the decode launch with the most bytes (the
+# layer's FFN: two 4864 x 896 Q4_K matrices and a 896 x 4864 Q6_K one),
+# fixed so the line does not depend on which kernel a run's timings make the
+# largest; ffn_in (the two Q4_K matrices) where C2H_NO_FUSE runs the FFN's
+# launches apart.
+ROOFLINE_KERNEL = "ffn_in" if os.environ.get("C2H_NO_FUSE", "") in ("1", "qkv", "ffn") else "ffn_block"
 
 KERNEL_NAMES = {"qkv": "k_gemv_row<3, PRO_NORM, MODE_BIAS>", "attn": "k_attn_core",
                 "attn_out": "k_gemv_row<3, PRO_QUANT, MODE_RESID>", "ffn_in": "k_gemv_row<3, PRO_NORM, MODE_SWIGLU>",
                 "ffn_out": "k_gemv_row<19, PRO_QUANT, MODE_RESID>", "final_norm": "k_rmsnorm",
-                "vocab": "k_vocab<28>", "attn_block": "k_attn_block<TIER, 3>", "attn_oproj": "k_attn_oproj<TIER, 3>"}
+                "vocab": "k_vocab<28>", "attn_block": "k_attn_block<TIER, 3>", "attn_oproj": "k_attn_oproj<TIER, 3>",
+                "ffn_block": "k_ffn_block<3, 19>"}
 
 
 def decode_kernels(ctx, gf, desc, vocab_ms, step_ms, T, iters: int = 96):
@@ -232,8 +242,8 @@ def decode_kernels(ctx, gf, desc, vocab_ms, step_ms, T, iters: int = 96):
 
 
 def roofline_timing(ctx, gf, desc, prompt, iters: int):
-    """The roofline line's kernel (ffn_in) on a fixed state: the prompt
-    ingested by one batched prefill (which launches no k_gemv_row), then
+    """The roofline line's kernel (ffn_block) on a fixed state: the prompt
+    ingested by one batched prefill (which launches no decode layer kernel), then
     `iters` eager launches back to back over the 24 layers' weights, paced by
     the GPU, between one pair of HIP events.  The kernel's time depends on
     its input (the exact RMSNorm sum takes more rounds on some rows), so the

@@ -259,7 +259,7 @@ class Ctx:
         return ms.value
 
     KERNELS = ("qkv", "attn", "attn_out", "ffn_in", "ffn_out", "final_norm", "attn_block",
-               "attn_oproj")  # C2H_KERNEL_*
+               "attn_oproj", "ffn_block")  # C2H_KERNEL_*
 
     def time_layer_kernel(self, kernel: str, iters: int, captured: bool = False) -> float:
         """ms per launch of one decoder-layer kernel (c2h_time_layer_kernel):

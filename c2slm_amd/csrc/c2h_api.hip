@@ -57,8 +57,11 @@ struct c2h_ctx {
   float *X = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *h = nullptr;
   uint64_t* attn_tag = nullptr;  // the attention output as {value, tag} words (k_attn_oproj)
   uint64_t* qkv_tag = nullptr;   // q|k|v as {value, tag} words (k_attn_block)
+  uint64_t* h_tag = nullptr;     // the SwiGLU output as {value, tag} words (k_ffn_block)
+  float* dterm = nullptr;        // k_ffn_block's down terms [FOLD_NB][n_embd], added to X by the next k_attn_block
   bool fuse_oproj = true;        // attention and o-projection in one launch where an instance exists
   bool fuse_qkv = true;          // and qkv with them (layers past 0)
+  bool fuse_ffn = true;          // ffn_in and ffn_out in one launch where an instance exists
   bool h128_staged = false;      // head_dim 128: k_attn_h128<H128_VCH> (V through LDS) fits beside the scores
   float* normx[2] = {nullptr, nullptr};
   int nx_cur = 0, nx_prev = 0;
@@ -878,7 +881,8 @@ void enqueue_attn_oproj(c2h_ctx* c, int l, int form) {
 // x(RMSNorm(X)) + bias on 3 W workgroups (job-major, W the widest job's
 // count), stored tagged as well, then the two parts of k_attn_oproj, the
 // attention's reading q|k|v tagged
-void enqueue_attn_block(c2h_ctx* c, int l, int form) {
+// pend: the previous layer's k_ffn_block left its terms for X (dterm)
+void enqueue_attn_block(c2h_ctx* c, int l, int form, bool pend) {
   const c2h_model_desc& D = c->desc;
   Layer& L = c->layers[l];
   const int E = D.n_embd, KVd = D.n_kv_heads * D.head_dim;
@@ -897,11 +901,15 @@ void enqueue_attn_block(c2h_ctx* c, int l, int form) {
   Q.norm_w = L.attn_norm;
   Q.nb_in = nb_k(E);
   Q.y_tag = c->qkv_tag;
+  Q.x_pend = pend ? c->dterm : nullptr;
+  Q.pend_n = E;
   prep_gemv_row(Q);
   int w = 1;
   for (int j = 0; j < Q.n_jobs; ++j) w = std::max(w, Q.jobs[j].n_wg);
   const AttnCoreParams A = fused_attn_params(c, l);
-  const GemvParams P = fused_oproj_params(c, l);
+  GemvParams P = fused_oproj_params(c, l);
+  P.x_pend = Q.x_pend;
+  P.pend_n = E;
   const size_t lds = std::max(c->attn_lds, (size_t)Q.n_x_lds * sizeof(float));
   hipLaunchKernelGGL(attn_block_kernel(form), dim3(3 * w + A.n_attn_wg + P.jobs[0].n_wg), dim3(256), lds, c->stream,
                      A.state, A.kv, (const float*)c->X, E | (w << 16), (const uint64_t*)c->qkv_tag,
@@ -923,6 +931,48 @@ void enqueue_ffn_in(c2h_ctx* c, int l) {
 // ffn_out: X += Wd * x(h)
 void enqueue_ffn_out(c2h_ctx* c, int l) {
   launch_group(c, {{&c->layers[l].wd, nullptr, c->X, nullptr}}, PRO_QUANT, MODE_RESID, c->h, c->desc.n_ff, nullptr);
+}
+
+// Whether layer l's FFN runs as one launch (k_ffn_block) that leaves its
+// residual add to the next layer's k_attn_block: K-quant gate/up of 3
+// super-blocks per row, a Q6_K down projection of FOLD_NB (the instance
+// built), and a next layer that runs k_attn_block at this form.
+bool defer_ffn(const c2h_ctx* c, int l, int form) {
+  const Layer& L = c->layers[l];
+  return c->fuse_ffn && l + 1 < c->desc.n_layers && nb_k(c->desc.n_embd) == 3 &&
+         nb_k(c->desc.n_ff) == FOLD_NB && !float_input(L.wg.type) && !float_input(L.wu.type) &&
+         L.wd.type == C2H_Q6_K && fuse_attn_block(c, l + 1, form);
+}
+
+// ffn_in + ffn_out but for the residual add in one launch: gate|up stores h
+// tagged, the down projection runs by super-block on the tagged h and
+// leaves its terms in dterm for the next k_attn_block to add to X
+void enqueue_ffn_block(c2h_ctx* c, int l) {
+  const c2h_model_desc& D = c->desc;
+  Layer& L = c->layers[l];
+  GemvParams I = base_params(c);
+  add_job(I, L.wg, &L.wu, MODE_SWIGLU, c->h, nullptr, nullptr);
+  I.jobs[0].spare = 0;
+  I.prologue = PRO_NORM;
+  I.x = c->X;
+  I.x_out = c->X;
+  I.n_x = D.n_embd;
+  I.n_x_lds = chain_lds_floats(D.n_embd);
+  I.norm_w = L.ffn_norm;
+  I.nb_in = nb_k(D.n_embd);
+  I.y_tag = c->h_tag;
+  prep_gemv_row(I);
+  GemvParams O = base_params(c);
+  add_job(O, L.wd, nullptr, MODE_RESID, c->dterm, nullptr, nullptr);
+  O.jobs[0].n_wg = FOLD_NB * ((D.n_embd + 127) / 128);  // down_block_body workgroups
+  O.x = c->h;
+  O.n_x = D.n_ff;
+  O.x_tag = c->h_tag;
+  O.wait_err = c->tok_host + 2;
+  const int n_in = I.jobs[0].n_wg;
+  hipLaunchKernelGGL((k_ffn_block<3, FOLD_NB>), dim3(n_in + O.jobs[0].n_wg), dim3(512),
+                     (size_t)I.n_x_lds * sizeof(float), c->stream, (const float*)c->X, D.n_embd | (n_in << 16),
+                     c->state_dev, l, I, O);
 }
 
 // k_rmsnorm holds one float4 per thread
@@ -956,9 +1006,10 @@ void enqueue_final_norm(c2h_ctx* c, int advance = 0) {
 // either state->token (forward) or the argmax of the vocab partials (step).
 // form selects the attention kernels.
 void enqueue_layers(c2h_ctx* c, bool from_argmax, int form) {
+  bool pend = false;  // the previous layer's FFN left its residual add to this layer's k_attn_block
   for (int l = 0; l < c->desc.n_layers; ++l) {
     if (fuse_attn_block(c, l, form)) {
-      enqueue_attn_block(c, l, form);
+      enqueue_attn_block(c, l, form, pend);
     } else if (fuse_attn_block_f(c, l, form)) {
       enqueue_attn_block_f(c, l, form);
     } else {
@@ -970,8 +1021,13 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax, int form) {
         enqueue_attn_out(c, l);
       }
     }
-    enqueue_ffn_in(c, l);
-    enqueue_ffn_out(c, l);
+    pend = defer_ffn(c, l, form);
+    if (pend) {
+      enqueue_ffn_block(c, l);
+    } else {
+      enqueue_ffn_in(c, l);
+      enqueue_ffn_out(c, l);
+    }
   }
   enqueue_final_norm(c, from_argmax ? 1 : 0);
 }
@@ -1186,10 +1242,12 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   }
   const char* ng = getenv("C2H_NO_GRAPH");
   c->use_graphs = !(ng && ng[0] == '1');
-  // measurement aid: C2H_NO_FUSE=1 separate launches, =qkv qkv on its own
+  // measurement aid: C2H_NO_FUSE=1 separate launches, =qkv qkv on its own,
+  // =ffn the FFN's two launches apart
   const char* nf = getenv("C2H_NO_FUSE");
   c->fuse_oproj = !(nf && nf[0] == '1');
   c->fuse_qkv = c->fuse_oproj && !(nf && strcmp(nf, "qkv") == 0);
+  c->fuse_ffn = c->fuse_oproj && !(nf && strcmp(nf, "ffn") == 0);
   void* pinned = nullptr;
   if (hipHostMalloc(&pinned, sizeof(C2hState) * kStateRing + 64, hipHostMallocDefault) != hipSuccess) return bail(C2H_ERR_HIP);
   c->state_ring = reinterpret_cast<C2hState*>(pinned);
@@ -1239,11 +1297,14 @@ int c2h_create(const c2h_model_desc* desc, int device, c2h_ctx** out) {
   if ((rc = dalloc(c, &c->X, E * 4)) || (rc = dalloc(c, &c->q, E * 4)) || (rc = dalloc(c, &c->k, KV * 4)) ||
       (rc = dalloc(c, &c->v, KV * 4)) || (rc = dalloc(c, &c->attn, E * 4)) || (rc = dalloc(c, &c->h, F * 4)) ||
       (rc = dalloc(c, &c->normx[0], E * 4)) || (rc = dalloc(c, &c->normx[1], E * 4)) ||
-      (rc = dalloc(c, &c->attn_tag, (size_t)E * 8)) || (rc = dalloc(c, &c->qkv_tag, (size_t)(E + 2 * KV) * 8)))
+      (rc = dalloc(c, &c->attn_tag, (size_t)E * 8)) || (rc = dalloc(c, &c->qkv_tag, (size_t)(E + 2 * KV) * 8)) ||
+      (rc = dalloc(c, &c->h_tag, (size_t)F * 8)) || (rc = dalloc(c, &c->dterm, (size_t)FOLD_NB * E * 4)))
     return bail(rc);
   // tag 0xffffffff: no launch's (its layer field would be 255)
   if (hipMemsetAsync(c->attn_tag, 0xff, (size_t)E * 8, c->stream) != hipSuccess ||
-      hipMemsetAsync(c->qkv_tag, 0xff, (size_t)(E + 2 * KV) * 8, c->stream) != hipSuccess)
+      hipMemsetAsync(c->qkv_tag, 0xff, (size_t)(E + 2 * KV) * 8, c->stream) != hipSuccess ||
+      hipMemsetAsync(c->h_tag, 0xff, (size_t)F * 8, c->stream) != hipSuccess ||
+      hipMemsetAsync(c->dterm, 0, (size_t)FOLD_NB * E * 4, c->stream) != hipSuccess)
     return bail(C2H_ERR_HIP);
   size_t kv_bytes = (size_t)2 * D.n_layers * D.n_kv_heads * kv_slot(D.max_ctx) * D.head_dim * 4;
   if ((rc = dalloc(c, &c->kv, kv_bytes))) return bail(rc);
@@ -2645,7 +2706,7 @@ int c2h_time_steps(c2h_ctx* c, int32_t pos, int32_t iters, float penalty, int32_
 
 
 int c2h_time_layer_kernel(c2h_ctx* c, int32_t kernel, int32_t iters, int32_t captured, float* ms) {
-  if (!c || !ms || iters <= 0 || iters > 100000 || kernel < 0 || kernel > C2H_KERNEL_ATTN_OPROJ) return C2H_ERR_INVALID;
+  if (!c || !ms || iters <= 0 || iters > 100000 || kernel < 0 || kernel > C2H_KERNEL_FFN_BLOCK) return C2H_ERR_INVALID;
   HIPCHK(c, hipSetDevice(c->device));
   int rc = build_graphs(c);
   if (rc) return rc;
@@ -2671,6 +2732,8 @@ int c2h_time_layer_kernel(c2h_ctx* c, int32_t kernel, int32_t iters, int32_t cap
   if ((kernel == C2H_KERNEL_ATTN_BLOCK || kernel == C2H_KERNEL_ATTN_OPROJ) &&
       !(D.n_layers > 1 && fuse_attn_block(c, 1, form)))
     return fail(c, C2H_ERR_UNSUPPORTED, "no fused attention launch for this model or position");
+  if (kernel == C2H_KERNEL_FFN_BLOCK && !(D.n_layers > 1 && defer_ffn(c, 0, form)))
+    return fail(c, C2H_ERR_UNSUPPORTED, "no fused FFN launch for this model");
   // the residual kernels update X and the final norm writes normX[nx_out]:
   // both are restored afterwards
   float* saved = nullptr;
@@ -2685,8 +2748,9 @@ int c2h_time_layer_kernel(c2h_ctx* c, int32_t kernel, int32_t iters, int32_t cap
       case C2H_KERNEL_ATTN_OUT: enqueue_attn_out(c, l); break;
       case C2H_KERNEL_FFN_IN: enqueue_ffn_in(c, l); break;
       case C2H_KERNEL_FFN_OUT: enqueue_ffn_out(c, l); break;
-      case C2H_KERNEL_ATTN_BLOCK: enqueue_attn_block(c, l, form); break;
+      case C2H_KERNEL_ATTN_BLOCK: enqueue_attn_block(c, l, form, l > 0 && defer_ffn(c, l - 1, form)); break;
       case C2H_KERNEL_ATTN_OPROJ: enqueue_attn_oproj(c, l, form); break;
+      case C2H_KERNEL_FFN_BLOCK: enqueue_ffn_block(c, l); break;
       default: enqueue_final_norm(c); break;
     }
   };
@@ -2736,6 +2800,13 @@ int c2h_time_layer_kernel(c2h_ctx* c, int32_t kernel, int32_t iters, int32_t cap
   }
   if (ge) (void)hipGraphExecDestroy(ge);
   if (g) (void)hipGraphDestroy(g);
+  // the fused launches above left tags of the current epoch (launch i over
+  // layer i mod n_layers, so consecutive launches' tags differ): the next
+  // forward's launch of the last timed layer must not take them for its own
+  if (!rc) {
+    hipLaunchKernelGGL(k_next_epoch, dim3(1), dim3(64), 0, c->stream, c->state_dev);
+    if (hipGetLastError() != hipSuccess) rc = fail(c, C2H_ERR_HIP, "advancing the epoch failed");
+  }
   if (!rc && (hipMemcpyAsync(c->X, saved, (size_t)D.n_embd * 4, hipMemcpyDeviceToDevice, c->stream) != hipSuccess ||
               hipMemcpyAsync(nx_out, saved + D.n_embd, (size_t)D.n_embd * 4, hipMemcpyDeviceToDevice, c->stream) !=
                   hipSuccess))

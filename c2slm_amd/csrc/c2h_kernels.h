@@ -138,6 +138,11 @@ struct GemvParams {
   const uint64_t* x_tag;
   int* wait_err;
   uint64_t* y_tag;  // k_attn_block's q|k|v half: its outputs again as {value, tag} words (job offset in spare)
+  // k_attn_block's parts: X's pending terms [FOLD_NB][pend_n] (the previous
+  // layer's k_ffn_block down projection), added to X in block order before
+  // use (the qkv part's input, the o-projection's residual); nullptr: none
+  const float* x_pend;
+  int pend_n;
   int n_jobs;
   GemvJob jobs[MAX_JOBS];
 };
@@ -428,6 +433,15 @@ __global__ void k_attn_core(C2hState* st, float* kv, const float* qg, const floa
 // k_attn_core's XCD-grouped grid (P.n_attn_wg workgroups) followed by the
 // o-projection's k_gemv_row<NB, PRO_QUANT, MODE_RESID> workgroups of G,
 // 256 threads each, one launch; G.x_tag = P.out_tag
+// gate|up (xw >> 16 workgroups), then the Q6_K down projection by
+// super-block (Gd.jobs[0].n_wg = NBF * ceil(rows / 128) workgroups), 512
+// threads each, one launch; Gi.y_tag = Gd.x_tag (h); the terms go to
+// Gd.jobs[0].y as [NBF][rows], for the next k_attn_block to add to X
+// (GemvParams::x_pend)
+// the down blocks of the FFN launch, whose terms the next launch adds to X
+constexpr int FOLD_NB = 19;
+template <int NBE, int NBF>
+__global__ void k_ffn_block(const float* xp, int xw, C2hState* st, int layer, GemvParams Gi, GemvParams Gd);
 // qkv (3 W workgroups, W = xw >> 16), then k_attn_oproj's two parts, one
 // launch; Gq.y_tag = qkv_tag, Go.x_tag = P.out_tag
 template <int TIER, int NB>
@@ -541,6 +555,12 @@ __global__ void k_empty(const int* __restrict__ flag, int* __restrict__ out);
 // the host's enqueue rate.
 constexpr long long C2H_DELAY_MAX_TICKS = 1000000;  // 10 ms
 __global__ void k_delay(long long ticks);
+// st->epoch += 1 (one workgroup of 64): the tags launches store after it
+// differ from every tag stored before it
+__global__ void k_next_epoch(C2hState* st);
+// st->epoch += 1: the tags launches store after it differ from every tag
+// stored before it
+__global__ void k_next_epoch(C2hState* st);
 // Producer -> consumer wait in one launch (measurement of the cost of
 // replacing a kernel boundary by a counter wait).  Workgroups below n_prod
 // (mode 0) are producers: a dependent chain of `work` steps, then their

@@ -1001,13 +1001,18 @@ __device__ __forceinline__ void publish_token(const GemvParams& P, int tok) {
 // the weights, the job fields and the residual have been issued.  The wait
 // is bounded: a lane that runs out sets *P.wait_err (system scope) and goes
 // on with what it read.
-// TAGY (MODE_BIAS only): each output y[r] is also stored as a {value, tag}
-// word at P.y_tag[J.spare + r] for consumers in the same launch.
-template <int NB, int PRO, int MODE, bool TAGX, bool TAGY = false>
+// TAGY (MODE_BIAS, MODE_SWIGLU): each output y[r] is also stored as a
+// {value, tag} word at P.y_tag[J.spare + r] for consumers in the same launch.
+// PEND (PRO_NORM input or MODE_RESID residual, both X): where P.x_pend is
+// set, X's true value is X + the FOLD_NB pending terms of the previous FFN
+// launch, added from 0 in block order (as its own residual epilogue would)
+// and then to X; the terms load with X.
+template <int NB, int PRO, int MODE, bool TAGX, bool TAGY = false, bool PEND = false>
 __device__ __forceinline__ void gemv_row_body(const int bx, const int by, const float* __restrict__ xp, int n_xp,
                                               const GemvParams& P, const uint32_t tag) {
   static_assert(!TAGX || PRO == PRO_QUANT, "tagged input feeds the quantising prologue");
-  static_assert(!TAGY || MODE == MODE_BIAS, "tagged output from the bias epilogue");
+  static_assert(!TAGY || MODE == MODE_BIAS || MODE == MODE_SWIGLU, "tagged output from the bias or SwiGLU epilogue");
+  static_assert(!PEND || PRO == PRO_NORM || MODE == MODE_RESID, "pending terms add to X as input or residual");
   constexpr int NT = row_threads(NB, PRO, MODE);
   constexpr int NI = row_item_threads(NB, PRO, MODE);  // threads per matrix's items
   constexpr int NW = NT / 64;
@@ -1037,15 +1042,23 @@ __device__ __forceinline__ void gemv_row_body(const int bx, const int by, const 
   // themselves, lane l from x[16l, 16l+16)
   const bool sum_regs = (PRO == PRO_NORM) && n_xp <= 64 * SPEC_C;
   const int swave = __builtin_amdgcn_readfirstlane(wave);
+  const bool pend = PEND && P.x_pend != nullptr;  // uniform
   float4 xs[SPEC_C / 4];
+  float4 tx[PEND && PRO == PRO_NORM ? FOLD_NB : 1];
   if (PRO == PRO_NORM) {
-    if (sum_regs && swave < NB) {
+    if (sum_regs && swave < NB && !pend) {  // pending terms: from LDS once added
       const float4* x4 = reinterpret_cast<const float4*>(xp);
       const int last4 = (n_xp >> 2) - 1;
 #pragma unroll
       for (int k = 0; k < SPEC_C / 4; ++k) xs[k] = x4[min(4 * lane + k, last4)];
     }
     xa[0] = load4(xp, n_xp);
+    if constexpr (PEND && PRO == PRO_NORM) {
+      if (pend) {
+#pragma unroll
+        for (int k = 0; k < FOLD_NB; ++k) tx[k] = load4(P.x_pend + k * P.pend_n, n_xp);
+      }
+    }
   } else if (!NORM && !TAGX) {
 #pragma unroll
     for (int i = 0; i < BPW; ++i) xa[i] = reinterpret_cast<const float4*>(xp + min(wave + NW * i, NB - 1) * QK_K)[lane];
@@ -1082,6 +1095,13 @@ __device__ __forceinline__ void gemv_row_body(const int bx, const int by, const 
   if (PAIRED && !SPLIT) w2 = load_item(J.w2, J.type2, NB, row_c, b_c, u);
   float yres = 0.0f;
   if (MODE == MODE_RESID) yres = J.y[out_row];
+  float ty[PEND && MODE == MODE_RESID ? FOLD_NB : 1];
+  if constexpr (PEND && MODE == MODE_RESID) {
+    if (pend) {
+#pragma unroll
+      for (int k = 0; k < FOLD_NB; ++k) ty[k] = P.x_pend[k * P.pend_n + out_row];
+    }
+  }
   // an absent bias reads x instead (a valid address) and is not added
   if (MODE == MODE_BIAS) yres = (J.bias ? J.bias : xp)[J.bias ? out_row : 0];
   issue_fence();
@@ -1092,6 +1112,25 @@ __device__ __forceinline__ void gemv_row_body(const int bx, const int by, const 
 
   // ---- prologue: the Q8_K input row in LDS
   if (NORM) {
+    if constexpr (PEND && PRO == PRO_NORM) {
+      if (pend) {  // X + the pending terms; the register sums read it back from LDS
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int k = 0; k < FOLD_NB; ++k)
+          a = make_float4(a.x + tx[k].x, a.y + tx[k].y, a.z + tx[k].z, a.w + tx[k].w);
+        xa[0] = make_float4(xa[0].x + a.x, xa[0].y + a.y, xa[0].z + a.z, xa[0].w + a.w);
+        if (sum_regs) {
+          if (4 * tid < n_xp) reinterpret_cast<float4*>(sq)[tid] = xa[0];
+          __syncthreads();
+          if (swave < NB) {
+            const float4* s4 = reinterpret_cast<const float4*>(sq);
+            const int last4 = (n_xp >> 2) - 1;
+#pragma unroll
+            for (int k = 0; k < SPEC_C / 4; ++k) xs[k] = s4[min(4 * lane + k, last4)];
+          }
+        }
+      }
+    }
     if (PRO != PRO_NORM && bx == 0 && by == 0) {  // layer 0 publishes the embedded token
       if (4 * tid < n_xp) reinterpret_cast<float4*>(P.x_out)[tid] = xa[0];
       if (tid == 0) {
@@ -1140,7 +1179,11 @@ __device__ __forceinline__ void gemv_row_body(const int bx, const int by, const 
       }
       if (PAIRED) {
         const int n8 = J.rows - (J.rows % 8);
-        J.y[r] = (r < n8) ? swiglu_poly(acc, up) : swiglu_tail(acc, up);
+        const float yv = (r < n8) ? swiglu_poly(acc, up) : swiglu_tail(acc, up);
+        J.y[r] = yv;
+        if constexpr (TAGY)
+          __hip_atomic_store(&P.y_tag[J.spare + r], ((uint64_t)tag << 32) | __float_as_uint(yv), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
       } else if (MODE == MODE_BIAS) {
         const float yv = J.bias ? acc + yres : acc;
         J.y[r] = yv;
@@ -1148,7 +1191,16 @@ __device__ __forceinline__ void gemv_row_body(const int bx, const int by, const 
           __hip_atomic_store(&P.y_tag[J.spare + r], ((uint64_t)tag << 32) | __float_as_uint(yv), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
       } else {
-        J.y[r] = yres + acc;
+        float yr = yres;
+        if constexpr (PEND && MODE == MODE_RESID) {
+          if (pend) {
+            float a = 0.0f;
+#pragma unroll
+            for (int k = 0; k < FOLD_NB; ++k) a = a + ty[k];
+            yr = yr + a;
+          }
+        }
+        J.y[r] = yr + acc;
       }
     }
   }
@@ -1158,6 +1210,63 @@ template <int NB, int PRO, int MODE>
 __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(const float* __restrict__ xp, int n_xp, GemvParams P) {
   gemv_row_body<NB, PRO, MODE, false>((int)blockIdx.x, (int)blockIdx.y, xp, n_xp, P, 0u);
 }
+
+// The down projection split by super-block (a Q6_K matrix of NB blocks per
+// row, c2_tensor_gemv2_q6_k_q8_k_gen.go:168-209 per row): workgroup bx
+// takes block b = bx / ng of rows [128 g, 128 g + 128), g = bx % ng, one
+// quarter-item per thread.  Wave 0 polls the block's 256 inputs (tagged
+// words at P.x_tag), quantises that block alone (Q8_K blocks are
+// independent, c2_quantize_q8_k_gen.go:11-91), and every quad computes its
+// row's term f32(isum) * (d * q8d) as k_gemv_row's items do; the term goes
+// to J.y[b * rows + row] (block-major: whole cache lines per workgroup).
+// The weights are issued first.  The row's fold, X += the terms added in
+// block order from 0 (the Q6_K fold of fold_terms), is left to the next
+// launch (GemvParams::x_pend), past the kernel boundary.
+template <int NB>
+__device__ __forceinline__ void down_block_body(const int bx, const GemvParams& P, const uint32_t tag) {
+  static_assert(NB == FOLD_NB, "the next launch adds FOLD_NB terms");
+  __shared__ Q8KRow<NB> s;
+  const GemvJob J = P.jobs[0];
+  const int ng = (J.rows + 127) >> 7;
+  const int b = bx / ng, g = bx - b * ng;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int row = g * 128 + (tid >> 2), u = tid & 3;
+  const ItemW w = load_item(J.w, T_Q6_K, NB, min(row, J.rows - 1), b, u);
+  issue_fence();
+  if (wave == 0) {
+    const float4 v[1] = {poll_tagged4(P.x_tag + b * QK_K + 4 * lane, tag, P.wait_err)};
+    quantize_blocks<1>(v, b, 0, b + 1, s);
+  }
+  __syncthreads();
+  if (row < J.rows) {  // whole quads: a row's four quarters
+    const float t = item_value(w, T_Q6_K, s, b, u);
+    if (u == 0) J.y[(size_t)b * J.rows + row] = t;
+  }
+}
+
+// The FFN of one layer in one launch (engine/forward.go:120-131) but for
+// the residual add, 512 threads per workgroup: [0, xw >> 16) k_gemv_row<NBE,
+// PRO_NORM, MODE_SWIGLU>'s workgroups (gate|up of RMSNorm(X), SwiGLU; h
+// stored tagged as well, Gi.y_tag = Gd.x_tag), then Gd.jobs[0].n_wg
+// down_block_body workgroups (the Q6_K down projection by super-block, its
+// terms to Gd.jobs[0].y).  The down workgroups wait only for the gate|up
+// ones, dispatched before them; each reads 256 values of h, not all of it.
+// X is not written: the next launch (k_attn_block) adds the terms.  x and
+// its length (xw & 0xffff) are preloaded arguments.
+template <int NBE, int NBF>
+__global__ void __launch_bounds__(512)
+    k_ffn_block(const float* __restrict__ xp, int xw, C2hState* __restrict__ st, int layer, GemvParams Gi,
+                GemvParams Gd) {
+  static_assert(row_threads(NBE, PRO_NORM, MODE_SWIGLU) == 512, "gate|up runs 512-thread workgroups");
+  const int b = (int)blockIdx.x, n_in = xw >> 16;
+  const uint32_t tag = (uint32_t)st->epoch * 256u + (uint32_t)layer;
+  if (b < n_in) {
+    gemv_row_body<NBE, PRO_NORM, MODE_SWIGLU, false, true>(b, 0, xp, xw & 0xffff, Gi, tag);
+    return;
+  }
+  down_block_body<NBF>(b - n_in, Gd, tag);
+}
+template __global__ void k_ffn_block<3, 19>(const float*, int, C2hState*, int, GemvParams, GemvParams);
 
 #define C2H_GEMV_ROW(NB_, PRO_, MODE_) \
   template __global__ void k_gemv_row<NB_, PRO_, MODE_>(const float*, int, GemvParams);
@@ -2189,7 +2298,10 @@ __global__ void __launch_bounds__(256)
 // tagged as well (Gq.y_tag = qkv_tag); the next P.n_attn_wg run
 // k_attn_core's XCD-grouped grid on them (polled after the K/V rows are
 // issued); the rest run the o-projection of Go on the tagged attention
-// output.  x, its length (xw & 0xffff) and the tagged q|k|v arrive as
+// output.  Where Gq.x_pend / Go.x_pend are set, the previous layer's FFN
+// launch left its down-projection terms for X: the qkv part adds them to X
+// for its norm, the o-projection to its residual, and X is written with
+// them.  x, its length (xw & 0xffff) and the tagged q|k|v arrive as
 // preloaded kernel arguments with the state and the KV cache.
 template <int TIER, int NB>
 __global__ void __launch_bounds__(256)
@@ -2203,7 +2315,7 @@ __global__ void __launch_bounds__(256)
   if (b < nq) {
     const int by = b / w;
     const uint32_t tag = (uint32_t)st->epoch * 256u + (uint32_t)(dims & 0xff);
-    gemv_row_body<NB, PRO_NORM, MODE_BIAS, false, true>(b - by * w, by, xp, xw & 0xffff, Gq, tag);
+    gemv_row_body<NB, PRO_NORM, MODE_BIAS, false, true, true>(b - by * w, by, xp, xw & 0xffff, Gq, tag);
     return;
   }
   const int n_attn = P.n_attn_wg;
@@ -2212,7 +2324,7 @@ __global__ void __launch_bounds__(256)
     return;
   }
   const uint32_t tag = (uint32_t)st->epoch * 256u + (uint32_t)(dims & 0xff);
-  gemv_row_body<NB, PRO_QUANT, MODE_RESID, true>(b - nq - n_attn, 0, nullptr, 0, Go, tag);
+  gemv_row_body<NB, PRO_QUANT, MODE_RESID, true, false, true>(b - nq - n_attn, 0, nullptr, 0, Go, tag);
 }
 #define C2H_ATTN_BLOCK(TIER_, NB_)                                                                                 \
   template __global__ void k_attn_block<TIER_, NB_>(C2hState*, float*, const float*, int, const uint64_t*, int, int, \
@@ -4029,6 +4141,10 @@ __global__ void __launch_bounds__(64) k_delay(long long ticks) {
   const long long t0 = (long long)__builtin_amdgcn_s_memrealtime();
   const long long n = min(max(ticks, 0ll), C2H_DELAY_MAX_TICKS);
   while ((long long)__builtin_amdgcn_s_memrealtime() - t0 < n) __builtin_amdgcn_s_sleep(8);
+}
+
+__global__ void __launch_bounds__(64) k_next_epoch(C2hState* st) {
+  if (threadIdx.x == 0) st->epoch = st->epoch + 1u;
 }
 
 __global__ void __launch_bounds__(256) k_fill_u32(unsigned* p, int n, unsigned v) {

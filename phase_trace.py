@@ -78,6 +78,11 @@ __device__ __forceinline__ int phase_kind_f() {
   if (kd_ >= 0 && (threadIdx.x & 63) == 0 && by == 0 && (bx == 0 || bx == J.n_wg - 1)) \
     for (int k_ = 0; k_ < 16; ++k_) \
       g_phase[kd_][bx == 0 ? 0 : 1][threadIdx.x >> 6][k_] = ph_s_[threadIdx.x >> 6][k_]; } while (0)
+// the FFN launch's down-projection blocks (slot 3, the ffn_out row)
+#define PH_D_END(kd_, first_, last_) do { \
+  if ((threadIdx.x & 63) == 0 && ((first_) || (last_))) \
+    for (int k_ = 0; k_ < 16; ++k_) \
+      g_phase[kd_][(first_) ? 0 : 1][threadIdx.x >> 6][k_] = ph_s_[threadIdx.x >> 6][k_]; } while (0)
 #define PH_AT(k, t) do { if ((threadIdx.x & 63) == 0) ph_s_[threadIdx.x >> 6][k] = (t); } while (0)
 #define PH_A_END do { const bool f_ = h == 0; \
   const bool l_ = h == P.n_heads - 1; \
@@ -162,6 +167,17 @@ def instrument(kernels: str) -> str:
                    ("  if (tid < HD) {\n    acc = __builtin_fmaf(sc[pos], v_s[d], acc);\n",
                     "  PH_A(7);\n  if (tid < HD) {\n    acc = __builtin_fmaf(sc[pos], v_s[d], acc);\n"),
                ]).replace("PH_END;", "PH_A(8);\n  PH_A_END;", 1)
+    # the FFN launch's down blocks (slot 3, the ffn_out row): entry, args, issued (weights), x (h polled,
+    # wave 0), quant (wave 0), w (after the barrier), end (terms stored)
+    s = _patch(s, "template <int NB>\n__device__ __forceinline__ void down_block_body(",
+               "// The FFN of one layer in one launch", [
+                   ("  __shared__ Q8KRow<NB> s;\n", "  __shared__ Q8KRow<NB> s;\n  PH_DECL;\n  PH_G(0);\n"),
+                   ("  const int row = g * 128 + (tid >> 2), u = tid & 3;\n",
+                    "  const int row = g * 128 + (tid >> 2), u = tid & 3;\n  PH_G(1);\n"),
+                   ("    const float4 v[1] = {poll_tagged4(P.x_tag + b * QK_K + 4 * lane, tag, P.wait_err)};\n    quantize_blocks<1>(v, b, 0, b + 1, s);\n",
+                    "    PH_G(2);\n    const float4 v[1] = {poll_tagged4(P.x_tag + b * QK_K + 4 * lane, tag, P.wait_err)};\n    PH_G(3);\n    quantize_blocks<1>(v, b, 0, b + 1, s);\n    PH_G(5);\n"),
+                   ("  __syncthreads();\n  if (row < J.rows) {  // whole quads", "  __syncthreads();\n  PH_G(6);\n  if (row < J.rows) {  // whole quads"),
+               ]).replace("PH_END;", "PH_G(8);\n  PH_D_END(3, bx == 0, bx == ng * NB - 1);", 1)
     # float-input projections (k_gemv_f): entry, args, issued, norm_start, norm_end, x (staged in LDS),
     # items (the block terms in LDS), end
     s = _patch(s, "__device__ __forceinline__ void gemv_f_body(",

@@ -2,9 +2,12 @@
 
 A layer past 0 runs q|k|v, attention and the o-projection as one launch
 (k_attn_block, or k_attn_block_f for Q5_0 / Q8_0 projections), layer 0 as
-q|k|v then attention + o-projection (k_attn_oproj); C2H_NO_FUSE, read when a
-context is created, selects the separate forms ("qkv": q|k|v on its own,
-"1": every kernel on its own), which models without the fused instances run.
+q|k|v then attention + o-projection (k_attn_oproj); with K-quant gate/up and
+a Q6_K down projection the FFN is one launch too (k_ffn_block: the down
+projection split by super-block, its terms folded in block order).
+C2H_NO_FUSE, read when a context is created, selects the separate forms
+("qkv": q|k|v on its own, "ffn": the FFN's two launches apart, "1": every
+kernel on its own), which models without the fused instances run.
 Each form: a 20-token ingest, normX after every forward, every K and V row,
 then a 40-step greedy stream (positions 20..59, crossing the 32- and
 64-position attention tiers), on the Qwen2.5-0.5B layer shape with the
@@ -19,7 +22,7 @@ from tests.test_gpu_model import PENALTY, bits
 
 pytestmark = pytest.mark.gpu
 
-FORMS = ["1", "qkv", ""]  # separate, attention + o-projection only, all fused
+FORMS = ["1", "qkv", "ffn", ""]  # separate, attention + o-projection only, the FFN apart, all fused
 
 
 @pytest.fixture(scope="module", params=["k-quants", "real-formats"])
