@@ -829,7 +829,8 @@ bool fuse_attn_block_f(const c2h_ctx* c, int l, int form) {
 }
 
 // qkv + attention + attn_out in one launch, the GEMV parts k_gemv_f's
-void enqueue_attn_block_f(c2h_ctx* c, int l, int form) {
+// pend: the previous layer's FFN launch left its terms for X (dterm)
+void enqueue_attn_block_f(c2h_ctx* c, int l, int form, bool pend) {
   const c2h_model_desc& D = c->desc;
   Layer& L = c->layers[l];
   const int E = D.n_embd, KVd = D.n_kv_heads * D.head_dim;
@@ -848,6 +849,8 @@ void enqueue_attn_block_f(c2h_ctx* c, int l, int form) {
   Q.norm_w = L.attn_norm;
   Q.nb_in = nb8_of(E);
   Q.y_tag = c->qkv_tag;
+  Q.x_pend = pend ? c->dterm : nullptr;
+  Q.pend_n = E;
   int w = 1;
   for (int j = 0; j < Q.n_jobs; ++j) w = std::max(w, Q.jobs[j].n_wg);
   const AttnCoreParams A = fused_attn_params(c, l);
@@ -861,6 +864,8 @@ void enqueue_attn_block_f(c2h_ctx* c, int l, int form) {
   P.nb_in = nb8_of(E);
   P.x_tag = c->attn_tag;
   P.wait_err = c->tok_host + 2;
+  P.x_pend = Q.x_pend;
+  P.pend_n = E;
   const size_t lds = std::max(c->attn_lds, (size_t)gemv_f_lds_floats(E) * sizeof(float));
   hipLaunchKernelGGL(attn_block_f_kernel(form), dim3(3 * w + A.n_attn_wg + P.jobs[0].n_wg), dim3(256), lds,
                      c->stream, A.state, A.kv, (const float*)c->X, w << 16, (const uint64_t*)c->qkv_tag,
@@ -906,13 +911,16 @@ void enqueue_attn_block(c2h_ctx* c, int l, int form, bool pend) {
   prep_gemv_row(Q);
   int w = 1;
   for (int j = 0; j < Q.n_jobs; ++j) w = std::max(w, Q.jobs[j].n_wg);
+  // the k and v jobs' workgroups (the same rows); the rest of their W exit
+  // at entry.  Rows of 3 super-blocks (E < 1024) keep W < 50.
+  const int nkv = std::max(Q.jobs[1].n_wg, Q.jobs[2].n_wg);
   const AttnCoreParams A = fused_attn_params(c, l);
   GemvParams P = fused_oproj_params(c, l);
   P.x_pend = Q.x_pend;
   P.pend_n = E;
   const size_t lds = std::max(c->attn_lds, (size_t)Q.n_x_lds * sizeof(float));
   hipLaunchKernelGGL(attn_block_kernel(form), dim3(3 * w + A.n_attn_wg + P.jobs[0].n_wg), dim3(256), lds, c->stream,
-                     A.state, A.kv, (const float*)c->X, E | (w << 16), (const uint64_t*)c->qkv_tag,
+                     A.state, A.kv, (const float*)c->X, E | (w << 16) | (nkv << 24), (const uint64_t*)c->qkv_tag,
                      attn_dims(A, D.n_heads / D.n_kv_heads), A.max_ctx, A, Q, P);
 }
 
@@ -933,23 +941,29 @@ void enqueue_ffn_out(c2h_ctx* c, int l) {
   launch_group(c, {{&c->layers[l].wd, nullptr, c->X, nullptr}}, PRO_QUANT, MODE_RESID, c->h, c->desc.n_ff, nullptr);
 }
 
-// Whether layer l's FFN runs as one launch (k_ffn_block) that leaves its
-// residual add to the next layer's k_attn_block: K-quant gate/up of 3
-// super-blocks per row, a Q6_K down projection of FOLD_NB (the instance
-// built), and a next layer that runs k_attn_block at this form.
+// Whether layer l's FFN runs as one launch that leaves its residual add to
+// the next layer's fused attention launch (k_attn_block or k_attn_block_f,
+// which add the terms): a Q6_K down projection of FOLD_NB super-blocks
+// (the instances built), and gate/up either K-quants of 3 super-blocks per
+// row (k_ffn_block) or both the same Q5_0 / Q8_0 type over rows of a
+// multiple of 128 values, at most 1,024 (k_ffn_block_f).
 bool defer_ffn(const c2h_ctx* c, int l, int form) {
+  const c2h_model_desc& D = c->desc;
   const Layer& L = c->layers[l];
-  return c->fuse_ffn && l + 1 < c->desc.n_layers && nb_k(c->desc.n_embd) == 3 &&
-         nb_k(c->desc.n_ff) == FOLD_NB && !float_input(L.wg.type) && !float_input(L.wu.type) &&
-         L.wd.type == C2H_Q6_K && fuse_attn_block(c, l + 1, form);
+  if (!c->fuse_ffn || l + 1 >= D.n_layers || nb_k(D.n_ff) != FOLD_NB || L.wd.type != C2H_Q6_K) return false;
+  if (!fuse_attn_block(c, l + 1, form) && !fuse_attn_block_f(c, l + 1, form)) return false;
+  const bool fg = float_input(L.wg.type), fu = float_input(L.wu.type);
+  if (!fg && !fu) return nb_k(D.n_embd) == 3;
+  return fg && fu && L.wg.type == L.wu.type && D.n_embd % 128 == 0 && D.n_embd <= 1024;
 }
 
 // ffn_in + ffn_out but for the residual add in one launch: gate|up stores h
 // tagged, the down projection runs by super-block on the tagged h and
-// leaves its terms in dterm for the next k_attn_block to add to X
+// leaves its terms in dterm for the next fused attention launch to add to X
 void enqueue_ffn_block(c2h_ctx* c, int l) {
   const c2h_model_desc& D = c->desc;
   Layer& L = c->layers[l];
+  const bool fin = float_input(L.wg.type);
   GemvParams I = base_params(c);
   add_job(I, L.wg, &L.wu, MODE_SWIGLU, c->h, nullptr, nullptr);
   I.jobs[0].spare = 0;
@@ -959,20 +973,26 @@ void enqueue_ffn_block(c2h_ctx* c, int l) {
   I.n_x = D.n_embd;
   I.n_x_lds = chain_lds_floats(D.n_embd);
   I.norm_w = L.ffn_norm;
-  I.nb_in = nb_k(D.n_embd);
+  I.nb_in = fin ? nb8_of(D.n_embd) : nb_k(D.n_embd);
   I.y_tag = c->h_tag;
-  prep_gemv_row(I);
+  if (!fin) prep_gemv_row(I);
   GemvParams O = base_params(c);
   add_job(O, L.wd, nullptr, MODE_RESID, c->dterm, nullptr, nullptr);
-  O.jobs[0].n_wg = FOLD_NB * ((D.n_embd + 127) / 128);  // down_block_body workgroups
+  const int rw = fin ? 64 : 128;  // down rows per workgroup: 256 or 512 threads
+  O.jobs[0].n_wg = FOLD_NB * ((D.n_embd + rw - 1) / rw);  // down_block_body workgroups
   O.x = c->h;
   O.n_x = D.n_ff;
   O.x_tag = c->h_tag;
   O.wait_err = c->tok_host + 2;
   const int n_in = I.jobs[0].n_wg;
-  hipLaunchKernelGGL((k_ffn_block<3, FOLD_NB>), dim3(n_in + O.jobs[0].n_wg), dim3(512),
-                     (size_t)I.n_x_lds * sizeof(float), c->stream, (const float*)c->X, D.n_embd | (n_in << 16),
-                     c->state_dev, l, I, O);
+  if (fin)
+    hipLaunchKernelGGL(k_ffn_block_f<FOLD_NB>, dim3(n_in + O.jobs[0].n_wg), dim3(256),
+                       (size_t)gemv_f_lds_floats(D.n_embd) * sizeof(float), c->stream, c->state_dev, n_in << 16, l, I,
+                       O);
+  else
+    hipLaunchKernelGGL((k_ffn_block<3, FOLD_NB>), dim3(n_in + O.jobs[0].n_wg), dim3(512),
+                       (size_t)I.n_x_lds * sizeof(float), c->stream, (const float*)c->X, D.n_embd | (n_in << 16),
+                       c->state_dev, l, I, O);
 }
 
 // k_rmsnorm holds one float4 per thread
@@ -1011,7 +1031,7 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax, int form) {
     if (fuse_attn_block(c, l, form)) {
       enqueue_attn_block(c, l, form, pend);
     } else if (fuse_attn_block_f(c, l, form)) {
-      enqueue_attn_block_f(c, l, form);
+      enqueue_attn_block_f(c, l, form, pend);
     } else {
       enqueue_qkv(c, l, (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM);
       if (fuse_attn_oproj(c, l, form)) {

@@ -442,6 +442,11 @@ __global__ void k_attn_core(C2hState* st, float* kv, const float* qg, const floa
 constexpr int FOLD_NB = 19;
 template <int NBE, int NBF>
 __global__ void k_ffn_block(const float* xp, int xw, C2hState* st, int layer, GemvParams Gi, GemvParams Gd);
+// The same with Q5_0 / Q8_0 gate|up (k_gemv_f's workgroups, xw >> 16 of
+// them), 256 threads per workgroup, the down projection in rows of 64
+// (Gd.jobs[0].n_wg = NBF * ceil(rows / 64))
+template <int NBF>
+__global__ void k_ffn_block_f(C2hState* st, int xw, int layer, GemvParams Gi, GemvParams Gd);
 // qkv (3 W workgroups, W = xw >> 16), then k_attn_oproj's two parts, one
 // launch; Gq.y_tag = qkv_tag, Go.x_tag = P.out_tag
 template <int TIER, int NB>

@@ -1212,9 +1212,9 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(const f
 }
 
 // The down projection split by super-block (a Q6_K matrix of NB blocks per
-// row, c2_tensor_gemv2_q6_k_q8_k_gen.go:168-209 per row): workgroup bx
-// takes block b = bx / ng of rows [128 g, 128 g + 128), g = bx % ng, one
-// quarter-item per thread.  Wave 0 polls the block's 256 inputs (tagged
+// row, c2_tensor_gemv2_q6_k_q8_k_gen.go:168-209 per row): workgroup bx of
+// NT threads takes block b = bx / ng of rows [RW g, RW g + RW), RW = NT / 4,
+// g = bx % ng, one quarter-item per thread.  Wave 0 polls the block's 256 inputs (tagged
 // words at P.x_tag), quantises that block alone (Q8_K blocks are
 // independent, c2_quantize_q8_k_gen.go:11-91), and every quad computes its
 // row's term f32(isum) * (d * q8d) as k_gemv_row's items do; the term goes
@@ -1222,15 +1222,17 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(const f
 // The weights are issued first.  The row's fold, X += the terms added in
 // block order from 0 (the Q6_K fold of fold_terms), is left to the next
 // launch (GemvParams::x_pend), past the kernel boundary.
-template <int NB>
+template <int NB, int NT>
 __device__ __forceinline__ void down_block_body(const int bx, const GemvParams& P, const uint32_t tag) {
   static_assert(NB == FOLD_NB, "the next launch adds FOLD_NB terms");
+  static_assert(NT == 256 || NT == 512, "whole waves of quads");
+  constexpr int RW = NT / 4;  // rows per workgroup
   __shared__ Q8KRow<NB> s;
   const GemvJob J = P.jobs[0];
-  const int ng = (J.rows + 127) >> 7;
+  const int ng = (J.rows + RW - 1) / RW;
   const int b = bx / ng, g = bx - b * ng;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int row = g * 128 + (tid >> 2), u = tid & 3;
+  const int row = g * RW + (tid >> 2), u = tid & 3;
   const ItemW w = load_item(J.w, T_Q6_K, NB, min(row, J.rows - 1), b, u);
   issue_fence();
   if (wave == 0) {
@@ -1264,9 +1266,10 @@ __global__ void __launch_bounds__(512)
     gemv_row_body<NBE, PRO_NORM, MODE_SWIGLU, false, true>(b, 0, xp, xw & 0xffff, Gi, tag);
     return;
   }
-  down_block_body<NBF>(b - n_in, Gd, tag);
+  down_block_body<NBF, 512>(b - n_in, Gd, tag);
 }
 template __global__ void k_ffn_block<3, 19>(const float*, int, C2hState*, int, GemvParams, GemvParams);
+
 
 #define C2H_GEMV_ROW(NB_, PRO_, MODE_) \
   template __global__ void k_gemv_row<NB_, PRO_, MODE_>(const float*, int, GemvParams);
@@ -1465,12 +1468,14 @@ __device__ __forceinline__ float q80_row_sum(float acc) {
 // the output of producers in the same launch, {value, tag} words at
 // P.x_tag, polled (every element this thread stages, bounded as
 // poll_tagged4) after the weights and the residual are issued.  TAGY
-// (MODE_BIAS): each output y[r] is also stored as a {value, tag} word at
-// P.y_tag[J.spare + r].
-template <int PRO, int MODE, bool TAGX = false, bool TAGY = false>
+// (MODE_BIAS, MODE_SWIGLU): each output y[r] is also stored as a {value,
+// tag} word at P.y_tag[J.spare + r].  PEND: X's pending terms as in
+// gemv_row_body (P.x_pend, the norm prologue's input or the residual).
+template <int PRO, int MODE, bool TAGX = false, bool TAGY = false, bool PEND = false>
 __device__ __forceinline__ void gemv_f_body(const int bx, const int by, const GemvParams& P, const uint32_t tag) {
   static_assert(!TAGX || PRO == PRO_QUANT, "tagged input feeds the plain prologue");
-  static_assert(!TAGY || MODE == MODE_BIAS, "tagged output from the bias epilogue");
+  static_assert(!TAGY || MODE == MODE_BIAS || MODE == MODE_SWIGLU, "tagged output from the bias or SwiGLU epilogue");
+  static_assert(!PEND || PRO == PRO_NORM || MODE == MODE_RESID, "pending terms add to X as input or residual");
   constexpr bool PAIRED = (MODE == MODE_SWIGLU);
   constexpr bool NORM = (PRO == PRO_NORM || PRO == PRO_EMBED_NORM || PRO == PRO_ARGMAX_EMBED_NORM);
   extern __shared__ __align__(16) unsigned char smem[];
@@ -1504,12 +1509,22 @@ __device__ __forceinline__ void gemv_f_body(const int bx, const int by, const Ge
   // loads, lane l from x[16l, 16l+16), as k_gemv_row's norm waves do (no LDS
   // round trip, no barrier)
   float4 xs[SPEC_C / 4];
+  const bool pend = PEND && P.x_pend != nullptr;  // uniform
+  float4 tx[PEND && PRO == PRO_NORM ? FOLD_NB : 1];
   if (PRO == PRO_NORM) {
-    const float4* x4 = reinterpret_cast<const float4*>(P.x);
-    const int last4 = (P.n_x >> 2) - 1;
+    if (!pend) {  // pending terms: from LDS once added
+      const float4* x4 = reinterpret_cast<const float4*>(P.x);
+      const int last4 = (P.n_x >> 2) - 1;
 #pragma unroll
-    for (int k = 0; k < SPEC_C / 4; ++k) xs[k] = x4[min(4 * (tid & 63) + k, last4)];
+      for (int k = 0; k < SPEC_C / 4; ++k) xs[k] = x4[min(4 * (tid & 63) + k, last4)];
+    }
     xa = load4(P.x, P.n_x);
+    if constexpr (PEND && PRO == PRO_NORM) {
+      if (pend) {
+#pragma unroll
+        for (int k = 0; k < FOLD_NB; ++k) tx[k] = load4(P.x_pend + k * P.pend_n, P.n_x);
+      }
+    }
   } else if (NORM) {
     tok = (PRO == PRO_ARGMAX_EMBED_NORM) ? reduce_argmax_partials<256>(P.part_v, P.part_i, P.n_part, ared)
                                          : P.state->token;
@@ -1527,6 +1542,13 @@ __device__ __forceinline__ void gemv_f_body(const int bx, const int by, const Ge
   }
   float yres = 0.0f;
   if (MODE == MODE_RESID) yres = J.y[out_row];
+  float ty[PEND && MODE == MODE_RESID ? FOLD_NB : 1];
+  if constexpr (PEND && MODE == MODE_RESID) {
+    if (pend) {
+#pragma unroll
+      for (int k = 0; k < FOLD_NB; ++k) ty[k] = P.x_pend[k * P.pend_n + out_row];
+    }
+  }
   if (MODE == MODE_BIAS) yres = (J.bias ? J.bias : P.x)[J.bias ? out_row : 0];
   issue_fence();
 
@@ -1537,6 +1559,21 @@ __device__ __forceinline__ void gemv_f_body(const int bx, const int by, const Ge
     xp[(b * 8 + (kk & 7)) * 4 + (kk >> 3)] = v;
   };
   if (NORM) {
+    if constexpr (PEND && PRO == PRO_NORM) {
+      if (pend) {  // X + the pending terms; every wave's sums read it back from LDS
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int k = 0; k < FOLD_NB; ++k)
+          a = make_float4(a.x + tx[k].x, a.y + tx[k].y, a.z + tx[k].z, a.w + tx[k].w);
+        xa = make_float4(xa.x + a.x, xa.y + a.y, xa.z + a.z, xa.w + a.w);
+        if (4 * tid < P.n_x) reinterpret_cast<float4*>(sq)[tid] = xa;
+        __syncthreads();
+        const float4* s4 = reinterpret_cast<const float4*>(sq);
+        const int last4 = (P.n_x >> 2) - 1;
+#pragma unroll
+        for (int k = 0; k < SPEC_C / 4; ++k) xs[k] = s4[min(4 * (tid & 63) + k, last4)];
+      }
+    }
     if (PRO != PRO_NORM && bx == 0 && by == 0) {  // layer 0 publishes the embedded token
       if (4 * tid < P.n_x) reinterpret_cast<float4*>(P.x_out)[tid] = xa;
       if (tid == 0) {
@@ -1629,7 +1666,11 @@ __device__ __forceinline__ void gemv_f_body(const int bx, const int by, const Ge
     if (r < J.rows) {
       if (PAIRED) {
         const int n8 = J.rows - (J.rows % 8);
-        J.y[r] = (r < n8) ? swiglu_poly(acc, acc2) : swiglu_tail(acc, acc2);
+        const float yv = (r < n8) ? swiglu_poly(acc, acc2) : swiglu_tail(acc, acc2);
+        J.y[r] = yv;
+        if constexpr (TAGY)
+          __hip_atomic_store(&P.y_tag[J.spare + r], ((uint64_t)tag << 32) | __float_as_uint(yv), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
       } else if (MODE == MODE_BIAS) {
         const float yv = J.bias ? acc + yres : acc;
         J.y[r] = yv;
@@ -1637,7 +1678,16 @@ __device__ __forceinline__ void gemv_f_body(const int bx, const int by, const Ge
           __hip_atomic_store(&P.y_tag[J.spare + r], ((uint64_t)tag << 32) | __float_as_uint(yv), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
       } else if (MODE == MODE_RESID) {
-        J.y[r] = yres + acc;
+        float yr = yres;
+        if constexpr (PEND && MODE == MODE_RESID) {
+          if (pend) {
+            float a = 0.0f;
+#pragma unroll
+            for (int k = 0; k < FOLD_NB; ++k) a = a + ty[k];
+            yr = yr + a;
+          }
+        }
+        J.y[r] = yr + acc;
       } else {
         J.y[r] = acc;
       }
@@ -1658,6 +1708,24 @@ C2H_GEMV_F(PRO_NORM, MODE_SWIGLU)
 C2H_GEMV_F(PRO_QUANT, MODE_RESID)
 C2H_GEMV_F(PRO_QUANT, MODE_STORE)
 #undef C2H_GEMV_F
+
+// The same FFN launch with Q5_0 / Q8_0 gate|up (the float-input GEMV), 256
+// threads per workgroup: [0, xw >> 16) k_gemv_f<PRO_NORM, MODE_SWIGLU>'s
+// workgroups (h stored tagged as well), then the down projection's
+// down_block_body<NBF, 256> workgroups (rows of 64); the residual add is
+// the next launch's.
+template <int NBF>
+__global__ void __launch_bounds__(256)
+    k_ffn_block_f(C2hState* __restrict__ st, int xw, int layer, GemvParams Gi, GemvParams Gd) {
+  const int b = (int)blockIdx.x, n_in = xw >> 16;
+  const uint32_t tag = (uint32_t)st->epoch * 256u + (uint32_t)layer;
+  if (b < n_in) {
+    gemv_f_body<PRO_NORM, MODE_SWIGLU, false, true>(b, 0, Gi, tag);
+    return;
+  }
+  down_block_body<NBF, 256>(b - n_in, Gd, tag);
+}
+template __global__ void k_ffn_block_f<19>(C2hState*, int, int, GemvParams, GemvParams);
 
 // ------------------------------------------------------------- final norm
 
@@ -2298,11 +2366,12 @@ __global__ void __launch_bounds__(256)
 // tagged as well (Gq.y_tag = qkv_tag); the next P.n_attn_wg run
 // k_attn_core's XCD-grouped grid on them (polled after the K/V rows are
 // issued); the rest run the o-projection of Go on the tagged attention
-// output.  Where Gq.x_pend / Go.x_pend are set, the previous layer's FFN
+// output.  The k and v jobs have xw >> 24 workgroups each: the rest of
+// their W exit at entry, before any load.  Where Gq.x_pend / Go.x_pend are set, the previous layer's FFN
 // launch left its down-projection terms for X: the qkv part adds them to X
 // for its norm, the o-projection to its residual, and X is written with
-// them.  x, its length (xw & 0xffff) and the tagged q|k|v arrive as
-// preloaded kernel arguments with the state and the KV cache.
+// them.  x, its length (xw & 0xffff), W ((xw >> 16) & 0xff) and the tagged
+// q|k|v arrive as preloaded kernel arguments with the state and the KV cache.
 template <int TIER, int NB>
 __global__ void __launch_bounds__(256)
     k_attn_block(C2hState* __restrict__ st, float* __restrict__ kv, const float* __restrict__ xp, int xw,
@@ -2311,11 +2380,12 @@ __global__ void __launch_bounds__(256)
   static_assert(row_threads(NB, PRO_NORM, MODE_BIAS) == 256 && row_threads(NB, PRO_QUANT, MODE_RESID) == 256,
                 "every part runs 256-thread workgroups");
   const int b = (int)blockIdx.x;
-  const int w = xw >> 16, nq = 3 * w;
+  const int w = (xw >> 16) & 0xff, nq = 3 * w;
   if (b < nq) {
-    const int by = b / w;
+    const int by = b / w, bx = b - by * w;
+    if (by > 0 && bx >= (int)((unsigned)xw >> 24)) return;  // a spare of the k or v job
     const uint32_t tag = (uint32_t)st->epoch * 256u + (uint32_t)(dims & 0xff);
-    gemv_row_body<NB, PRO_NORM, MODE_BIAS, false, true, true>(b - by * w, by, xp, xw & 0xffff, Gq, tag);
+    gemv_row_body<NB, PRO_NORM, MODE_BIAS, false, true, true>(bx, by, xp, xw & 0xffff, Gq, tag);
     return;
   }
   const int n_attn = P.n_attn_wg;
@@ -2351,7 +2421,7 @@ __global__ void __launch_bounds__(256)
   const uint32_t tag = (uint32_t)st->epoch * 256u + (uint32_t)(dims & 0xff);
   if (b < nq) {
     const int by = b / w;
-    gemv_f_body<PRO_NORM, MODE_BIAS, false, true>(b - by * w, by, Gq, tag);
+    gemv_f_body<PRO_NORM, MODE_BIAS, false, true, true>(b - by * w, by, Gq, tag);
     return;
   }
   const int n_attn = P.n_attn_wg;
@@ -2359,7 +2429,7 @@ __global__ void __launch_bounds__(256)
     attn_core_body<TIER, true, true>(b - nq, 0, 0, st, kv, nullptr, nullptr, nullptr, dims, max_ctx, P, qkv_tag);
     return;
   }
-  gemv_f_body<PRO_QUANT, MODE_RESID, true>(b - nq - n_attn, 0, Go, tag);
+  gemv_f_body<PRO_QUANT, MODE_RESID, true, false, true>(b - nq - n_attn, 0, Go, tag);
 }
 template __global__ void k_attn_block_f<ATT_TIER_32>(C2hState*, float*, const float*, int, const uint64_t*, int, int,
                                                      AttnCoreParams, GemvParams, GemvParams);

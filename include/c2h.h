@@ -323,8 +323,7 @@ int c2h_check_rms_scale(c2h_ctx* ctx, uint32_t lo, uint64_t hi, uint64_t* mismat
  * otherwise): */
 #define C2H_KERNEL_ATTN_BLOCK 6 /* QKV + ATTN + ATTN_OUT in one launch (layers past 0) */
 #define C2H_KERNEL_ATTN_OPROJ 7 /* ATTN + ATTN_OUT in one launch (layer 0) */
-#define C2H_KERNEL_FFN_BLOCK 8  /* FFN_IN + FFN_OUT in one launch (K-quant gate/up, Q6_K down of 19 blocks) */
-#define C2H_KERNEL_FFN_BLOCK 8  /* FFN_IN + FFN_OUT in one launch (K-quant gate/up, Q6_K down of 19 blocks) */
+#define C2H_KERNEL_FFN_BLOCK 8  /* FFN_IN + FFN_OUT but the residual add in one launch (Q6_K down of 19 blocks) */
 
 /* Measurement aid with no counterpart in the reference: average device time
  * (ms) of one decoder-layer kernel, `iters` launches back to back on the

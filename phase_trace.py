@@ -169,11 +169,11 @@ def instrument(kernels: str) -> str:
                ]).replace("PH_END;", "PH_A(8);\n  PH_A_END;", 1)
     # the FFN launch's down blocks (slot 3, the ffn_out row): entry, args, issued (weights), x (h polled,
     # wave 0), quant (wave 0), w (after the barrier), end (terms stored)
-    s = _patch(s, "template <int NB>\n__device__ __forceinline__ void down_block_body(",
+    s = _patch(s, "template <int NB, int NT>\n__device__ __forceinline__ void down_block_body(",
                "// The FFN of one layer in one launch", [
                    ("  __shared__ Q8KRow<NB> s;\n", "  __shared__ Q8KRow<NB> s;\n  PH_DECL;\n  PH_G(0);\n"),
-                   ("  const int row = g * 128 + (tid >> 2), u = tid & 3;\n",
-                    "  const int row = g * 128 + (tid >> 2), u = tid & 3;\n  PH_G(1);\n"),
+                   ("  const int row = g * RW + (tid >> 2), u = tid & 3;\n",
+                    "  const int row = g * RW + (tid >> 2), u = tid & 3;\n  PH_G(1);\n"),
                    ("    const float4 v[1] = {poll_tagged4(P.x_tag + b * QK_K + 4 * lane, tag, P.wait_err)};\n    quantize_blocks<1>(v, b, 0, b + 1, s);\n",
                     "    PH_G(2);\n    const float4 v[1] = {poll_tagged4(P.x_tag + b * QK_K + 4 * lane, tag, P.wait_err)};\n    PH_G(3);\n    quantize_blocks<1>(v, b, 0, b + 1, s);\n    PH_G(5);\n"),
                    ("  __syncthreads();\n  if (row < J.rows) {  // whole quads", "  __syncthreads();\n  PH_G(6);\n  if (row < J.rows) {  // whole quads"),
