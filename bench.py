@@ -179,21 +179,22 @@ def kernel_bytes(gf, desc, T: float) -> dict:
 def step_launches(n_layers: int) -> dict:
     """Launches of each decode kernel per step.  The Qwen2.5-0.5B shape has
     the fused attention launches (k_attn_block on layers past 0, qkv then
-    k_attn_oproj on layer 0) and, on every layer but the last, the FFN as
-    one launch (k_ffn_block) whose residual add the next k_attn_block does,
-    unless C2H_NO_FUSE selects the separate forms (=1: every kernel on its
-    own; =qkv: qkv on its own, attention and the o-projection fused, the
-    FFN's two launches apart; =ffn: the FFN's two launches apart)."""
+    k_attn_oproj on layer 0) and the FFN as one launch (k_ffn_block) whose
+    residual add the next k_attn_block, or after the last layer the final
+    norm, does, unless C2H_NO_FUSE selects the separate forms (=1: every
+    kernel on its own; =qkv: qkv on its own, attention and the o-projection
+    fused, the FFN's two launches apart but on the last layer; =ffn: the
+    FFN's two launches apart)."""
     nf = os.environ.get("C2H_NO_FUSE", "")
     L = n_layers
-    n = dict(qkv=1, attn=0, attn_out=0, attn_block=L - 1, attn_oproj=1, ffn_in=1, ffn_out=1, ffn_block=L - 1,
+    n = dict(qkv=1, attn=0, attn_out=0, attn_block=L - 1, attn_oproj=1, ffn_in=0, ffn_out=0, ffn_block=L,
              final_norm=1, vocab=1)
-    if nf in ("1", "qkv", "ffn"):
+    if nf in ("1", "ffn"):
         n.update(ffn_in=L, ffn_out=L, ffn_block=0)
     if nf == "1":
         n.update(qkv=L, attn=L, attn_out=L, attn_block=0, attn_oproj=0)
     elif nf == "qkv":
-        n.update(qkv=L, attn_oproj=L, attn_block=0)
+        n.update(qkv=L, attn_oproj=L, attn_block=0, ffn_in=L - 1, ffn_out=L - 1, ffn_block=1)
     return n
 
 
@@ -202,7 +203,7 @@ def step_launches(n_layers: int) -> dict:
 # fixed so the line does not depend on which kernel a run's timings make the
 # largest; ffn_in (the two Q4_K matrices) where C2H_NO_FUSE runs the FFN's
 # launches apart.
-ROOFLINE_KERNEL = "ffn_in" if os.environ.get("C2H_NO_FUSE", "") in ("1", "qkv", "ffn") else "ffn_block"
+ROOFLINE_KERNEL = "ffn_in" if os.environ.get("C2H_NO_FUSE", "") in ("1", "ffn") else "ffn_block"
 
 KERNEL_NAMES = {"qkv": "k_gemv_row<3, PRO_NORM, MODE_BIAS>", "attn": "k_attn_core",
                 "attn_out": "k_gemv_row<3, PRO_QUANT, MODE_RESID>", "ffn_in": "k_gemv_row<3, PRO_NORM, MODE_SWIGLU>",

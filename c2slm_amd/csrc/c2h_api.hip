@@ -942,16 +942,18 @@ void enqueue_ffn_out(c2h_ctx* c, int l) {
 }
 
 // Whether layer l's FFN runs as one launch that leaves its residual add to
-// the next layer's fused attention launch (k_attn_block or k_attn_block_f,
-// which add the terms): a Q6_K down projection of FOLD_NB super-blocks
+// the next launch: the next layer's fused attention launch (k_attn_block or
+// k_attn_block_f), or after the last layer the final norm, which add the
+// terms.  It needs a Q6_K down projection of FOLD_NB super-blocks
 // (the instances built), and gate/up either K-quants of 3 super-blocks per
 // row (k_ffn_block) or both the same Q5_0 / Q8_0 type over rows of a
 // multiple of 128 values, at most 1,024 (k_ffn_block_f).
 bool defer_ffn(const c2h_ctx* c, int l, int form) {
   const c2h_model_desc& D = c->desc;
   const Layer& L = c->layers[l];
-  if (!c->fuse_ffn || l + 1 >= D.n_layers || nb_k(D.n_ff) != FOLD_NB || L.wd.type != C2H_Q6_K) return false;
-  if (!fuse_attn_block(c, l + 1, form) && !fuse_attn_block_f(c, l + 1, form)) return false;
+  if (!c->fuse_ffn || nb_k(D.n_ff) != FOLD_NB || L.wd.type != C2H_Q6_K) return false;
+  if (l + 1 < D.n_layers && !fuse_attn_block(c, l + 1, form) && !fuse_attn_block_f(c, l + 1, form)) return false;
+  if (D.n_embd > 1024) return false;  // the final norm folds with 256 threads, a float4 each
   const bool fg = float_input(L.wg.type), fu = float_input(L.wu.type);
   if (!fg && !fu) return nb_k(D.n_embd) == 3;
   return fg && fu && L.wg.type == L.wu.type && D.n_embd % 128 == 0 && D.n_embd <= 1024;
@@ -1000,7 +1002,8 @@ int norm_threads(int n) { return n <= 1024 ? 256 : 512; }
 
 // the final RMSNorm into the normX buffer the step state names; a step
 // graph's also leaves the next step's state (advance)
-void enqueue_final_norm(c2h_ctx* c, int advance = 0) {
+// pend: the last layer's FFN launch left its terms for X (dterm)
+void enqueue_final_norm(c2h_ctx* c, int advance = 0, bool pend = false) {
   const c2h_model_desc& D = c->desc;
   NormParams N;
   memset(&N, 0, sizeof(N));
@@ -1014,6 +1017,8 @@ void enqueue_final_norm(c2h_ctx* c, int advance = 0) {
   N.state = c->state_dev;
   N.n_lds = chain_lds_floats(D.n_embd);
   N.advance = advance;
+  N.x_pend = pend ? c->dterm : nullptr;
+  N.x_back = c->X;
   if (D.head_dim == 64) {  // the advance leaves the next position's RoPE row in the state
     N.rope_cos = c->rope_cos;
     N.rope_sin = c->rope_sin;
@@ -1049,7 +1054,7 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax, int form) {
       enqueue_ffn_out(c, l);
     }
   }
-  enqueue_final_norm(c, from_argmax ? 1 : 0);
+  enqueue_final_norm(c, from_argmax ? 1 : 0, pend);
 }
 
 void enqueue_step(c2h_ctx* c, int form) {

@@ -165,6 +165,10 @@ struct NormParams {
   const float* rope_cos;  // head_dim 64: the RoPE table the advance takes the next row from (else nullptr)
   const float* rope_sin;
   int rope_len;
+  // the last layer's FFN launch left X's pending terms [FOLD_NB][n]: x is
+  // X + their sum in block order, also written back to x_back; nullptr: none
+  const float* x_pend;
+  float* x_back;
 };
 
 // KV cache: [K|V][layer][kv head][kv_slot(max_ctx)][hd] floats.  K rows are

@@ -1737,12 +1737,25 @@ __global__ void __launch_bounds__(512) k_rmsnorm(NormParams P) {
   float* sq = reinterpret_cast<float*>(smem);
   __shared__ float inv_slot;
   asm volatile("" ::"s"(P.x), "s"(P.w), "s"(P.n), "s"(P.eps), "s"(P.out_sel), "s"(P.out), "s"(P.out_buf[0]),
-               "s"(P.out_buf[1]), "s"(P.state), "s"(P.advance), "s"(P.rope_cos), "s"(P.rope_sin), "s"(P.rope_len));
-  const float4 x = load4(P.x, P.n);
+               "s"(P.out_buf[1]), "s"(P.state), "s"(P.advance), "s"(P.rope_cos), "s"(P.rope_sin), "s"(P.rope_len),
+               "s"(P.x_pend), "s"(P.x_back));
+  float4 x = load4(P.x, P.n);
+  float4 tx[FOLD_NB];
+  if (P.x_pend) {  // uniform
+#pragma unroll
+    for (int k = 0; k < FOLD_NB; ++k) tx[k] = load4(P.x_pend + k * P.n, P.n);
+  }
   const float4 w = load4(P.w, P.n);
   const int nx_out = P.out_sel ? P.state->nx_out : 0;  // with the loads, not after the sum
   const int pos = P.advance ? P.state->pos : 0;
   issue_fence();
+  if (P.x_pend) {  // X + the pending terms, added from 0 in block order as ffn_out's epilogue would
+    float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int k = 0; k < FOLD_NB; ++k) a = make_float4(a.x + tx[k].x, a.y + tx[k].y, a.z + tx[k].z, a.w + tx[k].w);
+    x = make_float4(x.x + a.x, x.y + a.y, x.z + a.z, x.w + a.w);
+    if (4 * (int)threadIdx.x < P.n) reinterpret_cast<float4*>(P.x_back)[threadIdx.x] = x;
+  }
   // the next position's RoPE row, loaded by wave 1 (idle during wave 0's
   // sum) and stored with the rest of the advance
   const int rt = (int)threadIdx.x - 64;

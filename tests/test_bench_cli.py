@@ -54,7 +54,7 @@ def test_roofline_kernel_is_fixed_and_its_traffic_is_recorded():
     ffn_in's (the FFN's launches apart) within 10 %."""
     sys.path.insert(0, ROOT)
     import bench
-    if os.environ.get("C2H_NO_FUSE", "") in ("1", "qkv", "ffn"):
+    if os.environ.get("C2H_NO_FUSE", "") in ("1", "ffn"):
         assert bench.ROOFLINE_KERNEL == "ffn_in"
     else:
         assert bench.ROOFLINE_KERNEL == "ffn_block"
