@@ -64,3 +64,21 @@ def test_roofline_kernel_is_fixed_and_its_traffic_is_recorded():
     t = bench.profiled_traffic("ffn_in")
     assert isinstance(t, int)
     assert 1.0 <= t / 4_229_120 < 1.1
+
+
+def test_step_launches_per_launch_form(monkeypatch):
+    """Launches per decode step of the 24-layer shape in each C2H_NO_FUSE
+    form: fused (qkv + attention + attn_out on layers past 0, every FFN one
+    launch whose residual add the next launch does) 51; =ffn (the FFN's two
+    launches apart) 75; =qkv (qkv on its own, so no layer's FFN can leave
+    its add to an attention launch; the last one's goes to the final norm)
+    97; =1 (every kernel on its own) 122."""
+    sys.path.insert(0, ROOT)
+    import bench
+    for form, total in (("", 51), ("ffn", 75), ("qkv", 97), ("1", 122)):
+        monkeypatch.setenv("C2H_NO_FUSE", form)
+        n = bench.step_launches(24)
+        assert sum(n.values()) == total, (form, n)
+        assert n["vocab"] == 1 and n["final_norm"] == 1
+        assert n["ffn_block"] + n["ffn_in"] == 24 and n["ffn_in"] == n["ffn_out"]
+        assert n["qkv"] + n["attn_block"] == 24
