@@ -700,10 +700,32 @@ void launch_group(c2h_ctx* c, std::initializer_list<ProjJob> jobs, int pro, int 
 // The launches of one decoder layer (engine/forward.go:65-131), each on its
 // own so the measurement entry points can time them one by one.
 // q|k|v = W * x(RMSNorm(X)) + bias; layer 0 embeds the token first (pro).
-void enqueue_qkv(c2h_ctx* c, int l, int pro) {
+// pend (layers past 0 with K-quant q/k/v of 3 super-blocks): the previous
+// layer's FFN launch left its terms for X (dterm), added by k_gemv_row_pend.
+void enqueue_qkv(c2h_ctx* c, int l, int pro, bool pend = false) {
   Layer& L = c->layers[l];
-  launch_group(c, {{&L.wq, nullptr, c->q, L.bq}, {&L.wk, nullptr, c->k, L.bk}, {&L.wv, nullptr, c->v, L.bv}}, pro,
-               MODE_BIAS, c->X, c->desc.n_embd, L.attn_norm);
+  if (!pend) {
+    launch_group(c, {{&L.wq, nullptr, c->q, L.bq}, {&L.wk, nullptr, c->k, L.bk}, {&L.wv, nullptr, c->v, L.bv}}, pro,
+                 MODE_BIAS, c->X, c->desc.n_embd, L.attn_norm);
+    return;
+  }
+  const int E = c->desc.n_embd;
+  GemvParams P = base_params(c);
+  add_job(P, L.wq, nullptr, MODE_BIAS, c->q, L.bq, nullptr);
+  add_job(P, L.wk, nullptr, MODE_BIAS, c->k, L.bk, nullptr);
+  add_job(P, L.wv, nullptr, MODE_BIAS, c->v, L.bv, nullptr);
+  P.prologue = PRO_NORM;
+  P.x = c->X;
+  P.x_out = c->X;
+  P.n_x = E;
+  P.n_x_lds = chain_lds_floats(E);
+  P.norm_w = L.attn_norm;
+  P.nb_in = nb_k(E);
+  P.x_pend = c->dterm;
+  P.pend_n = E;
+  prep_gemv_row(P);
+  hipLaunchKernelGGL((k_gemv_row_pend<3, PRO_NORM, MODE_BIAS>), job_grid(P), dim3(row_threads(3, PRO_NORM, MODE_BIAS)),
+                     (size_t)P.n_x_lds * sizeof(float), c->stream, P.x, P.n_x, P);
 }
 
 // attention: RoPE, KV store, scores, softmax, AV
@@ -925,9 +947,27 @@ void enqueue_attn_block(c2h_ctx* c, int l, int form, bool pend) {
 }
 
 // attn_out: X += Wo * x(attn)
-void enqueue_attn_out(c2h_ctx* c, int l) {
-  launch_group(c, {{&c->layers[l].wo, nullptr, c->X, nullptr}}, PRO_QUANT, MODE_RESID, c->attn, c->desc.n_embd,
-               nullptr);
+// pend: as in enqueue_qkv, the residual X + the previous FFN's terms
+void enqueue_attn_out(c2h_ctx* c, int l, bool pend = false) {
+  if (!pend) {
+    launch_group(c, {{&c->layers[l].wo, nullptr, c->X, nullptr}}, PRO_QUANT, MODE_RESID, c->attn, c->desc.n_embd,
+                 nullptr);
+    return;
+  }
+  const int E = c->desc.n_embd;
+  GemvParams P = base_params(c);
+  add_job(P, c->layers[l].wo, nullptr, MODE_RESID, c->X, nullptr, nullptr);
+  P.prologue = PRO_QUANT;
+  P.x = c->attn;
+  P.x_out = c->X;
+  P.n_x = E;
+  P.n_x_lds = chain_lds_floats(E);
+  P.nb_in = nb_k(E);
+  P.x_pend = c->dterm;
+  P.pend_n = E;
+  prep_gemv_row(P);
+  hipLaunchKernelGGL((k_gemv_row_pend<3, PRO_QUANT, MODE_RESID>), job_grid(P),
+                     dim3(row_threads(3, PRO_QUANT, MODE_RESID)), 0, c->stream, P.x, P.n_x, P);
 }
 
 // ffn_in: h = SwiGLU(Wg * n, Wu * n), n = x(RMSNorm(X))
@@ -941,10 +981,21 @@ void enqueue_ffn_out(c2h_ctx* c, int l) {
   launch_group(c, {{&c->layers[l].wd, nullptr, c->X, nullptr}}, PRO_QUANT, MODE_RESID, c->h, c->desc.n_ff, nullptr);
 }
 
+// Whether layer l runs q|k|v, attention and attn_out as launches of their
+// own that can add X's pending terms (k_gemv_row_pend): past layer 0, no
+// fused attention launch at this form, K-quant q/k/v/o rows of 3
+// super-blocks.
+bool pend_separate(const c2h_ctx* c, int l, int form) {
+  const Layer& L = c->layers[l];
+  return l > 0 && nb_k(c->desc.n_embd) == 3 && !fuse_attn_block(c, l, form) && !fuse_attn_block_f(c, l, form) &&
+         !fuse_attn_oproj(c, l, form) && !float_input(L.wq.type) && !float_input(L.wk.type) &&
+         !float_input(L.wv.type) && !float_input(L.wo.type);
+}
+
 // Whether layer l's FFN runs as one launch that leaves its residual add to
 // the next launch: the next layer's fused attention launch (k_attn_block or
-// k_attn_block_f), or after the last layer the final norm, which add the
-// terms.  It needs a Q6_K down projection of FOLD_NB super-blocks
+// k_attn_block_f) or its q|k|v and attn_out launches (pend_separate), or
+// after the last layer the final norm, which add the terms.  It needs a Q6_K down projection of FOLD_NB super-blocks
 // (the instances built), and gate/up either K-quants of 3 super-blocks per
 // row (k_ffn_block) or both the same Q5_0 / Q8_0 type over rows of a
 // multiple of 128 values, at most 1,024 (k_ffn_block_f).
@@ -952,7 +1003,9 @@ bool defer_ffn(const c2h_ctx* c, int l, int form) {
   const c2h_model_desc& D = c->desc;
   const Layer& L = c->layers[l];
   if (!c->fuse_ffn || nb_k(D.n_ff) != FOLD_NB || L.wd.type != C2H_Q6_K) return false;
-  if (l + 1 < D.n_layers && !fuse_attn_block(c, l + 1, form) && !fuse_attn_block_f(c, l + 1, form)) return false;
+  if (l + 1 < D.n_layers && !fuse_attn_block(c, l + 1, form) && !fuse_attn_block_f(c, l + 1, form) &&
+      !pend_separate(c, l + 1, form))
+    return false;
   if (D.n_embd > 1024) return false;  // the final norm folds with 256 threads, a float4 each
   const bool fg = float_input(L.wg.type), fu = float_input(L.wu.type);
   if (!fg && !fu) return nb_k(D.n_embd) == 3;
@@ -1038,12 +1091,13 @@ void enqueue_layers(c2h_ctx* c, bool from_argmax, int form) {
     } else if (fuse_attn_block_f(c, l, form)) {
       enqueue_attn_block_f(c, l, form, pend);
     } else {
-      enqueue_qkv(c, l, (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM);
+      // (pend here means pend_separate: layer l > 0, no fused launch)
+      enqueue_qkv(c, l, (l == 0) ? (from_argmax ? PRO_ARGMAX_EMBED_NORM : PRO_EMBED_NORM) : PRO_NORM, pend);
       if (fuse_attn_oproj(c, l, form)) {
         enqueue_attn_oproj(c, l, form);
       } else {
         enqueue_attn(c, l, form);
-        enqueue_attn_out(c, l);
+        enqueue_attn_out(c, l, pend);
       }
     }
     pend = defer_ffn(c, l, form);

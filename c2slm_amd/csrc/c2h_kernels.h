@@ -444,6 +444,11 @@ __global__ void k_attn_core(C2hState* st, float* kv, const float* qg, const floa
 // (GemvParams::x_pend)
 // the down blocks of the FFN launch, whose terms the next launch adds to X
 constexpr int FOLD_NB = 19;
+// k_gemv_row that adds X's pending terms (GemvParams::x_pend) to its norm
+// input (PRO_NORM) or residual (MODE_RESID); instances <3, PRO_NORM,
+// MODE_BIAS> and <3, PRO_QUANT, MODE_RESID>
+template <int NB, int PRO, int MODE>
+__global__ void k_gemv_row_pend(const float* xp, int n_xp, GemvParams P);
 template <int NBE, int NBF>
 __global__ void k_ffn_block(const float* xp, int xw, C2hState* st, int layer, GemvParams Gi, GemvParams Gd);
 // The same with Q5_0 / Q8_0 gate|up (k_gemv_f's workgroups, xw >> 16 of

@@ -1211,6 +1211,17 @@ __global__ void __launch_bounds__(row_threads(NB, PRO, MODE)) k_gemv_row(const f
   gemv_row_body<NB, PRO, MODE, false>((int)blockIdx.x, (int)blockIdx.y, xp, n_xp, P, 0u);
 }
 
+// k_gemv_row adding X's pending terms (P.x_pend, the previous layer's FFN
+// launch): the q|k|v launch's norm input, or attn_out's residual, where a
+// layer runs them as launches of their own (the long-context forms)
+template <int NB, int PRO, int MODE>
+__global__ void __launch_bounds__(row_threads(NB, PRO, MODE))
+    k_gemv_row_pend(const float* __restrict__ xp, int n_xp, GemvParams P) {
+  gemv_row_body<NB, PRO, MODE, false, false, true>((int)blockIdx.x, (int)blockIdx.y, xp, n_xp, P, 0u);
+}
+template __global__ void k_gemv_row_pend<3, PRO_NORM, MODE_BIAS>(const float*, int, GemvParams);
+template __global__ void k_gemv_row_pend<3, PRO_QUANT, MODE_RESID>(const float*, int, GemvParams);
+
 // The down projection split by super-block (a Q6_K matrix of NB blocks per
 // row, c2_tensor_gemv2_q6_k_q8_k_gen.go:168-209 per row): workgroup bx of
 // NT threads takes block b = bx / ng of rows [RW g, RW g + RW), RW = NT / 4,
