@@ -11,7 +11,10 @@ kernel on its own), which models without the fused instances run.
 Each form: a 20-token ingest, normX after every forward, every K and V row,
 then a 40-step greedy stream (positions 20..59, crossing the 32- and
 64-position attention tiers), on the Qwen2.5-0.5B layer shape with the
-synthetic K-quant mix and with the published file's format mix."""
+synthetic K-quant mix and with the published file's format mix; and two
+corners of the FFN's residual add moving to the next launch: a one-layer
+model (layer 0's FFN leaves it to the final norm) and K-quant attention
+with Q5_0 gate/up (the float-input FFN launch leaves it to k_attn_block)."""
 import numpy as np
 import pytest
 
@@ -25,13 +28,17 @@ pytestmark = pytest.mark.gpu
 FORMS = ["1", "qkv", "ffn", ""]  # separate, attention + o-projection only, the FFN apart, all fused
 
 
-@pytest.fixture(scope="module", params=["k-quants", "real-formats"])
+@pytest.fixture(scope="module", params=["k-quants", "real-formats", "one-layer", "q50-ffn"])
 def model(request, tmp_path_factory):
     p = str(tmp_path_factory.mktemp("forms") / f"{request.param}.gguf")
     shape = G.ModelShape(n_layers=2, n_vocab=4096)
     if request.param == "real-formats":
         shape = G.ModelShape(n_layers=2, n_vocab=4096, t_q=G.Q5_0, t_k=G.Q5_0, t_v=G.Q8_0, t_o=G.Q5_0,
                              t_gate=G.Q5_0, t_up=G.Q5_0, t_down=G.Q6_K)
+    elif request.param == "one-layer":
+        shape = G.ModelShape(n_layers=1, n_vocab=4096)
+    elif request.param == "q50-ffn":
+        shape = G.ModelShape(n_layers=2, n_vocab=4096, t_gate=G.Q5_0, t_up=G.Q5_0, t_down=G.Q6_K)
     G.write_synthetic_model(p, shape, seed=77)
     gf = G.GGUFFile(p)
     _, im_end, eos = G.special_token_ids(gf)
@@ -62,7 +69,7 @@ def test_launch_form_bitexact(model, form, monkeypatch):
         for i, t in enumerate(prompt):
             assert np.array_equal(bits(ctx.forward(int(t), i)), bits(nx[i])), (name, form, i)
         for which in (0, 1):
-            for layer in range(2):
+            for layer in range(kv.shape[1]):  # [K|V][layer][kv head][position][dim]
                 for h in range(2):
                     assert np.array_equal(bits(ctx.kv(which, layer, h, len(prompt))),
                                           bits(kv[which, layer, h])), (name, form, which, layer, h)
