@@ -992,24 +992,29 @@ bool pend_separate(const c2h_ctx* c, int l, int form) {
          !float_input(L.wv.type) && !float_input(L.wo.type);
 }
 
+// The tensor types the FFN launch reads on layer l: a Q6_K down projection
+// of FOLD_NB super-blocks (the instances built), and gate/up either K-quants
+// of 3 super-blocks per row (k_ffn_block) or both the same Q5_0 / Q8_0 type
+// over rows of a multiple of 128 values (k_ffn_block_f); rows of at most
+// 1,024 values (the final norm adds the last layer's terms with 256
+// threads, a float4 each).
+bool ffn_block_types(const c2h_ctx* c, int l) {
+  const c2h_model_desc& D = c->desc;
+  const Layer& L = c->layers[l];
+  if (nb_k(D.n_ff) != FOLD_NB || L.wd.type != C2H_Q6_K || D.n_embd > 1024) return false;
+  const bool fg = float_input(L.wg.type), fu = float_input(L.wu.type);
+  if (!fg && !fu) return nb_k(D.n_embd) == 3;
+  return fg && fu && L.wg.type == L.wu.type && D.n_embd % 128 == 0;
+}
+
 // Whether layer l's FFN runs as one launch that leaves its residual add to
 // the next launch: the next layer's fused attention launch (k_attn_block or
 // k_attn_block_f) or its q|k|v and attn_out launches (pend_separate), or
-// after the last layer the final norm, which add the terms.  It needs a Q6_K down projection of FOLD_NB super-blocks
-// (the instances built), and gate/up either K-quants of 3 super-blocks per
-// row (k_ffn_block) or both the same Q5_0 / Q8_0 type over rows of a
-// multiple of 128 values, at most 1,024 (k_ffn_block_f).
+// after the last layer the final norm, which add the terms.
 bool defer_ffn(const c2h_ctx* c, int l, int form) {
-  const c2h_model_desc& D = c->desc;
-  const Layer& L = c->layers[l];
-  if (!c->fuse_ffn || nb_k(D.n_ff) != FOLD_NB || L.wd.type != C2H_Q6_K) return false;
-  if (l + 1 < D.n_layers && !fuse_attn_block(c, l + 1, form) && !fuse_attn_block_f(c, l + 1, form) &&
-      !pend_separate(c, l + 1, form))
-    return false;
-  if (D.n_embd > 1024) return false;  // the final norm folds with 256 threads, a float4 each
-  const bool fg = float_input(L.wg.type), fu = float_input(L.wu.type);
-  if (!fg && !fu) return nb_k(D.n_embd) == 3;
-  return fg && fu && L.wg.type == L.wu.type && D.n_embd % 128 == 0 && D.n_embd <= 1024;
+  if (!c->fuse_ffn || !ffn_block_types(c, l)) return false;
+  return l + 1 >= c->desc.n_layers || fuse_attn_block(c, l + 1, form) || fuse_attn_block_f(c, l + 1, form) ||
+         pend_separate(c, l + 1, form);
 }
 
 // ffn_in + ffn_out but for the residual add in one launch: gate|up stores h
@@ -2807,12 +2812,21 @@ int c2h_time_layer_kernel(c2h_ctx* c, int32_t kernel, int32_t iters, int32_t cap
   s.nx_out = c->nx_cur ^ 1;
   if ((rc = push_state(c, s))) return rc;
   const int form = attn_form(c, pos + 1);
-  // the fused launches exist where layer 1's would run (the timing runs them on every layer)
-  if ((kernel == C2H_KERNEL_ATTN_BLOCK || kernel == C2H_KERNEL_ATTN_OPROJ) &&
-      !(D.n_layers > 1 && fuse_attn_block(c, 1, form)))
-    return fail(c, C2H_ERR_UNSUPPORTED, "no fused attention launch for this model or position");
-  if (kernel == C2H_KERNEL_FFN_BLOCK && !(D.n_layers > 1 && defer_ffn(c, 0, form)))
-    return fail(c, C2H_ERR_UNSUPPORTED, "no fused FFN launch for this model");
+  // the timing runs a fused launch on every layer: every layer's tensors
+  // must be of the types that launch reads (a file may mix them by layer)
+  if (kernel == C2H_KERNEL_ATTN_BLOCK || kernel == C2H_KERNEL_ATTN_OPROJ || kernel == C2H_KERNEL_FFN_BLOCK) {
+    bool ok = D.n_layers > 1;
+    for (int l = 0; ok && l < D.n_layers; ++l) {
+      const Layer& L = c->layers[l];
+      if (kernel == C2H_KERNEL_FFN_BLOCK)
+        ok = c->fuse_ffn && ffn_block_types(c, l);
+      else
+        ok = fuse_attn_oproj(c, l, form) &&
+             (kernel == C2H_KERNEL_ATTN_OPROJ || (c->fuse_qkv && !float_input(L.wq.type) &&
+                                                  !float_input(L.wk.type) && !float_input(L.wv.type)));
+    }
+    if (!ok) return fail(c, C2H_ERR_UNSUPPORTED, "no fused launch of this kind for every layer at this position");
+  }
   // the residual kernels update X and the final norm writes normX[nx_out]:
   // both are restored afterwards
   float* saved = nullptr;

@@ -340,10 +340,11 @@ int c2h_check_rms_scale(c2h_ctx* ctx, uint32_t lo, uint64_t hi, uint64_t* mismat
  * of that position, which no later read depends on until a forward or step
  * at SeqLen rewrites them; X, which the residual kernels update, is restored
  * afterwards, and so is the normX buffer the final-norm kernel writes (the
- * one c2h_restore_normx switches back to).  The fused kernels (6-8) exist
- * where the model's layer 1 runs them at SeqLen + 1 attended positions
- * (else C2H_ERR_UNSUPPORTED); the call ends by advancing the state's
- * handover epoch, so the next forward takes none of the words they left. */
+ * one c2h_restore_normx switches back to).  A fused kernel (6-8) is timed
+ * only where every layer's tensors are of the types it reads, at SeqLen + 1
+ * attended positions (else C2H_ERR_UNSUPPORTED); the call ends by advancing
+ * the state's handover epoch, so the next forward takes none of the words
+ * they left. */
 int c2h_time_layer_kernel(c2h_ctx* ctx, int32_t kernel, int32_t iters, int32_t captured, float* ms_per_launch);
 
 /* Measurement aid with no counterpart in the reference: average device time
