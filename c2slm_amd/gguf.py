@@ -16,7 +16,7 @@ from __future__ import annotations
 
 import dataclasses
 import struct
-from typing import Any, Dict, List, Optional
+from typing import Any, Dict, List, Optional, Tuple
 
 import numpy as np
 
@@ -301,6 +301,9 @@ class ModelShape:
     t_gate: int = Q4_K
     t_up: int = Q4_K
     t_down: int = Q6_K
+    # per-layer ffn_down types, layer i taking entry i (None: t_down on every
+    # layer), as a Q4_K_M file keeps Q6_K on some layers and Q4_K on others
+    t_down_layers: Optional[Tuple[int, ...]] = None
     t_embd: int = Q8_0
     t_out: Optional[int] = None  # an untied output.weight of this type (None: tied to token_embd)
     # Qwen3 files: qwen3.* metadata keys, per-head attn_q_norm / attn_k_norm
@@ -390,7 +393,7 @@ def write_synthetic_model(path: str, shape: ModelShape = QWEN05B, seed: int = 20
         f32(f"blk.{i}.ffn_norm.weight", np.ones(E, np.float32))
         quant(f"blk.{i}.ffn_gate.weight", shape.t_gate, F, E)
         quant(f"blk.{i}.ffn_up.weight", shape.t_up, F, E)
-        quant(f"blk.{i}.ffn_down.weight", shape.t_down, E, F)
+        quant(f"blk.{i}.ffn_down.weight", shape.t_down_layers[i] if shape.t_down_layers else shape.t_down, E, F)
 
     a = shape.arch
     md = [

@@ -13,8 +13,10 @@ then a 40-step greedy stream (positions 20..59, crossing the 32- and
 64-position attention tiers), on the Qwen2.5-0.5B layer shape with the
 synthetic K-quant mix and with the published file's format mix; and two
 corners of the FFN's residual add moving to the next launch: a one-layer
-model (layer 0's FFN leaves it to the final norm) and K-quant attention
-with Q5_0 gate/up (the float-input FFN launch leaves it to k_attn_block)."""
+model (layer 0's FFN leaves it to the final norm), K-quant attention with
+Q5_0 gate/up (the float-input FFN launch leaves it to k_attn_block), and
+ffn_down Q6_K / Q4_K / Q6_K by layer, as a Q4_K_M file mixes it (the FFN as
+one launch on layers 0 and 2, as two on layer 1)."""
 import numpy as np
 import pytest
 
@@ -28,7 +30,7 @@ pytestmark = pytest.mark.gpu
 FORMS = ["1", "qkv", "ffn", ""]  # separate, attention + o-projection only, the FFN apart, all fused
 
 
-@pytest.fixture(scope="module", params=["k-quants", "real-formats", "one-layer", "q50-ffn"])
+@pytest.fixture(scope="module", params=["k-quants", "real-formats", "one-layer", "q50-ffn", "mixed-down"])
 def model(request, tmp_path_factory):
     p = str(tmp_path_factory.mktemp("forms") / f"{request.param}.gguf")
     shape = G.ModelShape(n_layers=2, n_vocab=4096)
@@ -39,6 +41,8 @@ def model(request, tmp_path_factory):
         shape = G.ModelShape(n_layers=1, n_vocab=4096)
     elif request.param == "q50-ffn":
         shape = G.ModelShape(n_layers=2, n_vocab=4096, t_gate=G.Q5_0, t_up=G.Q5_0, t_down=G.Q6_K)
+    elif request.param == "mixed-down":  # the FFN one launch on layers 0 and 2, two on layer 1
+        shape = G.ModelShape(n_layers=3, n_vocab=4096, t_down_layers=(G.Q6_K, G.Q4_K, G.Q6_K))
     G.write_synthetic_model(p, shape, seed=77)
     gf = G.GGUFFile(p)
     _, im_end, eos = G.special_token_ids(gf)
